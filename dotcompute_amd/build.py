@@ -1,0 +1,112 @@
+"""Offline build of the gfx950 HIP backend (no JIT, no torch extension machinery).
+
+Produces, in-tree:
+  dotcompute_amd/lib/libdotcompute_hip.so     the C-ABI library (include/dotcompute_hip.h)
+  dotcompute_amd/lib/dc_kernels_gfx950.hsaco  code object for the generic module-load path
+  dotcompute_amd/lib/libdotcompute_host.so    C++ host layer (orchestrator, LINQ provider, algorithms)
+  dotcompute_amd/lib/dc_host_tests             C++ tests of the host layer
+Run: python -m dotcompute_amd.build
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+HOST = os.path.join(PKG, "host")
+LIB = os.path.join(PKG, "lib")
+BUILD = os.path.join(PKG, "_build")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+
+# Device flags: gfx950 only; packed-FP32 instructions disabled; one rounding per float operation
+# (bit-exact LINQ maps); correctly rounded fp32 divide/sqrt (as .NET).
+HIP_FLAGS = [
+    "-O3", "-std=c++17", f"--offload-arch={ARCH}", "-fPIC",
+    "-ffp-contract=off", "-fhip-fp32-correctly-rounded-divide-sqrt",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function",
+]
+HIP_SOURCES = ["dc_runtime.hip", "dc_streaming.hip", "dc_linq.hip", "dc_gemm.hip", "dc_spmv.hip"]
+
+
+def _run(cmd: list[str]) -> None:
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in r.stdout.splitlines() if "packed-fp32-ops' is not a recognized feature" not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f"build step failed ({r.returncode}): {' '.join(cmd)}\n{out}")
+    if out.strip():
+        print(out, file=sys.stderr)
+
+
+def build_hip_library(jobs: int = 8) -> str:
+    os.makedirs(BUILD, exist_ok=True)
+    os.makedirs(LIB, exist_ok=True)
+    objs = []
+    cmds = []
+    for src in HIP_SOURCES:
+        obj = os.path.join(BUILD, src.replace(".hip", ".o"))
+        objs.append(obj)
+        cmds.append([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        list(ex.map(_run, cmds))
+    out = os.path.join(LIB, "libdotcompute_hip.so")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", out + ".tmp", *objs, "-lpthread", "-ldl"])
+    os.replace(out + ".tmp", out)
+    return out
+
+
+def build_code_object() -> str:
+    os.makedirs(LIB, exist_ok=True)
+    out = os.path.join(LIB, "dc_kernels_gfx950.hsaco")
+    _run([HIPCC, "--genco", f"--offload-arch={ARCH}", "-O3", "-ffp-contract=off",
+          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          os.path.join(CSRC, "dc_module_kernels.hip"), "-o", out + ".tmp"])
+    os.replace(out + ".tmp", out)
+    return out
+
+
+def build_host_layer() -> str | None:
+    """C++ host layer + its test binary (g++, links libdotcompute_hip.so)."""
+    if not os.path.isdir(HOST):
+        return None
+    srcs = sorted(os.path.join(HOST, "src", f) for f in os.listdir(os.path.join(HOST, "src")) if f.endswith(".cpp"))
+    inc = ["-I", os.path.join(HOST, "include"), "-I", os.path.join(ROOT, "include")]
+    flags = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter", "-pthread"]
+    out = os.path.join(LIB, "libdotcompute_host.so")
+    _run(["g++", *flags, *inc, "-shared", "-o", out + ".tmp", *srcs, "-L", LIB, "-ldotcompute_hip",
+          "-Wl,-rpath,$ORIGIN"])
+    os.replace(out + ".tmp", out)
+    tests = os.path.join(HOST, "tests")
+    if os.path.isdir(tests):
+        tsrcs = sorted(os.path.join(tests, f) for f in os.listdir(tests) if f.endswith(".cpp"))
+        tbin = os.path.join(LIB, "dc_host_tests")
+        _run(["g++", *flags, *inc, "-o", tbin + ".tmp", *tsrcs, "-L", LIB, "-ldotcompute_host", "-ldotcompute_hip",
+              "-Wl,-rpath,$ORIGIN"])
+        os.replace(tbin + ".tmp", tbin)
+    return out
+
+
+def build_oracle() -> str:
+    subprocess.run(["make", "-s", "-B", "-C", os.path.join(ROOT, "oracle")], check=True)
+    return os.path.join(ROOT, "oracle", "liboracle.so")
+
+
+def build_all() -> None:
+    with cf.ThreadPoolExecutor(max_workers=3) as ex:
+        f_lib = ex.submit(build_hip_library)
+        f_co = ex.submit(build_code_object)
+        f_or = ex.submit(build_oracle)
+        f_lib.result()
+        f_co.result()
+        f_or.result()
+    build_host_layer()
+
+
+if __name__ == "__main__":
+    build_all()
+    print("built:", sorted(os.listdir(LIB)))

@@ -1,0 +1,84 @@
+// dc_internal.hpp — shared host-side state of libdotcompute_hip.so (not part of the ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <mutex>
+
+#include "../../include/dotcompute_hip.h"
+
+// One device + one in-order stream + the scratch memory the kernels need.
+struct dc_hip_ctx {
+  int device = 0;
+  int cu_count = 0;
+  hipStream_t stream = nullptr;
+  std::mutex mu;
+
+  // Fixed 4 KiB block of counters (tile tickets, last-block tickets). Zeroed at creation; every
+  // kernel that takes a ticket puts its counter back to zero before it exits.
+  uint32_t* counters = nullptr;
+
+  // Per-block partial results of the reductions (double or int64 each; grows on demand).
+  void* partials = nullptr;
+  size_t partials_bytes = 0;
+
+  // Decoupled-lookback status words, one uint64 per tile (grows on demand). A word is valid only
+  // when its epoch field equals the launch's epoch, so the array never needs clearing between
+  // launches; it is cleared once when allocated and again whenever the epoch counter wraps.
+  uint64_t* status = nullptr;
+  size_t status_words = 0;
+  uint32_t epoch = 0;
+};
+
+struct dc_hip_event {
+  hipEvent_t ev = nullptr;
+  int device = 0;
+};
+
+struct dc_hip_module {
+  hipModule_t mod = nullptr;
+  int device = 0;
+};
+
+// Counter slots inside ctx->counters.
+enum dc_counter_slot : int {
+  DC_SLOT_REDUCE_DONE = 0,
+  DC_SLOT_LINQ_TICKET = 1,
+  DC_SLOT_LINQ_SUM_DONE = 2,
+  DC_SLOT_SPMV_DONE = 3,
+  DC_SLOT_COUNT = 1024
+};
+
+#define DC_RETURN_IF_HIP(expr)                         \
+  do {                                                 \
+    hipError_t dc_e_ = (expr);                         \
+    if (dc_e_ != hipSuccess) return (int32_t)dc_e_;    \
+  } while (0)
+
+#define DC_RETURN_IF(status_expr)                      \
+  do {                                                 \
+    int32_t dc_s_ = (status_expr);                     \
+    if (dc_s_ != DC_OK) return dc_s_;                  \
+  } while (0)
+
+// Lock the context and make its device current; every op entry point starts with this.
+#define DC_CTX_ENTER(ctx)                                      \
+  if (!(ctx)) return DC_ERR_INVALID_ARGUMENT;                  \
+  std::lock_guard<std::mutex> dc_lock_((ctx)->mu);             \
+  DC_RETURN_IF_HIP(hipSetDevice((ctx)->device))
+
+namespace dc {
+
+// Grows ctx->partials to at least `bytes` (caller holds the lock).
+int32_t ensure_partials(dc_hip_ctx* ctx, size_t bytes);
+// Grows ctx->status to at least `words` and returns the epoch to use for the next launch.
+int32_t ensure_status(dc_hip_ctx* ctx, size_t words, uint32_t* epoch_out);
+// Fills device memory with zero bytes using a kernel (capture-safe).
+int32_t zero_async(dc_hip_ctx* ctx, void* dst, size_t bytes);
+inline int32_t last_launch_status() { return (int32_t)hipGetLastError(); }
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace dc

@@ -1,0 +1,330 @@
+/*
+ * dotcompute_hip.h — C ABI of libdotcompute_hip.so, the MI355X (gfx950) HIP backend of DotCompute.
+ *
+ * This is the boundary the managed backend (DotCompute.Backends.HIP, C#) binds with
+ * [LibraryImport]; every other caller (the C++ host layer under dotcompute_amd/host, the Python
+ * ctypes harness in dotcompute_amd/hip.py) goes through exactly the same symbols.
+ *
+ * Conventions
+ *   - Every function returns int32_t: 0 (DC_OK) on success, a positive hipError_t value when a HIP
+ *     runtime call failed, or one of the negative DC_ERR_* codes below. dc_hip_error_string()
+ *     maps any of them to static text.
+ *   - A context (dc_hip_ctx) is one device plus one in-order HIP stream plus the scratch memory the
+ *     kernels need (lookback status words, tile tickets, partial sums). Calls on one context are
+ *     serialised by a mutex inside the library; different contexts are independent.
+ *   - Op entry points (dc_hip_vector_add_f32 … dc_hip_spmv_*) take DEVICE pointers, enqueue work on
+ *     the context's stream and return without waiting (like cuLaunchKernel in the CUDA backend);
+ *     their scalar results (sums, counts) are written to device memory. dc_hip_synchronize()
+ *     waits for the stream, which is what the reference does after every launch.
+ *   - Device memory is allocated by dc_hip_malloc and owned by the caller's buffer object, which
+ *     must free it exactly once with dc_hip_free.
+ *
+ * Reference interfaces each group replaces are cited per declaration (paths relative to the
+ * DotCompute repository root).
+ */
+#ifndef DOTCOMPUTE_HIP_H
+#define DOTCOMPUTE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(_WIN32)
+#define DC_HIP_API __declspec(dllexport)
+#else
+#define DC_HIP_API __attribute__((visibility("default")))
+#endif
+
+#define DC_HIP_ABI_VERSION 1
+
+/* ---------------------------------------------------------------------------------------------
+ * Status codes (replaces CudaError + CudaErrorClassification,
+ * src/Backends/DotCompute.Backends.CUDA/ErrorHandling/CudaErrorClassification.cs:17)
+ * ------------------------------------------------------------------------------------------- */
+#define DC_OK 0
+#define DC_ERR_INVALID_ARGUMENT (-1)  /* null pointer, negative size, bad shape                  */
+#define DC_ERR_NO_DEVICE (-2)         /* no HIP device / device index out of range              */
+#define DC_ERR_UNSUPPORTED (-3)       /* device is not gfx950, or a LINQ chain the kernels cannot run */
+#define DC_ERR_OVERFLOW (-4)          /* checked int32 sum overflowed (System.OverflowException)  */
+#define DC_ERR_MISALIGNED (-5)        /* pointer alignment the kernel requires was not met        */
+#define DC_ERR_DIMENSION (-6)         /* matrix/vector dimension mismatch (ArgumentException)     */
+#define DC_ERR_OUT_OF_MEMORY (-7)     /* scratch or host allocation failed                        */
+#define DC_ERR_NOT_FOUND (-8)         /* module / function name not found                         */
+
+DC_HIP_API const char* dc_hip_error_string(int32_t status);
+DC_HIP_API int32_t dc_hip_abi_version(void);
+
+/* ---------------------------------------------------------------------------------------------
+ * Devices and contexts
+ * Replaces cudaGetDeviceCount / cudaGetDeviceProperties
+ * (src/Backends/DotCompute.Backends.CUDA/Types/Native/CudaRuntime.cs:160) and the accelerator's
+ * context/stream creation (src/Backends/DotCompute.Backends.CUDA/CudaAccelerator.cs:140-146).
+ * ------------------------------------------------------------------------------------------- */
+typedef struct dc_hip_device_info {
+  char name[256];
+  char gcn_arch_name[64];       /* e.g. "gfx950:sramecc+:xnack-" */
+  int32_t device_id;
+  int32_t compute_units;
+  int32_t wave_size;            /* 64 on CDNA */
+  int32_t max_threads_per_block;
+  int32_t clock_khz;
+  int32_t memory_clock_khz;
+  int32_t memory_bus_width_bits;
+  int32_t l2_cache_bytes;
+  int64_t total_global_mem;
+  int64_t lds_per_block;
+  int32_t pci_bus_id;
+  int32_t is_gfx950;            /* 1 when the kernels in this library can run on the device */
+} dc_hip_device_info;
+
+typedef struct dc_hip_ctx dc_hip_ctx;
+typedef struct dc_hip_event dc_hip_event;
+typedef struct dc_hip_module dc_hip_module;
+
+DC_HIP_API int32_t dc_hip_device_count(int32_t* count);
+DC_HIP_API int32_t dc_hip_device_info_get(int32_t device, dc_hip_device_info* info);
+DC_HIP_API int32_t dc_hip_ctx_create(int32_t device, dc_hip_ctx** ctx);
+DC_HIP_API int32_t dc_hip_ctx_destroy(dc_hip_ctx* ctx);
+DC_HIP_API int32_t dc_hip_ctx_device(const dc_hip_ctx* ctx, int32_t* device);
+/* Blocks until every operation enqueued on the context's stream has finished
+ * (replaces cudaDeviceSynchronize, CudaAccelerator.cs:198-208). */
+DC_HIP_API int32_t dc_hip_synchronize(dc_hip_ctx* ctx);
+
+/* ---------------------------------------------------------------------------------------------
+ * Memory (replaces cudaMalloc/cudaFree/cudaMemcpyAsync/cudaMemset,
+ * src/Backends/DotCompute.Backends.CUDA/Types/Native/CudaRuntime.cs:243,247,278,291, used by
+ * IUnifiedMemoryManager.AllocateAsync/CopyToDeviceAsync/CopyFromDeviceAsync/FreeAsync,
+ * src/Core/DotCompute.Abstractions/Interfaces/IUnifiedMemoryManager.cs:47,130,143,160).
+ * Copies are asynchronous on the context stream; host memory must stay valid (pinned, for
+ * managed callers) until dc_hip_synchronize returns.
+ * ------------------------------------------------------------------------------------------- */
+DC_HIP_API int32_t dc_hip_malloc(dc_hip_ctx* ctx, size_t bytes, void** device_ptr);
+DC_HIP_API int32_t dc_hip_free(dc_hip_ctx* ctx, void* device_ptr);
+DC_HIP_API int32_t dc_hip_malloc_host(dc_hip_ctx* ctx, size_t bytes, void** host_ptr); /* pinned */
+DC_HIP_API int32_t dc_hip_free_host(dc_hip_ctx* ctx, void* host_ptr);
+DC_HIP_API int32_t dc_hip_memcpy_h2d_async(dc_hip_ctx* ctx, void* dst, const void* src, size_t bytes);
+DC_HIP_API int32_t dc_hip_memcpy_d2h_async(dc_hip_ctx* ctx, void* dst, const void* src, size_t bytes);
+DC_HIP_API int32_t dc_hip_memcpy_d2d_async(dc_hip_ctx* ctx, void* dst, const void* src, size_t bytes);
+/* Fills `bytes` bytes with `value` (a kernel, not hipMemsetAsync, so it is safe under capture). */
+DC_HIP_API int32_t dc_hip_memset_async(dc_hip_ctx* ctx, void* dst, int32_t value, size_t bytes);
+DC_HIP_API int32_t dc_hip_mem_info(dc_hip_ctx* ctx, size_t* free_bytes, size_t* total_bytes);
+
+/* ---------------------------------------------------------------------------------------------
+ * Events on the context stream (the profiling hook; the reference times launches with
+ * cudaEvent pairs, src/Backends/DotCompute.Backends.CUDA/Timing/CudaEventTimer.cs:219 and
+ * src/Backends/DotCompute.Backends.CUDA/Types/Native/CudaRuntime.cs:524).
+ * ------------------------------------------------------------------------------------------- */
+DC_HIP_API int32_t dc_hip_event_create(dc_hip_ctx* ctx, dc_hip_event** event);
+DC_HIP_API int32_t dc_hip_event_destroy(dc_hip_event* event);
+DC_HIP_API int32_t dc_hip_event_record(dc_hip_ctx* ctx, dc_hip_event* event);
+DC_HIP_API int32_t dc_hip_event_synchronize(dc_hip_event* event);
+DC_HIP_API int32_t dc_hip_event_elapsed_ms(dc_hip_event* start, dc_hip_event* stop, float* ms);
+
+/* ---------------------------------------------------------------------------------------------
+ * Modules and generic launch: the ICompiledKernel path for prebuilt gfx950 code objects.
+ * Replaces cuModuleLoadData / cuModuleGetFunction / cuLaunchKernel
+ * (src/Backends/DotCompute.Backends.CUDA/Types/Native/CudaRuntime.cs:451,464,470) as driven by
+ * CudaKernelLauncher.LaunchKernelInternalAsync (Kernels/CudaKernelLauncher.cs:205-349): `args` is
+ * an array of pointers to the argument values, in parameter order.
+ * ------------------------------------------------------------------------------------------- */
+DC_HIP_API int32_t dc_hip_module_load(dc_hip_ctx* ctx, const char* path, dc_hip_module** module);
+DC_HIP_API int32_t dc_hip_module_load_data(dc_hip_ctx* ctx, const void* image, dc_hip_module** module);
+DC_HIP_API int32_t dc_hip_module_unload(dc_hip_module* module);
+DC_HIP_API int32_t dc_hip_module_get_function(dc_hip_module* module, const char* name, void** function);
+DC_HIP_API int32_t dc_hip_launch_kernel(dc_hip_ctx* ctx, void* function,
+                                        uint32_t grid_x, uint32_t grid_y, uint32_t grid_z,
+                                        uint32_t block_x, uint32_t block_y, uint32_t block_z,
+                                        uint32_t shared_mem_bytes, void** args);
+/* Path of the code object (dc_kernels_gfx950.hsaco) installed next to this library, or "" */
+DC_HIP_API const char* dc_hip_default_module_path(void);
+
+/* ---------------------------------------------------------------------------------------------
+ * Seeded, counter-based input generators (device side). Element i of stream s with seed k is
+ * r = splitmix64(k ^ (s << 40) ^ i). Floats: [-1,1) -> (r >> 40) * 2^-23 - 1, [0,1) -> (r >> 40) *
+ * 2^-24 (both exact in float32). Integers in [lo, hi]: lo + ((r >> 32) * (hi - lo + 1) >> 32).
+ * dc_gen_* below reproduce the same streams bit-for-bit on the host.
+ * ------------------------------------------------------------------------------------------- */
+DC_HIP_API int32_t dc_hip_fill_uniform_f32(dc_hip_ctx* ctx, float* dst, int64_t n, uint64_t seed,
+                                           uint32_t stream, int32_t unit_interval /* 0:[-1,1) 1:[0,1) */);
+DC_HIP_API int32_t dc_hip_fill_uniform_i32(dc_hip_ctx* ctx, int32_t* dst, int64_t n, uint64_t seed,
+                                           uint32_t stream, int32_t lo, int32_t hi);
+DC_HIP_API int32_t dc_gen_uniform_f32(float* dst, int64_t n, uint64_t seed, uint32_t stream,
+                                      int32_t unit_interval);
+DC_HIP_API int32_t dc_gen_uniform_i32(int32_t* dst, int64_t n, uint64_t seed, uint32_t stream,
+                                      int32_t lo, int32_t hi);
+/* Synthetic PageRank-style CSR graph (host, multithreaded): out-degree of row r drawn from a
+ * Zipf(alpha) law on [1, max_degree]; column indices uniform over [0, cols) without self-loops;
+ * value = 1/out-degree. Call once with row_pointers only to learn nnz (row_pointers[rows]),
+ * then again with col_indices/values sized nnz. */
+DC_HIP_API int32_t dc_gen_zipf_csr_rowptr(int64_t rows, double alpha, int32_t max_degree,
+                                          uint64_t seed, int32_t* row_pointers /* rows+1 */);
+DC_HIP_API int32_t dc_gen_zipf_csr_fill(int64_t rows, int64_t cols, uint64_t seed,
+                                        const int32_t* row_pointers, int32_t* col_indices,
+                                        float* values);
+
+/* ---------------------------------------------------------------------------------------------
+ * VectorAdd — the README [Kernel] quick start, result[i] = a[i] + b[i]
+ * Replaces the generated CUDA kernel launched by KernelExecutionService.ExecuteAsync
+ * (src/Runtime/DotCompute.Runtime/Services/KernelExecutionService.cs:290-335; body emitted by
+ * src/Runtime/DotCompute.Generators/Kernel/Generation/KernelExecutionMetadataEmitter.cs:65-105)
+ * and OptimizedVectorAddKernel (src/Backends/DotCompute.Backends.CPU/Kernels/Optimized/
+ * OptimizedVectorAddKernel.cs:81-111).
+ * ------------------------------------------------------------------------------------------- */
+DC_HIP_API int32_t dc_hip_vector_add_f32(dc_hip_ctx* ctx, const float* a, const float* b,
+                                         float* result, int64_t n);
+
+/* ---------------------------------------------------------------------------------------------
+ * Sum reductions (deterministic: fixed per-thread order, fixed tree, last-block combine).
+ * f32: accumulated in float64, result written as a double; the managed caller casts to float,
+ *      as Enumerable.Sum(IEnumerable<float>) does (reached from
+ *      src/Extensions/DotCompute.Linq/ComputeQueryableExtensions.cs:265-267) and as
+ *      OptimizedReductionKernel does (src/Backends/DotCompute.Backends.CPU/Kernels/Optimized/
+ *      OptimizedReductionKernel.cs:69-95).
+ * i32: exact int64 total written to *sum_out; *overflow_out (device int32) is set to 1 when the
+ *      total does not fit int32, which the managed caller raises as OverflowException
+ *      (checked Enumerable.Sum(IEnumerable<int>)).
+ * Replaces CudaKernelGenerator.GenerateReduceOperation
+ * (src/Extensions/DotCompute.Linq/CodeGeneration/CudaKernelGenerator.cs:399-463).
+ * ------------------------------------------------------------------------------------------- */
+DC_HIP_API int32_t dc_hip_reduce_sum_f32(dc_hip_ctx* ctx, const float* input, int64_t n,
+                                         double* sum_out);
+DC_HIP_API int32_t dc_hip_reduce_sum_i32(dc_hip_ctx* ctx, const int32_t* input, int64_t n,
+                                         int64_t* sum_out, int32_t* overflow_out);
+
+/* ---------------------------------------------------------------------------------------------
+ * Fused LINQ chains: Where / Select stages over float32, compiled by the host-side fusion planner
+ * into a small register program (dc_linq_chain) that one prebuilt kernel interprets.
+ * Replaces the per-chain CUDA-C that CudaKernelGenerator emits
+ * (src/Extensions/DotCompute.Linq/CodeGeneration/CudaKernelGenerator.cs:81-125, fused
+ * :1058-1134, filter :351-376) and the launch in RuntimeExecutor.ExecuteGpuKernelAsync
+ * (src/Extensions/DotCompute.Linq/CodeGeneration/RuntimeExecutor.cs:245-312), with the
+ * LINQ-to-objects semantics the provider falls back to today (ComputeQueryableExtensions.cs:628-633):
+ * output is compacted and order-preserving.
+ *
+ * Program model. Per element the kernel holds: e (the pipeline element), v (accumulator), s0, s1
+ * (saved values), p and q (predicate registers) and k (keep flag, initially true).
+ * Each instruction: op, src (operand source), imm (constant operand).
+ *   value ops   v = f(v, operand)         LOAD ADD SUB RSUB MUL DIV RDIV MIN MAX NEG ABS SQRT
+ *   STORE_S0/1  s0/s1 = v
+ *   CMP_*       c = (v <cmp> operand); p = c (mode SET), p && c (AND), p || c (OR)
+ *   PNOT        p = !p;  PSTORE q = p;  PAND_Q p = p && q;  POR_Q p = p || q
+ *   FILTER      k = k && p                 (ends a Where stage)
+ *   MAP         e = v                      (ends a Select stage)
+ * Every float operation rounds once to float32 (no contraction), matching .NET's scalar float
+ * arithmetic, so outputs are bit-identical to LINQ-to-objects for the same lambdas.
+ * ------------------------------------------------------------------------------------------- */
+#define DC_LINQ_MAX_INSTR 48
+
+enum dc_linq_op {
+  DC_LQ_NOP = 0,
+  DC_LQ_LOAD = 1,
+  DC_LQ_ADD = 2,
+  DC_LQ_SUB = 3,
+  DC_LQ_RSUB = 4,
+  DC_LQ_MUL = 5,
+  DC_LQ_DIV = 6,
+  DC_LQ_RDIV = 7,
+  DC_LQ_MIN = 8,
+  DC_LQ_MAX = 9,
+  DC_LQ_NEG = 10,
+  DC_LQ_ABS = 11,
+  DC_LQ_SQRT = 12,
+  DC_LQ_STORE_S0 = 13,
+  DC_LQ_STORE_S1 = 14,
+  DC_LQ_CMP_GT = 20,
+  DC_LQ_CMP_GE = 21,
+  DC_LQ_CMP_LT = 22,
+  DC_LQ_CMP_LE = 23,
+  DC_LQ_CMP_EQ = 24,
+  DC_LQ_CMP_NE = 25,
+  DC_LQ_PNOT = 26,
+  DC_LQ_PSTORE = 27,
+  DC_LQ_PAND_Q = 28,
+  DC_LQ_POR_Q = 29,
+  DC_LQ_FILTER = 30,
+  DC_LQ_MAP = 31
+};
+
+enum dc_linq_src {
+  DC_LQ_SRC_IMM = 0,   /* the instruction's constant */
+  DC_LQ_SRC_ELEM = 1,  /* e */
+  DC_LQ_SRC_S0 = 2,
+  DC_LQ_SRC_S1 = 3
+};
+
+enum dc_linq_cmp_mode { DC_LQ_CMP_SET = 0, DC_LQ_CMP_AND = 1, DC_LQ_CMP_OR = 2 };
+
+typedef struct dc_linq_instr {
+  uint8_t op;    /* enum dc_linq_op */
+  uint8_t src;   /* enum dc_linq_src (value and CMP ops) */
+  uint8_t mode;  /* enum dc_linq_cmp_mode (CMP ops) */
+  uint8_t pad;
+  float imm;
+} dc_linq_instr;
+
+typedef struct dc_linq_chain {
+  int32_t n_instr;
+  int32_t flags;  /* reserved, 0 */
+  dc_linq_instr code[DC_LINQ_MAX_INSTR];
+} dc_linq_chain;
+
+/* Checks a program for structural validity (opcodes, operand sources, length). */
+DC_HIP_API int32_t dc_linq_chain_validate(const dc_linq_chain* chain);
+
+/* Where/Select → ToArray: writes the kept, mapped elements in input order to `output` (capacity n)
+ * and their number to *count_out (device int64). Single pass, decoupled lookback. */
+DC_HIP_API int32_t dc_hip_linq_where_select_f32(dc_hip_ctx* ctx, const dc_linq_chain* chain,
+                                                const float* input, int64_t n, float* output,
+                                                int64_t* count_out);
+/* Where/Select → Sum (and Count): float64-accumulated sum of the kept, mapped elements to
+ * *sum_out and their number to *count_out (either may be NULL). Deterministic. */
+DC_HIP_API int32_t dc_hip_linq_where_select_sum_f32(dc_hip_ctx* ctx, const dc_linq_chain* chain,
+                                                    const float* input, int64_t n,
+                                                    double* sum_out, int64_t* count_out);
+
+/* ---------------------------------------------------------------------------------------------
+ * Dense GEMM, row-major: C[m×n] = A[m×k] · B[k×n].
+ * Replaces OptimizedMatrixMultiplyKernel (src/Backends/DotCompute.Backends.CPU/Kernels/Optimized/
+ * OptimizedMatrixMultiplyKernel.cs:72-96), MatrixOperations.MultiplyAsync / MultiplyOnGPUAsync
+ * (src/Extensions/DotCompute.Algorithms/LinearAlgebra/Operations/MatrixOperations.cs:28-64,359-440)
+ * and the 16×16 tiled string kernels (LinearAlgebra/MatrixKernels.cs:11-80).
+ * f32: fp32 inputs, fp32 MFMA (v_mfma_f32_*_f32), fp32 accumulate.
+ * bf16: bf16 inputs (uint16 bit patterns), bf16 MFMA, fp32 accumulate and output.
+ * Leading dimensions equal the row lengths (k for A, n for B and C).
+ * ------------------------------------------------------------------------------------------- */
+DC_HIP_API int32_t dc_hip_gemm_f32(dc_hip_ctx* ctx, const float* a, const float* b, float* c,
+                                   int64_t m, int64_t n, int64_t k);
+DC_HIP_API int32_t dc_hip_gemm_bf16(dc_hip_ctx* ctx, const uint16_t* a, const uint16_t* b, float* c,
+                                    int64_t m, int64_t n, int64_t k);
+/* Round-to-nearest-even float32 → bfloat16 conversion (NaN stays NaN). */
+DC_HIP_API int32_t dc_hip_convert_f32_to_bf16(dc_hip_ctx* ctx, const float* input, uint16_t* output,
+                                              int64_t n);
+
+/* ---------------------------------------------------------------------------------------------
+ * CSR SpMV, y = A·x in float32 (CsrMatrix<T> + SparseOps.SpMV,
+ * src/Extensions/DotCompute.Algorithms/Sparse/SparseMatrix.cs:68-272,669-692; the never-launched
+ * CUDA string kernel Kernels/LinearAlgebra/SparseMatrixKernels.cs:47-75).
+ * row_pointers has rows+1 entries (int32 offsets, as CsrMatrix<T>); x has cols entries.
+ * ------------------------------------------------------------------------------------------- */
+DC_HIP_API int32_t dc_hip_spmv_csr_f32(dc_hip_ctx* ctx, const int32_t* row_pointers,
+                                       const int32_t* col_indices, const float* values,
+                                       const float* x, float* y, int64_t rows, int64_t cols,
+                                       int64_t nnz);
+/* Power iteration used by the SpMV benchmark: repeat `iterations` times
+ *   y = A·x;  s = Σ y (float64);  x = y / s
+ * leaving the normalised vector in x (rows == cols required). `y` is caller-provided scratch of
+ * rows floats. The final L1 norm before the last normalisation is written to *last_sum_out
+ * (device double, may be NULL). */
+DC_HIP_API int32_t dc_hip_spmv_power_iterate_f32(dc_hip_ctx* ctx, const int32_t* row_pointers,
+                                                 const int32_t* col_indices, const float* values,
+                                                 float* x, float* y, int64_t rows, int64_t nnz,
+                                                 int32_t iterations, double* last_sum_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DOTCOMPUTE_HIP_H */

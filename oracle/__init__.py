@@ -1,0 +1,241 @@
+"""CPU oracle for the DotCompute HIP hot path — TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import
+this package, and only as the checker (or as the timed CPU baseline). The HIP product path never
+imports it. The functions are thin numpy wrappers over ``oracle/liboracle.so`` (plain C, see
+``oracle/oracle.c`` for the reference file:line each function restates).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+_i64, _i32, _u64, _u32, _f64 = C.c_int64, C.c_int32, C.c_uint64, C.c_uint32, C.c_double
+_P = C.c_void_p
+
+
+def build() -> str:
+    subprocess.run(["make", "-s", "-B", "-C", HERE], check=True)
+    return LIB_PATH
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        sig = {
+            "oracle_splitmix64": (_u64, [_u64]),
+            "oracle_gen_uniform_f32": (None, [_P, _i64, _u64, _u32, _i32]),
+            "oracle_gen_uniform_i32": (None, [_P, _i64, _u64, _u32, _i32, _i32]),
+            "oracle_gen_zipf_rowptr": (_i64, [_i64, _f64, _i32, _u64, _P]),
+            "oracle_gen_zipf_fill": (None, [_i64, _i64, _u64, _P, _P, _P]),
+            "oracle_vector_add_f32": (None, [_P, _P, _P, _i64]),
+            "oracle_sum_f32_enumerable": (C.c_float, [_P, _i64, _P]),
+            "oracle_sum_f32_partitioned": (C.c_float, [_P, _i64, _i32, _P]),
+            "oracle_sum_f32_compensated": (_f64, [_P, _i64]),
+            "oracle_sum_i32_checked": (_i32, [_P, _i64, _P]),
+            "oracle_sum_i32_exact": (_i64, [_P, _i64]),
+            "oracle_where_gt0_select_2x_plus_1": (_i64, [_P, _i64, _P]),
+            "oracle_where_gt0_select_2x_plus_1_sum": (C.c_float, [_P, _i64, _P, _P]),
+            "oracle_linq_eval": (_i32, [_P, C.c_float, _P]),
+            "oracle_linq_where_select": (_i64, [_P, _P, _i64, _P]),
+            "oracle_linq_where_select_sum": (C.c_float, [_P, _P, _i64, _P, _P]),
+            "oracle_gemm_f32_naive": (None, [_P, _P, _P, _i64, _i64, _i64, _i32]),
+            "oracle_gemm_f32_naive_rows": (None, [_P, _P, _P, _i64, _i64, _i64, _i64, _i64, _i32]),
+            "oracle_gemm_f32_blocked": (None, [_P, _P, _P, _i64, _i64, _i64]),
+            "oracle_gemm_f64_rows": (None, [_P, _P, _P, _P, _i64, _i64, _i64, _P, _i64, _i32]),
+            "oracle_f32_to_bf16": (C.c_uint16, [C.c_float]),
+            "oracle_bf16_to_f32": (C.c_float, [C.c_uint16]),
+            "oracle_f32_to_bf16_array": (None, [_P, _P, _i64]),
+            "oracle_spmv_csr_f32": (_i32, [_P, _P, _P, _P, _P, _i64, _i64, _i64]),
+            "oracle_spmv_csr_f64": (None, [_P, _P, _P, _P, _P, _i64]),
+            "oracle_spmv_power_f32": (_i32, [_P, _P, _P, _P, _P, _i64, _i32, _P]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+# ---- generators ----
+def splitmix64(z: int) -> int:
+    return lib().oracle_splitmix64(z)
+
+
+def gen_uniform_f32(n: int, seed: int, stream: int = 0, unit_interval: bool = False) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().oracle_gen_uniform_f32(_p(out), n, seed, stream, int(unit_interval))
+    return out
+
+
+def gen_uniform_i32(n: int, seed: int, stream: int = 1, lo: int = -1000, hi: int = 1000) -> np.ndarray:
+    out = np.empty(n, np.int32)
+    lib().oracle_gen_uniform_i32(_p(out), n, seed, stream, lo, hi)
+    return out
+
+
+def gen_zipf_csr(rows: int, seed: int, alpha: float = 2.0, max_degree: int = 4096, cols: int | None = None):
+    cols = rows if cols is None else cols
+    rp = np.empty(rows + 1, np.int32)
+    nnz = lib().oracle_gen_zipf_rowptr(rows, alpha, max_degree, seed, _p(rp))
+    if nnz < 0:
+        raise OverflowError("nnz does not fit int32 row pointers")
+    col = np.empty(nnz, np.int32)
+    val = np.empty(nnz, np.float32)
+    lib().oracle_gen_zipf_fill(rows, cols, seed, _p(rp), _p(col), _p(val))
+    return rp, col, val
+
+
+# ---- ops ----
+def vector_add_f32(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    out = np.empty_like(a)
+    lib().oracle_vector_add_f32(_p(a), _p(b), _p(out), a.size)
+    return out
+
+
+def sum_f32_enumerable(x: np.ndarray):
+    d = C.c_double()
+    f = lib().oracle_sum_f32_enumerable(_p(x), x.size, C.byref(d))
+    return np.float32(f), d.value
+
+
+def sum_f32_partitioned(x: np.ndarray, partitions: int):
+    d = C.c_double()
+    f = lib().oracle_sum_f32_partitioned(_p(x), x.size, partitions, C.byref(d))
+    return np.float32(f), d.value
+
+
+def sum_f32_compensated(x: np.ndarray) -> float:
+    return lib().oracle_sum_f32_compensated(_p(x), x.size)
+
+
+def sum_i32_checked(x: np.ndarray):
+    """Returns the int32 sum, or raises OverflowError as checked Enumerable.Sum does."""
+    out = C.c_int32()
+    st = lib().oracle_sum_i32_checked(_p(x), x.size, C.byref(out))
+    if st == -4:
+        raise OverflowError("Arithmetic operation resulted in an overflow.")
+    return out.value
+
+
+def sum_i32_exact(x: np.ndarray) -> int:
+    return lib().oracle_sum_i32_exact(_p(x), x.size)
+
+
+def where_gt0_select_2x_plus_1(x: np.ndarray) -> np.ndarray:
+    out = np.empty_like(x)
+    k = lib().oracle_where_gt0_select_2x_plus_1(_p(x), x.size, _p(out))
+    return out[:k].copy()
+
+
+def where_gt0_select_2x_plus_1_sum(x: np.ndarray):
+    cnt = C.c_int64()
+    d = C.c_double()
+    f = lib().oracle_where_gt0_select_2x_plus_1_sum(_p(x), x.size, C.byref(cnt), C.byref(d))
+    return np.float32(f), d.value, cnt.value
+
+
+def linq_where_select(chain, x: np.ndarray) -> np.ndarray:
+    out = np.empty_like(x)
+    k = lib().oracle_linq_where_select(C.byref(chain), _p(x), x.size, _p(out))
+    if k < 0:
+        raise ValueError(f"malformed chain ({k})")
+    return out[:k].copy()
+
+
+def linq_where_select_sum(chain, x: np.ndarray):
+    cnt = C.c_int64()
+    d = C.c_double()
+    f = lib().oracle_linq_where_select_sum(C.byref(chain), _p(x), x.size, C.byref(cnt), C.byref(d))
+    if cnt.value < 0:
+        raise ValueError(f"malformed chain ({cnt.value})")
+    return np.float32(f), d.value, cnt.value
+
+
+def linq_eval(chain, x: float):
+    y = C.c_float()
+    r = lib().oracle_linq_eval(C.byref(chain), C.c_float(x), C.byref(y))
+    return r, np.float32(y.value)
+
+
+def gemm_f32_naive(a: np.ndarray, b: np.ndarray, threads: int = 1, rows: tuple[int, int] | None = None):
+    m, k = a.shape
+    k2, n = b.shape
+    assert k == k2
+    c = np.zeros((m, n), np.float32)
+    r0, r1 = rows if rows else (0, m)
+    lib().oracle_gemm_f32_naive_rows(_p(a), _p(b), _p(c), m, n, k, r0, r1, threads)
+    return c
+
+
+def gemm_f32_blocked(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    m, k = a.shape
+    _, n = b.shape
+    c = np.empty((m, n), np.float32)
+    lib().oracle_gemm_f32_blocked(_p(a), _p(b), _p(c), m, n, k)
+    return c
+
+
+def gemm_f64_rows(a: np.ndarray, b: np.ndarray, rows: np.ndarray, threads: int = 8):
+    m, k = a.shape
+    _, n = b.shape
+    rows = np.ascontiguousarray(rows, np.int64)
+    c = np.empty((rows.size, n), np.float64)
+    ac = np.empty((rows.size, n), np.float64)
+    lib().oracle_gemm_f64_rows(_p(a), _p(b), _p(c), _p(ac), m, n, k, _p(rows), rows.size, threads)
+    return c, ac
+
+
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().oracle_f32_to_bf16_array(_p(x), _p(out), x.size)
+    return out
+
+
+def bf16_to_f32(h: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(h, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def spmv_csr_f32(rp, col, val, x, cols: int | None = None) -> np.ndarray:
+    rows = rp.size - 1
+    cols = x.size if cols is None else cols
+    y = np.empty(rows, np.float32)
+    st = lib().oracle_spmv_csr_f32(_p(rp), _p(col), _p(val), _p(x), _p(y), rows, cols, x.size)
+    if st == -6:
+        raise ValueError("SpMV dimension mismatch")
+    return y
+
+
+def spmv_csr_f64(rp, col, val, x64) -> np.ndarray:
+    rows = rp.size - 1
+    y = np.empty(rows, np.float64)
+    lib().oracle_spmv_csr_f64(_p(rp), _p(col), _p(val), _p(x64), _p(y), rows)
+    return y
+
+
+def spmv_power_f32(rp, col, val, x0, iterations: int):
+    rows = rp.size - 1
+    x = np.array(x0, np.float32, copy=True)
+    y = np.empty(rows, np.float32)
+    s = C.c_double()
+    lib().oracle_spmv_power_f32(_p(rp), _p(col), _p(val), _p(x), _p(y), rows, iterations, C.byref(s))
+    return x, s.value

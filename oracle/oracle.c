@@ -1,0 +1,525 @@
+/*
+ * oracle.c — CPU restatement of the DotCompute reference semantics for the HIP hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY: loaded by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg as the checker / timed CPU baseline; never by the HIP product path.
+ *
+ * Built with -ffp-contract=off so every float operation rounds once, as .NET's RyuJIT does for
+ * scalar float arithmetic (it never contracts a*b+c into an FMA).
+ * Citations are paths in the mivertowski/DotCompute repository.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------------------------ */
+/* Generators: this build's input specification (not reference code).                          */
+/* ------------------------------------------------------------------------------------------ */
+
+/* SplitMix64 finaliser (Steele, Lea, Flood, "Fast splittable pseudorandom number generators",
+ * OOPSLA 2014; constants as published with Java 8's SplittableRandom). */
+uint64_t oracle_splitmix64(uint64_t z) {
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+static inline uint64_t key_of(uint64_t seed, uint32_t stream, uint64_t i) {
+  return seed ^ ((uint64_t)stream << 40) ^ i;
+}
+
+void oracle_gen_uniform_f32(float* dst, int64_t n, uint64_t seed, uint32_t stream, int32_t unit_interval) {
+  for (int64_t i = 0; i < n; ++i) {
+    uint64_t r = oracle_splitmix64(key_of(seed, stream, (uint64_t)i));
+    float u = (float)(uint32_t)(r >> 40);
+    if (unit_interval)
+      dst[i] = u * 0x1p-24f;          /* [0, 1) */
+    else
+      dst[i] = u * 0x1p-23f - 1.0f;   /* [-1, 1), exact */
+  }
+}
+
+void oracle_gen_uniform_i32(int32_t* dst, int64_t n, uint64_t seed, uint32_t stream, int32_t lo, int32_t hi) {
+  uint64_t span = (uint64_t)((int64_t)hi - (int64_t)lo + 1);
+  for (int64_t i = 0; i < n; ++i) {
+    uint64_t r = oracle_splitmix64(key_of(seed, stream, (uint64_t)i));
+    dst[i] = (int32_t)((int64_t)lo + (int64_t)(((r >> 32) * span) >> 32));
+  }
+}
+
+/* Zipf(alpha) on [1, max_degree] by inverse CDF: degree = smallest d with cdf[d] > u, u in [0,1)
+ * from 53 random bits. Stream 3 keyed by row index. */
+int64_t oracle_gen_zipf_rowptr(int64_t rows, double alpha, int32_t max_degree, uint64_t seed,
+                               int32_t* row_pointers) {
+  if (rows < 0 || max_degree < 1) return -1;
+  double* cdf = (double*)malloc(sizeof(double) * (size_t)(max_degree + 1));
+  if (!cdf) return -1;
+  double total = 0.0;
+  for (int32_t d = 1; d <= max_degree; ++d) total += pow((double)d, -alpha);
+  double acc = 0.0;
+  cdf[0] = 0.0;
+  for (int32_t d = 1; d <= max_degree; ++d) {
+    acc += pow((double)d, -alpha);
+    cdf[d] = acc / total;
+  }
+  cdf[max_degree] = 1.0;
+  int64_t nnz = 0;
+  row_pointers[0] = 0;
+  for (int64_t r = 0; r < rows; ++r) {
+    uint64_t z = oracle_splitmix64(key_of(seed, 3u, (uint64_t)r));
+    double u = (double)(z >> 11) * 0x1p-53;
+    int32_t lo = 1, hi = max_degree; /* smallest d in [1,max] with cdf[d] > u */
+    while (lo < hi) {
+      int32_t mid = lo + (hi - lo) / 2;
+      if (cdf[mid] > u) hi = mid; else lo = mid + 1;
+    }
+    nnz += lo;
+    if (nnz > 2147483647LL) { free(cdf); return -1; }
+    row_pointers[r + 1] = (int32_t)nnz;
+  }
+  free(cdf);
+  return nnz;
+}
+
+/* Columns: stream 4 keyed by the global nonzero index; uniform over the cols-1 non-diagonal
+ * columns (self-loops skipped by shifting c >= row up by one). Values: 1/out-degree. */
+void oracle_gen_zipf_fill(int64_t rows, int64_t cols, uint64_t seed, const int32_t* row_pointers,
+                          int32_t* col_indices, float* values) {
+  uint64_t span = (uint64_t)(cols - 1);
+  for (int64_t r = 0; r < rows; ++r) {
+    int32_t b = row_pointers[r], e = row_pointers[r + 1];
+    float v = 1.0f / (float)(e - b);
+    for (int32_t j = b; j < e; ++j) {
+      uint64_t z = oracle_splitmix64(key_of(seed, 4u, (uint64_t)j));
+      int64_t c = (int64_t)(((z >> 32) * span) >> 32);
+      if (c >= r) c += 1;
+      col_indices[j] = (int32_t)c;
+      values[j] = v;
+    }
+  }
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* VectorAdd                                                                                    */
+/* ------------------------------------------------------------------------------------------ */
+
+/* The generator-emitted CPU invoker runs the [Kernel] body `result[i] = a[i] + b[i]` over the
+ * flat range [0, N) on one thread (src/Runtime/DotCompute.Generators/Kernel/Generation/
+ * KernelExecutionMetadataEmitter.cs:117-170, invoked by src/Runtime/DotCompute.Runtime/Services/
+ * KernelExecutionService.cs:275-288). OptimizedVectorAddKernel computes the same sums with
+ * Vector<float> (src/Backends/DotCompute.Backends.CPU/Kernels/Optimized/
+ * OptimizedVectorAddKernel.cs:91-108); one IEEE rounding per element either way. */
+void oracle_vector_add_f32(const float* a, const float* b, float* result, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) result[i] = a[i] + b[i];
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* Sum                                                                                          */
+/* ------------------------------------------------------------------------------------------ */
+
+/* Enumerable.Sum(IEnumerable<float>) as reached from ComputeQueryProvider.Execute's scalar branch
+ * (src/Extensions/DotCompute.Linq/ComputeQueryableExtensions.cs:265-267): a sequential double
+ * accumulator, cast to float at the end (.NET 10 BCL System.Linq, Sum.cs). */
+float oracle_sum_f32_enumerable(const float* x, int64_t n, double* as_double) {
+  double s = 0.0;
+  for (int64_t i = 0; i < n; ++i) s += (double)x[i];
+  if (as_double) *as_double = s;
+  return (float)s;
+}
+
+typedef struct {
+  const float* x;
+  int64_t start, end;
+  double sum;
+} part_arg;
+
+static void* part_worker(void* p) {
+  part_arg* a = (part_arg*)p;
+  double s = 0.0;
+  for (int64_t i = a->start; i < a->end; ++i) s += (double)a->x[i];
+  a->sum = s;
+  return NULL;
+}
+
+/* OptimizedReductionKernel: ProcessorCount contiguous partitions (the last takes the remainder),
+ * each a sequential double sum, run under Parallel.For, then partitionSums.Sum() in partition
+ * order and a float cast (src/Backends/DotCompute.Backends.CPU/Kernels/Optimized/
+ * OptimizedReductionKernel.cs:69-95). One thread per partition here. */
+float oracle_sum_f32_partitioned(const float* x, int64_t n, int32_t partitions, double* as_double) {
+  if (partitions < 1) partitions = 1;
+  part_arg* args = (part_arg*)calloc((size_t)partitions, sizeof(part_arg));
+  pthread_t* th = (pthread_t*)calloc((size_t)partitions, sizeof(pthread_t));
+  int64_t per = n / partitions;
+  for (int32_t p = 0; p < partitions; ++p) {
+    args[p].x = x;
+    args[p].start = (int64_t)p * per;
+    args[p].end = (p == partitions - 1) ? n : args[p].start + per;
+    pthread_create(&th[p], NULL, part_worker, &args[p]);
+  }
+  double total = 0.0;
+  for (int32_t p = 0; p < partitions; ++p) {
+    pthread_join(th[p], NULL);
+    total += args[p].sum;
+  }
+  free(args);
+  free(th);
+  if (as_double) *as_double = total;
+  return (float)total;
+}
+
+/* Neumaier-compensated double sum: the near-exact float64 host reference the fp32 tolerance
+ * rel 1e-5*log2(N) is measured against. */
+double oracle_sum_f32_compensated(const float* x, int64_t n) {
+  double s = 0.0, c = 0.0;
+  for (int64_t i = 0; i < n; ++i) {
+    double v = (double)x[i];
+    double t = s + v;
+    if (fabs(s) >= fabs(v)) c += (s - t) + v; else c += (v - t) + s;
+    s = t;
+  }
+  return s + c;
+}
+
+/* Enumerable.Sum(IEnumerable<int>) is `checked` int32 arithmetic and throws OverflowException
+ * (.NET BCL, reached from ComputeQueryableExtensions.cs:265-267). Returns DC_ERR_OVERFLOW where it
+ * would throw: sequentially, as soon as a running total leaves int32. */
+int32_t oracle_sum_i32_checked(const int32_t* x, int64_t n, int32_t* sum_out) {
+  int64_t s = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    s += x[i];
+    if (s > 2147483647LL || s < -2147483648LL) return DC_ERR_OVERFLOW;
+  }
+  if (sum_out) *sum_out = (int32_t)s;
+  return DC_OK;
+}
+
+int64_t oracle_sum_i32_exact(const int32_t* x, int64_t n) {
+  int64_t s = 0;
+  for (int64_t i = 0; i < n; ++i) s += x[i];
+  return s;
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* LINQ Where -> Select                                                                         */
+/* ------------------------------------------------------------------------------------------ */
+
+/* The configuration's chain written out by hand, as LINQ-to-objects evaluates it after
+ * ComputeQueryProvider.ExecuteTyped falls back (ComputeQueryableExtensions.cs:346-352 ->
+ * ExecuteFallback :628-633 -> Enumerable.Where(...).Select(...).ToArray()): elements visited in
+ * order, `x > 0f` keeps (so -0 and +0 are dropped), `x * 2f + 1f` rounds after each operation. */
+int64_t oracle_where_gt0_select_2x_plus_1(const float* in, int64_t n, float* out) {
+  int64_t k = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    float x = in[i];
+    if (x > 0.0f) {
+      float t = x * 2.0f;
+      out[k++] = t + 1.0f;
+    }
+  }
+  return k;
+}
+
+/* .Where(x > 0f).Select(x * 2f + 1f).Sum(): Enumerable.Sum over the iterator chain (double
+ * accumulator, float result), ComputeQueryableExtensions.cs:265-267. */
+float oracle_where_gt0_select_2x_plus_1_sum(const float* in, int64_t n, int64_t* count, double* as_double) {
+  double s = 0.0;
+  int64_t k = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    float x = in[i];
+    if (x > 0.0f) {
+      float t = x * 2.0f;
+      float y = t + 1.0f;
+      s += (double)y;
+      ++k;
+    }
+  }
+  if (count) *count = k;
+  if (as_double) *as_double = s;
+  return (float)s;
+}
+
+/* MathF.Min/MathF.Max (.NET Core 3.0+): IEEE 754-2019 minimum/maximum, NaN-propagating and
+ * ordering -0 below +0. */
+static float net_min(float a, float b) {
+  if (a != a) return a;
+  if (b != b) return b;
+  if (a == b) return signbit(a) ? a : b;
+  return a < b ? a : b;
+}
+static float net_max(float a, float b) {
+  if (a != a) return a;
+  if (b != b) return b;
+  if (a == b) return signbit(a) ? b : a;
+  return a > b ? a : b;
+}
+
+/* Reference interpreter of the dc_linq_chain register program for ONE element (the program model
+ * is documented in include/dotcompute_hip.h). Returns 1 if the element is kept, 0 if filtered,
+ * negative on a malformed program. */
+int32_t oracle_linq_eval(const dc_linq_chain* chain, float x, float* y_out) {
+  float e = x, v = 0.0f, s0 = 0.0f, s1 = 0.0f;
+  int p = 0, q = 0, keep = 1;
+  if (!chain || chain->n_instr < 0 || chain->n_instr > DC_LINQ_MAX_INSTR) return DC_ERR_INVALID_ARGUMENT;
+  for (int32_t pc = 0; pc < chain->n_instr; ++pc) {
+    const dc_linq_instr* in = &chain->code[pc];
+    float o;
+    switch (in->src) {
+      case DC_LQ_SRC_IMM: o = in->imm; break;
+      case DC_LQ_SRC_ELEM: o = e; break;
+      case DC_LQ_SRC_S0: o = s0; break;
+      case DC_LQ_SRC_S1: o = s1; break;
+      default: return DC_ERR_INVALID_ARGUMENT;
+    }
+    int c = 0, is_cmp = 0;
+    switch (in->op) {
+      case DC_LQ_NOP: break;
+      case DC_LQ_LOAD: v = o; break;
+      case DC_LQ_ADD: v = v + o; break;
+      case DC_LQ_SUB: v = v - o; break;
+      case DC_LQ_RSUB: v = o - v; break;
+      case DC_LQ_MUL: v = v * o; break;
+      case DC_LQ_DIV: v = v / o; break;
+      case DC_LQ_RDIV: v = o / v; break;
+      case DC_LQ_MIN: v = net_min(v, o); break;
+      case DC_LQ_MAX: v = net_max(v, o); break;
+      case DC_LQ_NEG: v = -v; break;
+      case DC_LQ_ABS: v = fabsf(v); break;
+      case DC_LQ_SQRT: v = sqrtf(v); break;
+      case DC_LQ_STORE_S0: s0 = v; break;
+      case DC_LQ_STORE_S1: s1 = v; break;
+      case DC_LQ_CMP_GT: c = v > o; is_cmp = 1; break;
+      case DC_LQ_CMP_GE: c = v >= o; is_cmp = 1; break;
+      case DC_LQ_CMP_LT: c = v < o; is_cmp = 1; break;
+      case DC_LQ_CMP_LE: c = v <= o; is_cmp = 1; break;
+      case DC_LQ_CMP_EQ: c = v == o; is_cmp = 1; break;
+      case DC_LQ_CMP_NE: c = v != o; is_cmp = 1; break;
+      case DC_LQ_PNOT: p = !p; break;
+      case DC_LQ_PSTORE: q = p; break;
+      case DC_LQ_PAND_Q: p = p && q; break;
+      case DC_LQ_POR_Q: p = p || q; break;
+      case DC_LQ_FILTER: keep = keep && p; break;
+      case DC_LQ_MAP: e = v; break;
+      default: return DC_ERR_INVALID_ARGUMENT;
+    }
+    if (is_cmp) {
+      if (in->mode == DC_LQ_CMP_SET) p = c;
+      else if (in->mode == DC_LQ_CMP_AND) p = p && c;
+      else if (in->mode == DC_LQ_CMP_OR) p = p || c;
+      else return DC_ERR_INVALID_ARGUMENT;
+    }
+  }
+  if (y_out) *y_out = e;
+  return keep;
+}
+
+/* LINQ-to-objects Where/Select chain (ComputeQueryableExtensions.cs:628-633): order-preserving
+ * compaction of the kept, mapped elements. Returns the count, or a negative status. */
+int64_t oracle_linq_where_select(const dc_linq_chain* chain, const float* in, int64_t n, float* out) {
+  int64_t k = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    float y;
+    int32_t r = oracle_linq_eval(chain, in[i], &y);
+    if (r < 0) return r;
+    if (r) out[k++] = y;
+  }
+  return k;
+}
+
+float oracle_linq_where_select_sum(const dc_linq_chain* chain, const float* in, int64_t n,
+                                   int64_t* count, double* as_double) {
+  double s = 0.0;
+  int64_t k = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    float y;
+    int32_t r = oracle_linq_eval(chain, in[i], &y);
+    if (r < 0) { if (count) *count = r; return 0.0f; }
+    if (r) { s += (double)y; ++k; }
+  }
+  if (count) *count = k;
+  if (as_double) *as_double = s;
+  return (float)s;
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* GEMM                                                                                          */
+/* ------------------------------------------------------------------------------------------ */
+
+typedef struct {
+  const float* a; const float* b; float* c;
+  int64_t n, k, r0, r1;
+} gemm_arg;
+
+static void* gemm_worker(void* p) {
+  gemm_arg* g = (gemm_arg*)p;
+  for (int64_t i = g->r0; i < g->r1; ++i) {
+    for (int64_t j = 0; j < g->n; ++j) {
+      float sum = 0.0f;
+      for (int64_t l = 0; l < g->k; ++l) sum += g->a[i * g->k + l] * g->b[l * g->n + j];
+      g->c[i * g->n + j] = sum;
+    }
+  }
+  return NULL;
+}
+
+/* OptimizedMatrixMultiplyKernel: Parallel.For over rows i, then j, then a sequential fp32
+ * `sum += A[i*n+k] * B[k*n+j]` (src/Backends/DotCompute.Backends.CPU/Kernels/Optimized/
+ * OptimizedMatrixMultiplyKernel.cs:72-96; square there, general m×k·k×n here). Rows
+ * [row_begin, row_end) only, split over `threads` threads. */
+void oracle_gemm_f32_naive_rows(const float* a, const float* b, float* c, int64_t m, int64_t n,
+                                int64_t k, int64_t row_begin, int64_t row_end, int32_t threads) {
+  (void)m;
+  if (threads < 1) threads = 1;
+  int64_t rows = row_end - row_begin;
+  if (rows <= 0) return;
+  if (threads > rows) threads = (int32_t)rows;
+  gemm_arg* args = (gemm_arg*)calloc((size_t)threads, sizeof(gemm_arg));
+  pthread_t* th = (pthread_t*)calloc((size_t)threads, sizeof(pthread_t));
+  for (int32_t t = 0; t < threads; ++t) {
+    args[t] = (gemm_arg){a, b, c, n, k, row_begin + rows * t / threads, row_begin + rows * (t + 1) / threads};
+    pthread_create(&th[t], NULL, gemm_worker, &args[t]);
+  }
+  for (int32_t t = 0; t < threads; ++t) pthread_join(th[t], NULL);
+  free(args);
+  free(th);
+}
+
+void oracle_gemm_f32_naive(const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k,
+                           int32_t threads) {
+  oracle_gemm_f32_naive_rows(a, b, c, m, n, k, 0, m, threads);
+}
+
+/* MatrixOperations.MultiplyBlocked: 64-blocked i0/j0/k0 loops; the running result[i,j] carries
+ * across k-blocks, so each entry is still a sequential-k fp32 sum
+ * (src/Extensions/DotCompute.Algorithms/LinearAlgebra/Operations/MatrixOperations.cs:570-612). */
+void oracle_gemm_f32_blocked(const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k) {
+  const int64_t B = 64;
+  for (int64_t i = 0; i < m * n; ++i) c[i] = 0.0f;
+  for (int64_t i0 = 0; i0 < m; i0 += B)
+    for (int64_t j0 = 0; j0 < n; j0 += B)
+      for (int64_t k0 = 0; k0 < k; k0 += B) {
+        int64_t im = i0 + B < m ? i0 + B : m;
+        int64_t jm = j0 + B < n ? j0 + B : n;
+        int64_t km = k0 + B < k ? k0 + B : k;
+        for (int64_t i = i0; i < im; ++i)
+          for (int64_t j = j0; j < jm; ++j) {
+            float sum = c[i * n + j];
+            for (int64_t l = k0; l < km; ++l) sum += a[i * k + l] * b[l * n + j];
+            c[i * n + j] = sum;
+          }
+      }
+}
+
+typedef struct {
+  const float* a; const float* b; double* c; double* abs_c;
+  int64_t n, k; const int64_t* rows; int64_t r0, r1;
+} gemm64_arg;
+
+static void* gemm64_worker(void* p) {
+  gemm64_arg* g = (gemm64_arg*)p;
+  double* acc = (double*)calloc((size_t)g->n, sizeof(double));
+  double* aacc = (double*)calloc((size_t)g->n, sizeof(double));
+  for (int64_t t = g->r0; t < g->r1; ++t) {
+    int64_t i = g->rows[t];
+    memset(acc, 0, sizeof(double) * (size_t)g->n);
+    memset(aacc, 0, sizeof(double) * (size_t)g->n);
+    for (int64_t l = 0; l < g->k; ++l) {
+      double av = (double)g->a[i * g->k + l];
+      const float* brow = g->b + l * g->n;
+      for (int64_t j = 0; j < g->n; ++j) {
+        double bv = (double)brow[j];
+        acc[j] += av * bv;
+        aacc[j] += fabs(av * bv);
+      }
+    }
+    memcpy(g->c + t * g->n, acc, sizeof(double) * (size_t)g->n);
+    if (g->abs_c) memcpy(g->abs_c + t * g->n, aacc, sizeof(double) * (size_t)g->n);
+  }
+  free(acc);
+  free(aacc);
+  return NULL;
+}
+
+/* float64 GEMM rows (the tolerance reference): row t of the output holds row rows[t] of A·B, and
+ * abs_c the matching row of |A|·|B| for the per-entry bound. */
+void oracle_gemm_f64_rows(const float* a, const float* b, double* c, double* abs_c, int64_t m,
+                          int64_t n, int64_t k, const int64_t* rows, int64_t n_rows, int32_t threads) {
+  (void)m;
+  if (threads < 1) threads = 1;
+  if (threads > n_rows) threads = (int32_t)(n_rows > 0 ? n_rows : 1);
+  gemm64_arg* args = (gemm64_arg*)calloc((size_t)threads, sizeof(gemm64_arg));
+  pthread_t* th = (pthread_t*)calloc((size_t)threads, sizeof(pthread_t));
+  for (int32_t t = 0; t < threads; ++t) {
+    args[t] = (gemm64_arg){a, b, c, abs_c, n, k, rows, n_rows * t / threads, n_rows * (t + 1) / threads};
+    pthread_create(&th[t], NULL, gemm64_worker, &args[t]);
+  }
+  for (int32_t t = 0; t < threads; ++t) pthread_join(th[t], NULL);
+  free(args);
+  free(th);
+}
+
+/* IEEE binary32 -> bfloat16, round to nearest even on the dropped 16 bits; NaN stays a quiet NaN. */
+uint16_t oracle_f32_to_bf16(float x) {
+  uint32_t u;
+  memcpy(&u, &x, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
+  uint32_t lsb = (u >> 16) & 1u;
+  u += 0x7fffu + lsb;
+  return (uint16_t)(u >> 16);
+}
+
+float oracle_bf16_to_f32(uint16_t h) {
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+void oracle_f32_to_bf16_array(const float* x, uint16_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = oracle_f32_to_bf16(x[i]);
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* SpMV                                                                                          */
+/* ------------------------------------------------------------------------------------------ */
+
+/* SparseOps.SpMV<T>: throws when A.Columns != x.Length, then per row a sequential
+ * `sum += Values[i] * x[ColumnIndices[i]]` in T = float, y[row] = sum
+ * (src/Extensions/DotCompute.Algorithms/Sparse/SparseMatrix.cs:669-692). */
+int32_t oracle_spmv_csr_f32(const int32_t* row_pointers, const int32_t* col_indices, const float* values,
+                            const float* x, float* y, int64_t rows, int64_t cols, int64_t x_len) {
+  if (cols != x_len) return DC_ERR_DIMENSION;
+  for (int64_t r = 0; r < rows; ++r) {
+    float sum = 0.0f;
+    for (int32_t i = row_pointers[r]; i < row_pointers[r + 1]; ++i) sum += values[i] * x[col_indices[i]];
+    y[r] = sum;
+  }
+  return DC_OK;
+}
+
+void oracle_spmv_csr_f64(const int32_t* row_pointers, const int32_t* col_indices, const float* values,
+                         const double* x, double* y, int64_t rows) {
+  for (int64_t r = 0; r < rows; ++r) {
+    double sum = 0.0;
+    for (int32_t i = row_pointers[r]; i < row_pointers[r + 1]; ++i) sum += (double)values[i] * x[col_indices[i]];
+    y[r] = sum;
+  }
+}
+
+/* The SpMV benchmark's power iteration: `iterations` times y = SpMV(A, x) (as above), then the
+ * L1 normalisation x = y / sum(y) with the sum in float64 and each quotient rounded to float. */
+int32_t oracle_spmv_power_f32(const int32_t* row_pointers, const int32_t* col_indices, const float* values,
+                              float* x, float* y, int64_t rows, int32_t iterations, double* last_sum) {
+  double s = 0.0;
+  for (int32_t it = 0; it < iterations; ++it) {
+    oracle_spmv_csr_f32(row_pointers, col_indices, values, x, y, rows, rows, rows);
+    s = 0.0;
+    for (int64_t r = 0; r < rows; ++r) s += (double)y[r];
+    for (int64_t r = 0; r < rows; ++r) x[r] = (float)((double)y[r] / s);
+  }
+  if (last_sum) *last_sum = s;
+  return DC_OK;
+}

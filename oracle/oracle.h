@@ -1,0 +1,87 @@
+/*
+ * oracle.h — CPU restatement of the DotCompute reference semantics for the HIP hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
+ * may load liboracle.so, and only as the checker (or as the timed CPU baseline). The HIP product
+ * path never calls it.
+ *
+ * The reference (mivertowski/DotCompute) is C#/.NET 10; there is no .NET SDK in this image, so
+ * the reference cannot be compiled or run here (oracle/_ref stays empty). Each function below
+ * cites the reference file:line whose behaviour it restates; the inputs come from this build's
+ * own counter-based generators (the reference's System.Random streams are BCL-internal).
+ *
+ * Pinning (what each function is checked against in tests/test_oracle.py):
+ *   generators ........ golden fixtures (tests/golden), splitmix64 published test vectors,
+ *                       distribution moments, Zipf CDF closed form
+ *   vector_add ........ reference known-answer tests, closed form
+ *   sum_f32 ............ reference known answers (Sum 1..5 = 15, Sum 1..1000 = 500500), exact
+ *                       integer-valued floats, math.fsum / Neumaier, permutation invariance
+ *   sum_i32 ............ exact Python int sum, overflow boundaries
+ *   linq ............... reference LINQ golden vectors ({1..5}.Where(x>3) -> {4,5}, ...), numpy
+ *                       boolean-mask evaluation, hand-written lambdas vs the program interpreter
+ *   gemm ............... numpy float64 matmul, identity/permutation matrices, rank-1 closed form
+ *   spmv ............... dense brute force (numpy) on small graphs, stochastic-matrix invariants
+ */
+#ifndef DC_ORACLE_H
+#define DC_ORACLE_H
+
+#include <stdint.h>
+
+#include "../include/dotcompute_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- generators (this build's input spec) ---- */
+uint64_t oracle_splitmix64(uint64_t z);
+void oracle_gen_uniform_f32(float* dst, int64_t n, uint64_t seed, uint32_t stream, int32_t unit_interval);
+void oracle_gen_uniform_i32(int32_t* dst, int64_t n, uint64_t seed, uint32_t stream, int32_t lo, int32_t hi);
+int64_t oracle_gen_zipf_rowptr(int64_t rows, double alpha, int32_t max_degree, uint64_t seed,
+                               int32_t* row_pointers);
+void oracle_gen_zipf_fill(int64_t rows, int64_t cols, uint64_t seed, const int32_t* row_pointers,
+                          int32_t* col_indices, float* values);
+
+/* ---- VectorAdd ---- */
+void oracle_vector_add_f32(const float* a, const float* b, float* result, int64_t n);
+
+/* ---- Sum ---- */
+float oracle_sum_f32_enumerable(const float* x, int64_t n, double* as_double);
+float oracle_sum_f32_partitioned(const float* x, int64_t n, int32_t partitions, double* as_double);
+double oracle_sum_f32_compensated(const float* x, int64_t n);
+int32_t oracle_sum_i32_checked(const int32_t* x, int64_t n, int32_t* sum_out);
+int64_t oracle_sum_i32_exact(const int32_t* x, int64_t n);
+
+/* ---- LINQ Where/Select ---- */
+int64_t oracle_where_gt0_select_2x_plus_1(const float* in, int64_t n, float* out);
+float oracle_where_gt0_select_2x_plus_1_sum(const float* in, int64_t n, int64_t* count, double* as_double);
+int32_t oracle_linq_eval(const dc_linq_chain* chain, float x, float* y_out);
+int64_t oracle_linq_where_select(const dc_linq_chain* chain, const float* in, int64_t n, float* out);
+float oracle_linq_where_select_sum(const dc_linq_chain* chain, const float* in, int64_t n,
+                                   int64_t* count, double* as_double);
+
+/* ---- GEMM ---- */
+void oracle_gemm_f32_naive(const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k,
+                           int32_t threads);
+void oracle_gemm_f32_naive_rows(const float* a, const float* b, float* c, int64_t m, int64_t n,
+                                int64_t k, int64_t row_begin, int64_t row_end, int32_t threads);
+void oracle_gemm_f32_blocked(const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k);
+void oracle_gemm_f64_rows(const float* a, const float* b, double* c, double* abs_c, int64_t m,
+                          int64_t n, int64_t k, const int64_t* rows, int64_t n_rows, int32_t threads);
+uint16_t oracle_f32_to_bf16(float x);
+float oracle_bf16_to_f32(uint16_t h);
+void oracle_f32_to_bf16_array(const float* x, uint16_t* out, int64_t n);
+
+/* ---- SpMV ---- */
+int32_t oracle_spmv_csr_f32(const int32_t* row_pointers, const int32_t* col_indices, const float* values,
+                            const float* x, float* y, int64_t rows, int64_t cols, int64_t x_len);
+void oracle_spmv_csr_f64(const int32_t* row_pointers, const int32_t* col_indices, const float* values,
+                         const double* x, double* y, int64_t rows);
+int32_t oracle_spmv_power_f32(const int32_t* row_pointers, const int32_t* col_indices, const float* values,
+                              float* x, float* y, int64_t rows, int32_t iterations, double* last_sum);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

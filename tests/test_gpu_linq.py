@@ -1,0 +1,220 @@
+"""GPU parity: fused Where/Select -> ToArray (order-preserving compaction) and -> Sum.
+
+The benchmark chain is src.AsComputeQueryable().Where(x => x > 0f).Select(x => x * 2f + 1f);
+count, order and every output bit must equal LINQ-to-objects (the reference's fallback path,
+ComputeQueryableExtensions.cs:628-633), which the oracle restates by hand. Random programs are
+checked against the oracle's interpreter. Sums: rel 1e-5*log2(N) vs the float64 host sum.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from dotcompute_amd import hip
+from dotcompute_amd.hip import (ABS, ADD, CMP_AND, CMP_EQ, CMP_GE, CMP_GT, CMP_LE, CMP_LT, CMP_NE, CMP_OR, DIV,
+                                FILTER, LOAD, MAP, MAX, MIN, MUL, NEG, PAND_Q, PNOT, POR_Q, PSTORE, RDIV, RSUB,
+                                SQRT, SRC_ELEM, SRC_IMM, SRC_S0, SRC_S1, STORE_S0, STORE_S1, SUB, LinqChain)
+
+pytestmark = pytest.mark.gpu
+
+CHAIN = hip.where_gt0_select_2x_plus_1()
+
+
+def run_to_array(ctx, chain, x, offset=0):
+    n = x.size
+    dx = ctx.empty(n + offset + 1, np.float32)
+    if n:
+        hip.check(hip.load().dc_hip_memcpy_h2d_async(ctx.handle, dx.ptr + 4 * offset, x.ctypes.data, x.nbytes), "h2d")
+    src = hip.DeviceArray(ctx, dx.ptr + 4 * offset, 4 * n, np.dtype(np.float32), (n,))
+    out = ctx.empty(n + 1, np.float32)
+    cnt = ctx.empty(1, np.int64)
+    ctx.where_select_f32(chain, src, out, cnt, n)
+    ctx.synchronize()
+    k = int(cnt.to_host()[0])
+    got = out.to_host(k) if k else np.empty(0, np.float32)
+    for a in (dx, out, cnt):
+        ctx.free(a)
+    return got
+
+
+def run_sum(ctx, chain, x):
+    n = x.size
+    dx = ctx.to_device(x) if n else ctx.empty(1, np.float32)
+    s = ctx.empty(1, np.float64)
+    c = ctx.empty(1, np.int64)
+    ctx.where_select_sum_f32(chain, dx, s, c, n)
+    ctx.synchronize()
+    res = (s.to_host()[0], int(c.to_host()[0]))
+    for a in (dx, s, c):
+        ctx.free(a)
+    return res
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def same_floats(a, b) -> bool:
+    """Bit-for-bit equality, except that any two NaNs match (x86 and CDNA produce different
+    default NaN payloads; .NET exposes no payload semantics)."""
+    a, b = np.ascontiguousarray(a, np.float32), np.ascontiguousarray(b, np.float32)
+    if a.shape != b.shape:
+        return False
+    nan = np.isnan(a)
+    return bool(np.array_equal(nan, np.isnan(b)) and np.array_equal(bits(a[~nan]), bits(b[~nan])))
+
+
+@pytest.mark.parametrize("n", [0, 1, 2, 63, 64, 4095, 4096, 4097, 12_289, 1_000_000, 16_000_000])
+def test_where_select_to_array_bit_exact(ctx, n):
+    x = oracle.gen_uniform_f32(n, 42 + 2, 0)
+    got = run_to_array(ctx, CHAIN, x)
+    ref = oracle.where_gt0_select_2x_plus_1(x)
+    assert got.size == ref.size
+    assert np.array_equal(bits(got), bits(ref))
+
+
+def test_where_select_misaligned_input(ctx):
+    x = oracle.gen_uniform_f32(10_000, 5, 0)
+    got = run_to_array(ctx, CHAIN, x, offset=1)
+    assert np.array_equal(bits(got), bits(oracle.where_gt0_select_2x_plus_1(x)))
+
+
+def test_where_select_signed_zero_and_extremes(ctx):
+    x = np.array([0.0, -0.0, 1e-45, -1e-45, 3.4e38, -3.4e38, np.inf, -np.inf, np.nan, 1.0, -1.0] * 500, np.float32)
+    got = run_to_array(ctx, CHAIN, x)
+    ref = oracle.where_gt0_select_2x_plus_1(x)
+    assert np.array_equal(bits(got), bits(ref))  # +inf*2+1 = inf; 3.4e38*2 = inf
+
+
+def test_reference_linq_golden_vectors(ctx):
+    """Known answers of the reference LINQ tests, on the GPU."""
+    def chain_gt_mul(t, m):
+        return LinqChain.assemble([(LOAD, SRC_ELEM, 0), (CMP_GT, SRC_IMM, t), (FILTER, SRC_IMM, 0),
+                                   (LOAD, SRC_ELEM, 0), (MUL, SRC_IMM, m), (MAP, SRC_IMM, 0)])
+    # ComputeQueryProviderTests.cs:341-365: {1..5}.Where(x > 3) -> {4, 5}
+    w = LinqChain.assemble([(LOAD, SRC_ELEM, 0), (CMP_GT, SRC_IMM, 3), (FILTER, SRC_IMM, 0)])
+    assert run_to_array(ctx, w, np.arange(1, 6, dtype=np.float32)).tolist() == [4, 5]
+    # {1,2,3}.Select(x * 2) -> {2,4,6}
+    s = LinqChain.assemble([(LOAD, SRC_ELEM, 0), (MUL, SRC_IMM, 2), (MAP, SRC_IMM, 0)])
+    assert run_to_array(ctx, s, np.array([1, 2, 3], np.float32)).tolist() == [2, 4, 6]
+    # LinqBackendIntegrationTests.cs:51-66: {1..5}.Where(x > 2).Select(x * 2) -> {6, 8, 10}
+    assert run_to_array(ctx, chain_gt_mul(2, 2), np.arange(1, 6, dtype=np.float32)).tolist() == [6, 8, 10]
+    # :139-161: {1..10}.Where(x > 3).Select(x * 3) -> {12, ..., 30}
+    assert run_to_array(ctx, chain_gt_mul(3, 3), np.arange(1, 11, dtype=np.float32)).tolist() == list(range(12, 31, 3))
+    # :309-325: 1..100 .Where(x % 2 == 0).Select(x * x): count 50, first 4, last 10000.
+    # The op set has no remainder; for integer-valued x < 2^22, x is even exactly when rounding
+    # x * 0.5 to an integer (adding and subtracting 2^23) and doubling gives x back.
+    xs = np.arange(1, 101, dtype=np.float32)
+    even = LinqChain.assemble([(LOAD, SRC_ELEM, 0), (STORE_S0, SRC_IMM, 0), (MUL, SRC_IMM, 0.5),
+                               (ADD, SRC_IMM, 8388608.0), (SUB, SRC_IMM, 8388608.0), (MUL, SRC_IMM, 2.0),
+                               (CMP_EQ, SRC_S0, 0), (FILTER, SRC_IMM, 0),
+                               (LOAD, SRC_ELEM, 0), (MUL, SRC_ELEM, 0), (MAP, SRC_IMM, 0)])
+    got = run_to_array(ctx, even, xs)
+    assert got.size == 50 and got[0] == 4 and got[-1] == 10000
+    assert np.array_equal(got, oracle.linq_where_select(even, xs))
+    # Sum(1..1000) = 500500 through the fused Sum kernel with an empty chain
+    empty = LinqChain.assemble([])
+    ssum, cnt = run_sum(ctx, empty, np.arange(1, 1001, dtype=np.float32))
+    assert ssum == 500500.0 and cnt == 1000
+
+
+@pytest.mark.parametrize("n", [0, 1, 1000, 1_000_000, 16_000_000])
+def test_where_select_sum(ctx, n):
+    x = oracle.gen_uniform_f32(n, 44, 0)
+    got, cnt = run_sum(ctx, CHAIN, x)
+    f32_ref, seq_double, ref_cnt = oracle.where_gt0_select_2x_plus_1_sum(x)
+    assert cnt == ref_cnt
+    tol = 1e-5 * max(1.0, math.log2(max(n, 2)))
+    assert abs(got - seq_double) <= tol * max(abs(seq_double), 1e-30) + 1e-12
+
+
+def _random_program(rng):
+    """A random but well-formed program: 1-3 stages, each a filter or a map."""
+    code = []
+    uses_saves = bool(rng.integers(0, 2))
+    for _ in range(int(rng.integers(1, 4))):
+        if rng.integers(0, 2):  # filter
+            code.append((LOAD, SRC_ELEM, 0))
+            code.append((int(rng.choice([CMP_GT, CMP_GE, CMP_LT, CMP_LE, CMP_NE])), SRC_IMM,
+                         float(rng.uniform(-1, 1)), 0))
+            if rng.integers(0, 2):
+                code.append((PSTORE, SRC_IMM, 0))
+                code.append((LOAD, SRC_ELEM, 0))
+                code.append((ABS, SRC_IMM, 0))
+                code.append((CMP_LT, SRC_IMM, float(rng.uniform(0.2, 1.0)), int(rng.choice([CMP_AND, CMP_OR]))))
+                code.append((int(rng.choice([PAND_Q, POR_Q])), SRC_IMM, 0))
+            if rng.integers(0, 4) == 0:
+                code.append((PNOT, SRC_IMM, 0))
+            code.append((FILTER, SRC_IMM, 0))
+        else:  # map
+            code.append((LOAD, SRC_ELEM, 0))
+            for _ in range(int(rng.integers(1, 5))):
+                op = int(rng.choice([ADD, SUB, RSUB, MUL, DIV, RDIV, MIN, MAX, NEG, ABS, SQRT]))
+                src = SRC_IMM
+                if uses_saves and rng.integers(0, 3) == 0:
+                    code.append((STORE_S0, SRC_IMM, 0))
+                    src = SRC_S0
+                elif rng.integers(0, 4) == 0:
+                    src = SRC_ELEM
+                code.append((op, src, float(rng.uniform(-2, 2))))
+            if uses_saves:
+                code.append((STORE_S1, SRC_IMM, 0))
+                code.append((ADD, SRC_S1, 0))
+            code.append((MAP, SRC_IMM, 0))
+    return LinqChain.assemble(code)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_programs_match_interpreter(ctx, seed):
+    rng = np.random.default_rng(seed)
+    prog = _random_program(rng)
+    assert hip.load().dc_linq_chain_validate(prog) == 0
+    x = oracle.gen_uniform_f32(50_000 + seed * 977, 100 + seed, 0)
+    got = run_to_array(ctx, prog, x)
+    ref = oracle.linq_where_select(prog, x)
+    assert got.size == ref.size
+    assert same_floats(got, ref)
+    s, c = run_sum(ctx, prog, x)
+    _, sd, rc = oracle.linq_where_select_sum(prog, x)
+    assert c == rc
+    if np.isfinite(sd):
+        assert abs(s - sd) <= 1e-5 * math.log2(x.size) * max(abs(sd), 1.0)
+
+
+def test_invalid_program_rejected(ctx):
+    bad = LinqChain.assemble([(99, SRC_IMM, 0)])
+    x = ctx.empty(16, np.float32)
+    out = ctx.empty(16, np.float32)
+    cnt = ctx.empty(1, np.int64)
+    with pytest.raises(hip.HipError) as e:
+        ctx.where_select_f32(bad, x, out, cnt, 16)
+    assert e.value.status == hip.DC_ERR_UNSUPPORTED
+    for a in (x, out, cnt):
+        ctx.free(a)
+
+
+@pytest.mark.slow
+def test_where_select_256m(ctx):
+    n = 256 * 1024 * 1024
+    dx = ctx.empty(n, np.float32)
+    ctx.fill_uniform_f32(dx, seed=44, stream=0)
+    out = ctx.empty(n, np.float32)
+    cnt = ctx.empty(1, np.int64)
+    ctx.where_select_f32(CHAIN, dx, out, cnt)
+    ctx.synchronize()
+    k = int(cnt.to_host()[0])
+    x = oracle.gen_uniform_f32(n, 44, 0)
+    ref = oracle.where_gt0_select_2x_plus_1(x)
+    del x
+    assert k == ref.size
+    assert np.array_equal(bits(out.to_host(k)), bits(ref))
+    s = ctx.empty(1, np.float64)
+    c = ctx.empty(1, np.int64)
+    ctx.where_select_sum_f32(CHAIN, dx, s, c)
+    ctx.synchronize()
+    assert int(c.to_host()[0]) == k
+    ref_sum = float(np.sum(ref, dtype=np.float64))
+    assert abs(s.to_host()[0] - ref_sum) <= 1e-5 * 28 * abs(ref_sum)
+    for a in (dx, out, cnt, s, c):
+        ctx.free(a)
