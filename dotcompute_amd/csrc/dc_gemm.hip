@@ -1,7 +1,420 @@
-// dc_gemm.hip — placeholder until the MFMA GEMM lands.
+// dc_gemm.hip — dense row-major GEMM C[m×n] = A[m×k]·B[k×n] on the gfx950 matrix cores.
+//
+// fp32: v_mfma_f32_32x32x2_f32 (fp32 inputs, fp32 accumulate).
+// bf16: v_mfma_f32_32x32x16_bf16 (bf16 inputs, fp32 accumulate).
+//
+// Block tile 128×128, 256 threads = 4 waves, each wave a 64×64 sub-tile = 2×2 MFMA 32×32 tiles
+// (64 fp32 accumulators per lane). K advances BK elements per iteration through a double-buffered
+// LDS tile; the next tile's global loads are issued before the current tile's MFMAs and stored
+// to the other buffer afterwards, so there is one barrier per iteration.
+//
+// Operand layout. For a 32×32 MFMA lane l supplies row (A) / column (B) l % 32 and the k-group
+// h = l / 32; the instruction pairs A and B values by (h, element index), so any assignment of
+// actual k indices to (h, element) is valid as long as A and B agree. Here lane group h takes
+// the 8 consecutive k's [8h, 8h+8) of each 16-wide k step: with A held in LDS as As[m][k] and B
+// transposed as Bs[n][k] (row pitch BK+4 floats), a lane's operands for 8 MFMAs are two
+// contiguous 16-byte LDS reads, bank-conflict free (row pitch 80 B maps 8 rows onto disjoint banks).
+//
+// Tile order: consecutive workgroups are dispatched round-robin over the 8 XCDs (each with its own
+// L2). Block b is mapped to tile (b % 8) * (T / 8) + b / 8, so each XCD works on a contiguous
+// range of tiles, and within it tiles are walked in groups of 8 tile-rows, column by column, so
+// the blocks resident on one XCD share A row-panels and B column-panels in that XCD's L2.
+#include <algorithm>
+
+#include "dc_device.hpp"
 #include "dc_internal.hpp"
-extern "C" {
-DC_HIP_API int32_t dc_hip_gemm_f32(dc_hip_ctx*, const float*, const float*, float*, int64_t, int64_t, int64_t) { return DC_ERR_UNSUPPORTED; }
-DC_HIP_API int32_t dc_hip_gemm_bf16(dc_hip_ctx*, const uint16_t*, const uint16_t*, float*, int64_t, int64_t, int64_t) { return DC_ERR_UNSUPPORTED; }
-DC_HIP_API int32_t dc_hip_convert_f32_to_bf16(dc_hip_ctx*, const float*, uint16_t*, int64_t) { return DC_ERR_UNSUPPORTED; }
+
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBM = 128;
+constexpr int kBN = 128;
+constexpr int kThreads = 256;
+constexpr int kGroupM = 8;
+
+struct TileCoord {
+  int tm, tn;
+};
+
+__device__ inline TileCoord map_tile(int tiles_m, int tiles_n) {
+  const int total = tiles_m * tiles_n;
+  int b = blockIdx.x;
+  int t = (total % 8 == 0) ? (b % 8) * (total / 8) + b / 8 : b;
+  const int group = kGroupM * tiles_n;
+  const int g = t / group;
+  const int first_m = g * kGroupM;
+  const int gm = min(tiles_m - first_m, kGroupM);
+  const int in_g = t - g * group;
+  return TileCoord{first_m + in_g % gm, in_g / gm};
 }
+
+// ---------------------------------------------------------------------------------------------
+// fp32
+// ---------------------------------------------------------------------------------------------
+template <int BK>
+struct F32Smem {
+  static constexpr int kPitch = BK + 4;  // floats per LDS row
+  float a[2][kBM][kPitch];
+  float b[2][kBN][kPitch];
+};
+
+// Global -> register prefetch for one BK slice. A: (128 rows × BK) as float4 slots,
+// slot s -> row s / (BK/4), kq = s % (BK/4). B: (BK × 128) as float4 slots, slot s ->
+// nq = s / BK, k = s % BK (a wave covers 16 k-rows × 4 column quads, which spreads the transposed
+// LDS writes over the banks).
+template <int BK, bool CHECKED>
+struct F32Loader {
+  static constexpr int kASlots = kBM * BK / 4 / kThreads;
+  static constexpr int kBSlots = kBN * BK / 4 / kThreads;
+  dc::f32x4 ra[kASlots];
+  dc::f32x4 rb[kBSlots];
+
+  __device__ inline void load(const float* __restrict__ A, const float* __restrict__ B, int M, int N, int K,
+                              int m0, int n0, int k0, int tid) {
+#pragma unroll
+    for (int i = 0; i < kASlots; ++i) {
+      const int s = tid + i * kThreads;
+      const int row = s / (BK / 4), kq = s % (BK / 4);
+      const int gm = m0 + row, gk = k0 + 4 * kq;
+      if (!CHECKED) {
+        ra[i] = *reinterpret_cast<const dc::f32x4*>(A + (size_t)gm * K + gk);
+      } else {
+        dc::f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        if (gm < M) {
+          const float* p = A + (size_t)gm * K;
+          if (gk + 0 < K) v.x = p[gk + 0];
+          if (gk + 1 < K) v.y = p[gk + 1];
+          if (gk + 2 < K) v.z = p[gk + 2];
+          if (gk + 3 < K) v.w = p[gk + 3];
+        }
+        ra[i] = v;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kBSlots; ++i) {
+      const int s = tid + i * kThreads;
+      const int nq = s / BK, k = s % BK;
+      const int gk = k0 + k, gn = n0 + 4 * nq;
+      if (!CHECKED) {
+        rb[i] = *reinterpret_cast<const dc::f32x4*>(B + (size_t)gk * N + gn);
+      } else {
+        dc::f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        if (gk < K) {
+          const float* p = B + (size_t)gk * N;
+          if (gn + 0 < N) v.x = p[gn + 0];
+          if (gn + 1 < N) v.y = p[gn + 1];
+          if (gn + 2 < N) v.z = p[gn + 2];
+          if (gn + 3 < N) v.w = p[gn + 3];
+        }
+        rb[i] = v;
+      }
+    }
+  }
+
+  __device__ inline void store(F32Smem<BK>& sm, int buf, int tid) {
+#pragma unroll
+    for (int i = 0; i < kASlots; ++i) {
+      const int s = tid + i * kThreads;
+      const int row = s / (BK / 4), kq = s % (BK / 4);
+      *reinterpret_cast<dc::f32x4*>(&sm.a[buf][row][4 * kq]) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < kBSlots; ++i) {
+      const int s = tid + i * kThreads;
+      const int nq = s / BK, k = s % BK;
+      sm.b[buf][4 * nq + 0][k] = rb[i].x;
+      sm.b[buf][4 * nq + 1][k] = rb[i].y;
+      sm.b[buf][4 * nq + 2][k] = rb[i].z;
+      sm.b[buf][4 * nq + 3][k] = rb[i].w;
+    }
+  }
+};
+
+template <int BK, bool CHECKED>
+__global__ __launch_bounds__(kThreads, 2) void gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B,
+                                                               float* __restrict__ C, int M, int N, int K, int tiles_m,
+                                                               int tiles_n) {
+  __shared__ F32Smem<BK> sm;
+  const TileCoord tc = map_tile(tiles_m, tiles_n);
+  const int m0 = tc.tm * kBM, n0 = tc.tn * kBN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int r = lane & 31, h = lane >> 5;
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  F32Loader<BK, CHECKED> ld;
+  const int kt_count = (K + BK - 1) / BK;
+  ld.load(A, B, M, N, K, m0, n0, 0, tid);
+  ld.store(sm, 0, tid);
+  __syncthreads();
+
+  for (int kt = 0; kt < kt_count; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < kt_count) ld.load(A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
+#pragma unroll
+    for (int ks = 0; ks < BK; ks += 16) {
+      dc::f32x4 a[2][2], b[2][2];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const float* p = &sm.a[buf][wm * 64 + mt * 32 + r][ks + 8 * h];
+        a[mt][0] = *reinterpret_cast<const dc::f32x4*>(p);
+        a[mt][1] = *reinterpret_cast<const dc::f32x4*>(p + 4);
+      }
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        const float* p = &sm.b[buf][wn * 64 + nt * 32 + r][ks + 8 * h];
+        b[nt][0] = *reinterpret_cast<const dc::f32x4*>(p);
+        b[nt][1] = *reinterpret_cast<const dc::f32x4*>(p + 4);
+      }
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int nt = 0; nt < 2; ++nt)
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[mt][kk >> 2][kk & 3], b[nt][kk >> 2][kk & 3],
+                                                               acc[mt][nt], 0, 0, 0);
+      }
+    }
+    if (kt + 1 < kt_count) ld.store(sm, buf ^ 1, tid);
+    __syncthreads();
+  }
+
+  // acc[mt][nt][v] holds C[row][col], row = 8*(v/4) + 4*h + v%4, col = r (within the 32×32 tile).
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const int col = n0 + wn * 64 + nt * 32 + r;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int row = m0 + wm * 64 + mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (!CHECKED || (row < M && col < N)) C[(size_t)row * N + col] = acc[mt][nt][v];
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// bf16 (inputs as raw bf16 bit patterns), fp32 accumulate
+// ---------------------------------------------------------------------------------------------
+template <int BK>
+struct Bf16Smem {
+  static constexpr int kPitch = BK + 8;  // bf16 elements per LDS row (16-byte aligned rows)
+  unsigned short a[2][kBM][kPitch];
+  unsigned short b[2][kBN][kPitch];
+};
+
+template <int BK, bool CHECKED>
+struct Bf16Loader {
+  // 8 bf16 (16 bytes) per slot.
+  static constexpr int kASlots = kBM * BK / 8 / kThreads;
+  static constexpr int kBSlots = kBN * BK / 8 / kThreads;
+  u16x8 ra[kASlots];
+  u16x8 rb[kBSlots];
+
+  __device__ inline void load(const unsigned short* __restrict__ A, const unsigned short* __restrict__ B, int M, int N,
+                              int K, int m0, int n0, int k0, int tid) {
+#pragma unroll
+    for (int i = 0; i < kASlots; ++i) {
+      const int s = tid + i * kThreads;
+      const int row = s / (BK / 8), kq = s % (BK / 8);
+      const int gm = m0 + row, gk = k0 + 8 * kq;
+      if (!CHECKED) {
+        ra[i] = *reinterpret_cast<const u16x8*>(A + (size_t)gm * K + gk);
+      } else {
+        u16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (gm < M) {
+          const unsigned short* p = A + (size_t)gm * K;
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (gk + e < K) v[e] = p[gk + e];
+        }
+        ra[i] = v;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kBSlots; ++i) {
+      const int s = tid + i * kThreads;
+      const int nq = s / BK, k = s % BK;
+      const int gk = k0 + k, gn = n0 + 8 * nq;
+      if (!CHECKED) {
+        rb[i] = *reinterpret_cast<const u16x8*>(B + (size_t)gk * N + gn);
+      } else {
+        u16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (gk < K) {
+          const unsigned short* p = B + (size_t)gk * N;
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (gn + e < N) v[e] = p[gn + e];
+        }
+        rb[i] = v;
+      }
+    }
+  }
+
+  __device__ inline void store(Bf16Smem<BK>& sm, int buf, int tid) {
+#pragma unroll
+    for (int i = 0; i < kASlots; ++i) {
+      const int s = tid + i * kThreads;
+      const int row = s / (BK / 8), kq = s % (BK / 8);
+      *reinterpret_cast<u16x8*>(&sm.a[buf][row][8 * kq]) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < kBSlots; ++i) {
+      const int s = tid + i * kThreads;
+      const int nq = s / BK, k = s % BK;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sm.b[buf][8 * nq + e][k] = rb[i][e];
+    }
+  }
+};
+
+template <int BK, bool CHECKED>
+__global__ __launch_bounds__(kThreads, 2) void gemm_bf16_kernel(const unsigned short* __restrict__ A,
+                                                                const unsigned short* __restrict__ B,
+                                                                float* __restrict__ C, int M, int N, int K,
+                                                                int tiles_m, int tiles_n) {
+  __shared__ Bf16Smem<BK> sm;
+  const TileCoord tc = map_tile(tiles_m, tiles_n);
+  const int m0 = tc.tm * kBM, n0 = tc.tn * kBN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int r = lane & 31, h = lane >> 5;
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  Bf16Loader<BK, CHECKED> ld;
+  const int kt_count = (K + BK - 1) / BK;
+  ld.load(A, B, M, N, K, m0, n0, 0, tid);
+  ld.store(sm, 0, tid);
+  __syncthreads();
+
+  for (int kt = 0; kt < kt_count; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < kt_count) ld.load(A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
+#pragma unroll
+    for (int ks = 0; ks < BK; ks += 16) {
+      bf16x8 a[2], b[2];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+        a[mt] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(&sm.a[buf][wm * 64 + mt * 32 + r][ks + 8 * h]));
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+        b[nt] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(&sm.b[buf][wn * 64 + nt * 32 + r][ks + 8 * h]));
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[mt], b[nt], acc[mt][nt], 0, 0, 0);
+    }
+    if (kt + 1 < kt_count) ld.store(sm, buf ^ 1, tid);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const int col = n0 + wn * 64 + nt * 32 + r;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int row = m0 + wm * 64 + mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (!CHECKED || (row < M && col < N)) C[(size_t)row * N + col] = acc[mt][nt][v];
+      }
+    }
+}
+
+// Round-to-nearest-even fp32 -> bf16 (quiet NaN kept NaN).
+__global__ __launch_bounds__(256) void f32_to_bf16_kernel(const float* __restrict__ x, unsigned short* __restrict__ y,
+                                                          int64_t n) {
+  int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) {
+    uint32_t u = __builtin_bit_cast(uint32_t, x[i]);
+    unsigned short h;
+    if ((u & 0x7fffffffu) > 0x7f800000u) {
+      h = (unsigned short)((u >> 16) | 0x0040u);
+    } else {
+      u += 0x7fffu + ((u >> 16) & 1u);
+      h = (unsigned short)(u >> 16);
+    }
+    y[i] = h;
+  }
+}
+
+constexpr int kBKf32 = 32;
+constexpr int kBKbf16 = 64;
+
+int32_t check_dims(int64_t m, int64_t n, int64_t k) {
+  if (m < 0 || n < 0 || k < 0) return DC_ERR_INVALID_ARGUMENT;
+  if (m > INT32_MAX / 2 || n > INT32_MAX / 2 || k > INT32_MAX / 2) return DC_ERR_INVALID_ARGUMENT;
+  return DC_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+DC_HIP_API int32_t dc_hip_gemm_f32(dc_hip_ctx* ctx, const float* a, const float* b, float* c, int64_t m, int64_t n,
+                                   int64_t k) {
+  DC_RETURN_IF(check_dims(m, n, k));
+  if (m == 0 || n == 0) return ctx ? DC_OK : DC_ERR_INVALID_ARGUMENT;
+  if (!c || (k > 0 && (!a || !b))) return DC_ERR_INVALID_ARGUMENT;
+  DC_CTX_ENTER(ctx);
+  if (k == 0) return dc::zero_async(ctx, c, (size_t)(m * n) * sizeof(float));
+  const int tiles_m = (int)((m + kBM - 1) / kBM), tiles_n = (int)((n + kBN - 1) / kBN);
+  const unsigned grid = (unsigned)(tiles_m * tiles_n);
+  const bool full = (m % kBM == 0) && (n % kBN == 0) && (k % kBKf32 == 0) && dc::aligned16(a) && dc::aligned16(b);
+  if (full)
+    gemm_f32_kernel<kBKf32, false><<<grid, kThreads, 0, ctx->stream>>>(a, b, c, (int)m, (int)n, (int)k, tiles_m, tiles_n);
+  else
+    gemm_f32_kernel<kBKf32, true><<<grid, kThreads, 0, ctx->stream>>>(a, b, c, (int)m, (int)n, (int)k, tiles_m, tiles_n);
+  return dc::last_launch_status();
+}
+
+DC_HIP_API int32_t dc_hip_gemm_bf16(dc_hip_ctx* ctx, const uint16_t* a, const uint16_t* b, float* c, int64_t m,
+                                    int64_t n, int64_t k) {
+  DC_RETURN_IF(check_dims(m, n, k));
+  if (m == 0 || n == 0) return ctx ? DC_OK : DC_ERR_INVALID_ARGUMENT;
+  if (!c || (k > 0 && (!a || !b))) return DC_ERR_INVALID_ARGUMENT;
+  DC_CTX_ENTER(ctx);
+  if (k == 0) return dc::zero_async(ctx, c, (size_t)(m * n) * sizeof(float));
+  const int tiles_m = (int)((m + kBM - 1) / kBM), tiles_n = (int)((n + kBN - 1) / kBN);
+  const unsigned grid = (unsigned)(tiles_m * tiles_n);
+  const bool full = (m % kBM == 0) && (n % kBN == 0) && (k % kBKbf16 == 0) && dc::aligned16(a) && dc::aligned16(b);
+  const unsigned short* A = reinterpret_cast<const unsigned short*>(a);
+  const unsigned short* B = reinterpret_cast<const unsigned short*>(b);
+  if (full)
+    gemm_bf16_kernel<kBKbf16, false><<<grid, kThreads, 0, ctx->stream>>>(A, B, c, (int)m, (int)n, (int)k, tiles_m, tiles_n);
+  else
+    gemm_bf16_kernel<kBKbf16, true><<<grid, kThreads, 0, ctx->stream>>>(A, B, c, (int)m, (int)n, (int)k, tiles_m, tiles_n);
+  return dc::last_launch_status();
+}
+
+DC_HIP_API int32_t dc_hip_convert_f32_to_bf16(dc_hip_ctx* ctx, const float* input, uint16_t* output, int64_t n) {
+  if (n < 0 || (n > 0 && (!input || !output))) return DC_ERR_INVALID_ARGUMENT;
+  DC_CTX_ENTER(ctx);
+  if (n == 0) return DC_OK;
+  const unsigned grid = (unsigned)std::max<int64_t>(1, std::min<int64_t>((n + 255) / 256, 16384));
+  f32_to_bf16_kernel<<<grid, 256, 0, ctx->stream>>>(input, reinterpret_cast<unsigned short*>(output), n);
+  return dc::last_launch_status();
+}
+
+}  // extern "C"

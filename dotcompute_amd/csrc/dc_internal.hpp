@@ -24,6 +24,11 @@ struct dc_hip_ctx {
   void* partials = nullptr;
   size_t partials_bytes = 0;
 
+  // SpMV scratch: the list of long rows (handled a workgroup per row) and small device scalars.
+  int32_t* spmv_rows = nullptr;
+  size_t spmv_rows_cap = 0;
+  double* scalars = nullptr;  // 64 doubles
+
   // Decoupled-lookback status words, one uint64 per tile (grows on demand). A word is valid only
   // when its epoch field equals the launch's epoch, so the array never needs clearing between
   // launches; it is cleared once when allocated and again whenever the epoch counter wraps.
@@ -44,10 +49,8 @@ struct dc_hip_module {
 
 // Counter slots inside ctx->counters.
 enum dc_counter_slot : int {
-  DC_SLOT_REDUCE_DONE = 0,
-  DC_SLOT_LINQ_TICKET = 1,
-  DC_SLOT_LINQ_SUM_DONE = 2,
-  DC_SLOT_SPMV_DONE = 3,
+  DC_SLOT_LINQ_TICKET = 0,   // tile ticket of the compaction kernel (returned to 0 by the kernel)
+  DC_SLOT_SPMV_LONG = 1,     // number of long rows found by the SpMV classification pass
   DC_SLOT_COUNT = 1024
 };
 
@@ -64,10 +67,13 @@ enum dc_counter_slot : int {
   } while (0)
 
 // Lock the context and make its device current; every op entry point starts with this.
+// hipGetLastError() also clears the runtime's sticky last-error slot, so a failed lookup in an
+// earlier call (e.g. a missing module function) is not reported by this call's launch check.
 #define DC_CTX_ENTER(ctx)                                      \
   if (!(ctx)) return DC_ERR_INVALID_ARGUMENT;                  \
   std::lock_guard<std::mutex> dc_lock_((ctx)->mu);             \
-  DC_RETURN_IF_HIP(hipSetDevice((ctx)->device))
+  DC_RETURN_IF_HIP(hipSetDevice((ctx)->device));               \
+  (void)hipGetLastError()
 
 namespace dc {
 
@@ -75,6 +81,10 @@ namespace dc {
 int32_t ensure_partials(dc_hip_ctx* ctx, size_t bytes);
 // Grows ctx->status to at least `words` and returns the epoch to use for the next launch.
 int32_t ensure_status(dc_hip_ctx* ctx, size_t words, uint32_t* epoch_out);
+// Grows ctx->spmv_rows to at least `count` entries (caller holds the lock).
+int32_t ensure_spmv_rows(dc_hip_ctx* ctx, size_t count);
+// Two-pass deterministic float64 sum of n floats into *sum_out (device), on the ctx stream.
+int32_t launch_reduce_sum_f32(dc_hip_ctx* ctx, const float* input, int64_t n, double* sum_out);
 // Fills device memory with zero bytes using a kernel (capture-safe).
 int32_t zero_async(dc_hip_ctx* ctx, void* dst, size_t bytes);
 inline int32_t last_launch_status() { return (int32_t)hipGetLastError(); }

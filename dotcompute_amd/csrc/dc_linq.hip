@@ -222,7 +222,8 @@ __global__ __launch_bounds__(kBlock) void where_select_kernel(const dc_linq_chai
   const int wave = tid >> 6;
 
   if (tid == 0) {
-    uint32_t t = dc::fetch_add_agent_u32(ticket, 1u);
+    // Relaxed: the ticket only orders tile indices; no data is published through it.
+    uint32_t t = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_tile = t;
     // Every ticket has been handed out once the last one is taken: reset for the next launch.
     if ((int64_t)t == num_tiles - 1) dc::store_agent_u32(ticket, 0u);
@@ -310,80 +311,87 @@ __global__ __launch_bounds__(kBlock) void where_select_kernel(const dc_linq_chai
 }
 
 // ---- Where/Select -> Sum / Count ----------------------------------------------------------------
+// Pass 1: each block runs the program over one contiguous chunk (a thread takes 4 vectors, 16
+// elements, per step) and writes its float64 sum and kept count; pass 2 sums the partials in block
+// order (fixed tree, deterministic).
+constexpr int kSumBlock = 512;
+
 template <bool SAVES>
-__global__ __launch_bounds__(kBlock) void where_select_sum_kernel(const dc_linq_chain prog,
-                                                                  const float* __restrict__ in, int64_t n,
-                                                                  int vec_ok, double* __restrict__ partials,
-                                                                  uint32_t* __restrict__ done,
-                                                                  double* __restrict__ sum_out,
-                                                                  int64_t* __restrict__ count_out) {
-  __shared__ double lds_d[kWaves];
-  __shared__ int64_t lds_i[kWaves];
-  __shared__ bool s_last;
+__global__ __launch_bounds__(kSumBlock) void where_select_sum_pass1(const dc_linq_chain prog,
+                                                                    const float* __restrict__ in, int64_t n,
+                                                                    int vec_ok, double* __restrict__ psum,
+                                                                    int64_t* __restrict__ pcnt) {
+  __shared__ double lds_d[kSumBlock / dc::kWave];
+  __shared__ int64_t lds_i[kSumBlock / dc::kWave];
   double acc = 0.0;
   int64_t cnt = 0;
-  const int64_t tid = blockIdx.x * (int64_t)kBlock + threadIdx.x;
-  const int64_t stride = (int64_t)gridDim.x * kBlock;
-  // Each step a thread takes 4 vectors (16 elements) spaced `stride` vectors apart.
   const int64_t n4 = vec_ok ? (n >> 2) : 0;
+  const int64_t per = (n4 + gridDim.x - 1) / gridDim.x;
+  const int64_t v0 = min(n4, (int64_t)blockIdx.x * per), v1 = min(n4, v0 + per);
   const dc::f32x4* in4 = reinterpret_cast<const dc::f32x4*>(in);
-  int64_t i = tid;
-  for (; i + 3 * stride < n4; i += 4 * stride) {
+  int64_t i = v0 + threadIdx.x;
+  for (; i + 3 * kSumBlock < v1; i += 4 * kSumBlock) {
     float e[16];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      dc::f32x4 x = dc::load_stream(in4 + i + j * stride);
+      dc::f32x4 x = dc::load_stream(in4 + i + j * kSumBlock);
       e[4 * j + 0] = x.x;
       e[4 * j + 1] = x.y;
       e[4 * j + 2] = x.z;
       e[4 * j + 3] = x.w;
     }
-    uint32_t keep = run_program<16, SAVES>(prog, e);
+    const uint32_t keep = run_program<16, SAVES>(prog, e);
 #pragma unroll
     for (int j = 0; j < 16; ++j)
       if ((keep >> j) & 1u) acc += (double)e[j];
     cnt += __builtin_popcount(keep);
   }
-  for (; i < n4; i += stride) {
+  for (; i < v1; i += kSumBlock) {
     float e[4];
     dc::f32x4 x = dc::load_stream(in4 + i);
     e[0] = x.x; e[1] = x.y; e[2] = x.z; e[3] = x.w;
-    uint32_t keep = run_program<4, SAVES>(prog, e);
+    const uint32_t keep = run_program<4, SAVES>(prog, e);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       if ((keep >> j) & 1u) acc += (double)e[j];
     cnt += __builtin_popcount(keep);
   }
-  for (int64_t s = (n4 << 2) + tid; s < n; s += stride) {
-    float e[1] = {in[s]};
-    uint32_t keep = run_program<1, SAVES>(prog, e);
-    if (keep & 1u) { acc += (double)e[0]; cnt += 1; }
+  if (blockIdx.x == gridDim.x - 1) {
+    for (int64_t s = (n4 << 2) + threadIdx.x; s < n; s += kSumBlock) {
+      float e[1] = {in[s]};
+      if (run_program<1, SAVES>(prog, e) & 1u) {
+        acc += (double)e[0];
+        cnt += 1;
+      }
+    }
   }
-  const double bsum = dc::block_sum64<kBlock>(acc, lds_d);
-  const int64_t bcnt = dc::block_sum64<kBlock>(cnt, lds_i);
-  double* psum = partials;
-  int64_t* pcnt = reinterpret_cast<int64_t*>(partials + gridDim.x);
+  const double bsum = dc::block_sum64<kSumBlock>(acc, lds_d);
+  const int64_t bcnt = dc::block_sum64<kSumBlock>(cnt, lds_i);
   if (threadIdx.x == 0) {
     psum[blockIdx.x] = bsum;
     pcnt[blockIdx.x] = bcnt;
-    dc::fence_release_agent();
-    s_last = dc::fetch_add_agent_u32(done, 1u) == gridDim.x - 1;
   }
-  __syncthreads();
-  if (!s_last) return;
-  dc::fence_acquire_agent();
+}
+
+constexpr int kFinalBlock = 1024;
+
+__global__ __launch_bounds__(kFinalBlock) void where_select_sum_pass2(const double* __restrict__ psum,
+                                                                      const int64_t* __restrict__ pcnt, int count,
+                                                                      double* __restrict__ sum_out,
+                                                                      int64_t* __restrict__ count_out) {
+  __shared__ double lds_d[kFinalBlock / dc::kWave];
+  __shared__ int64_t lds_i[kFinalBlock / dc::kWave];
   double a = 0.0;
   int64_t c = 0;
-  for (unsigned b = threadIdx.x; b < gridDim.x; b += kBlock) {
-    a += __hip_atomic_load(psum + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    c += __hip_atomic_load(pcnt + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int b = threadIdx.x; b < count; b += kFinalBlock) {
+    a += psum[b];
+    c += pcnt[b];
   }
-  const double total = dc::block_sum64<kBlock>(a, lds_d);
-  const int64_t total_cnt = dc::block_sum64<kBlock>(c, lds_i);
+  const double total = dc::block_sum64<kFinalBlock>(a, lds_d);
+  const int64_t total_cnt = dc::block_sum64<kFinalBlock>(c, lds_i);
   if (threadIdx.x == 0) {
     if (sum_out) *sum_out = total;
     if (count_out) *count_out = total_cnt;
-    dc::store_agent_u32(done, 0u);
   }
 }
 
@@ -425,13 +433,14 @@ DC_HIP_API int32_t dc_hip_linq_where_select_sum_f32(dc_hip_ctx* ctx, const dc_li
   if (n < 0 || (n > 0 && !input)) return DC_ERR_INVALID_ARGUMENT;
   DC_RETURN_IF(dc_linq_chain_validate(chain));
   DC_CTX_ENTER(ctx);
-  const int64_t per_block = (int64_t)kBlock * 16;
+  const int64_t per_block = (int64_t)kSumBlock * 16 * 4;  // elements per block-iteration x 4
   const unsigned grid = (unsigned)std::max<int64_t>(1, std::min<int64_t>((n + per_block - 1) / per_block, kSumBlocksMax));
   DC_RETURN_IF(dc::ensure_partials(ctx, (size_t)grid * 16));
-  auto kernel = program_uses_saves(*chain) ? where_select_sum_kernel<true> : where_select_sum_kernel<false>;
-  kernel<<<grid, kBlock, 0, ctx->stream>>>(*chain, input, n, dc::aligned16(input) ? 1 : 0,
-                                           static_cast<double*>(ctx->partials),
-                                           ctx->counters + DC_SLOT_LINQ_SUM_DONE, sum_out, count_out);
+  double* psum = static_cast<double*>(ctx->partials);
+  int64_t* pcnt = reinterpret_cast<int64_t*>(psum + grid);
+  auto kernel = program_uses_saves(*chain) ? where_select_sum_pass1<true> : where_select_sum_pass1<false>;
+  kernel<<<grid, kSumBlock, 0, ctx->stream>>>(*chain, input, n, dc::aligned16(input) ? 1 : 0, psum, pcnt);
+  where_select_sum_pass2<<<1, kFinalBlock, 0, ctx->stream>>>(psum, pcnt, (int)grid, sum_out, count_out);
   return dc::last_launch_status();
 }
 

@@ -85,6 +85,20 @@ int32_t ensure_partials(dc_hip_ctx* ctx, size_t bytes) {
   return DC_OK;
 }
 
+int32_t ensure_spmv_rows(dc_hip_ctx* ctx, size_t count) {
+  if (ctx->spmv_rows_cap >= count) return DC_OK;
+  size_t want = std::max<size_t>(count, 4096);
+  DC_RETURN_IF_HIP(hipStreamSynchronize(ctx->stream));
+  if (ctx->spmv_rows) DC_RETURN_IF_HIP(hipFree(ctx->spmv_rows));
+  ctx->spmv_rows = nullptr;
+  ctx->spmv_rows_cap = 0;
+  void* p = nullptr;
+  if (hipMalloc(&p, want * sizeof(int32_t)) != hipSuccess) return DC_ERR_OUT_OF_MEMORY;
+  ctx->spmv_rows = static_cast<int32_t*>(p);
+  ctx->spmv_rows_cap = want;
+  return DC_OK;
+}
+
 int32_t ensure_status(dc_hip_ctx* ctx, size_t words, uint32_t* epoch_out) {
   constexpr uint32_t kEpochMask = (1u << 22) - 1;  // 22-bit epoch field in each status word
   if (ctx->status_words < words) {
@@ -197,9 +211,19 @@ DC_HIP_API int32_t dc_hip_ctx_create(int32_t device, dc_hip_ctx** out) {
     return (int32_t)e;
   }
   ctx->counters = static_cast<uint32_t*>(c);
+  void* sc = nullptr;
+  e = hipMalloc(&sc, 64 * sizeof(double));
+  if (e != hipSuccess) {
+    (void)hipFree(ctx->counters);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return (int32_t)e;
+  }
+  ctx->scalars = static_cast<double*>(sc);
   int32_t st = dc::zero_async(ctx, ctx->counters, DC_SLOT_COUNT * sizeof(uint32_t));
   if (st == DC_OK) st = (int32_t)hipStreamSynchronize(ctx->stream);
   if (st != DC_OK) {
+    (void)hipFree(ctx->scalars);
     (void)hipFree(ctx->counters);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
@@ -218,6 +242,8 @@ DC_HIP_API int32_t dc_hip_ctx_destroy(dc_hip_ctx* ctx) {
     if (ctx->partials) (void)hipFree(ctx->partials);
     if (ctx->status) (void)hipFree(ctx->status);
     if (ctx->counters) (void)hipFree(ctx->counters);
+    if (ctx->scalars) (void)hipFree(ctx->scalars);
+    if (ctx->spmv_rows) (void)hipFree(ctx->spmv_rows);
     (void)hipStreamDestroy(ctx->stream);
   }
   delete ctx;
