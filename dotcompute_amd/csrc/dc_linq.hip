@@ -7,15 +7,15 @@
 // thread holds in registers.
 //
 // ToArray (order-preserving stream compaction, single pass):
-//   tile = 256 threads x 16 elements = 4096 consecutive elements, claimed through an atomic
-//   ticket (so a tile only ever waits on tiles that started before it);
-//   thread t loads 16-byte vectors j = 0..3 at tile + j*1024 + t*4 (coalesced, non-temporal);
-//   for each vector j and lane k the wave takes ballot(keep) -> the element's rank among the
-//   kept elements of (j, wave) is sum_k' mbcnt(ballot_k') + (kept lanes k'' < k of this thread);
-//   16 (j, wave) counts are scanned in LDS -> tile-local positions; the tile aggregate is
+//   tile = 512 threads x 32 elements = 16384 consecutive elements (64 KiB), claimed through an
+//   atomic ticket (so a tile only ever waits on tiles that started before it);
+//   thread t loads 16-byte vectors j = 0..7 at tile + j*2048 + t*4 (coalesced, non-temporal);
+//   for each vector j and slot k the wave takes ballot(keep) -> the element's rank among the
+//   kept elements of (j, wave) is sum_k' mbcnt(ballot_k') + (kept slots k'' < k of this thread);
+//   the 64 (j, wave) counts are scanned in LDS -> tile-local positions; the tile aggregate is
 //   published for decoupled lookback and the tile's exclusive prefix is resolved by wave 0 from
-//   the status words of up to 64 predecessors at once; kept values are staged in LDS in output
-//   order and written out with coalesced stores.
+//   the status words of up to 256 predecessors per round; kept values go straight from registers
+//   to their output positions (each (j, wave) group fills one contiguous run).
 // Every float operation rounds once (the file is compiled with -ffp-contract=off), so the output
 // equals LINQ-to-objects bit-for-bit.
 #include <algorithm>
@@ -25,11 +25,13 @@
 
 namespace {
 
-constexpr int kBlock = 256;
+constexpr int kBlock = 512;                        // compaction workgroup: 8 waves
 constexpr int kWaves = kBlock / dc::kWave;
-constexpr int kVecPerThread = 4;
-constexpr int kElemPerThread = 4 * kVecPerThread;  // 16
-constexpr int kTile = kBlock * kElemPerThread;     // 4096
+constexpr int kVecPerThread = 8;
+constexpr int kElemPerThread = 4 * kVecPerThread;  // 32
+constexpr int kTile = kBlock * kElemPerThread;     // 16384 elements = 64 KiB of input
+constexpr int kChunk = 16;                         // elements interpreted per program pass
+constexpr int kLookbackPerLane = 4;                // status words read per lane per lookback round
 constexpr int kSumBlocksMax = 2048;
 
 // ---- interpreter -------------------------------------------------------------------------------
@@ -162,90 +164,234 @@ __device__ inline uint64_t pack_status(uint64_t flag, uint32_t epoch, uint64_t v
   return flag | ((uint64_t)epoch << 40) | (value & kValueMask);
 }
 
-// Called by all 64 lanes of wave 0. Returns the exclusive prefix of `tile` (valid in every lane).
-__device__ inline int64_t lookback(uint64_t* __restrict__ status, int64_t tile, uint64_t aggregate,
-                                   uint32_t epoch) {
+// Tile 0 publishes its inclusive prefix at once; every other tile first publishes its aggregate.
+__device__ inline void publish_aggregate(uint64_t* __restrict__ status, int64_t tile, uint64_t aggregate,
+                                         uint32_t epoch) {
+  dc::store_agent_u64(status + tile, pack_status(tile == 0 ? kFlagInc : kFlagAgg, epoch, aggregate));
+}
+
+// Called by all 64 lanes of one wave after publish_aggregate. Returns the exclusive prefix of `tile`
+// (valid in every lane) and publishes the tile's inclusive prefix. Each round reads the status of
+// the 256 nearest unresolved predecessors (lane l: tiles end - 4l .. end - 4l - 3) and stops at
+// the nearest inclusive prefix, adding the aggregates in between. Wide rounds matter: while the
+// tiles in flight outrun the prefix front, every tile has to fold all aggregates between itself
+// and the front, and each round costs one agent-scope round trip. A tile only waits on tiles with
+// smaller tickets, which are all owned by running workgroups, so the wait always ends.
+__device__ inline int64_t lookback(uint64_t* __restrict__ status, int64_t tile, uint64_t aggregate, uint32_t epoch) {
+  if (tile == 0) return 0;
+  constexpr int P = kLookbackPerLane;
   const int lane = threadIdx.x & 63;
-  if (tile == 0) {
-    if (lane == 0) dc::store_agent_u64(status, pack_status(kFlagInc, epoch, aggregate));
-    return 0;
-  }
-  if (lane == 0) dc::store_agent_u64(status + tile, pack_status(kFlagAgg, epoch, aggregate));
   int64_t exclusive = 0;
-  int64_t end = tile - 1;  // lane l inspects tile end - l
+  int64_t end = tile - 1;
   while (true) {
-    const int64_t idx = end - lane;
-    bool valid = true, inc = true;
-    uint64_t value = 0;
-    if (idx >= 0) {
-      uint64_t w = dc::load_agent_u64(status + idx);
-      uint32_t w_epoch = (uint32_t)((w >> 40) & ((1u << 22) - 1));
-      uint64_t flag = w & (3ull << 62);
-      valid = (flag != 0) && (w_epoch == epoch);
-      inc = valid && (flag == kFlagInc);
-      value = w & kValueMask;
+    uint64_t w[P];
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+      const int64_t idx = end - (int64_t)(P * lane + q);
+      w[q] = idx >= 0 ? dc::load_agent_u64(status + idx) : pack_status(kFlagInc, epoch, 0);
     }
-    const uint64_t inc_mask = __ballot(inc);
-    const uint64_t bad_mask = __ballot(!valid);
+    // Per lane: first inclusive slot (P if none), whether a not-yet-published slot precedes it,
+    // and the sum of the values up to and including it.
+    int first_inc = P;
+    bool bad = false;
+    int64_t part = 0;
+#pragma unroll
+    for (int q = P - 1; q >= 0; --q) {
+      const uint32_t w_epoch = (uint32_t)((w[q] >> 40) & ((1u << 22) - 1));
+      const uint64_t flag = w[q] & (3ull << 62);
+      const bool valid = (flag != 0) && (w_epoch == epoch);
+      if (valid && flag == kFlagInc) first_inc = q;
+    }
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+      if (q <= first_inc || first_inc == P) {
+        const uint32_t w_epoch = (uint32_t)((w[q] >> 40) & ((1u << 22) - 1));
+        const uint64_t flag = w[q] & (3ull << 62);
+        const bool valid = (flag != 0) && (w_epoch == epoch);
+        bad |= !valid && (q < first_inc || first_inc == P);
+        part += (int64_t)(w[q] & kValueMask);
+      }
+    }
+    const uint64_t inc_mask = __ballot(first_inc < P);
+    const uint64_t bad_mask = __ballot(bad);
     const int limit = inc_mask ? __builtin_ctzll(inc_mask) : 63;  // lanes [0, limit] are needed
     const uint64_t need = (limit == 63) ? ~0ull : ((2ull << limit) - 1);
     if (bad_mask & need) {
       __builtin_amdgcn_s_sleep(1);
       continue;
     }
-    int64_t contrib = (lane <= limit) ? (int64_t)value : 0;
-    exclusive += dc::wave_sum64<int64_t>(contrib);
+    exclusive += dc::wave_sum64<int64_t>(lane <= limit ? part : (int64_t)0);
     if (inc_mask) break;
-    end -= 64;
+    end -= 64 * P;
   }
   if (lane == 0) dc::store_agent_u64(status + tile, pack_status(kFlagInc, epoch, (uint64_t)exclusive + aggregate));
   return exclusive;
 }
 
+// ---- affine-chain fast path -------------------------------------------------------------------
+// Chains whose every stage is `Where(x <cmp> c)` or `Select(x * a + b)` (also x*a, x+b, x-b) are
+// lowered to a stage table and run without the interpreter's scratch registers, which lets more
+// tiles be resident. Each stage rounds exactly as the interpreter does (x*a, then +b).
+constexpr int kMaxAffineStages = 8;
+enum AffineKind : uint8_t { kStageFilter = 0, kStageMap = 1 };
+struct AffineChain {
+  int32_t n_stages;
+  uint8_t kind[kMaxAffineStages];
+  uint8_t op[kMaxAffineStages];      // filter: DC_LQ_CMP_*; map: bit0 = has mul, bit1 = has add
+  float c0[kMaxAffineStages];        // filter: constant; map: multiplier
+  float c1[kMaxAffineStages];        // map: addend
+};
+
+// Host-side lowering; returns false when the program is not an affine chain.
+inline bool lower_affine(const dc_linq_chain& prog, AffineChain* out) {
+  AffineChain a{};
+  int pc = 0;
+  while (pc < prog.n_instr) {
+    if (a.n_stages == kMaxAffineStages) return false;
+    const dc_linq_instr* c = &prog.code[pc];
+    if (c->op != DC_LQ_LOAD || c->src != DC_LQ_SRC_ELEM) return false;
+    ++pc;
+    if (pc + 1 < prog.n_instr && prog.code[pc].op >= DC_LQ_CMP_GT && prog.code[pc].op <= DC_LQ_CMP_NE &&
+        prog.code[pc].src == DC_LQ_SRC_IMM && prog.code[pc].mode == DC_LQ_CMP_SET && prog.code[pc + 1].op == DC_LQ_FILTER) {
+      a.kind[a.n_stages] = kStageFilter;
+      a.op[a.n_stages] = prog.code[pc].op;
+      a.c0[a.n_stages] = prog.code[pc].imm;
+      ++a.n_stages;
+      pc += 2;
+      continue;
+    }
+    uint8_t flags = 0;
+    float mul = 1.0f, add = 0.0f;
+    if (pc < prog.n_instr && prog.code[pc].op == DC_LQ_MUL && prog.code[pc].src == DC_LQ_SRC_IMM) {
+      flags |= 1;
+      mul = prog.code[pc].imm;
+      ++pc;
+    }
+    if (pc < prog.n_instr && prog.code[pc].src == DC_LQ_SRC_IMM &&
+        (prog.code[pc].op == DC_LQ_ADD || prog.code[pc].op == DC_LQ_SUB)) {
+      flags |= 2;
+      // x - b is computed as x + (-b): negating the constant is exact, so the rounding is the same.
+      add = prog.code[pc].op == DC_LQ_ADD ? prog.code[pc].imm : -prog.code[pc].imm;
+      ++pc;
+    }
+    if (pc >= prog.n_instr || prog.code[pc].op != DC_LQ_MAP) return false;
+    ++pc;
+    a.kind[a.n_stages] = kStageMap;
+    a.op[a.n_stages] = flags;
+    a.c0[a.n_stages] = mul;
+    a.c1[a.n_stages] = add;
+    ++a.n_stages;
+  }
+  *out = a;
+  return true;
+}
+
+template <int EPT>
+__device__ inline uint64_t run_affine(const AffineChain& ch, float (&e)[EPT]) {
+  uint64_t keep = (EPT == 64) ? ~0ull : ((1ull << EPT) - 1);
+  for (int s = 0; s < ch.n_stages; ++s) {
+    const float c0 = ch.c0[s], c1 = ch.c1[s];
+    if (ch.kind[s] == kStageFilter) {
+      uint64_t c = 0;
+      switch (ch.op[s]) {
+#define DC_AFF_CMP(OPC, EXPR) \
+  case OPC: _Pragma("unroll") for (int j = 0; j < EPT; ++j) c |= (uint64_t)(EXPR) << j; break
+        DC_AFF_CMP(DC_LQ_CMP_GT, e[j] > c0);
+        DC_AFF_CMP(DC_LQ_CMP_GE, e[j] >= c0);
+        DC_AFF_CMP(DC_LQ_CMP_LT, e[j] < c0);
+        DC_AFF_CMP(DC_LQ_CMP_LE, e[j] <= c0);
+        DC_AFF_CMP(DC_LQ_CMP_EQ, e[j] == c0);
+        default: DC_AFF_CMP(DC_LQ_CMP_NE, e[j] != c0);
+#undef DC_AFF_CMP
+      }
+      keep &= c;
+    } else {
+      const uint8_t f = ch.op[s];
+      if (f & 1) {
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) e[j] = e[j] * c0;
+      }
+      if (f & 2) {
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) e[j] = e[j] + c1;
+      }
+    }
+  }
+  return keep;
+}
+
 // ---- Where/Select -> ToArray ------------------------------------------------------------------
-template <bool SAVES>
-__global__ __launch_bounds__(kBlock) void where_select_kernel(const dc_linq_chain prog, const float* __restrict__ in,
-                                                              int64_t n, float* __restrict__ out,
+// One tile per workgroup, claimed by ticket. Element order inside a tile is (vector j, wave, lane,
+// slot k): thread t loads 16-byte vectors j = 0..7 at tile + 2048 j + 4 t. After the lookback each
+// wave compacts the kept elements of one (j, wave) group through a 1 KiB LDS buffer and writes the
+// group's contiguous output run with fully coalesced stores.
+__device__ inline uint32_t take_ticket(uint32_t* __restrict__ ticket, uint32_t total_takes) {
+  // Relaxed: the ticket only orders tile indices; no data is published through it.
+  const uint32_t t = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (t == total_takes - 1) dc::store_agent_u32(ticket, 0u);
+  return t;
+}
+
+enum ProgramMode : int { kModeInterp = 0, kModeInterpSaves = 1, kModeAffine = 2 };
+
+template <int MODE>
+__device__ inline uint64_t apply_program(const dc_linq_chain& prog, const AffineChain& aff,
+                                         float (&e)[kElemPerThread]) {
+  if constexpr (MODE == kModeAffine) {
+    return run_affine<kElemPerThread>(aff, e);
+  } else {
+    uint64_t keep = 0;
+#pragma unroll
+    for (int c = 0; c < kElemPerThread / kChunk; ++c) {
+      float sub[kChunk];
+#pragma unroll
+      for (int i = 0; i < kChunk; ++i) sub[i] = e[c * kChunk + i];
+      keep |= (uint64_t)run_program<kChunk, MODE == kModeInterpSaves>(prog, sub) << (c * kChunk);
+#pragma unroll
+      for (int i = 0; i < kChunk; ++i) e[c * kChunk + i] = sub[i];
+    }
+    return keep;
+  }
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kBlock) void where_select_kernel(const dc_linq_chain prog, const AffineChain aff,
+                                                              const float* __restrict__ in, int64_t n,
+                                                              float* __restrict__ out,
                                                               int64_t* __restrict__ count_out,
                                                               uint64_t* __restrict__ status,
                                                               uint32_t* __restrict__ ticket, uint32_t epoch,
-                                                              int64_t num_tiles, int vec_ok) {
+                                                              uint32_t num_tiles, int vec_ok) {
+  static_assert(kVecPerThread * kWaves == 64, "the group scan gives one (j, wave) group to each lane of wave 0");
   __shared__ uint32_t s_tile;
-  __shared__ uint32_t s_count[kVecPerThread][kWaves];
   __shared__ uint32_t s_offset[kVecPerThread][kWaves];
   __shared__ uint32_t s_aggregate;
   __shared__ int64_t s_exclusive;
-  __shared__ float s_stage[kTile];
+  __shared__ float s_wbuf[kWaves][4 * dc::kWave];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
 
-  if (tid == 0) {
-    // Relaxed: the ticket only orders tile indices; no data is published through it.
-    uint32_t t = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_tile = t;
-    // Every ticket has been handed out once the last one is taken: reset for the next launch.
-    if ((int64_t)t == num_tiles - 1) dc::store_agent_u32(ticket, 0u);
-  }
+  if (tid == 0) s_tile = take_ticket(ticket, num_tiles);
   __syncthreads();
-  const int64_t tile = s_tile;
+  const uint32_t tile = s_tile;
   if (tile >= num_tiles) return;  // cannot happen while the ticket counter starts at zero
-  const int64_t base = tile * kTile;
+  const int64_t base = (int64_t)tile * kTile;
 
   float e[kElemPerThread];
-  uint32_t valid;
+  uint64_t valid;
   if (vec_ok && base + kTile <= n) {
     const dc::f32x4* in4 = reinterpret_cast<const dc::f32x4*>(in + base);
 #pragma unroll
     for (int j = 0; j < kVecPerThread; ++j) {
-      dc::f32x4 x = dc::load_stream(in4 + j * kBlock + tid);
+      const dc::f32x4 x = dc::load_stream(in4 + j * kBlock + tid);
       e[4 * j + 0] = x.x;
       e[4 * j + 1] = x.y;
       e[4 * j + 2] = x.z;
       e[4 * j + 3] = x.w;
     }
-    valid = 0xFFFFu;
+    valid = ~0ull;
   } else {
     valid = 0;
 #pragma unroll
@@ -255,18 +401,17 @@ __global__ __launch_bounds__(kBlock) void where_select_kernel(const dc_linq_chai
         const int64_t idx = base + (int64_t)j * (4 * kBlock) + tid * 4 + k;
         const bool ok = idx < n;
         e[4 * j + k] = ok ? in[idx] : 0.0f;
-        valid |= (uint32_t)ok << (4 * j + k);
+        valid |= (uint64_t)ok << (4 * j + k);
       }
   }
 
-  const uint32_t keep = run_program<kElemPerThread, SAVES>(prog, e) & valid;
+  const uint64_t keep = apply_program<MODE>(prog, aff, e) & valid;
 
-  // Rank of this thread's first kept element of vector j inside its (j, wave) group: the kept
-  // elements of lower lanes, counted with one ballot + mbcnt per element slot k.
+  // Kept count of every (j, wave) group, and this lane's rank inside it (ballot + mbcnt per slot).
   uint32_t below[kVecPerThread];
 #pragma unroll
   for (int j = 0; j < kVecPerThread; ++j) {
-    uint32_t bl = 0, total = 0;
+    uint32_t total = 0, bl = 0;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const uint64_t b = __ballot((keep >> (4 * j + k)) & 1u);
@@ -274,40 +419,47 @@ __global__ __launch_bounds__(kBlock) void where_select_kernel(const dc_linq_chai
       total += (uint32_t)__builtin_popcountll(b);
     }
     below[j] = bl;
-    if (lane == 0) s_count[j][wave] = total;
+    if (lane == 0) s_offset[j][wave] = total;
   }
   __syncthreads();
-  if (tid == 0) {
-    uint32_t run = 0;
+  if (wave == 0) {  // exclusive scan of the 64 group counts in output order, one group per lane
+    uint32_t* flat = &s_offset[0][0];
+    const uint32_t c = flat[lane];
+    uint32_t incl = c;
 #pragma unroll
-    for (int j = 0; j < kVecPerThread; ++j)
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        s_offset[j][w] = run;
-        run += s_count[j][w];
-      }
-    s_aggregate = run;
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t o = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += o;
+    }
+    flat[lane] = incl - c;
+    if (lane == 63) {
+      s_aggregate = incl;
+      publish_aggregate(status, tile, incl, epoch);
+    }
   }
   __syncthreads();
   const uint32_t aggregate = s_aggregate;
-
   if (wave == 0) {
-    int64_t excl = lookback(status, tile, aggregate, epoch);
+    const int64_t excl = lookback(status, tile, aggregate, epoch);
     if (lane == 0) s_exclusive = excl;
   }
-  // Stage kept elements in output order.
+  __syncthreads();
+  float* dst = out + s_exclusive;
 #pragma unroll
   for (int j = 0; j < kVecPerThread; ++j) {
-    uint32_t pos = s_offset[j][wave] + below[j];
+    const int g = j * kWaves + wave;  // flat group index; the run ends where the next group starts
+    const uint32_t gbase = s_offset[j][wave];
+    const uint32_t gend = (g == 63) ? aggregate : (&s_offset[0][0])[g + 1];
+    uint32_t pos = below[j];
 #pragma unroll
     for (int k = 0; k < 4; ++k)
-      if ((keep >> (4 * j + k)) & 1u) s_stage[pos++] = e[4 * j + k];
+      if ((keep >> (4 * j + k)) & 1u) s_wbuf[wave][pos++] = e[4 * j + k];
+    __builtin_amdgcn_wave_barrier();
+    float* gdst = dst + gbase;
+    for (uint32_t i = lane; i < gend - gbase; i += dc::kWave) gdst[i] = s_wbuf[wave][i];
+    __builtin_amdgcn_wave_barrier();
   }
-  __syncthreads();
-  const int64_t exclusive = s_exclusive;
-  float* dst = out + exclusive;
-  for (uint32_t i = tid; i < aggregate; i += kBlock) __builtin_nontemporal_store(s_stage[i], dst + i);
-  if (tid == 0 && tile == num_tiles - 1) *count_out = exclusive + (int64_t)aggregate;
+  if (tid == 0 && tile == num_tiles - 1) *count_out = s_exclusive + (int64_t)aggregate;
 }
 
 // ---- Where/Select -> Sum / Count ----------------------------------------------------------------
@@ -316,8 +468,14 @@ __global__ __launch_bounds__(kBlock) void where_select_kernel(const dc_linq_chai
 // order (fixed tree, deterministic).
 constexpr int kSumBlock = 512;
 
-template <bool SAVES>
-__global__ __launch_bounds__(kSumBlock) void where_select_sum_pass1(const dc_linq_chain prog,
+template <int MODE, int EPT>
+__device__ inline uint32_t apply_small(const dc_linq_chain& prog, const AffineChain& aff, float (&e)[EPT]) {
+  if constexpr (MODE == kModeAffine) return (uint32_t)run_affine<EPT>(aff, e);
+  else return run_program<EPT, MODE == kModeInterpSaves>(prog, e);
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kSumBlock) void where_select_sum_pass1(const dc_linq_chain prog, const AffineChain aff,
                                                                     const float* __restrict__ in, int64_t n,
                                                                     int vec_ok, double* __restrict__ psum,
                                                                     int64_t* __restrict__ pcnt) {
@@ -340,26 +498,24 @@ __global__ __launch_bounds__(kSumBlock) void where_select_sum_pass1(const dc_lin
       e[4 * j + 2] = x.z;
       e[4 * j + 3] = x.w;
     }
-    const uint32_t keep = run_program<16, SAVES>(prog, e);
+    const uint32_t keep = apply_small<MODE, 16>(prog, aff, e);
 #pragma unroll
-    for (int j = 0; j < 16; ++j)
-      if ((keep >> j) & 1u) acc += (double)e[j];
+    for (int j = 0; j < 16; ++j) acc += ((keep >> j) & 1u) ? (double)e[j] : 0.0;
     cnt += __builtin_popcount(keep);
   }
   for (; i < v1; i += kSumBlock) {
     float e[4];
     dc::f32x4 x = dc::load_stream(in4 + i);
     e[0] = x.x; e[1] = x.y; e[2] = x.z; e[3] = x.w;
-    const uint32_t keep = run_program<4, SAVES>(prog, e);
+    const uint32_t keep = apply_small<MODE, 4>(prog, aff, e);
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if ((keep >> j) & 1u) acc += (double)e[j];
+    for (int j = 0; j < 4; ++j) acc += ((keep >> j) & 1u) ? (double)e[j] : 0.0;
     cnt += __builtin_popcount(keep);
   }
   if (blockIdx.x == gridDim.x - 1) {
     for (int64_t s = (n4 << 2) + threadIdx.x; s < n; s += kSumBlock) {
       float e[1] = {in[s]};
-      if (run_program<1, SAVES>(prog, e) & 1u) {
+      if (apply_small<MODE, 1>(prog, aff, e) & 1u) {
         acc += (double)e[0];
         cnt += 1;
       }
@@ -418,12 +574,16 @@ DC_HIP_API int32_t dc_hip_linq_where_select_f32(dc_hip_ctx* ctx, const dc_linq_c
   if (n >= (int64_t)1 << 40) return DC_ERR_INVALID_ARGUMENT;  // 40-bit counts in the status words
   DC_CTX_ENTER(ctx);
   const int64_t tiles = std::max<int64_t>(1, (n + kTile - 1) / kTile);
-  if (tiles > 0xFFFFFFFFll) return DC_ERR_INVALID_ARGUMENT;
+  if (tiles > 0x7FFFFFFFll) return DC_ERR_INVALID_ARGUMENT;
   uint32_t epoch = 0;
   DC_RETURN_IF(dc::ensure_status(ctx, (size_t)tiles, &epoch));
-  auto kernel = program_uses_saves(*chain) ? where_select_kernel<true> : where_select_kernel<false>;
-  kernel<<<(unsigned)tiles, kBlock, 0, ctx->stream>>>(*chain, input, n, output, count_out, ctx->status,
-                                                      ctx->counters + DC_SLOT_LINQ_TICKET, epoch, tiles,
+  AffineChain aff{};
+  const bool affine = lower_affine(*chain, &aff);
+  auto kernel = affine ? where_select_kernel<kModeAffine>
+                       : (program_uses_saves(*chain) ? where_select_kernel<kModeInterpSaves>
+                                                     : where_select_kernel<kModeInterp>);
+  kernel<<<(unsigned)tiles, kBlock, 0, ctx->stream>>>(*chain, aff, input, n, output, count_out, ctx->status,
+                                                      ctx->counters + DC_SLOT_LINQ_TICKET, epoch, (uint32_t)tiles,
                                                       dc::aligned16(input) ? 1 : 0);
   return dc::last_launch_status();
 }
@@ -438,8 +598,12 @@ DC_HIP_API int32_t dc_hip_linq_where_select_sum_f32(dc_hip_ctx* ctx, const dc_li
   DC_RETURN_IF(dc::ensure_partials(ctx, (size_t)grid * 16));
   double* psum = static_cast<double*>(ctx->partials);
   int64_t* pcnt = reinterpret_cast<int64_t*>(psum + grid);
-  auto kernel = program_uses_saves(*chain) ? where_select_sum_pass1<true> : where_select_sum_pass1<false>;
-  kernel<<<grid, kSumBlock, 0, ctx->stream>>>(*chain, input, n, dc::aligned16(input) ? 1 : 0, psum, pcnt);
+  AffineChain aff{};
+  const bool affine = lower_affine(*chain, &aff);
+  auto kernel = affine ? where_select_sum_pass1<kModeAffine>
+                       : (program_uses_saves(*chain) ? where_select_sum_pass1<kModeInterpSaves>
+                                                     : where_select_sum_pass1<kModeInterp>);
+  kernel<<<grid, kSumBlock, 0, ctx->stream>>>(*chain, aff, input, n, dc::aligned16(input) ? 1 : 0, psum, pcnt);
   where_select_sum_pass2<<<1, kFinalBlock, 0, ctx->stream>>>(psum, pcnt, (int)grid, sum_out, count_out);
   return dc::last_launch_status();
 }

@@ -218,3 +218,33 @@ def test_where_select_256m(ctx):
     assert abs(s.to_host()[0] - ref_sum) <= 1e-5 * 28 * abs(ref_sum)
     for a in (dx, out, cnt, s, c):
         ctx.free(a)
+
+
+AFFINE_CHAINS = [
+    # (description, program) — all lowered to the affine fast path
+    ("Where(x >= 0.25)", [(LOAD, SRC_ELEM, 0), (CMP_GE, SRC_IMM, 0.25), (FILTER, SRC_IMM, 0)]),
+    ("Select(x * 3)", [(LOAD, SRC_ELEM, 0), (MUL, SRC_IMM, 3.0), (MAP, SRC_IMM, 0)]),
+    ("Select(x - 0.1)", [(LOAD, SRC_ELEM, 0), (SUB, SRC_IMM, 0.1), (MAP, SRC_IMM, 0)]),
+    ("Where(x < 0).Select(x * -0.5 + 2).Where(x != 2.25)",
+     [(LOAD, SRC_ELEM, 0), (CMP_LT, SRC_IMM, 0.0), (FILTER, SRC_IMM, 0),
+      (LOAD, SRC_ELEM, 0), (MUL, SRC_IMM, -0.5), (ADD, SRC_IMM, 2.0), (MAP, SRC_IMM, 0),
+      (LOAD, SRC_ELEM, 0), (CMP_NE, SRC_IMM, 2.25), (FILTER, SRC_IMM, 0)]),
+    ("Select(x * 1.1).Where(x <= 0.3).Select(x + 7)",
+     [(LOAD, SRC_ELEM, 0), (MUL, SRC_IMM, 1.1), (MAP, SRC_IMM, 0),
+      (LOAD, SRC_ELEM, 0), (CMP_LE, SRC_IMM, 0.3), (FILTER, SRC_IMM, 0),
+      (LOAD, SRC_ELEM, 0), (ADD, SRC_IMM, 7.0), (MAP, SRC_IMM, 0)]),
+    ("Where(x == 0)", [(LOAD, SRC_ELEM, 0), (CMP_EQ, SRC_IMM, 0.0), (FILTER, SRC_IMM, 0)]),
+]
+
+
+@pytest.mark.parametrize("idx", range(len(AFFINE_CHAINS)))
+def test_affine_fast_path_matches_interpreter(ctx, idx):
+    _, code = AFFINE_CHAINS[idx]
+    prog = LinqChain.assemble(code)
+    x = oracle.gen_uniform_f32(300_001, 77 + idx, 0)
+    got = run_to_array(ctx, prog, x)
+    assert same_floats(got, oracle.linq_where_select(prog, x))
+    s, c = run_sum(ctx, prog, x)
+    _, sd, rc = oracle.linq_where_select_sum(prog, x)
+    assert c == rc
+    assert abs(s - sd) <= 1e-5 * math.log2(x.size) * max(abs(sd), 1.0)
