@@ -40,16 +40,27 @@ __global__ __launch_bounds__(kBlock) void spmv_short_rows(const int32_t* __restr
   if (sub == 0) y[row] = sum;
 }
 
+// Appends every row longer than long_threshold to `list`. One atomic per wave (ballot + mbcnt
+// give each long row its slot), so the counter is not hammered once per long row.
 __global__ __launch_bounds__(kBlock) void spmv_classify(const int32_t* __restrict__ rp, int64_t rows,
                                                         int32_t long_threshold, int32_t* __restrict__ list,
                                                         uint32_t* __restrict__ count) {
-  int64_t r = blockIdx.x * (int64_t)kBlock + threadIdx.x;
   const int64_t stride = (int64_t)gridDim.x * kBlock;
-  for (; r < rows; r += stride) {
-    if (rp[r + 1] - rp[r] > long_threshold) {
-      const uint32_t slot = __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      list[slot] = (int32_t)r;
-    }
+  const int lane = threadIdx.x & 63;
+  // Every lane of a wave runs the same number of iterations (the bound is rounded up to whole
+  // strides), so the ballot and the broadcast below always see the full wave.
+  const int64_t iters = (rows + stride - 1) / stride;
+  for (int64_t it = 0; it < iters; ++it) {
+    const int64_t r = it * stride + blockIdx.x * (int64_t)kBlock + threadIdx.x;
+    const bool is_long = r < rows && (rp[r + 1] - rp[r] > long_threshold);
+    const uint64_t m = __ballot(is_long);
+    if (m == 0) continue;
+    uint32_t base = 0;
+    if (lane == 0)
+      base = __hip_atomic_fetch_add(count, (uint32_t)__builtin_popcountll(m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+    if (is_long)
+      list[base + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u))] = (int32_t)r;
   }
 }
 
