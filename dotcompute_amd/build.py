@@ -70,24 +70,23 @@ def build_code_object() -> str:
     return out
 
 
-def build_host_layer() -> str | None:
-    """C++ host layer + its test binary (g++, links libdotcompute_hip.so)."""
-    if not os.path.isdir(HOST):
-        return None
+def build_host_layer() -> str:
+    """C++ host layer (g++, links libdotcompute_hip.so) and its test binary (tests/cpp, which also
+    links the CPU oracle as its checker)."""
     srcs = sorted(os.path.join(HOST, "src", f) for f in os.listdir(os.path.join(HOST, "src")) if f.endswith(".cpp"))
     inc = ["-I", os.path.join(HOST, "include"), "-I", os.path.join(ROOT, "include")]
-    flags = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter", "-pthread"]
+    flags = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter", "-pthread", "-ffp-contract=off"]
     out = os.path.join(LIB, "libdotcompute_host.so")
     _run(["g++", *flags, *inc, "-shared", "-o", out + ".tmp", *srcs, "-L", LIB, "-ldotcompute_hip",
           "-Wl,-rpath,$ORIGIN"])
     os.replace(out + ".tmp", out)
-    tests = os.path.join(HOST, "tests")
-    if os.path.isdir(tests):
-        tsrcs = sorted(os.path.join(tests, f) for f in os.listdir(tests) if f.endswith(".cpp"))
-        tbin = os.path.join(LIB, "dc_host_tests")
-        _run(["g++", *flags, *inc, "-o", tbin + ".tmp", *tsrcs, "-L", LIB, "-ldotcompute_host", "-ldotcompute_hip",
-              "-Wl,-rpath,$ORIGIN"])
-        os.replace(tbin + ".tmp", tbin)
+    tests = os.path.join(ROOT, "tests", "cpp")
+    tsrcs = sorted(os.path.join(tests, f) for f in os.listdir(tests) if f.endswith(".cpp"))
+    tbin = os.path.join(LIB, "dc_host_tests")
+    oracle_dir = os.path.join(ROOT, "oracle")
+    _run(["g++", *flags, *inc, "-o", tbin + ".tmp", *tsrcs, "-L", LIB, "-ldotcompute_host", "-ldotcompute_hip",
+          "-L", oracle_dir, "-loracle", "-Wl,-rpath,$ORIGIN", "-Wl,-rpath,$ORIGIN/../../oracle"])
+    os.replace(tbin + ".tmp", tbin)
     return out
 
 

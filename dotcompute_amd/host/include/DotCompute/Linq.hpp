@@ -1,0 +1,232 @@
+// Linq.hpp — the LINQ provider for the HIP backend: expression trees for float lambdas, the
+// operation graph, the fusion planner that lowers a Where/Select(/Sum) chain to ONE prebuilt
+// gfx950 kernel (a dc_linq_chain register program), and the queryable front end.
+//
+// Reference: AsComputeQueryable / ComputeQueryProvider / ComputeQueryable<T>
+// (src/Extensions/DotCompute.Linq/ComputeQueryableExtensions.cs:19-68,74-646),
+// ExpressionTreeVisitor (Compilation/ExpressionTreeVisitor.cs:38-159,234-272), OperationGraph /
+// Operation / OperationType (Optimization/OperationGraph.cs:14-80, Optimization/OperationType.cs:12),
+// the fusion rules of CudaKernelGenerator (CodeGeneration/CudaKernelGenerator.cs:1163-1226),
+// BackendSelector + ComputeBackend (CodeGeneration/BackendSelector.cs:27-326, ComputeBackend.cs:9-28)
+// and RuntimeExecutor (CodeGeneration/RuntimeExecutor.cs:148-179,245-312).
+//
+// Lambdas are written with a small expression DSL, e.g.
+//   auto x = Linq::Param();
+//   AsComputeQueryable(src).Where(x > 0.0f).Select(x * 2.0f + 1.0f).ToArray();
+// which builds the same tree C# builds for `x => x > 0f` and `x => x * 2f + 1f`.
+#pragma once
+
+#include <optional>
+
+#include "Abstractions.hpp"
+#include "Backends/Hip.hpp"
+
+namespace DotCompute::Linq {
+
+// ---- expression trees ---------------------------------------------------------------------------
+enum class ExprKind {
+  Parameter, Constant,
+  Negate, Abs, Sqrt,
+  Add, Subtract, Multiply, Divide, Min, Max,
+  GreaterThan, GreaterThanOrEqual, LessThan, LessThanOrEqual, Equal, NotEqual,
+  AndAlso, OrElse, Not
+};
+
+struct ExprNode {
+  ExprKind Kind;
+  float Value = 0.0f;  // Constant
+  std::shared_ptr<const ExprNode> Left, Right;
+};
+
+class Expr {
+ public:
+  Expr(float constant);  // implicit: a float literal in a lambda body
+  explicit Expr(std::shared_ptr<const ExprNode> n) : node_(std::move(n)) {}
+  static Expr Parameter();
+  const ExprNode& Node() const { return *node_; }
+  std::shared_ptr<const ExprNode> Ptr() const { return node_; }
+  bool IsPredicate() const;  // comparison or logical node
+  std::string ToString() const;
+
+ private:
+  std::shared_ptr<const ExprNode> node_;
+};
+
+inline Expr Param() { return Expr::Parameter(); }
+Expr operator+(const Expr& a, const Expr& b);
+Expr operator-(const Expr& a, const Expr& b);
+Expr operator*(const Expr& a, const Expr& b);
+Expr operator/(const Expr& a, const Expr& b);
+Expr operator-(const Expr& a);
+Expr operator>(const Expr& a, const Expr& b);
+Expr operator>=(const Expr& a, const Expr& b);
+Expr operator<(const Expr& a, const Expr& b);
+Expr operator<=(const Expr& a, const Expr& b);
+Expr operator==(const Expr& a, const Expr& b);
+Expr operator!=(const Expr& a, const Expr& b);
+Expr operator&&(const Expr& a, const Expr& b);
+Expr operator||(const Expr& a, const Expr& b);
+Expr operator!(const Expr& a);
+
+namespace MathF {  // System.MathF members usable in lambdas
+Expr Abs(const Expr& a);
+Expr Sqrt(const Expr& a);
+Expr Min(const Expr& a, const Expr& b);
+Expr Max(const Expr& a, const Expr& b);
+}  // namespace MathF
+
+// ---- query representation: the Queryable.* method-call chain -------------------------------------
+struct MethodCall {
+  std::string Method;          // "Where", "Select", "Sum", "Count", "OrderBy", ...
+  std::optional<Expr> Lambda;  // absent for parameterless operators (Sum(), Count())
+};
+
+// ---- operation graph ------------------------------------------------------------------------------
+enum class OperationType { Map = 0, Filter = 1, Reduce = 2, Scan = 3, Join = 4, GroupBy = 5, OrderBy = 6, Aggregate = 7 };
+
+struct Operation {
+  std::string Id;                       // "op_0", "op_1", ...
+  OperationType Type = OperationType::Map;
+  std::vector<std::string> Dependencies;
+  std::string Method;                   // the LINQ method it came from
+  std::optional<Expr> Lambda;           // Metadata["Lambda"]
+};
+
+struct OperationGraph {
+  std::vector<Operation> Operations;
+  const Operation* Root() const { return Operations.empty() ? nullptr : &Operations.back(); }
+};
+
+class ExpressionTreeVisitor {
+ public:
+  OperationGraph Visit(const std::vector<MethodCall>& chain) const;
+  // ExpressionTreeVisitor.cs:234-272; nullopt for unsupported methods.
+  static std::optional<OperationType> MapMethodToOperationType(const std::string& method);
+};
+
+// ---- backend selection ---------------------------------------------------------------------------
+enum class ComputeBackend { CpuSimd = 0, Cuda = 1, Metal = 2, Hip = 3 };
+
+struct WorkloadCharacteristics {
+  size_t DataSize = 0;
+  int OperationCount = 0;
+  bool HasReduction = false;
+};
+
+class BackendSelector {
+ public:
+  static constexpr size_t MinGpuDataSize = 10'000;  // BackendSelector.cs:27
+  explicit BackendSelector(bool hipAvailable) : hip_available_(hipAvailable) {}
+  // This build has exactly one compute backend. Without a HIP device it throws instead of
+  // returning CpuSimd: the queries must never silently run on the host.
+  ComputeBackend SelectBackend(const WorkloadCharacteristics& workload) const;
+
+ private:
+  bool hip_available_;
+};
+
+// ---- fusion planner / HIP kernel generator -------------------------------------------------------
+enum class Terminal { ToArray, Sum, Count, LongCount, Average };
+
+struct FusedKernelPlan {
+  dc_linq_chain Program{};                // one fused program for all Filter/Map stages
+  Terminal Term = Terminal::ToArray;
+  std::vector<std::string> FusedOperationIds;
+  std::string Listing() const;            // human-readable program
+};
+
+class HipKernelGenerator {
+ public:
+  // Lowers the graph to one fused kernel: all Filter/Map stages (CanBeFused chains) plus an
+  // optional terminal Reduce that selects the Sum/Count kernel. Throws NotSupportedException for
+  // graphs the prebuilt kernels cannot run (OrderBy, GroupBy, Join, Min/Max, non-float lambdas,
+  // expressions needing more than two saved registers).
+  FusedKernelPlan GenerateHipKernel(const OperationGraph& graph) const;
+  // CudaKernelGenerator.cs:1163-1226: consecutive Map/Filter operations form one group.
+  static std::vector<const Operation*> IdentifyFusableOperations(const OperationGraph& graph);
+  static bool CanBeFused(const Operation& op);
+  // Appends the register program of one lambda: a value (ends in v) or a predicate (ends in p).
+  static void CompileLambda(const Expr& lambda, bool predicate, std::vector<dc_linq_instr>& code);
+};
+
+// ---- execution -------------------------------------------------------------------------------------
+struct QueryResult {
+  std::vector<float> Values;  // ToArray
+  double Sum = 0.0;           // Sum / Average (float64 accumulator)
+  int64_t Count = 0;
+};
+
+class RuntimeExecutor {
+ public:
+  explicit RuntimeExecutor(std::shared_ptr<Backends::Hip::HipAccelerator> accelerator) : acc_(std::move(accelerator)) {}
+  // Host source: allocate, copy in, launch, copy back only the compacted result.
+  QueryResult Execute(const FusedKernelPlan& plan, const float* data, size_t n);
+  // Device-resident source (no host round trip for the input).
+  QueryResult Execute(const FusedKernelPlan& plan, const IUnifiedMemoryBuffer& source, size_t n);
+  Backends::Hip::HipAccelerator& Accelerator() { return *acc_; }
+
+ private:
+  QueryResult Run(const FusedKernelPlan& plan, const float* device_in, size_t n);
+  std::shared_ptr<Backends::Hip::HipAccelerator> acc_;
+};
+
+class ComputeQueryProvider {
+ public:
+  // Default: the HIP accelerator of device 0 (the reference's provider probes a CudaAccelerator,
+  // ComputeQueryableExtensions.cs:125-179). May hold no accelerator; executing then throws.
+  ComputeQueryProvider();
+  explicit ComputeQueryProvider(std::shared_ptr<Backends::Hip::HipAccelerator> accelerator);
+  static std::shared_ptr<ComputeQueryProvider> Default();
+
+  bool HasAccelerator() const { return executor_ != nullptr; }
+  // Stages of ExecuteTyped (ComputeQueryableExtensions.cs:329-443): visit -> select backend ->
+  // generate the fused kernel -> run it.
+  QueryResult Execute(const std::vector<MethodCall>& chain, Terminal terminal, const float* host, size_t n,
+                      const IUnifiedMemoryBuffer* device);
+  FusedKernelPlan Plan(const std::vector<MethodCall>& chain, Terminal terminal, size_t n) const;
+
+ private:
+  std::unique_ptr<RuntimeExecutor> executor_;
+};
+
+class ComputeQueryable {
+ public:
+  ComputeQueryable(const float* data, size_t n, std::shared_ptr<ComputeQueryProvider> provider);
+  ComputeQueryable(const IUnifiedMemoryBuffer& device, std::shared_ptr<ComputeQueryProvider> provider);
+
+  ComputeQueryable Where(const Expr& predicate) const;
+  ComputeQueryable Select(const Expr& selector) const;
+  ComputeQueryable ComputeWhere(const Expr& predicate) const { return Where(predicate); }
+  ComputeQueryable ComputeSelect(const Expr& selector) const { return Select(selector); }
+  // Operators the HIP kernels do not implement: accepted into the chain, rejected at execution
+  // with NotSupportedException (as the reference's generators reject them).
+  ComputeQueryable OrderBy(const Expr& key) const;
+
+  std::vector<float> ToArray() const;
+  std::vector<float> ToComputeArray() const { return ToArray(); }
+  float Sum() const;          // float64 accumulator, cast to float (Enumerable.Sum(IEnumerable<float>))
+  int32_t Count() const;      // throws OverflowException above int.MaxValue
+  int64_t LongCount() const;
+  float Average() const;      // throws InvalidOperationException on an empty sequence
+  float Min() const;          // NotSupportedException
+  float Max() const;          // NotSupportedException
+
+  const std::vector<MethodCall>& Chain() const { return chain_; }
+  FusedKernelPlan Explain(Terminal terminal = Terminal::ToArray) const;
+
+ private:
+  QueryResult Run(Terminal t) const;
+  const float* host_ = nullptr;
+  const IUnifiedMemoryBuffer* device_ = nullptr;
+  size_t n_ = 0;
+  std::shared_ptr<ComputeQueryProvider> provider_;
+  std::vector<MethodCall> chain_;
+};
+
+// AsComputeQueryable (ComputeQueryableExtensions.cs:19-23). The source must outlive the query.
+ComputeQueryable AsComputeQueryable(const std::vector<float>& source,
+                                    std::shared_ptr<ComputeQueryProvider> provider = nullptr);
+ComputeQueryable AsComputeQueryable(const float* data, size_t n, std::shared_ptr<ComputeQueryProvider> provider = nullptr);
+ComputeQueryable AsComputeQueryable(const IUnifiedMemoryBuffer& device, std::shared_ptr<ComputeQueryProvider> provider = nullptr);
+
+}  // namespace DotCompute::Linq

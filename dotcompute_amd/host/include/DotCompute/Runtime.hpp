@@ -1,0 +1,180 @@
+// Runtime.hpp — kernel registry, accelerator discovery, dependency-injection entry points and the
+// orchestrator (IComputeOrchestrator / KernelExecutionService) for the HIP backend.
+//
+// Reference: IComputeOrchestrator (src/Core/DotCompute.Abstractions/Interfaces/
+// IComputeOrchestrator.cs:12-105); KernelExecutionService (src/Runtime/DotCompute.Runtime/Services/
+// KernelExecutionService.cs:16-1029); KernelRegistrationInfo (KernelExecutionService_Simplified.cs:
+// 525-610); AcceleratorRuntime (src/Runtime/DotCompute.Runtime/AcceleratorRuntime.cs:17-229);
+// AddDotComputeRuntime (ServiceCollectionExtensions.cs:36-112); the generated KernelRegistry
+// (src/Runtime/DotCompute.Generators/Kernel/Generation/KernelRegistrationEmitter.cs:40-201).
+#pragma once
+
+#include <functional>
+#include <map>
+#include <mutex>
+#include <optional>
+
+#include "Abstractions.hpp"
+#include "Backends/Hip.hpp"
+
+namespace DotCompute {
+
+// ---- host-side kernel arguments (the C# `params object[] args`) --------------------------------
+struct HostArray {
+  void* Data = nullptr;
+  size_t Length = 0;
+  ElementType Type = ElementType::Float32;
+};
+using KernelArg = std::variant<HostArray, IUnifiedMemoryBuffer*, int32_t, uint32_t, int64_t, float, double>;
+
+template <typename T>
+KernelArg Arg(std::vector<T>& v) {
+  return HostArray{v.data(), v.size(), ElementTypeOf<T>::value};
+}
+inline KernelArg Arg(IUnifiedMemoryBuffer& b) { return &b; }
+template <typename T, typename = std::enable_if_t<std::is_arithmetic_v<T>>>
+KernelArg Arg(T scalar) {
+  return scalar;
+}
+
+// ---- registry -----------------------------------------------------------------------------------
+struct KernelParameterInfo {
+  std::string Name;
+  ElementType Type = ElementType::Float32;
+  bool IsBuffer = false;
+  bool IsReadOnly = true;
+};
+
+// Built-in op bindings: a registry kernel can be served by one of the library's tuned entry
+// points instead of a module launch (VectorAdd -> dc_hip_vector_add_f32).
+enum class HipOp { None, VectorAddF32 };
+
+struct KernelRegistrationInfo {
+  std::string Name;
+  std::string FullName;
+  std::vector<std::string> SupportedBackends;  // [Kernel(Backends=...)]; default CPU only
+  std::vector<KernelParameterInfo> Parameters;
+  int32_t Dimensions = 1;
+  // HIP slot (what CudaSource / CudaEntryPoint / CudaNeedsLength are for CUDA,
+  // KernelExecutionService_Simplified.cs:567-585): a prebuilt gfx950 entry point.
+  std::string HipEntryPoint;
+  bool HipNeedsLength = false;
+  HipOp HipBuiltin = HipOp::None;
+};
+
+namespace Generated {
+// The registry the source generator would emit for the kernels of this build (the README's
+// VectorAdd quick start).
+struct KernelRegistry {
+  static std::vector<KernelRegistrationInfo> GetAllKernels();
+};
+}  // namespace Generated
+
+// ---- discovery / DI -----------------------------------------------------------------------------
+class ServiceCollection;
+
+class AcceleratorRuntime {
+ public:
+  explicit AcceleratorRuntime(std::vector<std::function<std::shared_ptr<IAccelerator>()>> factories)
+      : factories_(std::move(factories)) {}
+  // Calls every registered factory once; factories returning nullptr are skipped
+  // (AcceleratorRuntime.cs:86-100).
+  void Initialize();
+  const std::vector<std::shared_ptr<IAccelerator>>& GetAccelerators() const { return accelerators_; }
+
+ private:
+  std::vector<std::function<std::shared_ptr<IAccelerator>()>> factories_;
+  std::vector<std::shared_ptr<IAccelerator>> accelerators_;
+  bool initialized_ = false;
+};
+
+class IComputeOrchestrator;
+
+class ServiceProvider {
+ public:
+  std::shared_ptr<IComputeOrchestrator> GetRequiredOrchestrator() const;
+  std::shared_ptr<AcceleratorRuntime> Runtime() const { return runtime_; }
+
+ private:
+  friend class ServiceCollection;
+  std::shared_ptr<AcceleratorRuntime> runtime_;
+  std::shared_ptr<IComputeOrchestrator> orchestrator_;
+};
+
+class ServiceCollection {
+ public:
+  // services.AddDotComputeRuntime() (ServiceCollectionExtensions.cs:36-112).
+  ServiceCollection& AddDotComputeRuntime();
+  // services.AddHipBackend(): registers a factory that yields the HIP accelerator, or nothing when
+  // no gfx950 device is present (AddCudaBackend, CudaBackendPlugin.cs:311-354).
+  ServiceCollection& AddHipBackend(Backends::Hip::HipBackendOptions options = {});
+  // Any other accelerator (tests, mocks).
+  ServiceCollection& AddAccelerator(std::function<std::shared_ptr<IAccelerator>()> factory);
+  std::shared_ptr<ServiceProvider> BuildServiceProvider() const;
+
+ private:
+  bool runtime_added_ = false;
+  std::vector<std::function<std::shared_ptr<IAccelerator>()>> factories_;
+};
+
+// ---- orchestrator -------------------------------------------------------------------------------
+class IComputeOrchestrator {
+ public:
+  virtual ~IComputeOrchestrator() = default;
+  // IComputeOrchestrator.cs:21,31,41,51,58,73,81. The result is the first writable array
+  // (copied back from the device), as in KernelExecutionService.cs:475-501.
+  virtual std::future<std::vector<float>> ExecuteAsync(const std::string& kernelName, std::vector<KernelArg> args) = 0;
+  virtual std::future<std::vector<float>> ExecuteAsync(const std::string& kernelName, const std::string& preferredBackend,
+                                                       std::vector<KernelArg> args) = 0;
+  virtual std::future<std::vector<float>> ExecuteAsync(const std::string& kernelName, IAccelerator& accelerator,
+                                                       std::vector<KernelArg> args) = 0;
+  virtual std::future<void> ExecuteWithBuffersAsync(const std::string& kernelName,
+                                                    std::vector<IUnifiedMemoryBuffer*> buffers,
+                                                    std::vector<ScalarValue> scalarArgs) = 0;
+  virtual std::shared_ptr<IAccelerator> GetOptimalAcceleratorAsync(const std::string& kernelName) = 0;
+  virtual std::vector<std::shared_ptr<IAccelerator>> GetSupportedAcceleratorsAsync(const std::string& kernelName) = 0;
+  virtual bool ValidateKernelArgsAsync(const std::string& kernelName, const std::vector<KernelArg>& args) = 0;
+  virtual void PrecompileKernelAsync(const std::string& kernelName, IAccelerator* accelerator = nullptr) = 0;
+};
+
+class KernelExecutionService final : public IComputeOrchestrator {
+ public:
+  explicit KernelExecutionService(std::shared_ptr<AcceleratorRuntime> runtime);
+
+  void RegisterKernels(const std::vector<KernelRegistrationInfo>& kernels);
+  std::optional<KernelRegistrationInfo> TryResolveKernel(const std::string& name) const;
+
+  std::future<std::vector<float>> ExecuteAsync(const std::string& kernelName, std::vector<KernelArg> args) override;
+  std::future<std::vector<float>> ExecuteAsync(const std::string& kernelName, const std::string& preferredBackend,
+                                               std::vector<KernelArg> args) override;
+  std::future<std::vector<float>> ExecuteAsync(const std::string& kernelName, IAccelerator& accelerator,
+                                               std::vector<KernelArg> args) override;
+  std::future<void> ExecuteWithBuffersAsync(const std::string& kernelName, std::vector<IUnifiedMemoryBuffer*> buffers,
+                                            std::vector<ScalarValue> scalarArgs) override;
+  std::shared_ptr<IAccelerator> GetOptimalAcceleratorAsync(const std::string& kernelName) override;
+  std::vector<std::shared_ptr<IAccelerator>> GetSupportedAcceleratorsAsync(const std::string& kernelName) override;
+  bool ValidateKernelArgsAsync(const std::string& kernelName, const std::vector<KernelArg>& args) override;
+  void PrecompileKernelAsync(const std::string& kernelName, IAccelerator* accelerator = nullptr) override;
+
+  // KernelExecutionService.cs:835-858 with "HIP" added (priority above CPU).
+  static std::string MapDeviceTypeToBackend(const std::string& deviceType);
+  static int GetBackendPriority(const std::string& deviceType);
+  // KernelExecutionService.cs:382-406 and :342-354.
+  static size_t DeriveWorkSize(const KernelRegistrationInfo& registration, const std::vector<KernelArg>& args);
+  static KernelLaunchConfiguration DeriveLaunch(const KernelRegistrationInfo& registration,
+                                                const std::vector<KernelArg>& args, size_t totalWork);
+
+ private:
+  void EnsureInitialized();
+  std::vector<float> ExecuteOn(const KernelRegistrationInfo& reg, IAccelerator& accelerator,
+                               std::vector<KernelArg>& args);
+  std::shared_ptr<ICompiledKernel> GetCompiled(const KernelRegistrationInfo& reg, IAccelerator& accelerator);
+
+  std::shared_ptr<AcceleratorRuntime> runtime_;
+  mutable std::mutex mu_;
+  bool initialized_ = false;
+  std::map<std::string, KernelRegistrationInfo> registry_;     // by full and short name
+  std::map<std::string, std::shared_ptr<ICompiledKernel>> cache_;  // "<accelerator id>/<kernel>"
+};
+
+}  // namespace DotCompute

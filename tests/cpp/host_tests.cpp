@@ -1,0 +1,446 @@
+// C++ tests of the host layer (orchestrator, LINQ provider + fusion planner, algorithms), mirroring
+// the reference's own tests. CPU cases (--cpu) touch no device; GPU cases (--gpu) run on gfx950 and
+// are checked against the CPU oracle (oracle/liboracle.so), which this test binary links as the
+// checker only.
+#include <algorithm>
+#include <random>
+
+#include "DotCompute/Algorithms.hpp"
+#include "DotCompute/Linq.hpp"
+#include "DotCompute/Runtime.hpp"
+#include "test_framework.hpp"
+
+extern "C" {
+#include "../../oracle/oracle.h"
+}
+
+using namespace DotCompute;
+using namespace DotCompute::Linq;
+using DotCompute::Algorithms::CsrMatrix;
+using DotCompute::Algorithms::Matrix;
+using DotCompute::Algorithms::MatrixOperations;
+using DotCompute::Algorithms::SparseOps;
+
+namespace {
+
+std::vector<float> Uniform(size_t n, uint64_t seed, uint32_t stream = 0, int unit = 0) {
+  std::vector<float> v(n);
+  oracle_gen_uniform_f32(v.data(), (int64_t)n, seed, stream, unit);
+  return v;
+}
+
+bool BitsEqual(const std::vector<float>& a, const std::vector<float>& b) {
+  return a.size() == b.size() && (a.empty() || std::memcmp(a.data(), b.data(), a.size() * sizeof(float)) == 0);
+}
+
+std::string Listing(const Expr& where, const Expr& select) {
+  auto q = ComputeQueryable(nullptr, 0, std::make_shared<ComputeQueryProvider>(nullptr)).Where(where).Select(select);
+  return q.Explain().Listing();
+}
+
+// Evaluates a lambda tree exactly as C# evaluates it (one float rounding per operation); used to
+// check the generated register program against the tree it came from.
+float EvalValue(const ExprNode& n, float x) {
+  switch (n.Kind) {
+    case ExprKind::Parameter: return x;
+    case ExprKind::Constant: return n.Value;
+    case ExprKind::Negate: return -EvalValue(*n.Left, x);
+    case ExprKind::Abs: return std::fabs(EvalValue(*n.Left, x));
+    case ExprKind::Sqrt: return std::sqrt(EvalValue(*n.Left, x));
+    case ExprKind::Add: return EvalValue(*n.Left, x) + EvalValue(*n.Right, x);
+    case ExprKind::Subtract: return EvalValue(*n.Left, x) - EvalValue(*n.Right, x);
+    case ExprKind::Multiply: return EvalValue(*n.Left, x) * EvalValue(*n.Right, x);
+    case ExprKind::Divide: return EvalValue(*n.Left, x) / EvalValue(*n.Right, x);
+    case ExprKind::Min: {
+      float a = EvalValue(*n.Left, x), b = EvalValue(*n.Right, x);
+      if (std::isnan(a) || std::isnan(b)) return NAN;
+      if (a == b) return std::signbit(a) ? a : b;
+      return a < b ? a : b;
+    }
+    case ExprKind::Max: {
+      float a = EvalValue(*n.Left, x), b = EvalValue(*n.Right, x);
+      if (std::isnan(a) || std::isnan(b)) return NAN;
+      if (a == b) return std::signbit(a) ? b : a;
+      return a > b ? a : b;
+    }
+    default: throw std::logic_error("not a value");
+  }
+}
+
+bool EvalPred(const ExprNode& n, float x) {
+  switch (n.Kind) {
+    case ExprKind::GreaterThan: return EvalValue(*n.Left, x) > EvalValue(*n.Right, x);
+    case ExprKind::GreaterThanOrEqual: return EvalValue(*n.Left, x) >= EvalValue(*n.Right, x);
+    case ExprKind::LessThan: return EvalValue(*n.Left, x) < EvalValue(*n.Right, x);
+    case ExprKind::LessThanOrEqual: return EvalValue(*n.Left, x) <= EvalValue(*n.Right, x);
+    case ExprKind::Equal: return EvalValue(*n.Left, x) == EvalValue(*n.Right, x);
+    case ExprKind::NotEqual: return EvalValue(*n.Left, x) != EvalValue(*n.Right, x);
+    case ExprKind::AndAlso: return EvalPred(*n.Left, x) && EvalPred(*n.Right, x);
+    case ExprKind::OrElse: return EvalPred(*n.Left, x) || EvalPred(*n.Right, x);
+    case ExprKind::Not: return !EvalPred(*n.Left, x);
+    default: throw std::logic_error("not a predicate");
+  }
+}
+
+// Planner output for a Where(pred).Select(sel) chain, run by the oracle's interpreter, must equal
+// the direct evaluation of the two trees on every input.
+void CheckProgramAgainstTree(const Expr& pred, const Expr& sel, const std::vector<float>& xs) {
+  auto q = ComputeQueryable(nullptr, 0, std::make_shared<ComputeQueryProvider>(nullptr)).Where(pred).Select(sel);
+  FusedKernelPlan plan = q.Explain();
+  for (float x : xs) {
+    float y = 0.0f;
+    int32_t keep = oracle_linq_eval(&plan.Program, x, &y);
+    CHECK(keep >= 0);
+    const bool want = EvalPred(pred.Node(), x);
+    CHECK((keep == 1) == want);
+    if (want) {
+      const float ref = EvalValue(sel.Node(), x);
+      CHECK((std::isnan(ref) && std::isnan(y)) || std::memcmp(&ref, &y, 4) == 0);
+    }
+  }
+}
+
+std::shared_ptr<Backends::Hip::HipAccelerator> Gpu() {
+  static auto acc = Backends::Hip::TryCreateAccelerator();
+  if (!acc) throw std::runtime_error("no gfx950 device");
+  return acc;
+}
+
+}  // namespace
+
+// ============================== CPU: fusion planner ==============================================
+
+TEST_CPU(planner_emits_the_benchmark_chain) {
+  auto x = Param();
+  const std::string l = Listing(x > 0.0f, x * 2.0f + 1.0f);
+  CHECK(l == "terminal ToArray\n0: LOAD e\n1: CMP_GT 0\n2: FILTER\n3: LOAD e\n4: MUL 2\n5: ADD 1\n6: MAP\n");
+}
+
+TEST_CPU(planner_swaps_constant_on_the_left) {
+  auto x = Param();
+  CHECK(Listing(0.5f < x, 2.0f - x) == "terminal ToArray\n0: LOAD e\n1: CMP_GT 0.5\n2: FILTER\n3: LOAD e\n4: RSUB 2\n5: MAP\n");
+  CHECK(Listing(1.0f >= x, 3.0f / x) == "terminal ToArray\n0: LOAD e\n1: CMP_LE 1\n2: FILTER\n3: LOAD e\n4: RDIV 3\n5: MAP\n");
+}
+
+TEST_CPU(planner_folds_constants_like_csharp) {
+  auto x = Param();
+  CHECK(Listing(x > (1.0f - 1.0f), x * (2.0f + 1.0f)) ==
+        "terminal ToArray\n0: LOAD e\n1: CMP_GT 0\n2: FILTER\n3: LOAD e\n4: MUL 3\n5: MAP\n");
+}
+
+TEST_CPU(planner_uses_save_registers_for_two_subtrees) {
+  auto x = Param();
+  const std::string l = Listing(x != 0.0f, (x + 1.0f) * (x - 1.0f));
+  CHECK(l.find("STORE_S0") != std::string::npos);
+  CHECK(l.find("MUL s0") != std::string::npos);
+  std::vector<float> xs = Uniform(2000, 3);
+  CheckProgramAgainstTree(x != 0.0f, (x + 1.0f) * (x - 1.0f), xs);
+  CheckProgramAgainstTree(x > -0.5f, ((x + 1.0f) * (x - 1.0f)) / ((x * x) + (x - 3.0f)), xs);
+}
+
+TEST_CPU(planner_rejects_too_deep_expressions) {
+  auto x = Param();
+  // Needs two saved values for the right operand and two more while computing the left one.
+  Expr p1 = ((x + 1.0f) * (x - 1.0f)) + ((x + 2.0f) * (x - 2.0f));
+  Expr p2 = ((x + 3.0f) * (x - 3.0f)) + ((x + 4.0f) * (x - 4.0f));
+  CHECK_THROWS(NotSupportedException, Listing(x > 0.0f, p1 / p2));
+  // Sethi-Ullman order keeps this one within the two saved registers.
+  Expr ok = ((x + 1.0f) * (x - 1.0f)) / (((x + 2.0f) * (x - 2.0f)) + ((x + 3.0f) * (x - 3.0f)));
+  CheckProgramAgainstTree(x > 0.0f, ok, Uniform(3000, 8));
+}
+
+TEST_CPU(planner_compound_predicates_match_tree_evaluation) {
+  auto x = Param();
+  std::vector<float> xs = Uniform(5000, 11);
+  xs.push_back(0.0f);
+  xs.push_back(-0.0f);
+  xs.push_back(NAN);
+  CheckProgramAgainstTree(x > 0.0f && x < 0.5f, x * 2.0f + 1.0f, xs);
+  CheckProgramAgainstTree(x < -0.5f || x > 0.5f, MathF::Abs(x), xs);
+  CheckProgramAgainstTree((x < -0.5f || x > 0.5f) && (x != 0.75f || x * x > 0.9f), x - 0.25f, xs);
+  CheckProgramAgainstTree(!(x >= 0.0f), MathF::Sqrt(-x), xs);
+  CheckProgramAgainstTree(x * x + x > 0.1f, MathF::Min(x, 0.25f) + MathF::Max(x * 3.0f, -1.0f), xs);
+  CheckProgramAgainstTree(x > 0.0f && x < 0.9f && x != 0.5f, 1.0f / (x + 1.0f), xs);
+}
+
+TEST_CPU(planner_rejects_three_composite_terms) {
+  auto x = Param();
+  Expr p = ((x < 0.0f || x > 1.0f) && (x != 2.0f || x != 3.0f)) || ((x < 5.0f || x > 6.0f) && (x != 7.0f || x != 8.0f));
+  CHECK_THROWS(NotSupportedException, Listing(p, x));
+}
+
+TEST_CPU(planner_where_needs_a_predicate_and_select_a_value) {
+  auto x = Param();
+  CHECK_THROWS(NotSupportedException, Listing(x + 1.0f, x));
+  CHECK_THROWS(NotSupportedException, Listing(x > 0.0f, x > 1.0f));
+}
+
+TEST_CPU(visitor_maps_methods_like_the_reference) {
+  CHECK(*ExpressionTreeVisitor::MapMethodToOperationType("Select") == OperationType::Map);
+  CHECK(*ExpressionTreeVisitor::MapMethodToOperationType("Where") == OperationType::Filter);
+  CHECK(*ExpressionTreeVisitor::MapMethodToOperationType("Sum") == OperationType::Reduce);
+  CHECK(*ExpressionTreeVisitor::MapMethodToOperationType("OrderBy") == OperationType::OrderBy);
+  CHECK(*ExpressionTreeVisitor::MapMethodToOperationType("GroupBy") == OperationType::GroupBy);
+  CHECK(!ExpressionTreeVisitor::MapMethodToOperationType("Zip").has_value());
+  auto x = Param();
+  OperationGraph g = ExpressionTreeVisitor().Visit({{"Where", x > 0.0f}, {"Select", x * 2.0f}, {"Sum", std::nullopt}});
+  CHECK(g.Operations.size() == 3);
+  CHECK(g.Operations[1].Dependencies.size() == 1 && g.Operations[1].Dependencies[0] == "op_0");
+  CHECK(HipKernelGenerator::IdentifyFusableOperations(g).size() == 2);
+  CHECK(g.Root()->Type == OperationType::Reduce);
+}
+
+TEST_CPU(planner_terminals_and_unsupported_operators) {
+  auto x = Param();
+  auto p = std::make_shared<ComputeQueryProvider>(nullptr);
+  auto q = ComputeQueryable(nullptr, 0, p).Where(x > 0.0f).Select(x * 2.0f + 1.0f);
+  CHECK(q.Explain(Terminal::Sum).Term == Terminal::Sum);
+  CHECK(q.Explain(Terminal::Average).Term == Terminal::Average);
+  CHECK(q.Explain(Terminal::Count).FusedOperationIds.size() == 3);
+  CHECK_THROWS(NotSupportedException, q.OrderBy(x).Explain());
+  CHECK_THROWS(NotSupportedException, q.Min());
+}
+
+// ============================== CPU: runtime, registry, no-device behaviour =======================
+
+TEST_CPU(orchestrator_backend_mapping_and_priority) {
+  CHECK(KernelExecutionService::MapDeviceTypeToBackend("hip") == "HIP");
+  CHECK(KernelExecutionService::MapDeviceTypeToBackend("ROCm") == "HIP");
+  CHECK(KernelExecutionService::MapDeviceTypeToBackend("cuda") == "CUDA");
+  CHECK(KernelExecutionService::GetBackendPriority("HIP") < KernelExecutionService::GetBackendPriority("CPU"));
+  CHECK(KernelExecutionService::GetBackendPriority("Vulkan") == 999);
+}
+
+TEST_CPU(orchestrator_work_size_and_launch) {
+  auto regs = Generated::KernelRegistry::GetAllKernels();
+  CHECK(regs.size() == 1 && regs[0].Name == "VectorAdd" && regs[0].HipNeedsLength);
+  std::vector<float> a(1000), b(1000), r(1000);
+  std::vector<KernelArg> args{Arg(a), Arg(b), Arg(r)};
+  CHECK(KernelExecutionService::DeriveWorkSize(regs[0], args) == 1000);
+  KernelLaunchConfiguration lc = KernelExecutionService::DeriveLaunch(regs[0], args, 1000);
+  CHECK(lc.BlockSize.X == 256 && lc.GridSize.X == 4 && lc.GridSize.Y == 1);
+}
+
+TEST_CPU(orchestrator_without_accelerators_throws) {
+  ServiceCollection services;
+  services.AddDotComputeRuntime();
+  auto sp = services.BuildServiceProvider();
+  auto orch = sp->GetRequiredOrchestrator();
+  std::vector<float> a{1, 2}, b{3, 4}, r(2);
+  CHECK_THROWS(InvalidOperationException, orch->ExecuteAsync("VectorAdd", {Arg(a), Arg(b), Arg(r)}).get());
+  CHECK_THROWS(ArgumentException, orch->ExecuteAsync("NoSuchKernel", {Arg(a)}).get());
+  CHECK(!orch->ValidateKernelArgsAsync("VectorAdd", {Arg(a), Arg(b)}));   // too few arguments
+  CHECK(!orch->ValidateKernelArgsAsync("VectorAdd", {Arg(a), Arg(b), Arg(1.0f)}));  // scalar for a buffer
+}
+
+TEST_CPU(service_provider_requires_runtime) {
+  ServiceCollection services;
+  CHECK_THROWS(InvalidOperationException, services.BuildServiceProvider()->GetRequiredOrchestrator());
+}
+
+TEST_CPU(hip_backend_registration_skips_missing_device) {
+  if (Backends::Hip::HipAccelerator::DeviceCount() > 0) return;  // only meaningful without a GPU
+  ServiceCollection services;
+  services.AddDotComputeRuntime().AddHipBackend();
+  auto sp = services.BuildServiceProvider();
+  sp->Runtime()->Initialize();
+  CHECK(sp->Runtime()->GetAccelerators().empty());
+  CHECK(Backends::Hip::TryCreateAccelerator() == nullptr);
+  // The LINQ provider refuses to run instead of falling back to the host.
+  auto x = Param();
+  std::vector<float> src{1, 2, 3};
+  auto q = AsComputeQueryable(src, std::make_shared<ComputeQueryProvider>(nullptr)).Where(x > 1.0f);
+  CHECK_THROWS(InvalidOperationException, q.ToArray());
+}
+
+TEST_CPU(csr_matrix_validation_matches_reference) {
+  CHECK_THROWS(ArgumentException, CsrMatrix<float>(2, 2, {1.0f}, {0}, {0, 1}));          // rowPointers != rows+1
+  CHECK_THROWS(ArgumentException, CsrMatrix<float>(1, 2, {1.0f, 2.0f}, {0}, {0, 2}));   // values vs columns
+  CsrMatrix<float> ok(1, 2, {1.0f, 2.0f}, {0, 1}, {0, 2});
+  CHECK(ok.NonZeroCount() == 2);
+  CHECK_THROWS(ArgumentException, Matrix(2, 2, std::vector<float>(3)));
+}
+
+// ============================== GPU: orchestrator ==================================================
+
+TEST_GPU(readme_quick_start_vector_add_on_hip) {
+  ServiceCollection services;
+  services.AddDotComputeRuntime().AddHipBackend();
+  auto orch = services.BuildServiceProvider()->GetRequiredOrchestrator();
+  std::vector<float> a{1, 2, 3, 4, 5}, b{10, 20, 30, 40, 50}, result(5);
+  std::vector<float> out = orch->ExecuteAsync("VectorAdd", "HIP", {Arg(a), Arg(b), Arg(result)}).get();
+  CHECK((result == std::vector<float>{11, 22, 33, 44, 55}));
+  CHECK(out == result);
+}
+
+TEST_GPU(vector_add_100k_bit_exact_and_unknown_backend_falls_back) {
+  ServiceCollection services;
+  services.AddDotComputeRuntime().AddHipBackend();
+  auto orch = services.BuildServiceProvider()->GetRequiredOrchestrator();
+  auto a = Uniform(100000, 42, 0), b = Uniform(100000, 42, 1);
+  std::vector<float> r(100000), ref(100000);
+  oracle_vector_add_f32(a.data(), b.data(), ref.data(), 100000);
+  orch->ExecuteAsync("VectorAdd", "HIP", {Arg(a), Arg(b), Arg(r)}).get();
+  CHECK(BitsEqual(r, ref));
+  std::fill(r.begin(), r.end(), 0.0f);
+  orch->ExecuteAsync("VectorAdd", "Vulkan", {Arg(a), Arg(b), Arg(r)}).get();  // -> optimal accelerator
+  CHECK(BitsEqual(r, ref));
+  std::fill(r.begin(), r.end(), 0.0f);
+  orch->ExecuteAsync("Kernels.VectorAdd", {Arg(a), Arg(b), Arg(r)}).get();     // full name, no backend
+  CHECK(BitsEqual(r, ref));
+}
+
+TEST_GPU(compiled_kernel_from_code_object_matches) {
+  auto acc = Gpu();
+  KernelDefinition def;
+  def.Name = "VectorAdd";
+  def.EntryPoint = "VectorAdd";
+  auto kernel = acc->CompileKernelAsync(def).get();
+  const size_t n = 70001;
+  auto a = Uniform(n, 5, 0), b = Uniform(n, 5, 1);
+  auto da = acc->Memory().AllocateAsync<float>(n), db = acc->Memory().AllocateAsync<float>(n),
+       dr = acc->Memory().AllocateAsync<float>(n);
+  da->CopyFromAsync(a).get();
+  db->CopyFromAsync(b).get();
+  KernelArguments args;
+  args.AddBuffer(da.get());
+  args.AddBuffer(db.get());
+  args.AddBuffer(dr.get());
+  args.AddScalar((uint32_t)n);
+  args.LaunchConfiguration.GridSize = {(uint32_t)((n + 255) / 256), 1, 1};
+  kernel->ExecuteAsync(args).get();
+  acc->SynchronizeAsync().get();
+  std::vector<float> r(n), ref(n);
+  dr->CopyToAsync(r).get();
+  oracle_vector_add_f32(a.data(), b.data(), ref.data(), (int64_t)n);
+  CHECK(BitsEqual(r, ref));
+  def.EntryPoint = "NoSuchKernel";
+  CHECK_THROWS(ArgumentException, acc->CompileKernelAsync(def).get());
+}
+
+// ============================== GPU: LINQ provider =================================================
+
+TEST_GPU(linq_reference_golden_vectors) {
+  auto x = Param();
+  auto p = std::make_shared<ComputeQueryProvider>(Gpu());
+  // ComputeQueryProviderTests.cs:341-365, :602-612
+  std::vector<float> s15{1, 2, 3, 4, 5};
+  CHECK((AsComputeQueryable(s15, p).Where(x > 3.0f).ToArray() == std::vector<float>{4, 5}));
+  std::vector<float> s3{1, 2, 3};
+  CHECK((AsComputeQueryable(s3, p).Select(x * 2.0f).ToArray() == std::vector<float>{2, 4, 6}));
+  CHECK(AsComputeQueryable(s15, p).Sum() == 15.0f);
+  // LinqBackendIntegrationTests.cs:51-66, :139-176
+  CHECK((AsComputeQueryable(s15, p).Where(x > 2.0f).Select(x * 2.0f).ToArray() == std::vector<float>{6, 8, 10}));
+  std::vector<float> s10(10);
+  for (int i = 0; i < 10; ++i) s10[i] = (float)(i + 1);
+  CHECK((AsComputeQueryable(s10, p).Where(x > 3.0f).Select(x * 3.0f).ToArray() ==
+         std::vector<float>{12, 15, 18, 21, 24, 27, 30}));
+  std::vector<float> s1000(1000);
+  for (int i = 0; i < 1000; ++i) s1000[i] = (float)(i + 1);
+  CHECK(AsComputeQueryable(s1000, p).Sum() == 500500.0f);
+  CHECK(AsComputeQueryable(s10, p).Where(x > 5.0f).Count() == 5);
+  CHECK(AsComputeQueryable(s10, p).Average() == 5.5f);
+  std::vector<float> empty;
+  CHECK_THROWS(InvalidOperationException, AsComputeQueryable(empty, p).Average());
+  CHECK(AsComputeQueryable(empty, p).Sum() == 0.0f);
+}
+
+TEST_GPU(linq_benchmark_chain_bit_exact_vs_linq_to_objects) {
+  auto x = Param();
+  auto p = std::make_shared<ComputeQueryProvider>(Gpu());
+  const size_t n = 1 << 20;
+  auto src = Uniform(n, 44, 0);
+  std::vector<float> ref(n);
+  ref.resize((size_t)oracle_where_gt0_select_2x_plus_1(src.data(), (int64_t)n, ref.data()));
+  auto q = AsComputeQueryable(src, p).Where(x > 0.0f).Select(x * 2.0f + 1.0f);
+  CHECK(BitsEqual(q.ToArray(), ref));
+  int64_t cnt = 0;
+  double seq = 0.0;
+  float fref = oracle_where_gt0_select_2x_plus_1_sum(src.data(), (int64_t)n, &cnt, &seq);
+  const float got = q.Sum();
+  CHECK(std::fabs(got - fref) <= 1e-5 * 20 * std::fabs(seq));
+  CHECK(q.LongCount() == cnt);
+}
+
+TEST_GPU(linq_device_resident_source) {
+  auto x = Param();
+  auto acc = Gpu();
+  auto p = std::make_shared<ComputeQueryProvider>(acc);
+  auto src = Uniform(300000, 9, 0);
+  auto dsrc = acc->Memory().AllocateAsync<float>(src.size());
+  dsrc->CopyFromAsync(src).get();
+  std::vector<float> ref(src.size());
+  ref.resize((size_t)oracle_where_gt0_select_2x_plus_1(src.data(), (int64_t)src.size(), ref.data()));
+  CHECK(BitsEqual(AsComputeQueryable(*dsrc, p).Where(x > 0.0f).Select(x * 2.0f + 1.0f).ToArray(), ref));
+}
+
+TEST_GPU(linq_general_lambdas_match_tree_evaluation) {
+  auto x = Param();
+  auto p = std::make_shared<ComputeQueryProvider>(Gpu());
+  auto src = Uniform(200000, 21, 0);
+  struct Case {
+    Expr w, s;
+  };
+  std::vector<Case> cases = {
+      {x > 0.0f && x < 0.5f, (x + 1.0f) * (x - 1.0f)},
+      {(x < -0.5f || x > 0.5f) && (x != 0.75f || x * x > 0.9f), MathF::Abs(x) - 0.25f},
+      {!(x >= 0.0f), MathF::Sqrt(-x) / (x - 2.0f)},
+      {x * x + x > 0.1f, MathF::Min(x, 0.25f) + MathF::Max(x * 3.0f, -1.0f)},
+  };
+  for (const Case& c : cases) {
+    std::vector<float> ref;
+    for (float v : src)
+      if (EvalPred(c.w.Node(), v)) ref.push_back(EvalValue(c.s.Node(), v));
+    CHECK(BitsEqual(AsComputeQueryable(src, p).Where(c.w).Select(c.s).ToArray(), ref));
+  }
+}
+
+// ============================== GPU: algorithms ====================================================
+
+TEST_GPU(matrix_multiply_matches_float64_reference) {
+  auto acc = Gpu();
+  const int m = 512, k = 384, n = 768;
+  Matrix a(m, k, Uniform((size_t)m * k, 42)), b(k, n, Uniform((size_t)k * n, 43));
+  Matrix c = MatrixOperations::MultiplyAsync(a, b, *acc).get();
+  std::vector<int64_t> rows(m);
+  for (int i = 0; i < m; ++i) rows[i] = i;
+  std::vector<double> ref((size_t)m * n), absref((size_t)m * n);
+  oracle_gemm_f64_rows(a.Data().data(), b.Data().data(), ref.data(), absref.data(), m, n, k, rows.data(), m, 8);
+  for (size_t i = 0; i < ref.size(); ++i) CHECK(std::fabs(c.Data()[i] - ref[i]) <= 1e-4 * absref[i]);
+  Matrix bad(k + 1, n);
+  CHECK_THROWS(ArgumentException, MatrixOperations::MultiplyAsync(a, bad, *acc).get());
+  Matrix cb = MatrixOperations::MultiplyAsync(a, b, *acc, Algorithms::MatMulPrecision::BFloat16).get();
+  double num = 0, den = 0;
+  for (size_t i = 0; i < ref.size(); ++i) {
+    num += (cb.Data()[i] - ref[i]) * (cb.Data()[i] - ref[i]);
+    den += ref[i] * ref[i];
+  }
+  CHECK(std::sqrt(num / den) < 1e-2);  // bf16 inputs vs fp32 inputs: ~2^-9 relative input rounding
+}
+
+TEST_GPU(sparse_spmv_and_power_iteration) {
+  auto acc = Gpu();
+  const int64_t rows = 200000;
+  std::vector<int32_t> rp(rows + 1);
+  int64_t nnz = oracle_gen_zipf_rowptr(rows, 2.0, 4096, 42, rp.data());
+  std::vector<int32_t> col((size_t)nnz);
+  std::vector<float> val((size_t)nnz);
+  oracle_gen_zipf_fill(rows, rows, 42, rp.data(), col.data(), val.data());
+  CsrMatrix<float> A((int32_t)rows, (int32_t)rows, val, col, rp);
+  auto x = Uniform((size_t)rows, 42, 5, 1);
+  std::vector<float> y = SparseOps::SpMV(A, x, *acc);
+  std::vector<double> x64(x.begin(), x.end()), y64((size_t)rows), scale((size_t)rows);
+  oracle_spmv_csr_f64(rp.data(), col.data(), val.data(), x64.data(), y64.data(), rows);
+  for (int64_t r = 0; r < rows; ++r) CHECK(std::fabs(y[r] - y64[r]) <= 1e-4 * std::fabs(y64[r]) + 1e-30);
+  std::vector<float> wrong((size_t)rows + 1);
+  CHECK_THROWS(ArgumentException, SparseOps::SpMV(A, wrong, *acc));
+  double s = 0.0;
+  std::vector<float> xp = SparseOps::PowerIterate(A, x, 20, *acc, &s);
+  std::vector<float> xo = x, yo((size_t)rows);
+  double so = 0.0;
+  oracle_spmv_power_f32(rp.data(), col.data(), val.data(), xo.data(), yo.data(), rows, 20, &so);
+  CHECK(std::fabs(s - so) <= 1e-4 * std::fabs(so));
+  for (int64_t r = 0; r < rows; ++r) CHECK(std::fabs(xp[r] - xo[r]) <= 1e-4 * std::fabs(xo[r]) + 1e-12);
+}
+
+int main(int argc, char** argv) { return dctest_main(argc, argv); }

@@ -1,0 +1,241 @@
+"""Pins the CPU oracle (oracle/liboracle.so) before it is trusted as the GPU checker.
+
+Each oracle function is checked against something independent of it: the reference's own known
+answers, the published SplitMix64 outputs, golden vectors computed with NumPy / math.fsum
+(tests/golden/hot_path_golden.json, written by tests/golden/make_golden.py without the oracle),
+closed forms (Zipf mean degree, identity matrices, stochastic-matrix invariants) and brute force
+on small inputs. A few tests plant a mistake in a copy of an oracle result and check that the
+comparison used by the GPU tests catches it.
+"""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+
+GOLDEN = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "hot_path_golden.json")))
+KA = GOLDEN["reference_known_answers"]
+
+
+def from_bits(bits):
+    return np.array(bits, np.uint32).view(np.float32)
+
+
+# ------------------------------------------------------------------ generators
+def test_splitmix64_published_outputs():
+    # First three outputs of SplitMix64 started from state 0 (Steele/Lea/Flood; Vigna's splitmix64.c).
+    expected = [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F]
+    state = 0
+    for e in expected:
+        assert oracle.splitmix64(state) == e
+        state = (state + 0x9E3779B97F4A7C15) & (2**64 - 1)
+    assert [int(h, 16) for h in GOLDEN["splitmix64_from_zero"]] == expected
+
+
+def test_uniform_generators_match_golden():
+    inp = GOLDEN["inputs"]
+    assert np.array_equal(oracle.gen_uniform_f32(4096, 42, 0).view(np.uint32), np.array(inp["f32_seed42_stream0_bits"], np.uint32))
+    assert np.array_equal(oracle.gen_uniform_f32(4096, 42, 1).view(np.uint32), np.array(inp["f32_seed42_stream1_bits"], np.uint32))
+    assert np.array_equal(oracle.gen_uniform_f32(64, 42, 5, True).view(np.uint32),
+                          np.array(inp["f32_unit_seed42_stream5_bits"], np.uint32))
+    assert oracle.gen_uniform_i32(4096, 43, 1, -1000, 1000).tolist() == inp["i32_seed43_stream1"]
+
+
+def test_uniform_distribution_properties():
+    x = oracle.gen_uniform_f32(1_000_000, 7, 0)
+    assert x.min() >= -1.0 and x.max() < 1.0
+    assert np.all((x.astype(np.float64) + 1.0) * 2**23 == np.round((x.astype(np.float64) + 1.0) * 2**23))  # 2^-23 grid
+    assert abs(float(x.mean())) < 3e-3 and abs(float((x > 0).mean()) - 0.5) < 2e-3
+    u = oracle.gen_uniform_f32(1_000_000, 7, 0, True)
+    assert u.min() >= 0.0 and u.max() < 1.0 and abs(float(u.mean()) - 0.5) < 2e-3
+    i = oracle.gen_uniform_i32(1_000_000, 7, 1, -1000, 1000)
+    assert i.min() == -1000 and i.max() == 1000 and abs(float(i.mean())) < 2.0
+
+
+def test_zipf_graph_closed_form_and_invariants():
+    rows = 1_000_000
+    rp, col, val = oracle.gen_zipf_csr(rows, 42, alpha=2.0, max_degree=4096)
+    deg = np.diff(rp)
+    # E[deg] for Zipf(2) on [1, 4096] = H_4096 / H_4096^(2)
+    k = np.arange(1, 4097, dtype=np.float64)
+    mean = (1.0 / k).sum() / (k ** -2.0).sum()
+    assert abs(mean - 5.4) < 0.02
+    assert abs(deg.mean() - mean) / mean < 0.02
+    assert deg.min() >= 1 and deg.max() <= 4096
+    p1 = 1.0 / (k ** -2.0).sum()  # P(deg = 1)
+    assert abs(float((deg == 1).mean()) - p1) < 3e-3
+    assert np.all(np.diff(rp) >= 1) and rp[0] == 0 and rp[-1] == col.size
+    rows_of = np.repeat(np.arange(rows), deg)
+    assert not np.any(col == rows_of), "self-loop"
+    assert col.min() >= 0 and col.max() < rows
+    assert np.array_equal(val, (np.float32(1.0) / deg.astype(np.float32))[rows_of])
+
+
+# ------------------------------------------------------------------ VectorAdd
+def test_vector_add_known_answer_and_golden():
+    r = KA["README.md:46-57 VectorAdd"]
+    assert oracle.vector_add_f32(np.array(r["a"], np.float32), np.array(r["b"], np.float32)).tolist() == r["result"]
+    a = from_bits(GOLDEN["inputs"]["f32_seed42_stream0_bits"])
+    b = from_bits(GOLDEN["inputs"]["f32_seed42_stream1_bits"])
+    assert np.array_equal(oracle.vector_add_f32(a, b).view(np.uint32), np.array(GOLDEN["vector_add_bits"], np.uint32))
+
+
+# ------------------------------------------------------------------ Sum
+def test_sum_known_answers():
+    assert oracle.sum_f32_enumerable(np.arange(1, 6, dtype=np.float32))[0] == KA["ComputeQueryProviderTests.cs:602-612 Sum 1..5"]
+    assert oracle.sum_f32_enumerable(np.arange(1, 1001, dtype=np.float32))[0] == KA["LinqBackendIntegrationTests.cs:164-176 Sum 1..1000"]
+    assert oracle.sum_f32_enumerable(np.zeros(0, np.float32))[0] == 0.0
+
+
+def test_sum_f32_against_exact_sum():
+    a = from_bits(GOLDEN["inputs"]["f32_seed42_stream0_bits"])
+    exact = GOLDEN["sum_f32_exact"]
+    assert oracle.sum_f32_compensated(a) == pytest.approx(exact, rel=1e-15, abs=1e-12)
+    f, d = oracle.sum_f32_enumerable(a)
+    assert abs(d - exact) <= 1e-12 * max(abs(exact), 1)
+    assert f == np.float32(d)
+    big = oracle.gen_uniform_f32(2_000_000, 9, 0)
+    fs = math.fsum(big.astype(np.float64))
+    assert abs(oracle.sum_f32_compensated(big) - fs) <= 1e-12 * abs(fs) + 1e-9
+    fp, dp = oracle.sum_f32_partitioned(big, 8)
+    assert abs(dp - fs) <= 1e-10 * abs(fs) + 1e-6
+    # the sum is invariant under permutation up to rounding
+    perm = np.random.default_rng(1).permutation(big)
+    assert abs(oracle.sum_f32_compensated(perm) - fs) <= 1e-12 * abs(fs) + 1e-9
+
+
+def test_sum_i32_exact_and_checked_semantics():
+    x = np.array(GOLDEN["inputs"]["i32_seed43_stream1"], np.int32)
+    assert oracle.sum_i32_exact(x) == GOLDEN["sum_i32_exact"] == oracle.sum_i32_checked(x)
+    with pytest.raises(OverflowError):
+        oracle.sum_i32_checked(np.array([2**31 - 1, 1], np.int32))
+    with pytest.raises(OverflowError):  # a running total that leaves int32 throws even if the end fits
+        oracle.sum_i32_checked(np.array([2**31 - 1, 1, -1], np.int32))
+    assert oracle.sum_i32_checked(np.array([2**31 - 1, -1, 1], np.int32)) == 2**31 - 1
+    assert oracle.sum_i32_checked(np.array([-(2**31), 0], np.int32)) == -(2**31)
+
+
+# ------------------------------------------------------------------ LINQ
+def _chain(code):
+    from dotcompute_amd.hip import LinqChain
+    return LinqChain.assemble(code)
+
+
+def test_where_select_known_answers_through_interpreter():
+    from dotcompute_amd.hip import CMP_GT, FILTER, LOAD, MAP, MUL, SRC_ELEM, SRC_IMM
+    w3 = _chain([(LOAD, SRC_ELEM, 0), (CMP_GT, SRC_IMM, 3), (FILTER, SRC_IMM, 0)])
+    assert oracle.linq_where_select(w3, np.arange(1, 6, dtype=np.float32)).tolist() == KA[
+        "ComputeQueryProviderTests.cs:341-365 Where(x>3) over 1..5"]
+    s2 = _chain([(LOAD, SRC_ELEM, 0), (MUL, SRC_IMM, 2), (MAP, SRC_IMM, 0)])
+    assert oracle.linq_where_select(s2, np.array([1, 2, 3], np.float32)).tolist() == KA[
+        "ComputeQueryProviderTests.cs:341-365 Select(x*2) over 1,2,3"]
+    ws = _chain([(LOAD, SRC_ELEM, 0), (CMP_GT, SRC_IMM, 2), (FILTER, SRC_IMM, 0),
+                 (LOAD, SRC_ELEM, 0), (MUL, SRC_IMM, 2), (MAP, SRC_IMM, 0)])
+    assert oracle.linq_where_select(ws, np.arange(1, 6, dtype=np.float32)).tolist() == KA[
+        "LinqBackendIntegrationTests.cs:51-66 Where(x>2).Select(x*2) over 1..5"]
+
+
+def test_benchmark_chain_matches_numpy_golden_and_interpreter():
+    from dotcompute_amd import hip
+
+    a = from_bits(GOLDEN["inputs"]["f32_seed42_stream0_bits"])
+    ref = np.array(GOLDEN["where_gt0_select_2x_plus_1_bits"], np.uint32)
+    hand = oracle.where_gt0_select_2x_plus_1(a)
+    assert np.array_equal(hand.view(np.uint32), ref)
+    interp = oracle.linq_where_select(hip.where_gt0_select_2x_plus_1(), a)
+    assert np.array_equal(interp.view(np.uint32), ref)
+    f, d, cnt = oracle.where_gt0_select_2x_plus_1_sum(a)
+    assert cnt == ref.size and abs(d - GOLDEN["where_gt0_select_2x_plus_1_sum_exact"]) <= 1e-12 * abs(d)
+    # +0 and -0 are dropped, NaN is dropped, inf maps to inf
+    edge = np.array([0.0, -0.0, np.nan, np.inf, 1e-45, -1.0], np.float32)
+    assert oracle.where_gt0_select_2x_plus_1(edge).tolist() == [np.inf, np.float32(1e-45) * 2 + 1]
+
+
+def test_planted_mistake_is_caught():
+    """The bit comparison the GPU tests use must reject an off-by-one-ulp or reordered result."""
+    a = oracle.gen_uniform_f32(10_000, 3, 0)
+    good = oracle.where_gt0_select_2x_plus_1(a)
+    bad = good.copy()
+    bad.view(np.uint32)[17] += 1
+    assert not np.array_equal(bad.view(np.uint32), good.view(np.uint32))
+    swapped = good.copy()
+    swapped[[3, 4]] = swapped[[4, 3]]
+    assert not np.array_equal(swapped.view(np.uint32), good.view(np.uint32))
+
+
+# ------------------------------------------------------------------ GEMM
+def test_gemm_against_numpy_float64_golden():
+    a = from_bits(GOLDEN["inputs"]["f32_seed42_stream0_bits"])[: 16 * 24].reshape(16, 24)
+    b = from_bits(GOLDEN["inputs"]["f32_seed42_stream1_bits"])[: 24 * 8].reshape(24, 8)
+    ref = np.array(GOLDEN["gemm_16x24x8_f64"]).reshape(16, 8)
+    c64, absc = oracle.gemm_f64_rows(a, b, np.arange(16))
+    assert np.allclose(c64, ref, rtol=0, atol=1e-12)
+    assert np.all(absc >= np.abs(c64) - 1e-12)
+    c32 = oracle.gemm_f32_naive(a, b)
+    assert np.all(np.abs(c32 - ref) <= 1e-5 * absc)
+
+
+def test_gemm_blocked_equals_naive_bitwise_and_identity():
+    a = oracle.gen_uniform_f32(70 * 130, 1, 0).reshape(70, 130)
+    b = oracle.gen_uniform_f32(130 * 90, 1, 1).reshape(130, 90)
+    # MatrixOperations.MultiplyBlocked keeps each entry's sequential-k order across 64-blocks
+    assert np.array_equal(oracle.gemm_f32_blocked(a, b), oracle.gemm_f32_naive(a, b, threads=4))
+    eye = np.eye(130, dtype=np.float32)
+    assert np.array_equal(oracle.gemm_f32_naive(a, eye), a)
+
+
+def test_gemm_rank_one_closed_form():
+    u = oracle.gen_uniform_f32(64, 2, 0).reshape(64, 1)
+    v = oracle.gen_uniform_f32(64, 2, 1).reshape(1, 64)
+    c, _ = oracle.gemm_f64_rows(u, v, np.arange(64))
+    assert np.array_equal(c, u.astype(np.float64) @ v.astype(np.float64))
+
+
+def test_bf16_rounding():
+    x = np.array([1.0, 1.0039062, 1.0117188, -2.5, np.inf, np.nan, 3.4028235e38, 3.3895314e38], np.float32)
+    h = oracle.f32_to_bf16(x)
+    # 1.0039062 = 0x3F808000: exact tie -> even (0x3F80); 1.0117188 = 0x3F818000: tie -> 0x3F82
+    assert h[0] == 0x3F80 and h[1] == 0x3F80 and h[2] == 0x3F82 and h[3] == 0xC020
+    assert h[4] == 0x7F80 and (h[5] & 0x7FFF) > 0x7F80
+    assert np.isinf(oracle.bf16_to_f32(h[6:7])[0])  # FLT_MAX rounds up past the largest finite bf16
+    assert h[7] == 0x7F7F  # the largest finite bf16 is exact
+    r = oracle.bf16_to_f32(oracle.f32_to_bf16(oracle.gen_uniform_f32(10000, 5, 0)))
+    assert np.max(np.abs(r - oracle.gen_uniform_f32(10000, 5, 0))) <= 2.0 ** -9
+
+
+# ------------------------------------------------------------------ SpMV
+def test_spmv_golden_and_dimension_check():
+    g = GOLDEN["csr_6x6"]
+    rp = np.array(g["row_pointers"], np.int32)
+    col = np.array(g["col_indices"], np.int32)
+    val = from_bits(g["values_f32_bits"])
+    x = np.array(g["x"], np.float32)
+    y = oracle.spmv_csr_f32(rp, col, val, x)
+    assert np.allclose(y, g["y_f64"], rtol=1e-6, atol=0)
+    assert y[1] == 0.0  # empty row
+    with pytest.raises(ValueError):
+        oracle.spmv_csr_f32(rp, col, val, x, cols=7)
+
+
+def test_spmv_dense_bruteforce_and_power_invariants():
+    rows = 300
+    rp, col, val = oracle.gen_zipf_csr(rows, 5, max_degree=rows - 1)
+    x = oracle.gen_uniform_f32(rows, 5, 5, True)
+    dense = np.zeros((rows, rows))
+    for r in range(rows):
+        for i in range(rp[r], rp[r + 1]):
+            dense[r, col[i]] += val[i]
+    assert np.allclose(oracle.spmv_csr_f32(rp, col, val, x), dense @ x.astype(np.float64), rtol=1e-5, atol=0)
+    # each row sums its out-degree values 1/deg: A·1 = 1 (row-stochastic)
+    assert np.allclose(oracle.spmv_csr_f32(rp, col, val, np.ones(rows, np.float32)), 1.0, rtol=1e-6)
+    xp, s = oracle.spmv_power_f32(rp, col, val, x, 20)
+    assert np.all(xp >= 0) and abs(float(np.sum(xp, dtype=np.float64)) - 1.0) < 1e-5
+    # power iteration of a row-stochastic matrix in float64 converges to the same direction
+    xd = x.astype(np.float64)
+    for _ in range(20):
+        yd = dense @ xd
+        xd = yd / yd.sum()
+    assert np.allclose(xp, xd, rtol=1e-4, atol=1e-9)
