@@ -27,6 +27,8 @@ struct dc_hip_ctx {
   // SpMV scratch: the list of long rows (handled a workgroup per row) and small device scalars.
   int32_t* spmv_rows = nullptr;
   size_t spmv_rows_cap = 0;
+  int32_t* spmv_windows = nullptr;  // first row of each nonzero window
+  size_t spmv_windows_cap = 0;
   double* scalars = nullptr;  // 64 doubles
 
   // Decoupled-lookback status words, one uint64 per tile (grows on demand). A word is valid only
@@ -81,8 +83,9 @@ namespace dc {
 int32_t ensure_partials(dc_hip_ctx* ctx, size_t bytes);
 // Grows ctx->status to at least `words` and returns the epoch to use for the next launch.
 int32_t ensure_status(dc_hip_ctx* ctx, size_t words, uint32_t* epoch_out);
-// Grows ctx->spmv_rows to at least `count` entries (caller holds the lock).
+// Grow ctx->spmv_rows / ctx->spmv_windows to at least `count` entries (caller holds the lock).
 int32_t ensure_spmv_rows(dc_hip_ctx* ctx, size_t count);
+int32_t ensure_spmv_windows(dc_hip_ctx* ctx, size_t count);
 // Two-pass deterministic float64 sum of n floats into *sum_out (device), on the ctx stream.
 int32_t launch_reduce_sum_f32(dc_hip_ctx* ctx, const float* input, int64_t n, double* sum_out);
 // Fills device memory with zero bytes using a kernel (capture-safe).

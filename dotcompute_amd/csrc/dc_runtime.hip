@@ -99,6 +99,20 @@ int32_t ensure_spmv_rows(dc_hip_ctx* ctx, size_t count) {
   return DC_OK;
 }
 
+int32_t ensure_spmv_windows(dc_hip_ctx* ctx, size_t count) {
+  if (ctx->spmv_windows_cap >= count) return DC_OK;
+  size_t want = std::max<size_t>(count, 4096);
+  DC_RETURN_IF_HIP(hipStreamSynchronize(ctx->stream));
+  if (ctx->spmv_windows) DC_RETURN_IF_HIP(hipFree(ctx->spmv_windows));
+  ctx->spmv_windows = nullptr;
+  ctx->spmv_windows_cap = 0;
+  void* p = nullptr;
+  if (hipMalloc(&p, want * sizeof(int32_t)) != hipSuccess) return DC_ERR_OUT_OF_MEMORY;
+  ctx->spmv_windows = static_cast<int32_t*>(p);
+  ctx->spmv_windows_cap = want;
+  return DC_OK;
+}
+
 int32_t ensure_status(dc_hip_ctx* ctx, size_t words, uint32_t* epoch_out) {
   constexpr uint32_t kEpochMask = (1u << 22) - 1;  // 22-bit epoch field in each status word
   if (ctx->status_words < words) {
@@ -244,6 +258,7 @@ DC_HIP_API int32_t dc_hip_ctx_destroy(dc_hip_ctx* ctx) {
     if (ctx->counters) (void)hipFree(ctx->counters);
     if (ctx->scalars) (void)hipFree(ctx->scalars);
     if (ctx->spmv_rows) (void)hipFree(ctx->spmv_rows);
+    if (ctx->spmv_windows) (void)hipFree(ctx->spmv_windows);
     (void)hipStreamDestroy(ctx->stream);
   }
   delete ctx;

@@ -62,6 +62,18 @@ std::future<Matrix> MatrixOperations::MultiplyAsync(const Matrix& a, const Matri
 }
 
 namespace {
+// The kernels index values/columns/x through the row pointers: reject a malformed CSR on the host
+// (the reference would fail with IndexOutOfRangeException inside SpMV).
+void ValidateCsr(const CsrMatrix<float>& a) {
+  if (a.Rows < 0 || a.Columns < 0) throw ArgumentException("CSR dimensions must be non-negative");
+  if (a.RowPointers.empty() || a.RowPointers[0] != 0 || (int64_t)a.RowPointers.back() != a.NonZeroCount())
+    throw ArgumentException("CSR rowPointers must start at 0 and end at NNZ");
+  for (size_t r = 0; r + 1 < a.RowPointers.size(); ++r)
+    if (a.RowPointers[r + 1] < a.RowPointers[r]) throw ArgumentException("CSR rowPointers must be non-decreasing");
+  for (int32_t c : a.ColumnIndices)
+    if (c < 0 || c >= a.Columns) throw ArgumentException("CSR column index out of range");
+}
+
 struct DeviceCsr {
   std::shared_ptr<IUnifiedMemoryBufferT<int32_t>> rp, col;
   std::shared_ptr<IUnifiedMemoryBufferT<float>> val;
@@ -89,6 +101,7 @@ std::vector<float> SparseOps::SpMV(const CsrMatrix<float>& a, const std::vector<
                             std::to_string(a.Columns) + " but vector x has " + std::to_string(x.size()) +
                             " element(s). For y = A·x the number of columns in A must equal the length of x.");
   HipAccelerator& hip = RequireHip(accelerator);
+  ValidateCsr(a);
   DeviceCsr d = Upload(hip, a);
   auto dx = hip.Memory().AllocateAsync<float>(std::max<size_t>(x.size(), 1));
   auto dy = hip.Memory().AllocateAsync<float>(std::max<int32_t>(a.Rows, 1));
@@ -108,6 +121,7 @@ std::vector<float> SparseOps::PowerIterate(const CsrMatrix<float>& a, const std:
   if ((int64_t)x0.size() != (int64_t)a.Columns) throw ArgumentException("x0 length must equal the column count");
   if (iterations < 0) throw ArgumentException("iterations must be non-negative");
   HipAccelerator& hip = RequireHip(accelerator);
+  ValidateCsr(a);
   DeviceCsr d = Upload(hip, a);
   auto dx = hip.Memory().AllocateAsync<float>(std::max<size_t>(x0.size(), 1));
   auto dy = hip.Memory().AllocateAsync<float>(std::max<size_t>(x0.size(), 1));

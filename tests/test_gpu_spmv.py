@@ -126,3 +126,16 @@ def test_power_iteration_16m_invariants(ctx):
         assert abs(x20[r] - yr / s20) <= REL * abs(yr / s20) + 1e-12
     for a in (drp, dcol, dval, dx, dy, s):
         ctx.free(a)
+
+
+def test_spmv_short_rows_bit_exact_with_sequential_reference(ctx):
+    """Rows of at most 512 nonzeros are summed by one thread in index order from products rounded
+    once each, exactly as SparseOps.SpMV does: bit-identical to the sequential float32 oracle."""
+    rows = 300_000
+    rp, col, val = oracle.gen_zipf_csr(rows, 7)
+    x = oracle.gen_uniform_f32(rows, 7, 5, unit_interval=True)
+    y = spmv_gpu(ctx, rp, col, val, x)
+    ref = oracle.spmv_csr_f32(rp, col, val, x)
+    short = np.diff(rp) <= 512
+    assert short.sum() > 0.99 * rows
+    assert np.array_equal(y[short].view(np.uint32), ref[short].view(np.uint32))
