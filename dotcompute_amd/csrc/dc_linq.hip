@@ -32,7 +32,7 @@ constexpr int kElemPerThread = 4 * kVecPerThread;  // 32
 constexpr int kTile = kBlock * kElemPerThread;     // 16384 elements = 64 KiB of input
 constexpr int kChunk = 16;                         // elements interpreted per program pass
 constexpr int kLookbackPerLane = 4;                // status words read per lane per lookback round
-constexpr int kSumBlocksMax = 2048;
+constexpr int kSumBlocksMax = 1024;
 
 // ---- interpreter -------------------------------------------------------------------------------
 
@@ -50,6 +50,20 @@ __device__ inline float net_max(float a, float b) {
   return a > b ? a : b;
 }
 
+// One instruction, widened to dwords. gfx950 has no scalar byte load: reading the uint8 fields
+// of dc_linq_instr directly compiles to a vector byte load per field, and the wait for it also
+// waits for every outstanding streaming load of the thread. Two dword reads at a wave-uniform
+// address stay scalar loads.
+struct Instr {
+  uint32_t op, src, mode;
+  float imm;
+};
+__device__ inline Instr fetch_instr(const dc_linq_chain& prog, int pc) {
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(&prog.code[pc]);
+  const uint32_t w0 = w[0];
+  return Instr{w0 & 0xFFu, (w0 >> 8) & 0xFFu, (w0 >> 16) & 0xFFu, __builtin_bit_cast(float, w[1])};
+}
+
 // Runs the program over the EPT elements of one thread. Returns the keep mask (bit j = element j).
 // SAVES = false drops the s0/s1 registers for programs that never use them (the common case),
 // which keeps the kernels at a higher occupancy. Operands are read in place (an immediate stays a
@@ -65,7 +79,7 @@ __device__ inline uint32_t run_program(const dc_linq_chain& prog, float (&e)[EPT
   uint32_t p = 0, q = 0, keep = (EPT == 32) ? 0xFFFFFFFFu : ((1u << EPT) - 1u);
   const int n = prog.n_instr;
   for (int pc = 0; pc < n; ++pc) {
-    const dc_linq_instr ins = prog.code[pc];
+    const Instr ins = fetch_instr(prog, pc);
     uint32_t c = 0;
     bool is_cmp = false;
 // Applies `body` (which reads the operand as O) to every element, for the instruction's source.
@@ -234,10 +248,11 @@ __device__ inline int64_t lookback(uint64_t* __restrict__ status, int64_t tile, 
 // tiles be resident. Each stage rounds exactly as the interpreter does (x*a, then +b).
 constexpr int kMaxAffineStages = 8;
 enum AffineKind : uint8_t { kStageFilter = 0, kStageMap = 1 };
+// Fields are 32-bit so the kernel reads them with scalar loads (no scalar byte loads on gfx950).
 struct AffineChain {
   int32_t n_stages;
-  uint8_t kind[kMaxAffineStages];
-  uint8_t op[kMaxAffineStages];      // filter: DC_LQ_CMP_*; map: bit0 = has mul, bit1 = has add
+  uint32_t kind[kMaxAffineStages];
+  uint32_t op[kMaxAffineStages];     // filter: DC_LQ_CMP_*; map: bit0 = has mul, bit1 = has add
   float c0[kMaxAffineStages];        // filter: constant; map: multiplier
   float c1[kMaxAffineStages];        // map: addend
 };
@@ -289,7 +304,10 @@ inline bool lower_affine(const dc_linq_chain& prog, AffineChain* out) {
 template <int EPT>
 __device__ inline uint64_t run_affine(const AffineChain& ch, float (&e)[EPT]) {
   uint64_t keep = (EPT == 64) ? ~0ull : ((1ull << EPT) - 1);
-  for (int s = 0; s < ch.n_stages; ++s) {
+  // Unrolled over the stage slots: constant indices keep the table in scalar registers.
+#pragma unroll
+  for (int s = 0; s < kMaxAffineStages; ++s) {
+    if (s >= ch.n_stages) break;
     const float c0 = ch.c0[s], c1 = ch.c1[s];
     if (ch.kind[s] == kStageFilter) {
       uint64_t c = 0;
@@ -306,7 +324,7 @@ __device__ inline uint64_t run_affine(const AffineChain& ch, float (&e)[EPT]) {
       }
       keep &= c;
     } else {
-      const uint8_t f = ch.op[s];
+      const uint32_t f = ch.op[s];
       if (f & 1) {
 #pragma unroll
         for (int j = 0; j < EPT; ++j) e[j] = e[j] * c0;

@@ -127,7 +127,7 @@ __global__ __launch_bounds__(kFinalBlock) void reduce_partials(const Acc* __rest
 unsigned reduce_grid(int64_t n) {
   const int64_t per_block = (int64_t)kRedBlock * 4 * kRedUnroll;  // elements per block-iteration
   const int64_t g = (n + per_block - 1) / per_block;
-  return (unsigned)std::max<int64_t>(1, std::min<int64_t>(g, 2048));
+  return (unsigned)std::max<int64_t>(1, std::min<int64_t>(g, 1024));  // 2 workgroups per CU: measured best
 }
 
 }  // namespace
