@@ -51,6 +51,21 @@ def time_launches(ctx, fn, iters: int) -> float:
     return ms
 
 
+def measured_traffic(profile: str):
+    """HBM bytes per launch that rocprofv3's FETCH_SIZE / WRITE_SIZE counters measured for a kernel
+    (calibrated against a copy of known size), from the `traffic_bytes_per_launch:` line of its
+    summary under profiles/; None when there is no such summary."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", profile)
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def roofline(bound: str, achieved: float, peak: float, unit: str, traffic=None) -> dict:
     return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
             "frac": round(achieved / peak, 4), "traffic": traffic}
@@ -64,6 +79,9 @@ def main() -> int:
     ap.add_argument("--skip-extras", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only", default="", help="comma list of extras to run (sum,linq_sum,vector_add,gemm,spmv)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run one 1 GiB device-to-device copy, the known-size reference for the HBM byte "
+                         "counters (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) that give roofline.traffic")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
@@ -100,6 +118,14 @@ def main() -> int:
     log(f"[bench] where_select 256M: kept={kept} kernel={ms_kernel*1e3:.1f} us wall/step={ms_per_step*1e3:.1f} us "
         f"-> {achieved:.0f} GB/s")
     extra: dict = {}
+    if args.copy_calibration:
+        # 1 GiB read + 1 GiB written by the runtime's copy kernel: a counter reading for it, divided
+        # by 1 GiB, is the scale factor for the headline kernel's FETCH_SIZE / WRITE_SIZE readings
+        cal = ctx.empty(n, np.float32)
+        hip.check(hip.load().dc_hip_memcpy_d2d_async(ctx.handle, cal.ptr, x.ptr, 4 * n), "d2d copy")
+        ctx.synchronize()
+        ctx.free(cal)
+        log("[bench] copy calibration: 1 GiB device-to-device copy done")
 
     def want(name):
         return not args.skip_extras and (not args.only or name in args.only.split(","))
@@ -203,7 +229,8 @@ def main() -> int:
         "config": {"workload": "AsComputeQueryable().Where(x => x > 0f).Select(x => x * 2f + 1f).ToArray()",
                    "n": n, "kept": kept, "selectivity": round(kept / n, 6), "bytes_per_step": step_bytes,
                    "parallelism": "single GPU"},
-        "roofline": roofline("hbm", achieved, HBM_PEAK_GBS, "GB/s"),
+        "roofline": roofline("hbm", achieved, HBM_PEAK_GBS, "GB/s",
+                             traffic=measured_traffic("where_select_rounds_256M.md")),
         "cpu_baseline": cpu,
         "extra": extra,
     }

@@ -37,6 +37,17 @@ struct dc_hip_ctx {
   uint64_t* status = nullptr;
   size_t status_words = 0;
   uint32_t epoch = 0;
+
+  // Per-round tile counts of the round-robin compaction kernel: one 32-bit word per tile,
+  // (epoch16 << 16) | count, so a word left from an earlier launch never reads as current. Cleared
+  // once when allocated and again whenever the 16-bit epoch wraps.
+  uint32_t* round_counts = nullptr;
+  size_t round_counts_words = 0;
+  uint32_t round_epoch = 0;
+  // Whether one 1024-thread workgroup of each round-robin kernel fits on a CU: -1 not yet asked.
+  int rounds_fit = -1;
+  // Completion event of this context's last resident-grid launch (see dc::resident_launch_*).
+  hipEvent_t resident_done = nullptr;
 };
 
 struct dc_hip_event {
@@ -53,6 +64,7 @@ struct dc_hip_module {
 enum dc_counter_slot : int {
   DC_SLOT_LINQ_TICKET = 0,   // tile ticket of the compaction kernel (returned to 0 by the kernel)
   DC_SLOT_SPMV_LONG = 1,     // number of long rows found by the SpMV classification pass
+  DC_SLOT_LINQ_DONE = 2,     // finished-workgroup word of the round-robin compaction (returned to 0)
   DC_SLOT_COUNT = 1024
 };
 
@@ -83,6 +95,20 @@ namespace dc {
 int32_t ensure_partials(dc_hip_ctx* ctx, size_t bytes);
 // Grows ctx->status to at least `words` and returns the epoch to use for the next launch.
 int32_t ensure_status(dc_hip_ctx* ctx, size_t words, uint32_t* epoch_out);
+// Grows ctx->round_counts to at least `words` and returns the 16-bit epoch for the next launch.
+int32_t ensure_round_counts(dc_hip_ctx* ctx, size_t words, uint32_t* epoch_out);
+// Resident grids (kernels whose workgroups wait for each other, launched with one workgroup per CU)
+// must not share the device with another resident grid: two such grids could each hold half of
+// the CUs while waiting for workgroups that cannot start. Every resident launch of this library
+// on a device is therefore ordered after the previous one, from any context of the process:
+// resident_launch_begin makes the context stream wait for the previous resident grid of the
+// device; resident_launch_end records this launch as the new last one. The caller holds the
+// context lock. (Other processes on the same device are not covered; the kernels' waits are
+// bounded and report a failure instead of hanging.)
+int32_t resident_launch_begin(dc_hip_ctx* ctx);
+int32_t resident_launch_end(dc_hip_ctx* ctx);
+// Forgets the context's event (context destruction).
+void resident_forget(dc_hip_ctx* ctx);
 // Grow ctx->spmv_rows / ctx->spmv_windows to at least `count` entries (caller holds the lock).
 int32_t ensure_spmv_rows(dc_hip_ctx* ctx, size_t count);
 int32_t ensure_spmv_windows(dc_hip_ctx* ctx, size_t count);

@@ -6,16 +6,18 @@
 // wave-uniform: dispatch is scalar branching, and each instruction is applied to the 16 elements a
 // thread holds in registers.
 //
-// ToArray (order-preserving stream compaction, single pass):
-//   tile = 512 threads x 32 elements = 16384 consecutive elements (64 KiB), claimed through an
-//   atomic ticket (so a tile only ever waits on tiles that started before it);
-//   thread t loads 16-byte vectors j = 0..7 at tile + j*2048 + t*4 (coalesced, non-temporal);
-//   for each vector j and slot k the wave takes ballot(keep) -> the element's rank among the
-//   kept elements of (j, wave) is sum_k' mbcnt(ballot_k') + (kept slots k'' < k of this thread);
-//   the 64 (j, wave) counts are scanned in LDS -> tile-local positions; the tile aggregate is
-//   published for decoupled lookback and the tile's exclusive prefix is resolved by wave 0 from
-//   the status words of up to 256 predecessors per round; kept values go straight from registers
-//   to their output positions (each (j, wave) group fills one contiguous run).
+// ToArray (order-preserving stream compaction, one pass over the input), two kernels:
+//  - large 16-byte aligned inputs: the round-robin kernel (where_select_rounds_kernel, described
+//    at its definition): a resident grid, one workgroup per CU, tile counts published per round
+//    and summed by every workgroup, so no prefix travels from tile to tile;
+//  - everything else: a ticket-ordered grid with a decoupled lookback. tile = 512 threads x 32
+//    elements = 16384 consecutive elements (64 KiB), claimed through an atomic ticket (so a tile
+//    only ever waits on tiles that started before it); thread t loads 16-byte vectors j = 0..7 at
+//    tile + j*2048 + t*4; for each vector j and slot k the wave takes ballot(keep) -> the element's
+//    rank among the kept elements of (j, wave) is sum_k' mbcnt(ballot_k') + (kept slots k'' < k of
+//    this thread); the 64 (j, wave) counts are scanned in LDS -> tile-local positions; the tile
+//    aggregate is published for decoupled lookback and the tile's exclusive prefix is resolved by
+//    wave 0 from the status words of up to 256 predecessors per round.
 // Every float operation rounds once (the file is compiled with -ffp-contract=off), so the output
 // equals LINQ-to-objects bit-for-bit.
 #include <algorithm>
@@ -338,6 +340,98 @@ __device__ inline uint64_t run_affine(const AffineChain& ch, float (&e)[EPT]) {
   return keep;
 }
 
+enum ProgramMode : int { kModeInterp = 0, kModeInterpSaves = 1, kModeAffine = 2 };
+
+// Sets bit j of `mask` to p with one v_lshl_or_b32 (inline shift amount). Written as plain C the
+// compiler turns each bit into a select between 0 and the literal 1 << j and hoists those literals
+// into loop-invariant registers (a register per bit).
+__device__ inline uint32_t insert_bit(uint32_t mask, bool p, int j) {
+  uint32_t r;
+  asm volatile("v_lshl_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"((uint32_t)p), "i"(j), "v"(mask));
+  return r;
+}
+
+// ---- one- and two-stage affine chains in a branch-free canonical form ------------------------------
+// Used by the round-robin kernel, whose software pipeline only keeps its loads in flight across
+// rounds when the per-tile code has no branches (a branch makes the compiler's wait counts
+// conservative and it then waits for every outstanding load once per unrolled loop).
+//   filter:  y = x * sign;  keep = ((y >= c) & A) ^ ((y > c) & B) ^ C        (A, B, C in {0, 1})
+//            x > t : sign  1, c  t, A 0 B 1 C 0      x >= t: sign  1, c  t, A 1 B 0 C 0
+//            x < t : sign -1, c -t, A 0 B 1 C 0      x <= t: sign -1, c -t, A 1 B 0 C 0
+//            x == t: sign  1, c  t, A 1 B 1 C 0      x != t: sign  1, c  t, A 1 B 1 C 1
+//            (x * -1 and -t are exact, NaN compares false, and == is ge ^ gt, so every case
+//            equals the direct comparison bit for bit, signed zeros and NaN included)
+//   map:     x = x * a; x = x + b   (a missing multiply is a = 1, a missing add is b = -0: both exact)
+enum Shape2 : int { kShapeF = 0, kShapeM = 1, kShapeFM = 2, kShapeMF = 3 };
+struct Canon2 {
+  float sign, c, a, b;
+  uint32_t A, B, C;
+};
+
+inline bool lower_canon2(const AffineChain& ch, Canon2* out, int* shape) {
+  const int n = ch.n_stages;
+  if (n < 1 || n > 2 || (n == 2 && ch.kind[0] == ch.kind[1])) return false;
+  Canon2 k{1.0f, 0.0f, 1.0f, -0.0f, 0u, 0u, 1u};
+  for (int s = 0; s < n; ++s) {
+    if (ch.kind[s] == kStageFilter) {
+      const float t = ch.c0[s];
+      switch (ch.op[s]) {
+        case DC_LQ_CMP_GT: k.sign = 1.0f; k.A = 0; k.B = 1; k.C = 0; break;
+        case DC_LQ_CMP_GE: k.sign = 1.0f; k.A = 1; k.B = 0; k.C = 0; break;
+        case DC_LQ_CMP_LT: k.sign = -1.0f; k.A = 0; k.B = 1; k.C = 0; break;
+        case DC_LQ_CMP_LE: k.sign = -1.0f; k.A = 1; k.B = 0; k.C = 0; break;
+        case DC_LQ_CMP_EQ: k.sign = 1.0f; k.A = 1; k.B = 1; k.C = 0; break;
+        case DC_LQ_CMP_NE: k.sign = 1.0f; k.A = 1; k.B = 1; k.C = 1; break;
+        default: return false;
+      }
+      k.c = k.sign < 0.0f ? -t : t;
+    } else {
+      k.a = (ch.op[s] & 1u) ? ch.c0[s] : 1.0f;
+      k.b = (ch.op[s] & 2u) ? ch.c1[s] : -0.0f;
+    }
+  }
+  *shape = n == 1 ? (ch.kind[0] == kStageFilter ? kShapeF : kShapeM)
+                  : (ch.kind[0] == kStageFilter ? kShapeFM : kShapeMF);
+  *out = k;
+  return true;
+}
+
+template <int SHAPE, int EPT>
+__device__ inline uint32_t run_canon2(const Canon2& k, float (&e)[EPT]) {
+  static_assert(EPT < 32, "keep mask");
+  uint32_t keep = SHAPE == kShapeM ? ((1u << EPT) - 1u) : 0u;
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    if (SHAPE == kShapeM || SHAPE == kShapeMF) {
+      e[j] = e[j] * k.a;
+      e[j] = e[j] + k.b;
+    }
+    if (SHAPE != kShapeM) {
+      const float y = e[j] * k.sign;
+      const uint32_t ge = y >= k.c, gt = y > k.c;
+      keep = insert_bit(keep, (((ge & k.A) ^ (gt & k.B) ^ k.C) & 1u) != 0u, j);
+    }
+    if (SHAPE == kShapeFM) {
+      e[j] = e[j] * k.a;
+      e[j] = e[j] + k.b;
+    }
+  }
+  return keep;
+}
+
+// Round-robin kernel variants: the interpreter (with or without save registers) and the four
+// canonical shapes.
+enum RoundsMode : int { kRrInterp = 0, kRrInterpSaves = 1, kRrF = 2, kRrM = 3, kRrFM = 4, kRrMF = 5 };
+
+template <int MODE, int EPT>
+__device__ inline uint32_t apply_rounds(const dc_linq_chain& prog, const Canon2& k, float (&e)[EPT]) {
+  if constexpr (MODE == kRrF) return run_canon2<kShapeF, EPT>(k, e);
+  else if constexpr (MODE == kRrM) return run_canon2<kShapeM, EPT>(k, e);
+  else if constexpr (MODE == kRrFM) return run_canon2<kShapeFM, EPT>(k, e);
+  else if constexpr (MODE == kRrMF) return run_canon2<kShapeMF, EPT>(k, e);
+  else return run_program<EPT, MODE == kRrInterpSaves>(prog, e);
+}
+
 // ---- Where/Select -> ToArray ------------------------------------------------------------------
 // One tile per workgroup, claimed by ticket. Element order inside a tile is (vector j, wave, lane,
 // slot k): thread t loads 16-byte vectors j = 0..7 at tile + 2048 j + 4 t. After the lookback each
@@ -350,7 +444,6 @@ __device__ inline uint32_t take_ticket(uint32_t* __restrict__ ticket, uint32_t t
   return t;
 }
 
-enum ProgramMode : int { kModeInterp = 0, kModeInterpSaves = 1, kModeAffine = 2 };
 
 template <int MODE>
 __device__ inline uint64_t apply_program(const dc_linq_chain& prog, const AffineChain& aff,
@@ -370,6 +463,13 @@ __device__ inline uint64_t apply_program(const dc_linq_chain& prog, const Affine
     }
     return keep;
   }
+}
+
+// Program over EPT <= 32 elements of one lane; bit j of the result = element j is kept.
+template <int MODE, int EPT>
+__device__ inline uint32_t apply_small(const dc_linq_chain& prog, const AffineChain& aff, float (&e)[EPT]) {
+  if constexpr (MODE == kModeAffine) return (uint32_t)run_affine<EPT>(aff, e);
+  else return run_program<EPT, MODE == kModeInterpSaves>(prog, e);
 }
 
 template <int MODE>
@@ -480,17 +580,252 @@ __global__ __launch_bounds__(kBlock) void where_select_kernel(const dc_linq_chai
   if (tid == 0 && tile == num_tiles - 1) *count_out = s_exclusive + (int64_t)aggregate;
 }
 
+// ---- Where/Select -> ToArray, round-robin kernel for large inputs --------------------------------
+// A resident grid of P workgroups (one per CU, all running at once). Workgroup w owns tile r*P + w of
+// round r, so every round is a contiguous stretch of P tiles. Each tile publishes its kept count as
+// one epoch-tagged word; the output offset of tile (r, w) is
+//     base_r + sum_{w' < w} count(r, w'),   base_{r+1} = base_r + sum_{w'} count(r, w'),
+// and every workgroup reads all P counts of a round itself, so no prefix ever has to travel from tile
+// to tile (the serial front that limits a decoupled lookback). The loop is software-pipelined:
+//   - loads run kRrAhead rounds ahead (kRrAhead + 1 register buffers per lane);
+//   - kept values of a tile wait in LDS for kRrDelay rounds before they are written, and the count
+//     words of that round are read one round before the write, so they were published
+//     kRrDelay - 2 full rounds earlier and are almost always already visible.
+// Roles inside the 1024-thread workgroup: wave 0 reads and checks the count words and broadcasts the
+// output offset; waves 1..15 each own a contiguous 512-element chunk of every tile, rank their kept
+// elements with ballot + mbcnt, stage them in a private LDS ring (in input order) and later write
+// them as one contiguous run. The last wave to finish a tile (an LDS atomic) publishes its count.
+// One workgroup barrier per round.
+constexpr int kRrBlock = 1024;
+constexpr int kRrWorkers = kRrBlock / dc::kWave - 1;     // 15 worker waves
+constexpr int kRrVec = 2;                                // 16-byte loads per lane per tile
+constexpr int kRrEpt = 4 * kRrVec;                       // 8 elements per lane
+constexpr int kRrChunk = dc::kWave * kRrEpt;             // 512 elements per worker wave
+constexpr int64_t kRrTile = (int64_t)kRrWorkers * kRrChunk;  // 7680 elements = 30 KiB
+constexpr int kRrAhead = 4;
+constexpr int kRrDelay = 3;
+constexpr int kRrRing = 2048;                            // floats per worker wave (power of two)
+constexpr int kRrCountsPerLane = 4;
+constexpr int kRrMaxGroups = dc::kWave * kRrCountsPerLane;  // P <= 256
+constexpr uint32_t kRrSpinLimit = 1u << 22;              // ~seconds: a wait that never ends reports
+constexpr int kRrMinRounds = 4;                          // below this the ticket kernel is used
+static_assert((kRrDelay + 1) * kRrChunk <= kRrRing, "the ring holds every staged tile at 100% selectivity");
+static_assert(kRrDelay < 8 && kRrDelay >= 2, "per-tile LDS tables are indexed modulo 8");
+
+// Count words of `round` for workgroups q*64 + lane (q < 4): four coalesced 256-byte loads.
+__device__ inline void rr_issue_counts(uint32_t (&c)[kRrCountsPerLane], const uint32_t* __restrict__ counts,
+                                       uint32_t round, uint32_t P) {
+  const uint32_t lane = threadIdx.x & 63;
+#pragma unroll
+  for (int q = 0; q < kRrCountsPerLane; ++q) {
+    const uint32_t g = q * 64 + lane;
+    c[q] = g < P ? dc::load_agent_u32(counts + (size_t)round * P + g) : 0u;
+  }
+}
+
+// Wave 0: re-reads until every count word of `round` carries this launch's epoch (bounded), then
+// returns the sum of the counts of workgroups before `me` and the round total.
+__device__ inline bool rr_resolve(uint32_t (&c)[kRrCountsPerLane], const uint32_t* __restrict__ counts, uint32_t round,
+                                  uint32_t P, uint32_t epoch16, uint32_t me, uint32_t* pref, uint32_t* total) {
+  const uint32_t lane = threadIdx.x & 63;
+  for (uint32_t spin = 0;; ++spin) {
+    bool missing = false;
+#pragma unroll
+    for (int q = 0; q < kRrCountsPerLane; ++q) missing |= (q * 64 + lane < P) && ((c[q] >> 16) != epoch16);
+    if (!__ballot(missing)) break;
+    if (spin == kRrSpinLimit) return false;
+    __builtin_amdgcn_s_sleep(4);
+    rr_issue_counts(c, counts, round, P);
+  }
+  uint32_t p = 0, t = 0;
+#pragma unroll
+  for (int q = 0; q < kRrCountsPerLane; ++q) {
+    const uint32_t g = q * 64 + lane;
+    const uint32_t v = g < P ? (c[q] & 0xFFFFu) : 0u;
+    t += v;
+    p += g < me ? v : 0u;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    t += __shfl_xor(t, off, 64);
+    p += __shfl_xor(p, off, 64);
+  }
+  *pref = p;
+  *total = t;
+  return true;
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
+    const dc_linq_chain prog, const Canon2 canon, const float* __restrict__ in, int64_t n, float* __restrict__ out,
+    int64_t* __restrict__ count_out, uint32_t* __restrict__ counts, uint32_t epoch16, uint32_t P,
+    uint32_t* __restrict__ done) {
+  constexpr uint32_t kMask = kRrRing - 1;
+  __shared__ float s_ring[kRrWorkers][kRrRing];
+  __shared__ uint32_t s_wcount[8][16];  // kept count of (tile slot, worker wave)
+  __shared__ uint32_t s_acc[8];         // (waves finished << 24) | kept so far, per tile slot
+  __shared__ int64_t s_off[2];          // output offset of the tile being written, by round parity
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t w = blockIdx.x;
+  const int64_t num_tiles = (n + kRrTile - 1) / kRrTile;
+  const uint32_t R0 = (uint32_t)((n / kRrTile) / P);  // rounds in which every tile is full
+  const uint32_t rounds = R0 > 0 ? R0 + kRrDelay : 0;
+  const bool tail_round = (int64_t)R0 * P < num_tiles;
+  if (tid < 8) s_acc[tid] = 0;
+  __syncthreads();
+
+  if (wave == 0) {
+    // ---------------- control wave
+    int64_t base = 0;
+    uint32_t c[kRrCountsPerLane];
+    bool ok = true;
+    for (uint32_t r = 0; r < rounds; ++r) {
+      if (r >= (uint32_t)kRrDelay) {
+        uint32_t pf = 0, tt = 0;
+        if (ok && !rr_resolve(c, counts, r - kRrDelay, P, epoch16, w, &pf, &tt)) ok = false;
+        if (lane == 0) s_off[r & 1] = base + pf;
+        base += tt;
+      }
+      if (r + 1 >= (uint32_t)kRrDelay && r + 1 - kRrDelay < R0) rr_issue_counts(c, counts, r + 1 - kRrDelay, P);
+      if (lane == 0) s_acc[(r + 1) & 7] = 0;
+      __syncthreads();
+    }
+    if (tail_round) {
+      __syncthreads();  // the workers published the tail round's counts
+      uint32_t pf = 0, tt = 0;
+      rr_issue_counts(c, counts, R0, P);
+      if (ok && !rr_resolve(c, counts, R0, P, epoch16, w, &pf, &tt)) ok = false;
+      if (lane == 0) s_off[0] = base + pf;
+      base += tt;
+      __syncthreads();
+    }
+    if (lane == 0) {
+      // Completion word: low 16 bits count finished workgroups, the rest counts failed ones. The last
+      // workgroup writes the total (every workgroup holds the same base) or -1 if any wait gave up.
+      const uint32_t add = 1u | (ok ? 0u : (1u << 16));
+      const uint32_t prev = __hip_atomic_fetch_add(done, add, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+      if ((prev & 0xFFFFu) == P - 1) {
+        *count_out = ((prev >> 16) == 0 && ok) ? base : (int64_t)-1;
+        dc::store_agent_u32(done, 0u);
+      }
+    }
+    return;
+  }
+
+  // ---------------- worker waves
+  const int ww = wave - 1;
+  float* ring = s_ring[ww];
+  uint32_t head = 0, tail = 0;
+  const int64_t chunk = (int64_t)ww * kRrChunk;
+
+  auto load = [&](float (&e)[kRrEpt], uint32_t round) {
+    const dc::f32x4* in4 = reinterpret_cast<const dc::f32x4*>(in + ((int64_t)round * P + w) * kRrTile + chunk);
+#pragma unroll
+    for (int j = 0; j < kRrVec; ++j) {
+      const dc::f32x4 x = dc::load_stream(in4 + j * dc::kWave + lane);
+      e[4 * j] = x.x; e[4 * j + 1] = x.y; e[4 * j + 2] = x.z; e[4 * j + 3] = x.w;
+    }
+  };
+  // Ranks the kept elements of this wave's chunk (order: vector j, lane, slot k), appends them to the
+  // ring, and publishes the tile count when this is the last worker wave to finish the tile.
+  auto stage = [&](float (&e)[kRrEpt], uint32_t keep, uint32_t r) {
+    uint32_t run = 0, pos[kRrVec];
+#pragma unroll
+    for (int j = 0; j < kRrVec; ++j) {
+      uint32_t below = 0, total = 0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint64_t b = __ballot((keep >> (4 * j + k)) & 1u);
+        below += __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+        total += (uint32_t)__builtin_popcountll(b);
+      }
+      pos[j] = run + below;
+      run += total;
+    }
+#pragma unroll
+    for (int j = 0; j < kRrVec; ++j) {
+      uint32_t p = head + pos[j];
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if ((keep >> (4 * j + k)) & 1u) ring[(p++) & kMask] = e[4 * j + k];
+    }
+    head += run;
+    if (lane == 0) {
+      s_wcount[r & 7][ww] = run;
+      const uint32_t prev = atomicAdd(&s_acc[r & 7], (1u << 24) | run);
+      if ((prev >> 24) == kRrWorkers - 1)
+        dc::store_agent_u32(counts + (size_t)r * P + w, (epoch16 << 16) | ((prev & 0xFFFFFFu) + run));
+    }
+  };
+  // Writes this wave's staged run of the tile of round q at its place in the output.
+  auto write = [&](uint32_t q, uint32_t parity) {
+    const uint32_t slot = q & 7;
+    uint32_t cnt = 0, before = 0;
+#pragma unroll
+    for (int i = 0; i < kRrWorkers; ++i) {
+      const uint32_t c = s_wcount[slot][i];
+      before += i < ww ? c : 0u;
+      cnt = i == ww ? c : cnt;
+    }
+    float* dst = out + s_off[parity] + before;
+    for (uint32_t i = lane; i < cnt; i += dc::kWave) dst[i] = ring[(tail + i) & kMask];
+    tail += cnt;
+  };
+
+  float e0[kRrEpt], e1[kRrEpt], e2[kRrEpt], e3[kRrEpt], e4[kRrEpt];
+  if (R0 > 0) load(e0, 0);
+  if (R0 > 1) load(e1, 1);
+  if (R0 > 2) load(e2, 2);
+  if (R0 > 3) load(e3, 3);
+  uint32_t r = 0;
+  // One round: issue the loads of round r + kRrAhead into EN, stage round r from EC, write round
+  // r - kRrDelay. Unrolled five ways so the register buffers rotate without copies.
+#define DC_RR_ROUND(EC, EN)                                                              \
+  {                                                                                      \
+    if (r + kRrAhead < R0) load(EN, r + kRrAhead);                                       \
+    stage(EC, apply_rounds<MODE, kRrEpt>(prog, canon, EC), r);                              \
+    __syncthreads();                                                                     \
+    if (r >= (uint32_t)kRrDelay) write(r - kRrDelay, r & 1);                             \
+    if (++r >= R0) break;                                                                \
+  }
+  static_assert(kRrAhead == 4, "five register buffers");
+  while (r < R0) {
+    DC_RR_ROUND(e0, e4);
+    DC_RR_ROUND(e1, e0);
+    DC_RR_ROUND(e2, e1);
+    DC_RR_ROUND(e3, e2);
+    DC_RR_ROUND(e4, e3);
+  }
+#undef DC_RR_ROUND
+  for (; r < rounds; ++r) {  // drain: the last kRrDelay staged tiles
+    __syncthreads();
+    write(r - kRrDelay, r & 1);
+  }
+  if (tail_round) {  // tiles R0*P .. num_tiles-1 (full, partial or none), bounded loads
+    const int64_t t = (int64_t)R0 * P + w;
+    float e[kRrEpt];
+    uint32_t valid = 0;
+#pragma unroll
+    for (int j = 0; j < kRrVec; ++j) {
+      const int64_t at = t * kRrTile + chunk + j * 4 * dc::kWave + 4 * lane;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) e[4 * j + k] = (t < num_tiles && at + k < n) ? in[at + k] : 0.0f;
+      const int64_t nv = t < num_tiles ? min(max(n - at, (int64_t)0), (int64_t)4) : 0;
+      valid |= ((1u << (uint32_t)nv) - 1u) << (4 * j);
+    }
+    stage(e, apply_rounds<MODE, kRrEpt>(prog, canon, e) & valid, R0);
+    __syncthreads();
+    __syncthreads();
+    write(R0, 0);
+  }
+}
+
 // ---- Where/Select -> Sum / Count ----------------------------------------------------------------
 // Pass 1: each block runs the program over one contiguous chunk (a thread takes 4 vectors, 16
 // elements, per step) and writes its float64 sum and kept count; pass 2 sums the partials in block
 // order (fixed tree, deterministic).
 constexpr int kSumBlock = 512;
 
-template <int MODE, int EPT>
-__device__ inline uint32_t apply_small(const dc_linq_chain& prog, const AffineChain& aff, float (&e)[EPT]) {
-  if constexpr (MODE == kModeAffine) return (uint32_t)run_affine<EPT>(aff, e);
-  else return run_program<EPT, MODE == kModeInterpSaves>(prog, e);
-}
 
 template <int MODE>
 __global__ __launch_bounds__(kSumBlock) void where_select_sum_pass1(const dc_linq_chain prog, const AffineChain aff,
@@ -569,6 +904,50 @@ __global__ __launch_bounds__(kFinalBlock) void where_select_sum_pass2(const doub
   }
 }
 
+// ---- strategy choice -----------------------------------------------------------------------------
+const void* rounds_kernel(int mode) {
+  switch (mode) {
+    case kRrF: return reinterpret_cast<const void*>(&where_select_rounds_kernel<kRrF>);
+    case kRrM: return reinterpret_cast<const void*>(&where_select_rounds_kernel<kRrM>);
+    case kRrFM: return reinterpret_cast<const void*>(&where_select_rounds_kernel<kRrFM>);
+    case kRrMF: return reinterpret_cast<const void*>(&where_select_rounds_kernel<kRrMF>);
+    case kRrInterpSaves: return reinterpret_cast<const void*>(&where_select_rounds_kernel<kRrInterpSaves>);
+    default: return reinterpret_cast<const void*>(&where_select_rounds_kernel<kRrInterp>);
+  }
+}
+
+// Picks the round-robin variant for a program and fills its canonical constants.
+int rounds_mode(const dc_linq_chain& prog, Canon2* canon) {
+  AffineChain aff{};
+  int shape = 0;
+  if (lower_affine(prog, &aff) && lower_canon2(aff, canon, &shape)) {
+    return shape == kShapeF ? kRrF : shape == kShapeM ? kRrM : shape == kShapeFM ? kRrFM : kRrMF;
+  }
+  *canon = Canon2{1.0f, 0.0f, 1.0f, -0.0f, 0u, 0u, 1u};
+  return program_uses_saves(prog) ? kRrInterpSaves : kRrInterp;
+}
+
+uint32_t rounds_groups(const dc_hip_ctx* ctx) { return (uint32_t)std::min(ctx->cu_count, kRrMaxGroups); }
+
+// The round-robin kernel needs a 16-byte aligned input of at least kRrMinRounds full rounds and
+// room for one 1024-thread workgroup per CU (every program variant; asked once per context). The
+// caller holds the context lock.
+bool use_rounds(dc_hip_ctx* ctx, const float* input, int64_t n) {
+  const uint32_t groups = rounds_groups(ctx);
+  if (!dc::aligned16(input) || groups == 0 || n / kRrTile < (int64_t)kRrMinRounds * groups) return false;
+  if (ctx->rounds_fit < 0) {
+    bool fit = true;
+    for (int mode : {kRrInterp, kRrInterpSaves, kRrF, kRrM, kRrFM, kRrMF}) {
+      int per_cu = 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, rounds_kernel(mode), kRrBlock, 0) != hipSuccess ||
+          per_cu < 1)
+        fit = false;
+    }
+    ctx->rounds_fit = fit ? 1 : 0;
+  }
+  return ctx->rounds_fit == 1;
+}
+
 }  // namespace
 
 extern "C" {
@@ -585,21 +964,55 @@ DC_HIP_API int32_t dc_linq_chain_validate(const dc_linq_chain* chain) {
   return DC_OK;
 }
 
+DC_HIP_API int32_t dc_hip_linq_to_array_strategy(dc_hip_ctx* ctx, const float* input, int64_t n,
+                                                 int32_t* strategy_out) {
+  if (!ctx || !strategy_out || n < 0) return DC_ERR_INVALID_ARGUMENT;
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  *strategy_out = use_rounds(ctx, input, n) ? DC_LINQ_STRATEGY_ROUNDS : DC_LINQ_STRATEGY_LOOKBACK;
+  return DC_OK;
+}
+
 DC_HIP_API int32_t dc_hip_linq_where_select_f32(dc_hip_ctx* ctx, const dc_linq_chain* chain, const float* input,
                                                 int64_t n, float* output, int64_t* count_out) {
   if (n < 0 || !count_out || (n > 0 && (!input || !output))) return DC_ERR_INVALID_ARGUMENT;
   DC_RETURN_IF(dc_linq_chain_validate(chain));
   if (n >= (int64_t)1 << 40) return DC_ERR_INVALID_ARGUMENT;  // 40-bit counts in the status words
   DC_CTX_ENTER(ctx);
+  if (use_rounds(ctx, input, n)) {
+    Canon2 canon{};
+    const void* fn = rounds_kernel(rounds_mode(*chain, &canon));
+    const uint32_t groups = rounds_groups(ctx);
+    const int64_t tiles = (n + kRrTile - 1) / kRrTile;
+    const size_t words = (size_t)((tiles + groups - 1) / groups + 1) * groups;
+    uint32_t epoch16 = 0;
+    DC_RETURN_IF(dc::ensure_round_counts(ctx, words, &epoch16));
+    dc_linq_chain prog = *chain;
+    const float* in_arg = input;
+    int64_t n_arg = n;
+    float* out_arg = output;
+    int64_t* count_arg = count_out;
+    uint32_t* counts_arg = ctx->round_counts;
+    uint32_t groups_arg = groups;
+    uint32_t* done_arg = ctx->counters + DC_SLOT_LINQ_DONE;
+    void* args[] = {&prog, &canon, &in_arg, &n_arg, &out_arg, &count_arg, &counts_arg, &epoch16, &groups_arg, &done_arg};
+    // One workgroup per CU, each needing most of a CU's LDS, on an otherwise idle device: every
+    // workgroup is resident at once (an ordinary launch; measured faster than a cooperative one).
+    DC_RETURN_IF(dc::resident_launch_begin(ctx));
+    DC_RETURN_IF_HIP(hipLaunchKernel(fn, dim3(groups), dim3(kRrBlock), args, 0, ctx->stream));
+    DC_RETURN_IF(dc::last_launch_status());
+    return dc::resident_launch_end(ctx);
+  }
+
+  AffineChain aff{};
+  const bool affine = lower_affine(*chain, &aff);
+  const int mode = affine ? kModeAffine : (program_uses_saves(*chain) ? kModeInterpSaves : kModeInterp);
   const int64_t tiles = std::max<int64_t>(1, (n + kTile - 1) / kTile);
   if (tiles > 0x7FFFFFFFll) return DC_ERR_INVALID_ARGUMENT;
   uint32_t epoch = 0;
   DC_RETURN_IF(dc::ensure_status(ctx, (size_t)tiles, &epoch));
-  AffineChain aff{};
-  const bool affine = lower_affine(*chain, &aff);
-  auto kernel = affine ? where_select_kernel<kModeAffine>
-                       : (program_uses_saves(*chain) ? where_select_kernel<kModeInterpSaves>
-                                                     : where_select_kernel<kModeInterp>);
+  auto kernel = mode == kModeAffine ? where_select_kernel<kModeAffine>
+              : mode == kModeInterpSaves ? where_select_kernel<kModeInterpSaves>
+                                         : where_select_kernel<kModeInterp>;
   kernel<<<(unsigned)tiles, kBlock, 0, ctx->stream>>>(*chain, aff, input, n, output, count_out, ctx->status,
                                                       ctx->counters + DC_SLOT_LINQ_TICKET, epoch, (uint32_t)tiles,
                                                       dc::aligned16(input) ? 1 : 0);

@@ -137,6 +137,63 @@ int32_t ensure_status(dc_hip_ctx* ctx, size_t words, uint32_t* epoch_out) {
   return DC_OK;
 }
 
+int32_t ensure_round_counts(dc_hip_ctx* ctx, size_t words, uint32_t* epoch_out) {
+  if (ctx->round_counts_words < words) {
+    size_t want = std::max<size_t>(words, 16384);
+    DC_RETURN_IF_HIP(hipStreamSynchronize(ctx->stream));
+    if (ctx->round_counts) DC_RETURN_IF_HIP(hipFree(ctx->round_counts));
+    ctx->round_counts = nullptr;
+    ctx->round_counts_words = 0;
+    void* p = nullptr;
+    if (hipMalloc(&p, want * sizeof(uint32_t)) != hipSuccess) return DC_ERR_OUT_OF_MEMORY;
+    ctx->round_counts = static_cast<uint32_t*>(p);
+    ctx->round_counts_words = want;
+    DC_RETURN_IF(zero_async(ctx, ctx->round_counts, want * sizeof(uint32_t)));
+    ctx->round_epoch = 0;
+  }
+  ctx->round_epoch = (ctx->round_epoch + 1) & 0xFFFFu;
+  if (ctx->round_epoch == 0) {  // wrapped: clear so no stale word can match the next epochs
+    DC_RETURN_IF(zero_async(ctx, ctx->round_counts, ctx->round_counts_words * sizeof(uint32_t)));
+    ctx->round_epoch = 1;
+  }
+  *epoch_out = ctx->round_epoch;
+  return DC_OK;
+}
+
+namespace {
+struct ResidentSlot {
+  std::mutex mu;
+  dc_hip_ctx* last_ctx = nullptr;  // context whose resident_done event marks the last resident grid
+};
+ResidentSlot g_resident[64];
+}  // namespace
+
+int32_t resident_launch_begin(dc_hip_ctx* ctx) {
+  if (ctx->device < 0 || ctx->device >= 64) return DC_ERR_UNSUPPORTED;
+  if (!ctx->resident_done) DC_RETURN_IF_HIP(hipEventCreateWithFlags(&ctx->resident_done, hipEventDisableTiming));
+  ResidentSlot& slot = g_resident[ctx->device];
+  std::lock_guard<std::mutex> lock(slot.mu);
+  if (slot.last_ctx && slot.last_ctx != ctx) DC_RETURN_IF_HIP(hipStreamWaitEvent(ctx->stream, slot.last_ctx->resident_done, 0));
+  return DC_OK;
+}
+
+int32_t resident_launch_end(dc_hip_ctx* ctx) {
+  ResidentSlot& slot = g_resident[ctx->device];
+  std::lock_guard<std::mutex> lock(slot.mu);
+  DC_RETURN_IF_HIP(hipEventRecord(ctx->resident_done, ctx->stream));
+  slot.last_ctx = ctx;
+  return DC_OK;
+}
+
+void resident_forget(dc_hip_ctx* ctx) {
+  if (ctx->device < 0 || ctx->device >= 64) return;
+  ResidentSlot& slot = g_resident[ctx->device];
+  std::lock_guard<std::mutex> lock(slot.mu);
+  if (slot.last_ctx == ctx) slot.last_ctx = nullptr;
+  if (ctx->resident_done) (void)hipEventDestroy(ctx->resident_done);
+  ctx->resident_done = nullptr;
+}
+
 }  // namespace dc
 
 extern "C" {
@@ -255,6 +312,8 @@ DC_HIP_API int32_t dc_hip_ctx_destroy(dc_hip_ctx* ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->partials) (void)hipFree(ctx->partials);
     if (ctx->status) (void)hipFree(ctx->status);
+    if (ctx->round_counts) (void)hipFree(ctx->round_counts);
+    dc::resident_forget(ctx);
     if (ctx->counters) (void)hipFree(ctx->counters);
     if (ctx->scalars) (void)hipFree(ctx->scalars);
     if (ctx->spmv_rows) (void)hipFree(ctx->spmv_rows);

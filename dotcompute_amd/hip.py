@@ -27,6 +27,10 @@ DC_ERR_DIMENSION = -6
 DC_ERR_OUT_OF_MEMORY = -7
 DC_ERR_NOT_FOUND = -8
 
+# dc_linq_strategy: which kernel dc_hip_linq_where_select_f32 runs for an input
+STRATEGY_LOOKBACK = 0
+STRATEGY_ROUNDS = 1
+
 DC_LINQ_MAX_INSTR = 48
 
 # dc_linq_op
@@ -138,6 +142,7 @@ SIGNATURES: dict[str, list] = {
     "dc_linq_chain_validate": [C.POINTER(LinqChain)],
     "dc_hip_linq_where_select_f32": [_P, C.POINTER(LinqChain), _P, _i64, _P, _P],
     "dc_hip_linq_where_select_sum_f32": [_P, C.POINTER(LinqChain), _P, _i64, _P, _P],
+    "dc_hip_linq_to_array_strategy": [_P, _P, _i64, _P],
     "dc_hip_gemm_f32": [_P, _P, _P, _P, _i64, _i64, _i64],
     "dc_hip_gemm_bf16": [_P, _P, _P, _P, _i64, _i64, _i64],
     "dc_hip_convert_f32_to_bf16": [_P, _P, _P, _i64],
@@ -328,6 +333,14 @@ class Context:
         n = x.size if n is None else n
         check(load().dc_hip_linq_where_select_f32(self.handle, C.byref(chain), x.ptr, n, out.ptr, count.ptr),
               "dc_hip_linq_where_select_f32")
+
+    def to_array_strategy(self, x: DeviceArray, n: int | None = None) -> int:
+        """Kernel that where_select_f32 uses for this input: STRATEGY_LOOKBACK or STRATEGY_ROUNDS."""
+        n = x.size if n is None else n
+        out = C.c_int32(-1)
+        check(load().dc_hip_linq_to_array_strategy(self.handle, x.ptr, n, C.byref(out)),
+              "dc_hip_linq_to_array_strategy")
+        return out.value
 
     def where_select_sum_f32(self, chain: LinqChain, x: DeviceArray, sum_out: DeviceArray | None,
                              count: DeviceArray | None, n: int | None = None) -> None:

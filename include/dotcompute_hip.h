@@ -275,10 +275,19 @@ typedef struct dc_linq_chain {
 DC_HIP_API int32_t dc_linq_chain_validate(const dc_linq_chain* chain);
 
 /* Where/Select → ToArray: writes the kept, mapped elements in input order to `output` (capacity n)
- * and their number to *count_out (device int64). Single pass, decoupled lookback. */
+ * and their number to *count_out (device int64). One pass over the input. Large 16-byte aligned
+ * inputs run on a resident grid (one workgroup per CU, per-round tile counts); the others on a
+ * ticket-ordered grid with a decoupled lookback (dc_hip_linq_to_array_strategy tells which).
+ * *count_out is -1 if the resident grid's bounded wait for a tile count ever gave up (the device
+ * did not run every workgroup of the grid at once); the output is then undefined. */
 DC_HIP_API int32_t dc_hip_linq_where_select_f32(dc_hip_ctx* ctx, const dc_linq_chain* chain,
                                                 const float* input, int64_t n, float* output,
                                                 int64_t* count_out);
+/* The kernel dc_hip_linq_where_select_f32 would use for this input (no device work). Diagnostic:
+ * no counterpart in the reference, whose filter kernel has one shape (CudaKernelGenerator.cs:351-376). */
+enum dc_linq_strategy { DC_LINQ_STRATEGY_LOOKBACK = 0, DC_LINQ_STRATEGY_ROUNDS = 1 };
+DC_HIP_API int32_t dc_hip_linq_to_array_strategy(dc_hip_ctx* ctx, const float* input, int64_t n,
+                                                 int32_t* strategy_out);
 /* Where/Select → Sum (and Count): float64-accumulated sum of the kept, mapped elements to
  * *sum_out and their number to *count_out (either may be NULL). Deterministic. */
 DC_HIP_API int32_t dc_hip_linq_where_select_sum_f32(dc_hip_ctx* ctx, const dc_linq_chain* chain,

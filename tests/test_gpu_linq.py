@@ -248,3 +248,135 @@ def test_affine_fast_path_matches_interpreter(ctx, idx):
     _, sd, rc = oracle.linq_where_select_sum(prog, x)
     assert c == rc
     assert abs(s - sd) <= 1e-5 * math.log2(x.size) * max(abs(sd), 1.0)
+
+
+# ---- the round-robin kernel (large, 16-byte aligned inputs) ------------------------------------
+# Tiles of 15 worker waves x 64 lanes x 8 elements; used from 4 full rounds of min(CUs, 256) tiles.
+RR_TILE = 15 * 64 * 8
+
+
+def rr_min_n():
+    return 4 * min(hip.device_info(0).compute_units, 256) * RR_TILE
+
+
+def run_to_array_checked(ctx, chain, x, strategy, offset=0):
+    """run_to_array, asserting which kernel the library picks for this input."""
+    n = x.size
+    dx = ctx.empty(n + offset + 1, np.float32)
+    hip.check(hip.load().dc_hip_memcpy_h2d_async(ctx.handle, dx.ptr + 4 * offset, x.ctypes.data, x.nbytes), "h2d")
+    src = hip.DeviceArray(ctx, dx.ptr + 4 * offset, 4 * n, np.dtype(np.float32), (n,))
+    assert ctx.to_array_strategy(src, n) == strategy
+    out = ctx.empty(n + 1, np.float32)
+    cnt = ctx.empty(1, np.int64)
+    ctx.where_select_f32(chain, src, out, cnt, n)
+    ctx.synchronize()
+    k = int(cnt.to_host()[0])
+    assert k >= 0, "resident grid reported a wait that gave up"
+    got = out.to_host(k) if k else np.empty(0, np.float32)
+    for a in (dx, out, cnt):
+        ctx.free(a)
+    return got
+
+
+@pytest.mark.parametrize("extra", [0, 1, 4097, RR_TILE * 3 + 5, 256 * RR_TILE - 1, 256 * RR_TILE * 2 + 12345])
+def test_round_robin_sizes_bit_exact(ctx, extra):
+    n = rr_min_n() + extra
+    x = oracle.gen_uniform_f32(n, 500 + extra % 97, 0)
+    got = run_to_array_checked(ctx, CHAIN, x, hip.STRATEGY_ROUNDS)
+    ref = oracle.where_gt0_select_2x_plus_1(x)
+    assert got.size == ref.size
+    assert np.array_equal(bits(got), bits(ref))
+
+
+def test_round_robin_threshold_and_alignment(ctx):
+    n = rr_min_n()
+    x = oracle.gen_uniform_f32(n + 3, 61, 0)
+    # one element short of four rounds, and a misaligned start: the lookback kernel, same result
+    got = run_to_array_checked(ctx, CHAIN, x[: n - 1], hip.STRATEGY_LOOKBACK)
+    assert np.array_equal(bits(got), bits(oracle.where_gt0_select_2x_plus_1(x[: n - 1])))
+    got = run_to_array_checked(ctx, CHAIN, x, hip.STRATEGY_LOOKBACK, offset=1)
+    assert np.array_equal(bits(got), bits(oracle.where_gt0_select_2x_plus_1(x)))
+
+
+@pytest.mark.parametrize("cmp,imm", [(CMP_GT, -2.0), (CMP_GT, 2.0), (CMP_LT, -0.999)])
+def test_round_robin_all_none_and_sparse(ctx, cmp, imm):
+    # every element kept (the staging ring at 100% selectivity), none kept, and ~0.05% kept
+    prog = LinqChain.assemble([(LOAD, SRC_ELEM, 0), (cmp, SRC_IMM, imm), (FILTER, SRC_IMM, 0),
+                               (LOAD, SRC_ELEM, 0), (MUL, SRC_IMM, 3.0), (MAP, SRC_IMM, 0)])
+    x = oracle.gen_uniform_f32(rr_min_n() + 999, 71, 0)
+    got = run_to_array_checked(ctx, prog, x, hip.STRATEGY_ROUNDS)
+    assert same_floats(got, oracle.linq_where_select(prog, x))
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_round_robin_random_programs(ctx, seed):
+    # interpreter variants (with and without save registers) on the resident grid
+    rng = np.random.default_rng(1000 + seed)
+    prog = _random_program(rng)
+    x = oracle.gen_uniform_f32(rr_min_n() + 777 * seed, 300 + seed, 0)
+    got = run_to_array_checked(ctx, prog, x, hip.STRATEGY_ROUNDS)
+    assert same_floats(got, oracle.linq_where_select(prog, x))
+
+
+def _salted_input(n, seed):
+    """Uniform input with signed zeros, infinities, NaN, denormals and exact thresholds mixed in."""
+    x = oracle.gen_uniform_f32(n, seed, 0).copy()
+    rng = np.random.default_rng(seed)
+    specials = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-45, -1e-45, 1.17e-38, 0.25, -0.25, 0.5],
+                        dtype=np.float32)
+    idx = rng.choice(n, size=n // 50, replace=False)
+    x[idx] = specials[rng.integers(0, specials.size, size=idx.size)]
+    return x
+
+
+SHAPE_PROGRAMS = {
+    "F": lambda cmp, t: [(LOAD, SRC_ELEM, 0), (cmp, SRC_IMM, t), (FILTER, SRC_IMM, 0)],
+    "M": lambda cmp, t: [(LOAD, SRC_ELEM, 0), (MUL, SRC_IMM, -3.0), (ADD, SRC_IMM, 0.5), (MAP, SRC_IMM, 0)],
+    "FM": lambda cmp, t: [(LOAD, SRC_ELEM, 0), (cmp, SRC_IMM, t), (FILTER, SRC_IMM, 0),
+                          (LOAD, SRC_ELEM, 0), (MUL, SRC_IMM, 2.0), (ADD, SRC_IMM, 1.0), (MAP, SRC_IMM, 0)],
+    "MF": lambda cmp, t: [(LOAD, SRC_ELEM, 0), (ADD, SRC_IMM, -0.25), (MAP, SRC_IMM, 0),
+                          (LOAD, SRC_ELEM, 0), (cmp, SRC_IMM, t), (FILTER, SRC_IMM, 0)],
+    "Fmul": lambda cmp, t: [(LOAD, SRC_ELEM, 0), (cmp, SRC_IMM, t), (FILTER, SRC_IMM, 0),
+                            (LOAD, SRC_ELEM, 0), (MUL, SRC_IMM, 0.1), (MAP, SRC_IMM, 0)],
+}
+
+
+@pytest.mark.parametrize("shape", sorted(SHAPE_PROGRAMS))
+@pytest.mark.parametrize("cmp", [CMP_GT, CMP_GE, CMP_LT, CMP_LE, CMP_EQ, CMP_NE])
+def test_round_robin_canonical_shapes_special_values(ctx, shape, cmp):
+    # one- and two-stage affine chains take a branch-free form of the comparison on the resident
+    # grid; it must equal the direct comparison for every input, including -0, +-inf, NaN and
+    # denormals, and for thresholds 0 (signed zeros) and values present in the input
+    for t in (0.0, 0.25):
+        if shape == "M" and t != 0.0:
+            continue
+        prog = LinqChain.assemble(SHAPE_PROGRAMS[shape](cmp, t))
+        x = _salted_input(rr_min_n() + 1234, 900 + cmp)
+        got = run_to_array_checked(ctx, prog, x, hip.STRATEGY_ROUNDS)
+        assert same_floats(got, oracle.linq_where_select(prog, x)), (shape, cmp, t)
+
+
+def test_round_robin_two_contexts_interleaved(ctx):
+    # two contexts on one device each queue resident grids without host synchronisation between
+    # them; the library orders resident grids device-wide, so both finish with exact results
+    n = rr_min_n() + 333
+    xs = [oracle.gen_uniform_f32(n, 610 + i, 0) for i in range(2)]
+    ctxs = [ctx, hip.Context(0)]
+    bufs = []
+    for c, x in zip(ctxs, xs):
+        dx = c.to_device(x)
+        assert c.to_array_strategy(dx, n) == hip.STRATEGY_ROUNDS
+        bufs.append((dx, c.empty(n, np.float32), c.empty(1, np.int64)))
+    for _ in range(3):
+        for c, (dx, out, cnt) in zip(ctxs, bufs):
+            c.where_select_f32(CHAIN, dx, out, cnt, n)
+    for c in ctxs:
+        c.synchronize()
+    for c, x, (dx, out, cnt) in zip(ctxs, xs, bufs):
+        k = int(cnt.to_host()[0])
+        ref = oracle.where_gt0_select_2x_plus_1(x)
+        assert k == ref.size
+        assert np.array_equal(bits(out.to_host(k)), bits(ref))
+        for a in (dx, out, cnt):
+            c.free(a)
+    ctxs[1].close()
