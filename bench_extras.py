@@ -70,13 +70,31 @@ def bench_spmv(ctx, log, time_launches, roofline, hbm_peak, sizes=(1_000_000, 16
         ms1 = time_launches(ctx, single, 10)
         spmv_bytes = 8 * nnz + 4 * (rows + 1) + 4 * rows + 4 * rows
         gbs1 = spmv_bytes / (ms1 * 1e-3) / 1e9
+        # the column-sliced plan: analysis once, then SpMV through it
+        t_build = ctx.event(), ctx.event()
+        t_build[0].record()
+        plan = ctx.spmv_plan(drp, dcol, dval, rows, rows, nnz)
+        t_build[1].record()
+        t_build[1].synchronize()
+        ms_build = t_build[0].elapsed_ms(t_build[1])
+        for e in t_build:
+            e.destroy()
+        slices, slice_cols, plan_bytes = plan.info()
+        plan.execute(x, y)
+        ctx.synchronize()
+        ms_plan = time_launches(ctx, lambda: plan.execute(x, y), 20)
+        gbs_plan = spmv_bytes / (ms_plan * 1e-3) / 1e9
+        plan.destroy()
         out[f"spmv_power20_{rows // 1_000_000}M"] = {
             "ms": round(ms, 4), "nnz": nnz, "mean_degree": round(nnz / rows, 3), "GB/s": round(gbs, 1),
             "iter_ms": round(ms / iters, 4),
             "roofline": roofline("hbm", gbs, hbm_peak, "GB/s"),
-            "single_spmv_ms": round(ms1, 4), "single_spmv_GB/s": round(gbs1, 1)}
+            "single_spmv_ms": round(ms1, 4), "single_spmv_GB/s": round(gbs1, 1),
+            "plan_build_ms": round(ms_build, 4), "plan_slices": slices, "plan_slice_cols": slice_cols,
+            "plan_device_bytes": plan_bytes, "plan_spmv_ms": round(ms_plan, 4), "plan_spmv_GB/s": round(gbs_plan, 1)}
         log(f"[bench] spmv x{iters} rows={rows} nnz={nnz}: {ms:.3f} ms ({ms / iters * 1e3:.1f} us/iter) -> {gbs:.0f} GB/s;"
-            f" single SpMV {ms1 * 1e3:.1f} us -> {gbs1:.0f} GB/s")
+            f" single SpMV {ms1 * 1e3:.1f} us -> {gbs1:.0f} GB/s; plan build {ms_build * 1e3:.0f} us ({slices} slices),"
+            f" plan SpMV {ms_plan * 1e3:.1f} us -> {gbs_plan:.0f} GB/s")
         for a in (drp, dcol, dval, x0, x, y):
             ctx.free(a)
     return out

@@ -30,6 +30,9 @@ struct dc_hip_ctx {
   int32_t* spmv_windows = nullptr;  // first row of each nonzero window
   size_t spmv_windows_cap = 0;
   double* scalars = nullptr;  // 64 doubles
+  // Device memory of the column-sliced SpMV plan built by dc_hip_spmv_power_iterate_f32 (grows).
+  void* spmv_plan_mem = nullptr;
+  size_t spmv_plan_bytes = 0;
 
   // Decoupled-lookback status words, one uint64 per tile (grows on demand). A word is valid only
   // when its epoch field equals the launch's epoch, so the array never needs clearing between
@@ -112,8 +115,11 @@ void resident_forget(dc_hip_ctx* ctx);
 // Grow ctx->spmv_rows / ctx->spmv_windows to at least `count` entries (caller holds the lock).
 int32_t ensure_spmv_rows(dc_hip_ctx* ctx, size_t count);
 int32_t ensure_spmv_windows(dc_hip_ctx* ctx, size_t count);
+int32_t ensure_spmv_plan_mem(dc_hip_ctx* ctx, size_t bytes);
 // Two-pass deterministic float64 sum of n floats into *sum_out (device), on the ctx stream.
 int32_t launch_reduce_sum_f32(dc_hip_ctx* ctx, const float* input, int64_t n, double* sum_out);
+// *sum_out = partials[0] + ... + partials[count-1] (float64, fixed order; one workgroup).
+int32_t launch_reduce_partials_f64(dc_hip_ctx* ctx, const double* partials, int count, double* sum_out);
 // Fills device memory with zero bytes using a kernel (capture-safe).
 int32_t zero_async(dc_hip_ctx* ctx, void* dst, size_t bytes);
 inline int32_t last_launch_status() { return (int32_t)hipGetLastError(); }

@@ -113,6 +113,19 @@ int32_t ensure_spmv_windows(dc_hip_ctx* ctx, size_t count) {
   return DC_OK;
 }
 
+int32_t ensure_spmv_plan_mem(dc_hip_ctx* ctx, size_t bytes) {
+  if (ctx->spmv_plan_bytes >= bytes) return DC_OK;
+  DC_RETURN_IF_HIP(hipStreamSynchronize(ctx->stream));
+  if (ctx->spmv_plan_mem) DC_RETURN_IF_HIP(hipFree(ctx->spmv_plan_mem));
+  ctx->spmv_plan_mem = nullptr;
+  ctx->spmv_plan_bytes = 0;
+  void* p = nullptr;
+  if (hipMalloc(&p, bytes) != hipSuccess) return DC_ERR_OUT_OF_MEMORY;
+  ctx->spmv_plan_mem = p;
+  ctx->spmv_plan_bytes = bytes;
+  return DC_OK;
+}
+
 int32_t ensure_status(dc_hip_ctx* ctx, size_t words, uint32_t* epoch_out) {
   constexpr uint32_t kEpochMask = (1u << 22) - 1;  // 22-bit epoch field in each status word
   if (ctx->status_words < words) {
@@ -318,6 +331,7 @@ DC_HIP_API int32_t dc_hip_ctx_destroy(dc_hip_ctx* ctx) {
     if (ctx->scalars) (void)hipFree(ctx->scalars);
     if (ctx->spmv_rows) (void)hipFree(ctx->spmv_rows);
     if (ctx->spmv_windows) (void)hipFree(ctx->spmv_windows);
+    if (ctx->spmv_plan_mem) (void)hipFree(ctx->spmv_plan_mem);
     (void)hipStreamDestroy(ctx->stream);
   }
   delete ctx;

@@ -112,7 +112,15 @@ __global__ __launch_bounds__(kFinalBlock) void reduce_partials(const Acc* __rest
                                                                Acc* __restrict__ out, int32_t* __restrict__ overflow) {
   __shared__ Acc lds[kFinalBlock / dc::kWave];
   Acc acc = 0;
-  for (int i = threadIdx.x; i < count; i += kFinalBlock) acc += partials[i];
+  // Thread t adds partials t, t + 1024, t + 2048, ... in that order; eight loads go out together.
+  for (int i0 = threadIdx.x; i0 < count; i0 += 8 * kFinalBlock) {
+    Acc v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = i0 + k * kFinalBlock < count ? partials[i0 + k * kFinalBlock] : Acc(0);
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (i0 + k * kFinalBlock < count) acc += v[k];
+  }
   Acc total = dc::block_sum64<kFinalBlock>(acc, lds);
   if (threadIdx.x == 0) {
     *out = total;
@@ -140,6 +148,11 @@ int32_t launch_reduce_sum_f32(dc_hip_ctx* ctx, const float* input, int64_t n, do
   double* partials = static_cast<double*>(ctx->partials);
   reduce_sum_f32_pass1<<<grid, kRedBlock, 0, ctx->stream>>>(input, n, dc::aligned16(input) ? 1 : 0, partials);
   reduce_partials<double><<<1, kFinalBlock, 0, ctx->stream>>>(partials, (int)grid, sum_out, nullptr);
+  return dc::last_launch_status();
+}
+
+int32_t launch_reduce_partials_f64(dc_hip_ctx* ctx, const double* partials, int count, double* sum_out) {
+  reduce_partials<double><<<1, kFinalBlock, 0, ctx->stream>>>(partials, count, sum_out, nullptr);
   return dc::last_launch_status();
 }
 

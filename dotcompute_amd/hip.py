@@ -148,6 +148,11 @@ SIGNATURES: dict[str, list] = {
     "dc_hip_convert_f32_to_bf16": [_P, _P, _P, _i64],
     "dc_hip_spmv_csr_f32": [_P, _P, _P, _P, _P, _P, _i64, _i64, _i64],
     "dc_hip_spmv_power_iterate_f32": [_P, _P, _P, _P, _P, _P, _i64, _i64, _i32, _P],
+    "dc_hip_spmv_plan_create": [_P, _P, _P, _P, _i64, _i64, _i64, _i64, _PP],
+    "dc_hip_spmv_plan_execute_f32": [_P, _P, _P, _P],
+    "dc_hip_spmv_plan_power_iterate_f32": [_P, _P, _P, _P, _i32, _P],
+    "dc_hip_spmv_plan_info": [_P, C.POINTER(_i32), C.POINTER(_i64), C.POINTER(_i64)],
+    "dc_hip_spmv_plan_destroy": [_P],
 }
 _RESTYPES = {"dc_hip_error_string": C.c_char_p, "dc_hip_default_module_path": C.c_char_p}
 
@@ -370,6 +375,45 @@ class Context:
         check(load().dc_hip_spmv_power_iterate_f32(self.handle, rp.ptr, col.ptr, val.ptr, x.ptr, y.ptr, rows, nnz,
                                                   iterations, last_sum.ptr if last_sum else None),
               "dc_hip_spmv_power_iterate_f32")
+
+    def spmv_plan(self, rp: DeviceArray, col: DeviceArray, val: DeviceArray, rows: int, cols: int, nnz: int,
+                  slice_cols_max: int = 0) -> "SpmvPlan":
+        h = C.c_void_p()
+        check(load().dc_hip_spmv_plan_create(self.handle, rp.ptr, col.ptr, val.ptr, rows, cols, nnz, slice_cols_max,
+                                             C.byref(h)), "dc_hip_spmv_plan_create")
+        return SpmvPlan(self, h.value, rows, cols)
+
+
+class SpmvPlan:
+    """Column-sliced SpMV plan (dc_hip_spmv_plan_*): built once, executed many times."""
+
+    def __init__(self, ctx: "Context", handle, rows: int, cols: int):
+        self.ctx, self.handle, self.rows, self.cols = ctx, handle, rows, cols
+
+    def info(self) -> tuple[int, int, int]:
+        s, w, b = C.c_int32(), C.c_int64(), C.c_int64()
+        check(load().dc_hip_spmv_plan_info(self.handle, C.byref(s), C.byref(w), C.byref(b)), "dc_hip_spmv_plan_info")
+        return s.value, w.value, b.value
+
+    def execute(self, x: DeviceArray, y: DeviceArray) -> None:
+        check(load().dc_hip_spmv_plan_execute_f32(self.ctx.handle, self.handle, x.ptr, y.ptr),
+              "dc_hip_spmv_plan_execute_f32")
+
+    def power_iterate(self, x: DeviceArray, y: DeviceArray, iterations: int, last_sum: DeviceArray | None = None) -> None:
+        check(load().dc_hip_spmv_plan_power_iterate_f32(self.ctx.handle, self.handle, x.ptr, y.ptr, iterations,
+                                                        last_sum.ptr if last_sum else None),
+              "dc_hip_spmv_plan_power_iterate_f32")
+
+    def destroy(self) -> None:
+        if self.handle:
+            check(load().dc_hip_spmv_plan_destroy(self.handle), "dc_hip_spmv_plan_destroy")
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.destroy()
 
 
 def gen_zipf_csr(rows: int, seed: int, alpha: float = 2.0, max_degree: int = 4096, cols: int | None = None):

@@ -326,11 +326,41 @@ DC_HIP_API int32_t dc_hip_spmv_csr_f32(dc_hip_ctx* ctx, const int32_t* row_point
  *   y = A·x;  s = Σ y (float64);  x = y / s
  * leaving the normalised vector in x (rows == cols required). `y` is caller-provided scratch of
  * rows floats. The final L1 norm before the last normalisation is written to *last_sum_out
- * (device double, may be NULL). */
+ * (device double, may be NULL). Builds a column-sliced plan (below) in context scratch first and
+ * runs every iteration through it. */
 DC_HIP_API int32_t dc_hip_spmv_power_iterate_f32(dc_hip_ctx* ctx, const int32_t* row_pointers,
                                                  const int32_t* col_indices, const float* values,
                                                  float* x, float* y, int64_t rows, int64_t nnz,
                                                  int32_t iterations, double* last_sum_out);
+
+/* Column-sliced SpMV plan: an analysis of a CSR matrix, built once on the device, for matrices
+ * that are multiplied many times (CsrMatrix<T> reused across SparseOps.SpMV calls,
+ * src/Extensions/DotCompute.Algorithms/Sparse/SparseMatrix.cs:669-692; the power iteration).
+ * The plan holds its own slice-major copy of the nonzeros (device memory owned by the plan), so
+ * the CSR arrays may be freed once the creating call's stream work has run. Columns are cut into
+ * slices of at most `slice_cols_max` columns (0 = the default, 1M columns = 4 MB of x, one XCD's
+ * L2) and each XCD gathers from its own slices. Result: y[r] = 0.0f + (partial of slice 0) +
+ * (partial of slice 1) + ..., each partial summed in index order, so with one slice (cols <=
+ * slice width) rows of at most 256 nonzeros equal the sequential row sum bit for bit; otherwise
+ * the row sum is reassociated by slice (within the fp32 tolerance). Column indices outside
+ * [0, cols) are clamped into range on the device (they never fault); callers validate first. */
+typedef struct dc_hip_spmv_plan dc_hip_spmv_plan;
+DC_HIP_API int32_t dc_hip_spmv_plan_create(dc_hip_ctx* ctx, const int32_t* row_pointers,
+                                           const int32_t* col_indices, const float* values,
+                                           int64_t rows, int64_t cols, int64_t nnz,
+                                           int64_t slice_cols_max, dc_hip_spmv_plan** plan_out);
+/* y = A·x through the plan (asynchronous on the context stream). */
+DC_HIP_API int32_t dc_hip_spmv_plan_execute_f32(dc_hip_ctx* ctx, const dc_hip_spmv_plan* plan,
+                                                const float* x, float* y);
+/* The power iteration above, through an existing plan (rows == cols). */
+DC_HIP_API int32_t dc_hip_spmv_plan_power_iterate_f32(dc_hip_ctx* ctx, const dc_hip_spmv_plan* plan,
+                                                      float* x, float* y, int32_t iterations,
+                                                      double* last_sum_out);
+/* Number of column slices, columns per slice, device bytes held. Any pointer may be NULL. */
+DC_HIP_API int32_t dc_hip_spmv_plan_info(const dc_hip_spmv_plan* plan, int32_t* slices,
+                                         int64_t* slice_cols, int64_t* device_bytes);
+/* Waits for the device, then frees the plan. */
+DC_HIP_API int32_t dc_hip_spmv_plan_destroy(dc_hip_spmv_plan* plan);
 
 #ifdef __cplusplus
 }
