@@ -236,12 +236,10 @@ constexpr int kMaxSlices = 32;
 constexpr int64_t kSliceCols = 1 << 20;   // columns per slice: 4 MB of x, one XCD's L2
 constexpr int kWW = 512;                  // nonzeros per wave window
 constexpr int kLongSeg = 256;             // longer segments go to the long-segment pass
+constexpr int kSeqSeg = 32;               // longer segments are summed by the whole wave
 constexpr int kSpan = kWW + kLongSeg;     // products a window can hold (its segments end before this)
 constexpr int kXcds = 8;
 constexpr int kGatherBlock = 256;         // 4 waves, each with its own windows
-constexpr int kGatherPerCu = 8;           // resident gather workgroups per CU (LDS: 4 x kSpan floats each)
-constexpr int kSlots = kSpan / 64;        // column/value loads per lane: the whole span, no remainder
-constexpr int kSegGroups = kWW / 64;      // segment starts per lane: a window holds at most kWW segments
 constexpr int kXcdWords = 8;              // per (phase, XCD): nranges, total, (start, count, stride)
 constexpr int kMaxPhases = kMaxSlices / 8;
 constexpr int kScanBlock = 1024;
@@ -301,8 +299,9 @@ __device__ inline int wave_row_of(int32_t start, int32_t i) {
 // Counts the wave's rows into cnt[row][slice] (LDS adds without return). kChunks chunks of column
 // loads go out together, so a wave waits one memory round trip per kChunks * 64 nonzeros.
 constexpr int kChunks = 4;
+template <int SMAX>
 __device__ inline void wave_count(const int32_t* __restrict__ col, const WaveRows& w, uint32_t cols, uint32_t width,
-                                  int32_t (*cnt)[kMaxSlices + 1]) {
+                                  int32_t (*cnt)[SMAX + 1]) {
   const int lane = threadIdx.x & 63;
   for (int32_t base = w.nz0; base < w.nz1; base += 64 * kChunks) {
     int32_t c[kChunks];
@@ -317,16 +316,30 @@ __device__ inline void wave_count(const int32_t* __restrict__ col, const WaveRow
   }
 }
 
-// P1: per (slice, block of kRB rows), the number of nonzeros and of segments.
+// Row blocks are handed to workgroups XCD by XCD: workgroup w (on XCD w % 8) takes block
+// (w % 8) * per + w / 8, so each XCD works through one contiguous range of rows and the
+// slice-major lines it writes are not shared with another XCD's L2. -1: no block for w.
+__device__ inline int32_t xcd_block(int32_t nblocks) {
+  const int32_t per = (nblocks + kXcds - 1) / kXcds;
+  const int32_t b = (int32_t)(blockIdx.x % kXcds) * per + (int32_t)(blockIdx.x / kXcds);
+  return b < nblocks ? b : -1;
+}
+
+// P1: per (slice, block of kRB rows), the number of nonzeros and of segments. SMAX >= S sizes the
+// LDS table.
+template <int SMAX>
 __global__ __launch_bounds__(kRB) void plan_count(const int32_t* __restrict__ rp, const int32_t* __restrict__ col,
                                                   int64_t rows, int32_t nnz, int32_t S, uint32_t width, uint32_t cols,
-                                                  int32_t* __restrict__ tn, int32_t* __restrict__ ts, int32_t ld) {
-  __shared__ int32_t cnt[kRB][kMaxSlices + 1];
+                                                  int32_t* __restrict__ tn, int32_t* __restrict__ ts, int32_t ld,
+                                                  int32_t nblocks) {
+  __shared__ int32_t cnt[kRB][SMAX + 1];
+  const int32_t blk = xcd_block(nblocks);
+  if (blk < 0) return;  // whole workgroup
   const int t = threadIdx.x, wave = t >> 6;
   for (int s = 0; s < S; ++s) cnt[t][s] = 0;
   __syncthreads();
-  const int64_t rw0 = (int64_t)blockIdx.x * kRB + wave * 64;
-  if (rw0 < rows) wave_count(col, wave_rows(rp, rw0, rows, nnz), cols, width, cnt + wave * 64);
+  const int64_t rw0 = (int64_t)blk * kRB + wave * 64;
+  if (rw0 < rows) wave_count<SMAX>(col, wave_rows(rp, rw0, rows, nnz), cols, width, cnt + wave * 64);
   __syncthreads();
   // Column sums over the block's rows: thread t -> slice t / 8, rows (t % 8) * 32 .. + 31.
   const int s = t >> 3, part = t & 7;
@@ -344,8 +357,8 @@ __global__ __launch_bounds__(kRB) void plan_count(const int32_t* __restrict__ rp
     g += __shfl_xor(g, off, 64);
   }
   if (s < S && part == 0) {
-    tn[(int64_t)s * ld + blockIdx.x] = n;
-    ts[(int64_t)s * ld + blockIdx.x] = g;
+    tn[(int64_t)s * ld + blk] = n;
+    ts[(int64_t)s * ld + blk] = g;
   }
 }
 
@@ -446,6 +459,7 @@ __global__ void plan_bases(const int32_t* __restrict__ tot, int32_t S, int32_t* 
 // P4: stable scatter of every row's nonzeros into the slice-major copy, plus per (row, slice)
 // segment its first nonzero (seg_ptr) and its row within the block (seg_row). The per-row counts
 // are recomputed exactly as plan_count computes them, so both passes agree.
+template <int SMAX>
 __global__ __launch_bounds__(kRB) void plan_scatter(const int32_t* __restrict__ rp, const int32_t* __restrict__ col,
                                                     const float* __restrict__ val, int64_t rows, int32_t nnz, int32_t S,
                                                     uint32_t width, uint32_t cols, const int32_t* __restrict__ tn,
@@ -454,18 +468,20 @@ __global__ __launch_bounds__(kRB) void plan_scatter(const int32_t* __restrict__ 
                                                     int32_t* __restrict__ col_s, float* __restrict__ val_s,
                                                     int32_t* __restrict__ seg_ptr, uint8_t* __restrict__ seg_row,
                                                     int32_t* __restrict__ long_list, uint32_t* __restrict__ long_cnt,
-                                                    int32_t long_cap) {
-  __shared__ int32_t cnt[kRB][kMaxSlices + 1];
-  __shared__ int32_t wn[kRB / 64][kMaxSlices], wg[kRB / 64][kMaxSlices];
+                                                    int32_t long_cap, int32_t nblocks) {
+  __shared__ int32_t cnt[kRB][SMAX + 1];
+  __shared__ int32_t wn[kRB / 64][SMAX], wg[kRB / 64][SMAX];
+  const int32_t blk = xcd_block(nblocks);
+  if (blk < 0) return;  // whole workgroup
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   for (int s = 0; s < S; ++s) cnt[t][s] = 0;
   __syncthreads();
-  const int64_t rw0 = (int64_t)blockIdx.x * kRB + wave * 64;
+  const int64_t rw0 = (int64_t)blk * kRB + wave * 64;
   const bool active = rw0 < rows;  // wave-uniform
   WaveRows w{0, 0, 0};
   if (active) {
     w = wave_rows(rp, rw0, rows, nnz);
-    wave_count(col, w, cols, width, cnt + wave * 64);
+    wave_count<SMAX>(col, w, cols, width, cnt + wave * 64);
   }
   __syncthreads();
   for (int s = 0; s < S; ++s) {
@@ -486,7 +502,7 @@ __global__ __launch_bounds__(kRB) void plan_scatter(const int32_t* __restrict__ 
       pg += wg[v][s];
     }
     if (c > 0) {
-      const int64_t k = (int64_t)s * ld + blockIdx.x;
+      const int64_t k = (int64_t)s * ld + blk;
       const int32_t p = nb[s] + tn[k] + pn + excl;
       const int32_t g = sb[s] + ts[k] + pg + (int32_t)lane_rank(bal);
       seg_ptr[g] = p;
@@ -504,7 +520,7 @@ __global__ __launch_bounds__(kRB) void plan_scatter(const int32_t* __restrict__ 
   if (!active) return;
   // Stream the wave's nonzeros again. Within a chunk, the lanes of one (row, slice) pair keep their
   // index order: rank = lanes below this one with the same slice, from the row's first lane on.
-  int32_t (*cur)[kMaxSlices + 1] = cnt + wave * 64;
+  int32_t (*cur)[SMAX + 1] = cnt + wave * 64;
   for (int32_t base0 = w.nz0; base0 < w.nz1; base0 += 64 * kChunks) {
     uint32_t cc[kChunks];
     float vv[kChunks];
@@ -595,33 +611,38 @@ __device__ inline float lds_seq_sum(const float* __restrict__ p, int32_t i0, int
 }
 
 // Buffer resource over [p, p + bytes): loads past the end return 0 and stores past it are dropped
-// by the hardware range check, so a window's loads and stores need no branches (and their number
-// is the same in every window, which keeps the compiler's memory-counter waits exact).
+// by the hardware range check, so a window's loads and stores need no branches.
 __device__ inline __amdgpu_buffer_rsrc_t range_rsrc(const void* p, int32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
 }
 constexpr int kNt = 2;                   // cache policy: non-temporal (streamed once)
 constexpr uint32_t kDrop = 0x80000000u;  // a buffer offset past any range: the access is dropped
+constexpr int kChunksW = kSpan / 256;    // 16-byte loads per lane covering a window's span
+constexpr int kSegChunks = (kWW + 1 + 255) / 256;  // ... and its segment starts plus the end
 
+// A window's loads, 16 bytes per lane: lane l holds elements 256 k + 4 l .. + 3 of chunk k.
 struct WindowLoads {
-  int32_t sp[kSegGroups + 1];  // seg_ptr[g0 + lane + 64 q]
-  int32_t c[kSlots];           // col_s[b + lane + 64 q] (0 past e)
-  float v[kSlots];             // val_s[b + lane + 64 q] (0 past e)
+  dc::i32x4 sp[kSegChunks];  // seg_ptr[g0 + ...]
+  dc::i32x4 c[kChunksW];     // col_s[b + ...]
+  dc::f32x4 v[kChunksW];     // val_s[b + ...]
 };
 
+// Ranges are rounded up to whole 16-byte groups (the arrays carry 16 bytes of slack), so a load is
+// either wholly inside or wholly past the range; elements past e (or past g1) are ignored.
 __device__ inline void window_issue(const int4 d, const int32_t* __restrict__ seg_ptr,
                                     const int32_t* __restrict__ col_s, const float* __restrict__ val_s,
                                     WindowLoads& w) {
-  const uint32_t lane4 = (threadIdx.x & 63) * 4;
-  const auto rs = range_rsrc(seg_ptr + d.x, (d.y - d.x + 1) * 4);
-  const auto rc = range_rsrc(col_s + d.z, (d.w - d.z) * 4);
-  const auto rv = range_rsrc(val_s + d.z, (d.w - d.z) * 4);
+  const uint32_t lane16 = (threadIdx.x & 63) * 16;
+  const auto rs = range_rsrc(seg_ptr + d.x, ((d.y - d.x + 1 + 3) & ~3) * 4);
+  const auto rc = range_rsrc(col_s + d.z, ((d.w - d.z + 3) & ~3) * 4);
+  const auto rv = range_rsrc(val_s + d.z, ((d.w - d.z + 3) & ~3) * 4);
 #pragma unroll
-  for (int q = 0; q <= kSegGroups; ++q) w.sp[q] = __builtin_amdgcn_raw_buffer_load_b32(rs, lane4 + 256 * q, 0, kNt);
+  for (int k = 0; k < kSegChunks; ++k)
+    w.sp[k] = __builtin_bit_cast(dc::i32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, lane16 + 1024 * k, 0, kNt));
 #pragma unroll
-  for (int q = 0; q < kSlots; ++q) {
-    w.c[q] = __builtin_amdgcn_raw_buffer_load_b32(rc, lane4 + 256 * q, 0, kNt);
-    w.v[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rv, lane4 + 256 * q, 0, kNt));
+  for (int k = 0; k < kChunksW; ++k) {
+    w.c[k] = __builtin_bit_cast(dc::i32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, lane16 + 1024 * k, 0, kNt));
+    w.v[k] = __builtin_bit_cast(dc::f32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, lane16 + 1024 * k, 0, kNt));
   }
 }
 
@@ -630,18 +651,36 @@ __device__ inline int4 uniform_int4(int4 d) {
                    __builtin_amdgcn_readfirstlane(d.z), __builtin_amdgcn_readfirstlane(d.w));
 }
 
-// Gather pass: persistent grid, XCD-affine; each wave walks its XCD's windows, software-pipelined:
-// the gathers of window n, then every load of window n + 1, then window n's products, segment sums
-// and stores. One lane per segment adds its products in index order (seg_ptr[g + 1], the segment's
-// end, is the next lane's start, taken with a shuffle).
+// Float sum over the wave's 64 lanes in a fixed DPP tree order (result broadcast from lane 63).
+__device__ inline float wave_sum_f32(float v) {
+  auto step = [](float a, uint32_t b) { return a + __builtin_bit_cast(float, b); };
+  v = step(v, dc::dpp_u32<0xB1, 0xF>(__builtin_bit_cast(uint32_t, v)));   // lanes xor 1
+  v = step(v, dc::dpp_u32<0x4E, 0xF>(__builtin_bit_cast(uint32_t, v)));   // lanes xor 2
+  v = step(v, dc::dpp_u32<0x141, 0xF>(__builtin_bit_cast(uint32_t, v)));  // half-row mirror
+  v = step(v, dc::dpp_u32<0x140, 0xF>(__builtin_bit_cast(uint32_t, v)));  // row mirror
+  v = step(v, dc::dpp_u32<0x142, 0xA>(__builtin_bit_cast(uint32_t, v)));  // row_bcast:15
+  v = step(v, dc::dpp_u32<0x143, 0xC>(__builtin_bit_cast(uint32_t, v)));  // row_bcast:31
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+__device__ inline int32_t elem(const dc::i32x4& v, int j) { return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w; }
+
+
+// Gather pass: persistent grid, XCD-affine; each wave walks its XCD's windows. Per window: one
+// round trip for the 16-byte column/value/segment-start loads, one for the gathers (only the
+// chunks that hold products), products to the wave's LDS (one 16-byte write per chunk), then the
+// segment sums. The address unit is the limit here, so the number of memory instructions per
+// window is what this layout minimises. Segment sums: up to kSeqSeg products, one lane adds them
+// in index order; longer segments (up to kLongSeg) are summed by the whole wave: lane k adds
+// products k, k + 64, ... in order, then a fixed DPP tree. Lane l owns segments 256 k + 4 l + j.
 __global__ __launch_bounds__(kGatherBlock) void spmv_slice_windows(const int4* __restrict__ desc,
                                                                    const int32_t* __restrict__ seg_ptr,
                                                                    const int32_t* __restrict__ col_s,
                                                                    const float* __restrict__ val_s,
                                                                    const float* __restrict__ x,
                                                                    float* __restrict__ partial,
-                                                                   const int32_t* __restrict__ xcd) {
-  __shared__ float prod[kGatherBlock / 64][kSpan];
+                                                                   const int32_t* __restrict__ xcd, int32_t cols) {
+  __shared__ dc::f32x4 prod[kGatherBlock / 64][kSpan / 4];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = blockIdx.x & (kXcds - 1);
@@ -650,9 +689,11 @@ __global__ __launch_bounds__(kGatherBlock) void spmv_slice_windows(const int4* _
   const int32_t* xr = xcd + j * kXcdWords;
   const int32_t nr = xr[0], total = xr[1];
   if (v >= total) return;
-  float* wp = prod[wave];
+  dc::f32x4* wp4 = prod[wave];
+  const float* wp = reinterpret_cast<const float*>(prod[wave]);
+  const auto rx = range_rsrc(x, (int32_t)((uint32_t)cols * 4u));  // x < 4 GB (checked at plan creation)
   auto window_desc = [&](int32_t l) {
-    if (l >= total) return make_int4(0, 0, 0, 0);  // no window: empty ranges, every access dropped
+    if (l >= total) return make_int4(0, 0, 0, 0);
     int32_t rem = l, k = 0;
     for (int q = 0; q < nr; ++q) {
       const int32_t cnt = xr[3 + 3 * q];
@@ -665,41 +706,84 @@ __global__ __launch_bounds__(kGatherBlock) void spmv_slice_windows(const int4* _
     return uniform_int4(desc[k]);
   };
   int4 d = window_desc(v);
-  WindowLoads cur;
-  window_issue(d, seg_ptr, col_s, val_s, cur);
-  int4 dn = window_desc(v + per_xcd_waves);
   for (int32_t l = v; l < total; l += per_xcd_waves) {
     const int32_t g0 = d.x, g1 = d.y, b = d.z, e = d.w;
-    float xv[kSlots];
+    WindowLoads w;
+    window_issue(d, seg_ptr, col_s, val_s, w);
+    const int4 dn = window_desc(l + per_xcd_waves);
+    const int32_t span = e - b;
+    // gathers: only chunks that hold products (a wave-uniform skip); x[0] for elements past e
+    dc::f32x4 xv[kChunksW];
 #pragma unroll
-    for (int q = 0; q < kSlots; ++q) xv[q] = x[cur.c[q]];  // c = 0 past e: gathered, then dropped
-    WindowLoads nxt;
-    window_issue(dn, seg_ptr, col_s, val_s, nxt);
-    const int4 dnn = window_desc(l + 2 * per_xcd_waves);
+    for (int k = 0; k < kChunksW; ++k) {
+      xv[k] = dc::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      if (256 * k < span) {
 #pragma unroll
-    for (int q = 0; q < kSlots; ++q)
-      if (lane + 64 * q < e - b) wp[lane + 64 * q] = cur.v[q] * xv[q];
-    wave_lds_sync();
-    float psum[kSegGroups];
-    uint32_t off[kSegGroups];
-#pragma unroll
-    for (int q = 0; q < kSegGroups; ++q) {
-      const int32_t rb = cur.sp[q];
-      const int32_t nxt0 = __shfl(cur.sp[q + 1], 0, 64);
-      const int32_t re0 = __shfl_down(rb, 1, 64);
-      const int32_t re = lane == 63 ? nxt0 : re0;
-      const bool ok = lane + 64 * q < g1 - g0 && re - rb <= kLongSeg;
-      psum[q] = ok ? lds_seq_sum(wp, rb - b, min(re, e) - b) : 0.0f;
-      off[q] = ok ? (uint32_t)(lane + 64 * q) * 4u : kDrop;
+        for (int q = 0; q < 4; ++q) {
+          const float g = __builtin_bit_cast(
+              float, __builtin_amdgcn_raw_buffer_load_b32(rx, (uint32_t)elem(w.c[k], q) * 4u, 0, 0));
+          if (q == 0) xv[k].x = g; else if (q == 1) xv[k].y = g; else if (q == 2) xv[k].z = g; else xv[k].w = g;
+        }
+      }
     }
-    const auto rp = range_rsrc(partial + g0, (g1 - g0) * 4);
 #pragma unroll
-    for (int q = 0; q < kSegGroups; ++q)
-      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int32_t, psum[q]), rp, off[q], 0, kNt);
+    for (int k = 0; k < kChunksW; ++k)
+      if (256 * k + 4 * lane < span) wp4[64 * k + lane] = w.v[k] * xv[k];  // products past e are never read
+    wave_lds_sync();
+    // segment sums: lane l, chunk k, element q -> segment s = 256 k + 4 l + q
+    constexpr int kSumChunks = kWW / 256;  // a window owns at most kWW segments; the last chunk of
+    constexpr int kSegSlots = kSumChunks * 4;  // starts only supplies the final segment's end
+    float psum[kSegSlots];
+    uint32_t off[kSegSlots];
+    uint64_t wide[kSegSlots];
+    const int32_t nseg = g1 - g0;
+#pragma unroll
+    for (int k = 0; k < kSumChunks; ++k) {
+      const int32_t next_lane = __shfl(w.sp[k].x, (lane + 1) & 63, 64);  // lane l + 1's first start
+      const int32_t next_chunk = __shfl(w.sp[k + 1].x, 0, 64);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int si = 4 * k + q;
+        const int32_t sidx = 256 * k + 4 * lane + q;
+        const int32_t rb = elem(w.sp[k], q);
+        const int32_t re = q < 3 ? elem(w.sp[k], q + 1) : (lane < 63 ? next_lane : next_chunk);
+        const bool in = sidx < nseg;
+        const bool seq = in && re - rb <= kSeqSeg;
+        wide[si] = __ballot(in && re - rb > kSeqSeg && re - rb <= kLongSeg);
+        psum[si] = seq ? lds_seq_sum(wp, rb - b, min(re, e) - b) : 0.0f;
+        off[si] = seq ? (uint32_t)sidx * 4u : kDrop;
+      }
+    }
+#pragma unroll
+    for (int si = 0; si < kSegSlots; ++si) {
+      for (uint64_t m = wide[si]; m; m &= m - 1) {  // wave-uniform loop over this slot's wide segments
+        const int L = __builtin_ctzll(m);
+        const int k = si / 4, q = si % 4;
+        const int32_t rb = __shfl(elem(w.sp[k], q), L, 64);
+        int32_t re;
+        if (q < 3) re = __shfl(elem(w.sp[k], q + 1), L, 64);
+        else if (L < 63) re = __shfl(w.sp[k].x, L + 1, 64);
+        else re = __shfl(w.sp[k + 1].x, 0, 64);
+        float t = 0.0f;
+        for (int32_t i = rb - b + lane; i < min(re, e) - b; i += 64) t += wp[i];
+        const float tw = wave_sum_f32(t);
+        if (lane == L) {
+          psum[si] = tw;
+          off[si] = (uint32_t)(256 * k + 4 * L + q) * 4u;
+        }
+      }
+    }
+    const auto rp = range_rsrc(partial + g0, nseg * 4);
+#pragma unroll
+    for (int k = 0; k < kSumChunks; ++k) {
+      if (256 * k < nseg) {  // wave-uniform: groups holding no segment issue no store
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int32_t, psum[4 * k + q]), rp, off[4 * k + q], 0, kNt);
+      }
+    }
     wave_lds_sync();
     d = dn;
-    dn = dnn;
-    cur = nxt;
   }
 }
 
@@ -871,9 +955,11 @@ void plan_layout(dc_hip_spmv_plan* p, void* mem) {
   };
   const size_t nz = (size_t)std::max<int64_t>(p->nnz, 1);
   const size_t tab = (size_t)p->slices * (p->nblocks + 1) * 4;
-  p->col_s = reinterpret_cast<int32_t*>(take(nz * 4));
-  p->val_s = reinterpret_cast<float*>(take(nz * 4));
-  p->seg_ptr = reinterpret_cast<int32_t*>(take((nz + 1) * 4));
+  // col_s, val_s and seg_ptr are read with 16-byte loads over ranges rounded up to whole groups:
+  // 16 bytes of slack after each keeps those loads inside the allocation
+  p->col_s = reinterpret_cast<int32_t*>(take(nz * 4 + 16));
+  p->val_s = reinterpret_cast<float*>(take(nz * 4 + 16));
+  p->seg_ptr = reinterpret_cast<int32_t*>(take((nz + 1) * 4 + 16));
   p->partial = reinterpret_cast<float*>(take(nz * 4));
   p->seg_row = reinterpret_cast<uint8_t*>(take(nz));
   p->tn = reinterpret_cast<int32_t*>(take(tab));
@@ -917,15 +1003,33 @@ int32_t plan_build(dc_hip_ctx* ctx, dc_hip_spmv_plan* p, const int32_t* rp, cons
   const uint32_t width = (uint32_t)p->slice_cols, cols = (uint32_t)std::max<int64_t>(p->cols, 1);
   const int32_t nnz = (int32_t)p->nnz;
   if (p->rows == 0) return DC_OK;
-  plan_count<<<(unsigned)p->nblocks, kRB, 0, ctx->stream>>>(rp, col, p->rows, nnz, S, width, cols, p->tn, p->ts, ld);
+  const unsigned agrid = (unsigned)(kXcds * ((p->nblocks + kXcds - 1) / kXcds));
+#define DC_PLAN_COUNT(SM)                                                                                      \
+  plan_count<SM><<<agrid, kRB, 0, ctx->stream>>>(rp, col, p->rows, nnz, S, width, cols, p->tn, p->ts, ld, \
+                                                 p->nblocks)
+  if (S <= 1) DC_PLAN_COUNT(1);
+  else if (S <= 2) DC_PLAN_COUNT(2);
+  else if (S <= 4) DC_PLAN_COUNT(4);
+  else if (S <= 8) DC_PLAN_COUNT(8);
+  else if (S <= 16) DC_PLAN_COUNT(16);
+  else DC_PLAN_COUNT(32);
+#undef DC_PLAN_COUNT
   DC_RETURN_IF(dc::last_launch_status());
   plan_scan<<<(unsigned)S, kScanBlock, 0, ctx->stream>>>(p->tn, p->ts, p->nblocks, ld, S, p->tot);
   DC_RETURN_IF(dc::last_launch_status());
   plan_bases<<<1, 64, 0, ctx->stream>>>(p->tot, S, p->nb, p->sb, p->seg_ptr, p->xcd, p->long_cnt);
   DC_RETURN_IF(dc::last_launch_status());
-  plan_scatter<<<(unsigned)p->nblocks, kRB, 0, ctx->stream>>>(rp, col, val, p->rows, nnz, S, width, cols, p->tn, p->ts,
-                                                              ld, p->nb, p->sb, p->col_s, p->val_s, p->seg_ptr,
-                                                              p->seg_row, p->long_list, p->long_cnt, p->long_cap);
+#define DC_PLAN_SCATTER(SM)                                                                                 \
+  plan_scatter<SM><<<agrid, kRB, 0, ctx->stream>>>(rp, col, val, p->rows, nnz, S, width, cols, p->tn, p->ts, ld, \
+                                                   p->nb, p->sb, p->col_s, p->val_s, p->seg_ptr, p->seg_row,      \
+                                                   p->long_list, p->long_cnt, p->long_cap, p->nblocks)
+  if (S <= 1) DC_PLAN_SCATTER(1);
+  else if (S <= 2) DC_PLAN_SCATTER(2);
+  else if (S <= 4) DC_PLAN_SCATTER(4);
+  else if (S <= 8) DC_PLAN_SCATTER(8);
+  else if (S <= 16) DC_PLAN_SCATTER(16);
+  else DC_PLAN_SCATTER(32);
+#undef DC_PLAN_SCATTER
   DC_RETURN_IF(dc::last_launch_status());
   if (p->nwin > 0) {
     plan_desc<<<(unsigned)((p->nwin + 255) / 256), 256, 0, ctx->stream>>>(p->seg_ptr, p->nb, p->sb, S, p->nwin,
@@ -942,11 +1046,19 @@ int32_t plan_spmv(dc_hip_ctx* ctx, const dc_hip_spmv_plan* p, const float* x, fl
   if (p->nwin > 0) {
     const int per_xcd_cus = std::max(1, ctx->cu_count / kXcds);
     const int phases = p->slices >= kXcds ? p->slices / kXcds : 1;
+    // resident gather workgroups per CU (registers and LDS decide it), asked once per process
+    static const int per_cu = [] {
+      int n = 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, spmv_slice_windows, kGatherBlock, 0) != hipSuccess || n < 1)
+        n = 4;
+      return n;
+    }();
     const int64_t want = (p->nwin / phases / kXcds + 3) / 4 + 1;  // workgroups per XCD, one window per wave
-    const int64_t per_xcd = std::min<int64_t>(want, (int64_t)per_xcd_cus * kGatherPerCu);
+    const int64_t per_xcd = std::min<int64_t>(want, (int64_t)per_xcd_cus * per_cu);
     for (int ph = 0; ph < phases; ++ph) {
       spmv_slice_windows<<<(unsigned)(per_xcd * kXcds), kGatherBlock, 0, ctx->stream>>>(
-          p->desc, p->seg_ptr, p->col_s, p->val_s, x, p->partial, p->xcd + ph * kXcds * kXcdWords);
+          p->desc, p->seg_ptr, p->col_s, p->val_s, x, p->partial, p->xcd + ph * kXcds * kXcdWords,
+          (int32_t)p->cols);
       DC_RETURN_IF(dc::last_launch_status());
     }
     const int64_t lgrid = std::min<int64_t>((int64_t)p->long_cap, (int64_t)per_xcd_cus * 2);
@@ -977,7 +1089,8 @@ int32_t plan_power_iterate(dc_hip_ctx* ctx, const dc_hip_spmv_plan* p, float* x,
 }
 
 int32_t check_plan_shape(int64_t rows, int64_t cols, int64_t nnz) {
-  if (cols < 0 || cols > INT32_MAX || (nnz > 0 && cols == 0)) return DC_ERR_INVALID_ARGUMENT;
+  if (cols < 0 || (nnz > 0 && cols == 0)) return DC_ERR_INVALID_ARGUMENT;
+  if (cols > (int64_t{1} << 30) - 1) return DC_ERR_UNSUPPORTED;  // x is addressed with 32-bit byte offsets
   (void)rows;
   return DC_OK;
 }
