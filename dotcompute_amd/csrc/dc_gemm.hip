@@ -341,6 +341,168 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_bf16_kernel(const unsigned s
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// bf16, large tiles: C = A·B with B first transposed to Bt[n][k] (a separate pass, so both
+// operands are k-contiguous and every global load and LDS access is 16 bytes wide).
+//
+// Macro tile 256×256, BK = 64, double-buffered LDS (2 × (256 + 256) rows × 72 bf16 = 144 KiB,
+// one workgroup per CU). WAVES = 8: 512 threads as 2×4 waves of 128×64 (4×2 MFMA 32×32×16 tiles,
+// 128 accumulators per lane), two waves per SIMD so one's LDS and barrier waits overlap the
+// other's MFMAs. Row pitch 72 bf16 = 144 B: the eight 16-byte reads of one LDS cycle (rows
+// r..r+7) land on disjoint banks. Each k step (16 wide) is one scheduling region: its MFMAs with
+// the next step's LDS reads spread between them; the next tile's global loads go out with the
+// first step and its LDS writes with the last.
+// ---------------------------------------------------------------------------------------------
+constexpr int kBM2 = 256, kBN2 = 256, kBK2 = 64, kPitch2 = kBK2 + 8;
+constexpr int kBigThreads = 512;
+constexpr int kWaveM = 128, kWaveN = 64;       // wave tile
+constexpr int kMT = kWaveM / 32, kNT = kWaveN / 32;
+
+struct Bf16BigSmem {
+  unsigned short a[2][kBM2][kPitch2];
+  unsigned short b[2][kBN2][kPitch2];
+};
+
+// One BK slice of A (256 rows) and Bt (256 rows), 8 bf16 per 16-byte slot: slot s -> row s / 8,
+// k-octet s % 8; 2048 slots per operand.
+struct Bf16BigLoader {
+  static constexpr int kSlots = kBM2 * kBK2 / 8 / kBigThreads;
+  u16x8 ra[kSlots];
+  u16x8 rb[kSlots];
+
+  __device__ inline void load(const unsigned short* __restrict__ A, const unsigned short* __restrict__ Bt, int K,
+                              int m0, int n0, int k0, int tid) {
+#pragma unroll
+    for (int i = 0; i < kSlots; ++i) {
+      const int s = tid + i * kBigThreads;
+      const int row = s >> 3, kq = s & 7;
+      ra[i] = *reinterpret_cast<const u16x8*>(A + (size_t)(m0 + row) * K + k0 + 8 * kq);
+      rb[i] = *reinterpret_cast<const u16x8*>(Bt + (size_t)(n0 + row) * K + k0 + 8 * kq);
+    }
+  }
+
+  __device__ inline void store(Bf16BigSmem& sm, int buf, int tid) {
+#pragma unroll
+    for (int i = 0; i < kSlots; ++i) {
+      const int s = tid + i * kBigThreads;
+      const int row = s >> 3, kq = s & 7;
+      *reinterpret_cast<u16x8*>(&sm.a[buf][row][8 * kq]) = ra[i];
+      *reinterpret_cast<u16x8*>(&sm.b[buf][row][8 * kq]) = rb[i];
+    }
+  }
+};
+
+__global__ __launch_bounds__(kBigThreads, 1) void gemm_bf16_big_kernel(const unsigned short* __restrict__ A,
+                                                                       const unsigned short* __restrict__ Bt,
+                                                                       float* __restrict__ C, int M, int N, int K,
+                                                                       int tiles_m, int tiles_n) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  Bf16BigSmem& sm = *reinterpret_cast<Bf16BigSmem*>(smem_raw);
+  const TileCoord tc = map_tile(tiles_m, tiles_n);
+  const int m0 = tc.tm * kBM2, n0 = tc.tn * kBN2;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / (kBN2 / kWaveN), wn = wave % (kBN2 / kWaveN);
+  const int r = lane & 31, h = lane >> 5;
+
+  f32x16 acc[kMT][kNT];
+#pragma unroll
+  for (int i = 0; i < kMT; ++i)
+#pragma unroll
+    for (int j = 0; j < kNT; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  Bf16BigLoader ld;
+  const int kt_count = K / kBK2;
+  ld.load(A, Bt, K, m0, n0, 0, tid);
+  ld.store(sm, 0, tid);
+  __syncthreads();
+
+  auto read_frags = [&](int buf, int ks, bf16x8* a, bf16x8* b) {
+#pragma unroll
+    for (int mt = 0; mt < kMT; ++mt)
+      a[mt] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(&sm.a[buf][wm * kWaveM + mt * 32 + r][ks + 8 * h]));
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt)
+      b[nt] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(&sm.b[buf][wn * kWaveN + nt * 32 + r][ks + 8 * h]));
+  };
+  constexpr int kSteps = kBK2 / 16, kMfma = kMT * kNT, kReads = kMT + kNT;
+  for (int kt = 0; kt < kt_count; ++kt) {
+    const int buf = kt & 1;
+    const bool more = kt + 1 < kt_count;
+    bf16x8 fa[2][kMT], fb[2][kNT];
+    read_frags(buf, 0, fa[0], fb[0]);
+#pragma unroll
+    for (int step = 0; step < kSteps; ++step) {
+      const int cur = step & 1;
+      __builtin_amdgcn_sched_barrier(0);
+      if (step == 0 && more) ld.load(A, Bt, K, m0, n0, (kt + 1) * kBK2, tid);
+      if (step + 1 < kSteps) read_frags(buf, 16 * (step + 1), fa[cur ^ 1], fb[cur ^ 1]);
+      if (step + 1 == kSteps && more) ld.store(sm, buf ^ 1, tid);
+#pragma unroll
+      for (int mt = 0; mt < kMT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt)
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cur][mt], fb[cur][nt], acc[mt][nt], 0, 0, 0);
+      if (step + 1 < kSteps) {
+#pragma unroll
+        for (int i = 0; i < kReads; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < kMfma; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // 1 LDS write
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __syncthreads();
+  }
+
+  // acc[mt][nt][v] holds C[row][col], row = 8*(v/4) + 4*h + v%4, col = r (within the 32×32 tile).
+#pragma unroll
+  for (int mt = 0; mt < kMT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) {
+      const int col = n0 + wn * kWaveN + nt * 32 + r;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int row = m0 + wm * kWaveM + mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+        C[(size_t)row * N + col] = acc[mt][nt][v];
+      }
+    }
+}
+
+// Bt[n][k] = B[k][n] for bf16 bit patterns, 64×64 tiles through LDS with 16-byte global loads and
+// stores on both sides (K and N multiples of 64 and rows 16-byte aligned, as the large-tile GEMM
+// requires). A thread loads 8 consecutive n of one k row, then gathers 8 consecutive k of one n
+// column from LDS (pitch 66 bf16 spreads those reads over the banks) and stores them as 16 bytes.
+__global__ __launch_bounds__(256) void transpose_u16_kernel(const unsigned short* __restrict__ B,
+                                                            unsigned short* __restrict__ Bt, int K, int N) {
+  __shared__ unsigned short t[64][66];
+  const int k0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {  // 512 slots of 8 bf16: slot -> k row s / 8, n octet s % 8
+    const int sl = tid + 256 * i, kr = sl >> 3, no = (sl & 7) * 8;
+    const u16x8 v = *reinterpret_cast<const u16x8*>(B + (size_t)(k0 + kr) * N + n0 + no);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[kr][no + e] = v[e];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {  // slot -> n row s / 8, k octet s % 8
+    const int sl = tid + 256 * i, nr = sl >> 3, ko = (sl & 7) * 8;
+    u16x8 v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = t[ko + e][nr];
+    *reinterpret_cast<u16x8*>(Bt + (size_t)(n0 + nr) * K + k0 + ko) = v;
+  }
+}
+
 // Round-to-nearest-even fp32 -> bf16 (quiet NaN kept NaN).
 __global__ __launch_bounds__(256) void f32_to_bf16_kernel(const float* __restrict__ x, unsigned short* __restrict__ y,
                                                           int64_t n) {
@@ -398,9 +560,25 @@ DC_HIP_API int32_t dc_hip_gemm_bf16(dc_hip_ctx* ctx, const uint16_t* a, const ui
   if (k == 0) return dc::zero_async(ctx, c, (size_t)(m * n) * sizeof(float));
   const int tiles_m = (int)((m + kBM - 1) / kBM), tiles_n = (int)((n + kBN - 1) / kBN);
   const unsigned grid = (unsigned)(tiles_m * tiles_n);
-  const bool full = (m % kBM == 0) && (n % kBN == 0) && (k % kBKbf16 == 0) && dc::aligned16(a) && dc::aligned16(b);
   const unsigned short* A = reinterpret_cast<const unsigned short*>(a);
   const unsigned short* B = reinterpret_cast<const unsigned short*>(b);
+  if ((m % kBM2 == 0) && (n % kBN2 == 0) && (k % kBK2 == 0) && dc::aligned16(a) && dc::aligned16(b)) {
+    // large tiles: B transposed into context scratch first
+    DC_RETURN_IF(dc::ensure_gemm_scratch(ctx, (size_t)n * (size_t)k * sizeof(unsigned short)));
+    unsigned short* Bt = static_cast<unsigned short*>(ctx->gemm_scratch);
+    transpose_u16_kernel<<<dim3((unsigned)((n + 63) / 64), (unsigned)((k + 63) / 64)), 256, 0, ctx->stream>>>(
+        B, Bt, (int)k, (int)n);
+    DC_RETURN_IF(dc::last_launch_status());
+    const int tm2 = (int)(m / kBM2), tn2 = (int)(n / kBN2);
+    static const hipError_t lds_ok = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_bf16_big_kernel),
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                         (int)sizeof(Bf16BigSmem));
+    DC_RETURN_IF_HIP(lds_ok);
+    gemm_bf16_big_kernel<<<(unsigned)(tm2 * tn2), kBigThreads, sizeof(Bf16BigSmem), ctx->stream>>>(
+        A, Bt, c, (int)m, (int)n, (int)k, tm2, tn2);
+    return dc::last_launch_status();
+  }
+  const bool full = (m % kBM == 0) && (n % kBN == 0) && (k % kBKbf16 == 0) && dc::aligned16(a) && dc::aligned16(b);
   if (full)
     gemm_bf16_kernel<kBKbf16, false><<<grid, kThreads, 0, ctx->stream>>>(A, B, c, (int)m, (int)n, (int)k, tiles_m, tiles_n);
   else
