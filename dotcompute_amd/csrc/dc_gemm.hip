@@ -53,23 +53,24 @@ __device__ inline TileCoord map_tile(int tiles_m, int tiles_n) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// fp32
+// fp32. T = macro tile (128, or 64 when 128-tiles cannot occupy the CUs: 1024² has only 64 of
+// them); 4 waves as 2×2, each wave (T/2)×(T/2) = (T/64)×(T/64) MFMA 32×32 tiles.
 // ---------------------------------------------------------------------------------------------
-template <int BK>
+template <int BK, int T>
 struct F32Smem {
   static constexpr int kPitch = BK + 4;  // floats per LDS row
-  float a[2][kBM][kPitch];
-  float b[2][kBN][kPitch];
+  float a[2][T][kPitch];
+  float b[2][T][kPitch];
 };
 
-// Global -> register prefetch for one BK slice. A: (128 rows × BK) as float4 slots,
-// slot s -> row s / (BK/4), kq = s % (BK/4). B: (BK × 128) as float4 slots, slot s ->
+// Global -> register prefetch for one BK slice. A: (T rows × BK) as float4 slots,
+// slot s -> row s / (BK/4), kq = s % (BK/4). B: (BK × T) as float4 slots, slot s ->
 // nq = s / BK, k = s % BK (a wave covers 16 k-rows × 4 column quads, which spreads the transposed
 // LDS writes over the banks).
-template <int BK, bool CHECKED>
+template <int BK, bool CHECKED, int T>
 struct F32Loader {
-  static constexpr int kASlots = kBM * BK / 4 / kThreads;
-  static constexpr int kBSlots = kBN * BK / 4 / kThreads;
+  static constexpr int kASlots = T * BK / 4 / kThreads;
+  static constexpr int kBSlots = T * BK / 4 / kThreads;
   dc::f32x4 ra[kASlots];
   dc::f32x4 rb[kBSlots];
 
@@ -115,7 +116,7 @@ struct F32Loader {
     }
   }
 
-  __device__ inline void store(F32Smem<BK>& sm, int buf, int tid) {
+  __device__ inline void store(F32Smem<BK, T>& sm, int buf, int tid) {
 #pragma unroll
     for (int i = 0; i < kASlots; ++i) {
       const int s = tid + i * kThreads;
@@ -134,26 +135,27 @@ struct F32Loader {
   }
 };
 
-template <int BK, bool CHECKED>
+template <int BK, bool CHECKED, int T>
 __global__ __launch_bounds__(kThreads, 2) void gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B,
                                                                float* __restrict__ C, int M, int N, int K, int tiles_m,
                                                                int tiles_n) {
-  __shared__ F32Smem<BK> sm;
+  constexpr int kW = T / 2, kMT = T / 64;  // wave tile edge, MFMA tiles per wave edge
+  __shared__ F32Smem<BK, T> sm;
   const TileCoord tc = map_tile(tiles_m, tiles_n);
-  const int m0 = tc.tm * kBM, n0 = tc.tn * kBN;
+  const int m0 = tc.tm * T, n0 = tc.tn * T;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int r = lane & 31, h = lane >> 5;
 
-  f32x16 acc[2][2];
+  f32x16 acc[kMT][kMT];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < kMT; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < kMT; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  F32Loader<BK, CHECKED> ld;
+  F32Loader<BK, CHECKED, T> ld;
   const int kt_count = (K + BK - 1) / BK;
   ld.load(A, B, M, N, K, m0, n0, 0, tid);
   ld.store(sm, 0, tid);
@@ -164,25 +166,25 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_kernel(const float* __re
     if (kt + 1 < kt_count) ld.load(A, B, M, N, K, m0, n0, (kt + 1) * BK, tid);
 #pragma unroll
     for (int ks = 0; ks < BK; ks += 16) {
-      dc::f32x4 a[2][2], b[2][2];
+      dc::f32x4 a[kMT][2], b[kMT][2];
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const float* p = &sm.a[buf][wm * 64 + mt * 32 + r][ks + 8 * h];
+      for (int mt = 0; mt < kMT; ++mt) {
+        const float* p = &sm.a[buf][wm * kW + mt * 32 + r][ks + 8 * h];
         a[mt][0] = *reinterpret_cast<const dc::f32x4*>(p);
         a[mt][1] = *reinterpret_cast<const dc::f32x4*>(p + 4);
       }
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const float* p = &sm.b[buf][wn * 64 + nt * 32 + r][ks + 8 * h];
+      for (int nt = 0; nt < kMT; ++nt) {
+        const float* p = &sm.b[buf][wn * kW + nt * 32 + r][ks + 8 * h];
         b[nt][0] = *reinterpret_cast<const dc::f32x4*>(p);
         b[nt][1] = *reinterpret_cast<const dc::f32x4*>(p + 4);
       }
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk) {
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+        for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
-          for (int nt = 0; nt < 2; ++nt)
+          for (int nt = 0; nt < kMT; ++nt)
             acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[mt][kk >> 2][kk & 3], b[nt][kk >> 2][kk & 3],
                                                                acc[mt][nt], 0, 0, 0);
       }
@@ -193,13 +195,13 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_kernel(const float* __re
 
   // acc[mt][nt][v] holds C[row][col], row = 8*(v/4) + 4*h + v%4, col = r (within the 32×32 tile).
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+  for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const int col = n0 + wn * 64 + nt * 32 + r;
+    for (int nt = 0; nt < kMT; ++nt) {
+      const int col = n0 + wn * kW + nt * 32 + r;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int row = m0 + wm * 64 + mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+        const int row = m0 + wm * kW + mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
         if (!CHECKED || (row < M && col < N)) C[(size_t)row * N + col] = acc[mt][nt][v];
       }
     }
@@ -541,13 +543,22 @@ DC_HIP_API int32_t dc_hip_gemm_f32(dc_hip_ctx* ctx, const float* a, const float*
   if (!c || (k > 0 && (!a || !b))) return DC_ERR_INVALID_ARGUMENT;
   DC_CTX_ENTER(ctx);
   if (k == 0) return dc::zero_async(ctx, c, (size_t)(m * n) * sizeof(float));
-  const int tiles_m = (int)((m + kBM - 1) / kBM), tiles_n = (int)((n + kBN - 1) / kBN);
+  // 128×128 tiles unless that leaves fewer than two per CU; then 64×64 (four times the tiles)
+  const int64_t tiles128 = ((m + 127) / 128) * ((n + 127) / 128);
+  const bool small = tiles128 < 2 * (int64_t)std::max(1, ctx->cu_count);
+  const int T = small ? 64 : 128;
+  const int tiles_m = (int)((m + T - 1) / T), tiles_n = (int)((n + T - 1) / T);
   const unsigned grid = (unsigned)(tiles_m * tiles_n);
-  const bool full = (m % kBM == 0) && (n % kBN == 0) && (k % kBKf32 == 0) && dc::aligned16(a) && dc::aligned16(b);
-  if (full)
-    gemm_f32_kernel<kBKf32, false><<<grid, kThreads, 0, ctx->stream>>>(a, b, c, (int)m, (int)n, (int)k, tiles_m, tiles_n);
-  else
-    gemm_f32_kernel<kBKf32, true><<<grid, kThreads, 0, ctx->stream>>>(a, b, c, (int)m, (int)n, (int)k, tiles_m, tiles_n);
+  const bool full = (m % T == 0) && (n % T == 0) && (k % kBKf32 == 0) && dc::aligned16(a) && dc::aligned16(b);
+#define DC_GEMM_F32(CHECKED, TT)                                                                                   \
+  gemm_f32_kernel<kBKf32, CHECKED, TT><<<grid, kThreads, 0, ctx->stream>>>(a, b, c, (int)m, (int)n, (int)k, tiles_m, \
+                                                                          tiles_n)
+  if (small) {
+    if (full) DC_GEMM_F32(false, 64); else DC_GEMM_F32(true, 64);
+  } else {
+    if (full) DC_GEMM_F32(false, 128); else DC_GEMM_F32(true, 128);
+  }
+#undef DC_GEMM_F32
   return dc::last_launch_status();
 }
 

@@ -79,7 +79,10 @@ def test_gemm_f32_reference_case_vs_fp32_loop(ctx):
     assert np.max(np.abs(c - expected)) <= 1e-3
 
 
-@pytest.mark.parametrize("shape", [(1, 1, 1), (3, 5, 7), (100, 37, 53), (129, 130, 131), (257, 64, 1000)])
+# Shapes with fewer than 2 * CUs tiles of 128x128 run 64x64 tiles; (4000, 2100, 37) has 544 of them
+# and takes the bounds-checked 128x128 kernel.
+@pytest.mark.parametrize("shape", [(1, 1, 1), (3, 5, 7), (100, 37, 53), (129, 130, 131), (257, 64, 1000),
+                                   (4000, 2100, 37)])
 def test_gemm_f32_ragged(ctx, shape):
     m, n, k = shape
     a, b = make_inputs(m, n, k, 7, 8)
