@@ -772,30 +772,44 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
     tail += cnt;
   };
 
+  // Every load below is unconditional: rounds past the last one re-load round R0 - 1 (loaded one
+  // round earlier, so mostly served by the cache). The compiler's memory-counter waits are
+  // path-insensitive: on a path that skipped a later load, the wait for the round being staged
+  // would have to cover every load still in flight, draining the pipeline.
+  const uint32_t last = R0 > 0 ? R0 - 1 : 0;
   float e0[kRrEpt], e1[kRrEpt], e2[kRrEpt], e3[kRrEpt], e4[kRrEpt];
-  if (R0 > 0) load(e0, 0);
-  if (R0 > 1) load(e1, 1);
-  if (R0 > 2) load(e2, 2);
-  if (R0 > 3) load(e3, 3);
+  if (R0 > 0) {
+    load(e0, 0);
+    load(e1, min(1u, last));
+    load(e2, min(2u, last));
+    load(e3, min(3u, last));
+  }
   uint32_t r = 0;
   // One round: issue the loads of round r + kRrAhead into EN, stage round r from EC, write round
-  // r - kRrDelay. Unrolled five ways so the register buffers rotate without copies.
+  // r - kRrDelay. Unrolled five ways so the register buffers rotate without copies. The main loop
+  // runs whole five-round iterations with no early exit: a `break` between rounds becomes a path
+  // back to the loop head after a partial iteration, and the waits at the head would then assume
+  // fewer loads in flight than the full iteration leaves. The last R0 % 5 rounds follow it.
 #define DC_RR_ROUND(EC, EN)                                                              \
   {                                                                                      \
-    if (r + kRrAhead < R0) load(EN, r + kRrAhead);                                       \
+    load(EN, min(r + kRrAhead, last));                                                   \
     stage(EC, apply_rounds<MODE, kRrEpt>(prog, canon, EC), r);                              \
     __syncthreads();                                                                     \
     if (r >= (uint32_t)kRrDelay) write(r - kRrDelay, r & 1);                             \
-    if (++r >= R0) break;                                                                \
+    ++r;                                                                                 \
   }
   static_assert(kRrAhead == 4, "five register buffers");
-  while (r < R0) {
+  for (uint32_t it = R0 / 5; it > 0; --it) {
     DC_RR_ROUND(e0, e4);
     DC_RR_ROUND(e1, e0);
     DC_RR_ROUND(e2, e1);
     DC_RR_ROUND(e3, e2);
     DC_RR_ROUND(e4, e3);
   }
+  if (r < R0) DC_RR_ROUND(e0, e4);
+  if (r < R0) DC_RR_ROUND(e1, e0);
+  if (r < R0) DC_RR_ROUND(e2, e1);
+  if (r < R0) DC_RR_ROUND(e3, e2);
 #undef DC_RR_ROUND
   for (; r < rounds; ++r) {  // drain: the last kRrDelay staged tiles
     __syncthreads();
