@@ -9,7 +9,7 @@ order-preserving compaction kernel. Throughput = algorithmic bytes (4 B read per
 
 Also reported (outside the timed steps, each with its own roofline): Sum f32 / i32 at 256M, the
 fused Where->Select->Sum at 256M, VectorAdd at N=100,000 and 256M, dense fp32 and bf16 MatMul,
-CSR SpMV x20. The CPU baseline is the oracle's single-thread LINQ-to-objects restatement of the
+CSR SpMV x20. These legs run first and the headline's W warmup + K timed steps run after them. The CPU baseline is the oracle's single-thread LINQ-to-objects restatement of the
 headline chain, timed on this host.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-extras]
@@ -30,15 +30,25 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix, published
 BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix, published
 N_MAIN = 256 * 1024 * 1024
+LEG_WARM_MS = 40.0  # untimed warm-up of each reported leg (device clock ramp after idle)
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def time_launches(ctx, fn, iters: int) -> float:
+def time_launches(ctx, fn, iters: int, warm_ms: float = 0.0) -> float:
     """Average duration (ms) of `fn` over `iters` back-to-back launches, from HIP events recorded
-    on the context stream the kernels run on."""
+    on the context stream the kernels run on. With warm_ms > 0, `fn` first runs untimed until the
+    device has been busy with it for that long: after ~0.5 s idle the device needs ~25 ms of load
+    to reach its full clocks, and a leg timed from idle would be measured on that ramp."""
+    if warm_ms > 0:
+        t0 = time.perf_counter()
+        for _ in range(1000):
+            fn()
+            ctx.synchronize()
+            if (time.perf_counter() - t0) * 1e3 >= warm_ms:
+                break
     e0, e1 = ctx.event(), ctx.event()
     e0.record()
     for _ in range(iters):
@@ -74,8 +84,8 @@ def roofline(bound: str, achieved: float, peak: float, unit: str, traffic=None) 
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--skip-extras", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only", default="", help="comma list of extras to run (sum,linq_sum,vector_add,gemm,spmv)")
@@ -94,13 +104,88 @@ def main() -> int:
     log(f"[bench] device {info.name.decode()} {info.gcn_arch_name.decode()} CUs={info.compute_units}")
     ctx = hip.Context(0)
     chain = hip.where_gt0_select_2x_plus_1()
+    extra: dict = {}
 
-    # ---------------- headline: Where->Select->ToArray, N = 256M, resident in HBM -------------
+    # ---------------- inputs: N = 256M float32, resident in HBM ------------------------------
     n = N_MAIN
     x = ctx.empty(n, np.float32)
     ctx.fill_uniform_f32(x, seed=44, stream=0)
     out = ctx.empty(n, np.float32)
     cnt = ctx.empty(1, np.int64)
+    if args.copy_calibration:
+        # 1 GiB read + 1 GiB written by the runtime's copy kernel: a counter reading for it, divided
+        # by 1 GiB, is the scale factor for the headline kernel's FETCH_SIZE / WRITE_SIZE readings
+        cal = ctx.empty(n, np.float32)
+        hip.check(hip.load().dc_hip_memcpy_d2d_async(ctx.handle, cal.ptr, x.ptr, 4 * n), "d2d copy")
+        ctx.synchronize()
+        ctx.free(cal)
+        log("[bench] copy calibration: 1 GiB device-to-device copy done")
+
+    warm_timer = lambda c, f, it: time_launches(c, f, it, warm_ms=LEG_WARM_MS)
+
+    def want(name):
+        return not args.skip_extras and (not args.only or name in args.only.split(","))
+
+    # ---------------- dense MatMul -------------------------------------------------------------
+    if want("gemm"):
+        from bench_extras import bench_gemm  # noqa: E402
+
+        extra.update(bench_gemm(ctx, log, warm_timer, roofline, FP32_MFMA_PEAK_TFLOPS, BF16_MFMA_PEAK_TFLOPS))
+    # ---------------- CSR SpMV x20 ---------------------------------------------------------------
+    if want("spmv"):
+        from bench_extras import bench_spmv  # noqa: E402
+
+        extra.update(bench_spmv(ctx, log, warm_timer, roofline, HBM_PEAK_GBS))
+
+    # ---------------- fused Where->Select->Sum and plain Sum at 256M --------------------------
+    if want("linq_sum"):
+        s = ctx.empty(1, np.float64)
+        c = ctx.empty(1, np.int64)
+        f = lambda: ctx.where_select_sum_f32(chain, x, s, c, n)
+        f(); ctx.synchronize()
+        ms = time_launches(ctx, f, 20, warm_ms=LEG_WARM_MS)
+        gbs = 4 * n / (ms * 1e-3) / 1e9
+        extra["where_select_sum_f32_256M"] = {"ms": round(ms, 4), "GB/s": round(gbs, 1), "count": int(c.to_host()[0]),
+                                               "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
+        log(f"[bench] where_select_sum 256M: {ms*1e3:.1f} us -> {gbs:.0f} GB/s")
+    if want("sum"):
+        s = ctx.empty(1, np.float64)
+        f = lambda: ctx.reduce_sum_f32(x, s, n)
+        f(); ctx.synchronize()
+        ms = time_launches(ctx, f, 20, warm_ms=LEG_WARM_MS)
+        gbs = 4 * n / (ms * 1e-3) / 1e9
+        extra["sum_f32_256M"] = {"ms": round(ms, 4), "GB/s": round(gbs, 1),
+                                 "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
+        log(f"[bench] sum_f32 256M: {ms*1e3:.1f} us -> {gbs:.0f} GB/s")
+        xi = ctx.empty(n, np.int32)
+        ctx.fill_uniform_i32(xi, seed=43, stream=1)
+        si = ctx.empty(1, np.int64)
+        ov = ctx.empty(1, np.int32)
+        f = lambda: ctx.reduce_sum_i32(xi, si, ov, n)
+        f(); ctx.synchronize()
+        ms = time_launches(ctx, f, 20, warm_ms=LEG_WARM_MS)
+        gbs = 4 * n / (ms * 1e-3) / 1e9
+        extra["sum_i32_256M"] = {"ms": round(ms, 4), "GB/s": round(gbs, 1),
+                                 "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
+        log(f"[bench] sum_i32 256M: {ms*1e3:.1f} us -> {gbs:.0f} GB/s")
+        ctx.free(xi)
+    if want("vector_add"):
+        for nv, label in ((100_000, "vector_add_f32_100K"), (n, "vector_add_f32_256M")):
+            a = x
+            b = ctx.empty(nv, np.float32)
+            ctx.fill_uniform_f32(b, seed=42, stream=1)
+            r = out
+            f = lambda: ctx.vector_add_f32(a, b, r, nv)
+            f(); ctx.synchronize()
+            ms = time_launches(ctx, f, 50 if nv < n else 20, warm_ms=LEG_WARM_MS)
+            gbs = 12 * nv / (ms * 1e-3) / 1e9
+            extra[label] = {"ms": round(ms, 5), "GB/s": round(gbs, 1),
+                            "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
+            log(f"[bench] {label}: {ms*1e3:.2f} us -> {gbs:.0f} GB/s")
+            ctx.free(b)
+
+    # ---------------- headline, timed last: the other legs have run by now, so the device's clocks
+    # have left their idle state before the timed steps (the W warmup steps alone last ~2 ms)
     run = lambda: ctx.where_select_f32(chain, x, out, cnt, n)
     for _ in range(args.warmup):
         run()
@@ -117,79 +202,8 @@ def main() -> int:
     achieved = step_bytes / (ms_kernel * 1e-3) / 1e9
     log(f"[bench] where_select 256M: kept={kept} kernel={ms_kernel*1e3:.1f} us wall/step={ms_per_step*1e3:.1f} us "
         f"-> {achieved:.0f} GB/s")
-    extra: dict = {}
-    if args.copy_calibration:
-        # 1 GiB read + 1 GiB written by the runtime's copy kernel: a counter reading for it, divided
-        # by 1 GiB, is the scale factor for the headline kernel's FETCH_SIZE / WRITE_SIZE readings
-        cal = ctx.empty(n, np.float32)
-        hip.check(hip.load().dc_hip_memcpy_d2d_async(ctx.handle, cal.ptr, x.ptr, 4 * n), "d2d copy")
-        ctx.synchronize()
-        ctx.free(cal)
-        log("[bench] copy calibration: 1 GiB device-to-device copy done")
-
-    def want(name):
-        return not args.skip_extras and (not args.only or name in args.only.split(","))
-
-    # ---------------- fused Where->Select->Sum and plain Sum at 256M --------------------------
-    if want("linq_sum"):
-        s = ctx.empty(1, np.float64)
-        c = ctx.empty(1, np.int64)
-        f = lambda: ctx.where_select_sum_f32(chain, x, s, c, n)
-        f(); ctx.synchronize()
-        ms = time_launches(ctx, f, 20)
-        gbs = 4 * n / (ms * 1e-3) / 1e9
-        extra["where_select_sum_f32_256M"] = {"ms": round(ms, 4), "GB/s": round(gbs, 1), "count": int(c.to_host()[0]),
-                                               "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
-        log(f"[bench] where_select_sum 256M: {ms*1e3:.1f} us -> {gbs:.0f} GB/s")
-    if want("sum"):
-        s = ctx.empty(1, np.float64)
-        f = lambda: ctx.reduce_sum_f32(x, s, n)
-        f(); ctx.synchronize()
-        ms = time_launches(ctx, f, 20)
-        gbs = 4 * n / (ms * 1e-3) / 1e9
-        extra["sum_f32_256M"] = {"ms": round(ms, 4), "GB/s": round(gbs, 1),
-                                 "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
-        log(f"[bench] sum_f32 256M: {ms*1e3:.1f} us -> {gbs:.0f} GB/s")
-        xi = ctx.empty(n, np.int32)
-        ctx.fill_uniform_i32(xi, seed=43, stream=1)
-        si = ctx.empty(1, np.int64)
-        ov = ctx.empty(1, np.int32)
-        f = lambda: ctx.reduce_sum_i32(xi, si, ov, n)
-        f(); ctx.synchronize()
-        ms = time_launches(ctx, f, 20)
-        gbs = 4 * n / (ms * 1e-3) / 1e9
-        extra["sum_i32_256M"] = {"ms": round(ms, 4), "GB/s": round(gbs, 1),
-                                 "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
-        log(f"[bench] sum_i32 256M: {ms*1e3:.1f} us -> {gbs:.0f} GB/s")
-        ctx.free(xi)
-    if want("vector_add"):
-        for nv, label in ((100_000, "vector_add_f32_100K"), (n, "vector_add_f32_256M")):
-            a = x
-            b = ctx.empty(nv, np.float32)
-            ctx.fill_uniform_f32(b, seed=42, stream=1)
-            r = out
-            f = lambda: ctx.vector_add_f32(a, b, r, nv)
-            f(); ctx.synchronize()
-            ms = time_launches(ctx, f, 50 if nv < n else 20)
-            gbs = 12 * nv / (ms * 1e-3) / 1e9
-            extra[label] = {"ms": round(ms, 5), "GB/s": round(gbs, 1),
-                            "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
-            log(f"[bench] {label}: {ms*1e3:.2f} us -> {gbs:.0f} GB/s")
-            ctx.free(b)
-
     ctx.free(out)
     ctx.free(x)
-
-    # ---------------- dense MatMul -------------------------------------------------------------
-    if want("gemm"):
-        from bench_extras import bench_gemm  # noqa: E402
-
-        extra.update(bench_gemm(ctx, log, time_launches, roofline, FP32_MFMA_PEAK_TFLOPS, BF16_MFMA_PEAK_TFLOPS))
-    # ---------------- CSR SpMV x20 ---------------------------------------------------------------
-    if want("spmv"):
-        from bench_extras import bench_spmv  # noqa: E402
-
-        extra.update(bench_spmv(ctx, log, time_launches, roofline, HBM_PEAK_GBS))
 
     # ---------------- CPU baseline (oracle restatement, single thread) -------------------------
     cpu = None

@@ -22,6 +22,8 @@
 // equals LINQ-to-objects bit-for-bit.
 #include <algorithm>
 
+#include <utility>
+
 #include "dc_device.hpp"
 #include "dc_internal.hpp"
 
@@ -71,7 +73,7 @@ __device__ inline Instr fetch_instr(const dc_linq_chain& prog, int pc) {
 // which keeps the kernels at a higher occupancy. Operands are read in place (an immediate stays a
 // scalar operand of the vector instruction), so no per-element operand copy is materialised.
 template <int EPT, bool SAVES>
-__device__ inline uint32_t run_program(const dc_linq_chain& prog, float (&e)[EPT]) {
+__device__ __attribute__((always_inline)) inline uint32_t run_program(const dc_linq_chain& prog, float (&e)[EPT]) {
   float v[EPT];
   float s0[SAVES ? EPT : 1], s1[SAVES ? EPT : 1];
 #pragma unroll
@@ -424,7 +426,7 @@ __device__ inline uint32_t run_canon2(const Canon2& k, float (&e)[EPT]) {
 enum RoundsMode : int { kRrInterp = 0, kRrInterpSaves = 1, kRrF = 2, kRrM = 3, kRrFM = 4, kRrMF = 5 };
 
 template <int MODE, int EPT>
-__device__ inline uint32_t apply_rounds(const dc_linq_chain& prog, const Canon2& k, float (&e)[EPT]) {
+__device__ __attribute__((always_inline)) inline uint32_t apply_rounds(const dc_linq_chain& prog, const Canon2& k, float (&e)[EPT]) {
   if constexpr (MODE == kRrF) return run_canon2<kShapeF, EPT>(k, e);
   else if constexpr (MODE == kRrM) return run_canon2<kShapeM, EPT>(k, e);
   else if constexpr (MODE == kRrFM) return run_canon2<kShapeFM, EPT>(k, e);
@@ -612,6 +614,13 @@ constexpr int kRrMinRounds = 4;                          // below this the ticke
 static_assert((kRrDelay + 1) * kRrChunk <= kRrRing, "the ring holds every staged tile at 100% selectivity");
 static_assert(kRrDelay < 8 && kRrDelay >= 2, "per-tile LDS tables are indexed modulo 8");
 
+// Calls f(std::integral_constant<int, U>) for U = 0, 1, ... in order: a compile-time unrolled loop, so
+// the index into an array of register buffers is a constant.
+template <typename F, int... U>
+__device__ __attribute__((always_inline)) inline void for_each_index(F&& f, std::integer_sequence<int, U...>) {
+  (f(std::integral_constant<int, U>{}), ...);
+}
+
 // Count words of `round` for workgroups q*64 + lane (q < 4): four coalesced 256-byte loads.
 __device__ inline void rr_issue_counts(uint32_t (&c)[kRrCountsPerLane], const uint32_t* __restrict__ counts,
                                        uint32_t round, uint32_t P) {
@@ -718,7 +727,7 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
   uint32_t head = 0, tail = 0;
   const int64_t chunk = (int64_t)ww * kRrChunk;
 
-  auto load = [&](float (&e)[kRrEpt], uint32_t round) {
+  auto load = [&](float (&e)[kRrEpt], uint32_t round) __attribute__((always_inline)) {
     const dc::f32x4* in4 = reinterpret_cast<const dc::f32x4*>(in + ((int64_t)round * P + w) * kRrTile + chunk);
 #pragma unroll
     for (int j = 0; j < kRrVec; ++j) {
@@ -728,7 +737,7 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
   };
   // Ranks the kept elements of this wave's chunk (order: vector j, lane, slot k), appends them to the
   // ring, and publishes the tile count when this is the last worker wave to finish the tile.
-  auto stage = [&](float (&e)[kRrEpt], uint32_t keep, uint32_t r) {
+  auto stage = [&](float (&e)[kRrEpt], uint32_t keep, uint32_t r) __attribute__((always_inline)) {
     uint32_t run = 0, pos[kRrVec];
 #pragma unroll
     for (int j = 0; j < kRrVec; ++j) {
@@ -758,7 +767,7 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
     }
   };
   // Writes this wave's staged run of the tile of round q at its place in the output.
-  auto write = [&](uint32_t q, uint32_t parity) {
+  auto write = [&](uint32_t q, uint32_t parity) __attribute__((always_inline)) {
     const uint32_t slot = q & 7;
     uint32_t cnt = 0, before = 0;
 #pragma unroll
@@ -777,40 +786,29 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
   // path-insensitive: on a path that skipped a later load, the wait for the round being staged
   // would have to cover every load still in flight, draining the pipeline.
   const uint32_t last = R0 > 0 ? R0 - 1 : 0;
-  float e0[kRrEpt], e1[kRrEpt], e2[kRrEpt], e3[kRrEpt], e4[kRrEpt];
-  if (R0 > 0) {
-    load(e0, 0);
-    load(e1, min(1u, last));
-    load(e2, min(2u, last));
-    load(e3, min(3u, last));
-  }
+  constexpr int kBufs = kRrAhead + 1;
+  float e[kBufs][kRrEpt];  // register buffers: constant indices only, after full unrolling
+  if (R0 > 0)
+    for_each_index([&](auto U) __attribute__((always_inline)) { load(e[U.value], min((uint32_t)U.value, last)); },
+                   std::make_integer_sequence<int, kRrAhead>{});
   uint32_t r = 0;
-  // One round: issue the loads of round r + kRrAhead into EN, stage round r from EC, write round
-  // r - kRrDelay. Unrolled five ways so the register buffers rotate without copies. The main loop
-  // runs whole five-round iterations with no early exit: a `break` between rounds becomes a path
-  // back to the loop head after a partial iteration, and the waits at the head would then assume
-  // fewer loads in flight than the full iteration leaves. The last R0 % 5 rounds follow it.
-#define DC_RR_ROUND(EC, EN)                                                              \
-  {                                                                                      \
-    load(EN, min(r + kRrAhead, last));                                                   \
-    stage(EC, apply_rounds<MODE, kRrEpt>(prog, canon, EC), r);                              \
-    __syncthreads();                                                                     \
-    if (r >= (uint32_t)kRrDelay) write(r - kRrDelay, r & 1);                             \
-    ++r;                                                                                 \
-  }
-  static_assert(kRrAhead == 4, "five register buffers");
-  for (uint32_t it = R0 / 5; it > 0; --it) {
-    DC_RR_ROUND(e0, e4);
-    DC_RR_ROUND(e1, e0);
-    DC_RR_ROUND(e2, e1);
-    DC_RR_ROUND(e3, e2);
-    DC_RR_ROUND(e4, e3);
-  }
-  if (r < R0) DC_RR_ROUND(e0, e4);
-  if (r < R0) DC_RR_ROUND(e1, e0);
-  if (r < R0) DC_RR_ROUND(e2, e1);
-  if (r < R0) DC_RR_ROUND(e3, e2);
-#undef DC_RR_ROUND
+  // One round: issue the loads of round r + kRrAhead into buffer `en`, stage round r from `ec`,
+  // write round r - kRrDelay. Unrolled kBufs ways so the buffers rotate without copies. The main
+  // loop runs whole kBufs-round iterations with no early exit: a `break` between rounds becomes a
+  // path back to the loop head after a partial iteration, and the waits at the head would then
+  // assume fewer loads in flight than a full iteration leaves. The last R0 % kBufs rounds follow.
+  auto round = [&](float (&ec)[kRrEpt], float (&en)[kRrEpt]) __attribute__((always_inline)) {
+    load(en, min(r + kRrAhead, last));
+    stage(ec, apply_rounds<MODE, kRrEpt>(prog, canon, ec), r);
+    __syncthreads();
+    if (r >= (uint32_t)kRrDelay) write(r - kRrDelay, r & 1);
+    ++r;
+  };
+  for (uint32_t it = R0 / kBufs; it > 0; --it)
+    for_each_index([&](auto U) __attribute__((always_inline)) { round(e[U.value], e[(U.value + kRrAhead) % kBufs]); },
+                   std::make_integer_sequence<int, kBufs>{});
+  for_each_index([&](auto U) __attribute__((always_inline)) { if (r < R0) round(e[U.value], e[(U.value + kRrAhead) % kBufs]); },
+                 std::make_integer_sequence<int, kRrAhead>{});
   for (; r < rounds; ++r) {  // drain: the last kRrDelay staged tiles
     __syncthreads();
     write(r - kRrDelay, r & 1);
