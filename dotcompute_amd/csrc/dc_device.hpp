@@ -118,4 +118,12 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 __device__ inline f32x4 load_stream(const f32x4* p) { return __builtin_nontemporal_load(p); }
 __device__ inline i32x4 load_stream(const i32x4* p) { return __builtin_nontemporal_load(p); }
 
+// Buffer resource over [p, p + bytes) (bytes < 4 GiB): loads past the end return 0 and stores past
+// it are dropped by the hardware range check, without touching memory, so code can issue a fixed
+// set of accesses with no branches around them.
+__device__ inline __amdgpu_buffer_rsrc_t range_rsrc(const void* p, int32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
+}
+constexpr int kBufNt = 2;  // buffer cache policy: non-temporal (streamed once)
+
 }  // namespace dc

@@ -610,12 +610,10 @@ __device__ inline float lds_seq_sum(const float* __restrict__ p, int32_t i0, int
   return sum;
 }
 
-// Buffer resource over [p, p + bytes): loads past the end return 0 and stores past it are dropped
-// by the hardware range check, so a window's loads and stores need no branches.
-__device__ inline __amdgpu_buffer_rsrc_t range_rsrc(const void* p, int32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
-}
-constexpr int kNt = 2;                   // cache policy: non-temporal (streamed once)
+// Buffer resources (dc::range_rsrc): loads past a range's end return 0 and stores past it are
+// dropped by the hardware range check, so a window's loads and stores need no branches.
+using dc::range_rsrc;
+constexpr int kNt = dc::kBufNt;
 constexpr uint32_t kDrop = 0x80000000u;  // a buffer offset past any range: the access is dropped
 constexpr int kChunksW = kSpan / 256;    // 16-byte loads per lane covering a window's span
 constexpr int kSegChunks = (kWW + 1 + 255) / 256;  // ... and its segment starts plus the end
