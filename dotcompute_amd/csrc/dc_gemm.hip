@@ -21,6 +21,9 @@
 // the blocks resident on one XCD share A row-panels and B column-panels in that XCD's L2.
 #include <algorithm>
 
+#include <cstddef>
+#include <type_traits>
+
 #include "dc_device.hpp"
 #include "dc_internal.hpp"
 
@@ -347,52 +350,53 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_bf16_kernel(const unsigned s
 // bf16, large tiles: C = A·B with B first transposed to Bt[n][k] (a separate pass, so both
 // operands are k-contiguous and every global load and LDS access is 16 bytes wide).
 //
-// Macro tile 256×256, BK = 64, double-buffered LDS (2 × (256 + 256) rows × 72 bf16 = 144 KiB,
-// one workgroup per CU). WAVES = 8: 512 threads as 2×4 waves of 128×64 (4×2 MFMA 32×32×16 tiles,
-// 128 accumulators per lane), two waves per SIMD so one's LDS and barrier waits overlap the
-// other's MFMAs. Row pitch 72 bf16 = 144 B: the eight 16-byte reads of one LDS cycle (rows
-// r..r+7) land on disjoint banks. Each k step (16 wide) is one scheduling region: its MFMAs with
-// the next step's LDS reads spread between them; the next tile's global loads go out with the
-// first step and its LDS writes with the last.
+// Macro tile 256×256, BK = 64, double-buffered LDS (2 × (256 + 256) rows × 128 B = 128 KiB, one
+// workgroup per CU). 512 threads as 2×4 waves of 128×64 (4×2 MFMA 32×32×16 tiles, 128
+// accumulators per lane), two waves per SIMD so one's LDS and barrier waits overlap the other's
+// MFMAs.
+//
+// Global -> LDS: direct-to-LDS loads (global_load_lds_dwordx4): lane L of a wave's load writes
+// LDS bytes 16·L of a 1 KiB block (8 rows of 128 B), so no registers stage the tile and a tile's
+// loads can stay in flight for a whole tile of MFMAs. Rows are unpadded; the 16-byte k-octet q of
+// row R sits in slot q ^ ((R >> 1) & 7) of the row, so a fragment read (rows R0..R0+15 at one
+// octet for each 16 lanes) touches 16 distinct 16-byte bank groups. The swizzle is applied on the
+// global side: each lane fetches the octet that belongs in its slot.
+//
+// Pipeline of tile kt (buffer kt & 1): steps 0..2 run their MFMAs with the next step's fragment
+// reads between them; then the tile's one barrier (which also waits for tile kt+1's loads, issued
+// a tile earlier); right after it the loads of tile kt+2 go out into the buffer tile kt just
+// finished with, and the last step's MFMAs run with tile kt+1's step-0 fragment reads between
+// them, so no LDS latency is exposed after the barrier.
 // ---------------------------------------------------------------------------------------------
-constexpr int kBM2 = 256, kBN2 = 256, kBK2 = 64, kPitch2 = kBK2 + 8;
+constexpr int kBM2 = 256, kBN2 = 256, kBK2 = 64;
 constexpr int kBigThreads = 512;
 constexpr int kWaveM = 128, kWaveN = 64;       // wave tile
 constexpr int kMT = kWaveM / 32, kNT = kWaveN / 32;
+constexpr int kRowElems = kBK2;                // bf16 per LDS row (128 B, unpadded)
 
 struct Bf16BigSmem {
-  unsigned short a[2][kBM2][kPitch2];
-  unsigned short b[2][kBN2][kPitch2];
+  unsigned short a[2][kBM2 * kRowElems];
+  unsigned short b[2][kBN2 * kRowElems];
 };
 
-// One BK slice of A (256 rows) and Bt (256 rows), 8 bf16 per 16-byte slot: slot s -> row s / 8,
-// k-octet s % 8; 2048 slots per operand.
-struct Bf16BigLoader {
-  static constexpr int kSlots = kBM2 * kBK2 / 8 / kBigThreads;
-  u16x8 ra[kSlots];
-  u16x8 rb[kSlots];
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-  __device__ inline void load(const unsigned short* __restrict__ A, const unsigned short* __restrict__ Bt, int K,
-                              int m0, int n0, int k0, int tid) {
+// Issues the direct-to-LDS loads of one BK slice (columns k0..k0+63) of the workgroup's A panel
+// (rows m0..m0+255, buffer resource `ra`) and Bt panel (`rb`) into LDS buffer `buf`. Wave w's load
+// i fills LDS rows 8·(8i + w) .. +7 (1 KiB); lane L takes row 8·(8i + w) + L / 8 and slot L % 8,
+// i.e. k-octet (L % 8) ^ ((row >> 1) % 8) of that row. `voff` is the lane's byte offset
+// ((L / 8)·K + 8·octet)·2 (row >> 1 depends on w and L only); the row block and k0 are uniform.
+template <int BUF>
+__device__ inline void bf16_tile_to_lds(Bf16BigSmem& sm, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb, int K,
+                                        int k0, int wave, uint32_t voff) {
 #pragma unroll
-    for (int i = 0; i < kSlots; ++i) {
-      const int s = tid + i * kBigThreads;
-      const int row = s >> 3, kq = s & 7;
-      ra[i] = *reinterpret_cast<const u16x8*>(A + (size_t)(m0 + row) * K + k0 + 8 * kq);
-      rb[i] = *reinterpret_cast<const u16x8*>(Bt + (size_t)(n0 + row) * K + k0 + 8 * kq);
-    }
+  for (int i = 0; i < kBM2 / 64; ++i) {
+    const int row0 = 8 * (8 * i + wave);
+    const int32_t soff = (row0 * K + k0) * (int32_t)sizeof(unsigned short);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)&sm.a[BUF][row0 * kRowElems], 16, voff, soff, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)&sm.b[BUF][row0 * kRowElems], 16, voff, soff, 0, 0);
   }
-
-  __device__ inline void store(Bf16BigSmem& sm, int buf, int tid) {
-#pragma unroll
-    for (int i = 0; i < kSlots; ++i) {
-      const int s = tid + i * kBigThreads;
-      const int row = s >> 3, kq = s & 7;
-      *reinterpret_cast<u16x8*>(&sm.a[buf][row][8 * kq]) = ra[i];
-      *reinterpret_cast<u16x8*>(&sm.b[buf][row][8 * kq]) = rb[i];
-    }
-  }
-};
+}
 
 __global__ __launch_bounds__(kBigThreads, 1) void gemm_bf16_big_kernel(const unsigned short* __restrict__ A,
                                                                        const unsigned short* __restrict__ Bt,
@@ -402,9 +406,28 @@ __global__ __launch_bounds__(kBigThreads, 1) void gemm_bf16_big_kernel(const uns
   Bf16BigSmem& sm = *reinterpret_cast<Bf16BigSmem*>(smem_raw);
   const TileCoord tc = map_tile(tiles_m, tiles_n);
   const int m0 = tc.tm * kBM2, n0 = tc.tn * kBN2;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // wave index in a scalar register: the loads' LDS bases and scalar offsets derive from it
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / (kBN2 / kWaveN), wn = wave % (kBN2 / kWaveN);
   const int r = lane & 31, h = lane >> 5;
+  // load side: panels as buffer ranges (256 rows of K bf16 < 2 GiB, checked by the host)
+  const int32_t panel_bytes = kBM2 * K * (int32_t)sizeof(unsigned short);
+  const auto ra = dc::range_rsrc(A + (size_t)m0 * K, panel_bytes);
+  const auto rb = dc::range_rsrc(Bt + (size_t)n0 * K, panel_bytes);
+  const int lrow = lane >> 3;
+  const int lswz = ((8 * wave + lrow) >> 1) & 7;  // (row >> 1) % 8 for rows 8·(8i + w) + lrow, any i
+  const uint32_t voff = (uint32_t)((lrow * K + 8 * ((lane & 7) ^ lswz)) * (int)sizeof(unsigned short));
+  // read side: fragment rows R = 32·t + r (t: wave and tile offsets, multiples of 32), so the
+  // swizzle is (r >> 1) % 8; k-octet 2·step + h. Byte offsets of step s in buffer 0 of a and b
+  // (buffer, mt and nt offsets are immediates).
+  const int rswz = (r >> 1) & 7;
+  uint32_t aoff[4], boff[4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    const uint32_t slot = 16u * (uint32_t)((2 * st + h) ^ rswz);
+    aoff[st] = (uint32_t)(wm * kWaveM + r) * (kRowElems * 2) + slot;
+    boff[st] = (uint32_t)offsetof(Bf16BigSmem, b) + (uint32_t)(wn * kWaveN + r) * (kRowElems * 2) + slot;
+  }
 
   f32x16 acc[kMT][kNT];
 #pragma unroll
@@ -414,55 +437,67 @@ __global__ __launch_bounds__(kBigThreads, 1) void gemm_bf16_big_kernel(const uns
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  Bf16BigLoader ld;
+  constexpr int kSteps = kBK2 / 16, kReads = kMT + kNT;
+  static_assert(kSteps == 4, "four 16-wide k steps per tile");
   const int kt_count = K / kBK2;
-  ld.load(A, Bt, K, m0, n0, 0, tid);
-  ld.store(sm, 0, tid);
-  __syncthreads();
+  bf16_tile_to_lds<0>(sm, ra, rb, K, 0, wave, voff);
+  __syncthreads();  // waits for the loads of tile 0 (workgroup release of the LDS writes)
+  if (kt_count > 1) bf16_tile_to_lds<1>(sm, ra, rb, K, kBK2, wave, voff);
 
-  auto read_frags = [&](int buf, int ks, bf16x8* a, bf16x8* b) {
+  const unsigned char* lds = smem_raw;
+  auto read_frags = [&](auto BUF, int step, bf16x8* a, bf16x8* b) __attribute__((always_inline)) {
+    constexpr uint32_t kBuf = (uint32_t)decltype(BUF)::value * kBM2 * kRowElems * 2;
 #pragma unroll
     for (int mt = 0; mt < kMT; ++mt)
-      a[mt] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(&sm.a[buf][wm * kWaveM + mt * 32 + r][ks + 8 * h]));
+      a[mt] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(lds + aoff[step] + kBuf + mt * 32 * kRowElems * 2));
 #pragma unroll
     for (int nt = 0; nt < kNT; ++nt)
-      b[nt] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(&sm.b[buf][wn * kWaveN + nt * 32 + r][ks + 8 * h]));
+      b[nt] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(lds + boff[step] + kBuf + nt * 32 * kRowElems * 2));
   };
-  constexpr int kSteps = kBK2 / 16, kMfma = kMT * kNT, kReads = kMT + kNT;
-  for (int kt = 0; kt < kt_count; ++kt) {
-    const int buf = kt & 1;
-    const bool more = kt + 1 < kt_count;
-    bf16x8 fa[2][kMT], fb[2][kNT];
-    read_frags(buf, 0, fa[0], fb[0]);
+  auto mfmas = [&](const bf16x8* a, const bf16x8* b) __attribute__((always_inline)) {
 #pragma unroll
-    for (int step = 0; step < kSteps; ++step) {
-      const int cur = step & 1;
-      __builtin_amdgcn_sched_barrier(0);
-      if (step == 0 && more) ld.load(A, Bt, K, m0, n0, (kt + 1) * kBK2, tid);
-      if (step + 1 < kSteps) read_frags(buf, 16 * (step + 1), fa[cur ^ 1], fb[cur ^ 1]);
-      if (step + 1 == kSteps && more) ld.store(sm, buf ^ 1, tid);
+    for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
-      for (int mt = 0; mt < kMT; ++mt)
+      for (int nt = 0; nt < kNT; ++nt)
+        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[mt], b[nt], acc[mt][nt], 0, 0, 0);
+  };
+  // One LDS read after each of the first kReads MFMAs of the region (the rest run back to back).
+  auto interleave_reads = []() __attribute__((always_inline)) {
 #pragma unroll
-        for (int nt = 0; nt < kNT; ++nt)
-          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cur][mt], fb[cur][nt], acc[mt][nt], 0, 0, 0);
-      if (step + 1 < kSteps) {
-#pragma unroll
-        for (int i = 0; i < kReads; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < kMfma; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // 1 LDS write
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
+    for (int i = 0; i < kReads; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
     }
-    __syncthreads();
+  };
+  bf16x8 fa[2][kMT], fb[2][kNT];
+  read_frags(std::integral_constant<int, 0>{}, 0, fa[0], fb[0]);
+  // Tile kt in LDS buffer BUF = kt % 2 (the loop is unrolled by two, so buffer offsets are
+  // constants; a macro rather than a lambda keeps the fragment arrays plain registers).
+#define DC_BF16_TILE(BUF, KT)                                                                      \
+  {                                                                                                \
+    _Pragma("unroll") for (int step = 0; step + 1 < kSteps; ++step) {                              \
+      const int cur = step & 1;                                                                    \
+      __builtin_amdgcn_sched_barrier(0);                                                           \
+      read_frags(std::integral_constant<int, BUF>{}, step + 1, fa[cur ^ 1], fb[cur ^ 1]);          \
+      mfmas(fa[cur], fb[cur]);                                                                     \
+      interleave_reads();                                                                          \
+      __builtin_amdgcn_sched_barrier(0);                                                           \
+    }                                                                                              \
+    /* tile KT+1 is in LDS; every wave is done reading buffer BUF (after the last tile the */     \
+    /* barrier and the reads of the other buffer are harmless and unused) */                      \
+    __syncthreads();                                                                               \
+    if ((KT) + 2 < kt_count) bf16_tile_to_lds<BUF>(sm, ra, rb, K, ((KT) + 2) * kBK2, wave, voff);   \
+    __builtin_amdgcn_sched_barrier(0);                                                             \
+    read_frags(std::integral_constant<int, 1 - (BUF)>{}, 0, fa[0], fb[0]);                         \
+    mfmas(fa[1], fb[1]);                                                                           \
+    interleave_reads();                                                                            \
+    __builtin_amdgcn_sched_barrier(0);                                                             \
   }
+  for (int kt = 0; kt < kt_count; kt += 2) {
+    DC_BF16_TILE(0, kt);
+    if (kt + 1 < kt_count) DC_BF16_TILE(1, kt + 1);
+  }
+#undef DC_BF16_TILE
 
   // acc[mt][nt][v] holds C[row][col], row = 8*(v/4) + 4*h + v%4, col = r (within the 32×32 tile).
 #pragma unroll
@@ -573,7 +608,8 @@ DC_HIP_API int32_t dc_hip_gemm_bf16(dc_hip_ctx* ctx, const uint16_t* a, const ui
   const unsigned grid = (unsigned)(tiles_m * tiles_n);
   const unsigned short* A = reinterpret_cast<const unsigned short*>(a);
   const unsigned short* B = reinterpret_cast<const unsigned short*>(b);
-  if ((m % kBM2 == 0) && (n % kBN2 == 0) && (k % kBK2 == 0) && dc::aligned16(a) && dc::aligned16(b)) {
+  if ((m % kBM2 == 0) && (n % kBN2 == 0) && (k % kBK2 == 0) && dc::aligned16(a) && dc::aligned16(b) &&
+      (int64_t)k * kBM2 * 2 < ((int64_t)1 << 31)) {  // the panel buffer ranges: 256 rows of k bf16 < 2 GiB
     // large tiles: B transposed into context scratch first
     DC_RETURN_IF(dc::ensure_gemm_scratch(ctx, (size_t)n * (size_t)k * sizeof(unsigned short)));
     unsigned short* Bt = static_cast<unsigned short*>(ctx->gemm_scratch);
