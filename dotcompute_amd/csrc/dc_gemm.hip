@@ -56,6 +56,180 @@ __device__ inline TileCoord map_tile(int tiles_m, int tiles_n) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// fp32, full tiles (m, n multiples of T, k a multiple of 32): direct-to-LDS loads, no staging
+// registers and no transposing LDS stores.
+//   A tile [T rows][32 k] (128 B rows, unpadded): the 16-byte k-quad q of row R sits in slot
+//   q ^ ((R >> 1) & 7), so a fragment read (16 lanes = rows R0..R0+15 at one quad) touches 16
+//   distinct 16-byte bank groups.
+//   B tile [32 k][T n] in its natural row-major layout: the n-quad Q of k-row k sits at quad
+//   Q ^ (8·((k >> 3) & 1)). Lane (r, h) of MFMA step kk reads B[ks + 8h + kk][n = r] with a 4-byte
+//   LDS load: the h = 0 and h = 1 halves read rows 8 apart and land in opposite 128-byte halves of
+//   the bank window.
+// A wave's direct-to-LDS load writes 1 KiB (lane L -> bytes 16·L): the swizzles are applied on
+// the global side (each lane fetches the quad that belongs in its slot).
+// Pipeline as in the bf16 large-tile kernel: step 0 (k 0..15) runs its MFMAs with step 1's
+// fragment reads between them; then the tile's one barrier (which also waits for tile kt+1's
+// loads, issued a tile earlier); the loads of tile kt+2 go out into the buffer tile kt finished
+// with, and step 1's MFMAs run with tile kt+1's step-0 fragment reads between them.
+// ---------------------------------------------------------------------------------------------
+constexpr int kBKd = 32;
+
+// One LDS buffer per (operand, stage) as a separate __shared__ object, so the compiler can tell that
+// loads into one stage's buffers do not alias reads of the other's (and need no wait before them).
+template <int T>
+struct F32DmaSmem {
+  float* a[2];
+  float* b[2];
+};
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Waits until this wave's direct-to-LDS loads have landed (vmcnt(0); expcnt and lgkmcnt left
+// alone), then the workgroup barrier: after it every wave's loads issued before are visible.
+__device__ inline void dma_barrier() {
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // gfx9 encoding: vmcnt = 0, expcnt = 7, lgkmcnt = 15
+  __syncthreads();
+}
+
+template <int T, int BUF>
+__device__ inline void f32_tile_to_lds(const F32DmaSmem<T>& sm, __amdgpu_buffer_rsrc_t ra, const float* __restrict__ B, int N,
+                                       int K, int n0, int k0, int wave, uint32_t avoff, const uint32_t (&bvoff)[T / 32]) {
+  // A: T/8 blocks of 8 rows; wave w issues blocks w, w + 4, ...
+#pragma unroll
+  for (int i = 0; i < T / 32; ++i) {
+    const int row0 = 8 * (4 * i + wave);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(sm.a[BUF] + row0 * kBKd), 16, avoff,
+                                             (row0 * K + k0) * (int)sizeof(float), 0, 0);
+  }
+  // B: T/8 blocks of 256/T k-rows (this k slice only, as its own buffer range)
+  const auto rb = dc::range_rsrc(B + (size_t)k0 * N + n0, ((kBKd - 1) * N + T) * (int)sizeof(float));
+  constexpr int kRowsPerBlock = 256 / T;
+#pragma unroll
+  for (int i = 0; i < T / 32; ++i) {
+    const int krow0 = kRowsPerBlock * (4 * i + wave);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)(sm.b[BUF] + krow0 * T), 16, bvoff[i],
+                                             krow0 * N * (int)sizeof(float), 0, 0);
+  }
+}
+
+template <int T>
+__global__ __launch_bounds__(kThreads, 2) void gemm_f32_dma_kernel(const float* __restrict__ A,
+                                                                   const float* __restrict__ B, float* __restrict__ C,
+                                                                   int M, int N, int K, int tiles_m, int tiles_n) {
+  constexpr int kW = T / 2, kMT = T / 64;  // wave tile edge, MFMA tiles per wave edge
+  constexpr int kQuads = T / 4;            // n-quads per B row
+  __shared__ __align__(16) float lds_a0[T * kBKd], lds_a1[T * kBKd], lds_b0[kBKd * T], lds_b1[kBKd * T];
+  const F32DmaSmem<T> sm{{lds_a0, lds_a1}, {lds_b0, lds_b1}};
+  const TileCoord tc = map_tile(tiles_m, tiles_n);
+  const int m0 = tc.tm * T, n0 = tc.tn * T;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int r = lane & 31, h = lane >> 5;
+
+  // load side: A panel as a buffer range (T rows of K floats < 2 GiB, checked by the host)
+  const auto ra = dc::range_rsrc(A + (size_t)m0 * K, T * K * (int)sizeof(float));
+  // A block 4i + w holds rows 8(4i + w) + L/8: (row >> 1) & 7 = (4·(w & 1) + L/16) & 7
+  const uint32_t avoff =
+      (uint32_t)(((lane >> 3) * K + 4 * ((lane & 7) ^ ((4 * (wave & 1) + (lane >> 4)) & 7))) * (int)sizeof(float));
+  uint32_t bvoff[T / 32];
+#pragma unroll
+  for (int i = 0; i < T / 32; ++i) {
+    const int kr = lane / kQuads;                        // k-row within the block
+    const int k = (256 / T) * (4 * i + wave) + kr;       // k-row within the slice
+    const int q = (lane % kQuads) ^ (8 * ((k >> 3) & 1));
+    bvoff[i] = (uint32_t)((kr * N + 4 * q) * (int)sizeof(float));
+  }
+
+  f32x16 acc[kMT][kMT];
+#pragma unroll
+  for (int i = 0; i < kMT; ++i)
+#pragma unroll
+    for (int j = 0; j < kMT; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  const int kt_count = K / kBKd;
+  f32_tile_to_lds<T, 0>(sm, ra, B, N, K, n0, 0, wave, avoff, bvoff);
+  dma_barrier();
+  if (kt_count > 1) f32_tile_to_lds<T, 1>(sm, ra, B, N, K, n0, kBKd, wave, avoff, bvoff);
+
+  // Fragments of one 16-wide k step: A quads (2 per MFMA tile row block), B scalars (8 per column block).
+  const int aswz = (r >> 1) & 7;
+  auto read_frags = [&](auto BUF, int ks, dc::f32x4 (&a)[kMT][2], float (&b)[kMT][8]) __attribute__((always_inline)) {
+    constexpr int kB = decltype(BUF)::value;
+#pragma unroll
+    for (int mt = 0; mt < kMT; ++mt)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        a[mt][j] = *reinterpret_cast<const dc::f32x4*>(
+            &(kB ? lds_a1 : lds_a0)[(wm * kW + mt * 32 + r) * kBKd + 4 * ((ks / 4 + 2 * h + j) ^ aswz)]);
+#pragma unroll
+    for (int nt = 0; nt < kMT; ++nt) {
+      const int n = wn * kW + nt * 32 + r;
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk)
+        b[nt][kk] = (kB ? lds_b1 : lds_b0)[(ks + 8 * h + kk) * T + 4 * ((n >> 2) ^ (8 * h)) + (n & 3)];
+    }
+  };
+  auto mfmas = [&](const dc::f32x4 (&a)[kMT][2], const float (&b)[kMT][8]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+      for (int mt = 0; mt < kMT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < kMT; ++nt)
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[mt][kk >> 2][kk & 3], b[nt][kk], acc[mt][nt], 0, 0, 0);
+  };
+  constexpr int kReads = 2 * kMT + 8 * kMT;  // LDS reads per step
+  auto interleave_reads = []() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < kReads; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+    }
+  };
+  dc::f32x4 fa0[kMT][2], fa1[kMT][2];
+  float fb0[kMT][8], fb1[kMT][8];
+  read_frags(std::integral_constant<int, 0>{}, 0, fa0, fb0);
+  // Tile KT in LDS buffer BUF = KT % 2 (unrolled by two so buffer offsets are constants; a macro
+  // keeps the fragment arrays plain registers). After the last tile the barrier and the reads of
+  // the other buffer are harmless and unused.
+#define DC_F32_TILE(BUF, KT)                                                                      \
+  {                                                                                               \
+    __builtin_amdgcn_sched_barrier(0);                                                            \
+    read_frags(std::integral_constant<int, BUF>{}, 16, fa1, fb1);                                 \
+    mfmas(fa0, fb0);                                                                              \
+    interleave_reads();                                                                           \
+    __builtin_amdgcn_sched_barrier(0);                                                            \
+    dma_barrier(); /* tile KT+1 is in LDS; every wave is done reading buffer BUF */               \
+    if ((KT) + 2 < kt_count) f32_tile_to_lds<T, BUF>(sm, ra, B, N, K, n0, ((KT) + 2) * kBKd, wave, avoff, bvoff); \
+    __builtin_amdgcn_sched_barrier(0);                                                            \
+    read_frags(std::integral_constant<int, 1 - (BUF)>{}, 0, fa0, fb0);                            \
+    mfmas(fa1, fb1);                                                                              \
+    interleave_reads();                                                                           \
+    __builtin_amdgcn_sched_barrier(0);                                                            \
+  }
+  for (int kt = 0; kt < kt_count; kt += 2) {
+    DC_F32_TILE(0, kt);
+    if (kt + 1 < kt_count) DC_F32_TILE(1, kt + 1);
+  }
+#undef DC_F32_TILE
+
+  // acc[mt][nt][v] holds C[row][col], row = 8*(v/4) + 4*h + v%4, col = r (within the 32×32 tile).
+#pragma unroll
+  for (int mt = 0; mt < kMT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < kMT; ++nt) {
+      const int col = n0 + wn * kW + nt * 32 + r;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int row = m0 + wm * kW + mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+        C[(size_t)row * N + col] = acc[mt][nt][v];
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
 // fp32. T = macro tile (128, or 64 when 128-tiles cannot occupy the CUs: 1024² has only 64 of
 // them); 4 waves as 2×2, each wave (T/2)×(T/2) = (T/64)×(T/64) MFMA 32×32 tiles.
 // ---------------------------------------------------------------------------------------------
@@ -379,7 +553,6 @@ struct Bf16BigSmem {
   unsigned short b[2][kBN2 * kRowElems];
 };
 
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 // Issues the direct-to-LDS loads of one BK slice (columns k0..k0+63) of the workgroup's A panel
 // (rows m0..m0+255, buffer resource `ra`) and Bt panel (`rb`) into LDS buffer `buf`. Wave w's load
@@ -441,7 +614,7 @@ __global__ __launch_bounds__(kBigThreads, 1) void gemm_bf16_big_kernel(const uns
   static_assert(kSteps == 4, "four 16-wide k steps per tile");
   const int kt_count = K / kBK2;
   bf16_tile_to_lds<0>(sm, ra, rb, K, 0, wave, voff);
-  __syncthreads();  // waits for the loads of tile 0 (workgroup release of the LDS writes)
+  dma_barrier();
   if (kt_count > 1) bf16_tile_to_lds<1>(sm, ra, rb, K, kBK2, wave, voff);
 
   const unsigned char* lds = smem_raw;
@@ -485,7 +658,7 @@ __global__ __launch_bounds__(kBigThreads, 1) void gemm_bf16_big_kernel(const uns
     }                                                                                              \
     /* tile KT+1 is in LDS; every wave is done reading buffer BUF (after the last tile the */     \
     /* barrier and the reads of the other buffer are harmless and unused) */                      \
-    __syncthreads();                                                                               \
+    dma_barrier();                                                                                 \
     if ((KT) + 2 < kt_count) bf16_tile_to_lds<BUF>(sm, ra, rb, K, ((KT) + 2) * kBK2, wave, voff);   \
     __builtin_amdgcn_sched_barrier(0);                                                             \
     read_frags(std::integral_constant<int, 1 - (BUF)>{}, 0, fa[0], fb[0]);                         \
@@ -584,16 +757,21 @@ DC_HIP_API int32_t dc_hip_gemm_f32(dc_hip_ctx* ctx, const float* a, const float*
   const int T = small ? 64 : 128;
   const int tiles_m = (int)((m + T - 1) / T), tiles_n = (int)((n + T - 1) / T);
   const unsigned grid = (unsigned)(tiles_m * tiles_n);
-  const bool full = (m % T == 0) && (n % T == 0) && (k % kBKf32 == 0) && dc::aligned16(a) && dc::aligned16(b);
-#define DC_GEMM_F32(CHECKED, TT)                                                                                   \
-  gemm_f32_kernel<kBKf32, CHECKED, TT><<<grid, kThreads, 0, ctx->stream>>>(a, b, c, (int)m, (int)n, (int)k, tiles_m, \
-                                                                          tiles_n)
+  // full tiles take the direct-to-LDS kernel; its A panel (T rows of k floats) is one buffer range
+  const bool full = (m % T == 0) && (n % T == 0) && (k % kBKd == 0) && dc::aligned16(a) && dc::aligned16(b) &&
+                    (int64_t)T * k * 4 < ((int64_t)1 << 31) && ((int64_t)kBKd * n + T) * 4 < ((int64_t)1 << 31);
+#define DC_GEMM_F32_DMA(TT) \
+  gemm_f32_dma_kernel<TT><<<grid, kThreads, 0, ctx->stream>>>(a, b, c, (int)m, (int)n, (int)k, tiles_m, tiles_n)
+#define DC_GEMM_F32_CHECKED(TT)                                                                                 \
+  gemm_f32_kernel<kBKf32, true, TT><<<grid, kThreads, 0, ctx->stream>>>(a, b, c, (int)m, (int)n, (int)k, tiles_m, \
+                                                                       tiles_n)
   if (small) {
-    if (full) DC_GEMM_F32(false, 64); else DC_GEMM_F32(true, 64);
+    if (full) DC_GEMM_F32_DMA(64); else DC_GEMM_F32_CHECKED(64);
   } else {
-    if (full) DC_GEMM_F32(false, 128); else DC_GEMM_F32(true, 128);
+    if (full) DC_GEMM_F32_DMA(128); else DC_GEMM_F32_CHECKED(128);
   }
-#undef DC_GEMM_F32
+#undef DC_GEMM_F32_DMA
+#undef DC_GEMM_F32_CHECKED
   return dc::last_launch_status();
 }
 

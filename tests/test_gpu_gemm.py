@@ -70,6 +70,17 @@ def test_gemm_f32_full_tiles(ctx, shape):
     check_rows(c, a, b, np.arange(m))
 
 
+# Full-tile shapes run the direct-to-LDS kernel (64-tiles below 2 * CUs 128-tiles, else 128-tiles);
+# these cover one, two and an odd number of 32-wide k tiles for both tile sizes.
+@pytest.mark.parametrize("shape", [(128, 128, 32), (192, 320, 96), (256, 64, 64), (4096, 2048, 32),
+                                   (2048, 4096, 64), (4096, 2048, 96)])
+def test_gemm_f32_k_tile_counts(ctx, shape):
+    m, n, k = shape
+    a, b = make_inputs(m, n, k)
+    c = run_gemm(ctx, a, b)
+    check_rows(c, a, b, np.arange(m))
+
+
 def test_gemm_f32_reference_case_vs_fp32_loop(ctx):
     """CudaRealWorldAlgorithmTests.cs:56-96: m=512, n=768, k=384, abs tol 1e-3 vs the fp32 triple loop."""
     m, n, k = 512, 768, 384
