@@ -8,7 +8,7 @@ order-preserving compaction kernel. Throughput = algorithmic bytes (4 B read per
 4 B written per kept element) / wall time per step.
 
 Also reported (outside the timed steps, each with its own roofline): Sum f32 / i32 at 256M, the
-fused Where->Select->Sum at 256M, VectorAdd at N=100,000 and 256M, dense fp32 and bf16 MatMul,
+fused Where->Select->Sum and ->Min/Max at 256M, VectorAdd at N=100,000 and 256M, dense fp32 and bf16 MatMul,
 CSR SpMV x20. These legs run first and the headline's W warmup + K timed steps run after them. The CPU baseline is the oracle's single-thread LINQ-to-objects restatement of the
 headline chain, timed on this host.
 
@@ -88,7 +88,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--skip-extras", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of extras to run (sum,linq_sum,vector_add,gemm,spmv)")
+    ap.add_argument("--only", default="", help="comma list of extras to run (sum,linq_sum,linq_minmax,vector_add,gemm,spmv)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one 1 GiB device-to-device copy, the known-size reference for the HBM byte "
                          "counters (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) that give roofline.traffic")
@@ -148,6 +148,18 @@ def main() -> int:
         extra["where_select_sum_f32_256M"] = {"ms": round(ms, 4), "GB/s": round(gbs, 1), "count": int(c.to_host()[0]),
                                                "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
         log(f"[bench] where_select_sum 256M: {ms*1e3:.1f} us -> {gbs:.0f} GB/s")
+    if want("linq_minmax"):
+        mv = ctx.empty(1, np.float32)
+        mc = ctx.empty(1, np.int64)
+        for name, op in (("min", hip.LINQ_MIN), ("max", hip.LINQ_MAX)):
+            f = lambda: ctx.where_select_minmax_f32(chain, x, op, mv, mc, n)
+            f(); ctx.synchronize()
+            ms = time_launches(ctx, f, 20, warm_ms=LEG_WARM_MS)
+            gbs = 4 * n / (ms * 1e-3) / 1e9
+            extra[f"where_select_{name}_f32_256M"] = {"ms": round(ms, 4), "GB/s": round(gbs, 1),
+                                                      "value": float(mv.to_host()[0]),
+                                                      "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
+            log(f"[bench] where_select_{name} 256M: {ms*1e3:.1f} us -> {gbs:.0f} GB/s")
     if want("sum"):
         s = ctx.empty(1, np.float64)
         f = lambda: ctx.reduce_sum_f32(x, s, n)

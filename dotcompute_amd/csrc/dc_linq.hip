@@ -916,6 +916,169 @@ __global__ __launch_bounds__(kFinalBlock) void where_select_sum_pass2(const doub
   }
 }
 
+// ---- Where/Select -> Min / Max ------------------------------------------------------------------
+// Same two-pass shape as the sum. The BCL's enumerator loops (Min: the first NaN, else the first
+// smallest element; Max: NaNs skipped, the first largest, the last NaN when all are NaN) depend on
+// the order only through ties, so every partial carries the sequence index of its candidate and the
+// combination breaks ties by index. That combination is commutative and associative, so the grid's
+// result is the enumerator's bit for bit (signed zeros and NaN payloads included), whatever the
+// order in which lanes, waves and workgroups meet. An index of -1 marks "no element yet".
+enum MinMaxOp : int { kOpMin = DC_LINQ_MIN, kOpMax = DC_LINQ_MAX };
+
+template <int OP>
+__device__ inline void mm_take(float& v, int64_t& i, float cv, int64_t ci) {
+  if (ci < 0) return;
+  bool take;
+  if (i < 0) {
+    take = true;
+  } else {
+    const bool vn = __builtin_isnan(v), cn = __builtin_isnan(cv);
+    if (OP == kOpMin) {
+      take = (vn || cn) ? (cn && (!vn || ci < i))           // the first NaN wins
+                        : (cv < v || (cv == v && ci < i));  // else the first smallest
+    } else {
+      take = (vn || cn) ? (vn && (!cn || ci > i))           // a number beats NaN; all NaN: the last
+                        : (cv > v || (cv == v && ci < i));  // else the first largest
+    }
+  }
+  if (take) {
+    v = cv;
+    i = ci;
+  }
+}
+
+// Wave-wide combination (butterfly: every lane ends with the wave's result).
+template <int OP>
+__device__ inline void mm_wave(float& v, int64_t& i, int64_t& c) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(v, off, 64);
+    const int64_t oi = __shfl_xor(i, off, 64);
+    c += __shfl_xor(c, off, 64);
+    mm_take<OP>(v, i, ov, oi);
+  }
+}
+
+// Block-wide combination; the result is valid in thread 0.
+template <int OP, int BLOCK>
+__device__ inline void mm_block(float& v, int64_t& i, int64_t& c) {
+  __shared__ float sv[BLOCK / dc::kWave];
+  __shared__ int64_t si[BLOCK / dc::kWave], sc[BLOCK / dc::kWave];
+  mm_wave<OP>(v, i, c);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    sv[wave] = v;
+    si[wave] = i;
+    sc[wave] = c;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < BLOCK / dc::kWave; ++w) {
+      mm_take<OP>(v, i, sv[w], si[w]);
+      c += sc[w];
+    }
+  }
+}
+
+// In sequence order (every candidate comes after the current one) the enumerator's own rule
+// applies and no index comparison is needed: Min takes x unless a NaN is held or x >= current;
+// Max takes x when the current is NaN or x is larger.
+template <int OP>
+__device__ inline bool mm_in_order(bool have, float cur, float x) {
+  if (OP == kOpMin) return !have || (!__builtin_isnan(cur) && !(x >= cur));
+  return !have || __builtin_isnan(cur) || x > cur;
+}
+
+template <int MODE, int OP>
+__global__ __launch_bounds__(kSumBlock) void where_select_minmax_pass1(const dc_linq_chain prog, const AffineChain aff,
+                                                                       const float* __restrict__ in, int64_t n,
+                                                                       int vec_ok, float* __restrict__ pv,
+                                                                       int64_t* __restrict__ pi,
+                                                                       int64_t* __restrict__ pcnt) {
+  // A thread visits its elements in increasing sequence order (steps of 16 in index order, then
+  // single vectors, then the scalar tail), so it keeps the enumerator's state directly.
+  float bv = 0.0f;
+  int64_t bi = -1, cnt = 0;
+  auto fold = [&](float x, int64_t idx) __attribute__((always_inline)) {
+    if (mm_in_order<OP>(bi >= 0, bv, x)) {
+      bv = x;
+      bi = idx;
+    }
+  };
+  const int64_t n4 = vec_ok ? (n >> 2) : 0;
+  const int64_t per = (n4 + gridDim.x - 1) / gridDim.x;
+  const int64_t v0 = min(n4, (int64_t)blockIdx.x * per), v1 = min(n4, v0 + per);
+  const dc::f32x4* in4 = reinterpret_cast<const dc::f32x4*>(in);
+  int64_t i = v0 + threadIdx.x;
+  for (; i + 3 * kSumBlock < v1; i += 4 * kSumBlock) {
+    float e[16];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      dc::f32x4 x = dc::load_stream(in4 + i + j * kSumBlock);
+      e[4 * j + 0] = x.x;
+      e[4 * j + 1] = x.y;
+      e[4 * j + 2] = x.z;
+      e[4 * j + 3] = x.w;
+    }
+    const uint32_t keep = apply_small<MODE, 16>(prog, aff, e);
+    // the step's own winner (its elements in order), then one fold into the running state
+    float sv = 0.0f;
+    int sj = -1;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const bool t = ((keep >> j) & 1u) && mm_in_order<OP>(sj >= 0, sv, e[j]);
+      sv = t ? e[j] : sv;
+      sj = t ? j : sj;
+    }
+    if (sj >= 0) fold(sv, 4 * (i + (int64_t)(sj >> 2) * kSumBlock) + (sj & 3));
+    cnt += __builtin_popcount(keep);
+  }
+  for (; i < v1; i += kSumBlock) {
+    float e[4];
+    dc::f32x4 x = dc::load_stream(in4 + i);
+    e[0] = x.x; e[1] = x.y; e[2] = x.z; e[3] = x.w;
+    const uint32_t keep = apply_small<MODE, 4>(prog, aff, e);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if ((keep >> j) & 1u) fold(e[j], 4 * i + j);
+    cnt += __builtin_popcount(keep);
+  }
+  if (blockIdx.x == gridDim.x - 1) {
+    for (int64_t s = (n4 << 2) + threadIdx.x; s < n; s += kSumBlock) {
+      float e[1] = {in[s]};
+      if (apply_small<MODE, 1>(prog, aff, e) & 1u) {
+        fold(e[0], s);
+        cnt += 1;
+      }
+    }
+  }
+  mm_block<OP, kSumBlock>(bv, bi, cnt);
+  if (threadIdx.x == 0) {
+    pv[blockIdx.x] = bv;
+    pi[blockIdx.x] = bi;
+    pcnt[blockIdx.x] = cnt;
+  }
+}
+
+template <int OP>
+__global__ __launch_bounds__(kFinalBlock) void where_select_minmax_pass2(const float* __restrict__ pv,
+                                                                         const int64_t* __restrict__ pi,
+                                                                         const int64_t* __restrict__ pcnt, int count,
+                                                                         float* __restrict__ value_out,
+                                                                         int64_t* __restrict__ count_out) {
+  float v = 0.0f;
+  int64_t i = -1, c = 0;
+  for (int b = threadIdx.x; b < count; b += kFinalBlock) {
+    mm_take<OP>(v, i, pv[b], pi[b]);
+    c += pcnt[b];
+  }
+  mm_block<OP, kFinalBlock>(v, i, c);
+  if (threadIdx.x == 0) {
+    if (value_out) *value_out = i >= 0 ? v : 0.0f;
+    if (count_out) *count_out = c;
+  }
+}
+
 // ---- strategy choice -----------------------------------------------------------------------------
 const void* rounds_kernel(int mode) {
   switch (mode) {
@@ -1048,6 +1211,38 @@ DC_HIP_API int32_t dc_hip_linq_where_select_sum_f32(dc_hip_ctx* ctx, const dc_li
                                                      : where_select_sum_pass1<kModeInterp>);
   kernel<<<grid, kSumBlock, 0, ctx->stream>>>(*chain, aff, input, n, dc::aligned16(input) ? 1 : 0, psum, pcnt);
   where_select_sum_pass2<<<1, kFinalBlock, 0, ctx->stream>>>(psum, pcnt, (int)grid, sum_out, count_out);
+  return dc::last_launch_status();
+}
+
+DC_HIP_API int32_t dc_hip_linq_where_select_minmax_f32(dc_hip_ctx* ctx, const dc_linq_chain* chain,
+                                                       const float* input, int64_t n, int32_t op, float* value_out,
+                                                       int64_t* count_out) {
+  if (n < 0 || (n > 0 && !input) || (op != DC_LINQ_MIN && op != DC_LINQ_MAX)) return DC_ERR_INVALID_ARGUMENT;
+  DC_RETURN_IF(dc_linq_chain_validate(chain));
+  DC_CTX_ENTER(ctx);
+  const int64_t per_block = (int64_t)kSumBlock * 16 * 4;  // elements per block-iteration x 4
+  const unsigned grid = (unsigned)std::max<int64_t>(1, std::min<int64_t>((n + per_block - 1) / per_block, kSumBlocksMax));
+  DC_RETURN_IF(dc::ensure_partials(ctx, (size_t)grid * 24));
+  int64_t* pi = static_cast<int64_t*>(ctx->partials);
+  int64_t* pcnt = pi + grid;
+  float* pv = reinterpret_cast<float*>(pcnt + grid);
+  AffineChain aff{};
+  const bool affine = lower_affine(*chain, &aff);
+  const int mode = affine ? kModeAffine : (program_uses_saves(*chain) ? kModeInterpSaves : kModeInterp);
+  const int vec_ok = dc::aligned16(input) ? 1 : 0;
+#define DC_MINMAX(MODE, OP)                                                                                       \
+  where_select_minmax_pass1<MODE, OP><<<grid, kSumBlock, 0, ctx->stream>>>(*chain, aff, input, n, vec_ok, pv, pi, pcnt); \
+  where_select_minmax_pass2<OP><<<1, kFinalBlock, 0, ctx->stream>>>(pv, pi, pcnt, (int)grid, value_out, count_out)
+  if (op == DC_LINQ_MIN) {
+    if (mode == kModeAffine) { DC_MINMAX(kModeAffine, kOpMin); }
+    else if (mode == kModeInterpSaves) { DC_MINMAX(kModeInterpSaves, kOpMin); }
+    else { DC_MINMAX(kModeInterp, kOpMin); }
+  } else {
+    if (mode == kModeAffine) { DC_MINMAX(kModeAffine, kOpMax); }
+    else if (mode == kModeInterpSaves) { DC_MINMAX(kModeInterpSaves, kOpMax); }
+    else { DC_MINMAX(kModeInterp, kOpMax); }
+  }
+#undef DC_MINMAX
   return dc::last_launch_status();
 }
 

@@ -31,6 +31,10 @@ DC_ERR_NOT_FOUND = -8
 STRATEGY_LOOKBACK = 0
 STRATEGY_ROUNDS = 1
 
+# dc_linq_minmax: which terminal dc_hip_linq_where_select_minmax_f32 computes
+LINQ_MIN = 0
+LINQ_MAX = 1
+
 DC_LINQ_MAX_INSTR = 48
 
 # dc_linq_op
@@ -142,6 +146,7 @@ SIGNATURES: dict[str, list] = {
     "dc_linq_chain_validate": [C.POINTER(LinqChain)],
     "dc_hip_linq_where_select_f32": [_P, C.POINTER(LinqChain), _P, _i64, _P, _P],
     "dc_hip_linq_where_select_sum_f32": [_P, C.POINTER(LinqChain), _P, _i64, _P, _P],
+    "dc_hip_linq_where_select_minmax_f32": [_P, C.POINTER(LinqChain), _P, _i64, _i32, _P, _P],
     "dc_hip_linq_to_array_strategy": [_P, _P, _i64, _P],
     "dc_hip_gemm_f32": [_P, _P, _P, _P, _i64, _i64, _i64],
     "dc_hip_gemm_bf16": [_P, _P, _P, _P, _i64, _i64, _i64],
@@ -354,6 +359,15 @@ class Context:
                                                      sum_out.ptr if sum_out else None,
                                                      count.ptr if count else None),
               "dc_hip_linq_where_select_sum_f32")
+
+    def where_select_minmax_f32(self, chain: LinqChain, x: DeviceArray, op: int, value_out: DeviceArray | None,
+                                count: DeviceArray | None, n: int | None = None) -> None:
+        """op = LINQ_MIN or LINQ_MAX; value_out: float32[1], count: int64[1] (device)."""
+        n = x.size if n is None else n
+        check(load().dc_hip_linq_where_select_minmax_f32(self.handle, C.byref(chain), x.ptr, n, op,
+                                                        value_out.ptr if value_out else None,
+                                                        count.ptr if count else None),
+              "dc_hip_linq_where_select_minmax_f32")
 
     def gemm_f32(self, a: DeviceArray, b: DeviceArray, c: DeviceArray, m: int, n: int, k: int) -> None:
         check(load().dc_hip_gemm_f32(self.handle, a.ptr, b.ptr, c.ptr, m, n, k), "dc_hip_gemm_f32")

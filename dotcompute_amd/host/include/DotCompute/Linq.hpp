@@ -126,7 +126,7 @@ class BackendSelector {
 };
 
 // ---- fusion planner / HIP kernel generator -------------------------------------------------------
-enum class Terminal { ToArray, Sum, Count, LongCount, Average };
+enum class Terminal { ToArray, Sum, Count, LongCount, Average, Min, Max };
 
 struct FusedKernelPlan {
   dc_linq_chain Program{};                // one fused program for all Filter/Map stages
@@ -138,8 +138,8 @@ struct FusedKernelPlan {
 class HipKernelGenerator {
  public:
   // Lowers the graph to one fused kernel: all Filter/Map stages (CanBeFused chains) plus an
-  // optional terminal Reduce that selects the Sum/Count kernel. Throws NotSupportedException for
-  // graphs the prebuilt kernels cannot run (OrderBy, GroupBy, Join, Min/Max, non-float lambdas,
+  // optional terminal Reduce that selects the Sum/Count or Min/Max kernel. Throws
+  // NotSupportedException for graphs the prebuilt kernels cannot run (OrderBy, GroupBy, Join, non-float lambdas,
   // expressions needing more than two saved registers).
   FusedKernelPlan GenerateHipKernel(const OperationGraph& graph) const;
   // CudaKernelGenerator.cs:1163-1226: consecutive Map/Filter operations form one group.
@@ -153,6 +153,7 @@ class HipKernelGenerator {
 struct QueryResult {
   std::vector<float> Values;  // ToArray
   double Sum = 0.0;           // Sum / Average (float64 accumulator)
+  float Extreme = 0.0f;       // Min / Max
   int64_t Count = 0;
 };
 
@@ -208,8 +209,8 @@ class ComputeQueryable {
   int32_t Count() const;      // throws OverflowException above int.MaxValue
   int64_t LongCount() const;
   float Average() const;      // throws InvalidOperationException on an empty sequence
-  float Min() const;          // NotSupportedException
-  float Max() const;          // NotSupportedException
+  float Min() const;          // throws InvalidOperationException on an empty sequence
+  float Max() const;          // throws InvalidOperationException on an empty sequence
 
   const std::vector<MethodCall>& Chain() const { return chain_; }
   FusedKernelPlan Explain(Terminal terminal = Terminal::ToArray) const;

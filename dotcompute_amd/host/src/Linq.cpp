@@ -410,6 +410,8 @@ FusedKernelPlan HipKernelGenerator::GenerateHipKernel(const OperationGraph& grap
     else if (term.Method == "Count") plan.Term = Terminal::Count;
     else if (term.Method == "LongCount") plan.Term = Terminal::LongCount;
     else if (term.Method == "Average") plan.Term = Terminal::Average;
+    else if (term.Method == "Min") plan.Term = Terminal::Min;
+    else if (term.Method == "Max") plan.Term = Terminal::Max;
     else throw NotSupportedException("reduction '" + term.Method + "' has no HIP kernel");
     plan.FusedOperationIds.push_back(term.Id);
   }
@@ -423,7 +425,8 @@ FusedKernelPlan HipKernelGenerator::GenerateHipKernel(const OperationGraph& grap
 std::string FusedKernelPlan::Listing() const {
   std::ostringstream os;
   const char* term = Term == Terminal::ToArray ? "ToArray" : Term == Terminal::Sum ? "Sum"
-                     : Term == Terminal::Average ? "Average" : "Count";
+                     : Term == Terminal::Average ? "Average" : Term == Terminal::Min ? "Min"
+                     : Term == Terminal::Max ? "Max" : "Count";
   os << "terminal " << term << "\n";
   for (int i = 0; i < Program.n_instr; ++i) {
     const dc_linq_instr& in = Program.code[i];
@@ -457,6 +460,16 @@ QueryResult RuntimeExecutor::Run(const FusedKernelPlan& plan, const float* devic
     r.Count = k;
     r.Values.resize((size_t)k);
     out->CopyToHost(r.Values.data(), (size_t)k * sizeof(float));  // only the compacted prefix comes back
+  } else if (plan.Term == Terminal::Min || plan.Term == Terminal::Max) {
+    auto val = mem.AllocateAsync<float>(1);
+    auto cnt = mem.AllocateAsync<int64_t>(1);
+    Check(dc_hip_linq_where_select_minmax_f32(ctx, &plan.Program, device_in, (int64_t)n,
+                                              plan.Term == Terminal::Min ? DC_LINQ_MIN : DC_LINQ_MAX, val->Data(),
+                                              cnt->Data()),
+          "dc_hip_linq_where_select_minmax_f32");
+    acc_->Synchronize();
+    val->CopyToHost(&r.Extreme, sizeof(float));
+    cnt->CopyToHost(&r.Count, sizeof(int64_t));
   } else {
     auto sum = mem.AllocateAsync<double>(1);
     auto cnt = mem.AllocateAsync<int64_t>(1);
@@ -505,6 +518,8 @@ FusedKernelPlan ComputeQueryProvider::Plan(const std::vector<MethodCall>& chain,
     case Terminal::Count: full.push_back({"Count", std::nullopt}); break;
     case Terminal::LongCount: full.push_back({"LongCount", std::nullopt}); break;
     case Terminal::Average: full.push_back({"Average", std::nullopt}); break;
+    case Terminal::Min: full.push_back({"Min", std::nullopt}); break;
+    case Terminal::Max: full.push_back({"Max", std::nullopt}); break;
     case Terminal::ToArray: break;
   }
   // Stage 1: expression tree -> operation graph.
@@ -575,8 +590,19 @@ float ComputeQueryable::Average() const {
   return (float)(r.Sum / (double)r.Count);
 }
 
-float ComputeQueryable::Min() const { throw NotSupportedException("Min() has no HIP kernel in this build"); }
-float ComputeQueryable::Max() const { throw NotSupportedException("Max() has no HIP kernel in this build"); }
+// BCL Enumerable.Min/Max(IEnumerable<float>) semantics (the reference runs these as LINQ-to-objects):
+// the device reduction returns the same element bit for bit; an empty sequence throws.
+float ComputeQueryable::Min() const {
+  QueryResult r = Run(Terminal::Min);
+  if (r.Count == 0) throw InvalidOperationException("Sequence contains no elements");
+  return r.Extreme;
+}
+
+float ComputeQueryable::Max() const {
+  QueryResult r = Run(Terminal::Max);
+  if (r.Count == 0) throw InvalidOperationException("Sequence contains no elements");
+  return r.Extreme;
+}
 
 ComputeQueryable AsComputeQueryable(const std::vector<float>& source, std::shared_ptr<ComputeQueryProvider> provider) {
   return ComputeQueryable(source.data(), source.size(), provider ? provider : ComputeQueryProvider::Default());

@@ -293,6 +293,18 @@ DC_HIP_API int32_t dc_hip_linq_to_array_strategy(dc_hip_ctx* ctx, const float* i
 DC_HIP_API int32_t dc_hip_linq_where_select_sum_f32(dc_hip_ctx* ctx, const dc_linq_chain* chain,
                                                     const float* input, int64_t n,
                                                     double* sum_out, int64_t* count_out);
+/* Where/Select → Min or Max of the kept, mapped elements: the result to *value_out (device float)
+ * and the number of kept elements to *count_out (device int64; 0 = empty sequence, *value_out is
+ * then unspecified and the managed layer throws InvalidOperationException). Replaces the reference's
+ * Min/Max terminal operators (mapped to Reduce, src/Extensions/DotCompute.Linq/Compilation/
+ * ExpressionTreeVisitor.cs:244-245; executed as LINQ-to-objects through the scalar branch,
+ * ComputeQueryableExtensions.cs:265-267) and returns what the .NET 10 BCL Enumerable.Min/Max
+ * (IEnumerable<float>) returns, bit for bit: Min the first NaN, else the first smallest element;
+ * Max the first largest non-NaN element, or the last NaN when all are NaN. Deterministic. */
+enum dc_linq_minmax { DC_LINQ_MIN = 0, DC_LINQ_MAX = 1 };
+DC_HIP_API int32_t dc_hip_linq_where_select_minmax_f32(dc_hip_ctx* ctx, const dc_linq_chain* chain,
+                                                       const float* input, int64_t n, int32_t op,
+                                                       float* value_out, int64_t* count_out);
 
 /* ---------------------------------------------------------------------------------------------
  * Dense GEMM, row-major: C[m×n] = A[m×k] · B[k×n].

@@ -51,6 +51,8 @@ def lib() -> C.CDLL:
             "oracle_linq_eval": (_i32, [_P, C.c_float, _P]),
             "oracle_linq_where_select": (_i64, [_P, _P, _i64, _P]),
             "oracle_linq_where_select_sum": (C.c_float, [_P, _P, _i64, _P, _P]),
+            "oracle_linq_where_select_min": (_i64, [_P, _P, _i64, _P]),
+            "oracle_linq_where_select_max": (_i64, [_P, _P, _i64, _P]),
             "oracle_gemm_f32_naive": (None, [_P, _P, _P, _i64, _i64, _i64, _i32]),
             "oracle_gemm_f32_naive_rows": (None, [_P, _P, _P, _i64, _i64, _i64, _i64, _i64, _i32]),
             "oracle_gemm_f32_blocked": (None, [_P, _P, _P, _i64, _i64, _i64]),
@@ -168,6 +170,18 @@ def linq_where_select_sum(chain, x: np.ndarray):
     if cnt.value < 0:
         raise ValueError(f"malformed chain ({cnt.value})")
     return np.float32(f), d.value, cnt.value
+
+
+def linq_where_select_minmax(chain, x: np.ndarray, op: str):
+    """BCL Enumerable.Min/Max of the kept, mapped elements (restated in oracle.c). Returns
+    (value as float32, count of kept elements); value is meaningless when count == 0."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(1, np.float32)  # written through a pointer: NaN payload bits are kept
+    fn = lib().oracle_linq_where_select_min if op == "min" else lib().oracle_linq_where_select_max
+    k = fn(C.byref(chain), _p(x), x.size, _p(out))
+    if k < 0:
+        raise ValueError(f"malformed chain ({k})")
+    return out[0], int(k)
 
 
 def linq_eval(chain, x: float):

@@ -344,6 +344,47 @@ float oracle_linq_where_select_sum(const dc_linq_chain* chain, const float* in, 
   return (float)s;
 }
 
+/* BCL Enumerable.Min(IEnumerable<float>), .NET 10 (global.json:3-4), over the kept, mapped values:
+ * the enumerator loop stops at the first NaN; the count keeps running so an empty sequence is seen. */
+int64_t oracle_linq_where_select_min(const dc_linq_chain* chain, const float* in, int64_t n, float* out) {
+  int64_t k = 0;
+  float value = 0.0f;
+  int stopped = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    float x;
+    int32_t r = oracle_linq_eval(chain, in[i], &x);
+    if (r < 0) return r;
+    if (!r) continue;
+    if (k++ == 0) {
+      value = x;
+      if (isnan(value)) stopped = 1;
+      continue;
+    }
+    if (stopped) continue;
+    if (x < value) value = x;
+    else if (isnan(x)) { value = x; stopped = 1; }
+  }
+  if (out) *out = value;
+  return k;
+}
+
+/* BCL Enumerable.Max(IEnumerable<float>), .NET 10 (global.json:3-4): leading NaNs are replaced by
+ * the next element; after the first non-NaN value only a strictly larger element replaces it. */
+int64_t oracle_linq_where_select_max(const dc_linq_chain* chain, const float* in, int64_t n, float* out) {
+  int64_t k = 0;
+  float value = 0.0f;
+  for (int64_t i = 0; i < n; ++i) {
+    float x;
+    int32_t r = oracle_linq_eval(chain, in[i], &x);
+    if (r < 0) return r;
+    if (!r) continue;
+    if (k++ == 0 || isnan(value)) { value = x; continue; }
+    if (x > value) value = x;
+  }
+  if (out) *out = value;
+  return k;
+}
+
 /* ------------------------------------------------------------------------------------------ */
 /* GEMM                                                                                          */
 /* ------------------------------------------------------------------------------------------ */

@@ -59,6 +59,19 @@ int32_t oracle_linq_eval(const dc_linq_chain* chain, float x, float* y_out);
 int64_t oracle_linq_where_select(const dc_linq_chain* chain, const float* in, int64_t n, float* out);
 float oracle_linq_where_select_sum(const dc_linq_chain* chain, const float* in, int64_t n,
                                    int64_t* count, double* as_double);
+/* Where/Select -> Min / Max of the kept, mapped elements. The reference runs these terminal
+ * operators as LINQ-to-objects (ComputeQueryableExtensions.cs:265-267 scalar branch; Min/Max become
+ * Reduce operations, ExpressionTreeVisitor.cs:244-245), i.e. the .NET 10 BCL
+ * System.Linq.Enumerable.Min/Max(IEnumerable<float>) (global.json:3-4; not vendored in the
+ * reference), restated here as its published enumerator loop:
+ *   Min: the first element; if it is NaN return it; then for each x: if (x < value) value = x;
+ *        else if (IsNaN(x)) return x.       (the first NaN wins; else the first smallest)
+ *   Max: the first element; while it is NaN take the next (return it if none is left); then for
+ *        each x: if (x > value) value = x.  (NaNs skipped; the first largest; all NaN: the last)
+ * Writes the result to *out and returns the number of kept elements (0: the sequence is empty and
+ * the caller throws InvalidOperationException), or a negative value for an invalid program. */
+int64_t oracle_linq_where_select_min(const dc_linq_chain* chain, const float* in, int64_t n, float* out);
+int64_t oracle_linq_where_select_max(const dc_linq_chain* chain, const float* in, int64_t n, float* out);
 
 /* ---- GEMM ---- */
 void oracle_gemm_f32_naive(const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k,

@@ -3,6 +3,8 @@
 // are checked against the CPU oracle (oracle/liboracle.so), which this test binary links as the
 // checker only.
 #include <algorithm>
+#include <cmath>
+#include <cstring>
 #include <random>
 
 #include "DotCompute/Algorithms.hpp"
@@ -197,8 +199,10 @@ TEST_CPU(planner_terminals_and_unsupported_operators) {
   CHECK(q.Explain(Terminal::Sum).Term == Terminal::Sum);
   CHECK(q.Explain(Terminal::Average).Term == Terminal::Average);
   CHECK(q.Explain(Terminal::Count).FusedOperationIds.size() == 3);
+  CHECK(q.Explain(Terminal::Min).Term == Terminal::Min);
+  CHECK(q.Explain(Terminal::Max).Term == Terminal::Max);
   CHECK_THROWS(NotSupportedException, q.OrderBy(x).Explain());
-  CHECK_THROWS(NotSupportedException, q.Min());
+  CHECK_THROWS(InvalidOperationException, q.Min());  // no HIP device behind this provider
 }
 
 // ============================== CPU: runtime, registry, no-device behaviour =======================
@@ -343,6 +347,38 @@ TEST_GPU(linq_reference_golden_vectors) {
   std::vector<float> empty;
   CHECK_THROWS(InvalidOperationException, AsComputeQueryable(empty, p).Average());
   CHECK(AsComputeQueryable(empty, p).Sum() == 0.0f);
+  // FutureExpansionTests.cs:553-570: Range(1, 100) -> Sum 5050, Count 100, Max 100
+  std::vector<float> s100(100);
+  for (int i = 0; i < 100; ++i) s100[i] = (float)(i + 1);
+  CHECK(AsComputeQueryable(s100, p).Sum() == 5050.0f);
+  CHECK(AsComputeQueryable(s100, p).Count() == 100);
+  CHECK(AsComputeQueryable(s100, p).Max() == 100.0f);
+  // ExpressionTreeVisitorTests.cs:113-147: Min / Max of {5, 2, 8, 1}
+  std::vector<float> s4{5, 2, 8, 1};
+  CHECK(AsComputeQueryable(s4, p).Min() == 1.0f);
+  CHECK(AsComputeQueryable(s4, p).Max() == 8.0f);
+  CHECK_THROWS(InvalidOperationException, AsComputeQueryable(empty, p).Min());
+  CHECK_THROWS(InvalidOperationException, AsComputeQueryable(s4, p).Where(x > 9.0f).Max());
+}
+
+TEST_GPU(linq_min_max_match_enumerable) {
+  auto x = Param();
+  auto p = std::make_shared<ComputeQueryProvider>(Gpu());
+  auto src = Uniform(500000, 31, 0);
+  src[1234] = -0.0f;  // ties between signed zeros go to the earlier element
+  src[4321] = 0.0f;
+  auto q = AsComputeQueryable(src, p).Where(x < 0.75f).Select(x * 2.0f + 1.0f);
+  float mn = 0, mx = 0;
+  const FusedKernelPlan pmin = q.Explain(Terminal::Min), pmax = q.Explain(Terminal::Max);
+  CHECK(oracle_linq_where_select_min(&pmin.Program, src.data(), (int64_t)src.size(), &mn) > 0);
+  CHECK(oracle_linq_where_select_max(&pmax.Program, src.data(), (int64_t)src.size(), &mx) > 0);
+  const float gmn = q.Min(), gmx = q.Max();
+  CHECK(std::memcmp(&gmn, &mn, 4) == 0 && std::memcmp(&gmx, &mx, 4) == 0);
+  std::vector<float> with_nan = src;
+  with_nan[77777] = NAN;
+  auto qn = AsComputeQueryable(with_nan, p).Select(x * 1.0f);
+  CHECK(std::isnan(qn.Min()));   // Enumerable.Min: NaN is the smallest value
+  CHECK(!std::isnan(qn.Max()));  // Enumerable.Max: NaNs are skipped
 }
 
 TEST_GPU(linq_benchmark_chain_bit_exact_vs_linq_to_objects) {

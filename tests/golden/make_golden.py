@@ -93,6 +93,10 @@ def main() -> None:
         "LinqBackendIntegrationTests.cs:309-325 Where(x%2==0).Select(x*x) over 1..100": {"count": 50, "first": 4,
                                                                                          "last": 10000},
         "README.md:46-57 VectorAdd": {"a": [1, 2, 3, 4, 5], "b": [10, 20, 30, 40, 50], "result": [11, 22, 33, 44, 55]},
+        "FutureExpansionTests.cs:553-570 Sum/Count/Max over Range(1,100)": {"sum": 5050, "count": 100, "max": 100},
+        # ExpressionTreeVisitorTests.cs:113-147 asserts that Min()/Max() over {5,2,8,1} become Reduce
+        # operations; the values are those of Enumerable.Min/Max over the same input.
+        "ExpressionTreeVisitorTests.cs:113-147 Min/Max over 5,2,8,1": {"input": [5, 2, 8, 1], "min": 1, "max": 8},
     }
     with open(os.path.join(HERE, "hot_path_golden.json"), "w") as f:
         json.dump(g, f, indent=None, separators=(",", ":"))

@@ -51,6 +51,24 @@ def run_sum(ctx, chain, x):
     return res
 
 
+def run_minmax(ctx, chain, x, op, offset=0):
+    """Device Min/Max (op: hip.LINQ_MIN / LINQ_MAX) of the kept, mapped elements, with the input
+    placed `offset` floats into its allocation. Returns (value as float32, count)."""
+    n = x.size
+    dx = ctx.empty(n + offset + 1, np.float32)
+    if n:
+        hip.check(hip.load().dc_hip_memcpy_h2d_async(ctx.handle, dx.ptr + 4 * offset, x.ctypes.data, x.nbytes), "h2d")
+    src = hip.DeviceArray(ctx, dx.ptr + 4 * offset, 4 * n, np.dtype(np.float32), (n,))
+    v = ctx.empty(1, np.float32)
+    c = ctx.empty(1, np.int64)
+    ctx.where_select_minmax_f32(chain, src, op, v, c, n)
+    ctx.synchronize()
+    res = (v.to_host()[0], int(c.to_host()[0]))
+    for a in (dx, v, c):
+        ctx.free(a)
+    return res
+
+
 def bits(a):
     return np.ascontiguousarray(a, np.float32).view(np.uint32)
 
@@ -380,3 +398,79 @@ def test_round_robin_two_contexts_interleaved(ctx):
         for a in (dx, out, cnt):
             c.free(a)
     ctxs[1].close()
+
+
+# ---- Where/Select -> Min / Max: bit-identical to Enumerable.Min/Max (oracle restatement) ----------
+MINMAX = [("min", hip.LINQ_MIN), ("max", hip.LINQ_MAX)]
+EMPTY = LinqChain.assemble([])
+
+
+@pytest.mark.parametrize("n", [1, 2, 63, 64, 1000, 4095, 4097, 100_000, 1_000_000, 16_000_000])
+@pytest.mark.parametrize("which", MINMAX)
+def test_min_max_benchmark_chain(ctx, n, which):
+    name, op = which
+    x = oracle.gen_uniform_f32(n, 44, 0)
+    got, cnt = run_minmax(ctx, CHAIN, x, op)
+    ref, rcnt = oracle.linq_where_select_minmax(CHAIN, x, name)
+    assert cnt == rcnt
+    if rcnt:
+        assert bits(got) == bits(ref)
+
+
+@pytest.mark.parametrize("offset", [1, 2, 3])
+@pytest.mark.parametrize("which", MINMAX)
+def test_min_max_misaligned_and_golden(ctx, offset, which):
+    name, op = which
+    x = oracle.gen_uniform_f32(300_007, 5, 0)
+    got, cnt = run_minmax(ctx, CHAIN, x, op, offset)
+    ref, rcnt = oracle.linq_where_select_minmax(CHAIN, x, name)
+    assert cnt == rcnt and bits(got) == bits(ref)
+    r100 = np.arange(1, 101, dtype=np.float32)
+    assert run_minmax(ctx, EMPTY, r100, op, offset) == ((1.0 if name == "min" else 100.0), 100)
+    assert run_minmax(ctx, EMPTY, np.array([5, 2, 8, 1], np.float32), op)[0] == (1.0 if name == "min" else 8.0)
+
+
+@pytest.mark.parametrize("which", MINMAX)
+def test_min_max_empty_sequences(ctx, which):
+    _, op = which
+    assert run_minmax(ctx, EMPTY, np.empty(0, np.float32), op)[1] == 0
+    none = LinqChain.assemble([(LOAD, SRC_ELEM, 0), (CMP_GT, SRC_IMM, 5.0), (FILTER, SRC_IMM, 0)])
+    assert run_minmax(ctx, none, oracle.gen_uniform_f32(200_000, 3, 0), op)[1] == 0
+
+
+@pytest.mark.parametrize("n", [1000, 70_001, 2_000_000])
+@pytest.mark.parametrize("which", MINMAX)
+def test_min_max_ties_and_nans_pick_the_enumerator_element(ctx, n, which):
+    """Many equal minima/maxima of both zero signs, and NaNs with distinct payloads at random
+    places: the element chosen (its bits) must be the one the sequential enumerator returns."""
+    name, op = which
+    rng = np.random.default_rng(n)
+    signed_zeros = rng.choice(np.array([0x00000000, 0x80000000, 0x3F800000, 0xBF800000], np.uint32), n)
+    x = signed_zeros.view(np.float32)
+    for chain in (EMPTY, LinqChain.assemble([(LOAD, SRC_ELEM, 0), (CMP_NE, SRC_IMM, 1.0), (FILTER, SRC_IMM, 0)])):
+        got, cnt = run_minmax(ctx, chain, x, op)
+        ref, rcnt = oracle.linq_where_select_minmax(chain, x, name)
+        assert cnt == rcnt and bits(got) == bits(ref)
+    y = oracle.gen_uniform_f32(n, 9, 0).copy()
+    pos = rng.choice(n, 5, replace=False)
+    y.view(np.uint32)[pos] = 0x7FC00000 + np.arange(1, 6, dtype=np.uint32)  # quiet NaNs, distinct payloads
+    got, cnt = run_minmax(ctx, EMPTY, y, op)
+    ref, rcnt = oracle.linq_where_select_minmax(EMPTY, y, name)
+    assert cnt == rcnt and bits(got) == bits(ref)
+    all_nan = (0x7FC00000 + np.arange(1, n + 1, dtype=np.uint32) % 1000).view(np.float32)
+    got, cnt = run_minmax(ctx, EMPTY, all_nan, op)
+    ref, _ = oracle.linq_where_select_minmax(EMPTY, all_nan, name)
+    assert bits(got) == bits(ref)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_min_max_random_programs(ctx, seed):
+    rng = np.random.default_rng(500 + seed)
+    prog = _random_program(rng)
+    x = oracle.gen_uniform_f32(80_000 + 313 * seed, 200 + seed, 0)
+    for name, op in MINMAX:
+        got, cnt = run_minmax(ctx, prog, x, op)
+        ref, rcnt = oracle.linq_where_select_minmax(prog, x, name)
+        assert cnt == rcnt
+        if rcnt:
+            assert same_floats(np.array([got]), np.array([ref]))

@@ -166,6 +166,57 @@ def test_planted_mistake_is_caught():
     assert not np.array_equal(swapped.view(np.uint32), good.view(np.uint32))
 
 
+def _f32(bits_list):
+    return np.array(bits_list, np.uint32).view(np.float32)
+
+
+def test_min_max_known_answers_and_empty():
+    empty_chain = _chain([])
+    ka = KA["FutureExpansionTests.cs:553-570 Sum/Count/Max over Range(1,100)"]
+    r100 = np.arange(1, 101, dtype=np.float32)
+    assert oracle.linq_where_select_minmax(empty_chain, r100, "max") == (ka["max"], ka["count"])
+    assert oracle.linq_where_select_sum(empty_chain, r100)[1] == ka["sum"]
+    ka4 = KA["ExpressionTreeVisitorTests.cs:113-147 Min/Max over 5,2,8,1"]
+    x4 = np.array(ka4["input"], np.float32)
+    assert oracle.linq_where_select_minmax(empty_chain, x4, "min")[0] == ka4["min"]
+    assert oracle.linq_where_select_minmax(empty_chain, x4, "max")[0] == ka4["max"]
+    # an empty sequence (nothing kept) reports count 0; the host layer throws on it
+    from dotcompute_amd.hip import CMP_GT, FILTER, LOAD, SRC_ELEM, SRC_IMM
+    none = _chain([(LOAD, SRC_ELEM, 0), (CMP_GT, SRC_IMM, 100.0), (FILTER, SRC_IMM, 0)])
+    assert oracle.linq_where_select_minmax(none, x4, "min")[1] == 0
+    assert oracle.linq_where_select_minmax(empty_chain, np.empty(0, np.float32), "max")[1] == 0
+
+
+def test_min_max_signed_zero_and_nan_rules():
+    """Hand-worked cases of Enumerable.Min/Max(IEnumerable<float>): ties (+0 == -0) keep the earlier
+    element; Min returns the first NaN; Max skips NaNs and returns the last NaN when all are NaN."""
+    e = _chain([])
+    pz, nz = 0x00000000, 0x80000000
+    nan_a, nan_b, nan_c = 0x7FC00001, 0x7FC00002, 0x7FC00003
+    mm = lambda bits_list, op: oracle.linq_where_select_minmax(e, _f32(bits_list), op)[0].view(np.uint32)
+    assert mm([pz, nz], "min") == pz and mm([nz, pz], "min") == nz
+    assert mm([pz, nz], "max") == pz and mm([nz, pz], "max") == nz
+    one = np.float32(1).view(np.uint32)
+    two = np.float32(2).view(np.uint32)
+    assert mm([one, nan_a, pz, nan_b], "min") == nan_a   # first NaN, even after smaller values
+    assert mm([nan_a, nan_b], "min") == nan_a
+    assert mm([nan_a, nan_b, nan_c], "max") == nan_c     # all NaN: the last one
+    assert mm([nan_a, two, nan_b, one], "max") == two    # NaNs skipped
+    assert mm([one, two, nan_a], "max") == two
+
+
+def test_min_max_match_numpy_on_nan_free_data():
+    from dotcompute_amd import hip
+    a = oracle.gen_uniform_f32(100_003, 12, 0)
+    kept = oracle.where_gt0_select_2x_plus_1(a)
+    ch = hip.where_gt0_select_2x_plus_1()
+    assert oracle.linq_where_select_minmax(ch, a, "min") == (kept.min(), kept.size)
+    assert oracle.linq_where_select_minmax(ch, a, "max") == (kept.max(), kept.size)
+    # a planted mistake (taking the last of equal minima) is visible in the bits
+    z = _f32([0x3F800000, 0x80000000, 0x00000000])
+    assert oracle.linq_where_select_minmax(_chain([]), z, "min")[0].view(np.uint32) == 0x80000000
+
+
 # ------------------------------------------------------------------ GEMM
 def test_gemm_against_numpy_float64_golden():
     a = from_bits(GOLDEN["inputs"]["f32_seed42_stream0_bits"])[: 16 * 24].reshape(16, 24)
