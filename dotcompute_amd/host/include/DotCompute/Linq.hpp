@@ -211,6 +211,12 @@ class ComputeQueryable {
   float Average() const;      // throws InvalidOperationException on an empty sequence
   float Min() const;          // throws InvalidOperationException on an empty sequence
   float Max() const;          // throws InvalidOperationException on an empty sequence
+  // Any / All (Reduce operators, ExpressionTreeVisitor.cs:244-245) on the count kernel: Any(p) is
+  // "Where(p) keeps something", All(p) is "Where(!p) keeps nothing" (a NaN fails any comparison,
+  // so !p keeps it and All is false, as Enumerable.All evaluates p per element).
+  bool Any() const;
+  bool Any(const Expr& predicate) const;
+  bool All(const Expr& predicate) const;
 
   const std::vector<MethodCall>& Chain() const { return chain_; }
   FusedKernelPlan Explain(Terminal terminal = Terminal::ToArray) const;

@@ -604,6 +604,12 @@ float ComputeQueryable::Max() const {
   return r.Extreme;
 }
 
+bool ComputeQueryable::Any() const { return LongCount() > 0; }
+
+bool ComputeQueryable::Any(const Expr& predicate) const { return Where(predicate).LongCount() > 0; }
+
+bool ComputeQueryable::All(const Expr& predicate) const { return Where(!predicate).LongCount() == 0; }
+
 ComputeQueryable AsComputeQueryable(const std::vector<float>& source, std::shared_ptr<ComputeQueryProvider> provider) {
   return ComputeQueryable(source.data(), source.size(), provider ? provider : ComputeQueryProvider::Default());
 }

@@ -359,6 +359,15 @@ TEST_GPU(linq_reference_golden_vectors) {
   CHECK(AsComputeQueryable(s4, p).Max() == 8.0f);
   CHECK_THROWS(InvalidOperationException, AsComputeQueryable(empty, p).Min());
   CHECK_THROWS(InvalidOperationException, AsComputeQueryable(s4, p).Where(x > 9.0f).Max());
+  // ComputeQueryProviderTests.cs:573-597: {1,2,3}.Any(x > 2) and .All(x > 0) are true
+  CHECK(AsComputeQueryable(s3, p).Any(x > 2.0f));
+  CHECK(AsComputeQueryable(s3, p).All(x > 0.0f));
+  CHECK(!AsComputeQueryable(s3, p).Any(x > 3.0f));
+  CHECK(!AsComputeQueryable(s3, p).All(x > 1.0f));
+  CHECK(!AsComputeQueryable(empty, p).Any() && AsComputeQueryable(empty, p).All(x > 0.0f));
+  std::vector<float> with_nan{1.0f, NAN, 2.0f};
+  CHECK(!AsComputeQueryable(with_nan, p).All(x > 0.0f));  // NaN > 0 is false
+  CHECK(AsComputeQueryable(with_nan, p).Any(x != x));     // and NaN != NaN is true
 }
 
 TEST_GPU(linq_min_max_match_enumerable) {
