@@ -234,7 +234,14 @@ def test_where_select_256m(ctx):
     assert int(c.to_host()[0]) == k
     ref_sum = float(np.sum(ref, dtype=np.float64))
     assert abs(s.to_host()[0] - ref_sum) <= 1e-5 * 28 * abs(ref_sum)
-    for a in (dx, out, cnt, s, c):
+    # Min / Max of the same chain over the full input: the first smallest / largest kept element
+    v = ctx.empty(1, np.float32)
+    for op, ref_v in ((hip.LINQ_MIN, ref.min()), (hip.LINQ_MAX, ref.max())):
+        ctx.where_select_minmax_f32(CHAIN, dx, op, v, c)
+        ctx.synchronize()
+        assert int(c.to_host()[0]) == k
+        assert bits(v.to_host()) == bits(np.array([ref_v], np.float32))
+    for a in (dx, out, cnt, s, c, v):
         ctx.free(a)
 
 
