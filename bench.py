@@ -9,8 +9,10 @@ order-preserving compaction kernel. Throughput = algorithmic bytes (4 B read per
 
 Also reported (outside the timed steps, each with its own roofline): Sum f32 / i32 at 256M, the
 fused Where->Select->Sum and ->Min/Max at 256M, VectorAdd at N=100,000 and 256M, dense fp32 and bf16 MatMul,
-CSR SpMV x20. These legs run first and the headline's W warmup + K timed steps run after them. The CPU baseline is the oracle's single-thread LINQ-to-objects restatement of the
-headline chain, timed on this host.
+CSR SpMV x20. These legs run first and the headline's W warmup + K timed steps run after them. The CPU
+baseline is the oracle's single-thread LINQ-to-objects restatement of the headline chain, timed on this
+host; each reported leg carries its own bounded `cpu_baseline` from the oracle's restatement of the
+reference's CPU algorithm for it (same seeded inputs; `sample` says what was timed).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-extras]
 Prints exactly one JSON line on stdout; progress goes to stderr.
@@ -122,6 +124,9 @@ def main() -> int:
         log("[bench] copy calibration: 1 GiB device-to-device copy done")
 
     warm_timer = lambda c, f, it: time_launches(c, f, it, warm_ms=LEG_WARM_MS)
+    from bench_extras import host_cores  # noqa: E402
+
+    cores = host_cores()
 
     def want(name):
         return not args.skip_extras and (not args.only or name in args.only.split(","))
@@ -130,12 +135,13 @@ def main() -> int:
     if want("gemm"):
         from bench_extras import bench_gemm  # noqa: E402
 
-        extra.update(bench_gemm(ctx, log, warm_timer, roofline, FP32_MFMA_PEAK_TFLOPS, BF16_MFMA_PEAK_TFLOPS))
+        extra.update(bench_gemm(ctx, log, warm_timer, roofline, FP32_MFMA_PEAK_TFLOPS, BF16_MFMA_PEAK_TFLOPS,
+                                cpu_cores=None if args.skip_cpu else cores))
     # ---------------- CSR SpMV x20 ---------------------------------------------------------------
     if want("spmv"):
         from bench_extras import bench_spmv  # noqa: E402
 
-        extra.update(bench_spmv(ctx, log, warm_timer, roofline, HBM_PEAK_GBS))
+        extra.update(bench_spmv(ctx, log, warm_timer, roofline, HBM_PEAK_GBS, cpu=not args.skip_cpu))
 
     # ---------------- fused Where->Select->Sum and plain Sum at 256M --------------------------
     if want("linq_sum"):
@@ -236,6 +242,9 @@ def main() -> int:
                "sample": f"full N=256M input, {reps} passes ({t_cpu:.1f} s) of the oracle's single-thread "
                          f"LINQ-to-objects Where(x>0f).Select(x*2f+1f).ToArray() restatement"}
         log(f"[bench] cpu baseline: {cpu_gbs:.2f} GB/s over {reps} passes")
+        from bench_extras import stream_cpu_baselines  # noqa: E402
+
+        stream_cpu_baselines(extra, hx, cores, log)
         del hx
 
     ctx.close()

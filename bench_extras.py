@@ -1,10 +1,71 @@
-"""GEMM and SpMV legs of bench.py (inputs generated on device, resident before timing)."""
+"""GEMM and SpMV legs of bench.py (inputs generated on device, resident before timing), and the
+bounded CPU baselines timed beside each leg.
+
+The CPU baselines run the oracle's C restatements of the reference's CPU algorithms on the same
+seeded inputs (the counter-based generator gives the host the same elements the device fill
+wrote). They are reported beside the GPU figures, never measured as the product.
+"""
 from __future__ import annotations
+
+import os
+import statistics
+import time
 
 import numpy as np
 
 
-def bench_gemm(ctx, log, time_launches, roofline, fp32_peak, bf16_peak, sizes=(1024, 4096, 8192)) -> dict:
+def host_cores() -> int:
+    """Threads the multi-threaded CPU baselines use: this process's CPU share, at most 16."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def cpu_median(fn, reps: int, budget_s: float, warm: bool = False):
+    """Median host wall time (s) of fn() over up to `reps` timed runs (fewer once `budget_s` of timed
+    work has accumulated; at least one), after one untimed run when `warm`."""
+    if warm:
+        fn()
+    ts = []
+    while len(ts) < reps and (not ts or sum(ts) < budget_s):
+        t = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t)
+    return statistics.median(ts), len(ts)
+
+
+def runs(r: int) -> str:
+    return f"median of {r} runs" if r > 1 else "one run"
+
+
+def cpu_baseline(value: float, unit: str, cores: int, sample: str, **more) -> dict:
+    d = {"value": float(f"{value:.4g}"), "unit": unit, "cores": cores, "kind": "port", "sample": sample}
+    d.update(more)
+    return d
+
+
+def gemm_cpu_baseline(n: int, cores: int, log) -> dict:
+    """OptimizedMatrixMultiplyKernel's parallel-for over rows with the naive i-j-k fp32 loop (oracle
+    restatement) on the same A and B. Above 1024 a subset of rows is timed (every row costs the same
+    n*n multiply-adds) and the full-matrix time is extrapolated from it."""
+    import oracle
+
+    rows = n if n <= 1024 else 2 * cores
+    a = oracle.gen_uniform_f32(rows * n, 42, 0).reshape(rows, n)  # rows [0, rows) of the device's A
+    b = oracle.gen_uniform_f32(n * n, 43, 0).reshape(n, n)
+    t, reps = cpu_median(lambda: oracle.gemm_f32_naive(a, b, threads=cores), 3, 2.5)
+    tflops = 2.0 * rows * n * n / t / 1e12
+    full_ms = t * n / rows * 1e3
+    sample = (f"all {n} rows" if rows == n else f"rows 0..{rows - 1} of {n}, full-matrix time extrapolated "
+              f"x{n // rows}") + f"; {runs(reps)} of the oracle's naive i-j-k fp32 loop on {cores} threads"
+    log(f"[bench] cpu gemm_f32 {n}: {tflops * 1e3:.2f} GFLOP/s ({full_ms:.0f} ms full matrix, {sample})")
+    return cpu_baseline(tflops, "TFLOP/s", cores, sample, ms=round(full_ms, 1))
+
+
+def bench_gemm(ctx, log, time_launches, roofline, fp32_peak, bf16_peak, sizes=(1024, 4096, 8192),
+               cpu_cores: int | None = None) -> dict:
     out = {}
     for n in sizes:
         a = ctx.empty((n, n), np.float32)
@@ -21,6 +82,8 @@ def bench_gemm(ctx, log, time_launches, roofline, fp32_peak, bf16_peak, sizes=(1
         out[f"gemm_f32_{n}"] = {"ms": round(ms, 4), "TFLOP/s": round(tflops, 2),
                                 "roofline": roofline("mfma", tflops, fp32_peak, "TFLOP/s")}
         log(f"[bench] gemm_f32 {n}^3: {ms:.3f} ms -> {tflops:.1f} TFLOP/s ({100 * tflops / fp32_peak:.1f}% of fp32 MFMA)")
+        if cpu_cores:
+            out[f"gemm_f32_{n}"]["cpu_baseline"] = gemm_cpu_baseline(n, cpu_cores, log)
         if n == sizes[-1]:
             ab = ctx.empty((n, n), np.uint16)
             bb = ctx.empty((n, n), np.uint16)
@@ -41,7 +104,25 @@ def bench_gemm(ctx, log, time_launches, roofline, fp32_peak, bf16_peak, sizes=(1
     return out
 
 
-def bench_spmv(ctx, log, time_launches, roofline, hbm_peak, sizes=(1_000_000, 16_000_000), iters=20) -> dict:
+def spmv_cpu_baseline(rp, col, val, rows: int, iters: int, per_iter_bytes: int, log) -> dict:
+    """SparseMatrix.Multiply's row loop followed by the L1 normalisation (oracle restatement, one
+    thread) on the same CSR matrix and start vector. Above 10M non-zeros one iteration is timed and
+    the x`iters` time extrapolated (every iteration does the same work)."""
+    import oracle
+
+    x0 = oracle.gen_uniform_f32(rows, 42, 5, unit_interval=True)
+    n_it = iters if val.size < 10_000_000 else 1
+    t, reps = cpu_median(lambda: oracle.spmv_power_f32(rp, col, val, x0, n_it), 3, 2.0)
+    full_s = t * iters / n_it
+    gbs = iters * per_iter_bytes / full_s / 1e9
+    sample = (f"{n_it} iteration{'s' if n_it > 1 else ''}" + (f", x{iters} extrapolated" if n_it < iters else "")
+              + f"; {runs(reps)} of the oracle's single-thread CSR row loop + L1 normalisation")
+    log(f"[bench] cpu spmv x{iters} rows={rows}: {gbs:.2f} GB/s ({full_s * 1e3:.0f} ms, {sample})")
+    return cpu_baseline(gbs, "GB/s", 1, sample, ms=round(full_s * 1e3, 1))
+
+
+def bench_spmv(ctx, log, time_launches, roofline, hbm_peak, sizes=(1_000_000, 16_000_000), iters=20,
+               cpu: bool = False) -> dict:
     from dotcompute_amd import hip
 
     out = {}
@@ -97,4 +178,69 @@ def bench_spmv(ctx, log, time_launches, roofline, hbm_peak, sizes=(1_000_000, 16
             f" plan SpMV {ms_plan * 1e3:.1f} us -> {gbs_plan:.0f} GB/s")
         for a in (drp, dcol, dval, x0, x, y):
             ctx.free(a)
+        if cpu:
+            out[f"spmv_power20_{rows // 1_000_000}M"]["cpu_baseline"] = spmv_cpu_baseline(
+                rp, col, val, rows, iters, per_iter, log)
     return out
+
+
+def stream_cpu_baselines(extra: dict, hx: np.ndarray, cores: int, log) -> None:
+    """CPU baselines of the 256M streaming legs (Sum, fused Where->Select->Sum/Min/Max, VectorAdd),
+    added to the legs already in `extra`. `hx` is the 256M headline input generated on the host."""
+    import oracle
+
+    n = hx.size
+    mib = n * 4 // (1 << 20)
+    if "sum_f32_256M" in extra:
+        t, r = cpu_median(lambda: oracle.sum_f32_partitioned(hx, cores), 5, 1.0, warm=True)
+        t1, r1 = cpu_median(lambda: oracle.sum_f32_enumerable(hx), 3, 1.0)
+        extra["sum_f32_256M"]["cpu_baseline"] = cpu_baseline(
+            4 * n / t / 1e9, "GB/s", cores, f"full input ({mib} MiB), {runs(r)} of OptimizedReductionKernel's "
+            f"one-double-partial-per-thread sum over {cores} threads", ms=round(t * 1e3, 2))
+        extra["sum_f32_256M"]["cpu_baseline_sequential"] = cpu_baseline(
+            4 * n / t1 / 1e9, "GB/s", 1, f"full input, {runs(r1)} of Enumerable.Sum's sequential double "
+            f"accumulator", ms=round(t1 * 1e3, 2))
+        log(f"[bench] cpu sum_f32: {4 * n / t / 1e9:.1f} GB/s on {cores} threads, {4 * n / t1 / 1e9:.1f} GB/s sequential")
+    if "sum_i32_256M" in extra:
+        xi = oracle.gen_uniform_i32(n, 43, 1)
+        t, r = cpu_median(lambda: oracle.sum_i32_checked(xi), 3, 1.0)
+        extra["sum_i32_256M"]["cpu_baseline"] = cpu_baseline(
+            4 * n / t / 1e9, "GB/s", 1, f"full input, {runs(r)} of checked Enumerable.Sum(int)",
+            ms=round(t * 1e3, 2))
+        log(f"[bench] cpu sum_i32: {4 * n / t / 1e9:.1f} GB/s")
+        del xi
+    if "where_select_sum_f32_256M" in extra:
+        res = []
+        t, r = cpu_median(lambda: res.append(oracle.where_gt0_select_2x_plus_1_sum(hx)), 3, 2.0)
+        leg = extra["where_select_sum_f32_256M"]
+        leg["cpu_baseline"] = cpu_baseline(
+            4 * n / t / 1e9, "GB/s", 1, f"full input, {runs(r)} of LINQ-to-objects "
+            f"Where(x>0f).Select(x*2f+1f).Sum() with the lambdas written out", ms=round(t * 1e3, 2),
+            count_matches_gpu=bool(res[-1][2] == leg["count"]))
+        log(f"[bench] cpu where_select_sum: {4 * n / t / 1e9:.2f} GB/s")
+    for name in ("min", "max"):
+        label = f"where_select_{name}_f32_256M"
+        if label not in extra:
+            continue
+        res = []
+        t, r = cpu_median(lambda: res.append(oracle.where_gt0_select_2x_plus_1_minmax(hx, name)), 3, 2.0)
+        leg = extra[label]
+        leg["cpu_baseline"] = cpu_baseline(
+            4 * n / t / 1e9, "GB/s", 1, f"full input, {runs(r)} of LINQ-to-objects "
+            f"Where(x>0f).Select(x*2f+1f).{name.capitalize()}() with the lambdas written out",
+            ms=round(t * 1e3, 2), value_matches_gpu=bool(np.float32(leg["value"]) == res[-1][0]))
+        log(f"[bench] cpu where_select_{name}: {4 * n / t / 1e9:.2f} GB/s")
+    for nv, full, label, reps in ((100_000, 100_000, "vector_add_f32_100K", 200),
+                                  (32 << 20, n, "vector_add_f32_256M", 3)):
+        if label not in extra:
+            continue
+        a = hx[:nv]
+        b = oracle.gen_uniform_f32(nv, 42, 1)  # the device leg's second operand (seed 42, stream 1)
+        o = np.empty(nv, np.float32)
+        t, r = cpu_median(lambda: oracle.vector_add_f32(a, b, o), reps, 0.5, warm=True)
+        sample = (f"full input, {runs(r)}" if nv == full else
+                  f"first {nv >> 20}M of the {full >> 20}M elements, {runs(r)}") + \
+            " of the generated scalar [Kernel] CPU invoker loop into a preallocated result"
+        extra[label]["cpu_baseline"] = cpu_baseline(12 * nv / t / 1e9, "GB/s", 1, sample,
+                                                    ms=round(t * full / nv * 1e3, 4))
+        log(f"[bench] cpu {label}: {12 * nv / t / 1e9:.2f} GB/s")

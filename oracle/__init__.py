@@ -53,6 +53,7 @@ def lib() -> C.CDLL:
             "oracle_linq_where_select_sum": (C.c_float, [_P, _P, _i64, _P, _P]),
             "oracle_linq_where_select_min": (_i64, [_P, _P, _i64, _P]),
             "oracle_linq_where_select_max": (_i64, [_P, _P, _i64, _P]),
+            "oracle_where_gt0_select_2x_plus_1_minmax": (_i64, [_P, _i64, _i32, _P]),
             "oracle_gemm_f32_naive": (None, [_P, _P, _P, _i64, _i64, _i64, _i32]),
             "oracle_gemm_f32_naive_rows": (None, [_P, _P, _P, _i64, _i64, _i64, _i64, _i64, _i32]),
             "oracle_gemm_f32_blocked": (None, [_P, _P, _P, _i64, _i64, _i64]),
@@ -107,8 +108,9 @@ def gen_zipf_csr(rows: int, seed: int, alpha: float = 2.0, max_degree: int = 409
 
 
 # ---- ops ----
-def vector_add_f32(a: np.ndarray, b: np.ndarray) -> np.ndarray:
-    out = np.empty_like(a)
+def vector_add_f32(a: np.ndarray, b: np.ndarray, out: np.ndarray | None = None) -> np.ndarray:
+    out = np.empty_like(a) if out is None else out
+    assert out.shape == a.shape == b.shape and out.dtype == np.float32
     lib().oracle_vector_add_f32(_p(a), _p(b), _p(out), a.size)
     return out
 
@@ -181,6 +183,14 @@ def linq_where_select_minmax(chain, x: np.ndarray, op: str):
     k = fn(C.byref(chain), _p(x), x.size, _p(out))
     if k < 0:
         raise ValueError(f"malformed chain ({k})")
+    return out[0], int(k)
+
+
+def where_gt0_select_2x_plus_1_minmax(x: np.ndarray, op: str):
+    """Where(x > 0f).Select(x * 2f + 1f).Min() / .Max() with the lambdas written out; returns
+    (value as float32, count of kept elements)."""
+    out = np.zeros(1, np.float32)
+    k = lib().oracle_where_gt0_select_2x_plus_1_minmax(_p(x), x.size, 0 if op == "min" else 1, _p(out))
     return out[0], int(k)
 
 

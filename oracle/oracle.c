@@ -344,45 +344,73 @@ float oracle_linq_where_select_sum(const dc_linq_chain* chain, const float* in, 
   return (float)s;
 }
 
-/* BCL Enumerable.Min(IEnumerable<float>), .NET 10 (global.json:3-4), over the kept, mapped values:
- * the enumerator loop stops at the first NaN; the count keeps running so an empty sequence is seen. */
-int64_t oracle_linq_where_select_min(const dc_linq_chain* chain, const float* in, int64_t n, float* out) {
-  int64_t k = 0;
-  float value = 0.0f;
-  int stopped = 0;
-  for (int64_t i = 0; i < n; ++i) {
-    float x;
-    int32_t r = oracle_linq_eval(chain, in[i], &x);
-    if (r < 0) return r;
-    if (!r) continue;
-    if (k++ == 0) {
-      value = x;
-      if (isnan(value)) stopped = 1;
-      continue;
-    }
-    if (stopped) continue;
-    if (x < value) value = x;
-    else if (isnan(x)) { value = x; stopped = 1; }
+/* BCL Enumerable.Min / Max(IEnumerable<float>), .NET 10 (global.json:3-4), as one step per kept,
+ * mapped element. `k` counts the elements seen, so an empty sequence is visible to the caller.
+ * Min: the enumerator loop stops at the first NaN (`stopped`), else the first smallest wins.
+ * Max: leading NaNs are replaced by the next element; after the first non-NaN value only a
+ * strictly larger element replaces it. */
+typedef struct {
+  int64_t k;
+  float value;
+  int stopped;
+} bcl_extreme;
+
+static inline void bcl_min_step(bcl_extreme* s, float x) {
+  if (s->k++ == 0) {
+    s->value = x;
+    if (isnan(x)) s->stopped = 1;
+    return;
   }
-  if (out) *out = value;
-  return k;
+  if (s->stopped) return;
+  if (x < s->value) s->value = x;
+  else if (isnan(x)) { s->value = x; s->stopped = 1; }
 }
 
-/* BCL Enumerable.Max(IEnumerable<float>), .NET 10 (global.json:3-4): leading NaNs are replaced by
- * the next element; after the first non-NaN value only a strictly larger element replaces it. */
-int64_t oracle_linq_where_select_max(const dc_linq_chain* chain, const float* in, int64_t n, float* out) {
-  int64_t k = 0;
-  float value = 0.0f;
+static inline void bcl_max_step(bcl_extreme* s, float x) {
+  if (s->k++ == 0 || isnan(s->value)) { s->value = x; return; }
+  if (x > s->value) s->value = x;
+}
+
+int64_t oracle_linq_where_select_min(const dc_linq_chain* chain, const float* in, int64_t n, float* out) {
+  bcl_extreme s = {0, 0.0f, 0};
   for (int64_t i = 0; i < n; ++i) {
     float x;
     int32_t r = oracle_linq_eval(chain, in[i], &x);
     if (r < 0) return r;
-    if (!r) continue;
-    if (k++ == 0 || isnan(value)) { value = x; continue; }
-    if (x > value) value = x;
+    if (r) bcl_min_step(&s, x);
   }
-  if (out) *out = value;
-  return k;
+  if (out) *out = s.value;
+  return s.k;
+}
+
+int64_t oracle_linq_where_select_max(const dc_linq_chain* chain, const float* in, int64_t n, float* out) {
+  bcl_extreme s = {0, 0.0f, 0};
+  for (int64_t i = 0; i < n; ++i) {
+    float x;
+    int32_t r = oracle_linq_eval(chain, in[i], &x);
+    if (r < 0) return r;
+    if (r) bcl_max_step(&s, x);
+  }
+  if (out) *out = s.value;
+  return s.k;
+}
+
+/* .Where(x > 0f).Select(x * 2f + 1f).Min() / .Max() with the lambdas written out, as the
+ * LINQ-to-objects fallback runs them (ComputeQueryableExtensions.cs:265-267): the same steps as
+ * above without the chain interpreter. op 0 = Min, 1 = Max. */
+int64_t oracle_where_gt0_select_2x_plus_1_minmax(const float* in, int64_t n, int32_t op, float* out) {
+  bcl_extreme s = {0, 0.0f, 0};
+  for (int64_t i = 0; i < n; ++i) {
+    float x = in[i];
+    if (x > 0.0f) {
+      float t = x * 2.0f;
+      float y = t + 1.0f;
+      if (op == 0) bcl_min_step(&s, y);
+      else bcl_max_step(&s, y);
+    }
+  }
+  if (out) *out = s.value;
+  return s.k;
 }
 
 /* ------------------------------------------------------------------------------------------ */

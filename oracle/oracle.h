@@ -72,6 +72,9 @@ float oracle_linq_where_select_sum(const dc_linq_chain* chain, const float* in, 
  * the caller throws InvalidOperationException), or a negative value for an invalid program. */
 int64_t oracle_linq_where_select_min(const dc_linq_chain* chain, const float* in, int64_t n, float* out);
 int64_t oracle_linq_where_select_max(const dc_linq_chain* chain, const float* in, int64_t n, float* out);
+/* The same two operators after .Where(x > 0f).Select(x * 2f + 1f) with the lambdas written out
+ * (op 0 = Min, 1 = Max): the CPU baseline of the fused Min/Max leg. */
+int64_t oracle_where_gt0_select_2x_plus_1_minmax(const float* in, int64_t n, int32_t op, float* out);
 
 /* ---- GEMM ---- */
 void oracle_gemm_f32_naive(const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k,

@@ -212,6 +212,17 @@ def test_min_max_match_numpy_on_nan_free_data():
     ch = hip.where_gt0_select_2x_plus_1()
     assert oracle.linq_where_select_minmax(ch, a, "min") == (kept.min(), kept.size)
     assert oracle.linq_where_select_minmax(ch, a, "max") == (kept.max(), kept.size)
+    # the written-out lambdas (the bench's CPU baseline) agree with numpy and the interpreter,
+    # also with NaN, -0, +inf and a tie in the input
+    assert oracle.where_gt0_select_2x_plus_1_minmax(a, "min") == (kept.min(), kept.size)
+    assert oracle.where_gt0_select_2x_plus_1_minmax(a, "max") == (kept.max(), kept.size)
+    b = a.copy()
+    b[[5, 70, 900, 901, 4000]] = [np.nan, -0.0, np.inf, a[70], a[4000]]
+    for op in ("min", "max"):
+        got, ref = oracle.where_gt0_select_2x_plus_1_minmax(b, op), oracle.linq_where_select_minmax(ch, b, op)
+        assert got[1] == ref[1] and got[0].view(np.uint32) == ref[0].view(np.uint32)
+    assert oracle.where_gt0_select_2x_plus_1_minmax(b, "max")[0] == np.inf
+    assert oracle.where_gt0_select_2x_plus_1_minmax(-np.abs(a), "min")[1] == 0
     # a planted mistake (taking the last of equal minima) is visible in the bits
     z = _f32([0x3F800000, 0x80000000, 0x00000000])
     assert oracle.linq_where_select_minmax(_chain([]), z, "min")[0].view(np.uint32) == 0x80000000
