@@ -521,20 +521,25 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_bf16_kernel(const unsigned s
 }
 
 // ---------------------------------------------------------------------------------------------
-// bf16, large tiles: C = A·B with B first transposed to Bt[n][k] (a separate pass, so both
-// operands are k-contiguous and every global load and LDS access is 16 bytes wide).
+// bf16, large tiles: C = A·B straight from row-major A[M][K] and B[K][N].
 //
-// Macro tile 256×256, BK = 64, double-buffered LDS (2 × (256 + 256) rows × 128 B = 128 KiB, one
-// workgroup per CU). 512 threads as 2×4 waves of 128×64 (4×2 MFMA 32×32×16 tiles, 128
-// accumulators per lane), two waves per SIMD so one's LDS and barrier waits overlap the other's
-// MFMAs.
+// Macro tile 256×256, BK = 64, double-buffered LDS (2 × (32 + 32) KiB = 128 KiB, one workgroup
+// per CU). 512 threads as 2×4 waves of 128×64 (4×2 MFMA 32×32×16 tiles, 128 accumulators per
+// lane), two waves per SIMD so one's LDS and barrier waits overlap the other's MFMAs.
 //
-// Global -> LDS: direct-to-LDS loads (global_load_lds_dwordx4): lane L of a wave's load writes
-// LDS bytes 16·L of a 1 KiB block (8 rows of 128 B), so no registers stage the tile and a tile's
-// loads can stay in flight for a whole tile of MFMAs. Rows are unpadded; the 16-byte k-octet q of
-// row R sits in slot q ^ ((R >> 1) & 7) of the row, so a fragment read (rows R0..R0+15 at one
-// octet for each 16 lanes) touches 16 distinct 16-byte bank groups. The swizzle is applied on the
-// global side: each lane fetches the octet that belongs in its slot.
+// Global -> LDS: direct-to-LDS loads (buffer_load_dwordx4 ... lds): lane L of a wave's load
+// writes LDS bytes 16·L of a 1 KiB block, so no registers stage the tile and a tile's loads can
+// stay in flight for a whole tile of MFMAs. The swizzles below are applied on the global side:
+// each lane fetches the 16 bytes that belong in its LDS slot.
+// - A tile: 256 rows (m) of 64 k, 128 B per row. The 16-byte k-octet q of row R sits in slot
+//   q ^ ((R >> 1) & 7), so a fragment read (ds_read_b128: rows R0..R0+15 at one octet for each 16
+//   lanes) touches 16 distinct 16-byte bank groups.
+// - B tile: 64 rows (k) of 256 n, 512 B per row, as B is stored. The 64-byte block b of row k
+//   sits at block b ^ (k & 3). The MFMA wants 8 consecutive k of one column n per lane; the
+//   transposing LDS read ds_read_b64_tr_b16 gives that: within each 16 lanes, source lane
+//   s = 4j + p reads the 4 bf16 of row k0 + j at columns n0 + 4p..4p+3, and lane i receives
+//   B[k0 + j][n0 + i] for j = 0..3 (two such reads give k0..k0+7). The 32 lanes of each half
+//   wave read 4 rows × 64 B at four different 64-byte offsets modulo 256 B: no bank conflicts.
 //
 // Pipeline of tile kt (buffer kt & 1): steps 0..2 run their MFMAs with the next step's fragment
 // reads between them; then the tile's one barrier (which also waits for tile kt+1's loads, issued
@@ -546,33 +551,37 @@ constexpr int kBM2 = 256, kBN2 = 256, kBK2 = 64;
 constexpr int kBigThreads = 512;
 constexpr int kWaveM = 128, kWaveN = 64;       // wave tile
 constexpr int kMT = kWaveM / 32, kNT = kWaveN / 32;
-constexpr int kRowElems = kBK2;                // bf16 per LDS row (128 B, unpadded)
+constexpr int kARow = kBK2 * 2;                // bytes per A row in LDS (64 k)
+constexpr int kBRow = kBN2 * 2;                // bytes per B row in LDS (256 n)
 
 struct Bf16BigSmem {
-  unsigned short a[2][kBM2 * kRowElems];
-  unsigned short b[2][kBN2 * kRowElems];
+  unsigned short a[2][kBM2 * kBK2];
+  unsigned short b[2][kBK2 * kBN2];
 };
 
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4* lds_s16x4_ptr;
 
-// Issues the direct-to-LDS loads of one BK slice (columns k0..k0+63) of the workgroup's A panel
-// (rows m0..m0+255, buffer resource `ra`) and Bt panel (`rb`) into LDS buffer `buf`. Wave w's load
-// i fills LDS rows 8·(8i + w) .. +7 (1 KiB); lane L takes row 8·(8i + w) + L / 8 and slot L % 8,
-// i.e. k-octet (L % 8) ^ ((row >> 1) % 8) of that row. `voff` is the lane's byte offset
-// ((L / 8)·K + 8·octet)·2 (row >> 1 depends on w and L only); the row block and k0 are uniform.
+// Issues the direct-to-LDS loads of one BK slice (k0..k0+63) of the workgroup's A panel (rows
+// m0..m0+255, buffer resource `ra`) and B panel (columns n0..n0+255 of rows k0.., resource `rb`)
+// into LDS buffer BUF. Wave w's load i fills A rows 8·(8i + w) .. +7 and B rows 2·(8i + w) .. +1
+// (1 KiB each). `avoff` / `bvoff` are the lane's byte offsets inside such a block's global rows;
+// the block's global row offset is uniform (scalar).
 template <int BUF>
 __device__ inline void bf16_tile_to_lds(Bf16BigSmem& sm, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb, int K,
-                                        int k0, int wave, uint32_t voff) {
+                                        int N, int k0, int wave, uint32_t avoff, uint32_t bvoff) {
 #pragma unroll
-  for (int i = 0; i < kBM2 / 64; ++i) {
-    const int row0 = 8 * (8 * i + wave);
-    const int32_t soff = (row0 * K + k0) * (int32_t)sizeof(unsigned short);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)&sm.a[BUF][row0 * kRowElems], 16, voff, soff, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)&sm.b[BUF][row0 * kRowElems], 16, voff, soff, 0, 0);
+  for (int i = 0; i < 4; ++i) {
+    const int blk = 8 * i + wave;
+    const int32_t asoff = (8 * blk * K + k0) * (int32_t)sizeof(unsigned short);
+    const int32_t bsoff = (k0 + 2 * blk) * N * (int32_t)sizeof(unsigned short);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)&sm.a[BUF][blk * 512], 16, avoff, asoff, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)&sm.b[BUF][blk * 512], 16, bvoff, bsoff, 0, 0);
   }
 }
 
 __global__ __launch_bounds__(kBigThreads, 1) void gemm_bf16_big_kernel(const unsigned short* __restrict__ A,
-                                                                       const unsigned short* __restrict__ Bt,
+                                                                       const unsigned short* __restrict__ B,
                                                                        float* __restrict__ C, int M, int N, int K,
                                                                        int tiles_m, int tiles_n) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -583,23 +592,38 @@ __global__ __launch_bounds__(kBigThreads, 1) void gemm_bf16_big_kernel(const uns
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / (kBN2 / kWaveN), wn = wave % (kBN2 / kWaveN);
   const int r = lane & 31, h = lane >> 5;
-  // load side: panels as buffer ranges (256 rows of K bf16 < 2 GiB, checked by the host)
-  const int32_t panel_bytes = kBM2 * K * (int32_t)sizeof(unsigned short);
-  const auto ra = dc::range_rsrc(A + (size_t)m0 * K, panel_bytes);
-  const auto rb = dc::range_rsrc(Bt + (size_t)n0 * K, panel_bytes);
-  const int lrow = lane >> 3;
-  const int lswz = ((8 * wave + lrow) >> 1) & 7;  // (row >> 1) % 8 for rows 8·(8i + w) + lrow, any i
-  const uint32_t voff = (uint32_t)((lrow * K + 8 * ((lane & 7) ^ lswz)) * (int)sizeof(unsigned short));
-  // read side: fragment rows R = 32·t + r (t: wave and tile offsets, multiples of 32), so the
-  // swizzle is (r >> 1) % 8; k-octet 2·step + h. Byte offsets of step s in buffer 0 of a and b
-  // (buffer, mt and nt offsets are immediates).
+  // load side: A panel (256 rows of K) and B panel (K rows, 256 columns at row pitch N) as buffer
+  // ranges (both < 2 GiB, checked by the host)
+  const auto ra = dc::range_rsrc(A + (size_t)m0 * K, kBM2 * K * (int32_t)sizeof(unsigned short));
+  const auto rb = dc::range_rsrc(B + n0, ((K - 1) * N + kBN2) * (int32_t)sizeof(unsigned short));
+  // A: lane -> row L / 8 of the block, slot L % 8 = octet (L % 8) ^ ((row >> 1) % 8), where
+  // (row >> 1) % 8 depends on w and L only
+  const int arow = lane >> 3;
+  const int aswz = ((8 * wave + arow) >> 1) & 7;
+  const uint32_t avoff = (uint32_t)((arow * K + 8 * ((lane & 7) ^ aswz)) * (int)sizeof(unsigned short));
+  // B: lane -> row L / 32 of the block pair, 16-byte slot c = L % 32 (64-byte block c / 4), which
+  // holds global chunk 4·((c / 4) ^ (row & 3)) + c % 4; row & 3 = (2w + L / 32) & 3
+  const int brow = lane >> 5, bc = lane & 31;
+  const int bchunk = 4 * ((bc >> 2) ^ ((2 * wave + brow) & 3)) + (bc & 3);
+  const uint32_t bvoff = (uint32_t)((brow * N + 8 * bchunk) * (int)sizeof(unsigned short));
+  // read side, A: fragment rows R = 32·t + r (t: wave and tile offsets, multiples of 32), so the
+  // swizzle is (r >> 1) % 8; k-octet 2·step + h. Byte offsets of step s in buffer 0 (buffer and mt
+  // offsets are immediates).
   const int rswz = (r >> 1) & 7;
-  uint32_t aoff[4], boff[4];
+  uint32_t aoff[4];
 #pragma unroll
-  for (int st = 0; st < 4; ++st) {
-    const uint32_t slot = 16u * (uint32_t)((2 * st + h) ^ rswz);
-    aoff[st] = (uint32_t)(wm * kWaveM + r) * (kRowElems * 2) + slot;
-    boff[st] = (uint32_t)offsetof(Bf16BigSmem, b) + (uint32_t)(wn * kWaveN + r) * (kRowElems * 2) + slot;
+  for (int st = 0; st < 4; ++st)
+    aoff[st] = (uint32_t)(wm * kWaveM + r) * kARow + 16u * (uint32_t)((2 * st + h) ^ rswz);
+  // read side, B: source lane s = L % 16 = 4j + p reads row 8h + j (+16·step, +4 for the upper
+  // four k: immediates) at columns wn·64 + nt·32 + 16·((L / 16) & 1) + 4p, whose 64-byte block
+  // 2·wn + nt sits at (2·wn + nt) ^ j since the row is ≡ j (mod 4)
+  uint32_t boff[kNT];
+  {
+    const int j = (lane & 15) >> 2, p4 = lane & 3, cg = (lane >> 4) & 1;
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt)
+      boff[nt] = (uint32_t)offsetof(Bf16BigSmem, b) + (uint32_t)((8 * h + j) * kBRow) +
+                 64u * (uint32_t)((2 * wn + nt) ^ j) + (uint32_t)(32 * cg + 8 * p4);
   }
 
   f32x16 acc[kMT][kNT];
@@ -610,22 +634,31 @@ __global__ __launch_bounds__(kBigThreads, 1) void gemm_bf16_big_kernel(const uns
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  constexpr int kSteps = kBK2 / 16, kReads = kMT + kNT;
+  constexpr int kSteps = kBK2 / 16;
   static_assert(kSteps == 4, "four 16-wide k steps per tile");
   const int kt_count = K / kBK2;
-  bf16_tile_to_lds<0>(sm, ra, rb, K, 0, wave, voff);
-  dma_barrier();
-  if (kt_count > 1) bf16_tile_to_lds<1>(sm, ra, rb, K, kBK2, wave, voff);
-
   const unsigned char* lds = smem_raw;
-  auto read_frags = [&](auto BUF, int step, bf16x8* a, bf16x8* b) __attribute__((always_inline)) {
-    constexpr uint32_t kBuf = (uint32_t)decltype(BUF)::value * kBM2 * kRowElems * 2;
+  // B fragments of a whole tile (4 steps × kNT × 2 transposing reads) in one burst. The compiler
+  // cannot tell these intrinsic reads apart from the LDS the direct-to-LDS loads write, so it
+  // waits for every load in flight before each of them: the burst is issued while none is (right
+  // after a barrier that waited for them all, before the next tile's loads go out).
+  auto read_b_tile = [&](auto BUF, bf16x8 (*b)[kNT]) __attribute__((always_inline)) {
+    constexpr uint32_t kBufB = (uint32_t)decltype(BUF)::value * kBK2 * kBRow;
+#pragma unroll
+    for (int st = 0; st < kSteps; ++st)
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt) {
+        const unsigned char* q = lds + boff[nt] + kBufB + st * 16 * kBRow;
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(q));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(q + 4 * kBRow));
+        b[st][nt] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+  };
+  auto read_a = [&](auto BUF, int step, bf16x8* a) __attribute__((always_inline)) {
+    constexpr uint32_t kBufA = (uint32_t)decltype(BUF)::value * kBM2 * kARow;
 #pragma unroll
     for (int mt = 0; mt < kMT; ++mt)
-      a[mt] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(lds + aoff[step] + kBuf + mt * 32 * kRowElems * 2));
-#pragma unroll
-    for (int nt = 0; nt < kNT; ++nt)
-      b[nt] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(lds + boff[step] + kBuf + nt * 32 * kRowElems * 2));
+      a[mt] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(lds + aoff[step] + kBufA + mt * 32 * kARow));
   };
   auto mfmas = [&](const bf16x8* a, const bf16x8* b) __attribute__((always_inline)) {
 #pragma unroll
@@ -634,16 +667,20 @@ __global__ __launch_bounds__(kBigThreads, 1) void gemm_bf16_big_kernel(const uns
       for (int nt = 0; nt < kNT; ++nt)
         acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[mt], b[nt], acc[mt][nt], 0, 0, 0);
   };
-  // One LDS read after each of the first kReads MFMAs of the region (the rest run back to back).
+  // One A read after each of the first kMT MFMAs of the region (the rest run back to back).
   auto interleave_reads = []() __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < kReads; ++i) {
+    for (int i = 0; i < kMT; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
     }
   };
-  bf16x8 fa[2][kMT], fb[2][kNT];
-  read_frags(std::integral_constant<int, 0>{}, 0, fa[0], fb[0]);
+  bf16x8 fa[2][kMT], fb[2][kSteps][kNT];
+  bf16_tile_to_lds<0>(sm, ra, rb, K, N, 0, wave, avoff, bvoff);
+  dma_barrier();
+  read_b_tile(std::integral_constant<int, 0>{}, fb[0]);
+  read_a(std::integral_constant<int, 0>{}, 0, fa[0]);
+  if (kt_count > 1) bf16_tile_to_lds<1>(sm, ra, rb, K, N, kBK2, wave, avoff, bvoff);
   // Tile kt in LDS buffer BUF = kt % 2 (the loop is unrolled by two, so buffer offsets are
   // constants; a macro rather than a lambda keeps the fragment arrays plain registers).
 #define DC_BF16_TILE(BUF, KT)                                                                      \
@@ -651,25 +688,32 @@ __global__ __launch_bounds__(kBigThreads, 1) void gemm_bf16_big_kernel(const uns
     _Pragma("unroll") for (int step = 0; step + 1 < kSteps; ++step) {                              \
       const int cur = step & 1;                                                                    \
       __builtin_amdgcn_sched_barrier(0);                                                           \
-      read_frags(std::integral_constant<int, BUF>{}, step + 1, fa[cur ^ 1], fb[cur ^ 1]);          \
-      mfmas(fa[cur], fb[cur]);                                                                     \
+      read_a(std::integral_constant<int, BUF>{}, step + 1, fa[cur ^ 1]);                           \
+      mfmas(fa[cur], fb[BUF][step]);                                                               \
       interleave_reads();                                                                          \
       __builtin_amdgcn_sched_barrier(0);                                                           \
     }                                                                                              \
     /* tile KT+1 is in LDS; every wave is done reading buffer BUF (after the last tile the */     \
     /* barrier and the reads of the other buffer are harmless and unused) */                      \
     dma_barrier();                                                                                 \
-    if ((KT) + 2 < kt_count) bf16_tile_to_lds<BUF>(sm, ra, rb, K, ((KT) + 2) * kBK2, wave, voff);   \
+    read_b_tile(std::integral_constant<int, 1 - (BUF)>{}, fb[1 - (BUF)]);                          \
+    if ((KT) + 2 < kt_count)                                                                       \
+      bf16_tile_to_lds<BUF>(sm, ra, rb, K, N, ((KT) + 2) * kBK2, wave, avoff, bvoff);              \
     __builtin_amdgcn_sched_barrier(0);                                                             \
-    read_frags(std::integral_constant<int, 1 - (BUF)>{}, 0, fa[0], fb[0]);                         \
-    mfmas(fa[1], fb[1]);                                                                           \
+    read_a(std::integral_constant<int, 1 - (BUF)>{}, 0, fa[0]);                                    \
+    mfmas(fa[1], fb[BUF][kSteps - 1]);                                                             \
     interleave_reads();                                                                            \
     __builtin_amdgcn_sched_barrier(0);                                                             \
   }
-  for (int kt = 0; kt < kt_count; kt += 2) {
+  // K is a positive multiple of 64 (host check): at least one tile, and no zero-trip path that
+  // would keep the accumulators' initial values live beside the loop
+  __builtin_assume(kt_count > 0);
+  int kt = 0;
+  do {
     DC_BF16_TILE(0, kt);
     if (kt + 1 < kt_count) DC_BF16_TILE(1, kt + 1);
-  }
+    kt += 2;
+  } while (kt < kt_count);
 #undef DC_BF16_TILE
 
   // acc[mt][nt][v] holds C[row][col], row = 8*(v/4) + 4*h + v%4, col = r (within the 32×32 tile).
@@ -684,33 +728,6 @@ __global__ __launch_bounds__(kBigThreads, 1) void gemm_bf16_big_kernel(const uns
         C[(size_t)row * N + col] = acc[mt][nt][v];
       }
     }
-}
-
-// Bt[n][k] = B[k][n] for bf16 bit patterns, 64×64 tiles through LDS with 16-byte global loads and
-// stores on both sides (K and N multiples of 64 and rows 16-byte aligned, as the large-tile GEMM
-// requires). A thread loads 8 consecutive n of one k row, then gathers 8 consecutive k of one n
-// column from LDS (pitch 66 bf16 spreads those reads over the banks) and stores them as 16 bytes.
-__global__ __launch_bounds__(256) void transpose_u16_kernel(const unsigned short* __restrict__ B,
-                                                            unsigned short* __restrict__ Bt, int K, int N) {
-  __shared__ unsigned short t[64][66];
-  const int k0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {  // 512 slots of 8 bf16: slot -> k row s / 8, n octet s % 8
-    const int sl = tid + 256 * i, kr = sl >> 3, no = (sl & 7) * 8;
-    const u16x8 v = *reinterpret_cast<const u16x8*>(B + (size_t)(k0 + kr) * N + n0 + no);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) t[kr][no + e] = v[e];
-  }
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {  // slot -> n row s / 8, k octet s % 8
-    const int sl = tid + 256 * i, nr = sl >> 3, ko = (sl & 7) * 8;
-    u16x8 v;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = t[ko + e][nr];
-    *reinterpret_cast<u16x8*>(Bt + (size_t)(n0 + nr) * K + k0 + ko) = v;
-  }
 }
 
 // Round-to-nearest-even fp32 -> bf16 (quiet NaN kept NaN).
@@ -786,21 +803,17 @@ DC_HIP_API int32_t dc_hip_gemm_bf16(dc_hip_ctx* ctx, const uint16_t* a, const ui
   const unsigned grid = (unsigned)(tiles_m * tiles_n);
   const unsigned short* A = reinterpret_cast<const unsigned short*>(a);
   const unsigned short* B = reinterpret_cast<const unsigned short*>(b);
+  // large tiles: the A panel (256 rows of k bf16) and the B panel (k rows at pitch n) as buffer
+  // ranges, each < 2 GiB
   if ((m % kBM2 == 0) && (n % kBN2 == 0) && (k % kBK2 == 0) && dc::aligned16(a) && dc::aligned16(b) &&
-      (int64_t)k * kBM2 * 2 < ((int64_t)1 << 31)) {  // the panel buffer ranges: 256 rows of k bf16 < 2 GiB
-    // large tiles: B transposed into context scratch first
-    DC_RETURN_IF(dc::ensure_gemm_scratch(ctx, (size_t)n * (size_t)k * sizeof(unsigned short)));
-    unsigned short* Bt = static_cast<unsigned short*>(ctx->gemm_scratch);
-    transpose_u16_kernel<<<dim3((unsigned)((n + 63) / 64), (unsigned)((k + 63) / 64)), 256, 0, ctx->stream>>>(
-        B, Bt, (int)k, (int)n);
-    DC_RETURN_IF(dc::last_launch_status());
+      (int64_t)k * kBM2 * 2 < ((int64_t)1 << 31) && (int64_t)k * n * 2 < ((int64_t)1 << 31)) {
     const int tm2 = (int)(m / kBM2), tn2 = (int)(n / kBN2);
     static const hipError_t lds_ok = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_bf16_big_kernel),
                                                          hipFuncAttributeMaxDynamicSharedMemorySize,
                                                          (int)sizeof(Bf16BigSmem));
     DC_RETURN_IF_HIP(lds_ok);
     gemm_bf16_big_kernel<<<(unsigned)(tm2 * tn2), kBigThreads, sizeof(Bf16BigSmem), ctx->stream>>>(
-        A, Bt, c, (int)m, (int)n, (int)k, tm2, tn2);
+        A, B, c, (int)m, (int)n, (int)k, tm2, tn2);
     return dc::last_launch_status();
   }
   const bool full = (m % kBM == 0) && (n % kBN == 0) && (k % kBKbf16 == 0) && dc::aligned16(a) && dc::aligned16(b);

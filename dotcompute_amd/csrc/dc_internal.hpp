@@ -33,9 +33,6 @@ struct dc_hip_ctx {
   // Device memory of the column-sliced SpMV plan built by dc_hip_spmv_power_iterate_f32 (grows).
   void* spmv_plan_mem = nullptr;
   size_t spmv_plan_bytes = 0;
-  // GEMM operand staging (the transposed B of the bf16 kernel; grows).
-  void* gemm_scratch = nullptr;
-  size_t gemm_scratch_bytes = 0;
 
   // Decoupled-lookback status words, one uint64 per tile (grows on demand). A word is valid only
   // when its epoch field equals the launch's epoch, so the array never needs clearing between
@@ -119,7 +116,6 @@ void resident_forget(dc_hip_ctx* ctx);
 int32_t ensure_spmv_rows(dc_hip_ctx* ctx, size_t count);
 int32_t ensure_spmv_windows(dc_hip_ctx* ctx, size_t count);
 int32_t ensure_spmv_plan_mem(dc_hip_ctx* ctx, size_t bytes);
-int32_t ensure_gemm_scratch(dc_hip_ctx* ctx, size_t bytes);
 // Two-pass deterministic float64 sum of n floats into *sum_out (device), on the ctx stream.
 int32_t launch_reduce_sum_f32(dc_hip_ctx* ctx, const float* input, int64_t n, double* sum_out);
 // *sum_out = partials[0] + ... + partials[count-1] (float64, fixed order; one workgroup).

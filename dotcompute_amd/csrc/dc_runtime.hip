@@ -126,19 +126,6 @@ int32_t ensure_spmv_plan_mem(dc_hip_ctx* ctx, size_t bytes) {
   return DC_OK;
 }
 
-int32_t ensure_gemm_scratch(dc_hip_ctx* ctx, size_t bytes) {
-  if (ctx->gemm_scratch_bytes >= bytes) return DC_OK;
-  DC_RETURN_IF_HIP(hipStreamSynchronize(ctx->stream));
-  if (ctx->gemm_scratch) DC_RETURN_IF_HIP(hipFree(ctx->gemm_scratch));
-  ctx->gemm_scratch = nullptr;
-  ctx->gemm_scratch_bytes = 0;
-  void* p = nullptr;
-  if (hipMalloc(&p, bytes) != hipSuccess) return DC_ERR_OUT_OF_MEMORY;
-  ctx->gemm_scratch = p;
-  ctx->gemm_scratch_bytes = bytes;
-  return DC_OK;
-}
-
 int32_t ensure_status(dc_hip_ctx* ctx, size_t words, uint32_t* epoch_out) {
   constexpr uint32_t kEpochMask = (1u << 22) - 1;  // 22-bit epoch field in each status word
   if (ctx->status_words < words) {
@@ -345,7 +332,6 @@ DC_HIP_API int32_t dc_hip_ctx_destroy(dc_hip_ctx* ctx) {
     if (ctx->spmv_rows) (void)hipFree(ctx->spmv_rows);
     if (ctx->spmv_windows) (void)hipFree(ctx->spmv_windows);
     if (ctx->spmv_plan_mem) (void)hipFree(ctx->spmv_plan_mem);
-    if (ctx->gemm_scratch) (void)hipFree(ctx->gemm_scratch);
     (void)hipStreamDestroy(ctx->stream);
   }
   delete ctx;
