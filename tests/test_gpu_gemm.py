@@ -130,8 +130,9 @@ def test_gemm_f32_large_sampled(ctx, n):
     freivalds(c, a, b)
 
 
-# (256-multiples of m and n with k a multiple of 64 take the 256x256-tile kernel with B transposed
-# first; the others the 128x128 kernels)
+# (256-multiples of m and n with k a multiple of 64 take the 256x256-tile kernel, which reads
+# row-major B through transposing LDS reads, with 1, 2, 3, 6 and more 64-wide k tiles; the other
+# shapes the 128x128 kernels)
 @pytest.mark.parametrize("shape", [(128, 128, 64), (512, 768, 384), (100, 37, 53), (256, 256, 64),
                                    (1024, 512, 1024), (768, 1280, 192), (256, 512, 4096), (384, 256, 64),
                                    (512, 256, 128)])
