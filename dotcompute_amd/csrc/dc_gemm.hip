@@ -584,8 +584,7 @@ __global__ __launch_bounds__(kBigThreads, 1) void gemm_bf16_big_kernel(const uns
                                                                        const unsigned short* __restrict__ B,
                                                                        float* __restrict__ C, int M, int N, int K,
                                                                        int tiles_m, int tiles_n) {
-  extern __shared__ __align__(16) unsigned char smem_raw[];
-  Bf16BigSmem& sm = *reinterpret_cast<Bf16BigSmem*>(smem_raw);
+  __shared__ __align__(16) Bf16BigSmem sm;  // 128 KiB of static LDS (gfx950 has 160 KiB per CU)
   const TileCoord tc = map_tile(tiles_m, tiles_n);
   const int m0 = tc.tm * kBM2, n0 = tc.tn * kBN2;
   // wave index in a scalar register: the loads' LDS bases and scalar offsets derive from it
@@ -637,7 +636,7 @@ __global__ __launch_bounds__(kBigThreads, 1) void gemm_bf16_big_kernel(const uns
   constexpr int kSteps = kBK2 / 16;
   static_assert(kSteps == 4, "four 16-wide k steps per tile");
   const int kt_count = K / kBK2;
-  const unsigned char* lds = smem_raw;
+  const unsigned char* lds = reinterpret_cast<const unsigned char*>(&sm);
   // B fragments of a whole tile (4 steps × kNT × 2 transposing reads) in one burst. The compiler
   // cannot tell these intrinsic reads apart from the LDS the direct-to-LDS loads write, so it
   // waits for every load in flight before each of them: the burst is issued while none is (right
@@ -808,11 +807,7 @@ DC_HIP_API int32_t dc_hip_gemm_bf16(dc_hip_ctx* ctx, const uint16_t* a, const ui
   if ((m % kBM2 == 0) && (n % kBN2 == 0) && (k % kBK2 == 0) && dc::aligned16(a) && dc::aligned16(b) &&
       (int64_t)k * kBM2 * 2 < ((int64_t)1 << 31) && (int64_t)k * n * 2 < ((int64_t)1 << 31)) {
     const int tm2 = (int)(m / kBM2), tn2 = (int)(n / kBN2);
-    static const hipError_t lds_ok = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_bf16_big_kernel),
-                                                         hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                         (int)sizeof(Bf16BigSmem));
-    DC_RETURN_IF_HIP(lds_ok);
-    gemm_bf16_big_kernel<<<(unsigned)(tm2 * tn2), kBigThreads, sizeof(Bf16BigSmem), ctx->stream>>>(
+    gemm_bf16_big_kernel<<<(unsigned)(tm2 * tn2), kBigThreads, 0, ctx->stream>>>(
         A, B, c, (int)m, (int)n, (int)k, tm2, tn2);
     return dc::last_launch_status();
   }
