@@ -3,17 +3,24 @@
 // fp32: v_mfma_f32_32x32x2_f32 (fp32 inputs, fp32 accumulate).
 // bf16: v_mfma_f32_32x32x16_bf16 (bf16 inputs, fp32 accumulate).
 //
-// Block tile 128×128, 256 threads = 4 waves, each wave a 64×64 sub-tile = 2×2 MFMA 32×32 tiles
-// (64 fp32 accumulators per lane). K advances BK elements per iteration through a double-buffered
-// LDS tile; the next tile's global loads are issued before the current tile's MFMAs and stored
-// to the other buffer afterwards, so there is one barrier per iteration.
+// Kernels, by the shapes that take them:
+//   - gemm_f32_dma_kernel<T>: fp32 full tiles (m, n multiples of T = 128, or 64 when 128-tiles
+//     cannot fill the CUs; k a multiple of 32). Direct-to-LDS loads, double-buffered LDS, 4 waves
+//     of (T/2)×(T/2), two workgroups per CU.
+//   - gemm_bf16_big_kernel: bf16 with m, n multiples of 256 and k a multiple of 64. 256×256 macro
+//     tile, direct-to-LDS loads of row-major A and B, B fragments through transposing LDS reads,
+//     8 waves of 128×64, one workgroup per CU.
+//   - gemm_f32_kernel / gemm_bf16_kernel: every other shape (bounds-checked where a tile is
+//     ragged). Block tile 128×128, 4 waves of 64×64; the next tile's global loads go to registers
+//     before the current tile's MFMAs and are stored to the other LDS buffer afterwards, with B
+//     transposed on the way in (Bs[n][k], row pitch BK+4 floats), so a lane's operands for 8
+//     MFMAs are two contiguous, bank-conflict-free 16-byte LDS reads.
 //
 // Operand layout. For a 32×32 MFMA lane l supplies row (A) / column (B) l % 32 and the k-group
 // h = l / 32; the instruction pairs A and B values by (h, element index), so any assignment of
-// actual k indices to (h, element) is valid as long as A and B agree. Here lane group h takes
-// the 8 consecutive k's [8h, 8h+8) of each 16-wide k step: with A held in LDS as As[m][k] and B
-// transposed as Bs[n][k] (row pitch BK+4 floats), a lane's operands for 8 MFMAs are two
-// contiguous 16-byte LDS reads, bank-conflict free (row pitch 80 B maps 8 rows onto disjoint banks).
+// actual k indices to (h, element) is valid as long as A and B agree. bf16: lane group h takes
+// the 8 consecutive k's [8h, 8h+8) of each 16-wide k step; fp32 (one k per lane per MFMA): the
+// kernels choose k orders that make each lane's LDS reads contiguous.
 //
 // Tile order: consecutive workgroups are dispatched round-robin over the 8 XCDs (each with its own
 // L2). Block b is mapped to tile (b % 8) * (T / 8) + b / 8, so each XCD works on a contiguous
