@@ -45,6 +45,12 @@ def test_null_and_negative_arguments_are_rejected_before_any_device_work():
     assert L.dc_hip_reduce_sum_f32(None, None, 10, None) == hip.DC_ERR_INVALID_ARGUMENT
     assert L.dc_hip_gemm_f32(None, None, None, None, -1, 2, 2) == hip.DC_ERR_INVALID_ARGUMENT
     assert L.dc_hip_spmv_csr_f32(None, None, None, None, None, None, -1, 1, 0) == hip.DC_ERR_INVALID_ARGUMENT
+    assert L.dc_hip_gemm_bf16(None, None, None, None, 2, -1, 2) == hip.DC_ERR_INVALID_ARGUMENT
+    chain = hip.where_gt0_select_2x_plus_1()
+    assert L.dc_hip_linq_where_select_minmax_f32(None, C.byref(chain), None, -1, hip.LINQ_MIN, None,
+                                                  None) == hip.DC_ERR_INVALID_ARGUMENT
+    assert L.dc_hip_linq_where_select_minmax_f32(None, C.byref(chain), None, 0, 7, None,
+                                                  None) == hip.DC_ERR_INVALID_ARGUMENT  # op is neither Min nor Max
     assert L.dc_hip_ctx_create(0, None) == hip.DC_ERR_INVALID_ARGUMENT
     assert L.dc_hip_synchronize(None) == hip.DC_ERR_INVALID_ARGUMENT
 
