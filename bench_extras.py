@@ -95,7 +95,9 @@ def bench_gemm(ctx, log, time_launches, roofline, fp32_peak, bf16_peak, sizes=(1
             ms = time_launches(ctx, g, 10)
             tflops = 2.0 * n ** 3 / (ms * 1e-3) / 1e12
             out[f"gemm_bf16_{n}"] = {"ms": round(ms, 4), "TFLOP/s": round(tflops, 2),
-                                     "roofline": roofline("mfma", tflops, bf16_peak, "TFLOP/s")}
+                                     "roofline": roofline("mfma", tflops, bf16_peak, "TFLOP/s"),
+                                     "cpu_baseline": None,
+                                     "cpu_baseline_note": "the reference has no bf16 CPU GEMM to restate"}
             log(f"[bench] gemm_bf16 {n}^3: {ms:.3f} ms -> {tflops:.1f} TFLOP/s ({100 * tflops / bf16_peak:.1f}% of bf16)")
             ctx.free(ab)
             ctx.free(bb)
