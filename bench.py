@@ -214,6 +214,9 @@ def main() -> int:
     ctx.synchronize()
     wall = time.perf_counter() - t0
     kept = int(cnt.to_host()[0])
+    if kept < 0:  # the resident grid's bounded wait gave up: its output is undefined, so no number
+        raise SystemExit("headline kernel reported count -1: its resident grid was not fully resident "
+                         "(another process held CUs); no measurement")
     step_bytes = 4 * n + 4 * kept
     ms_per_step = wall * 1e3 / args.steps
     value = step_bytes / (ms_per_step * 1e-3) / 1e9

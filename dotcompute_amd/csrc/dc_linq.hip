@@ -1129,7 +1129,9 @@ extern "C" {
 
 DC_HIP_API int32_t dc_linq_chain_validate(const dc_linq_chain* chain) {
   if (!chain) return DC_ERR_INVALID_ARGUMENT;
-  if (chain->n_instr < 0 || chain->n_instr > DC_LINQ_MAX_INSTR || chain->flags != 0) return DC_ERR_INVALID_ARGUMENT;
+  if (chain->n_instr < 0 || chain->n_instr > DC_LINQ_MAX_INSTR ||
+      (chain->flags & ~DC_LINQ_FLAG_ORDERED_GRID) != 0)
+    return DC_ERR_INVALID_ARGUMENT;
   for (int i = 0; i < chain->n_instr; ++i) {
     const dc_linq_instr& in = chain->code[i];
     const bool op_ok = (in.op <= DC_LQ_STORE_S1) || (in.op >= DC_LQ_CMP_GT && in.op <= DC_LQ_MAP);
@@ -1153,7 +1155,7 @@ DC_HIP_API int32_t dc_hip_linq_where_select_f32(dc_hip_ctx* ctx, const dc_linq_c
   DC_RETURN_IF(dc_linq_chain_validate(chain));
   if (n >= (int64_t)1 << 40) return DC_ERR_INVALID_ARGUMENT;  // 40-bit counts in the status words
   DC_CTX_ENTER(ctx);
-  if (use_rounds(ctx, input, n)) {
+  if ((chain->flags & DC_LINQ_FLAG_ORDERED_GRID) == 0 && use_rounds(ctx, input, n)) {
     Canon2 canon{};
     const void* fn = rounds_kernel(rounds_mode(*chain, &canon));
     const uint32_t groups = rounds_groups(ctx);

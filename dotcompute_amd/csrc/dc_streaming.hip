@@ -66,14 +66,15 @@ __device__ inline int64_t add4(int64_t acc, dc::i32x4 v) {
   return acc + (int64_t)v.x + (int64_t)v.y + (int64_t)v.z + (int64_t)v.w;
 }
 
-// Vectors [v0, v1) of this block's chunk; the scalar tail (n % 4 elements) goes to the last block.
+// Vectors [v0, v1) of this block's chunk of the 16-byte aligned part x[h, h + 4*n4); the scalar
+// elements before it (h < 4, when x is not 16-byte aligned) and after it (< 4) go to the last block.
 template <typename In4, typename In, typename Acc>
-__device__ inline Acc chunk_partial(const In* __restrict__ x, int64_t n, bool vec_ok) {
+__device__ inline Acc chunk_partial(const In* __restrict__ x, int64_t n, int h) {
   Acc acc0 = 0, acc1 = 0;
-  const int64_t n4 = vec_ok ? (n >> 2) : 0;
+  const int64_t n4 = (n - h) >> 2;
   const int64_t per = (n4 + gridDim.x - 1) / gridDim.x;
   const int64_t v0 = min(n4, (int64_t)blockIdx.x * per), v1 = min(n4, v0 + per);
-  const In4* x4 = reinterpret_cast<const In4*>(x);
+  const In4* x4 = reinterpret_cast<const In4*>(x + h);
   int64_t i = v0 + threadIdx.x;
   for (; i + (kRedUnroll - 1) * kRedBlock < v1; i += kRedUnroll * kRedBlock) {
     In4 v[kRedUnroll];
@@ -86,31 +87,229 @@ __device__ inline Acc chunk_partial(const In* __restrict__ x, int64_t n, bool ve
     }
   }
   for (; i < v1; i += kRedBlock) acc0 = add4(acc0, dc::load_stream(x4 + i));
-  if (blockIdx.x == gridDim.x - 1)
-    for (int64_t s = (n4 << 2) + threadIdx.x; s < n; s += kRedBlock) acc1 += (Acc)x[s];
+  if (blockIdx.x == gridDim.x - 1 && threadIdx.x < 8) {
+    const int64_t s = threadIdx.x < 4 ? threadIdx.x : h + (n4 << 2) + (threadIdx.x - 4);
+    if ((threadIdx.x < 4 && s < h) || (threadIdx.x >= 4 && s < n)) acc1 += (Acc)x[s];
+  }
   return acc0 + acc1;
 }
 
-__global__ __launch_bounds__(kRedBlock) void reduce_sum_f32_pass1(const float* __restrict__ x, int64_t n, int vec_ok,
+__global__ __launch_bounds__(kRedBlock) void reduce_sum_f32_pass1(const float* __restrict__ x, int64_t n, int h,
                                                                   double* __restrict__ partials) {
   __shared__ double lds[kRedBlock / dc::kWave];
-  double acc = chunk_partial<dc::f32x4, float, double>(x, n, vec_ok != 0);
+  double acc = chunk_partial<dc::f32x4, float, double>(x, n, h);
   double t = dc::block_sum64<kRedBlock>(acc, lds);
   if (threadIdx.x == 0) partials[blockIdx.x] = t;
 }
 
-__global__ __launch_bounds__(kRedBlock) void reduce_sum_i32_pass1(const int32_t* __restrict__ x, int64_t n, int vec_ok,
-                                                                  int64_t* __restrict__ partials) {
-  __shared__ int64_t lds[kRedBlock / dc::kWave];
-  int64_t acc = chunk_partial<dc::i32x4, int32_t, int64_t>(x, n, vec_ok != 0);
-  int64_t t = dc::block_sum64<kRedBlock>(acc, lds);
-  if (threadIdx.x == 0) partials[blockIdx.x] = t;
+// ---------------------------------------------------------------------------------------------
+// Checked int32 Sum with the overflow rule of the .NET 10 BCL's Enumerable.Sum(IEnumerable<int>)
+// for array/list sources on x64 (System.Linq Sum.cs, SumSignedIntegersVectorized; reached from
+// ComputeQueryableExtensions.cs:265-267). With W = Vector<int>.Count = 8 lanes:
+//   n < 4W:  one checked running total: OverflowException as soon as a prefix sum leaves int32.
+//   n >= 4W: the elements [0, V) are summed in W wrapping lanes (lane c takes the elements whose
+//            index is c mod W, in order) and any lane add that overflows throws; then the lane
+//            totals are added in lane order with checked adds, then the elements [V, n), checked.
+//            V is where the BCL's vector loops stop (at most W elements before n; bcl_vector_end).
+// So an OverflowException happens iff (a) a prefix of some lane's subsequence leaves int32, or
+// (b) a prefix of (lane 0 total, lane 1 total, ...) leaves int32, or (c) that sum plus a prefix of
+// the scalar tail does. The exact int64 total is reported either way.
+//
+// GPU design: pass 1 (every workgroup, one contiguous chunk of 16-byte vectors) computes per lane
+// class c the chunk's class sum T_c and the sum of its positive elements P_c (int64). Pass 2 (one
+// workgroup) scans the class sums over the chunks to get each chunk's starting class prefix S_c;
+// a chunk cannot overflow class c if S_c + P_c and S_c + (T_c - P_c) both fit (every prefix inside
+// the chunk lies between them). Chunks that fail that screen (only inputs with huge magnitudes)
+// get an exact check: the chunk's elements are re-read and every class prefix inside it is
+// bounded by an ordered (sum, max prefix, min prefix) combination. Rules (b) and (c) touch at most
+// 8 + 8 values and run on one thread.
+// ---------------------------------------------------------------------------------------------
+constexpr int kBclLanes = 8;  // Vector<int>.Count on x64 (256-bit Vector<T>)
+
+__device__ inline int64_t parity_sum(int64_t v) {
+#pragma unroll
+  for (int off = 2; off < dc::kWave; off <<= 1) v += __shfl_xor(v, off, dc::kWave);
+  return v;
+}
+
+// xa = x + h is 16-byte aligned; the chunk of workgroup w is vectors [w*per, (w+1)*per) of xa's
+// first n4 vectors (per is even, so a thread's vectors all have the parity of its lane).
+// partials: [c*G + w] class sums, [(8 + c)*G + w] positive sums, c = lane class 0..7.
+__global__ __launch_bounds__(kRedBlock) void reduce_sum_i32_classes(const int32_t* __restrict__ xa, int64_t n4,
+                                                                    int64_t per, int h, int64_t* __restrict__ partials) {
+  int64_t cs[4] = {0, 0, 0, 0}, ps[4] = {0, 0, 0, 0};
+  const int64_t v0 = min(n4, (int64_t)blockIdx.x * per), v1 = min(n4, v0 + per);
+  const dc::i32x4* x4 = reinterpret_cast<const dc::i32x4*>(xa);
+  auto accumulate = [&](dc::i32x4 v) {
+    cs[0] += v.x; cs[1] += v.y; cs[2] += v.z; cs[3] += v.w;
+    ps[0] += (uint32_t)max(v.x, 0); ps[1] += (uint32_t)max(v.y, 0);
+    ps[2] += (uint32_t)max(v.z, 0); ps[3] += (uint32_t)max(v.w, 0);
+  };
+  int64_t i = v0 + threadIdx.x;
+  for (; i + (kRedUnroll - 1) * kRedBlock < v1; i += kRedUnroll * kRedBlock) {
+    dc::i32x4 v[kRedUnroll];
+#pragma unroll
+    for (int u = 0; u < kRedUnroll; ++u) v[u] = dc::load_stream(x4 + i + u * kRedBlock);
+#pragma unroll
+    for (int u = 0; u < kRedUnroll; ++u) accumulate(v[u]);
+  }
+  for (; i < v1; i += kRedBlock) accumulate(dc::load_stream(x4 + i));
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    cs[j] = parity_sum(cs[j]);
+    ps[j] = parity_sum(ps[j]);
+  }
+  __shared__ int64_t lds[kRedBlock / dc::kWave][2][8];
+  const int lane = threadIdx.x & (dc::kWave - 1), wave = threadIdx.x / dc::kWave;
+  if (lane < 2) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      lds[wave][lane][j] = cs[j];
+      lds[wave][lane][4 + j] = ps[j];
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    const int p = threadIdx.x >> 3, k = threadIdx.x & 7;
+    int64_t t = 0;
+#pragma unroll
+    for (int w = 0; w < kRedBlock / dc::kWave; ++w) t += lds[w][p][k];
+    // element h + 4*v + j has lane class (h + 4*(v & 1) + j) mod 8, and v & 1 == lane & 1 == p
+    const int cls = (h + 4 * p + (k & 3)) & (kBclLanes - 1);
+    partials[(size_t)((k >> 2) * kBclLanes + cls) * gridDim.x + blockIdx.x] = t;
+  }
+}
+
+__device__ inline bool fits_i32(int64_t v) { return v >= -2147483648LL && v <= 2147483647LL; }
+
+constexpr int kBclFinalBlock = 1024;
+
+__global__ __launch_bounds__(kBclFinalBlock) void reduce_sum_i32_bcl_final(
+    const int64_t* __restrict__ partials, int G, const int32_t* __restrict__ x, int64_t n, int h, int64_t n4,
+    int64_t V, int64_t per, int64_t* __restrict__ sum_out, int32_t* __restrict__ overflow_out) {
+  const int t = threadIdx.x, lane = t & (dc::kWave - 1), wave = t / dc::kWave;
+  if (n < 4 * kBclLanes) {  // the BCL's scalar checked loop
+    if (t == 0) {
+      int64_t s = 0;
+      int ovf = 0;
+      for (int64_t i = 0; i < n; ++i) {
+        s += x[i];
+        if (!fits_i32(s)) ovf = 1;
+      }
+      *sum_out = s;
+      if (overflow_out) *overflow_out = ovf;
+    }
+    return;
+  }
+  __shared__ int64_t wtot[kBclFinalBlock / dc::kWave][kBclLanes];
+  __shared__ int64_t lane_total[kBclLanes];
+  __shared__ int64_t cur_start[kBclLanes];
+  __shared__ int flag_list[kBclFinalBlock];
+  __shared__ int flag_count, ovf_s;
+  __shared__ int64_t tr_s[kBclFinalBlock], tr_max[kBclFinalBlock], tr_min[kBclFinalBlock];
+
+  int64_t T[kBclLanes], P[kBclLanes], start[kBclLanes];
+#pragma unroll
+  for (int c = 0; c < kBclLanes; ++c) {
+    T[c] = t < G ? partials[(size_t)c * G + t] : 0;
+    P[c] = t < G ? partials[(size_t)(kBclLanes + c) * G + t] : 0;
+  }
+  // Inclusive scan of the class sums over chunks (thread t = chunk t), per wave then across waves.
+#pragma unroll
+  for (int c = 0; c < kBclLanes; ++c) {
+    int64_t v = T[c];
+#pragma unroll
+    for (int off = 1; off < dc::kWave; off <<= 1) {
+      const int64_t y = __shfl_up(v, off, dc::kWave);
+      if (lane >= off) v += y;
+    }
+    start[c] = v;  // inclusive for now
+  }
+  if (lane == dc::kWave - 1)
+#pragma unroll
+    for (int c = 0; c < kBclLanes; ++c) wtot[wave][c] = start[c];
+  if (t == 0) {
+    flag_count = 0;
+    ovf_s = 0;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < kBclLanes; ++c) {
+    int64_t before = c < h ? (int64_t)x[c] : 0;  // the unaligned head element of class c, if any
+    for (int w = 0; w < wave; ++w) before += wtot[w][c];
+    start[c] = before + start[c] - T[c];
+  }
+  if (t == 0)
+    for (int c = 0; c < kBclLanes; ++c) {
+      int64_t tot = c < h ? (int64_t)x[c] : 0;
+      for (int w = 0; w < kBclFinalBlock / dc::kWave; ++w) tot += wtot[w][c];
+      lane_total[c] = tot;
+    }
+  bool flagged = false;
+  if (t < G)
+#pragma unroll
+    for (int c = 0; c < kBclLanes; ++c)
+      if (!fits_i32(start[c] + P[c]) || !fits_i32(start[c] + (T[c] - P[c]))) flagged = true;
+  if (flagged) flag_list[atomicAdd(&flag_count, 1)] = t;
+  __syncthreads();
+  const int nflag = flag_count;
+  for (int k = 0; k < nflag; ++k) {
+    const int f = flag_list[k];
+    if (t == f)
+      for (int c = 0; c < kBclLanes; ++c) cur_start[c] = start[c];
+    __syncthreads();
+    const int64_t e0 = h + 4 * min(n4, (int64_t)f * per), e1 = h + 4 * min(n4, (int64_t)(f + 1) * per);
+    const int64_t piece = (e1 - e0 + kBclFinalBlock - 1) / kBclFinalBlock;
+    const int64_t a = min(e1, e0 + t * piece), b = min(e1, a + piece);
+    for (int c = 0; c < kBclLanes; ++c) {
+      int64_t s = 0, mx = 0, mn = 0;  // relative prefix sum, its max and min (the empty prefix included)
+      for (int64_t i = a + ((c - a) & (kBclLanes - 1)); i < b; i += kBclLanes) {
+        s += x[i];
+        mx = max(mx, s);
+        mn = min(mn, s);
+      }
+      tr_s[t] = s;
+      tr_max[t] = mx;
+      tr_min[t] = mn;
+      __syncthreads();
+      for (int stride = 1; stride < kBclFinalBlock; stride <<= 1) {
+        if ((t & (2 * stride - 1)) == 0) {  // (left = t, right = t + stride), in sequence order
+          const int r = t + stride;
+          const int64_t ls = tr_s[t];
+          tr_max[t] = max(tr_max[t], ls + tr_max[r]);
+          tr_min[t] = min(tr_min[t], ls + tr_min[r]);
+          tr_s[t] = ls + tr_s[r];
+        }
+        __syncthreads();
+      }
+      if (t == 0 && (!fits_i32(cur_start[c] + tr_max[0]) || !fits_i32(cur_start[c] + tr_min[0]))) ovf_s = 1;
+      __syncthreads();
+    }
+    if (ovf_s) break;
+  }
+  if (t == 0) {
+    int ovf = ovf_s;
+    // The scalar elements after the last whole vector but before V, then each class's final prefix.
+    for (int64_t i = h + 4 * n4; i < V; ++i) lane_total[i & (kBclLanes - 1)] += x[i];
+    int64_t r = 0;
+    for (int c = 0; c < kBclLanes; ++c) {
+      if (!fits_i32(lane_total[c])) ovf = 1;
+      r += lane_total[c];
+      if (!fits_i32(r)) ovf = 1;  // the lane totals are added with checked int32 adds
+    }
+    for (int64_t i = V; i < n; ++i) {
+      r += x[i];
+      if (!fits_i32(r)) ovf = 1;  // the scalar tail, checked
+    }
+    *sum_out = r;
+    if (overflow_out) *overflow_out = ovf;
+  }
 }
 
 // Sums partials[0..count) in a fixed order: thread t takes t, t+1024, ... then the block tree.
 template <typename Acc>
 __global__ __launch_bounds__(kFinalBlock) void reduce_partials(const Acc* __restrict__ partials, int count,
-                                                               Acc* __restrict__ out, int32_t* __restrict__ overflow) {
+                                                               Acc* __restrict__ out) {
   __shared__ Acc lds[kFinalBlock / dc::kWave];
   Acc acc = 0;
   // Thread t adds partials t, t + 1024, t + 2048, ... in that order; eight loads go out together.
@@ -123,12 +322,7 @@ __global__ __launch_bounds__(kFinalBlock) void reduce_partials(const Acc* __rest
       if (i0 + k * kFinalBlock < count) acc += v[k];
   }
   Acc total = dc::block_sum64<kFinalBlock>(acc, lds);
-  if (threadIdx.x == 0) {
-    *out = total;
-    if constexpr (std::is_integral<Acc>::value) {
-      if (overflow) *overflow = (total > 2147483647LL || total < -2147483648LL) ? 1 : 0;
-    }
-  }
+  if (threadIdx.x == 0) *out = total;
 }
 
 // Grid for a reduction over n elements: a fixed function of n (not of the device), so results
@@ -139,6 +333,25 @@ unsigned reduce_grid(int64_t n) {
   return (unsigned)std::max<int64_t>(1, std::min<int64_t>(g, 1024));  // 2 workgroups per CU: measured best
 }
 
+// Elements before the first 16-byte boundary of x (0..3), capped at n.
+template <typename T>
+int head_to_aligned(const T* x, int64_t n) {
+  const int h = (int)(((16 - (reinterpret_cast<uintptr_t>(x) & 15)) & 15) / sizeof(T));
+  return (int)std::min<int64_t>(h, n);
+}
+
+// Where the BCL's vector loops in SumSignedIntegersVectorized stop for n >= 4W elements: a
+// do-while over blocks of 4W while index < n - 4W, then (if index < n - W) a do-while over blocks
+// of W while index < n - W. Closed form of those two loops.
+int64_t bcl_vector_end(int64_t n) {
+  const int64_t W = kBclLanes;
+  const int64_t lim1 = n - 4 * W;
+  int64_t index = 4 * W * std::max<int64_t>(1, (lim1 + 4 * W - 1) / (4 * W));
+  const int64_t lim2 = n - W;
+  if (index < lim2) index += W * ((lim2 - index + W - 1) / W);
+  return index;
+}
+
 }  // namespace
 
 namespace dc {
@@ -147,13 +360,13 @@ int32_t launch_reduce_sum_f32(dc_hip_ctx* ctx, const float* input, int64_t n, do
   unsigned grid = reduce_grid(n);
   DC_RETURN_IF(dc::ensure_partials(ctx, grid * sizeof(double)));
   double* partials = static_cast<double*>(ctx->partials);
-  reduce_sum_f32_pass1<<<grid, kRedBlock, 0, ctx->stream>>>(input, n, dc::aligned16(input) ? 1 : 0, partials);
-  reduce_partials<double><<<1, kFinalBlock, 0, ctx->stream>>>(partials, (int)grid, sum_out, nullptr);
+  reduce_sum_f32_pass1<<<grid, kRedBlock, 0, ctx->stream>>>(input, n, head_to_aligned(input, n), partials);
+  reduce_partials<double><<<1, kFinalBlock, 0, ctx->stream>>>(partials, (int)grid, sum_out);
   return dc::last_launch_status();
 }
 
 int32_t launch_reduce_partials_f64(dc_hip_ctx* ctx, const double* partials, int count, double* sum_out) {
-  reduce_partials<double><<<1, kFinalBlock, 0, ctx->stream>>>(partials, count, sum_out, nullptr);
+  reduce_partials<double><<<1, kFinalBlock, 0, ctx->stream>>>(partials, count, sum_out);
   return dc::last_launch_status();
 }
 
@@ -188,12 +401,19 @@ DC_HIP_API int32_t dc_hip_reduce_sum_f32(dc_hip_ctx* ctx, const float* input, in
 DC_HIP_API int32_t dc_hip_reduce_sum_i32(dc_hip_ctx* ctx, const int32_t* input, int64_t n, int64_t* sum_out,
                                          int32_t* overflow_out) {
   if (n < 0 || !sum_out || (n > 0 && !input)) return DC_ERR_INVALID_ARGUMENT;
+  if (n >= ((int64_t)1 << 32)) return DC_ERR_INVALID_ARGUMENT;  // int64 totals stay exact below 2^32 elements
+  if ((reinterpret_cast<uintptr_t>(input) & 3) != 0) return DC_ERR_MISALIGNED;
   DC_CTX_ENTER(ctx);
-  unsigned grid = reduce_grid(n);
-  DC_RETURN_IF(dc::ensure_partials(ctx, grid * sizeof(int64_t)));
+  const unsigned grid = reduce_grid(n);
+  DC_RETURN_IF(dc::ensure_partials(ctx, (size_t)grid * 2 * kBclLanes * sizeof(int64_t)));
   int64_t* partials = static_cast<int64_t*>(ctx->partials);
-  reduce_sum_i32_pass1<<<grid, kRedBlock, 0, ctx->stream>>>(input, n, dc::aligned16(input) ? 1 : 0, partials);
-  reduce_partials<int64_t><<<1, kFinalBlock, 0, ctx->stream>>>(partials, (int)grid, sum_out, overflow_out);
+  const int64_t V = n >= 4 * kBclLanes ? bcl_vector_end(n) : 0;
+  const int h = head_to_aligned(input, V);
+  const int64_t n4 = (V - h) >> 2;
+  const int64_t per = (((n4 + grid - 1) / grid) + 1) & ~(int64_t)1;  // even: a lane's vectors share one parity
+  reduce_sum_i32_classes<<<grid, kRedBlock, 0, ctx->stream>>>(input + h, n4, per, h, partials);
+  reduce_sum_i32_bcl_final<<<1, kBclFinalBlock, 0, ctx->stream>>>(partials, (int)grid, input, n, h, n4, V, per,
+                                                                  sum_out, overflow_out);
   return dc::last_launch_status();
 }
 

@@ -36,6 +36,9 @@ struct NotSupportedException : std::logic_error {
 struct OverflowException : std::overflow_error {
   using std::overflow_error::overflow_error;
 };
+struct IndexOutOfRangeException : std::out_of_range {
+  using std::out_of_range::out_of_range;
+};
 // A failed HIP runtime / library call (the reference raises CudaException with the CudaError).
 struct HipException : std::runtime_error {
   int32_t Status;

@@ -16,6 +16,7 @@
 // which builds the same tree C# builds for `x => x > 0f` and `x => x * 2f + 1f`.
 #pragma once
 
+#include <functional>
 #include <optional>
 
 #include "Abstractions.hpp"
@@ -165,6 +166,13 @@ class RuntimeExecutor {
   // Device-resident source (no host round trip for the input).
   QueryResult Execute(const FusedKernelPlan& plan, const IUnifiedMemoryBuffer& source, size_t n);
   Backends::Hip::HipAccelerator& Accelerator() { return *acc_; }
+
+  // Interprets the count the compaction kernel wrote. k >= 0 is the kept count. k == -1 means the
+  // resident grid's bounded wait for a tile count gave up (the device did not run every workgroup
+  // of the grid at once, e.g. because another process held CUs): the chain is then run once more
+  // through `rerunOrdered`, which uses the ticket-ordered lookback grid (it cannot stall), and
+  // that count is returned. Anything else, or a second -1, throws InvalidOperationException.
+  static int64_t ResolveCompactedCount(int64_t k, const std::function<int64_t()>& rerunOrdered);
 
  private:
   QueryResult Run(const FusedKernelPlan& plan, const float* device_in, size_t n);

@@ -445,6 +445,17 @@ std::string FusedKernelPlan::Listing() const {
 
 // ---- executor ----------------------------------------------------------------------------------------
 
+int64_t RuntimeExecutor::ResolveCompactedCount(int64_t k, const std::function<int64_t()>& rerunOrdered) {
+  if (k >= 0) return k;
+  if (k == -1) {
+    const int64_t k2 = rerunOrdered();
+    if (k2 >= 0) return k2;
+  }
+  throw InvalidOperationException(
+      "The HIP compaction kernel did not complete: its resident grid could not run all of its workgroups at "
+      "once, and the re-run on the ticket-ordered grid reported count " + std::to_string(k) + ".");
+}
+
 QueryResult RuntimeExecutor::Run(const FusedKernelPlan& plan, const float* device_in, size_t n) {
   dc_hip_ctx* ctx = acc_->Context();
   QueryResult r;
@@ -457,6 +468,16 @@ QueryResult RuntimeExecutor::Run(const FusedKernelPlan& plan, const float* devic
     acc_->Synchronize();
     int64_t k = 0;
     cnt->CopyToHost(&k, sizeof(k));
+    k = ResolveCompactedCount(k, [&]() {
+      dc_linq_chain ordered = plan.Program;
+      ordered.flags |= DC_LINQ_FLAG_ORDERED_GRID;
+      Check(dc_hip_linq_where_select_f32(ctx, &ordered, device_in, (int64_t)n, out->Data(), cnt->Data()),
+            "dc_hip_linq_where_select_f32");
+      acc_->Synchronize();
+      int64_t k2 = 0;
+      cnt->CopyToHost(&k2, sizeof(k2));
+      return k2;
+    });
     r.Count = k;
     r.Values.resize((size_t)k);
     out->CopyToHost(r.Values.data(), (size_t)k * sizeof(float));  // only the compacted prefix comes back

@@ -334,6 +334,16 @@ std::vector<float> KernelExecutionService::ExecuteOn(const KernelRegistrationInf
     }
   }
 
+  // An elementwise kernel indexes every buffer with the work-item index, so a buffer shorter than
+  // the work size would be read or written past its end: the CPU invoker throws
+  // IndexOutOfRangeException at the first such index; here the launch is refused instead.
+  if (reg.HipNeedsLength || reg.HipBuiltin != HipOp::None)
+    for (IUnifiedMemoryBuffer* b : bufferArgs)
+      if (b->Length() < totalWork)
+        throw IndexOutOfRangeException("Index was outside the bounds of the array: kernel '" + reg.Name +
+                                       "' runs " + std::to_string(totalWork) + " work items but a buffer argument holds " +
+                                       std::to_string(b->Length()) + " elements.");
+
   auto* hip = dynamic_cast<Backends::Hip::HipAccelerator*>(&accelerator);
   if (reg.HipBuiltin == HipOp::VectorAddF32 && hip && bufferArgs.size() == 3) {
     // Tuned library entry point (16-byte vector loads) for the registry's VectorAdd.

@@ -265,9 +265,13 @@ typedef struct dc_linq_instr {
   float imm;
 } dc_linq_instr;
 
+/* dc_linq_chain.flags bits. DC_LINQ_FLAG_ORDERED_GRID: run a ToArray on the ticket-ordered lookback
+ * grid even where the resident grid would be chosen (the retry after a resident grid gave up). */
+#define DC_LINQ_FLAG_ORDERED_GRID 1
+
 typedef struct dc_linq_chain {
   int32_t n_instr;
-  int32_t flags;  /* reserved, 0 */
+  int32_t flags;  /* DC_LINQ_FLAG_* bits; 0 by default */
   dc_linq_instr code[DC_LINQ_MAX_INSTR];
 } dc_linq_chain;
 
@@ -276,10 +280,12 @@ DC_HIP_API int32_t dc_linq_chain_validate(const dc_linq_chain* chain);
 
 /* Where/Select → ToArray: writes the kept, mapped elements in input order to `output` (capacity n)
  * and their number to *count_out (device int64). One pass over the input. Large 16-byte aligned
- * inputs run on a resident grid (one workgroup per CU, per-round tile counts); the others on a
- * ticket-ordered grid with a decoupled lookback (dc_hip_linq_to_array_strategy tells which).
- * *count_out is -1 if the resident grid's bounded wait for a tile count ever gave up (the device
- * did not run every workgroup of the grid at once); the output is then undefined. */
+ * inputs run on a resident grid (one workgroup per CU, per-round tile counts); the others, and
+ * chains with DC_LINQ_FLAG_ORDERED_GRID, on a ticket-ordered grid with a decoupled lookback
+ * (dc_hip_linq_to_array_strategy tells which). *count_out is -1 if the resident grid's bounded
+ * wait for a tile count ever gave up (the device did not run every workgroup of the grid at once);
+ * the output is then undefined and the caller re-runs the chain with DC_LINQ_FLAG_ORDERED_GRID,
+ * whose waits always end. */
 DC_HIP_API int32_t dc_hip_linq_where_select_f32(dc_hip_ctx* ctx, const dc_linq_chain* chain,
                                                 const float* input, int64_t n, float* output,
                                                 int64_t* count_out);

@@ -45,6 +45,7 @@ def lib() -> C.CDLL:
             "oracle_sum_f32_partitioned": (C.c_float, [_P, _i64, _i32, _P]),
             "oracle_sum_f32_compensated": (_f64, [_P, _i64]),
             "oracle_sum_i32_checked": (_i32, [_P, _i64, _P]),
+            "oracle_sum_i32_bcl": (_i32, [_P, _i64, _i32, _P]),
             "oracle_sum_i32_exact": (_i64, [_P, _i64]),
             "oracle_where_gt0_select_2x_plus_1": (_i64, [_P, _i64, _P]),
             "oracle_where_gt0_select_2x_plus_1_sum": (C.c_float, [_P, _i64, _P, _P]),
@@ -135,6 +136,16 @@ def sum_i32_checked(x: np.ndarray):
     """Returns the int32 sum, or raises OverflowError as checked Enumerable.Sum does."""
     out = C.c_int32()
     st = lib().oracle_sum_i32_checked(_p(x), x.size, C.byref(out))
+    if st == -4:
+        raise OverflowError("Arithmetic operation resulted in an overflow.")
+    return out.value
+
+
+def sum_i32_bcl(x: np.ndarray, lanes: int = 8):
+    """Enumerable.Sum(int[]) as the .NET 10 BCL computes it with Vector<int>.Count = `lanes`
+    (8 on x64): returns the int32 sum, or raises OverflowError where it throws."""
+    out = C.c_int32()
+    st = lib().oracle_sum_i32_bcl(_p(x), x.size, lanes, C.byref(out))
     if st == -4:
         raise OverflowError("Arithmetic operation resulted in an overflow.")
     return out.value

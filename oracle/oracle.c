@@ -197,6 +197,60 @@ int32_t oracle_sum_i32_checked(const int32_t* x, int64_t n, int32_t* sum_out) {
   return DC_OK;
 }
 
+/* Enumerable.Sum(IEnumerable<int>) as the .NET 10 BCL runs it for array / List<int> sources
+ * (dotnet/runtime, src/libraries/System.Linq/src/System/Linq/Sum.cs: Sum<T,TResult>(ReadOnlySpan<T>)
+ * and SumSignedIntegersVectorized; not vendored in the reference, reached from
+ * ComputeQueryableExtensions.cs:265-267). When Vector<int>.Count = W > 2 and n >= 4W it sums W
+ * wrapping int32 lanes (lane l takes elements l, l+W, l+2W, ...), tracking signed overflow of every
+ * lane add as (r ^ a) & (r ^ d) and throwing after each unrolled group of 4 vectors (then after the
+ * single-vector loop); the lane totals are then added in lane order with checked adds, then the
+ * remaining elements. Otherwise it is one checked running total. `lanes` = W (8 on x64, 4 on
+ * Arm64). Returns DC_ERR_OVERFLOW where the BCL throws OverflowException. */
+int32_t oracle_sum_i32_bcl(const int32_t* x, int64_t n, int32_t lanes, int32_t* sum_out) {
+  if (lanes > 2 && lanes <= 16 && n >= 4 * (int64_t)lanes) {
+    uint32_t acc[16] = {0};
+    const int64_t W = lanes;
+    int64_t index = 0;
+    int64_t limit = n - 4 * W;
+    do {
+      uint32_t tracking = 0;
+      for (int u = 0; u < 4; ++u)
+        for (int64_t l = 0; l < W; ++l) {
+          const uint32_t a = acc[l], d = (uint32_t)x[index + u * W + l], r = a + d;
+          tracking |= (r ^ a) & (r ^ d);
+          acc[l] = r;
+        }
+      if (tracking >> 31) return DC_ERR_OVERFLOW;
+      index += 4 * W;
+    } while (index < limit);
+    limit = n - W;
+    if (index < limit) {
+      uint32_t tracking = 0;
+      do {
+        for (int64_t l = 0; l < W; ++l) {
+          const uint32_t a = acc[l], d = (uint32_t)x[index + l], r = a + d;
+          tracking |= (r ^ a) & (r ^ d);
+          acc[l] = r;
+        }
+        index += W;
+      } while (index < limit);
+      if (tracking >> 31) return DC_ERR_OVERFLOW;
+    }
+    int64_t result = 0;
+    for (int64_t l = 0; l < W; ++l) {
+      result += (int32_t)acc[l];
+      if (result > 2147483647LL || result < -2147483648LL) return DC_ERR_OVERFLOW;
+    }
+    for (; index < n; ++index) {
+      result += x[index];
+      if (result > 2147483647LL || result < -2147483648LL) return DC_ERR_OVERFLOW;
+    }
+    if (sum_out) *sum_out = (int32_t)result;
+    return DC_OK;
+  }
+  return oracle_sum_i32_checked(x, n, sum_out);
+}
+
 int64_t oracle_sum_i32_exact(const int32_t* x, int64_t n) {
   int64_t s = 0;
   for (int64_t i = 0; i < n; ++i) s += x[i];

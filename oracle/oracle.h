@@ -50,6 +50,7 @@ float oracle_sum_f32_enumerable(const float* x, int64_t n, double* as_double);
 float oracle_sum_f32_partitioned(const float* x, int64_t n, int32_t partitions, double* as_double);
 double oracle_sum_f32_compensated(const float* x, int64_t n);
 int32_t oracle_sum_i32_checked(const int32_t* x, int64_t n, int32_t* sum_out);
+int32_t oracle_sum_i32_bcl(const int32_t* x, int64_t n, int32_t lanes, int32_t* sum_out);
 int64_t oracle_sum_i32_exact(const int32_t* x, int64_t n);
 
 /* ---- LINQ Where/Select ---- */

@@ -257,6 +257,22 @@ TEST_CPU(hip_backend_registration_skips_missing_device) {
   CHECK_THROWS(InvalidOperationException, q.ToArray());
 }
 
+TEST_CPU(compaction_give_up_is_retried_on_the_ordered_grid) {
+  // A resident grid that gave up reports count -1: the executor re-runs the chain once on the
+  // ticket-ordered grid and returns that count; a second failure or any other negative count throws.
+  int reruns = 0;
+  CHECK(RuntimeExecutor::ResolveCompactedCount(12, [&] { ++reruns; return int64_t(0); }) == 12);
+  CHECK(reruns == 0);
+  CHECK(RuntimeExecutor::ResolveCompactedCount(-1, [&] { ++reruns; return int64_t(7); }) == 7);
+  CHECK(reruns == 1);
+  CHECK_THROWS(InvalidOperationException,
+               RuntimeExecutor::ResolveCompactedCount(-1, [&] { ++reruns; return int64_t(-1); }));
+  CHECK(reruns == 2);
+  CHECK_THROWS(InvalidOperationException,
+               RuntimeExecutor::ResolveCompactedCount(-5, [&] { ++reruns; return int64_t(3); }));
+  CHECK(reruns == 2);  // only -1 (the documented give-up value) is retried
+}
+
 TEST_CPU(csr_matrix_validation_matches_reference) {
   CHECK_THROWS(ArgumentException, CsrMatrix<float>(2, 2, {1.0f}, {0}, {0, 1}));          // rowPointers != rows+1
   CHECK_THROWS(ArgumentException, CsrMatrix<float>(1, 2, {1.0f, 2.0f}, {0}, {0, 2}));   // values vs columns
@@ -320,6 +336,83 @@ TEST_GPU(compiled_kernel_from_code_object_matches) {
   CHECK(BitsEqual(r, ref));
   def.EntryPoint = "NoSuchKernel";
   CHECK_THROWS(ArgumentException, acc->CompileKernelAsync(def).get());
+}
+
+TEST_GPU(orchestrator_execute_with_device_buffers) {
+  // ExecuteWithBuffersAsync (IComputeOrchestrator.cs:51): device-resident buffers pass straight to
+  // the kernel; nothing is copied in or out.
+  ServiceCollection services;
+  services.AddDotComputeRuntime().AddHipBackend();
+  auto sp = services.BuildServiceProvider();
+  auto orch = sp->GetRequiredOrchestrator();
+  sp->Runtime()->Initialize();
+  auto& acc = *sp->Runtime()->GetAccelerators().at(0);
+  const size_t n = 250007;
+  auto a = Uniform(n, 11, 0), b = Uniform(n, 11, 1);
+  std::vector<float> ref(n), r(n);
+  oracle_vector_add_f32(a.data(), b.data(), ref.data(), (int64_t)n);
+  auto da = acc.Memory().AllocateRaw(n, ElementType::Float32), db = acc.Memory().AllocateRaw(n, ElementType::Float32),
+       dr = acc.Memory().AllocateRaw(n, ElementType::Float32);
+  da->CopyFromHost(a.data(), n * sizeof(float));
+  db->CopyFromHost(b.data(), n * sizeof(float));
+  orch->ExecuteWithBuffersAsync("VectorAdd", {da.get(), db.get(), dr.get()}, {}).get();
+  dr->CopyToHost(r.data(), n * sizeof(float));
+  CHECK(BitsEqual(r, ref));
+  // A shorter input buffer is refused before any launch (the CPU invoker throws
+  // IndexOutOfRangeException at the first index past its end).
+  auto shortB = acc.Memory().AllocateRaw(n - 1, ElementType::Float32);
+  CHECK_THROWS(IndexOutOfRangeException,
+               orch->ExecuteWithBuffersAsync("VectorAdd", {da.get(), shortB.get(), dr.get()}, {}).get());
+  std::vector<float> ha(n - 1);
+  CHECK_THROWS(IndexOutOfRangeException, orch->ExecuteAsync("VectorAdd", "HIP", {Arg(ha), Arg(b), Arg(r)}).get());
+}
+
+TEST_GPU(csr_spmv_code_object_kernel_matches_oracle) {
+  // The code-object kernel with SparseMatrixKernels.CUDASparseMatrixKernel's parameter list
+  // (values, col_indices, row_pointers, x, y, num_rows), launched through HipCompiledKernel with
+  // one wavefront per row, against float64 row sums.
+  auto acc = Gpu();
+  KernelDefinition def;
+  def.Name = "csr_spmv";
+  def.EntryPoint = "csr_spmv";
+  auto kernel = acc->CompileKernelAsync(def).get();
+  const int64_t rows = 1000000;
+  std::vector<int32_t> rp(rows + 1);
+  const int64_t nnz = oracle_gen_zipf_rowptr(rows, 2.0, 4096, 42, rp.data());
+  std::vector<int32_t> col((size_t)nnz);
+  std::vector<float> val((size_t)nnz);
+  oracle_gen_zipf_fill(rows, rows, 42, rp.data(), col.data(), val.data());
+  auto x = Uniform((size_t)rows, 42, 5, 1);
+  auto dval = acc->Memory().AllocateAsync<float>((size_t)nnz);
+  auto dcol = acc->Memory().AllocateAsync<int32_t>((size_t)nnz);
+  auto drp = acc->Memory().AllocateAsync<int32_t>((size_t)rows + 1);
+  auto dx = acc->Memory().AllocateAsync<float>((size_t)rows), dy = acc->Memory().AllocateAsync<float>((size_t)rows);
+  dval->CopyFromAsync(val).get();
+  dcol->CopyFromAsync(col).get();
+  drp->CopyFromAsync(rp).get();
+  dx->CopyFromAsync(x).get();
+  KernelArguments args;
+  args.AddBuffer(dval.get());
+  args.AddBuffer(dcol.get());
+  args.AddBuffer(drp.get());
+  args.AddBuffer(dx.get());
+  args.AddBuffer(dy.get());
+  args.AddScalar((int32_t)rows);
+  args.LaunchConfiguration.BlockSize = {256, 1, 1};
+  args.LaunchConfiguration.GridSize = {(uint32_t)((rows + 3) / 4), 1, 1};  // 4 rows (waves) per block
+  kernel->ExecuteAsync(args).get();
+  acc->SynchronizeAsync().get();
+  std::vector<float> y((size_t)rows);
+  dy->CopyToAsync(y).get();
+  std::vector<double> x64(x.begin(), x.end()), y64((size_t)rows), scale((size_t)rows), xabs((size_t)rows);
+  std::vector<float> vabs(val.size());
+  for (size_t i = 0; i < val.size(); ++i) vabs[i] = std::fabs(val[i]);
+  for (int64_t i = 0; i < rows; ++i) xabs[i] = std::fabs(x64[i]);
+  oracle_spmv_csr_f64(rp.data(), col.data(), val.data(), x64.data(), y64.data(), rows);
+  oracle_spmv_csr_f64(rp.data(), col.data(), vabs.data(), xabs.data(), scale.data(), rows);
+  int64_t bad = 0;
+  for (int64_t r = 0; r < rows; ++r) bad += std::fabs(y[r] - y64[r]) > 1e-4 * scale[r] + 1e-30;
+  CHECK(bad == 0);
 }
 
 // ============================== GPU: LINQ provider =================================================

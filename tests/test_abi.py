@@ -96,3 +96,43 @@ def test_product_zipf_graph_matches_oracle():
 def test_code_object_ships_next_to_the_library():
     assert os.path.exists(os.path.join(hip.LIB_DIR, "dc_kernels_gfx950.hsaco"))
     assert hip.load().dc_hip_default_module_path().decode().endswith("dc_kernels_gfx950.hsaco")
+
+
+# C# layouts written in INTEGRATION.md ([StructLayout(LayoutKind.Sequential)], natural alignment):
+# field -> (offset, size). The C header must place every field exactly there.
+CSHARP_LAYOUTS = {
+    "dc_hip_device_info": (376, [
+        ("name", 0, 256), ("gcn_arch_name", 256, 64), ("device_id", 320, 4), ("compute_units", 324, 4),
+        ("wave_size", 328, 4), ("max_threads_per_block", 332, 4), ("clock_khz", 336, 4),
+        ("memory_clock_khz", 340, 4), ("memory_bus_width_bits", 344, 4), ("l2_cache_bytes", 348, 4),
+        ("total_global_mem", 352, 8), ("lds_per_block", 360, 8), ("pci_bus_id", 368, 4), ("is_gfx950", 372, 4)]),
+    "dc_linq_instr": (8, [("op", 0, 1), ("src", 1, 1), ("mode", 2, 1), ("pad", 3, 1), ("imm", 4, 4)]),
+    "dc_linq_chain": (8 + 8 * 48, [("n_instr", 0, 4), ("flags", 4, 4), ("code", 8, 8 * 48)]),
+}
+
+
+def test_struct_layouts_match_the_csharp_binding(tmp_path):
+    """Compiles a probe against include/dotcompute_hip.h and checks offsetof/sizeof of every field
+    of the structs the C# binding declares (DeviceInfo, LinqInstr, LinqChain) against their
+    sequential layouts; the ctypes mirrors in dotcompute_amd/hip.py must agree too."""
+    import subprocess
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "dotcompute_hip.h"', "int main(void) {"]
+    for struct, (size, fields) in CSHARP_LAYOUTS.items():
+        lines.append(f'printf("{struct} %zu\\n", sizeof({struct}));')
+        for f, _, _ in fields:
+            lines.append(f'printf("{struct}.{f} %zu %zu\\n", offsetof({struct}, {f}), sizeof((({struct}*)0)->{f}));')
+    lines.append("return 0; }")
+    src = tmp_path / "probe.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "probe"
+    subprocess.run(["gcc", "-std=c11", "-I", os.path.join(root, "include"), str(src), "-o", str(exe)], check=True)
+    got = dict(l.split(" ", 1) for l in subprocess.run([str(exe)], capture_output=True, text=True, check=True)
+               .stdout.splitlines())
+    mirrors = {"dc_hip_device_info": hip.DeviceInfo, "dc_linq_instr": hip.LinqInstr, "dc_linq_chain": hip.LinqChain}
+    for struct, (size, fields) in CSHARP_LAYOUTS.items():
+        assert int(got[struct]) == size == C.sizeof(mirrors[struct]), struct
+        for f, off, fsize in fields:
+            assert got[f"{struct}.{f}"] == f"{off} {fsize}", (struct, f)
+            assert getattr(mirrors[struct], f).offset == off, (struct, f)

@@ -153,29 +153,111 @@ def test_sum_i32_bit_exact(ctx, n):
     ctx.reduce_sum_i32(dx, out, ovf, n)
     ctx.synchronize()
     assert out.to_host()[0] == oracle.sum_i32_exact(x)
-    assert out.to_host()[0] == oracle.sum_i32_checked(x)
+    assert out.to_host()[0] == oracle.sum_i32_bcl(x)
     assert ovf.to_host()[0] == 0
     for a in (dx, out, ovf):
         ctx.free(a)
 
 
-def test_sum_i32_overflow_is_reported(ctx):
-    x = np.full(4, 2**30, np.int32)  # 2^32 does not fit int32: checked Sum throws
-    with pytest.raises(OverflowError):
-        oracle.sum_i32_checked(x)
-    d = ctx.to_device(x)
+def gpu_sum_i32(ctx, x, offset=0):
+    """Runs dc_hip_reduce_sum_i32 on x placed `offset` ints into its allocation; returns (exact
+    int64 total, overflow flag)."""
+    n = x.size
+    d = ctx.empty(n + offset + 1, np.int32)
+    if n:
+        hip.check(hip.load().dc_hip_memcpy_h2d_async(ctx.handle, d.ptr + 4 * offset, x.ctypes.data, x.nbytes), "h2d")
+    src = hip.DeviceArray(ctx, d.ptr + 4 * offset, 4 * max(n, 1), np.dtype(np.int32), (n,))
     out = ctx.empty(1, np.int64)
     ovf = ctx.empty(1, np.int32)
-    ctx.reduce_sum_i32(d, out, ovf)
+    ctx.reduce_sum_i32(src, out, ovf, n)
     ctx.synchronize()
-    assert out.to_host()[0] == 2**32 and ovf.to_host()[0] == 1
-    x2 = np.array([2**31 - 1, 0, 0], np.int32)  # largest representable total: no overflow
-    d2 = ctx.to_device(x2)
-    ctx.reduce_sum_i32(d2, out, ovf)
-    ctx.synchronize()
-    assert out.to_host()[0] == 2**31 - 1 and ovf.to_host()[0] == 0
-    for a in (d, d2, out, ovf):
+    r = int(out.to_host()[0]), int(ovf.to_host()[0])
+    for a in (d, out, ovf):
         ctx.free(a)
+    return r
+
+
+def bcl_overflows(x):
+    try:
+        oracle.sum_i32_bcl(x)
+        return 0
+    except OverflowError:
+        return 1
+
+
+def test_sum_i32_overflow_follows_the_bcl_rule(ctx):
+    """Checked Sum throws where the .NET BCL's 8-lane vector path (or, below 32 elements, its
+    sequential loop) would: the overflow flag matches the oracle's restatement of that algorithm
+    on inputs where a prefix overflows but the total fits, and the reverse cases."""
+    big = 2**31 - 1
+
+    def vec(n, **at):
+        x = np.zeros(n, np.int32)
+        for k, v in at.items():
+            x[int(k[1:])] = v
+        return x
+
+    cases = [
+        np.full(4, 2**30, np.int32),            # total 2^32: throws
+        np.array([big, 0, 0], np.int32),        # largest total, fits
+        np.array([big, 1, -1], np.int32),       # short input: a running total overflows
+        vec(32, i0=big, i1=1, i8=-1),           # sequential prefix overflows, lanes do not: no throw
+        vec(32, i0=big, i1=-5, i8=1),           # lane 0 overflows, sequential prefixes fit: throws
+        vec(32, i8=big, i1=1, i2=-10),          # lane totals overflow in lane order: throws
+        vec(40, i0=big, i1=-1, i32=1),          # x32 in the scalar tail: fits
+        vec(41, i0=big, i1=-1, i32=1),          # x32 in lane 0: throws
+        vec(40, i32=big, i33=1, i34=-1),        # tail prefix overflows: throws
+    ]
+    for x in cases:
+        for offset in (0, 1, 2, 3):
+            total, ovf = gpu_sum_i32(ctx, x, offset)
+            assert total == int(x.astype(np.int64).sum())
+            assert ovf == bcl_overflows(x), (x[:12], x.size, offset)
+
+
+@pytest.mark.parametrize("n", [1_000_000, 16_000_000])
+def test_sum_i32_bcl_rule_on_large_inputs(ctx, n):
+    """Planted values near the int32 limit in a 1M / 16M input: the chunks holding them fail the
+    fast screen and take the exact per-lane prefix check. One lane's running total comes within
+    10^7 of 2^31 and back (no throw); then the same with 2^31 - 1 (its running total crosses unless
+    the lane's earlier prefix is negative, so the oracle decides); then lane totals whose
+    lane-order sum overflows."""
+    base = oracle.gen_uniform_i32(n, 44, 1, -1000, 1000)
+    i0 = (n // 3) & ~7
+    near = 2**31 - 1 - 10**7
+    x1 = base.copy()
+    x1[i0 + 8], x1[i0 + 8 * 1000] = near, -near        # lane 0, 1000 elements of its lane apart
+    x2 = base.copy()
+    x2[i0 + 3], x2[i0 + 3 + 8 * 5000] = 2**31 - 1, -(2**31 - 1)
+    x3 = base.copy()
+    x3[5 * 8 + 1] = near                                # lane 1 total ~ near, lane 2 total ~ near
+    x3[7 * 8 + 2] = near
+    for x in (x1, x2, x3):
+        for offset in (0, 1):
+            total, ovf = gpu_sum_i32(ctx, x, offset)
+            assert total == int(x.astype(np.int64).sum())
+            assert ovf == bcl_overflows(x), (n, offset)
+    assert bcl_overflows(x1) == 0 and bcl_overflows(x3) == 1
+
+
+def test_sum_misaligned_inputs(ctx):
+    """Inputs that start 1-3 elements past a 16-byte boundary run the vector path on the aligned
+    part (no single-workgroup fallback): same results as the aligned input."""
+    n = 3_000_001
+    xi = oracle.gen_uniform_i32(n, 45, 1, -1000, 1000)
+    xf = oracle.gen_uniform_f32(n, 45, 0)
+    ref_f = oracle.sum_f32_compensated(xf)
+    for offset in (1, 2, 3):
+        assert gpu_sum_i32(ctx, xi, offset) == (int(xi.astype(np.int64).sum()), 0)
+        d = ctx.empty(n + offset + 1, np.float32)
+        hip.check(hip.load().dc_hip_memcpy_h2d_async(ctx.handle, d.ptr + 4 * offset, xf.ctypes.data, xf.nbytes), "h2d")
+        src = hip.DeviceArray(ctx, d.ptr + 4 * offset, 4 * n, np.dtype(np.float32), (n,))
+        out = ctx.empty(1, np.float64)
+        ctx.reduce_sum_f32(src, out, n)
+        ctx.synchronize()
+        assert abs(out.to_host()[0] - ref_f) <= fp32_sum_tol(n) * abs(ref_f)
+        ctx.free(d)
+        ctx.free(out)
 
 
 @pytest.mark.slow

@@ -118,6 +118,73 @@ def test_sum_i32_exact_and_checked_semantics():
     assert oracle.sum_i32_checked(np.array([-(2**31), 0], np.int32)) == -(2**31)
 
 
+def _seq_checked(x):
+    """Sequential checked int32 running total with Python ints (the BCL's scalar loop, written
+    independently of the oracle): None where it throws."""
+    s = 0
+    for v in x.tolist():
+        s += v
+        if not -(2**31) <= s < 2**31:
+            return None
+    return s
+
+
+def _bcl(x, lanes=8):
+    try:
+        return oracle.sum_i32_bcl(np.asarray(x, np.int32), lanes)
+    except OverflowError:
+        return None
+
+
+def test_sum_i32_bcl_short_inputs_are_the_sequential_checked_loop():
+    rng = np.random.default_rng(3)
+    big = 2**31 - 1
+    for n in range(0, 32):
+        for _ in range(20):
+            x = rng.choice([big, -big - 1, 1, -1, 0, big // 2, -(big // 2)], size=n).astype(np.int32)
+            assert _bcl(x) == _seq_checked(x)
+    assert _bcl([big, 1, -1]) is None          # a running total that leaves int32 throws
+    assert _bcl([big, -1, 1]) == big
+
+
+def test_sum_i32_bcl_no_overflow_is_the_exact_sum():
+    for n in (32, 33, 39, 40, 41, 63, 64, 65, 1000, 4097, 100_003):
+        x = oracle.gen_uniform_i32(n, 17, 1, -1000, 1000)
+        assert _bcl(x) == int(x.astype(np.int64).sum())
+
+
+def test_sum_i32_bcl_lane_structure():
+    """Inputs that tell the BCL's vector path (8 lanes of element classes i mod 8, lane totals added
+    in lane order, then the tail from V) apart from a sequential running total."""
+    big = 2**31 - 1
+
+    def vec(n, **at):
+        x = np.zeros(n, np.int32)
+        for k, v in at.items():
+            x[int(k[1:])] = v
+        return x
+
+    # sequential overflows (big + 1), but lane 0 holds big - 1 and lane 1 holds 1: no throw
+    x = vec(32, i0=big, i1=1, i8=-1)
+    assert _seq_checked(x) is None and _bcl(x) == big
+    # lane 0's running total reaches 2^31 although every sequential prefix fits
+    x = vec(32, i0=big, i1=-5, i8=1)
+    assert _seq_checked(x) == big - 4 and _bcl(x) is None
+    # lane totals (big, 1, -10, ...) overflow when added in lane order; sequentially x1 + x2 comes first
+    x = vec(32, i8=big, i1=1, i2=-10)
+    assert _seq_checked(x) == big - 9 and _bcl(x) is None
+    # where the vector loops stop: n = 40 leaves [32, 40) to the scalar tail (lane 0 = {x0..x24}),
+    # n = 41 puts x32 into lane 0 (V = 40)
+    x40 = vec(40, i0=big, i1=-1, i32=1)
+    x41 = vec(41, i0=big, i1=-1, i32=1)
+    assert _bcl(x40) == big and _bcl(x41) is None
+    # a tail prefix that overflows although the final total fits
+    assert _bcl(vec(40, i32=big, i33=1, i34=-1)) is None
+    # the lane count matters: with 4 lanes (Arm64) x0 and x4 share a lane
+    x = vec(32, i0=big, i4=1, i1=-1)
+    assert _bcl(x, lanes=8) == big and _bcl(x, lanes=4) is None
+
+
 # ------------------------------------------------------------------ LINQ
 def _chain(code):
     from dotcompute_amd.hip import LinqChain
