@@ -74,6 +74,21 @@ __device__ inline T wave_sum64(T v) {
   return from_u64<T>(readlane_u64(as_u64(v), 63));
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave (lane i gets v_0 + ... + v_i) for 64-bit T:
+// row_shr 1, 2, 4, 8 scan each row of 16 lanes, then row_bcast 15 / 31 carry the row totals
+// forward. Every lane must be active.
+template <typename T>
+__device__ inline T wave_inclusive_scan64(T v) {
+  static_assert(sizeof(T) == 8, "64-bit lanes only");
+  v = v + from_u64<T>(dpp_u64<0x111, 0xF>(as_u64(v)));  // row_shr:1
+  v = v + from_u64<T>(dpp_u64<0x112, 0xF>(as_u64(v)));  // row_shr:2
+  v = v + from_u64<T>(dpp_u64<0x114, 0xF>(as_u64(v)));  // row_shr:4
+  v = v + from_u64<T>(dpp_u64<0x118, 0xF>(as_u64(v)));  // row_shr:8
+  v = v + from_u64<T>(dpp_u64<0x142, 0xA>(as_u64(v)));  // row_bcast:15 into rows 1 and 3
+  v = v + from_u64<T>(dpp_u64<0x143, 0xC>(as_u64(v)));  // row_bcast:31 into rows 2 and 3
+  return v;
+}
+
 // Block-wide sum for BLOCK threads (multiple of 64). Fixed order: wave sums, then waves 0..W-1
 // in order. Result valid in every thread. Uses `scratch` (W elements of shared memory).
 template <int BLOCK, typename T>

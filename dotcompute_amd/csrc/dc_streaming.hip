@@ -116,10 +116,11 @@ __global__ __launch_bounds__(kRedBlock) void reduce_sum_f32_pass1(const float* _
 // the scalar tail does. The exact int64 total is reported either way.
 //
 // GPU design: pass 1 (every workgroup, one contiguous chunk of 16-byte vectors) computes per lane
-// class c the chunk's class sum T_c and the sum of its positive elements P_c (int64). Pass 2 (one
-// workgroup) scans the class sums over the chunks to get each chunk's starting class prefix S_c;
-// a chunk cannot overflow class c if S_c + P_c and S_c + (T_c - P_c) both fit (every prefix inside
-// the chunk lies between them). Chunks that fail that screen (only inputs with huge magnitudes)
+// class c the chunk's class sum T_c (int64) and the chunk's largest and smallest element. Pass 2
+// (one workgroup) scans the class sums over the chunks to get each chunk's starting class prefix
+// S_c. A chunk holding k elements of class c cannot overflow that class if S_c + k*max(hi, 0) and
+// S_c + k*min(lo, 0) both fit (every prefix inside the chunk lies between them). Chunks that fail
+// that screen (inputs whose magnitudes reach about 2^31 / k, e.g. |x| >~ 6.5e4 at 256M elements)
 // get an exact check: the chunk's elements are re-read and every class prefix inside it is
 // bounded by an ordered (sum, max prefix, min prefix) combination. Rules (b) and (c) touch at most
 // 8 + 8 values and run on one thread.
@@ -134,16 +135,26 @@ __device__ inline int64_t parity_sum(int64_t v) {
 
 // xa = x + h is 16-byte aligned; the chunk of workgroup w is vectors [w*per, (w+1)*per) of xa's
 // first n4 vectors (per is even, so a thread's vectors all have the parity of its lane).
-// partials: [c*G + w] class sums, [(8 + c)*G + w] positive sums, c = lane class 0..7.
+// partials: [c*G + w] class sums (c = lane class 0..7), [8*G + w] the chunk's largest element,
+// [9*G + w] its smallest.
 __global__ __launch_bounds__(kRedBlock) void reduce_sum_i32_classes(const int32_t* __restrict__ xa, int64_t n4,
                                                                     int64_t per, int h, int64_t* __restrict__ partials) {
-  int64_t cs[4] = {0, 0, 0, 0}, ps[4] = {0, 0, 0, 0};
+  // Class sums are accumulated with a bias of 2^31 per element (x ^ 0x80000000 is x + 2^31 as an
+  // unsigned value): one 64-bit add of a zero-extended word, no sign extension; the bias is taken
+  // off at the end from the number of vectors the thread read.
+  uint64_t acc[4] = {0, 0, 0, 0};
+  int32_t hi = INT32_MIN, lo = INT32_MAX;
   const int64_t v0 = min(n4, (int64_t)blockIdx.x * per), v1 = min(n4, v0 + per);
   const dc::i32x4* x4 = reinterpret_cast<const dc::i32x4*>(xa);
   auto accumulate = [&](dc::i32x4 v) {
-    cs[0] += v.x; cs[1] += v.y; cs[2] += v.z; cs[3] += v.w;
-    ps[0] += (uint32_t)max(v.x, 0); ps[1] += (uint32_t)max(v.y, 0);
-    ps[2] += (uint32_t)max(v.z, 0); ps[3] += (uint32_t)max(v.w, 0);
+    acc[0] += (uint32_t)v.x ^ 0x80000000u;
+    acc[1] += (uint32_t)v.y ^ 0x80000000u;
+    acc[2] += (uint32_t)v.z ^ 0x80000000u;
+    acc[3] += (uint32_t)v.w ^ 0x80000000u;
+    hi = max(hi, max(v.x, v.y));
+    hi = max(hi, max(v.z, v.w));
+    lo = min(lo, min(v.x, v.y));
+    lo = min(lo, min(v.z, v.w));
   };
   int64_t i = v0 + threadIdx.x;
   for (; i + (kRedUnroll - 1) * kRedBlock < v1; i += kRedUnroll * kRedBlock) {
@@ -154,29 +165,38 @@ __global__ __launch_bounds__(kRedBlock) void reduce_sum_i32_classes(const int32_
     for (int u = 0; u < kRedUnroll; ++u) accumulate(v[u]);
   }
   for (; i < v1; i += kRedBlock) accumulate(dc::load_stream(x4 + i));
+  const int64_t mine = v1 > v0 + threadIdx.x ? (v1 - v0 - threadIdx.x + kRedBlock - 1) / kRedBlock : 0;
+  int64_t cs[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    cs[j] = parity_sum(cs[j]);
-    ps[j] = parity_sum(ps[j]);
-  }
-  __shared__ int64_t lds[kRedBlock / dc::kWave][2][8];
+  for (int j = 0; j < 4; ++j) cs[j] = parity_sum((int64_t)(acc[j] - ((uint64_t)mine << 31)));
+  __shared__ int64_t lds[kRedBlock / dc::kWave][2][4];
+  __shared__ int32_t lds_hi[kRedBlock / dc::kWave], lds_lo[kRedBlock / dc::kWave];
   const int lane = threadIdx.x & (dc::kWave - 1), wave = threadIdx.x / dc::kWave;
-  if (lane < 2) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      lds[wave][lane][j] = cs[j];
-      lds[wave][lane][4 + j] = ps[j];
-    }
+  for (int off = 1; off < dc::kWave; off <<= 1) {
+    hi = max(hi, __shfl_xor(hi, off, dc::kWave));
+    lo = min(lo, __shfl_xor(lo, off, dc::kWave));
+  }
+  if (lane < 2)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) lds[wave][lane][j] = cs[j];
+  if (lane == 0) {
+    lds_hi[wave] = hi;
+    lds_lo[wave] = lo;
   }
   __syncthreads();
-  if (threadIdx.x < 16) {
-    const int p = threadIdx.x >> 3, k = threadIdx.x & 7;
+  const unsigned G = gridDim.x;
+  if (threadIdx.x < 8) {
+    const int p = threadIdx.x >> 2, j = threadIdx.x & 3;
     int64_t t = 0;
 #pragma unroll
-    for (int w = 0; w < kRedBlock / dc::kWave; ++w) t += lds[w][p][k];
+    for (int w = 0; w < kRedBlock / dc::kWave; ++w) t += lds[w][p][j];
     // element h + 4*v + j has lane class (h + 4*(v & 1) + j) mod 8, and v & 1 == lane & 1 == p
-    const int cls = (h + 4 * p + (k & 3)) & (kBclLanes - 1);
-    partials[(size_t)((k >> 2) * kBclLanes + cls) * gridDim.x + blockIdx.x] = t;
+    partials[(size_t)((h + 4 * p + j) & (kBclLanes - 1)) * G + blockIdx.x] = t;
+  } else if (threadIdx.x == 8 || threadIdx.x == 9) {
+    int32_t m = threadIdx.x == 8 ? INT32_MIN : INT32_MAX;
+    for (int w = 0; w < kRedBlock / dc::kWave; ++w) m = threadIdx.x == 8 ? max(m, lds_hi[w]) : min(m, lds_lo[w]);
+    partials[(size_t)threadIdx.x * G + blockIdx.x] = m;
   }
 }
 
@@ -188,12 +208,32 @@ __global__ __launch_bounds__(kBclFinalBlock) void reduce_sum_i32_bcl_final(
     const int64_t* __restrict__ partials, int G, const int32_t* __restrict__ x, int64_t n, int h, int64_t n4,
     int64_t V, int64_t per, int64_t* __restrict__ sum_out, int32_t* __restrict__ overflow_out) {
   const int t = threadIdx.x, lane = t & (dc::kWave - 1), wave = t / dc::kWave;
+  // The few scalar elements, loaded once by separate threads (all independent loads in flight):
+  // n < 32: all of them; else the unaligned head [0, h), the elements [h + 4*n4, V) after the last
+  // whole vector, and the tail [V, n) (at most 8).
+  __shared__ int32_t elem[4 * kBclLanes];
+  __shared__ int64_t wpre[kBclFinalBlock / dc::kWave + 1][kBclLanes];
+  __shared__ int64_t lane_total[kBclLanes];
+  __shared__ int64_t cur_start[kBclLanes];
+  __shared__ int flag_list[kBclFinalBlock];
+  __shared__ int flag_count, ovf_s;
+  __shared__ int64_t tr_s[kBclFinalBlock], tr_max[kBclFinalBlock], tr_min[kBclFinalBlock];
+  const int64_t mid0 = h + 4 * n4;
+  if (t < 4 * kBclLanes) {
+    int64_t idx = -1;
+    if (n < 4 * kBclLanes) idx = t < n ? t : -1;
+    else if (t < 4) idx = t < h ? t : -1;
+    else if (t < 8) idx = mid0 + (t - 4) < V ? mid0 + (t - 4) : -1;
+    else if (t < 8 + 2 * kBclLanes) idx = V + (t - 8) < n ? V + (t - 8) : -1;
+    elem[t] = idx >= 0 ? x[idx] : 0;
+  }
   if (n < 4 * kBclLanes) {  // the BCL's scalar checked loop
+    __syncthreads();
     if (t == 0) {
       int64_t s = 0;
       int ovf = 0;
       for (int64_t i = 0; i < n; ++i) {
-        s += x[i];
+        s += elem[i];
         if (!fits_i32(s)) ovf = 1;
       }
       *sum_out = s;
@@ -201,55 +241,43 @@ __global__ __launch_bounds__(kBclFinalBlock) void reduce_sum_i32_bcl_final(
     }
     return;
   }
-  __shared__ int64_t wtot[kBclFinalBlock / dc::kWave][kBclLanes];
-  __shared__ int64_t lane_total[kBclLanes];
-  __shared__ int64_t cur_start[kBclLanes];
-  __shared__ int flag_list[kBclFinalBlock];
-  __shared__ int flag_count, ovf_s;
-  __shared__ int64_t tr_s[kBclFinalBlock], tr_max[kBclFinalBlock], tr_min[kBclFinalBlock];
 
-  int64_t T[kBclLanes], P[kBclLanes], start[kBclLanes];
+  int64_t T[kBclLanes], incl[kBclLanes];
 #pragma unroll
-  for (int c = 0; c < kBclLanes; ++c) {
-    T[c] = t < G ? partials[(size_t)c * G + t] : 0;
-    P[c] = t < G ? partials[(size_t)(kBclLanes + c) * G + t] : 0;
-  }
-  // Inclusive scan of the class sums over chunks (thread t = chunk t), per wave then across waves.
+  for (int c = 0; c < kBclLanes; ++c) T[c] = t < G ? partials[(size_t)c * G + t] : 0;
+  // A chunk of nv vectors holds at most (nv + 1) / 2 elements of each class.
+  const int64_t k_per_class = t < G ? (min(n4, (int64_t)(t + 1) * per) - min(n4, (int64_t)t * per) + 1) / 2 : 0;
+  const int64_t up = t < G ? k_per_class * max(partials[(size_t)8 * G + t], (int64_t)0) : 0;
+  const int64_t down = t < G ? k_per_class * min(partials[(size_t)9 * G + t], (int64_t)0) : 0;
+  // Inclusive scan of the class sums over chunks (thread t = chunk t): within each wave, then the
+  // wave totals by one thread per class.
 #pragma unroll
-  for (int c = 0; c < kBclLanes; ++c) {
-    int64_t v = T[c];
-#pragma unroll
-    for (int off = 1; off < dc::kWave; off <<= 1) {
-      const int64_t y = __shfl_up(v, off, dc::kWave);
-      if (lane >= off) v += y;
-    }
-    start[c] = v;  // inclusive for now
-  }
+  for (int c = 0; c < kBclLanes; ++c) incl[c] = dc::wave_inclusive_scan64(T[c]);
   if (lane == dc::kWave - 1)
 #pragma unroll
-    for (int c = 0; c < kBclLanes; ++c) wtot[wave][c] = start[c];
+    for (int c = 0; c < kBclLanes; ++c) wpre[wave + 1][c] = incl[c];
   if (t == 0) {
     flag_count = 0;
     ovf_s = 0;
   }
   __syncthreads();
+  if (t < kBclLanes) {  // exclusive prefix over the waves, starting from the head element of class t
+    int64_t run = t < h ? (int64_t)elem[t] : 0;
+    for (int w = 0; w < kBclFinalBlock / dc::kWave; ++w) {
+      const int64_t wt = wpre[w + 1][t];
+      wpre[w][t] = run;
+      run += wt;
+    }
+    lane_total[t] = run;
+  }
+  __syncthreads();
+  bool flagged = false;
+  int64_t start[kBclLanes];
 #pragma unroll
   for (int c = 0; c < kBclLanes; ++c) {
-    int64_t before = c < h ? (int64_t)x[c] : 0;  // the unaligned head element of class c, if any
-    for (int w = 0; w < wave; ++w) before += wtot[w][c];
-    start[c] = before + start[c] - T[c];
+    start[c] = wpre[wave][c] + incl[c] - T[c];
+    if (t < G && (!fits_i32(start[c] + up) || !fits_i32(start[c] + down))) flagged = true;
   }
-  if (t == 0)
-    for (int c = 0; c < kBclLanes; ++c) {
-      int64_t tot = c < h ? (int64_t)x[c] : 0;
-      for (int w = 0; w < kBclFinalBlock / dc::kWave; ++w) tot += wtot[w][c];
-      lane_total[c] = tot;
-    }
-  bool flagged = false;
-  if (t < G)
-#pragma unroll
-    for (int c = 0; c < kBclLanes; ++c)
-      if (!fits_i32(start[c] + P[c]) || !fits_i32(start[c] + (T[c] - P[c]))) flagged = true;
   if (flagged) flag_list[atomicAdd(&flag_count, 1)] = t;
   __syncthreads();
   const int nflag = flag_count;
@@ -290,7 +318,7 @@ __global__ __launch_bounds__(kBclFinalBlock) void reduce_sum_i32_bcl_final(
   if (t == 0) {
     int ovf = ovf_s;
     // The scalar elements after the last whole vector but before V, then each class's final prefix.
-    for (int64_t i = h + 4 * n4; i < V; ++i) lane_total[i & (kBclLanes - 1)] += x[i];
+    for (int64_t i = mid0; i < V; ++i) lane_total[i & (kBclLanes - 1)] += elem[4 + (i - mid0)];
     int64_t r = 0;
     for (int c = 0; c < kBclLanes; ++c) {
       if (!fits_i32(lane_total[c])) ovf = 1;
@@ -298,7 +326,7 @@ __global__ __launch_bounds__(kBclFinalBlock) void reduce_sum_i32_bcl_final(
       if (!fits_i32(r)) ovf = 1;  // the lane totals are added with checked int32 adds
     }
     for (int64_t i = V; i < n; ++i) {
-      r += x[i];
+      r += elem[8 + (i - V)];
       if (!fits_i32(r)) ovf = 1;  // the scalar tail, checked
     }
     *sum_out = r;
@@ -405,7 +433,7 @@ DC_HIP_API int32_t dc_hip_reduce_sum_i32(dc_hip_ctx* ctx, const int32_t* input, 
   if ((reinterpret_cast<uintptr_t>(input) & 3) != 0) return DC_ERR_MISALIGNED;
   DC_CTX_ENTER(ctx);
   const unsigned grid = reduce_grid(n);
-  DC_RETURN_IF(dc::ensure_partials(ctx, (size_t)grid * 2 * kBclLanes * sizeof(int64_t)));
+  DC_RETURN_IF(dc::ensure_partials(ctx, (size_t)grid * (kBclLanes + 2) * sizeof(int64_t)));
   int64_t* partials = static_cast<int64_t*>(ctx->partials);
   const int64_t V = n >= 4 * kBclLanes ? bcl_vector_end(n) : 0;
   const int h = head_to_aligned(input, V);
