@@ -51,6 +51,11 @@ struct dc_hip_ctx {
   int rounds_fit = -1;
   // Completion event of this context's last resident-grid launch (see dc::resident_launch_*).
   hipEvent_t resident_done = nullptr;
+
+  // Device address of the static scratch array of dc_hip_linq_where_select_sum_f32_noalloc on this
+  // context's device (resolved once per device at context creation), and the status of that lookup.
+  void* noalloc_scratch = nullptr;
+  int32_t noalloc_status = DC_ERR_NOT_FOUND;
 };
 
 struct dc_hip_event {
@@ -112,6 +117,9 @@ int32_t resident_launch_begin(dc_hip_ctx* ctx);
 int32_t resident_launch_end(dc_hip_ctx* ctx);
 // Forgets the context's event (context destruction).
 void resident_forget(dc_hip_ctx* ctx);
+// Looks up the device address of the no-alloc LINQ Sum's static scratch for ctx->device (the
+// device must be current) and stores it in ctx->noalloc_scratch. Calls no allocator.
+int32_t linq_noalloc_setup(dc_hip_ctx* ctx);
 // Grow ctx->spmv_rows / ctx->spmv_windows to at least `count` entries (caller holds the lock).
 int32_t ensure_spmv_rows(dc_hip_ctx* ctx, size_t count);
 int32_t ensure_spmv_windows(dc_hip_ctx* ctx, size_t count);

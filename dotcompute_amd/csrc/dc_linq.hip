@@ -21,6 +21,8 @@
 // Every float operation rounds once (the file is compiled with -ffp-contract=off), so the output
 // equals LINQ-to-objects bit-for-bit.
 #include <algorithm>
+#include <map>
+#include <mutex>
 
 #include <utility>
 
@@ -916,6 +918,56 @@ __global__ __launch_bounds__(kFinalBlock) void where_select_sum_pass2(const doub
   }
 }
 
+// Launches the two passes of Where/Select -> Sum with the partials in psum/pcnt (grid entries each).
+int32_t launch_where_select_sum(dc_hip_ctx* ctx, const dc_linq_chain* chain, const float* input, int64_t n,
+                                unsigned grid, double* psum, int64_t* pcnt, double* sum_out, int64_t* count_out) {
+  AffineChain aff{};
+  const bool affine = lower_affine(*chain, &aff);
+  auto kernel = affine ? where_select_sum_pass1<kModeAffine>
+                       : (program_uses_saves(*chain) ? where_select_sum_pass1<kModeInterpSaves>
+                                                     : where_select_sum_pass1<kModeInterp>);
+  kernel<<<grid, kSumBlock, 0, ctx->stream>>>(*chain, aff, input, n, dc::aligned16(input) ? 1 : 0, psum, pcnt);
+  where_select_sum_pass2<<<1, kFinalBlock, 0, ctx->stream>>>(psum, pcnt, (int)grid, sum_out, count_out);
+  return dc::last_launch_status();
+}
+
+unsigned where_select_sum_grid(int64_t n) {
+  const int64_t per_block = (int64_t)kSumBlock * 16 * 4;  // elements per block-iteration x 4
+  return (unsigned)std::max<int64_t>(1, std::min<int64_t>((n + per_block - 1) / per_block, kSumBlocksMax));
+}
+
+// Scratch of dc_hip_linq_where_select_sum_f32_noalloc: one launch's per-workgroup partials (a
+// float64 sum and an int64 count per workgroup, at most kSumBlocksMax workgroups), 16 KiB. One copy
+// per GPU, held until the process ends; every call on a GPU uses it, so calls that overlap on one
+// GPU race. Pass 1 writes every entry pass 2 reads, so nothing needs clearing between calls.
+constexpr size_t kNoAllocScratchBytes = (size_t)kSumBlocksMax * (sizeof(double) + sizeof(int64_t));
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+}  // namespace
+
+namespace dc {
+
+// Resolves the device address of `scratch` for the context's device (the device is current):
+// once per device, kept for every later context on it.
+int32_t linq_noalloc_setup(dc_hip_ctx* ctx) {
+  static std::mutex mu;
+  static std::map<int, void*> per_device;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = per_device.find(ctx->device);
+  if (it == per_device.end()) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return e != hipSuccess ? (int32_t)e : DC_ERR_NOT_FOUND;
+    it = per_device.emplace(ctx->device, p).first;
+  }
+  ctx->noalloc_scratch = it->second;
+  return DC_OK;
+}
+
+}  // namespace dc
+
+namespace {
+
 // ---- Where/Select -> Min / Max ------------------------------------------------------------------
 // Same two-pass shape as the sum. The BCL's enumerator loops (Min: the first NaN, else the first
 // smallest element; Max: NaNs skipped, the first largest, the last NaN when all are NaN) depend on
@@ -1201,19 +1253,26 @@ DC_HIP_API int32_t dc_hip_linq_where_select_sum_f32(dc_hip_ctx* ctx, const dc_li
   if (n < 0 || (n > 0 && !input)) return DC_ERR_INVALID_ARGUMENT;
   DC_RETURN_IF(dc_linq_chain_validate(chain));
   DC_CTX_ENTER(ctx);
-  const int64_t per_block = (int64_t)kSumBlock * 16 * 4;  // elements per block-iteration x 4
-  const unsigned grid = (unsigned)std::max<int64_t>(1, std::min<int64_t>((n + per_block - 1) / per_block, kSumBlocksMax));
+  const unsigned grid = where_select_sum_grid(n);
   DC_RETURN_IF(dc::ensure_partials(ctx, (size_t)grid * 16));
   double* psum = static_cast<double*>(ctx->partials);
   int64_t* pcnt = reinterpret_cast<int64_t*>(psum + grid);
-  AffineChain aff{};
-  const bool affine = lower_affine(*chain, &aff);
-  auto kernel = affine ? where_select_sum_pass1<kModeAffine>
-                       : (program_uses_saves(*chain) ? where_select_sum_pass1<kModeInterpSaves>
-                                                     : where_select_sum_pass1<kModeInterp>);
-  kernel<<<grid, kSumBlock, 0, ctx->stream>>>(*chain, aff, input, n, dc::aligned16(input) ? 1 : 0, psum, pcnt);
-  where_select_sum_pass2<<<1, kFinalBlock, 0, ctx->stream>>>(psum, pcnt, (int)grid, sum_out, count_out);
-  return dc::last_launch_status();
+  return launch_where_select_sum(ctx, chain, input, n, grid, psum, pcnt, sum_out, count_out);
+}
+
+DC_HIP_API int32_t dc_hip_linq_where_select_sum_f32_noalloc(dc_hip_ctx* ctx, const dc_linq_chain* chain,
+                                                            const float* input, int64_t n, double* sum_out,
+                                                            int64_t* count_out) {
+  if (n < 0 || (n > 0 && !input)) return DC_ERR_INVALID_ARGUMENT;
+  DC_RETURN_IF(dc_linq_chain_validate(chain));
+  DC_CTX_ENTER(ctx);
+  if (ctx->noalloc_status != DC_OK) return ctx->noalloc_status;  // the symbol lookup at set-up failed
+  const unsigned grid = where_select_sum_grid(n);
+  // The grid is capped, so every n fits; the check keeps that invariant explicit.
+  if ((size_t)grid * 16 > kNoAllocScratchBytes) return DC_ERR_OUT_OF_MEMORY;
+  double* psum = static_cast<double*>(ctx->noalloc_scratch);  // never `scratch` itself: a host stand-in
+  int64_t* pcnt = reinterpret_cast<int64_t*>(psum + grid);
+  return launch_where_select_sum(ctx, chain, input, n, grid, psum, pcnt, sum_out, count_out);
 }
 
 DC_HIP_API int32_t dc_hip_linq_where_select_minmax_f32(dc_hip_ctx* ctx, const dc_linq_chain* chain,

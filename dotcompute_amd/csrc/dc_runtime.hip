@@ -313,6 +313,9 @@ DC_HIP_API int32_t dc_hip_ctx_create(int32_t device, dc_hip_ctx** out) {
     delete ctx;
     return st;
   }
+  // Set-up of the allocation-free entry point (device current): its status is kept and returned by
+  // that entry point, so a failed lookup does not stop the context from serving everything else.
+  ctx->noalloc_status = dc::linq_noalloc_setup(ctx);
   *out = ctx;
   return DC_OK;
 }

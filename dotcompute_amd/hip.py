@@ -146,6 +146,7 @@ SIGNATURES: dict[str, list] = {
     "dc_linq_chain_validate": [C.POINTER(LinqChain)],
     "dc_hip_linq_where_select_f32": [_P, C.POINTER(LinqChain), _P, _i64, _P, _P],
     "dc_hip_linq_where_select_sum_f32": [_P, C.POINTER(LinqChain), _P, _i64, _P, _P],
+    "dc_hip_linq_where_select_sum_f32_noalloc": [_P, C.POINTER(LinqChain), _P, _i64, _P, _P],
     "dc_hip_linq_where_select_minmax_f32": [_P, C.POINTER(LinqChain), _P, _i64, _i32, _P, _P],
     "dc_hip_linq_to_array_strategy": [_P, _P, _i64, _P],
     "dc_hip_gemm_f32": [_P, _P, _P, _P, _i64, _i64, _i64],

@@ -299,6 +299,15 @@ DC_HIP_API int32_t dc_hip_linq_to_array_strategy(dc_hip_ctx* ctx, const float* i
 DC_HIP_API int32_t dc_hip_linq_where_select_sum_f32(dc_hip_ctx* ctx, const dc_linq_chain* chain,
                                                     const float* input, int64_t n,
                                                     double* sum_out, int64_t* count_out);
+/* dc_hip_linq_where_select_sum_f32 that allocates nothing: for callers that cannot call
+ * hipMalloc (code under HIP graph capture, tight serving loops, harnesses that forbid allocation).
+ * No counterpart in the reference. Same kernels, same results bit for bit; the per-workgroup partials
+ * live in a 16 KiB static device array (one per GPU, resolved at context creation) instead of
+ * context scratch that grows on demand. Every n fits (the grid is capped at 1024 workgroups).
+ * Calls that overlap on one GPU, from any context, share that array and race: serialise them. */
+DC_HIP_API int32_t dc_hip_linq_where_select_sum_f32_noalloc(dc_hip_ctx* ctx, const dc_linq_chain* chain,
+                                                            const float* input, int64_t n,
+                                                            double* sum_out, int64_t* count_out);
 /* Where/Select → Min or Max of the kept, mapped elements: the result to *value_out (device float)
  * and the number of kept elements to *count_out (device int64; 0 = empty sequence, *value_out is
  * then unspecified and the managed layer throws InvalidOperationException). Replaces the reference's
