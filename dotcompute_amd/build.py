@@ -2,7 +2,8 @@
 
 Produces, in-tree:
   dotcompute_amd/lib/libdotcompute_hip.so     the C-ABI library (include/dotcompute_hip.h)
-  dotcompute_amd/lib/dc_kernels_gfx950.hsaco  code object for the generic module-load path
+  dotcompute_amd/lib/dc_kernels_gfx950.hsaco  code object for the generic module-load path: the
+                                              kernels generated from dotcompute_amd/kernels/*.cs
   dotcompute_amd/lib/libdotcompute_host.so    C++ host layer (orchestrator, LINQ provider, algorithms)
   dotcompute_amd/lib/dc_host_tests             C++ tests of the host layer
 Run: python -m dotcompute_amd.build
@@ -20,6 +21,8 @@ CSRC = os.path.join(PKG, "csrc")
 HOST = os.path.join(PKG, "host")
 LIB = os.path.join(PKG, "lib")
 BUILD = os.path.join(PKG, "_build")
+GENERATED = os.path.join(BUILD, "generated")
+KERNELS = os.path.join(PKG, "kernels")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -60,12 +63,24 @@ def build_hip_library(jobs: int = 8) -> str:
     return out
 
 
+def generate_kernels() -> list:
+    """Translates the [Kernel] methods of dotcompute_amd/kernels/*.cs: the HIP kernels go into the
+    code object, the registry into the host library (KernelRegistry.g.cpp)."""
+    sys.path.insert(0, ROOT)
+    from dotcompute_amd.generator import generate
+
+    cs = sorted(os.path.join(KERNELS, f) for f in os.listdir(KERNELS) if f.endswith(".cs"))
+    return generate(cs, GENERATED, root=ROOT)
+
+
 def build_code_object() -> str:
+    """The code object of the module-load path: generated kernels + csr_spmv. -fwrapv gives signed
+    integer overflow C#'s wrapping meaning; divide and sqrt are correctly rounded, as in .NET."""
     os.makedirs(LIB, exist_ok=True)
     out = os.path.join(LIB, "dc_kernels_gfx950.hsaco")
-    _run([HIPCC, "--genco", f"--offload-arch={ARCH}", "-O3", "-ffp-contract=off",
-          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-          os.path.join(CSRC, "dc_module_kernels.hip"), "-o", out + ".tmp"])
+    _run([HIPCC, "--genco", f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-ffp-contract=off", "-fwrapv",
+          "-fhip-fp32-correctly-rounded-divide-sqrt", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          "-I", GENERATED, "-I", CSRC, os.path.join(CSRC, "dc_module_kernels.hip"), "-o", out + ".tmp"])
     os.replace(out + ".tmp", out)
     return out
 
@@ -74,6 +89,7 @@ def build_host_layer() -> str:
     """C++ host layer (g++, links libdotcompute_hip.so) and its test binary (tests/cpp, which also
     links the CPU oracle as its checker)."""
     srcs = sorted(os.path.join(HOST, "src", f) for f in os.listdir(os.path.join(HOST, "src")) if f.endswith(".cpp"))
+    srcs.append(os.path.join(GENERATED, "KernelRegistry.g.cpp"))
     inc = ["-I", os.path.join(HOST, "include"), "-I", os.path.join(ROOT, "include")]
     flags = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter", "-pthread", "-ffp-contract=off"]
     out = os.path.join(LIB, "libdotcompute_host.so")
@@ -96,6 +112,7 @@ def build_oracle() -> str:
 
 
 def build_all() -> None:
+    generate_kernels()
     with cf.ThreadPoolExecutor(max_workers=3) as ex:
         f_lib = ex.submit(build_hip_library)
         f_co = ex.submit(build_code_object)

@@ -1,25 +1,18 @@
 // dc_module_kernels.hip — the code object (dc_kernels_gfx950.hsaco) behind the generic
 // module-load + launch path (dc_hip_module_load / dc_hip_launch_kernel), i.e. what the managed
-// HipCompiledKernel resolves by registry name. Entry points keep the parameter lists of the
-// kernels the reference generates, so KernelArguments marshal unchanged.
+// HipCompiledKernel resolves by registry name: the kernels the generator translated from the
+// [Kernel] methods of dotcompute_amd/kernels/*.cs (dc_generated_kernels.hip, written into the build
+// directory), and a hand-written kernel with the parameter list of the reference's CUDA SpMV string.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
 
-// [Kernel] VectorAdd as KernelExecutionMetadataEmitter emits it for CUDA: buffers in parameter
-// order, then the implicit `__length` scalar that KernelExecutionService appends
-// (src/Runtime/DotCompute.Generators/Kernel/Generation/KernelExecutionMetadataEmitter.cs:65-105,
-// src/Runtime/DotCompute.Runtime/Services/KernelExecutionService.cs:312-315). Launched 1-D with
-// block 256 and grid ceil(N/256) (KernelExecutionService.cs:342-354).
-extern "C" __global__ __launch_bounds__(256) void VectorAdd(const float* __restrict__ a, const float* __restrict__ b,
-                                                            float* __restrict__ result, const unsigned int __length) {
-  const unsigned int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx < __length) result[idx] = a[idx] + b[idx];
-}
+#include "dc_generated_kernels.hip"
 
 // Sparse y = A·x with one wavefront per row (64 lanes stride the row's nonzeros, then a wave
 // reduction); parameter list of SparseMatrixKernels.CUDASparseMatrixKernel
 // (src/Extensions/DotCompute.Algorithms/Kernels/LinearAlgebra/SparseMatrixKernels.cs:47-75).
+// Launch: blocks of 256 threads, 4 rows per block.
 extern "C" __global__ __launch_bounds__(256) void csr_spmv(const float* __restrict__ values,
                                                            const int* __restrict__ col_indices,
                                                            const int* __restrict__ row_pointers,

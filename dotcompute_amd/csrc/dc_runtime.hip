@@ -279,6 +279,7 @@ DC_HIP_API int32_t dc_hip_ctx_create(int32_t device, dc_hip_ctx** out) {
   // The kernels are built for gfx950 only; refuse other devices instead of failing at launch.
   if (!info.is_gfx950) return DC_ERR_UNSUPPORTED;
   DC_RETURN_IF_HIP(hipSetDevice(device));
+  (void)hipGetLastError();  // start from a clean error slot: the launch checks below read it
   dc_hip_ctx* ctx = new dc_hip_ctx();
   ctx->device = device;
   ctx->cu_count = info.compute_units;
@@ -380,6 +381,14 @@ DC_HIP_API int32_t dc_hip_malloc_host(dc_hip_ctx* ctx, size_t bytes, void** host
   DC_CTX_ENTER(ctx);
   if (bytes == 0) return DC_OK;
   DC_RETURN_IF_HIP(hipHostMalloc(host_ptr, bytes, hipHostMallocDefault));
+  return DC_OK;
+}
+
+DC_HIP_API int32_t dc_hip_host_device_pointer(dc_hip_ctx* ctx, void* host_ptr, void** device_ptr) {
+  if (!host_ptr || !device_ptr) return DC_ERR_INVALID_ARGUMENT;
+  *device_ptr = nullptr;
+  DC_CTX_ENTER(ctx);
+  DC_RETURN_IF_HIP(hipHostGetDevicePointer(device_ptr, host_ptr, 0));
   return DC_OK;
 }
 
@@ -504,6 +513,7 @@ DC_HIP_API int32_t dc_hip_module_get_function(dc_hip_module* module, const char*
   DC_RETURN_IF_HIP(hipSetDevice(module->device));
   hipFunction_t f = nullptr;
   hipError_t e = hipModuleGetFunction(&f, module->mod, name);
+  if (e != hipSuccess) (void)hipGetLastError();  // a failed lookup must not surface in a later call
   if (e == hipErrorNotFound) return DC_ERR_NOT_FOUND;
   DC_RETURN_IF_HIP(e);
   *function = reinterpret_cast<void*>(f);

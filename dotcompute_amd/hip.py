@@ -65,6 +65,17 @@ class DeviceInfo(C.Structure):
     ]
 
 
+DC_GEN_MAX_BUFFERS = 16
+DC_GEN_BLOCK = 256
+DC_GEN_ERR_INDEX, DC_GEN_ERR_DIVIDE_BY_ZERO, DC_GEN_ERR_OVERFLOW = 0, 1, 2
+
+
+class GenLaunch(C.Structure):
+    """dc_gen_launch: the launch block a generated [Kernel] takes after its buffers and scalars."""
+    _fields_ = [("work", C.c_int64), ("epoch", C.c_uint32), ("reserved", C.c_uint32),
+                ("error", C.c_void_p), ("len", C.c_int64 * DC_GEN_MAX_BUFFERS)]
+
+
 class LinqInstr(C.Structure):
     _fields_ = [("op", C.c_uint8), ("src", C.c_uint8), ("mode", C.c_uint8), ("pad", C.c_uint8), ("imm", C.c_float)]
 
@@ -147,6 +158,7 @@ SIGNATURES: dict[str, list] = {
     "dc_hip_linq_where_select_f32": [_P, C.POINTER(LinqChain), _P, _i64, _P, _P],
     "dc_hip_linq_where_select_sum_f32": [_P, C.POINTER(LinqChain), _P, _i64, _P, _P],
     "dc_hip_linq_where_select_sum_f32_noalloc": [_P, C.POINTER(LinqChain), _P, _i64, _P, _P],
+    "dc_hip_host_device_pointer": [_P, _P, _P],
     "dc_hip_linq_where_select_minmax_f32": [_P, C.POINTER(LinqChain), _P, _i64, _i32, _P, _P],
     "dc_hip_linq_to_array_strategy": [_P, _P, _i64, _P],
     "dc_hip_gemm_f32": [_P, _P, _P, _P, _i64, _i64, _i64],

@@ -39,6 +39,9 @@ struct OverflowException : std::overflow_error {
 struct IndexOutOfRangeException : std::out_of_range {
   using std::out_of_range::out_of_range;
 };
+struct DivideByZeroException : std::domain_error {
+  using std::domain_error::domain_error;
+};
 // A failed HIP runtime / library call (the reference raises CudaException with the CudaError).
 struct HipException : std::runtime_error {
   int32_t Status;
@@ -76,7 +79,7 @@ struct AcceleratorInfo {
 };
 
 // ---- memory (IUnifiedMemoryBuffer / IUnifiedMemoryManager) ------------------------------------
-enum class ElementType : int32_t { Float32, Int32, UInt32, Int64, Float64, UInt16 };
+enum class ElementType : int32_t { Float32, Int32, UInt32, Int64, Float64, UInt16, UInt64, Int16, UInt8, Int8, Bool };
 size_t ElementSize(ElementType t);
 
 template <typename T>
@@ -87,6 +90,10 @@ template <> struct ElementTypeOf<uint32_t> { static constexpr ElementType value 
 template <> struct ElementTypeOf<int64_t> { static constexpr ElementType value = ElementType::Int64; };
 template <> struct ElementTypeOf<double> { static constexpr ElementType value = ElementType::Float64; };
 template <> struct ElementTypeOf<uint16_t> { static constexpr ElementType value = ElementType::UInt16; };
+template <> struct ElementTypeOf<uint64_t> { static constexpr ElementType value = ElementType::UInt64; };
+template <> struct ElementTypeOf<int16_t> { static constexpr ElementType value = ElementType::Int16; };
+template <> struct ElementTypeOf<uint8_t> { static constexpr ElementType value = ElementType::UInt8; };
+template <> struct ElementTypeOf<int8_t> { static constexpr ElementType value = ElementType::Int8; };
 
 // Untyped device buffer (IUnifiedMemoryBuffer). CopyFromAsync/CopyToAsync move host <-> device
 // (IUnifiedMemoryBuffer.cs:236,246); both complete before the returned future is ready.
@@ -100,6 +107,10 @@ class IUnifiedMemoryBuffer {
   virtual bool IsDisposed() const = 0;
   virtual void CopyFromHost(const void* src, size_t bytes, size_t offset_bytes = 0) = 0;
   virtual void CopyToHost(void* dst, size_t bytes, size_t offset_bytes = 0) const = 0;
+  // Enqueue the copy on the accelerator's stream without waiting; it has completed once the
+  // accelerator synchronises. The host memory must stay valid until then.
+  virtual void EnqueueCopyFromHost(const void* src, size_t bytes) { CopyFromHost(src, bytes); }
+  virtual void EnqueueCopyToHost(void* dst, size_t bytes) const { CopyToHost(dst, bytes); }
   virtual void Dispose() = 0;
 };
 
@@ -156,7 +167,11 @@ struct KernelLaunchConfiguration {
   uint32_t SharedMemoryBytes = 0;
 };
 
-using ScalarValue = std::variant<int32_t, uint32_t, int64_t, float, double>;
+// A by-value struct argument passed as raw bytes (the launch block of generated kernels).
+struct RawArgument {
+  std::vector<uint8_t> Bytes;
+};
+using ScalarValue = std::variant<int32_t, uint32_t, int64_t, uint64_t, float, double, RawArgument>;
 
 // Buffers first, then scalars, in parameter order (KernelArguments.cs:11-38; the orchestrator
 // builds them in that order, KernelExecutionService.cs:409-443).

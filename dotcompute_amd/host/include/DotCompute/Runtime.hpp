@@ -25,7 +25,7 @@ struct HostArray {
   size_t Length = 0;
   ElementType Type = ElementType::Float32;
 };
-using KernelArg = std::variant<HostArray, IUnifiedMemoryBuffer*, int32_t, uint32_t, int64_t, float, double>;
+using KernelArg = std::variant<HostArray, IUnifiedMemoryBuffer*, int32_t, uint32_t, int64_t, uint64_t, float, double>;
 
 template <typename T>
 KernelArg Arg(std::vector<T>& v) {
@@ -38,33 +38,52 @@ KernelArg Arg(T scalar) {
 }
 
 // ---- registry -----------------------------------------------------------------------------------
+// [Kernel(Backends = ...)] flags (src/Runtime/DotCompute.Generators.Attributes/KernelBackends.cs:
+// 26-46) with a HIP flag beside CUDA/Metal/OpenCL.
+enum class KernelBackends : int32_t { CPU = 1, CUDA = 2, Metal = 4, OpenCL = 8, HIP = 16, All = 1 | 2 | 4 | 8 | 16 };
+std::vector<std::string> BackendNames(int32_t flags);
+
 struct KernelParameterInfo {
   std::string Name;
   ElementType Type = ElementType::Float32;
   bool IsBuffer = false;
-  bool IsReadOnly = true;
+  bool IsReadOnly = true;   // ReadOnlySpan<T> (KernelExecutionMetadataEmitter.GetIsReadOnly)
+  // What the body does with a buffer (from the generator's analysis): the orchestrator copies in
+  // only buffers the kernel reads and copies back only those it writes. Conservative defaults.
+  bool IsRead = true;
+  bool IsWritten = !IsReadOnly;
 };
 
-// Built-in op bindings: a registry kernel can be served by one of the library's tuned entry
-// points instead of a module launch (VectorAdd -> dc_hip_vector_add_f32).
-enum class HipOp { None, VectorAddF32 };
+// How a registry kernel's HIP entry point takes its arguments.
+//  Plain:     buffers, scalars, then `unsigned __length` when HipNeedsLength (the reference's
+//             generated CUDA convention); launched with DeriveLaunch.
+//  Generated: buffers, scalars, then a dc_gen_launch block (include/dotcompute_hip.h); launched
+//             over the flat work range with bounds-checked accesses and C# exceptions reported back.
+enum class HipKernelAbi { Plain, Generated };
 
 struct KernelRegistrationInfo {
   std::string Name;
   std::string FullName;
+  std::string Namespace;
+  std::string ContainingType;
   std::vector<std::string> SupportedBackends;  // [Kernel(Backends=...)]; default CPU only
+  int32_t VectorSize = 8;
+  bool IsParallel = true;
   std::vector<KernelParameterInfo> Parameters;
   int32_t Dimensions = 1;
   // HIP slot (what CudaSource / CudaEntryPoint / CudaNeedsLength are for CUDA,
-  // KernelExecutionService_Simplified.cs:567-585): a prebuilt gfx950 entry point.
+  // KernelExecutionService_Simplified.cs:567-585): the entry point in the gfx950 code object,
+  // the HIP source it was built from, or why the body has no HIP translation.
   std::string HipEntryPoint;
   bool HipNeedsLength = false;
-  HipOp HipBuiltin = HipOp::None;
+  HipKernelAbi HipAbi = HipKernelAbi::Plain;
+  std::string HipSource;
+  std::string HipDiagnostic;
 };
 
 namespace Generated {
-// The registry the source generator would emit for the kernels of this build (the README's
-// VectorAdd quick start).
+// The registry the build generates from the [Kernel] methods of dotcompute_amd/kernels/*.cs
+// (KernelRegistry.g.cpp, written by dotcompute_amd/generator).
 struct KernelRegistry {
   static std::vector<KernelRegistrationInfo> GetAllKernels();
 };
@@ -168,6 +187,8 @@ class KernelExecutionService final : public IComputeOrchestrator {
   void EnsureInitialized();
   std::vector<float> ExecuteOn(const KernelRegistrationInfo& reg, IAccelerator& accelerator,
                                std::vector<KernelArg>& args);
+  std::vector<float> ExecuteGenerated(const KernelRegistrationInfo& reg, Backends::Hip::HipAccelerator& accelerator,
+                                      std::vector<KernelArg>& args);
   std::shared_ptr<ICompiledKernel> GetCompiled(const KernelRegistrationInfo& reg, IAccelerator& accelerator);
 
   std::shared_ptr<AcceleratorRuntime> runtime_;

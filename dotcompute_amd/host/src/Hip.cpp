@@ -1,7 +1,9 @@
 // Hip.cpp — HipAccelerator, HipMemoryManager, HipBuffer, HipCompiledKernel.
 #include "DotCompute/Backends/Hip.hpp"
 
+#include <algorithm>
 #include <cstring>
+#include <type_traits>
 
 namespace DotCompute {
 
@@ -27,8 +29,13 @@ size_t ElementSize(ElementType t) {
     case ElementType::Int32:
     case ElementType::UInt32: return 4;
     case ElementType::Int64:
+    case ElementType::UInt64:
     case ElementType::Float64: return 8;
-    case ElementType::UInt16: return 2;
+    case ElementType::UInt16:
+    case ElementType::Int16: return 2;
+    case ElementType::UInt8:
+    case ElementType::Int8:
+    case ElementType::Bool: return 1;
   }
   return 1;
 }
@@ -49,50 +56,118 @@ void Check(int32_t status, const char* what) {
   }
 }
 
+// ---- DevicePool --------------------------------------------------------------------------------
+
+size_t DevicePool::RoundedSize(size_t bytes) {
+  // 256 B granules below 64 KiB, 4 KiB granules above: the same request always maps to one class.
+  const size_t g = bytes < (64u << 10) ? 256 : 4096;
+  return (std::max<size_t>(bytes, 1) + g - 1) / g * g;
+}
+
+void* DevicePool::Acquire(size_t bytes) {
+  const size_t r = RoundedSize(bytes);
+  {
+    std::lock_guard<std::mutex> lock(mu_);
+    auto it = free_.find(r);
+    if (it != free_.end() && !it->second.empty()) {
+      void* p = it->second.back();
+      it->second.pop_back();
+      cached_ -= r;
+      ++hits_;
+      return p;
+    }
+  }
+  void* p = nullptr;
+  int32_t st = dc_hip_malloc(ctx_.get(), r, &p);
+  if (st != DC_OK) {
+    // Out of memory with blocks parked here: return them to the device and try once more.
+    std::map<size_t, std::vector<void*>> parked;
+    {
+      std::lock_guard<std::mutex> lock(mu_);
+      parked.swap(free_);
+      cached_ = 0;
+    }
+    for (auto& [sz, v] : parked)
+      for (void* q : v) dc_hip_free(ctx_.get(), q);
+    Check(dc_hip_malloc(ctx_.get(), r, &p), "dc_hip_malloc");
+  }
+  return p;
+}
+
+void DevicePool::Release(void* ptr, size_t bytes) {
+  if (!ptr) return;
+  const size_t r = RoundedSize(bytes);
+  {
+    std::lock_guard<std::mutex> lock(mu_);
+    if (cached_ + r <= kMaxCachedBytes) {
+      free_[r].push_back(ptr);
+      cached_ += r;
+      return;
+    }
+  }
+  dc_hip_free(ctx_.get(), ptr);
+}
+
+size_t DevicePool::CachedBytes() const {
+  std::lock_guard<std::mutex> lock(mu_);
+  return cached_;
+}
+
+DevicePool::~DevicePool() {
+  for (auto& [sz, v] : free_)
+    for (void* q : v) dc_hip_free(ctx_.get(), q);
+}
+
 // ---- HipAllocation -----------------------------------------------------------------------------
 
-HipAllocation::HipAllocation(std::shared_ptr<dc_hip_ctx> ctx, size_t bytes) : ctx_(std::move(ctx)), bytes_(bytes) {
-  if (bytes_ > 0) Check(dc_hip_malloc(ctx_.get(), bytes_, &ptr_), "dc_hip_malloc");
+HipAllocation::HipAllocation(std::shared_ptr<dc_hip_ctx> ctx, std::shared_ptr<DevicePool> pool, size_t bytes)
+    : ctx_(std::move(ctx)), pool_(std::move(pool)), bytes_(bytes) {
+  if (bytes_ > 0) ptr_ = pool_->Acquire(bytes_);
 }
 
 HipAllocation::~HipAllocation() {
-  if (ptr_) dc_hip_free(ctx_.get(), ptr_);
+  if (ptr_) pool_->Release(ptr_, bytes_);
 }
 
 void HipAllocation::Dispose() {
-  if (ptr_) Check(dc_hip_free(ctx_.get(), ptr_), "dc_hip_free");
+  if (ptr_) pool_->Release(ptr_, bytes_);
   ptr_ = nullptr;
   disposed_ = true;
 }
 
-void HipAllocation::CopyFromHost(const void* src, size_t bytes, size_t offset_bytes) {
+void HipAllocation::CopyFromHost(const void* src, size_t bytes, size_t offset_bytes, bool wait) {
   if (disposed_) throw InvalidOperationException("buffer has been disposed");
   if (offset_bytes + bytes > bytes_) throw ArgumentException("copy exceeds the buffer size");
   if (bytes == 0) return;
   if (!src) throw ArgumentNullException("source");
   Check(dc_hip_memcpy_h2d_async(ctx_.get(), static_cast<char*>(ptr_) + offset_bytes, src, bytes), "h2d");
-  Check(dc_hip_synchronize(ctx_.get()), "dc_hip_synchronize");
+  if (wait) Check(dc_hip_synchronize(ctx_.get()), "dc_hip_synchronize");
 }
 
-void HipAllocation::CopyToHost(void* dst, size_t bytes, size_t offset_bytes) const {
+void HipAllocation::CopyToHost(void* dst, size_t bytes, size_t offset_bytes, bool wait) const {
   if (disposed_) throw InvalidOperationException("buffer has been disposed");
   if (offset_bytes + bytes > bytes_) throw ArgumentException("copy exceeds the buffer size");
   if (bytes == 0) return;
   if (!dst) throw ArgumentNullException("destination");
   Check(dc_hip_memcpy_d2h_async(ctx_.get(), dst, static_cast<const char*>(ptr_) + offset_bytes, bytes), "d2h");
-  Check(dc_hip_synchronize(ctx_.get()), "dc_hip_synchronize");
+  if (wait) Check(dc_hip_synchronize(ctx_.get()), "dc_hip_synchronize");
 }
 
 // ---- HipMemoryManager -------------------------------------------------------------------------
 
 std::shared_ptr<IUnifiedMemoryBuffer> HipMemoryManager::AllocateRaw(size_t count, ElementType type) {
   switch (type) {
-    case ElementType::Float32: return std::make_shared<HipBuffer<float>>(ctx_, count);
-    case ElementType::Int32: return std::make_shared<HipBuffer<int32_t>>(ctx_, count);
-    case ElementType::UInt32: return std::make_shared<HipBuffer<uint32_t>>(ctx_, count);
-    case ElementType::Int64: return std::make_shared<HipBuffer<int64_t>>(ctx_, count);
-    case ElementType::Float64: return std::make_shared<HipBuffer<double>>(ctx_, count);
-    case ElementType::UInt16: return std::make_shared<HipBuffer<uint16_t>>(ctx_, count);
+    case ElementType::Float32: return std::make_shared<HipBuffer<float>>(ctx_, pool_, count);
+    case ElementType::Int32: return std::make_shared<HipBuffer<int32_t>>(ctx_, pool_, count);
+    case ElementType::UInt32: return std::make_shared<HipBuffer<uint32_t>>(ctx_, pool_, count);
+    case ElementType::Int64: return std::make_shared<HipBuffer<int64_t>>(ctx_, pool_, count);
+    case ElementType::Float64: return std::make_shared<HipBuffer<double>>(ctx_, pool_, count);
+    case ElementType::UInt16: return std::make_shared<HipBuffer<uint16_t>>(ctx_, pool_, count);
+    case ElementType::UInt64: return std::make_shared<HipBuffer<uint64_t>>(ctx_, pool_, count);
+    case ElementType::Int16: return std::make_shared<HipBuffer<int16_t>>(ctx_, pool_, count);
+    case ElementType::UInt8: return std::make_shared<HipBuffer<uint8_t>>(ctx_, pool_, count);
+    case ElementType::Int8: return std::make_shared<HipBuffer<int8_t>>(ctx_, pool_, count);
+    case ElementType::Bool: return std::make_shared<HipBuffer<uint8_t>>(ctx_, pool_, count);
   }
   throw ArgumentException("unknown element type");
 }
@@ -112,6 +187,7 @@ HipCompiledKernel::HipCompiledKernel(std::string name, std::shared_ptr<dc_hip_ct
 std::future<void> HipCompiledKernel::ExecuteAsync(const KernelArguments& arguments) {
   // One storage slot per argument, pointers to the slots in parameter order (as
   // CudaKernelLauncher pins a void*[] of argument slots, CudaKernelLauncher.cs:226-313).
+  // A struct argument (RawArgument) points at its own bytes.
   const size_t n = arguments.Buffers.size() + arguments.ScalarArguments.size();
   std::vector<uint64_t> storage(n, 0);
   std::vector<void*> slots(n, nullptr);
@@ -124,8 +200,16 @@ std::future<void> HipCompiledKernel::ExecuteAsync(const KernelArguments& argumen
     ++i;
   }
   for (const ScalarValue& s : arguments.ScalarArguments) {
-    std::visit([&](auto v) { std::memcpy(&storage[i], &v, sizeof(v)); }, s);
-    slots[i] = &storage[i];
+    if (auto* raw = std::get_if<RawArgument>(&s)) {
+      slots[i] = const_cast<uint8_t*>(raw->Bytes.data());
+    } else {
+      std::visit(
+          [&](const auto& v) {
+            if constexpr (!std::is_same_v<std::decay_t<decltype(v)>, RawArgument>) std::memcpy(&storage[i], &v, sizeof(v));
+          },
+          s);
+      slots[i] = &storage[i];
+    }
     ++i;
   }
   const KernelLaunchConfiguration& lc = arguments.LaunchConfiguration;
@@ -162,6 +246,36 @@ HipAccelerator::HipAccelerator(const HipBackendOptions& options)
   info_.MaxThreadsPerBlock = d.max_threads_per_block;
   info_.ClockRateKHz = d.clock_khz;
   info_.WarpSize = d.wave_size;
+  void* h = nullptr;
+  Check(dc_hip_malloc_host(ctx_.get(), 4 * sizeof(uint32_t), &h), "dc_hip_malloc_host");
+  err_host_ = static_cast<uint32_t*>(h);
+  std::memset(err_host_, 0, 4 * sizeof(uint32_t));
+  void* dptr = nullptr;
+  Check(dc_hip_host_device_pointer(ctx_.get(), h, &dptr), "dc_hip_host_device_pointer");
+  err_device_ = static_cast<uint32_t*>(dptr);
+}
+
+HipAccelerator::~HipAccelerator() {
+  if (err_host_) dc_hip_free_host(ctx_.get(), err_host_);
+}
+
+uint32_t HipAccelerator::NextLaunchEpoch() {
+  std::lock_guard<std::mutex> lock(module_mu_);
+  if (++epoch_ == 0) {  // wrapped: clear the words so no stale epoch can match
+    std::memset(err_host_, 0, 4 * sizeof(uint32_t));
+    epoch_ = 1;
+  }
+  return epoch_;
+}
+
+void HipAccelerator::ThrowIfGeneratedKernelFailed(uint32_t epoch, const std::string& kernel) const {
+  auto word = [&](int k) { return __atomic_load_n(&err_host_[k], __ATOMIC_ACQUIRE); };
+  if (word(DC_GEN_ERR_INDEX) == epoch)
+    throw IndexOutOfRangeException("Index was outside the bounds of the array. (kernel '" + kernel + "')");
+  if (word(DC_GEN_ERR_DIVIDE_BY_ZERO) == epoch)
+    throw DivideByZeroException("Attempted to divide by zero. (kernel '" + kernel + "')");
+  if (word(DC_GEN_ERR_OVERFLOW) == epoch)
+    throw OverflowException("Arithmetic operation resulted in an overflow. (kernel '" + kernel + "')");
 }
 
 int32_t HipAccelerator::DeviceCount() {
@@ -213,11 +327,27 @@ std::future<std::shared_ptr<ICompiledKernel>> HipAccelerator::CompileKernelAsync
   return p.get_future();
 }
 
+namespace {
+std::mutex g_create_mu;
+std::string g_create_error;
+}  // namespace
+
+std::string LastAcceleratorCreationError() {
+  std::lock_guard<std::mutex> lock(g_create_mu);
+  return g_create_error;
+}
+
 std::shared_ptr<HipAccelerator> TryCreateAccelerator(const HipBackendOptions& options) {
   try {
-    if (HipAccelerator::DeviceCount() <= options.DeviceId) return nullptr;
+    if (HipAccelerator::DeviceCount() <= options.DeviceId) {
+      std::lock_guard<std::mutex> lock(g_create_mu);
+      g_create_error = "no HIP device " + std::to_string(options.DeviceId);
+      return nullptr;
+    }
     return std::make_shared<HipAccelerator>(options);
-  } catch (const std::exception&) {
+  } catch (const std::exception& e) {
+    std::lock_guard<std::mutex> lock(g_create_mu);
+    g_create_error = e.what();
     return nullptr;  // no usable gfx950 device: discovery skips this backend
   }
 }

@@ -3,6 +3,8 @@
 
 #include <algorithm>
 #include <cctype>
+#include <climits>
+#include <cstring>
 
 namespace DotCompute {
 
@@ -14,23 +16,16 @@ std::string Upper(std::string s) {
 bool EqualsIgnoreCase(const std::string& a, const std::string& b) { return Upper(a) == Upper(b); }
 }  // namespace
 
-// ---- generated registry -------------------------------------------------------------------------
+// ---- registry helpers ----------------------------------------------------------------------------
 
-std::vector<KernelRegistrationInfo> Generated::KernelRegistry::GetAllKernels() {
-  // [Kernel] public static void VectorAdd(ReadOnlySpan<float> a, ReadOnlySpan<float> b,
-  //                                       Span<float> result)  — README.md quick start.
-  KernelRegistrationInfo vadd;
-  vadd.Name = "VectorAdd";
-  vadd.FullName = "Kernels.VectorAdd";
-  vadd.SupportedBackends = {"CPU"};  // the [Kernel] default (KernelAttribute.cs:36)
-  vadd.Parameters = {{"a", ElementType::Float32, true, true},
-                     {"b", ElementType::Float32, true, true},
-                     {"result", ElementType::Float32, true, false}};
-  vadd.Dimensions = 1;
-  vadd.HipEntryPoint = "VectorAdd";  // dc_kernels_gfx950.hsaco: (a, b, result, __length)
-  vadd.HipNeedsLength = true;
-  vadd.HipBuiltin = HipOp::VectorAddF32;
-  return {vadd};
+std::vector<std::string> BackendNames(int32_t flags) {
+  std::vector<std::string> out;
+  const std::pair<KernelBackends, const char*> names[] = {{KernelBackends::CPU, "CPU"}, {KernelBackends::CUDA, "CUDA"},
+                                                          {KernelBackends::Metal, "Metal"}, {KernelBackends::OpenCL, "OpenCL"},
+                                                          {KernelBackends::HIP, "HIP"}};
+  for (const auto& [f, n] : names)
+    if (flags & (int32_t)f) out.push_back(n);
+  return out;
 }
 
 // ---- discovery / DI -----------------------------------------------------------------------------
@@ -195,8 +190,9 @@ std::vector<std::shared_ptr<IAccelerator>> KernelExecutionService::GetSupportedA
     const std::string backend = MapDeviceTypeToBackend(acc->Info().DeviceType);
     bool ok = std::any_of(reg->SupportedBackends.begin(), reg->SupportedBackends.end(),
                           [&](const std::string& b) { return EqualsIgnoreCase(b, backend); });
-    // A registry kernel with a prebuilt HIP entry point runs on HIP regardless of [Kernel(Backends)].
-    if (backend == "HIP" && (!reg->HipEntryPoint.empty() || reg->HipBuiltin != HipOp::None)) ok = true;
+    // A registry kernel with a HIP entry point runs on HIP whether or not [Kernel(Backends)] names
+    // HIP, as ExecuteAsync(name, "CUDA", ...) runs a CPU-only [Kernel] on CUDA (:230-246).
+    if (backend == "HIP" && !reg->HipEntryPoint.empty()) ok = true;
     if (ok) out.push_back(acc);
   }
   return out;
@@ -269,7 +265,8 @@ std::shared_ptr<ICompiledKernel> KernelExecutionService::GetCompiled(const Kerne
     if (it != cache_.end()) return it->second;
   }
   if (reg.HipEntryPoint.empty())
-    throw NotSupportedException("Kernel '" + reg.Name + "' has no prebuilt HIP entry point for gfx950.");
+    throw NotSupportedException("Kernel '" + reg.Name + "' has no HIP translation for gfx950" +
+                                (reg.HipDiagnostic.empty() ? std::string(".") : ": " + reg.HipDiagnostic));
   KernelDefinition def;
   def.Name = reg.Name;
   def.EntryPoint = reg.HipEntryPoint;
@@ -294,20 +291,70 @@ void KernelExecutionService::PrecompileKernelAsync(const std::string& kernelName
     GetCompiled(*reg, *accelerator);
 }
 
+namespace {
+// The first writable float array, copied back (ExtractHostResult, KernelExecutionService.cs:475-501).
+struct CopyBack {
+  std::shared_ptr<IUnifiedMemoryBuffer> Buffer;
+  HostArray Host;
+};
+std::vector<float> FirstFloatResult(const std::vector<CopyBack>& copyBacks) {
+  for (const auto& cb : copyBacks)
+    if (cb.Host.Type == ElementType::Float32) {
+      const float* f = static_cast<const float*>(cb.Host.Data);
+      return std::vector<float>(f, f + cb.Host.Length);
+    }
+  return {};
+}
+
+// A scalar argument converted to the parameter's declared type (the C# invoker unboxes
+// `(T)args[i]`). Small types travel in a 32-bit slot; the kernel reads its low bytes.
+ScalarValue ToParameterType(const KernelArg& a, ElementType t) {
+  double d = 0;
+  int64_t i = 0;
+  uint64_t u = 0;
+  bool is_float = false, is_unsigned = false;
+  std::visit(
+      [&](auto v) {
+        using V = decltype(v);
+        if constexpr (std::is_same_v<V, float> || std::is_same_v<V, double>) {
+          d = (double)v;
+          is_float = true;
+        } else if constexpr (std::is_same_v<V, uint64_t> || std::is_same_v<V, uint32_t>) {
+          u = (uint64_t)v;
+          is_unsigned = true;
+        } else if constexpr (std::is_integral_v<V>) {
+          i = (int64_t)v;
+        }
+      },
+      a);
+  if (is_float && t != ElementType::Float32 && t != ElementType::Float64)
+    throw ArgumentException("a floating-point argument was passed for an integer parameter");
+  const int64_t iv = is_unsigned ? (int64_t)u : i;
+  switch (t) {
+    case ElementType::Float32: return is_float ? (float)d : is_unsigned ? (float)u : (float)i;
+    case ElementType::Float64: return is_float ? d : is_unsigned ? (double)u : (double)i;
+    case ElementType::Int64: return iv;
+    case ElementType::UInt64: return is_unsigned ? u : (uint64_t)i;
+    case ElementType::UInt32: return (uint32_t)iv;
+    default: return (int32_t)iv;  // int, short, ushort, byte, sbyte, bool
+  }
+}
+}  // namespace
+
 std::vector<float> KernelExecutionService::ExecuteOn(const KernelRegistrationInfo& reg, IAccelerator& accelerator,
                                                      std::vector<KernelArg>& args) {
   const std::string backend = MapDeviceTypeToBackend(accelerator.Info().DeviceType);
   if (backend != "HIP")
     throw NotSupportedException("this build drives HIP accelerators only (got device type '" +
                                 accelerator.Info().DeviceType + "')");
+  auto* hip = dynamic_cast<Backends::Hip::HipAccelerator*>(&accelerator);
+  if (reg.HipAbi == HipKernelAbi::Generated && hip) return ExecuteGenerated(reg, *hip, args);
   const size_t totalWork = DeriveWorkSize(reg, args);
+  auto compiled = GetCompiled(reg, accelerator);  // throws NotSupportedException without a HIP slot
 
-  // Marshal: a device buffer per host array, copied in (the reference copies every array,
-  // including outputs, KernelExecutionService.cs:409-443); device buffers pass through.
-  struct CopyBack {
-    std::shared_ptr<IUnifiedMemoryBuffer> Buffer;
-    HostArray Host;
-  };
+  // Plain entry points (kernels registered by hand against a code object): the reference's
+  // marshalling — a device buffer per host array, every array copied in, including outputs
+  // (KernelExecutionService.cs:409-443); device buffers pass through.
   std::vector<std::shared_ptr<IUnifiedMemoryBuffer>> owned;
   std::vector<CopyBack> copyBacks;
   KernelArguments kargs;
@@ -316,7 +363,7 @@ std::vector<float> KernelExecutionService::ExecuteOn(const KernelRegistrationInf
     const KernelParameterInfo* p = i < reg.Parameters.size() ? &reg.Parameters[i] : nullptr;
     if (auto* h = std::get_if<HostArray>(&args[i])) {
       auto buf = accelerator.Memory().AllocateRaw(h->Length, h->Type);
-      buf->CopyFromHost(h->Data, h->Length * ElementSize(h->Type));
+      buf->EnqueueCopyFromHost(h->Data, h->Length * ElementSize(h->Type));
       kargs.AddBuffer(buf.get());
       bufferArgs.push_back(buf.get());
       if (p && p->IsBuffer && !p->IsReadOnly) copyBacks.push_back({buf, *h});
@@ -325,52 +372,91 @@ std::vector<float> KernelExecutionService::ExecuteOn(const KernelRegistrationInf
       kargs.AddBuffer(*b);
       bufferArgs.push_back(*b);
     } else {
-      std::visit(
-          [&](auto v) {
-            using V = decltype(v);
-            if constexpr (!std::is_same_v<V, HostArray> && !std::is_same_v<V, IUnifiedMemoryBuffer*>) kargs.AddScalar(v);
-          },
-          args[i]);
+      kargs.AddScalar(ToParameterType(args[i], p ? p->Type : ElementType::Int32));
     }
   }
-
-  // An elementwise kernel indexes every buffer with the work-item index, so a buffer shorter than
-  // the work size would be read or written past its end: the CPU invoker throws
-  // IndexOutOfRangeException at the first such index; here the launch is refused instead.
-  if (reg.HipNeedsLength || reg.HipBuiltin != HipOp::None)
+  // An elementwise kernel indexes every buffer with the work-item index: a buffer shorter than
+  // the work size would be read or written past its end (the CPU invoker throws
+  // IndexOutOfRangeException at the first such index); the launch is refused instead.
+  if (reg.HipNeedsLength)
     for (IUnifiedMemoryBuffer* b : bufferArgs)
       if (b->Length() < totalWork)
         throw IndexOutOfRangeException("Index was outside the bounds of the array: kernel '" + reg.Name +
                                        "' runs " + std::to_string(totalWork) + " work items but a buffer argument holds " +
                                        std::to_string(b->Length()) + " elements.");
-
-  auto* hip = dynamic_cast<Backends::Hip::HipAccelerator*>(&accelerator);
-  if (reg.HipBuiltin == HipOp::VectorAddF32 && hip && bufferArgs.size() == 3) {
-    // Tuned library entry point (16-byte vector loads) for the registry's VectorAdd.
-    Backends::Hip::Check(dc_hip_vector_add_f32(hip->Context(), static_cast<const float*>(bufferArgs[0]->DevicePointer()),
-                                               static_cast<const float*>(bufferArgs[1]->DevicePointer()),
-                                               static_cast<float*>(bufferArgs[2]->DevicePointer()),
-                                               (int64_t)totalWork),
-                         "dc_hip_vector_add_f32");
-  } else {
-    auto compiled = GetCompiled(reg, accelerator);
-    if (reg.HipNeedsLength) kargs.AddScalar((uint32_t)totalWork);  // the implicit __length (:312-315)
-    kargs.LaunchConfiguration = DeriveLaunch(reg, args, totalWork);
-    compiled->ExecuteAsync(kargs).get();
-  }
+  if (reg.HipNeedsLength) kargs.AddScalar((uint32_t)totalWork);  // the implicit __length (:312-315)
+  kargs.LaunchConfiguration = DeriveLaunch(reg, args, totalWork);
+  compiled->ExecuteAsync(kargs).get();
+  for (auto& cb : copyBacks) cb.Buffer->EnqueueCopyToHost(cb.Host.Data, cb.Host.Length * ElementSize(cb.Host.Type));
   accelerator.SynchronizeAsync().get();
+  return FirstFloatResult(copyBacks);
+}
 
-  std::vector<float> first;
-  bool have_first = false;
-  for (auto& cb : copyBacks) {
-    cb.Buffer->CopyToHost(cb.Host.Data, cb.Host.Length * ElementSize(cb.Host.Type));
-    if (!have_first && cb.Host.Type == ElementType::Float32) {
-      const float* f = static_cast<const float*>(cb.Host.Data);
-      first.assign(f, f + cb.Host.Length);
-      have_first = true;
+std::vector<float> KernelExecutionService::ExecuteGenerated(const KernelRegistrationInfo& reg,
+                                                            Backends::Hip::HipAccelerator& accelerator,
+                                                            std::vector<KernelArg>& args) {
+  const size_t totalWork = DeriveWorkSize(reg, args);
+  if (totalWork > (size_t)INT32_MAX)
+    throw ArgumentException("kernel '" + reg.Name + "': more than 2^31 - 1 work items (C# spans hold int lengths)");
+  // The coordinates of a 2-D / 3-D work item divide by the trailing integer extents, as the CPU
+  // invoker does (KernelExecutionMetadataEmitter.cs:203-245): a zero extent throws there.
+  std::vector<int64_t> ints;
+  for (size_t i = 0; i < reg.Parameters.size(); ++i) {
+    const auto& p = reg.Parameters[i];
+    if (!p.IsBuffer && p.Type != ElementType::Float32 && p.Type != ElementType::Float64 && p.Type != ElementType::Bool)
+      std::visit([&](auto v) {
+        using V = decltype(v);
+        if constexpr (std::is_arithmetic_v<V>) ints.push_back((int64_t)v);
+      }, args[i]);
+  }
+  if (totalWork > 0 && reg.Dimensions >= 2 && ints.size() >= 2) {
+    const int32_t x = (int32_t)ints[ints.size() - 1], y = (int32_t)ints[ints.size() - 2];
+    const bool three = reg.Dimensions >= 3 && ints.size() >= 3;
+    if (x == 0 || (three && y == 0) || (three && (int32_t)((uint32_t)x * (uint32_t)y) == 0))
+      throw DivideByZeroException("Attempted to divide by zero. (kernel '" + reg.Name + "': a zero extent)");
+  }
+
+  dc_gen_launch launch{};
+  launch.work = (int64_t)totalWork;
+  launch.epoch = accelerator.NextLaunchEpoch();
+  launch.error = accelerator.GeneratedErrorWordsDevice();
+  std::vector<std::shared_ptr<IUnifiedMemoryBuffer>> owned;
+  std::vector<CopyBack> copyBacks;
+  KernelArguments kargs;
+  int nbuf = 0;
+  for (size_t i = 0; i < reg.Parameters.size(); ++i) {
+    const KernelParameterInfo& p = reg.Parameters[i];
+    if (p.IsBuffer) {
+      if (nbuf >= DC_GEN_MAX_BUFFERS) throw NotSupportedException("more than 16 buffer parameters");
+      IUnifiedMemoryBuffer* dev = nullptr;
+      if (auto* h = std::get_if<HostArray>(&args[i])) {
+        // Only what the body reads goes in and only what it writes comes back; the memory comes
+        // from the accelerator's pool (no device allocation once the sizes have been seen).
+        auto buf = accelerator.Memory().AllocateRaw(h->Length, h->Type);
+        if (p.IsRead) buf->EnqueueCopyFromHost(h->Data, h->Length * ElementSize(h->Type));
+        if (p.IsWritten) copyBacks.push_back({buf, *h});
+        dev = buf.get();
+        owned.push_back(std::move(buf));
+      } else {
+        dev = std::get<IUnifiedMemoryBuffer*>(args[i]);
+      }
+      launch.len[nbuf++] = (int64_t)dev->Length();
+      kargs.AddBuffer(dev);
+    } else {
+      kargs.AddScalar(ToParameterType(args[i], p.Type));
     }
   }
-  return first;
+  RawArgument block;
+  block.Bytes.resize(sizeof(launch));
+  std::memcpy(block.Bytes.data(), &launch, sizeof(launch));
+  kargs.AddScalar(std::move(block));
+  kargs.LaunchConfiguration.BlockSize = {DC_GEN_BLOCK, 1, 1};
+  kargs.LaunchConfiguration.GridSize = {(uint32_t)((totalWork + DC_GEN_BLOCK - 1) / DC_GEN_BLOCK), 1, 1};
+  if (totalWork > 0) GetCompiled(reg, accelerator)->ExecuteAsync(kargs).get();
+  for (auto& cb : copyBacks) cb.Buffer->EnqueueCopyToHost(cb.Host.Data, cb.Host.Length * ElementSize(cb.Host.Type));
+  accelerator.Synchronize();
+  accelerator.ThrowIfGeneratedKernelFailed(launch.epoch, reg.Name);
+  return FirstFloatResult(copyBacks);
 }
 
 std::future<void> KernelExecutionService::ExecuteWithBuffersAsync(const std::string& kernelName,
@@ -383,7 +469,15 @@ std::future<void> KernelExecutionService::ExecuteWithBuffersAsync(const std::str
   if (!acc) throw InvalidOperationException("no accelerator supports kernel '" + kernelName + "'");
   std::vector<KernelArg> args;
   for (auto* b : buffers) args.push_back(b);
-  for (auto& s : scalarArgs) std::visit([&](auto v) { args.push_back(v); }, s);
+  for (auto& s : scalarArgs)
+    std::visit(
+        [&](const auto& v) {
+          if constexpr (std::is_same_v<std::decay_t<decltype(v)>, RawArgument>)
+            throw ArgumentException("raw struct arguments are not kernel parameters");
+          else
+            args.push_back(v);
+        },
+        s);
   if (!ValidateKernelArgsAsync(kernelName, args)) throw ArgumentException("buffer/scalar arguments do not match the kernel");
   ExecuteOn(*reg, *acc, args);
   std::promise<void> p;

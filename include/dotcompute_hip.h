@@ -141,6 +141,31 @@ DC_HIP_API int32_t dc_hip_launch_kernel(dc_hip_ctx* ctx, void* function,
 /* Path of the code object (dc_kernels_gfx950.hsaco) installed next to this library, or "" */
 DC_HIP_API const char* dc_hip_default_module_path(void);
 
+/* Launch block of the kernels generated from [Kernel] C# bodies (the HIP slot of the kernel
+ * registry; the reference's generated CUDA kernels take (buffers..., scalars..., __length),
+ * KernelExecutionMetadataEmitter.cs:65-105). A generated kernel takes its buffers and scalars in
+ * declaration order, then this struct by value. It runs `work` work items, one per thread, in
+ * workgroups of 256 (grid ceil(work / 256)); `len` holds each buffer parameter's element count
+ * (Span<T>.Length), in buffer order. A work item that would throw in C# stores `epoch` into
+ * error[DC_GEN_ERR_*]; the caller clears nothing, and compares the words with the epoch it passed
+ * after the launch completes. `error` points to device-visible memory of 4 words. */
+#define DC_GEN_MAX_BUFFERS 16
+#define DC_GEN_BLOCK 256
+#define DC_GEN_ERR_INDEX 0          /* IndexOutOfRangeException */
+#define DC_GEN_ERR_DIVIDE_BY_ZERO 1 /* DivideByZeroException   */
+#define DC_GEN_ERR_OVERFLOW 2       /* OverflowException       */
+typedef struct dc_gen_launch {
+  int64_t work;
+  uint32_t epoch;
+  uint32_t reserved;
+  uint32_t* error;
+  int64_t len[DC_GEN_MAX_BUFFERS];
+} dc_gen_launch;
+
+/* Device address of pinned host memory from dc_hip_malloc_host (replaces cudaHostGetDevicePointer),
+ * for device-visible words such as dc_gen_launch.error. */
+DC_HIP_API int32_t dc_hip_host_device_pointer(dc_hip_ctx* ctx, void* host_ptr, void** device_ptr);
+
 /* ---------------------------------------------------------------------------------------------
  * Seeded, counter-based input generators (device side). Element i of stream s with seed k is
  * r = splitmix64(k ^ (s << 40) ^ i). Floats: [-1,1) -> (r >> 40) * 2^-23 - 1, [0,1) -> (r >> 40) *

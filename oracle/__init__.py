@@ -65,6 +65,18 @@ def lib() -> C.CDLL:
             "oracle_spmv_csr_f32": (_i32, [_P, _P, _P, _P, _P, _i64, _i64, _i64]),
             "oracle_spmv_csr_f64": (None, [_P, _P, _P, _P, _P, _i64]),
             "oracle_spmv_power_f32": (_i32, [_P, _P, _P, _P, _P, _i64, _i32, _P]),
+            "oracle_net_minf": (C.c_float, [C.c_float, C.c_float]),
+            "oracle_net_maxf": (C.c_float, [C.c_float, C.c_float]),
+            "oracle_net_f2l": (_i64, [C.c_float]),
+            "oracle_kernel_saxpy": (_i32, [_P, _i64, _P, _i64, C.c_float]),
+            "oracle_kernel_scale_clamp": (_i32, [_P, _i64, _P, _i64, C.c_float, C.c_float, C.c_float]),
+            "oracle_kernel_hash_mix": (_i32, [_P, _i64, _P, _i64, _u32]),
+            "oracle_kernel_long_mix": (_i32, [_P, _i64, _P, _i64, _P, _i64, _i32]),
+            "oracle_kernel_gather": (_i32, [_P, _i64, _P, _i64, _P, _i64]),
+            "oracle_kernel_int_divide": (_i32, [_P, _i64, _P, _i64, _P, _i64]),
+            "oracle_kernel_transpose": (_i32, [_P, _i64, _P, _i64, _i32, _i32]),
+            "oracle_kernel_matmul_naive": (_i32, [_P, _i64, _P, _i64, _P, _i64, _i32, _i32, _i32]),
+            "oracle_kernel_stencil3d": (_i32, [_P, _i64, _P, _i64, _i32, _i32, _i32]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -274,3 +286,56 @@ def spmv_power_f32(rp, col, val, x0, iterations: int):
     s = C.c_double()
     lib().oracle_spmv_power_f32(_p(rp), _p(col), _p(val), _p(x), _p(y), rows, iterations, C.byref(s))
     return x, s.value
+
+
+# ---------------------------------------------------------------------------------------------
+# [Kernel] samples (dotcompute_amd/kernels/*.cs) under the CPU invoker's semantics. Each returns
+# (status, output): status 0, or 1/2/3 for IndexOutOfRange / DivideByZero / Overflow.
+# ---------------------------------------------------------------------------------------------
+def _out(like, dtype):
+    return np.array(like, dtype, copy=True)
+
+
+def kernel_saxpy(x, y, a):
+    y = _out(y, np.float32)
+    return lib().oracle_kernel_saxpy(_p(x), x.size, _p(y), y.size, a), y
+
+
+def kernel_scale_clamp(inp, out_len, scale, lo, hi):
+    out = np.zeros(out_len, np.float32)
+    return lib().oracle_kernel_scale_clamp(_p(inp), inp.size, _p(out), out.size, scale, lo, hi), out
+
+
+def kernel_hash_mix(keys, out_len, seed):
+    out = np.zeros(out_len, np.uint32)
+    return lib().oracle_kernel_hash_mix(_p(keys), keys.size, _p(out), out.size, seed), out
+
+
+def kernel_long_mix(a, f, out_len, shift):
+    out = np.zeros(out_len, np.int64)
+    return lib().oracle_kernel_long_mix(_p(a), a.size, _p(f), f.size, _p(out), out.size, shift), out
+
+
+def kernel_gather(src, index, out_len):
+    out = np.zeros(out_len, np.float32)
+    return lib().oracle_kernel_gather(_p(src), src.size, _p(index), index.size, _p(out), out.size), out
+
+
+def kernel_int_divide(a, b, out_len):
+    out = np.zeros(out_len, np.int32)
+    return lib().oracle_kernel_int_divide(_p(a), a.size, _p(b), b.size, _p(out), out.size), out
+
+
+def kernel_transpose(inp, out_len, rows, cols):
+    out = np.zeros(out_len, np.float32)
+    return lib().oracle_kernel_transpose(_p(inp), inp.size, _p(out), out.size, rows, cols), out
+
+
+def kernel_matmul_naive(a, b, out_len, k, m, n):
+    out = np.zeros(out_len, np.float32)
+    return lib().oracle_kernel_matmul_naive(_p(a), a.size, _p(b), b.size, _p(out), out.size, k, m, n), out
+
+
+def kernel_stencil3d(src, out_len, depth, height, width):
+    out = np.zeros(out_len, np.float32)
+    return lib().oracle_kernel_stencil3d(_p(src), src.size, _p(out), out.size, depth, height, width), out

@@ -646,3 +646,152 @@ int32_t oracle_spmv_power_f32(const int32_t* row_pointers, const int32_t* col_in
   if (last_sum) *last_sum = s;
   return DC_OK;
 }
+
+/* ------------------------------------------------------------------------------------------ */
+/* [Kernel] sample bodies (dotcompute_amd/kernels/ (*.cs files)) as the reference's CPU backend runs them: */
+/* the generated CPU invoker loops __i over [0, work) (work = first writable buffer's length),    */
+/* rebuilds the coordinates from the trailing int parameters and runs the body once per work    */
+/* item, span accesses bounds-checked (KernelExecutionMetadataEmitter.cs:117-170, 203-245;       */
+/* KernelExecutionService.cs:275-288, 382-406). Returns 0, or the DC_GEN_ERR_* + 1 of the first  */
+/* exception in loop order.                                                                       */
+/* ------------------------------------------------------------------------------------------ */
+#define ORC_IDX(len, i) ((uint64_t)(int64_t)(i) < (uint64_t)(len))
+
+/* Math.Min / Math.Max(float) of .NET: IEEE 754-2019 minimum / maximum (NaN wins, -0 < +0). */
+float oracle_net_minf(float a, float b) {
+  if (a != b) return (a == a) ? (a < b ? a : b) : a;
+  return signbit(a) ? a : b;
+}
+float oracle_net_maxf(float a, float b) {
+  if (a != b) return (a == a) ? (b < a ? a : b) : a;
+  return signbit(b) ? a : b;
+}
+
+/* (long)x for a float x, .NET 9+: truncation, saturating, NaN -> 0. */
+int64_t oracle_net_f2l(float x) {
+  if (x != x) return 0;
+  if (x <= -9223372036854775808.0f) return INT64_MIN;
+  if (x >= 9223372036854775808.0f) return INT64_MAX;
+  return (int64_t)x;
+}
+
+int32_t oracle_kernel_saxpy(const float* x, int64_t nx, float* y, int64_t ny, float a) {
+  for (int64_t i = 0; i < ny; ++i) {
+    if (!ORC_IDX(nx, i)) return 1;
+    y[i] = a * x[i] + y[i];
+  }
+  return 0;
+}
+
+int32_t oracle_kernel_scale_clamp(const float* in, int64_t nin, float* out, int64_t nout, float scale, float lo,
+                                  float hi) {
+  for (int64_t i = 0; i < nout; ++i) {
+    if (!ORC_IDX(nin, i)) return 1;
+    const float v = in[i] * scale;
+    out[i] = v > 0.0f ? oracle_net_minf(v, hi) : (v < lo ? lo : oracle_net_maxf(v, lo * 0.5f));
+  }
+  return 0;
+}
+
+int32_t oracle_kernel_hash_mix(const uint32_t* keys, int64_t nk, uint32_t* hashes, int64_t nh, uint32_t seed) {
+  for (int64_t i = 0; i < nh; ++i) {
+    if (!ORC_IDX(nk, i)) return 1;
+    uint32_t h = keys[i] ^ seed;
+    h ^= h >> 16;
+    h *= 0x7feb352du;
+    h ^= h >> 15;
+    h *= 0x846ca68bu;
+    h ^= h >> 16;
+    hashes[i] = h;
+  }
+  return 0;
+}
+
+int32_t oracle_kernel_long_mix(const int64_t* a, int64_t na, const float* f, int64_t nf, int64_t* b, int64_t nb,
+                               int32_t shift) {
+  for (int64_t i = 0; i < nb; ++i) {
+    if (!ORC_IDX(na, i)) return 1;
+    const uint64_t s = (uint64_t)a[i] << (shift & 63);
+    if (!ORC_IDX(nf, i)) return 1;
+    const float prod = f[i] * 3.0e18f;
+    b[i] = (int64_t)(s + (uint64_t)oracle_net_f2l(prod) + (uint64_t)i);  /* unchecked: wraps */
+  }
+  return 0;
+}
+
+int32_t oracle_kernel_gather(const float* src, int64_t nsrc, const int32_t* index, int64_t nidx, float* dst,
+                             int64_t ndst) {
+  for (int64_t i = 0; i < ndst; ++i) {
+    if (!ORC_IDX(nidx, i)) return 1;
+    if (!ORC_IDX(nsrc, index[i])) return 1;
+    dst[i] = src[index[i]];
+  }
+  return 0;
+}
+
+int32_t oracle_kernel_int_divide(const int32_t* a, int64_t na, const int32_t* b, int64_t nb, int32_t* q, int64_t nq) {
+  for (int64_t i = 0; i < nq; ++i) {
+    if (!ORC_IDX(na, i) || !ORC_IDX(nb, i)) return 1;
+    if (b[i] == 0) return 2;
+    if (b[i] == -1 && a[i] == INT32_MIN) return 3;
+    q[i] = a[i] / b[i];
+  }
+  return 0;
+}
+
+int32_t oracle_kernel_transpose(const float* in, int64_t nin, float* out, int64_t nout, int32_t rows, int32_t cols) {
+  for (int64_t i = 0; i < nout; ++i) {
+    if (cols == 0) return 2;
+    const int32_t x = (int32_t)i % cols, y = (int32_t)i / cols;
+    if (y < rows && x < cols) {
+      const int64_t src = (int64_t)(int32_t)((uint32_t)y * (uint32_t)cols + (uint32_t)x);
+      const int64_t dst = (int64_t)(int32_t)((uint32_t)x * (uint32_t)rows + (uint32_t)y);
+      if (!ORC_IDX(nin, src) || !ORC_IDX(nout, dst)) return 1;
+      out[dst] = in[src];
+    }
+  }
+  return 0;
+}
+
+int32_t oracle_kernel_matmul_naive(const float* a, int64_t na, const float* b, int64_t nb, float* c, int64_t nc,
+                                   int32_t k, int32_t m, int32_t n) {
+  for (int64_t i = 0; i < nc; ++i) {
+    if (n == 0) return 2;
+    const int32_t col = (int32_t)i % n, row = (int32_t)i / n;
+    if (row < m && col < n) {
+      float sum = 0.0f;
+      for (int32_t p = 0; p < k; ++p) {
+        const int64_t ia = (int64_t)row * k + p, ib = (int64_t)p * n + col;
+        if (!ORC_IDX(na, ia) || !ORC_IDX(nb, ib)) return 1;
+        sum += a[ia] * b[ib];
+      }
+      const int64_t ic = (int64_t)row * n + col;
+      if (!ORC_IDX(nc, ic)) return 1;
+      c[ic] = sum;
+    }
+  }
+  return 0;
+}
+
+int32_t oracle_kernel_stencil3d(const float* src, int64_t ns, float* dst, int64_t nd, int32_t depth, int32_t height,
+                                int32_t width) {
+  for (int64_t i = 0; i < nd; ++i) {
+    if (width == 0 || height == 0) return 2;
+    const int32_t x = (int32_t)i % width, y = ((int32_t)i / width) % height, z = (int32_t)i / (width * height);
+    if (x < width && y < height && z < depth) {
+      const int64_t idx = ((int64_t)z * height + y) * width + x;
+      float left = 0.0f, below = 0.0f;
+      if (x > 0) {
+        if (!ORC_IDX(ns, idx - 1)) return 1;
+        left = src[idx - 1];
+      }
+      if (z > 0) {
+        if (!ORC_IDX(ns, idx - (int64_t)width * height)) return 1;
+        below = src[idx - (int64_t)width * height];
+      }
+      if (!ORC_IDX(ns, idx) || !ORC_IDX(nd, idx)) return 1;
+      dst[idx] = src[idx] * 2.0f - left - 0.5f * below;
+    }
+  }
+  return 0;
+}

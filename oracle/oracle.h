@@ -97,6 +97,27 @@ void oracle_spmv_csr_f64(const int32_t* row_pointers, const int32_t* col_indices
 int32_t oracle_spmv_power_f32(const int32_t* row_pointers, const int32_t* col_indices, const float* values,
                               float* x, float* y, int64_t rows, int32_t iterations, double* last_sum);
 
+
+/* [Kernel] samples of dotcompute_amd/kernels/ (*.cs files) under the CPU invoker's semantics.
+ * Return 0, or 1 (IndexOutOfRange), 2 (DivideByZero), 3 (Overflow) for the first exception. */
+float oracle_net_minf(float a, float b);
+float oracle_net_maxf(float a, float b);
+int64_t oracle_net_f2l(float x);
+int32_t oracle_kernel_saxpy(const float* x, int64_t nx, float* y, int64_t ny, float a);
+int32_t oracle_kernel_scale_clamp(const float* in, int64_t nin, float* out, int64_t nout, float scale, float lo,
+                                  float hi);
+int32_t oracle_kernel_hash_mix(const uint32_t* keys, int64_t nk, uint32_t* hashes, int64_t nh, uint32_t seed);
+int32_t oracle_kernel_long_mix(const int64_t* a, int64_t na, const float* f, int64_t nf, int64_t* b, int64_t nb,
+                               int32_t shift);
+int32_t oracle_kernel_gather(const float* src, int64_t nsrc, const int32_t* index, int64_t nidx, float* dst,
+                             int64_t ndst);
+int32_t oracle_kernel_int_divide(const int32_t* a, int64_t na, const int32_t* b, int64_t nb, int32_t* q, int64_t nq);
+int32_t oracle_kernel_transpose(const float* in, int64_t nin, float* out, int64_t nout, int32_t rows, int32_t cols);
+int32_t oracle_kernel_matmul_naive(const float* a, int64_t na, const float* b, int64_t nb, float* c, int64_t nc,
+                                   int32_t k, int32_t m, int32_t n);
+int32_t oracle_kernel_stencil3d(const float* src, int64_t ns, float* dst, int64_t nd, int32_t depth, int32_t height,
+                                int32_t width);
+
 #ifdef __cplusplus
 }
 #endif

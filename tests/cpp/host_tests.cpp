@@ -215,14 +215,44 @@ TEST_CPU(orchestrator_backend_mapping_and_priority) {
   CHECK(KernelExecutionService::GetBackendPriority("Vulkan") == 999);
 }
 
+const KernelRegistrationInfo& Registered(const std::vector<KernelRegistrationInfo>& regs, const std::string& name) {
+  for (const auto& r : regs)
+    if (r.Name == name) return r;
+  throw std::runtime_error("kernel not in the generated registry: " + name);
+}
+
 TEST_CPU(orchestrator_work_size_and_launch) {
   auto regs = Generated::KernelRegistry::GetAllKernels();
-  CHECK(regs.size() == 1 && regs[0].Name == "VectorAdd" && regs[0].HipNeedsLength);
+  const auto& vadd = Registered(regs, "VectorAdd");
+  CHECK(vadd.FullName == "Kernels.VectorAdd" && vadd.HipNeedsLength && vadd.HipAbi == HipKernelAbi::Generated);
   std::vector<float> a(1000), b(1000), r(1000);
   std::vector<KernelArg> args{Arg(a), Arg(b), Arg(r)};
-  CHECK(KernelExecutionService::DeriveWorkSize(regs[0], args) == 1000);
-  KernelLaunchConfiguration lc = KernelExecutionService::DeriveLaunch(regs[0], args, 1000);
+  CHECK(KernelExecutionService::DeriveWorkSize(vadd, args) == 1000);
+  KernelLaunchConfiguration lc = KernelExecutionService::DeriveLaunch(vadd, args, 1000);
   CHECK(lc.BlockSize.X == 256 && lc.GridSize.X == 4 && lc.GridSize.Y == 1);
+}
+
+TEST_CPU(generated_registry_describes_every_kernel) {
+  // KernelExecutionMetadataTests' checks, on this build's generated registry: dimensionality,
+  // parameter descriptors, the HIP slot, and CPU-only registration when a body has no translation.
+  auto regs = Generated::KernelRegistry::GetAllKernels();
+  CHECK(regs.size() == 11);
+  const auto& t = Registered(regs, "Transpose");
+  CHECK(t.Dimensions == 2 && t.FullName == "DotCompute.Samples.Grids.Transpose");
+  CHECK((t.SupportedBackends == std::vector<std::string>{"CPU", "HIP"}));
+  CHECK(t.Parameters.size() == 4 && t.Parameters[0].IsBuffer && t.Parameters[0].IsReadOnly &&
+        !t.Parameters[1].IsReadOnly && !t.Parameters[2].IsBuffer && t.Parameters[2].Type == ElementType::Int32);
+  CHECK(t.HipSource.find("__x = __ii % __xext, __y = __ii / __xext") != std::string::npos);
+  CHECK(Registered(regs, "Stencil3D").Dimensions == 3);
+  const auto& saxpy = Registered(regs, "Saxpy");  // reads and writes y; only reads x
+  CHECK(saxpy.Parameters[0].IsRead && !saxpy.Parameters[0].IsWritten);
+  CHECK(saxpy.Parameters[1].IsRead && saxpy.Parameters[1].IsWritten);
+  const auto& vadd = Registered(regs, "VectorAdd");  // the output is never read: not copied in
+  CHECK(!vadd.Parameters[2].IsRead && vadd.Parameters[2].IsWritten);
+  CHECK((vadd.SupportedBackends == std::vector<std::string>{"CPU"}));
+  const auto& soft = Registered(regs, "Softplus");
+  CHECK(soft.HipEntryPoint.empty() && soft.HipDiagnostic.find("MathF.Log") != std::string::npos);
+  CHECK((BackendNames((int32_t)KernelBackends::All) == std::vector<std::string>{"CPU", "CUDA", "Metal", "OpenCL", "HIP"}));
 }
 
 TEST_CPU(orchestrator_without_accelerators_throws) {
@@ -311,6 +341,8 @@ TEST_GPU(vector_add_100k_bit_exact_and_unknown_backend_falls_back) {
 }
 
 TEST_GPU(compiled_kernel_from_code_object_matches) {
+  // The generated VectorAdd through ICompiledKernel, packed the way a managed caller packs it:
+  // buffers, then the dc_gen_launch block as a by-value struct argument.
   auto acc = Gpu();
   KernelDefinition def;
   def.Name = "VectorAdd";
@@ -322,14 +354,23 @@ TEST_GPU(compiled_kernel_from_code_object_matches) {
        dr = acc->Memory().AllocateAsync<float>(n);
   da->CopyFromAsync(a).get();
   db->CopyFromAsync(b).get();
+  dc_gen_launch launch{};
+  launch.work = (int64_t)n;
+  launch.epoch = acc->NextLaunchEpoch();
+  launch.error = acc->GeneratedErrorWordsDevice();
+  launch.len[0] = launch.len[1] = launch.len[2] = (int64_t)n;
+  RawArgument block;
+  block.Bytes.resize(sizeof(launch));
+  std::memcpy(block.Bytes.data(), &launch, sizeof(launch));
   KernelArguments args;
   args.AddBuffer(da.get());
   args.AddBuffer(db.get());
   args.AddBuffer(dr.get());
-  args.AddScalar((uint32_t)n);
+  args.AddScalar(block);
   args.LaunchConfiguration.GridSize = {(uint32_t)((n + 255) / 256), 1, 1};
   kernel->ExecuteAsync(args).get();
   acc->SynchronizeAsync().get();
+  acc->ThrowIfGeneratedKernelFailed(launch.epoch, "VectorAdd");
   std::vector<float> r(n), ref(n);
   dr->CopyToAsync(r).get();
   oracle_vector_add_f32(a.data(), b.data(), ref.data(), (int64_t)n);
@@ -346,6 +387,8 @@ TEST_GPU(orchestrator_execute_with_device_buffers) {
   auto sp = services.BuildServiceProvider();
   auto orch = sp->GetRequiredOrchestrator();
   sp->Runtime()->Initialize();
+  if (sp->Runtime()->GetAccelerators().empty())
+    throw std::runtime_error("no accelerator: " + Backends::Hip::LastAcceleratorCreationError());
   auto& acc = *sp->Runtime()->GetAccelerators().at(0);
   const size_t n = 250007;
   auto a = Uniform(n, 11, 0), b = Uniform(n, 11, 1);
@@ -413,6 +456,140 @@ TEST_GPU(csr_spmv_code_object_kernel_matches_oracle) {
   int64_t bad = 0;
   for (int64_t r = 0; r < rows; ++r) bad += std::fabs(y[r] - y64[r]) > 1e-4 * scale[r] + 1e-30;
   CHECK(bad == 0);
+}
+
+// ============================== GPU: generated [Kernel] samples through the orchestrator ==========
+
+std::shared_ptr<IComputeOrchestrator> HipOrchestrator() {
+  ServiceCollection services;
+  services.AddDotComputeRuntime().AddHipBackend();
+  return services.BuildServiceProvider()->GetRequiredOrchestrator();
+}
+
+template <typename T>
+std::vector<T> Ints(size_t n, uint64_t seed, int32_t lo, int32_t hi) {
+  std::vector<int32_t> v(n);
+  oracle_gen_uniform_i32(v.data(), (int64_t)n, seed, 1, lo, hi);
+  return std::vector<T>(v.begin(), v.end());
+}
+
+template <typename T>
+bool SameBits(const std::vector<T>& a, const std::vector<T>& b) {
+  return a.size() == b.size() && (a.empty() || std::memcmp(a.data(), b.data(), a.size() * sizeof(T)) == 0);
+}
+
+TEST_GPU(generated_elementwise_kernels_match_oracle) {
+  auto orch = HipOrchestrator();
+  const size_t n = 1000003;
+  {  // Saxpy: y is read and written
+    auto x = Uniform(n, 70, 0), y = Uniform(n, 70, 1), ref = y;
+    CHECK(oracle_kernel_saxpy(x.data(), (int64_t)n, ref.data(), (int64_t)n, 1.75f) == 0);
+    std::vector<float> out = orch->ExecuteAsync("Saxpy", "HIP", {Arg(x), Arg(y), Arg(1.75f)}).get();
+    CHECK(BitsEqual(y, ref) && BitsEqual(out, ref));
+  }
+  {  // ScaleClamp with NaN, infinities and signed zeros among the inputs
+    auto in = Uniform(n, 71, 0);
+    const float specials[] = {NAN, -NAN, INFINITY, -INFINITY, 0.0f, -0.0f, 1e-40f, -1e-40f, 0.25f, -0.5f};
+    for (size_t i = 0; i < 10; ++i) in[i * 997] = specials[i];
+    std::vector<float> out(n), ref(n);
+    CHECK(oracle_kernel_scale_clamp(in.data(), (int64_t)n, ref.data(), (int64_t)n, 3.0f, -1.5f, 2.0f) == 0);
+    orch->ExecuteAsync("ScaleClamp", "HIP", {Arg(in), Arg(out), Arg(3.0f), Arg(-1.5f), Arg(2.0f)}).get();
+    CHECK(BitsEqual(out, ref));
+  }
+  {  // HashMix: wrapping uint multiplies and shifts
+    auto keys = Ints<uint32_t>(n, 72, -2000000000, 2000000000);
+    std::vector<uint32_t> out(n), ref(n);
+    CHECK(oracle_kernel_hash_mix(keys.data(), (int64_t)n, ref.data(), (int64_t)n, 0x9E3779B9u) == 0);
+    orch->ExecuteAsync("HashMix", "HIP", {Arg(keys), Arg(out), Arg((uint32_t)0x9E3779B9u)}).get();
+    CHECK(SameBits(out, ref));
+  }
+  {  // LongMix: shift count 65 masked to 1, float -> long saturation, wrapping sums
+    auto a = Ints<int64_t>(n, 73, -2000000000, 2000000000);
+    for (size_t i = 0; i < n; i += 3) a[i] = a[i] * 4294967296LL + 12345;
+    auto f = Uniform(n, 73, 2);
+    for (size_t i = 0; i < n; i += 5) f[i] *= 8.0f;  // |f * 3e18| up to 2.4e19: saturates
+    f[1] = NAN;
+    std::vector<int64_t> out(n), ref(n);
+    CHECK(oracle_kernel_long_mix(a.data(), (int64_t)n, f.data(), (int64_t)n, ref.data(), (int64_t)n, 65) == 0);
+    orch->ExecuteAsync("LongMix", "HIP", {Arg(a), Arg(f), Arg(out), Arg(65)}).get();
+    CHECK(SameBits(out, ref));
+  }
+  {  // Gather with valid indices
+    auto src = Uniform(5000, 74, 0);
+    auto idx = Ints<int32_t>(n, 74, 0, 4999);
+    std::vector<float> out(n), ref(n);
+    CHECK(oracle_kernel_gather(src.data(), 5000, idx.data(), (int64_t)n, ref.data(), (int64_t)n) == 0);
+    orch->ExecuteAsync("Gather", "HIP", {Arg(src), Arg(idx), Arg(out)}).get();
+    CHECK(BitsEqual(out, ref));
+  }
+  {  // IntDivide, divisors without zero
+    auto a = Ints<int32_t>(n, 75, -2147483647, 2147483647);
+    auto b = Ints<int32_t>(n, 76, 1, 100000);
+    for (size_t i = 0; i < n; i += 2) b[i] = -b[i];
+    std::vector<int32_t> out(n), ref(n);
+    CHECK(oracle_kernel_int_divide(a.data(), (int64_t)n, b.data(), (int64_t)n, ref.data(), (int64_t)n) == 0);
+    orch->ExecuteAsync("IntDivide", "HIP", {Arg(a), Arg(b), Arg(out)}).get();
+    CHECK(SameBits(out, ref));
+  }
+}
+
+TEST_GPU(generated_grid_kernels_match_oracle) {
+  auto orch = HipOrchestrator();
+  {  // 2-D transpose, rows x cols not a multiple of anything
+    const int32_t rows = 1001, cols = 777;
+    auto in = Uniform((size_t)rows * cols, 77, 0);
+    std::vector<float> out((size_t)rows * cols), ref(out.size());
+    CHECK(oracle_kernel_transpose(in.data(), (int64_t)in.size(), ref.data(), (int64_t)ref.size(), rows, cols) == 0);
+    orch->ExecuteAsync("Transpose", "HIP", {Arg(in), Arg(out), Arg(rows), Arg(cols)}).get();
+    CHECK(BitsEqual(out, ref));
+  }
+  {  // 2-D with a loop: the inner product in order, bit-identical to the sequential oracle
+    const int32_t m = 300, k = 211, n = 257;
+    auto a = Uniform((size_t)m * k, 78, 0), b = Uniform((size_t)k * n, 78, 1);
+    std::vector<float> c((size_t)m * n), ref(c.size());
+    CHECK(oracle_kernel_matmul_naive(a.data(), (int64_t)a.size(), b.data(), (int64_t)b.size(), ref.data(),
+                                     (int64_t)ref.size(), k, m, n) == 0);
+    std::vector<float> out = orch->ExecuteAsync("MatMulNaive", "HIP", {Arg(a), Arg(b), Arg(c), Arg(k), Arg(m), Arg(n)}).get();
+    CHECK(BitsEqual(c, ref) && BitsEqual(out, ref));
+  }
+  {  // 3-D stencil
+    const int32_t d = 21, h = 33, w = 45;
+    auto src = Uniform((size_t)d * h * w, 79, 0);
+    std::vector<float> dst(src.size()), ref(src.size());
+    CHECK(oracle_kernel_stencil3d(src.data(), (int64_t)src.size(), ref.data(), (int64_t)ref.size(), d, h, w) == 0);
+    orch->ExecuteAsync("Stencil3D", "HIP", {Arg(src), Arg(dst), Arg(d), Arg(h), Arg(w)}).get();
+    CHECK(BitsEqual(dst, ref));
+  }
+}
+
+TEST_GPU(generated_kernels_raise_csharp_exceptions) {
+  auto orch = HipOrchestrator();
+  // Index outside the source span: IndexOutOfRangeException (the oracle's CPU loop throws too).
+  auto src = Uniform(100, 80, 0);
+  std::vector<int32_t> idx{0, 5, 99, 100, 7};
+  std::vector<float> out(5);
+  CHECK(oracle_kernel_gather(src.data(), 100, idx.data(), 5, out.data(), 5) == 1);
+  CHECK_THROWS(IndexOutOfRangeException, orch->ExecuteAsync("Gather", "HIP", {Arg(src), Arg(idx), Arg(out)}).get());
+  idx[3] = -1;
+  CHECK_THROWS(IndexOutOfRangeException, orch->ExecuteAsync("Gather", "HIP", {Arg(src), Arg(idx), Arg(out)}).get());
+  idx[3] = 3;  // and the next launch on the same accelerator is clean
+  orch->ExecuteAsync("Gather", "HIP", {Arg(src), Arg(idx), Arg(out)}).get();
+  CHECK(out[3] == src[3]);
+  // Integer division by zero and int.MinValue / -1.
+  std::vector<int32_t> a{10, 20, 30}, b{1, 0, 3}, q(3);
+  CHECK_THROWS(DivideByZeroException, orch->ExecuteAsync("IntDivide", "HIP", {Arg(a), Arg(b), Arg(q)}).get());
+  a = {INT32_MIN, 1, 2};
+  b = {-1, 1, 1};
+  CHECK_THROWS(OverflowException, orch->ExecuteAsync("IntDivide", "HIP", {Arg(a), Arg(b), Arg(q)}).get());
+  // A shorter input than the work size (VectorAdd reads b[i] for every i < result.Length).
+  std::vector<float> x(1000, 1.0f), y(999, 2.0f), r(1000);
+  CHECK_THROWS(IndexOutOfRangeException, orch->ExecuteAsync("VectorAdd", "HIP", {Arg(x), Arg(y), Arg(r)}).get());
+  // A zero extent divides by zero in the coordinate reconstruction.
+  std::vector<float> in(6), tout(6);
+  CHECK_THROWS(DivideByZeroException, orch->ExecuteAsync("Transpose", "HIP", {Arg(in), Arg(tout), Arg(2), Arg(0)}).get());
+  // No HIP translation: the orchestrator says so instead of running anything.
+  std::vector<float> sx(10), sy(10);
+  CHECK_THROWS(NotSupportedException, orch->ExecuteAsync("Softplus", "HIP", {Arg(sx), Arg(sy)}).get());
 }
 
 // ============================== GPU: LINQ provider =================================================

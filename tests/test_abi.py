@@ -108,12 +108,14 @@ CSHARP_LAYOUTS = {
         ("total_global_mem", 352, 8), ("lds_per_block", 360, 8), ("pci_bus_id", 368, 4), ("is_gfx950", 372, 4)]),
     "dc_linq_instr": (8, [("op", 0, 1), ("src", 1, 1), ("mode", 2, 1), ("pad", 3, 1), ("imm", 4, 4)]),
     "dc_linq_chain": (8 + 8 * 48, [("n_instr", 0, 4), ("flags", 4, 4), ("code", 8, 8 * 48)]),
+    "dc_gen_launch": (152, [("work", 0, 8), ("epoch", 8, 4), ("reserved", 12, 4), ("error", 16, 8),
+                            ("len", 24, 8 * 16)]),
 }
 
 
 def test_struct_layouts_match_the_csharp_binding(tmp_path):
     """Compiles a probe against include/dotcompute_hip.h and checks offsetof/sizeof of every field
-    of the structs the C# binding declares (DeviceInfo, LinqInstr, LinqChain) against their
+    of the structs the C# binding declares (DeviceInfo, LinqInstr, LinqChain, GenLaunch) against their
     sequential layouts; the ctypes mirrors in dotcompute_amd/hip.py must agree too."""
     import subprocess
 
@@ -130,7 +132,8 @@ def test_struct_layouts_match_the_csharp_binding(tmp_path):
     subprocess.run(["gcc", "-std=c11", "-I", os.path.join(root, "include"), str(src), "-o", str(exe)], check=True)
     got = dict(l.split(" ", 1) for l in subprocess.run([str(exe)], capture_output=True, text=True, check=True)
                .stdout.splitlines())
-    mirrors = {"dc_hip_device_info": hip.DeviceInfo, "dc_linq_instr": hip.LinqInstr, "dc_linq_chain": hip.LinqChain}
+    mirrors = {"dc_hip_device_info": hip.DeviceInfo, "dc_linq_instr": hip.LinqInstr, "dc_linq_chain": hip.LinqChain,
+               "dc_gen_launch": hip.GenLaunch}
     for struct, (size, fields) in CSHARP_LAYOUTS.items():
         assert int(got[struct]) == size == C.sizeof(mirrors[struct]), struct
         for f, off, fsize in fields:

@@ -65,8 +65,10 @@ def test_vector_add_misaligned_pointers(ctx):
 
 
 def test_vector_add_through_code_object(ctx):
-    """The generic ICompiledKernel path: load dc_kernels_gfx950.hsaco, launch `VectorAdd` with
-    the reference's generated signature (a, b, result, __length), block 256, grid ceil(N/256)."""
+    """The generic ICompiledKernel path: load dc_kernels_gfx950.hsaco and launch the `VectorAdd`
+    the generator translated from the README [Kernel] — buffers (a, b, result), then the
+    dc_gen_launch block (work, epoch, error words, buffer lengths) — block 256, grid ceil(N/256).
+    A short `b` makes the kernel report IndexOutOfRange through the error words."""
     import ctypes as C
 
     L = hip.load()
@@ -77,18 +79,31 @@ def test_vector_add_through_code_object(ctx):
     fn = C.c_void_p()
     hip.check(L.dc_hip_module_get_function(mod, b"VectorAdd", C.byref(fn)), "get_function")
     assert L.dc_hip_module_get_function(mod, b"NoSuchKernel", C.byref(C.c_void_p())) == hip.DC_ERR_NOT_FOUND
+    err_host = C.c_void_p()
+    hip.check(L.dc_hip_malloc_host(ctx.handle, 16, C.byref(err_host)), "malloc_host")
+    C.memset(err_host, 0, 16)
+    err_dev = C.c_void_p()
+    hip.check(L.dc_hip_host_device_pointer(ctx.handle, err_host, C.byref(err_dev)), "host_device_pointer")
+    words = (C.c_uint32 * 4).from_address(err_host.value)
     n = 100_000
     a = oracle.gen_uniform_f32(n, 42, 0)
     b = oracle.gen_uniform_f32(n, 42, 1)
     da, db, dr = ctx.to_device(a), ctx.to_device(b), ctx.empty(n, np.float32)
-    pa, pb, pr = C.c_void_p(da.ptr), C.c_void_p(db.ptr), C.c_void_p(dr.ptr)
-    ln = C.c_uint32(n)
-    args = (C.c_void_p * 4)(C.addressof(pa), C.addressof(pb), C.addressof(pr), C.addressof(ln))
-    hip.check(L.dc_hip_launch_kernel(ctx.handle, fn, (n + 255) // 256, 1, 1, 256, 1, 1, 0,
-                                     C.cast(args, C.POINTER(C.c_void_p))), "launch")
-    ctx.synchronize()
-    assert np.array_equal(dr.to_host(), oracle.vector_add_f32(a, b))
+    for epoch, len_b in ((7, n), (8, n - 10)):
+        pa, pb, pr = C.c_void_p(da.ptr), C.c_void_p(db.ptr), C.c_void_p(dr.ptr)
+        block = hip.GenLaunch(work=n, epoch=epoch, error=err_dev.value)
+        block.len[0], block.len[1], block.len[2] = n, len_b, n
+        args = (C.c_void_p * 4)(C.addressof(pa), C.addressof(pb), C.addressof(pr), C.addressof(block))
+        hip.check(L.dc_hip_launch_kernel(ctx.handle, fn, (n + 255) // 256, 1, 1, 256, 1, 1, 0,
+                                         C.cast(args, C.POINTER(C.c_void_p))), "launch")
+        ctx.synchronize()
+        if len_b == n:
+            assert np.array_equal(dr.to_host(), oracle.vector_add_f32(a, b))
+            assert words[hip.DC_GEN_ERR_INDEX] != epoch
+        else:
+            assert words[hip.DC_GEN_ERR_INDEX] == epoch  # b[n-10] and after are out of range
     hip.check(L.dc_hip_module_unload(mod), "unload")
+    hip.check(L.dc_hip_free_host(ctx.handle, err_host), "free_host")
     for x in (da, db, dr):
         ctx.free(x)
 

@@ -368,3 +368,97 @@ def test_spmv_dense_bruteforce_and_power_invariants():
         yd = dense @ xd
         xd = yd / yd.sum()
     assert np.allclose(xp, xd, rtol=1e-4, atol=1e-9)
+
+
+# ------------------------------------------------------------------ [Kernel] samples
+# Each oracle restates a sample kernel body under the CPU invoker's flat-loop semantics; the pins
+# below are closed forms computed independently (numpy float32 array arithmetic, Python integers).
+def test_kernel_samples_elementwise_closed_forms():
+    x = oracle.gen_uniform_f32(1000, 60, 0)
+    y = oracle.gen_uniform_f32(1000, 60, 1)
+    st, got = oracle.kernel_saxpy(x, y, 1.75)
+    assert st == 0 and np.array_equal(got, np.float32(1.75) * x + y)  # two roundings, as numpy does
+    st, _ = oracle.kernel_saxpy(x[:999], y, 1.75)
+    assert st == 1  # x shorter than the work size: x[999] throws
+    keys = np.arange(0, 5000, 7, dtype=np.uint32)
+    st, h = oracle.kernel_hash_mix(keys, keys.size, 0x9E3779B9)
+
+    def lowbias32(v):
+        v ^= 0x9E3779B9
+        v ^= v >> 16
+        v = (v * 0x7FEB352D) & 0xFFFFFFFF
+        v ^= v >> 15
+        v = (v * 0x846CA68B) & 0xFFFFFFFF
+        return v ^ (v >> 16)
+
+    assert st == 0 and h.tolist() == [lowbias32(int(k)) for k in keys]
+    src = oracle.gen_uniform_f32(64, 61, 0)
+    idx = np.array([3, 0, 63, 17], np.int32)
+    assert np.array_equal(oracle.kernel_gather(src, idx, 4)[1], src[idx])
+    assert oracle.kernel_gather(src, np.array([3, 64], np.int32), 2)[0] == 1
+    assert oracle.kernel_gather(src, np.array([-1], np.int32), 1)[0] == 1
+    a = np.array([7, -7, 2**31 - 1, 5], np.int32)
+    assert oracle.kernel_int_divide(a, np.array([2, 2, -1, 5], np.int32), 4)[1].tolist() == [3, -3, -(2**31 - 1), 1]
+    assert oracle.kernel_int_divide(a, np.array([2, 0, 1, 1], np.int32), 4)[0] == 2
+    assert oracle.kernel_int_divide(np.array([-(2**31)], np.int32), np.array([-1], np.int32), 1)[0] == 3
+
+
+def test_kernel_samples_net_semantics():
+    nan = float("nan")
+    assert oracle.lib().oracle_net_maxf(-0.0, 0.0) == 0.0 and math.copysign(1, oracle.lib().oracle_net_maxf(-0.0, 0.0)) == 1
+    assert math.copysign(1, oracle.lib().oracle_net_maxf(0.0, -0.0)) == 1
+    assert math.copysign(1, oracle.lib().oracle_net_minf(0.0, -0.0)) == -1
+    assert math.copysign(1, oracle.lib().oracle_net_minf(-0.0, 0.0)) == -1
+    assert math.isnan(oracle.lib().oracle_net_maxf(nan, 1.0)) and math.isnan(oracle.lib().oracle_net_maxf(1.0, nan))
+    assert math.isnan(oracle.lib().oracle_net_minf(nan, 1.0)) and math.isnan(oracle.lib().oracle_net_minf(1.0, nan))
+    assert oracle.lib().oracle_net_minf(2.0, 3.0) == 2.0 and oracle.lib().oracle_net_maxf(2.0, 3.0) == 3.0
+    f2l = oracle.lib().oracle_net_f2l
+    assert f2l(nan) == 0 and f2l(1e30) == 2**63 - 1 and f2l(-1e30) == -(2**63) and f2l(-2.75) == -2
+    assert f2l(2.0**63) == 2**63 - 1  # 2^63 is a float32 and saturates
+    assert f2l(9.2233715e18) == 9223371487098961920  # the float32 just below 2^63 converts exactly
+    # ScaleClamp against numpy where no signed zeros or NaNs occur (numpy's maximum differs there)
+    x = oracle.gen_uniform_f32(5000, 62, 0)
+    st, out = oracle.kernel_scale_clamp(x, x.size, 3.0, -1.5, 2.0)
+    v = x * np.float32(3.0)
+    ref = np.where(v > 0, np.minimum(v, np.float32(2.0)),
+                   np.where(v < np.float32(-1.5), np.float32(-1.5), np.maximum(v, np.float32(-0.75))))
+    assert st == 0 and np.array_equal(out, ref.astype(np.float32))
+    # LongMix: shift masked to 6 bits, float -> long saturating, wrapping sum
+    a = np.array([1, -3, 2**62, 5], np.int64)
+    f = np.array([0.0, 1.0, 4.0, -0.25], np.float32)
+    st, b = oracle.kernel_long_mix(a, f, 4, 65)  # shift 65 & 63 = 1
+    prod = (f * np.float32(3.0e18))
+    sat = [0, int(prod[1]), 2**63 - 1, int(prod[3])]
+    want = [((int(a[i]) << 1) + sat[i] + i + 2**63) % 2**64 - 2**63 for i in range(4)]
+    assert st == 0 and b.tolist() == want
+
+
+def test_kernel_samples_grids_closed_forms():
+    rows, cols = 37, 53
+    inp = oracle.gen_uniform_f32(rows * cols, 63, 0)
+    st, out = oracle.kernel_transpose(inp, rows * cols, rows, cols)
+    assert st == 0 and np.array_equal(out, inp.reshape(rows, cols).T.ravel())
+    m, k, n = 9, 13, 7
+    a = oracle.gen_uniform_f32(m * k, 64, 0)
+    b = oracle.gen_uniform_f32(k * n, 64, 1)
+    st, c = oracle.kernel_matmul_naive(a, b, m * n, k, m, n)
+    ref = np.zeros((m, n), np.float32)
+    for i in range(m):  # in-order float32 accumulation, one rounding per multiply and per add
+        for j in range(n):
+            s = np.float32(0)
+            for p in range(k):
+                s = np.float32(s + np.float32(a[i * k + p] * b[p * n + j]))
+            ref[i, j] = s
+    assert st == 0 and np.array_equal(c, ref.ravel())
+    assert np.allclose(c.reshape(m, n), a.reshape(m, k).astype(np.float64) @ b.reshape(k, n), rtol=1e-5, atol=1e-5)
+    d, h, w = 5, 6, 7
+    src = oracle.gen_uniform_f32(d * h * w, 65, 0)
+    st, dst = oracle.kernel_stencil3d(src, d * h * w, d, h, w)
+    s3 = src.reshape(d, h, w)
+    left = np.zeros_like(s3)
+    left[:, :, 1:] = s3[:, :, :-1]
+    below = np.zeros_like(s3)
+    below[1:] = s3[:-1]
+    ref = s3 * np.float32(2) - left - np.float32(0.5) * below
+    assert st == 0 and np.array_equal(dst, ref.ravel())
+    assert oracle.kernel_transpose(inp, rows * cols, rows, 0)[0] == 2  # zero extent: __i % 0
