@@ -9,7 +9,10 @@ order-preserving compaction kernel. Throughput = algorithmic bytes (4 B read per
 
 Also reported (outside the timed steps, each with its own roofline): Sum f32 / i32 at 256M, the
 fused Where->Select->Sum and ->Min/Max at 256M, VectorAdd at N=100,000 and 256M, dense fp32 and bf16 MatMul,
-CSR SpMV x20. These legs run first and the headline's W warmup + K timed steps run after them. The CPU
+CSR SpMV x20, the cache-resident 1M / 16M sizes of Sum and Where->Select (ToArray, Sum), and the README
+VectorAdd end to end through the C++ orchestrator (host arrays in, result out). These legs run first and
+the headline's W warmup + K timed steps run after them; `roofline.ceiling` holds a 1 GiB device copy and
+the headline kernel with every / no element kept, measured in the same run. The CPU
 baseline is the oracle's single-thread LINQ-to-objects restatement of the headline chain, timed on this
 host; each reported leg carries its own bounded `cpu_baseline` from the oracle's restatement of the
 reference's CPU algorithm for it (same seeded inputs; `sample` says what was timed).
@@ -63,15 +66,17 @@ def time_launches(ctx, fn, iters: int, warm_ms: float = 0.0) -> float:
     return ms
 
 
-def measured_traffic(profile: str):
+def measured_traffic(profile: str, leg: str | None = None):
     """HBM bytes per launch that rocprofv3's FETCH_SIZE / WRITE_SIZE counters measured for a kernel
-    (calibrated against a copy of known size), from the `traffic_bytes_per_launch:` line of its
-    summary under profiles/; None when there is no such summary."""
+    (calibrated against a copy of known size), from the `traffic_bytes_per_launch:` line (or
+    `traffic_bytes_per_launch[<leg>]:` for a summary covering several legs) of its summary under
+    profiles/; None when there is no such summary."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", profile)
+    key = "traffic_bytes_per_launch" + (f"[{leg}]" if leg else "") + ":"
     try:
         with open(path) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
+                if line.startswith(key):
                     return int(line.split(":", 1)[1])
     except OSError:
         pass
@@ -90,7 +95,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--skip-extras", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of extras to run (sum,linq_sum,linq_minmax,vector_add,gemm,spmv)")
+    ap.add_argument("--only", default="",
+                    help="comma list of extras to run (sum,linq_sum,linq_minmax,vector_add,gemm,spmv,cache,orchestrator)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one 1 GiB device-to-device copy, the known-size reference for the HBM byte "
                          "counters (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) that give roofline.traffic")
@@ -137,6 +143,9 @@ def main() -> int:
 
         extra.update(bench_gemm(ctx, log, warm_timer, roofline, FP32_MFMA_PEAK_TFLOPS, BF16_MFMA_PEAK_TFLOPS,
                                 cpu_cores=None if args.skip_cpu else cores))
+        for leg in ("gemm_f32_8192", "gemm_bf16_8192"):
+            if leg in extra:
+                extra[leg]["roofline"]["traffic"] = measured_traffic("gemm_f32_bf16_8192.md", leg)
     # ---------------- CSR SpMV x20 ---------------------------------------------------------------
     if want("spmv"):
         from bench_extras import bench_spmv  # noqa: E402
@@ -202,6 +211,37 @@ def main() -> int:
             log(f"[bench] {label}: {ms*1e3:.2f} us -> {gbs:.0f} GB/s")
             ctx.free(b)
 
+    # ---------------- cache-resident sizes of the streaming configs (1M and 16M elements) ------
+    # 4 MB and 64 MB inputs stay in the 256 MB memory-side cache between launches: these rates are
+    # not HBM-bound, and launch latency dominates at 1M. Each runs on a prefix of the 256M input.
+    if want("cache"):
+        s = ctx.empty(1, np.float64)
+        c = ctx.empty(1, np.int64)
+        si = ctx.empty(1, np.int64)
+        ov = ctx.empty(1, np.int32)
+        xi = ctx.empty(16 << 20, np.int32)
+        ctx.fill_uniform_i32(xi, seed=43, stream=1)
+        for m, tag in ((1 << 20, "1M"), (16 << 20, "16M")):
+            legs = {
+                "sum_f32": (lambda: ctx.reduce_sum_f32(x, s, m), 4 * m),
+                "sum_i32": (lambda: ctx.reduce_sum_i32(xi, si, ov, m), 4 * m),
+                "where_select_sum_f32": (lambda: ctx.where_select_sum_f32(chain, x, s, c, m), 4 * m),
+                "where_select_to_array_f32": (lambda: ctx.where_select_f32(chain, x, out, cnt, m), None),
+            }
+            for name, (f, nbytes) in legs.items():
+                f(); ctx.synchronize()
+                ms = time_launches(ctx, f, 200, warm_ms=LEG_WARM_MS)
+                if nbytes is None:  # ToArray: 4 B read per input + 4 B written per kept element
+                    nbytes = 4 * m + 4 * int(cnt.to_host()[0])
+                gbs = nbytes / (ms * 1e-3) / 1e9
+                extra[f"{name}_{tag}"] = {"ms": round(ms, 5), "GB/s": round(gbs, 1), "cache_resident": True,
+                                          "strategy": ("lookback" if ctx.to_array_strategy(x, m) == hip.STRATEGY_LOOKBACK
+                                                       else "rounds") if "to_array" in name else None,
+                                          "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
+                log(f"[bench] {name} {tag} (cache-resident): {ms*1e3:.1f} us -> {gbs:.0f} GB/s")
+        for a_ in (s, c, si, ov, xi):
+            ctx.free(a_)
+
     # ---------------- headline, timed last: the other legs have run by now, so the device's clocks
     # have left their idle state before the timed steps (the W warmup steps alone last ~2 ms)
     run = lambda: ctx.where_select_f32(chain, x, out, cnt, n)
@@ -223,6 +263,26 @@ def main() -> int:
     achieved = step_bytes / (ms_kernel * 1e-3) / 1e9
     log(f"[bench] where_select 256M: kept={kept} kernel={ms_kernel*1e3:.1f} us wall/step={ms_per_step*1e3:.1f} us "
         f"-> {achieved:.0f} GB/s")
+
+    # ---------------- what the same memory can do in this run: the ceilings beside the peak -----
+    # a 1 GiB device-to-device copy (read 1 GiB + write 1 GiB), and the headline kernel with every
+    # element kept (x > -2f: read 1 GiB + write 1 GiB) and with none kept (x > 2f: read only)
+    ceiling = {}
+    cp = lambda: hip.check(hip.load().dc_hip_memcpy_d2d_async(ctx.handle, out.ptr, x.ptr, 4 * n), "d2d copy")
+    ms_cp = time_launches(ctx, cp, 20, warm_ms=LEG_WARM_MS)
+    ceiling["d2d_copy_1GiB"] = {"ms": round(ms_cp, 4), "GB/s": round(8 * n / (ms_cp * 1e-3) / 1e9, 1)}
+    for name, thr, wbytes in (("all_kept", -2.0, 4 * n), ("none_kept", 2.0, 0)):
+        ch = hip.LinqChain.assemble([(hip.LOAD, hip.SRC_ELEM, 0), (hip.CMP_GT, hip.SRC_IMM, thr), (hip.FILTER, 0, 0),
+                                     (hip.LOAD, hip.SRC_ELEM, 0), (hip.MUL, hip.SRC_IMM, 2.0),
+                                     (hip.ADD, hip.SRC_IMM, 1.0), (hip.MAP, 0, 0)])
+        g = lambda: ctx.where_select_f32(ch, x, out, cnt, n)
+        ms_g = time_launches(ctx, g, 20, warm_ms=LEG_WARM_MS)
+        ceiling[f"to_array_{name}_256M"] = {"ms": round(ms_g, 4), "GB/s": round((4 * n + wbytes) / (ms_g * 1e-3) / 1e9, 1)}
+    copy_gbs = ceiling["d2d_copy_1GiB"]["GB/s"]
+    ceiling["frac_of_copy"] = round(achieved / copy_gbs, 4)
+    log(f"[bench] ceilings: copy {copy_gbs:.0f} GB/s, all-kept ToArray {ceiling['to_array_all_kept_256M']['GB/s']:.0f} "
+        f"GB/s, none-kept {ceiling['to_array_none_kept_256M']['GB/s']:.0f} GB/s; headline = "
+        f"{100 * ceiling['frac_of_copy']:.1f}% of the copy")
     ctx.free(out)
     ctx.free(x)
 
@@ -251,6 +311,10 @@ def main() -> int:
         del hx
 
     ctx.close()
+    if want("orchestrator"):
+        from bench_extras import bench_orchestrator  # noqa: E402
+
+        extra.update(bench_orchestrator(log, cpu=not args.skip_cpu))
     result = {
         "metric": "fused LINQ filter-map + Sum GB/s (% of 8 TB/s HBM); fp32 MatMul TFLOPS",
         "value": round(value, 2),
@@ -267,8 +331,8 @@ def main() -> int:
         "config": {"workload": "AsComputeQueryable().Where(x => x > 0f).Select(x => x * 2f + 1f).ToArray()",
                    "n": n, "kept": kept, "selectivity": round(kept / n, 6), "bytes_per_step": step_bytes,
                    "parallelism": "single GPU"},
-        "roofline": roofline("hbm", achieved, HBM_PEAK_GBS, "GB/s",
-                             traffic=measured_traffic("where_select_rounds_256M.md")),
+        "roofline": dict(roofline("hbm", achieved, HBM_PEAK_GBS, "GB/s",
+                                  traffic=measured_traffic("where_select_rounds_256M.md")), ceiling=ceiling),
         "cpu_baseline": cpu,
         "extra": extra,
     }

@@ -6,6 +6,7 @@ Produces, in-tree:
                                               kernels generated from dotcompute_amd/kernels/*.cs
   dotcompute_amd/lib/libdotcompute_host.so    C++ host layer (orchestrator, LINQ provider, algorithms)
   dotcompute_amd/lib/dc_host_tests             C++ tests of the host layer
+  dotcompute_amd/lib/dc_orchestrator_bench     end-to-end orchestrator timing (bench.py runs it)
 Run: python -m dotcompute_amd.build
 """
 from __future__ import annotations
@@ -103,6 +104,10 @@ def build_host_layer() -> str:
     _run(["g++", *flags, *inc, "-o", tbin + ".tmp", *tsrcs, "-L", LIB, "-ldotcompute_host", "-ldotcompute_hip",
           "-L", oracle_dir, "-loracle", "-Wl,-rpath,$ORIGIN", "-Wl,-rpath,$ORIGIN/../../oracle"])
     os.replace(tbin + ".tmp", tbin)
+    bbin = os.path.join(LIB, "dc_orchestrator_bench")
+    _run(["g++", *flags, *inc, "-o", bbin + ".tmp", os.path.join(HOST, "bench", "orchestrator_bench.cpp"), "-L", LIB,
+          "-ldotcompute_host", "-ldotcompute_hip", "-Wl,-rpath,$ORIGIN"])
+    os.replace(bbin + ".tmp", bbin)
     return out
 
 
