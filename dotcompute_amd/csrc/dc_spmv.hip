@@ -162,7 +162,7 @@ __global__ __launch_bounds__(kLongBlock) void spmv_long_rows(const int32_t* __re
 }
 
 // x[i] = (float)(y[i] / s), s = *sum (float64 division, one rounding to float).
-__global__ __launch_bounds__(kBlock) void normalise_kernel(const float* __restrict__ y, float* __restrict__ x, int64_t n,
+__global__ __launch_bounds__(kBlock) void normalise_kernel(const float* y, float* x, int64_t n,
                                                            const double* __restrict__ sum) {
   const double s = *sum;
   int64_t i = blockIdx.x * (int64_t)kBlock + threadIdx.x;
@@ -785,26 +785,33 @@ __global__ __launch_bounds__(kGatherBlock) void spmv_slice_windows(const int4* _
   }
 }
 
-// Long segments: a workgroup per segment, on the XCD that owns its slice.
-__global__ __launch_bounds__(kLongBlock) void spmv_slice_long(const int32_t* __restrict__ seg_ptr,
-                                                              const int32_t* __restrict__ col_s,
-                                                              const float* __restrict__ val_s,
-                                                              const float* __restrict__ x, float* __restrict__ partial,
-                                                              const int32_t* __restrict__ long_list,
-                                                              const uint32_t* __restrict__ long_cnt, int32_t long_cap) {
-  __shared__ float lds[kLongBlock / dc::kWave];
+// Long segments (more than kLongSeg nonzeros in one slice): one wavefront per segment, on the XCD
+// that owns its slice. A segment's cost is a chain of dependent round trips (its bounds, its
+// columns and values, its gathers), so the pass is latency-bound: a wavefront per segment keeps as
+// many segments in flight as the device holds waves, and kLongBatch loads per lane cover segments
+// of up to kLongBatch * 64 nonzeros in one round trip each. Lane k adds products k, k + 64, ... in
+// order, then a fixed DPP tree: deterministic.
+constexpr int kLongWave = 64;
+constexpr int kLongBatch = 32;
+__global__ __launch_bounds__(kLongWave) void spmv_slice_long(const int32_t* __restrict__ seg_ptr,
+                                                             const int32_t* __restrict__ col_s,
+                                                             const float* __restrict__ val_s,
+                                                             const float* __restrict__ x, float* __restrict__ partial,
+                                                             const int32_t* __restrict__ long_list,
+                                                             const uint32_t* __restrict__ long_cnt, int32_t long_cap) {
   const int j = blockIdx.x & (kXcds - 1);
+  const int lane = threadIdx.x;
   const uint32_t n_long = min(long_cnt[j], (uint32_t)long_cap);
   for (uint32_t t = blockIdx.x / kXcds; t < n_long; t += gridDim.x / kXcds) {
     const int32_t g = long_list[(int64_t)j * long_cap + t];
     const int32_t b = seg_ptr[g], e = seg_ptr[g + 1];
     float sum = 0.0f;
-    for (int32_t i0 = b + (int32_t)threadIdx.x; i0 < e; i0 += 4 * kLongBlock) {
-      int32_t c[4];
-      float v[4], xv[4], p[4];
+    for (int32_t i0 = b + lane; i0 < e; i0 += kLongBatch * kLongWave) {
+      int32_t c[kLongBatch];
+      float v[kLongBatch], xv[kLongBatch];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int32_t i = i0 + k * kLongBlock;
+      for (int k = 0; k < kLongBatch; ++k) {
+        const int32_t i = i0 + k * kLongWave;
         c[k] = 0;
         v[k] = 0.0f;
         if (i < e) {
@@ -813,22 +820,12 @@ __global__ __launch_bounds__(kLongBlock) void spmv_slice_long(const int32_t* __r
         }
       }
 #pragma unroll
-      for (int k = 0; k < 4; ++k) xv[k] = x[c[k]];  // c = 0 past e: gathered, then dropped below
+      for (int k = 0; k < kLongBatch; ++k) xv[k] = x[c[k]];  // c = 0 past e: gathered, then dropped below
 #pragma unroll
-      for (int k = 0; k < 4; ++k) p[k] = (i0 + k * kLongBlock < e) ? v[k] * xv[k] : 0.0f;
-      sum += (p[0] + p[1]) + (p[2] + p[3]);
+      for (int k = 0; k < kLongBatch; ++k) sum += (i0 + k * kLongWave < e) ? v[k] * xv[k] : 0.0f;
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
-    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = sum;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      float total = lds[0];
-#pragma unroll
-      for (int w = 1; w < kLongBlock / dc::kWave; ++w) total += lds[w];
-      partial[g] = total;
-    }
-    __syncthreads();
+    const float total = wave_sum_f32(sum);
+    if (lane == 0) partial[g] = total;
   }
 }
 
@@ -839,12 +836,15 @@ __global__ __launch_bounds__(kLongBlock) void spmv_slice_long(const int32_t* __r
 // sum that starts at +0.0f unchanged). With kSums, also the block's float64 sum of y (fixed
 // order) for the power iteration. SMAX >= S sizes the LDS table.
 constexpr int kCombineBatch = 4;
+// With `scale` (the power iteration), y = (float)((double)row sum / *scale): the previous step's
+// normalisation x = y / s applied to this step's product instead (A·(u / s) = (A·u) / s).
 template <bool kSums, int SMAX>
 __global__ __launch_bounds__(kRB) void spmv_slice_combine(const int32_t* __restrict__ ts, int32_t ld, int32_t S,
                                                           const int32_t* __restrict__ sb,
                                                           const uint8_t* __restrict__ seg_row,
                                                           const float* __restrict__ partial, float* __restrict__ y,
-                                                          int64_t rows, double* __restrict__ block_sums) {
+                                                          int64_t rows, double* __restrict__ block_sums,
+                                                          const double* __restrict__ scale) {
   __shared__ float tab[kRB][SMAX + 1];
   __shared__ int32_t run_pre[SMAX + 1], run_base[SMAX];
   __shared__ double red[kRB / 64];
@@ -894,6 +894,7 @@ __global__ __launch_bounds__(kRB) void spmv_slice_combine(const int32_t* __restr
 #pragma unroll
   for (int s = 0; s < SMAX; ++s)
     if (s < S) acc += tab[t][s];
+  if (scale) acc = (float)((double)acc / *scale);
   const int64_t r = (int64_t)blockIdx.x * kRB + t;
   if (r < rows) y[r] = acc;
   if constexpr (kSums) {
@@ -904,9 +905,11 @@ __global__ __launch_bounds__(kRB) void spmv_slice_combine(const int32_t* __restr
 
 template <bool kSums>
 int32_t launch_combine(dc_hip_ctx* ctx, unsigned grid, const int32_t* ts, int32_t ld, int32_t S, const int32_t* sb,
-                       const uint8_t* seg_row, const float* partial, float* y, int64_t rows, double* block_sums) {
+                       const uint8_t* seg_row, const float* partial, float* y, int64_t rows, double* block_sums,
+                       const double* scale) {
 #define DC_COMBINE(SM)                                                                                          \
-  spmv_slice_combine<kSums, SM><<<grid, kRB, 0, ctx->stream>>>(ts, ld, S, sb, seg_row, partial, y, rows, block_sums)
+  spmv_slice_combine<kSums, SM><<<grid, kRB, 0, ctx->stream>>>(ts, ld, S, sb, seg_row, partial, y, rows, block_sums, \
+                                                               scale)
   if (S <= 1) DC_COMBINE(1);
   else if (S <= 2) DC_COMBINE(2);
   else if (S <= 4) DC_COMBINE(4);
@@ -1037,8 +1040,10 @@ int32_t plan_build(dc_hip_ctx* ctx, dc_hip_spmv_plan* p, const int32_t* rp, cons
   return DC_OK;
 }
 
-// One SpMV through the plan: y = A·x (and, with sums, the per-block float64 sums of y).
-int32_t plan_spmv(dc_hip_ctx* ctx, const dc_hip_spmv_plan* p, const float* x, float* y, bool sums) {
+// One SpMV through the plan: y = A·x (and, with sums, the per-block float64 sums of y). With
+// `scale`, y = (A·x) / *scale (the power iteration's normalisation of x, applied to the product).
+int32_t plan_spmv(dc_hip_ctx* ctx, const dc_hip_spmv_plan* p, const float* x, float* y, bool sums,
+                  const double* scale = nullptr) {
   if (p->rows == 0) return DC_OK;
   const int ld = p->nblocks + 1;
   if (p->nwin > 0) {
@@ -1059,29 +1064,38 @@ int32_t plan_spmv(dc_hip_ctx* ctx, const dc_hip_spmv_plan* p, const float* x, fl
           (int32_t)p->cols);
       DC_RETURN_IF(dc::last_launch_status());
     }
-    const int64_t lgrid = std::min<int64_t>((int64_t)p->long_cap, (int64_t)per_xcd_cus * 2);
-    spmv_slice_long<<<(unsigned)(std::max<int64_t>(1, lgrid) * kXcds), kLongBlock, 0, ctx->stream>>>(
+    // A wavefront per long segment (up to 16 resident per CU); those past the device-side count
+    // return at once.
+    const int64_t lgrid = std::min<int64_t>((int64_t)p->long_cap, (int64_t)per_xcd_cus * 16);
+    spmv_slice_long<<<(unsigned)(std::max<int64_t>(1, lgrid) * kXcds), kLongWave, 0, ctx->stream>>>(
         p->seg_ptr, p->col_s, p->val_s, x, p->partial, p->long_list, p->long_cnt, p->long_cap);
     DC_RETURN_IF(dc::last_launch_status());
   }
   if (sums)
     return launch_combine<true>(ctx, (unsigned)p->nblocks, p->ts, ld, p->slices, p->sb, p->seg_row, p->partial, y,
-                                p->rows, p->block_sums);
+                                p->rows, p->block_sums, scale);
   return launch_combine<false>(ctx, (unsigned)p->nblocks, p->ts, ld, p->slices, p->sb, p->seg_row, p->partial, y,
-                               p->rows, nullptr);
+                               p->rows, nullptr, scale);
 }
 
+// y_k = A·x_k; s_k = Σ y_k; x_{k+1} = y_k / s_k. The division moves into the next step's combine
+// (y_{k+1} = (A·y_k) / s_k), so the unnormalised y_k is the next step's input as it stands and the
+// buffers swap roles (x, y, x, ...); the last y is normalised into x once at the end.
 int32_t plan_power_iterate(dc_hip_ctx* ctx, const dc_hip_spmv_plan* p, float* x, float* y, int32_t iterations,
                            double* last_sum_out) {
   if (p->rows == 0 || iterations == 0) return DC_OK;
   double* s = p->scalars;
   const unsigned ngrid = (unsigned)std::max<int64_t>(1, std::min<int64_t>((p->rows + kBlock - 1) / kBlock, 16384));
+  const float* src = x;
+  float* dst = y;
   for (int32_t it = 0; it < iterations; ++it) {
-    DC_RETURN_IF(plan_spmv(ctx, p, x, y, true));
+    DC_RETURN_IF(plan_spmv(ctx, p, src, dst, true, it == 0 ? nullptr : s));
     DC_RETURN_IF(dc::launch_reduce_partials_f64(ctx, p->block_sums, p->nblocks, s));
-    normalise_kernel<<<ngrid, kBlock, 0, ctx->stream>>>(y, x, p->rows, s);
-    DC_RETURN_IF(dc::last_launch_status());
+    src = dst;
+    dst = dst == y ? x : y;
   }
+  normalise_kernel<<<ngrid, kBlock, 0, ctx->stream>>>(src, x, p->rows, s);  // in place when src == x
+  DC_RETURN_IF(dc::last_launch_status());
   if (last_sum_out) DC_RETURN_IF_HIP(hipMemcpyAsync(last_sum_out, s, sizeof(double), hipMemcpyDeviceToDevice, ctx->stream));
   return DC_OK;
 }
