@@ -24,6 +24,7 @@
 #include <map>
 #include <mutex>
 
+#include <type_traits>
 #include <utility>
 
 #include "dc_device.hpp"
@@ -834,60 +835,220 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
   }
 }
 
-// ---- Where/Select -> Sum / Count ----------------------------------------------------------------
-// Pass 1: each block runs the program over one contiguous chunk (a thread takes 4 vectors, 16
-// elements, per step) and writes its float64 sum and kept count; pass 2 sums the partials in block
-// order (fixed tree, deterministic).
+// ---- Where/Select -> Sum / Count / Min / Max: pass 1 ---------------------------------------------
+// Each workgroup runs the program over one contiguous chunk of the 16-byte aligned region that
+// starts h elements into the input: a thread loads 8 vectors (32 elements) per step and applies the
+// program to each half of 16; the vectors after the chunk's last whole step are taken one per
+// thread at a time. The elements before the aligned region (h < 4; h = n for an input that is not
+// even 4-byte aligned) and after it (< 4) go to the last workgroup. Pass 2 combines the
+// per-workgroup partials in a fixed tree (deterministic).
 constexpr int kSumBlock = 512;
+constexpr int kRdUnroll = 8;                                 // 16-byte vectors per thread per step
+constexpr int64_t kRdStep = (int64_t)kRdUnroll * kSumBlock;  // vectors per workgroup per step
 
+// Program variants of the reductions: the interpreter (with or without save registers), any
+// affine chain, and the one- and two-stage affine chains (filter, map, filter-then-map,
+// map-then-filter) with the comparison fixed at compile time, which makes a filter one compare
+// per element. Canonical modes are kRdCanon + 8 * shape + (comparison - DC_LQ_CMP_GT).
+enum ReduceMode : int { kRdInterp = 0, kRdInterpSaves = 1, kRdAffine = 2, kRdCanon = 16 };
+constexpr int rd_canon(int shape, int cmp) { return kRdCanon + 8 * shape + (cmp - DC_LQ_CMP_GT); }
+constexpr bool rd_is_canon(int rd) { return rd >= kRdCanon; }
+constexpr int rd_shape(int rd) { return (rd - kRdCanon) >> 3; }
+constexpr int rd_cmp(int rd) { return DC_LQ_CMP_GT + ((rd - kRdCanon) & 7); }
 
-template <int MODE>
+// Constants of a canonical chain: filter x <cmp> t; map x * a + b (a missing multiply is a = 1,
+// a missing add b = -0: both exact, as in the interpreter's rounding of x * a, then + b).
+struct RdConst {
+  float t, a, b;
+};
+
+struct ReducePlan {
+  int mode;
+  AffineChain aff;
+  RdConst k;
+};
+
+inline ReducePlan reduce_plan(const dc_linq_chain& prog) {
+  ReducePlan p{};
+  p.k = RdConst{0.0f, 1.0f, -0.0f};
+  Canon2 c{};
+  int shape = 0;
+  if (!lower_affine(prog, &p.aff)) {
+    p.mode = program_uses_saves(prog) ? kRdInterpSaves : kRdInterp;
+  } else if (lower_canon2(p.aff, &c, &shape)) {
+    int cmp = DC_LQ_CMP_GT;
+    for (int s = 0; s < p.aff.n_stages; ++s) {
+      if (p.aff.kind[s] == kStageFilter) {
+        cmp = (int)p.aff.op[s];
+        p.k.t = p.aff.c0[s];
+      } else {
+        p.k.a = c.a;
+        p.k.b = c.b;
+      }
+    }
+    p.mode = rd_canon(shape, cmp);
+  } else {
+    p.mode = kRdAffine;
+  }
+  return p;
+}
+
+template <int CMP>
+__device__ __attribute__((always_inline)) inline bool rd_compare(float x, float t) {
+  if constexpr (CMP == DC_LQ_CMP_GT) return x > t;
+  else if constexpr (CMP == DC_LQ_CMP_GE) return x >= t;
+  else if constexpr (CMP == DC_LQ_CMP_LT) return x < t;
+  else if constexpr (CMP == DC_LQ_CMP_LE) return x <= t;
+  else if constexpr (CMP == DC_LQ_CMP_EQ) return x == t;
+  else return x != t;  // true for NaN, as in C#
+}
+
+// The program over EPT elements with one flag per element (kept). The canonical modes compute the
+// flag with one compare, so it stays a lane mask.
+template <int RD, int EPT>
+__device__ __attribute__((always_inline)) inline void apply_reduce_flags(const dc_linq_chain& prog,
+                                                                         const AffineChain& aff, const RdConst& k,
+                                                                         float (&e)[EPT], bool (&kept)[EPT]) {
+  if constexpr (rd_is_canon(RD)) {
+    constexpr int SHAPE = rd_shape(RD), CMP = rd_cmp(RD);
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+      if (SHAPE == kShapeM || SHAPE == kShapeMF) {
+        e[j] = e[j] * k.a;
+        e[j] = e[j] + k.b;
+      }
+      kept[j] = SHAPE == kShapeM ? true : rd_compare<CMP>(e[j], k.t);
+      if (SHAPE == kShapeFM) {
+        e[j] = e[j] * k.a;
+        e[j] = e[j] + k.b;
+      }
+    }
+  } else {
+    uint32_t keep;
+    if constexpr (RD == kRdAffine) keep = (uint32_t)run_affine<EPT>(aff, e);
+    else keep = run_program<EPT, RD == kRdInterpSaves>(prog, e);
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) kept[j] = ((keep >> j) & 1u) != 0u;
+  }
+}
+
+// Calls f(std::integral_constant<int, mode>{}) for a reduction mode chosen at run time.
+#define DC_RD_CMP_MODES(X, SHAPE)                                                                        \
+  X(rd_canon(SHAPE, DC_LQ_CMP_GT)) X(rd_canon(SHAPE, DC_LQ_CMP_GE)) X(rd_canon(SHAPE, DC_LQ_CMP_LT)) \
+  X(rd_canon(SHAPE, DC_LQ_CMP_LE)) X(rd_canon(SHAPE, DC_LQ_CMP_EQ)) X(rd_canon(SHAPE, DC_LQ_CMP_NE))
+template <class F>
+void rd_dispatch(int mode, F&& f) {
+  switch (mode) {
+#define DC_RD_CASE(m)                   \
+  case (m):                             \
+    f(std::integral_constant<int, (m)>{}); \
+    return;
+    DC_RD_CASE(kRdInterpSaves)
+    DC_RD_CASE(kRdAffine)
+    DC_RD_CASE(rd_canon(kShapeM, DC_LQ_CMP_GT))
+    DC_RD_CMP_MODES(DC_RD_CASE, kShapeF)
+    DC_RD_CMP_MODES(DC_RD_CASE, kShapeFM)
+    DC_RD_CMP_MODES(DC_RD_CASE, kShapeMF)
+#undef DC_RD_CASE
+    default:
+      f(std::integral_constant<int, kRdInterp>{});
+      return;
+  }
+}
+#undef DC_RD_CMP_MODES
+
+// Elements before the first 16-byte boundary (the whole input when it is not 4-byte aligned).
+inline int64_t reduce_head(const float* in, int64_t n) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(in);
+  if (a & 3) return n;
+  return std::min<int64_t>(n, (int64_t)(((16 - (a & 15)) & 15) >> 2));
+}
+
+// Visits this workgroup's elements and returns this thread's share of the kept count.
+// half(e, kept, base): 16 elements in sequence order, element j at vector base + (j >> 2) *
+// kSumBlock of the aligned region, lane j & 3. single(x, kept, index): the remaining whole vectors,
+// element by element, in sequence order after the halves. loose(x, kept, index): head and tail
+// elements (last workgroup, out of order). The steps run a workgroup-uniform number of times, so
+// their kept elements are counted per wave with ballots (scalar work) and credited to lane 0.
+template <int RD, class Half, class Single, class Loose>
+__device__ __attribute__((always_inline)) inline int64_t visit_chunk(const dc_linq_chain& prog, const AffineChain& aff,
+                                                                     const RdConst& canon, const float* __restrict__ in,
+                                                                     int64_t n, int64_t h, Half&& half, Single&& single,
+                                                                     Loose&& loose) {
+  const int64_t n4 = (n - h) >> 2;
+  const int64_t per = (n4 + gridDim.x - 1) / gridDim.x;
+  const int64_t v0 = min(n4, (int64_t)blockIdx.x * per), v1 = min(n4, v0 + per);
+  const int64_t steps = (v1 - v0) / kRdStep;
+  const dc::f32x4* xa = reinterpret_cast<const dc::f32x4*>(in + h);
+  int64_t cnt = 0;
+  uint64_t wave_cnt = 0;
+  int64_t i = v0 + threadIdx.x;
+  for (int64_t s = 0; s < steps; ++s, i += kRdStep) {
+    dc::f32x4 v[kRdUnroll];
+#pragma unroll
+    for (int u = 0; u < kRdUnroll; ++u) v[u] = dc::load_stream(xa + i + u * kSumBlock);
+#pragma unroll
+    for (int g = 0; g < kRdUnroll / 4; ++g) {
+      float e[16];
+      bool kept[16];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        e[4 * m + 0] = v[4 * g + m].x;
+        e[4 * m + 1] = v[4 * g + m].y;
+        e[4 * m + 2] = v[4 * g + m].z;
+        e[4 * m + 3] = v[4 * g + m].w;
+      }
+      apply_reduce_flags<RD, 16>(prog, aff, canon, e, kept);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) wave_cnt += (uint64_t)__builtin_popcountll(__ballot(kept[j]));
+      half(e, kept, i + (int64_t)(4 * g) * kSumBlock);
+    }
+  }
+  if ((threadIdx.x & (dc::kWave - 1)) == 0) cnt += (int64_t)wave_cnt;
+  for (; i < v1; i += kSumBlock) {
+    const dc::f32x4 x = dc::load_stream(xa + i);
+    float e[4] = {x.x, x.y, x.z, x.w};
+    bool kept[4];
+    apply_reduce_flags<RD, 4>(prog, aff, canon, e, kept);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      single(e[j], kept[j], h + 4 * i + j);
+      cnt += kept[j] ? 1 : 0;
+    }
+  }
+  if (blockIdx.x == gridDim.x - 1) {
+    auto one = [&](int64_t s) __attribute__((always_inline)) {
+      float e[1] = {in[s]};
+      bool kept[1];
+      apply_reduce_flags<RD, 1>(prog, aff, canon, e, kept);
+      loose(e[0], kept[0], s);
+      cnt += kept[0] ? 1 : 0;
+    };
+    for (int64_t s = threadIdx.x; s < h; s += kSumBlock) one(s);
+    for (int64_t s = h + 4 * n4 + threadIdx.x; s < n; s += kSumBlock) one(s);
+  }
+  return cnt;
+}
+
+// Where/Select -> Sum / Count: float64 sum and kept count per workgroup.
+template <int RD>
 __global__ __launch_bounds__(kSumBlock) void where_select_sum_pass1(const dc_linq_chain prog, const AffineChain aff,
-                                                                    const float* __restrict__ in, int64_t n,
-                                                                    int vec_ok, double* __restrict__ psum,
+                                                                    const RdConst canon, const float* __restrict__ in,
+                                                                    int64_t n, int64_t h, double* __restrict__ psum,
                                                                     int64_t* __restrict__ pcnt) {
   __shared__ double lds_d[kSumBlock / dc::kWave];
   __shared__ int64_t lds_i[kSumBlock / dc::kWave];
+  // A dropped element adds +0.0, which leaves the float64 total unchanged (it starts at +0.0 and a
+  // sum of +0.0 and -0.0 is +0.0), so the selection happens in float before the widening.
   double acc = 0.0;
-  int64_t cnt = 0;
-  const int64_t n4 = vec_ok ? (n >> 2) : 0;
-  const int64_t per = (n4 + gridDim.x - 1) / gridDim.x;
-  const int64_t v0 = min(n4, (int64_t)blockIdx.x * per), v1 = min(n4, v0 + per);
-  const dc::f32x4* in4 = reinterpret_cast<const dc::f32x4*>(in);
-  int64_t i = v0 + threadIdx.x;
-  for (; i + 3 * kSumBlock < v1; i += 4 * kSumBlock) {
-    float e[16];
+  auto add = [&](float x, bool kept, int64_t) __attribute__((always_inline)) { acc += (double)(kept ? x : 0.0f); };
+  const int64_t cnt = visit_chunk<RD>(
+      prog, aff, canon, in, n, h,
+      [&](const float (&e)[16], const bool (&kept)[16], int64_t) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      dc::f32x4 x = dc::load_stream(in4 + i + j * kSumBlock);
-      e[4 * j + 0] = x.x;
-      e[4 * j + 1] = x.y;
-      e[4 * j + 2] = x.z;
-      e[4 * j + 3] = x.w;
-    }
-    const uint32_t keep = apply_small<MODE, 16>(prog, aff, e);
-#pragma unroll
-    for (int j = 0; j < 16; ++j) acc += ((keep >> j) & 1u) ? (double)e[j] : 0.0;
-    cnt += __builtin_popcount(keep);
-  }
-  for (; i < v1; i += kSumBlock) {
-    float e[4];
-    dc::f32x4 x = dc::load_stream(in4 + i);
-    e[0] = x.x; e[1] = x.y; e[2] = x.z; e[3] = x.w;
-    const uint32_t keep = apply_small<MODE, 4>(prog, aff, e);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc += ((keep >> j) & 1u) ? (double)e[j] : 0.0;
-    cnt += __builtin_popcount(keep);
-  }
-  if (blockIdx.x == gridDim.x - 1) {
-    for (int64_t s = (n4 << 2) + threadIdx.x; s < n; s += kSumBlock) {
-      float e[1] = {in[s]};
-      if (apply_small<MODE, 1>(prog, aff, e) & 1u) {
-        acc += (double)e[0];
-        cnt += 1;
-      }
-    }
-  }
+        for (int j = 0; j < 16; ++j) acc += (double)(kept[j] ? e[j] : 0.0f);
+      },
+      add, add);
   const double bsum = dc::block_sum64<kSumBlock>(acc, lds_d);
   const int64_t bcnt = dc::block_sum64<kSumBlock>(cnt, lds_i);
   if (threadIdx.x == 0) {
@@ -921,20 +1082,25 @@ __global__ __launch_bounds__(kFinalBlock) void where_select_sum_pass2(const doub
 // Launches the two passes of Where/Select -> Sum with the partials in psum/pcnt (grid entries each).
 int32_t launch_where_select_sum(dc_hip_ctx* ctx, const dc_linq_chain* chain, const float* input, int64_t n,
                                 unsigned grid, double* psum, int64_t* pcnt, double* sum_out, int64_t* count_out) {
-  AffineChain aff{};
-  const bool affine = lower_affine(*chain, &aff);
-  auto kernel = affine ? where_select_sum_pass1<kModeAffine>
-                       : (program_uses_saves(*chain) ? where_select_sum_pass1<kModeInterpSaves>
-                                                     : where_select_sum_pass1<kModeInterp>);
-  kernel<<<grid, kSumBlock, 0, ctx->stream>>>(*chain, aff, input, n, dc::aligned16(input) ? 1 : 0, psum, pcnt);
+  const ReducePlan p = reduce_plan(*chain);
+  const int64_t h = reduce_head(input, n);
+  rd_dispatch(p.mode, [&](auto mode) {
+    where_select_sum_pass1<decltype(mode)::value>
+        <<<grid, kSumBlock, 0, ctx->stream>>>(*chain, p.aff, p.k, input, n, h, psum, pcnt);
+  });
   where_select_sum_pass2<<<1, kFinalBlock, 0, ctx->stream>>>(psum, pcnt, (int)grid, sum_out, count_out);
   return dc::last_launch_status();
 }
 
-unsigned where_select_sum_grid(int64_t n) {
-  const int64_t per_block = (int64_t)kSumBlock * 16 * 4;  // elements per block-iteration x 4
-  return (unsigned)std::max<int64_t>(1, std::min<int64_t>((n + per_block - 1) / per_block, kSumBlocksMax));
+// One workgroup per CU (measured best: 8 waves per CU streaming one contiguous chunk each; more
+// workgroups, or larger ones, are slower at every size from 16M elements up), fewer when the
+// input gives a workgroup less than 8 vectors per thread.
+unsigned where_select_sum_grid(const dc_hip_ctx* ctx, int64_t n) {
+  const int64_t per_block = (int64_t)kSumBlock * 4 * 8;
+  const int64_t cap = std::min<int64_t>(std::max(ctx->cu_count, 1), kSumBlocksMax);
+  return (unsigned)std::max<int64_t>(1, std::min<int64_t>((n + per_block - 1) / per_block, cap));
 }
+
 
 // Scratch of dc_hip_linq_where_select_sum_f32_noalloc: one launch's per-workgroup partials (a
 // float64 sum and an int64 count per workgroup, at most kSumBlocksMax workgroups), 16 KiB. One copy
@@ -1032,78 +1198,122 @@ __device__ inline void mm_block(float& v, int64_t& i, int64_t& c) {
   }
 }
 
-// In sequence order (every candidate comes after the current one) the enumerator's own rule
-// applies and no index comparison is needed: Min takes x unless a NaN is held or x >= current;
-// Max takes x when the current is NaN or x is larger.
+// Order keys of pass 1. Within a thread elements arrive in sequence order, where the enumerator's
+// rule needs no index: Min replaces its value by a later one only if that is smaller, or if it is
+// a NaN and no NaN is held; Max only if it is larger, or if only NaNs are held. Both follow from an
+// integer key per element whose order is the comparison order with -0 and +0 one key (the
+// magnitude, negated for a negative sign) and NaN one key: Min's below every number, Max's below
+// every number but above "not kept". A strict key comparison is then the rule (with Max's
+// NaN-after-NaN case added), and a run of elements reduces as a plain integer min/max tree.
+// Only keys 0 (a zero of either sign) and NaN stand for more than one bit pattern; for every
+// other key the winner's bits follow from the key, so the winner's position is looked up only
+// when the key is one of those two.
 template <int OP>
-__device__ inline bool mm_in_order(bool have, float cur, float x) {
-  if (OP == kOpMin) return !have || (!__builtin_isnan(cur) && !(x >= cur));
-  return !have || __builtin_isnan(cur) || x > cur;
+struct MmKey {
+  static constexpr int32_t kAbsent = OP == kOpMin ? INT32_MAX : INT32_MIN;
+  static constexpr int32_t kNan = OP == kOpMin ? INT32_MIN : INT32_MIN + 1;
+};
+
+template <int OP>
+__device__ inline int32_t mm_key(float x, bool kept) {
+  const int32_t b = __builtin_bit_cast(int32_t, x);
+  const int32_t sgn = b >> 31;                         // 0 or -1
+  const int32_t key = ((b & 0x7FFFFFFF) ^ sgn) - sgn;  // +-magnitude
+  return !kept ? MmKey<OP>::kAbsent : (__builtin_isnan(x) ? MmKey<OP>::kNan : key);
 }
 
-template <int MODE, int OP>
+__device__ inline uint32_t mm_key_bits(int32_t key) {  // inverse of mm_key for keys other than 0 / NaN
+  const int32_t sgn = key >> 31;
+  return (uint32_t)((key ^ sgn) - sgn) | ((uint32_t)sgn & 0x80000000u);
+}
+
+template <int OP>
+__device__ inline bool mm_key_later_wins(int32_t cur, int32_t x) {
+  if (OP == kOpMin) return x < cur;
+  return x > cur || (x == MmKey<OP>::kNan && cur == MmKey<OP>::kNan);
+}
+
+template <int RD, int OP>
 __global__ __launch_bounds__(kSumBlock) void where_select_minmax_pass1(const dc_linq_chain prog, const AffineChain aff,
-                                                                       const float* __restrict__ in, int64_t n,
-                                                                       int vec_ok, float* __restrict__ pv,
+                                                                       const RdConst canon, const float* __restrict__ in,
+                                                                       int64_t n, int64_t h, float* __restrict__ pv,
                                                                        int64_t* __restrict__ pi,
                                                                        int64_t* __restrict__ pcnt) {
-  // A thread visits its elements in increasing sequence order (steps of 16 in index order, then
-  // single vectors, then the scalar tail), so it keeps the enumerator's state directly.
-  float bv = 0.0f;
-  int64_t bi = -1, cnt = 0;
-  auto fold = [&](float x, int64_t idx) __attribute__((always_inline)) {
-    if (mm_in_order<OP>(bi >= 0, bv, x)) {
-      bv = x;
-      bi = idx;
-    }
-  };
-  const int64_t n4 = vec_ok ? (n >> 2) : 0;
-  const int64_t per = (n4 + gridDim.x - 1) / gridDim.x;
-  const int64_t v0 = min(n4, (int64_t)blockIdx.x * per), v1 = min(n4, v0 + per);
-  const dc::f32x4* in4 = reinterpret_cast<const dc::f32x4*>(in);
-  int64_t i = v0 + threadIdx.x;
-  for (; i + 3 * kSumBlock < v1; i += 4 * kSumBlock) {
-    float e[16];
+  // Thread state: the winner's key and bits and where it came from, as (vector base, position id
+  // in its half); the sequence index is formed once, at the end (meaningful for keys 0 and NaN,
+  // where it breaks ties between threads; any index of the same bits serves the other keys). The
+  // loose head and tail elements are gathered apart with the index-ordered rule and joined after.
+  int32_t rk = MmKey<OP>::kAbsent;
+  uint32_t rbits = 0;
+  int64_t rbase = 0;
+  int rid = 0;
+  float lv = 0.0f;
+  int64_t li = -1;
+  int64_t cnt = visit_chunk<RD>(
+      prog, aff, canon, in, n, h,
+      [&](const float (&e)[16], const bool (&kept)[16], int64_t base) __attribute__((always_inline)) {
+        // Fast path: IEEE-754-2019 minimum/maximum (three operands per instruction) over the kept
+        // values, the others replaced by the identity (+inf for Min, -inf for Max). It propagates
+        // NaN and orders -0 below +0, so its result is the half's winner, bits included, unless
+        // it is a NaN or a zero; those halves (and only those) take the exact key path.
+        constexpr float kFill = OP == kOpMin ? __builtin_inff() : -__builtin_inff();
+        float f[16];
+        bool any = false;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      dc::f32x4 x = dc::load_stream(in4 + i + j * kSumBlock);
-      e[4 * j + 0] = x.x;
-      e[4 * j + 1] = x.y;
-      e[4 * j + 2] = x.z;
-      e[4 * j + 3] = x.w;
-    }
-    const uint32_t keep = apply_small<MODE, 16>(prog, aff, e);
-    // the step's own winner (its elements in order), then one fold into the running state
-    float sv = 0.0f;
-    int sj = -1;
+        for (int j = 0; j < 16; ++j) {
+          f[j] = kept[j] ? e[j] : kFill;
+          any = any || kept[j];
+        }
+        auto mm3 = [](float x, float y, float z) __attribute__((always_inline)) {
+          return OP == kOpMin ? __builtin_elementwise_minimum(__builtin_elementwise_minimum(x, y), z)
+                              : __builtin_elementwise_maximum(__builtin_elementwise_maximum(x, y), z);
+        };
+        const float g0 = mm3(f[0], f[1], f[2]), g1 = mm3(f[3], f[4], f[5]), g2 = mm3(f[6], f[7], f[8]);
+        const float g3 = mm3(f[9], f[10], f[11]), g4 = mm3(f[12], f[13], f[14]);
+        const float m = mm3(mm3(g0, g1, g2), mm3(g3, g4, f[15]), kFill);
+        int32_t hk = any ? mm_key<OP>(m, true) : MmKey<OP>::kAbsent;
+        uint32_t bits = __builtin_bit_cast(uint32_t, m);
+        int id = 0;
+        if (any && (__builtin_isnan(m) || m == 0.0f)) {
+          int32_t k[16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const bool t = ((keep >> j) & 1u) && mm_in_order<OP>(sj >= 0, sv, e[j]);
-      sv = t ? e[j] : sv;
-      sj = t ? j : sj;
-    }
-    if (sj >= 0) fold(sv, 4 * (i + (int64_t)(sj >> 2) * kSumBlock) + (sj & 3));
-    cnt += __builtin_popcount(keep);
-  }
-  for (; i < v1; i += kSumBlock) {
-    float e[4];
-    dc::f32x4 x = dc::load_stream(in4 + i);
-    e[0] = x.x; e[1] = x.y; e[2] = x.z; e[3] = x.w;
-    const uint32_t keep = apply_small<MODE, 4>(prog, aff, e);
+          for (int j = 0; j < 16; ++j) k[j] = mm_key<OP>(e[j], kept[j]);
+          hk = k[0];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if ((keep >> j) & 1u) fold(e[j], 4 * i + j);
-    cnt += __builtin_popcount(keep);
-  }
-  if (blockIdx.x == gridDim.x - 1) {
-    for (int64_t s = (n4 << 2) + threadIdx.x; s < n; s += kSumBlock) {
-      float e[1] = {in[s]};
-      if (apply_small<MODE, 1>(prog, aff, e) & 1u) {
-        fold(e[0], s);
-        cnt += 1;
-      }
-    }
-  }
+          for (int j = 1; j < 16; ++j) hk = OP == kOpMin ? min(hk, k[j]) : max(hk, k[j]);
+          // the enumerator's element among equal keys: the first, or for Max over NaNs the last
+          const bool last = OP == kOpMax && hk == MmKey<OP>::kNan;
+          bool found = false;
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const bool hit = k[j] == hk && (last || !found);
+            bits = hit ? __builtin_bit_cast(uint32_t, e[j]) : bits;
+            id = hit ? j : id;
+            found = found || hit;
+          }
+        }
+        if (mm_key_later_wins<OP>(rk, hk)) {
+          rk = hk;
+          rbits = bits;
+          rbase = base;
+          rid = id;
+        }
+      },
+      [&](float x, bool kept, int64_t idx) __attribute__((always_inline)) {
+        const int32_t xk = mm_key<OP>(x, kept);
+        if (mm_key_later_wins<OP>(rk, xk)) {
+          rk = xk;
+          rbits = __builtin_bit_cast(uint32_t, x);
+          rbase = (idx - h) >> 2;  // idx = h + 4 * vector + lane
+          rid = (int)((idx - h) & 3);
+        }
+      },
+      [&](float x, bool kept, int64_t idx) __attribute__((always_inline)) {
+        if (kept) mm_take<OP>(lv, li, x, idx);
+      });
+  float bv = __builtin_bit_cast(float, rbits);
+  int64_t bi = rk != MmKey<OP>::kAbsent ? h + 4 * (rbase + (int64_t)(rid >> 2) * kSumBlock) + (rid & 3) : -1;
+  mm_take<OP>(bv, bi, lv, li);
   mm_block<OP, kSumBlock>(bv, bi, cnt);
   if (threadIdx.x == 0) {
     pv[blockIdx.x] = bv;
@@ -1253,7 +1463,7 @@ DC_HIP_API int32_t dc_hip_linq_where_select_sum_f32(dc_hip_ctx* ctx, const dc_li
   if (n < 0 || (n > 0 && !input)) return DC_ERR_INVALID_ARGUMENT;
   DC_RETURN_IF(dc_linq_chain_validate(chain));
   DC_CTX_ENTER(ctx);
-  const unsigned grid = where_select_sum_grid(n);
+  const unsigned grid = where_select_sum_grid(ctx, n);
   DC_RETURN_IF(dc::ensure_partials(ctx, (size_t)grid * 16));
   double* psum = static_cast<double*>(ctx->partials);
   int64_t* pcnt = reinterpret_cast<int64_t*>(psum + grid);
@@ -1267,7 +1477,7 @@ DC_HIP_API int32_t dc_hip_linq_where_select_sum_f32_noalloc(dc_hip_ctx* ctx, con
   DC_RETURN_IF(dc_linq_chain_validate(chain));
   DC_CTX_ENTER(ctx);
   if (ctx->noalloc_status != DC_OK) return ctx->noalloc_status;  // the symbol lookup at set-up failed
-  const unsigned grid = where_select_sum_grid(n);
+  const unsigned grid = where_select_sum_grid(ctx, n);
   // The grid is capped, so every n fits; the check keeps that invariant explicit.
   if ((size_t)grid * 16 > kNoAllocScratchBytes) return DC_ERR_OUT_OF_MEMORY;
   double* psum = static_cast<double*>(ctx->noalloc_scratch);  // never `scratch` itself: a host stand-in
@@ -1281,29 +1491,26 @@ DC_HIP_API int32_t dc_hip_linq_where_select_minmax_f32(dc_hip_ctx* ctx, const dc
   if (n < 0 || (n > 0 && !input) || (op != DC_LINQ_MIN && op != DC_LINQ_MAX)) return DC_ERR_INVALID_ARGUMENT;
   DC_RETURN_IF(dc_linq_chain_validate(chain));
   DC_CTX_ENTER(ctx);
-  const int64_t per_block = (int64_t)kSumBlock * 16 * 4;  // elements per block-iteration x 4
-  const unsigned grid = (unsigned)std::max<int64_t>(1, std::min<int64_t>((n + per_block - 1) / per_block, kSumBlocksMax));
+  const unsigned grid = where_select_sum_grid(ctx, n);
   DC_RETURN_IF(dc::ensure_partials(ctx, (size_t)grid * 24));
   int64_t* pi = static_cast<int64_t*>(ctx->partials);
   int64_t* pcnt = pi + grid;
   float* pv = reinterpret_cast<float*>(pcnt + grid);
-  AffineChain aff{};
-  const bool affine = lower_affine(*chain, &aff);
-  const int mode = affine ? kModeAffine : (program_uses_saves(*chain) ? kModeInterpSaves : kModeInterp);
-  const int vec_ok = dc::aligned16(input) ? 1 : 0;
-#define DC_MINMAX(MODE, OP)                                                                                       \
-  where_select_minmax_pass1<MODE, OP><<<grid, kSumBlock, 0, ctx->stream>>>(*chain, aff, input, n, vec_ok, pv, pi, pcnt); \
-  where_select_minmax_pass2<OP><<<1, kFinalBlock, 0, ctx->stream>>>(pv, pi, pcnt, (int)grid, value_out, count_out)
-  if (op == DC_LINQ_MIN) {
-    if (mode == kModeAffine) { DC_MINMAX(kModeAffine, kOpMin); }
-    else if (mode == kModeInterpSaves) { DC_MINMAX(kModeInterpSaves, kOpMin); }
-    else { DC_MINMAX(kModeInterp, kOpMin); }
-  } else {
-    if (mode == kModeAffine) { DC_MINMAX(kModeAffine, kOpMax); }
-    else if (mode == kModeInterpSaves) { DC_MINMAX(kModeInterpSaves, kOpMax); }
-    else { DC_MINMAX(kModeInterp, kOpMax); }
-  }
-#undef DC_MINMAX
+  const ReducePlan p = reduce_plan(*chain);
+  const int64_t h = reduce_head(input, n);
+  rd_dispatch(p.mode, [&](auto mode) {
+    constexpr int RD = decltype(mode)::value;
+    if (op == DC_LINQ_MIN)
+      where_select_minmax_pass1<RD, kOpMin>
+          <<<grid, kSumBlock, 0, ctx->stream>>>(*chain, p.aff, p.k, input, n, h, pv, pi, pcnt);
+    else
+      where_select_minmax_pass1<RD, kOpMax>
+          <<<grid, kSumBlock, 0, ctx->stream>>>(*chain, p.aff, p.k, input, n, h, pv, pi, pcnt);
+  });
+  if (op == DC_LINQ_MIN)
+    where_select_minmax_pass2<kOpMin><<<1, kFinalBlock, 0, ctx->stream>>>(pv, pi, pcnt, (int)grid, value_out, count_out);
+  else
+    where_select_minmax_pass2<kOpMax><<<1, kFinalBlock, 0, ctx->stream>>>(pv, pi, pcnt, (int)grid, value_out, count_out);
   return dc::last_launch_status();
 }
 

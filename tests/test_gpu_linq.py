@@ -461,13 +461,14 @@ def test_min_max_ties_and_nans_pick_the_enumerator_element(ctx, n, which):
     y = oracle.gen_uniform_f32(n, 9, 0).copy()
     pos = rng.choice(n, 5, replace=False)
     y.view(np.uint32)[pos] = 0x7FC00000 + np.arange(1, 6, dtype=np.uint32)  # quiet NaNs, distinct payloads
-    got, cnt = run_minmax(ctx, EMPTY, y, op)
-    ref, rcnt = oracle.linq_where_select_minmax(EMPTY, y, name)
-    assert cnt == rcnt and bits(got) == bits(ref)
     all_nan = (0x7FC00000 + np.arange(1, n + 1, dtype=np.uint32) % 1000).view(np.float32)
-    got, cnt = run_minmax(ctx, EMPTY, all_nan, op)
-    ref, _ = oracle.linq_where_select_minmax(EMPTY, all_nan, name)
-    assert bits(got) == bits(ref)
+    # the identity chain runs the general affine kernel, Select(x * 2) a canonical map kernel
+    # (x * 2 + -0 keeps both zero signs and every NaN payload)
+    for chain in (EMPTY, LinqChain.assemble([(LOAD, SRC_ELEM, 0), (MUL, SRC_IMM, 2.0), (MAP, SRC_IMM, 0)])):
+        for data in (x, y, all_nan):
+            got, cnt = run_minmax(ctx, chain, data, op)
+            ref, rcnt = oracle.linq_where_select_minmax(chain, data, name)
+            assert cnt == rcnt and bits(got) == bits(ref)
 
 
 @pytest.mark.parametrize("seed", range(8))
@@ -481,3 +482,31 @@ def test_min_max_random_programs(ctx, seed):
         assert cnt == rcnt
         if rcnt:
             assert same_floats(np.array([got]), np.array([ref]))
+
+
+REDUCE_CANON = [(shape, cmp) for shape in sorted(SHAPE_PROGRAMS)
+                for cmp in ([CMP_GT] if shape == "M" else [CMP_GT, CMP_GE, CMP_LT, CMP_LE, CMP_EQ, CMP_NE])]
+
+
+@pytest.mark.parametrize("shape,cmp", REDUCE_CANON)
+def test_reductions_canonical_chains_special_values(ctx, shape, cmp):
+    """Sum / Count / Min / Max of the one- and two-stage affine chains, which run a kernel per
+    shape and comparison, on inputs salted with -0, +-inf, NaN, denormals and exact thresholds,
+    aligned and misaligned: counts and Min/Max bits equal the enumerator's."""
+    for t in (0.0, 0.25):
+        prog = LinqChain.assemble(SHAPE_PROGRAMS[shape](cmp, t))
+        x = _salted_input(200_003, 40 + cmp)
+        for offset in (0, 3):
+            for name, op in MINMAX:
+                got, cnt = run_minmax(ctx, prog, x, op, offset)
+                ref, rcnt = oracle.linq_where_select_minmax(prog, x, name)
+                assert cnt == rcnt, (shape, cmp, t, offset, name)
+                if rcnt:
+                    assert bits(got) == bits(ref), (shape, cmp, t, offset, name)
+        s, c = run_sum(ctx, prog, x)
+        _, sd, rc = oracle.linq_where_select_sum(prog, x)
+        assert c == rc
+        if np.isfinite(sd):
+            assert abs(s - sd) <= 1e-5 * math.log2(x.size) * max(abs(sd), 1.0)
+        else:
+            assert (math.isnan(s) and math.isnan(sd)) or s == sd
