@@ -677,8 +677,25 @@ __global__ __launch_bounds__(kGatherBlock) void spmv_slice_windows(const int4* _
                                                                    const float* __restrict__ val_s,
                                                                    const float* __restrict__ x,
                                                                    float* __restrict__ partial,
-                                                                   const int32_t* __restrict__ xcd, int32_t cols) {
+                                                                   const int32_t* __restrict__ xcd, int32_t cols,
+                                                                   const double* __restrict__ sums_in, int32_t nsums,
+                                                                   double* __restrict__ sum_out) {
   __shared__ dc::f32x4 prod[kGatherBlock / 64][kSpan / 4];
+  if (sum_out && blockIdx.x == 0) {
+    // The power iteration's previous L1 norm: workgroup 0 adds the previous SpMV's block sums in a
+    // fixed order (thread t takes t, t + 256, ...; eight loads in flight), then its windows.
+    __shared__ double red[kGatherBlock / 64];
+    double a = 0.0;
+    for (int32_t i0 = threadIdx.x; i0 < nsums; i0 += 8 * kGatherBlock) {
+      double v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = i0 + k * kGatherBlock < nsums ? sums_in[i0 + k * kGatherBlock] : 0.0;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) a += v[k];
+    }
+    const double total = dc::block_sum64<kGatherBlock>(a, red);
+    if (threadIdx.x == 0) *sum_out = total;
+  }
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = blockIdx.x & (kXcds - 1);
@@ -1040,10 +1057,13 @@ int32_t plan_build(dc_hip_ctx* ctx, dc_hip_spmv_plan* p, const int32_t* rp, cons
   return DC_OK;
 }
 
-// One SpMV through the plan: y = A·x (and, with sums, the per-block float64 sums of y). With
+// One SpMV through the plan: y = A·x (with `sums`, also the per-block float64 sums of y). With
 // `scale`, y = (A·x) / *scale (the power iteration's normalisation of x, applied to the product).
-int32_t plan_spmv(dc_hip_ctx* ctx, const dc_hip_spmv_plan* p, const float* x, float* y, bool sums,
-                  const double* scale = nullptr) {
+// With `prev_sum_out`, *prev_sum_out = the sum of the block sums as they stand (the previous
+// SpMV's), computed before this SpMV's combine replaces them: by the first gather launch, so it
+// costs no launch of its own.
+int32_t plan_spmv(dc_hip_ctx* ctx, const dc_hip_spmv_plan* p, const float* x, float* y, bool sums = false,
+                  const double* scale = nullptr, double* prev_sum_out = nullptr) {
   if (p->rows == 0) return DC_OK;
   const int ld = p->nblocks + 1;
   if (p->nwin > 0) {
@@ -1061,7 +1081,7 @@ int32_t plan_spmv(dc_hip_ctx* ctx, const dc_hip_spmv_plan* p, const float* x, fl
     for (int ph = 0; ph < phases; ++ph) {
       spmv_slice_windows<<<(unsigned)(per_xcd * kXcds), kGatherBlock, 0, ctx->stream>>>(
           p->desc, p->seg_ptr, p->col_s, p->val_s, x, p->partial, p->xcd + ph * kXcds * kXcdWords,
-          (int32_t)p->cols);
+          (int32_t)p->cols, p->block_sums, p->nblocks, ph == 0 ? prev_sum_out : nullptr);
       DC_RETURN_IF(dc::last_launch_status());
     }
     // A wavefront per long segment (up to 16 resident per CU); those past the device-side count
@@ -1070,6 +1090,8 @@ int32_t plan_spmv(dc_hip_ctx* ctx, const dc_hip_spmv_plan* p, const float* x, fl
     spmv_slice_long<<<(unsigned)(std::max<int64_t>(1, lgrid) * kXcds), kLongWave, 0, ctx->stream>>>(
         p->seg_ptr, p->col_s, p->val_s, x, p->partial, p->long_list, p->long_cnt, p->long_cap);
     DC_RETURN_IF(dc::last_launch_status());
+  } else if (prev_sum_out) {
+    DC_RETURN_IF(dc::launch_reduce_partials_f64(ctx, p->block_sums, p->nblocks, prev_sum_out));
   }
   if (sums)
     return launch_combine<true>(ctx, (unsigned)p->nblocks, p->ts, ld, p->slices, p->sb, p->seg_row, p->partial, y,
@@ -1080,7 +1102,9 @@ int32_t plan_spmv(dc_hip_ctx* ctx, const dc_hip_spmv_plan* p, const float* x, fl
 
 // y_k = A·x_k; s_k = Σ y_k; x_{k+1} = y_k / s_k. The division moves into the next step's combine
 // (y_{k+1} = (A·y_k) / s_k), so the unnormalised y_k is the next step's input as it stands and the
-// buffers swap roles (x, y, x, ...); the last y is normalised into x once at the end.
+// buffers swap roles (x, y, x, ...); the last y is normalised into x once at the end. s_k is formed
+// by step k + 1's first gather launch, from step k's block sums, before step k + 1's combine
+// (which divides by it) overwrites them, so it costs no launch of its own.
 int32_t plan_power_iterate(dc_hip_ctx* ctx, const dc_hip_spmv_plan* p, float* x, float* y, int32_t iterations,
                            double* last_sum_out) {
   if (p->rows == 0 || iterations == 0) return DC_OK;
@@ -1089,11 +1113,11 @@ int32_t plan_power_iterate(dc_hip_ctx* ctx, const dc_hip_spmv_plan* p, float* x,
   const float* src = x;
   float* dst = y;
   for (int32_t it = 0; it < iterations; ++it) {
-    DC_RETURN_IF(plan_spmv(ctx, p, src, dst, true, it == 0 ? nullptr : s));
-    DC_RETURN_IF(dc::launch_reduce_partials_f64(ctx, p->block_sums, p->nblocks, s));
+    DC_RETURN_IF(plan_spmv(ctx, p, src, dst, true, it == 0 ? nullptr : s, it == 0 ? nullptr : s));
     src = dst;
     dst = dst == y ? x : y;
   }
+  DC_RETURN_IF(dc::launch_reduce_partials_f64(ctx, p->block_sums, p->nblocks, s));
   normalise_kernel<<<ngrid, kBlock, 0, ctx->stream>>>(src, x, p->rows, s);  // in place when src == x
   DC_RETURN_IF(dc::last_launch_status());
   if (last_sum_out) DC_RETURN_IF_HIP(hipMemcpyAsync(last_sum_out, s, sizeof(double), hipMemcpyDeviceToDevice, ctx->stream));
@@ -1178,7 +1202,7 @@ DC_HIP_API int32_t dc_hip_spmv_plan_execute_f32(dc_hip_ctx* ctx, const dc_hip_sp
   if (!plan || (plan->rows > 0 && !y) || (plan->cols > 0 && !x)) return DC_ERR_INVALID_ARGUMENT;
   DC_CTX_ENTER(ctx);
   if (plan->device != ctx->device) return DC_ERR_INVALID_ARGUMENT;
-  return plan_spmv(ctx, plan, x, y, false);
+  return plan_spmv(ctx, plan, x, y);
 }
 
 DC_HIP_API int32_t dc_hip_spmv_plan_power_iterate_f32(dc_hip_ctx* ctx, const dc_hip_spmv_plan* plan, float* x,
