@@ -26,6 +26,7 @@
 
 #include <type_traits>
 #include <utility>
+#include <vector>
 
 #include "dc_device.hpp"
 #include "dc_internal.hpp"
@@ -347,49 +348,29 @@ __device__ inline uint64_t run_affine(const AffineChain& ch, float (&e)[EPT]) {
 
 enum ProgramMode : int { kModeInterp = 0, kModeInterpSaves = 1, kModeAffine = 2 };
 
-// Sets bit j of `mask` to p with one v_lshl_or_b32 (inline shift amount). Written as plain C the
-// compiler turns each bit into a select between 0 and the literal 1 << j and hoists those literals
-// into loop-invariant registers (a register per bit).
-__device__ inline uint32_t insert_bit(uint32_t mask, bool p, int j) {
-  uint32_t r;
-  asm volatile("v_lshl_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"((uint32_t)p), "i"(j), "v"(mask));
-  return r;
-}
-
-// ---- one- and two-stage affine chains in a branch-free canonical form ------------------------------
-// Used by the round-robin kernel, whose software pipeline only keeps its loads in flight across
-// rounds when the per-tile code has no branches (a branch makes the compiler's wait counts
-// conservative and it then waits for every outstanding load once per unrolled loop).
-//   filter:  y = x * sign;  keep = ((y >= c) & A) ^ ((y > c) & B) ^ C        (A, B, C in {0, 1})
-//            x > t : sign  1, c  t, A 0 B 1 C 0      x >= t: sign  1, c  t, A 1 B 0 C 0
-//            x < t : sign -1, c -t, A 0 B 1 C 0      x <= t: sign -1, c -t, A 1 B 0 C 0
-//            x == t: sign  1, c  t, A 1 B 1 C 0      x != t: sign  1, c  t, A 1 B 1 C 1
-//            (x * -1 and -t are exact, NaN compares false, and == is ge ^ gt, so every case
-//            equals the direct comparison bit for bit, signed zeros and NaN included)
-//   map:     x = x * a; x = x + b   (a missing multiply is a = 1, a missing add is b = -0: both exact)
+// ---- one- and two-stage affine chains -------------------------------------------------------------
+// A chain of one filter `x <cmp> t`, one map `x * a + b`, or one of each in either order is
+// lowered to its shape and constants, and the kernels are instantiated per shape and comparison:
+// a filter is then one compare per element (a lane mask, no per-element bit packing), a map two
+// operations (a missing multiply is a = 1, a missing add b = -0: both exact, so the rounding is the
+// interpreter's: x * a, then + b).
 enum Shape2 : int { kShapeF = 0, kShapeM = 1, kShapeFM = 2, kShapeMF = 3 };
-struct Canon2 {
-  float sign, c, a, b;
-  uint32_t A, B, C;
+
+// Constants of a canonical chain.
+struct RdConst {
+  float t, a, b;
 };
 
-inline bool lower_canon2(const AffineChain& ch, Canon2* out, int* shape) {
+inline bool lower_canon2(const AffineChain& ch, int* shape, int* cmp, RdConst* out) {
   const int n = ch.n_stages;
   if (n < 1 || n > 2 || (n == 2 && ch.kind[0] == ch.kind[1])) return false;
-  Canon2 k{1.0f, 0.0f, 1.0f, -0.0f, 0u, 0u, 1u};
+  RdConst k{0.0f, 1.0f, -0.0f};
+  int c = DC_LQ_CMP_GT;
   for (int s = 0; s < n; ++s) {
     if (ch.kind[s] == kStageFilter) {
-      const float t = ch.c0[s];
-      switch (ch.op[s]) {
-        case DC_LQ_CMP_GT: k.sign = 1.0f; k.A = 0; k.B = 1; k.C = 0; break;
-        case DC_LQ_CMP_GE: k.sign = 1.0f; k.A = 1; k.B = 0; k.C = 0; break;
-        case DC_LQ_CMP_LT: k.sign = -1.0f; k.A = 0; k.B = 1; k.C = 0; break;
-        case DC_LQ_CMP_LE: k.sign = -1.0f; k.A = 1; k.B = 0; k.C = 0; break;
-        case DC_LQ_CMP_EQ: k.sign = 1.0f; k.A = 1; k.B = 1; k.C = 0; break;
-        case DC_LQ_CMP_NE: k.sign = 1.0f; k.A = 1; k.B = 1; k.C = 1; break;
-        default: return false;
-      }
-      k.c = k.sign < 0.0f ? -t : t;
+      if (ch.op[s] < DC_LQ_CMP_GT || ch.op[s] > DC_LQ_CMP_NE) return false;
+      c = (int)ch.op[s];
+      k.t = ch.c0[s];
     } else {
       k.a = (ch.op[s] & 1u) ? ch.c0[s] : 1.0f;
       k.b = (ch.op[s] & 2u) ? ch.c1[s] : -0.0f;
@@ -397,45 +378,100 @@ inline bool lower_canon2(const AffineChain& ch, Canon2* out, int* shape) {
   }
   *shape = n == 1 ? (ch.kind[0] == kStageFilter ? kShapeF : kShapeM)
                   : (ch.kind[0] == kStageFilter ? kShapeFM : kShapeMF);
+  *cmp = c;
   *out = k;
   return true;
 }
 
-template <int SHAPE, int EPT>
-__device__ inline uint32_t run_canon2(const Canon2& k, float (&e)[EPT]) {
-  static_assert(EPT < 32, "keep mask");
-  uint32_t keep = SHAPE == kShapeM ? ((1u << EPT) - 1u) : 0u;
+// Program variants of the streaming kernels (ToArray's resident grid, Sum, Min/Max): the
+// interpreter (with or without save registers), any affine chain, and the one- and two-stage
+// affine chains with the shape and comparison fixed at compile time. Canonical modes are
+// kRdCanon + 8 * shape + (comparison - DC_LQ_CMP_GT).
+enum ReduceMode : int { kRdInterp = 0, kRdInterpSaves = 1, kRdAffine = 2, kRdCanon = 16 };
+constexpr int rd_canon(int shape, int cmp) { return kRdCanon + 8 * shape + (cmp - DC_LQ_CMP_GT); }
+constexpr bool rd_is_canon(int rd) { return rd >= kRdCanon; }
+constexpr int rd_shape(int rd) { return (rd - kRdCanon) >> 3; }
+constexpr int rd_cmp(int rd) { return DC_LQ_CMP_GT + ((rd - kRdCanon) & 7); }
+
+struct ReducePlan {
+  int mode;
+  AffineChain aff;
+  RdConst k;
+};
+
+inline ReducePlan reduce_plan(const dc_linq_chain& prog) {
+  ReducePlan p{};
+  p.k = RdConst{0.0f, 1.0f, -0.0f};
+  int shape = 0, cmp = DC_LQ_CMP_GT;
+  if (!lower_affine(prog, &p.aff)) p.mode = program_uses_saves(prog) ? kRdInterpSaves : kRdInterp;
+  else if (lower_canon2(p.aff, &shape, &cmp, &p.k)) p.mode = rd_canon(shape, cmp);
+  else p.mode = kRdAffine;
+  return p;
+}
+
+template <int CMP>
+__device__ __attribute__((always_inline)) inline bool rd_compare(float x, float t) {
+  if constexpr (CMP == DC_LQ_CMP_GT) return x > t;
+  else if constexpr (CMP == DC_LQ_CMP_GE) return x >= t;
+  else if constexpr (CMP == DC_LQ_CMP_LT) return x < t;
+  else if constexpr (CMP == DC_LQ_CMP_LE) return x <= t;
+  else if constexpr (CMP == DC_LQ_CMP_EQ) return x == t;
+  else return x != t;  // true for NaN, as in C#
+}
+
+// The program over EPT elements with one flag per element (kept). The canonical modes compute the
+// flag with one compare, so it stays a lane mask.
+template <int RD, int EPT>
+__device__ __attribute__((always_inline)) inline void apply_reduce_flags(const dc_linq_chain& prog,
+                                                                         const AffineChain& aff, const RdConst& k,
+                                                                         float (&e)[EPT], bool (&kept)[EPT]) {
+  if constexpr (rd_is_canon(RD)) {
+    constexpr int SHAPE = rd_shape(RD), CMP = rd_cmp(RD);
 #pragma unroll
-  for (int j = 0; j < EPT; ++j) {
-    if (SHAPE == kShapeM || SHAPE == kShapeMF) {
-      e[j] = e[j] * k.a;
-      e[j] = e[j] + k.b;
+    for (int j = 0; j < EPT; ++j) {
+      if (SHAPE == kShapeM || SHAPE == kShapeMF) {
+        e[j] = e[j] * k.a;
+        e[j] = e[j] + k.b;
+      }
+      kept[j] = SHAPE == kShapeM ? true : rd_compare<CMP>(e[j], k.t);
+      if (SHAPE == kShapeFM) {
+        e[j] = e[j] * k.a;
+        e[j] = e[j] + k.b;
+      }
     }
-    if (SHAPE != kShapeM) {
-      const float y = e[j] * k.sign;
-      const uint32_t ge = y >= k.c, gt = y > k.c;
-      keep = insert_bit(keep, (((ge & k.A) ^ (gt & k.B) ^ k.C) & 1u) != 0u, j);
-    }
-    if (SHAPE == kShapeFM) {
-      e[j] = e[j] * k.a;
-      e[j] = e[j] + k.b;
-    }
+  } else {
+    uint32_t keep;
+    if constexpr (RD == kRdAffine) keep = (uint32_t)run_affine<EPT>(aff, e);
+    else keep = run_program<EPT, RD == kRdInterpSaves>(prog, e);
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) kept[j] = ((keep >> j) & 1u) != 0u;
   }
-  return keep;
 }
 
-// Round-robin kernel variants: the interpreter (with or without save registers) and the four
-// canonical shapes.
-enum RoundsMode : int { kRrInterp = 0, kRrInterpSaves = 1, kRrF = 2, kRrM = 3, kRrFM = 4, kRrMF = 5 };
-
-template <int MODE, int EPT>
-__device__ __attribute__((always_inline)) inline uint32_t apply_rounds(const dc_linq_chain& prog, const Canon2& k, float (&e)[EPT]) {
-  if constexpr (MODE == kRrF) return run_canon2<kShapeF, EPT>(k, e);
-  else if constexpr (MODE == kRrM) return run_canon2<kShapeM, EPT>(k, e);
-  else if constexpr (MODE == kRrFM) return run_canon2<kShapeFM, EPT>(k, e);
-  else if constexpr (MODE == kRrMF) return run_canon2<kShapeMF, EPT>(k, e);
-  else return run_program<EPT, MODE == kRrInterpSaves>(prog, e);
+// Calls f(std::integral_constant<int, mode>{}) for a reduction mode chosen at run time.
+#define DC_RD_CMP_MODES(X, SHAPE)                                                                        \
+  X(rd_canon(SHAPE, DC_LQ_CMP_GT)) X(rd_canon(SHAPE, DC_LQ_CMP_GE)) X(rd_canon(SHAPE, DC_LQ_CMP_LT)) \
+  X(rd_canon(SHAPE, DC_LQ_CMP_LE)) X(rd_canon(SHAPE, DC_LQ_CMP_EQ)) X(rd_canon(SHAPE, DC_LQ_CMP_NE))
+template <class F>
+void rd_dispatch(int mode, F&& f) {
+  switch (mode) {
+#define DC_RD_CASE(m)                   \
+  case (m):                             \
+    f(std::integral_constant<int, (m)>{}); \
+    return;
+    DC_RD_CASE(kRdInterpSaves)
+    DC_RD_CASE(kRdAffine)
+    DC_RD_CASE(rd_canon(kShapeM, DC_LQ_CMP_GT))
+    DC_RD_CMP_MODES(DC_RD_CASE, kShapeF)
+    DC_RD_CMP_MODES(DC_RD_CASE, kShapeFM)
+    DC_RD_CMP_MODES(DC_RD_CASE, kShapeMF)
+#undef DC_RD_CASE
+    default:
+      f(std::integral_constant<int, kRdInterp>{});
+      return;
+  }
 }
+#undef DC_RD_CMP_MODES
 
 // ---- Where/Select -> ToArray ------------------------------------------------------------------
 // One tile per workgroup, claimed by ticket. Element order inside a tile is (vector j, wave, lane,
@@ -470,12 +506,6 @@ __device__ inline uint64_t apply_program(const dc_linq_chain& prog, const Affine
   }
 }
 
-// Program over EPT <= 32 elements of one lane; bit j of the result = element j is kept.
-template <int MODE, int EPT>
-__device__ inline uint32_t apply_small(const dc_linq_chain& prog, const AffineChain& aff, float (&e)[EPT]) {
-  if constexpr (MODE == kModeAffine) return (uint32_t)run_affine<EPT>(aff, e);
-  else return run_program<EPT, MODE == kModeInterpSaves>(prog, e);
-}
 
 template <int MODE>
 __global__ __launch_bounds__(kBlock) void where_select_kernel(const dc_linq_chain prog, const AffineChain aff,
@@ -595,7 +625,10 @@ __global__ __launch_bounds__(kBlock) void where_select_kernel(const dc_linq_chai
 //   - loads run kRrAhead rounds ahead (kRrAhead + 1 register buffers per lane);
 //   - kept values of a tile wait in LDS for kRrDelay rounds before they are written, and the count
 //     words of that round are read one round before the write, so they were published
-//     kRrDelay - 2 full rounds earlier and are almost always already visible.
+//     kRrDelay - 2 full rounds earlier and are almost always already visible;
+//   - the program is one of the compile-time variants (shape and comparison fixed for the one- and
+//     two-stage affine chains): the kernel is bound by its instruction issue at this rate, so
+//     the per-element work is kept to a compare, the map, and the ballot ranking.
 // Roles inside the 1024-thread workgroup: wave 0 reads and checks the count words and broadcasts the
 // output offset; waves 1..15 each own a contiguous 512-element chunk of every tile, rank their kept
 // elements with ballot + mbcnt, stage them in a private LDS ring (in input order) and later write
@@ -608,8 +641,8 @@ constexpr int kRrEpt = 4 * kRrVec;                       // 8 elements per lane
 constexpr int kRrChunk = dc::kWave * kRrEpt;             // 512 elements per worker wave
 constexpr int64_t kRrTile = (int64_t)kRrWorkers * kRrChunk;  // 7680 elements = 30 KiB
 constexpr int kRrAhead = 4;
-constexpr int kRrDelay = 3;
-constexpr int kRrRing = 2048;                            // floats per worker wave (power of two)
+constexpr int kRrDelay = 4;                              // measured: 3 -> 4 saves ~4 us at 256M
+constexpr int kRrRing = (kRrDelay + 1) * kRrChunk;       // floats per worker wave: 10 KiB, 150 KiB per workgroup
 constexpr int kRrCountsPerLane = 4;
 constexpr int kRrMaxGroups = dc::kWave * kRrCountsPerLane;  // P <= 256
 constexpr uint32_t kRrSpinLimit = 1u << 22;              // ~seconds: a wait that never ends reports
@@ -667,13 +700,15 @@ __device__ inline bool rr_resolve(uint32_t (&c)[kRrCountsPerLane], const uint32_
   return true;
 }
 
-template <int MODE>
+template <int RD>
 __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
-    const dc_linq_chain prog, const Canon2 canon, const float* __restrict__ in, int64_t n, float* __restrict__ out,
+    const dc_linq_chain prog, const AffineChain aff, const RdConst canon, const float* __restrict__ in, int64_t n,
+    float* __restrict__ out,
     int64_t* __restrict__ count_out, uint32_t* __restrict__ counts, uint32_t epoch16, uint32_t P,
     uint32_t* __restrict__ done) {
-  constexpr uint32_t kMask = kRrRing - 1;
   __shared__ float s_ring[kRrWorkers][kRrRing];
+  // ring positions stay in [0, kRrRing); a position below 2 * kRrRing wraps with one unsigned min
+  auto wrap = [](uint32_t q) __attribute__((always_inline)) { return min(q, q - (uint32_t)kRrRing); };
   __shared__ uint32_t s_wcount[8][16];  // kept count of (tile slot, worker wave)
   __shared__ uint32_t s_acc[8];         // (waves finished << 24) | kept so far, per tile slot
   __shared__ int64_t s_off[2];          // output offset of the tile being written, by round parity
@@ -740,14 +775,14 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
   };
   // Ranks the kept elements of this wave's chunk (order: vector j, lane, slot k), appends them to the
   // ring, and publishes the tile count when this is the last worker wave to finish the tile.
-  auto stage = [&](float (&e)[kRrEpt], uint32_t keep, uint32_t r) __attribute__((always_inline)) {
+  auto stage = [&](float (&e)[kRrEpt], const bool (&kept)[kRrEpt], uint32_t r) __attribute__((always_inline)) {
     uint32_t run = 0, pos[kRrVec];
 #pragma unroll
     for (int j = 0; j < kRrVec; ++j) {
       uint32_t below = 0, total = 0;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const uint64_t b = __ballot((keep >> (4 * j + k)) & 1u);
+        const uint64_t b = __ballot(kept[4 * j + k]);
         below += __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
         total += (uint32_t)__builtin_popcountll(b);
       }
@@ -759,9 +794,9 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
       uint32_t p = head + pos[j];
 #pragma unroll
       for (int k = 0; k < 4; ++k)
-        if ((keep >> (4 * j + k)) & 1u) ring[(p++) & kMask] = e[4 * j + k];
+        if (kept[4 * j + k]) ring[wrap(p++)] = e[4 * j + k];
     }
-    head += run;
+    head = wrap(head + run);
     if (lane == 0) {
       s_wcount[r & 7][ww] = run;
       const uint32_t prev = atomicAdd(&s_acc[r & 7], (1u << 24) | run);
@@ -780,8 +815,8 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
       cnt = i == ww ? c : cnt;
     }
     float* dst = out + s_off[parity] + before;
-    for (uint32_t i = lane; i < cnt; i += dc::kWave) dst[i] = ring[(tail + i) & kMask];
-    tail += cnt;
+    for (uint32_t i = lane; i < cnt; i += dc::kWave) dst[i] = ring[wrap(tail + i)];
+    tail = wrap(tail + cnt);
   };
 
   // Every load below is unconditional: rounds past the last one re-load round R0 - 1 (loaded one
@@ -802,7 +837,9 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
   // assume fewer loads in flight than a full iteration leaves. The last R0 % kBufs rounds follow.
   auto round = [&](float (&ec)[kRrEpt], float (&en)[kRrEpt]) __attribute__((always_inline)) {
     load(en, min(r + kRrAhead, last));
-    stage(ec, apply_rounds<MODE, kRrEpt>(prog, canon, ec), r);
+    bool kept[kRrEpt];
+    apply_reduce_flags<RD, kRrEpt>(prog, aff, canon, ec, kept);
+    stage(ec, kept, r);
     __syncthreads();
     if (r >= (uint32_t)kRrDelay) write(r - kRrDelay, r & 1);
     ++r;
@@ -828,7 +865,11 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
       const int64_t nv = t < num_tiles ? min(max(n - at, (int64_t)0), (int64_t)4) : 0;
       valid |= ((1u << (uint32_t)nv) - 1u) << (4 * j);
     }
-    stage(e, apply_rounds<MODE, kRrEpt>(prog, canon, e) & valid, R0);
+    bool kept[kRrEpt];
+    apply_reduce_flags<RD, kRrEpt>(prog, aff, canon, e, kept);
+#pragma unroll
+    for (int i = 0; i < kRrEpt; ++i) kept[i] = kept[i] && ((valid >> i) & 1u);
+    stage(e, kept, R0);
     __syncthreads();
     __syncthreads();
     write(R0, 0);
@@ -845,117 +886,6 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
 constexpr int kSumBlock = 512;
 constexpr int kRdUnroll = 8;                                 // 16-byte vectors per thread per step
 constexpr int64_t kRdStep = (int64_t)kRdUnroll * kSumBlock;  // vectors per workgroup per step
-
-// Program variants of the reductions: the interpreter (with or without save registers), any
-// affine chain, and the one- and two-stage affine chains (filter, map, filter-then-map,
-// map-then-filter) with the comparison fixed at compile time, which makes a filter one compare
-// per element. Canonical modes are kRdCanon + 8 * shape + (comparison - DC_LQ_CMP_GT).
-enum ReduceMode : int { kRdInterp = 0, kRdInterpSaves = 1, kRdAffine = 2, kRdCanon = 16 };
-constexpr int rd_canon(int shape, int cmp) { return kRdCanon + 8 * shape + (cmp - DC_LQ_CMP_GT); }
-constexpr bool rd_is_canon(int rd) { return rd >= kRdCanon; }
-constexpr int rd_shape(int rd) { return (rd - kRdCanon) >> 3; }
-constexpr int rd_cmp(int rd) { return DC_LQ_CMP_GT + ((rd - kRdCanon) & 7); }
-
-// Constants of a canonical chain: filter x <cmp> t; map x * a + b (a missing multiply is a = 1,
-// a missing add b = -0: both exact, as in the interpreter's rounding of x * a, then + b).
-struct RdConst {
-  float t, a, b;
-};
-
-struct ReducePlan {
-  int mode;
-  AffineChain aff;
-  RdConst k;
-};
-
-inline ReducePlan reduce_plan(const dc_linq_chain& prog) {
-  ReducePlan p{};
-  p.k = RdConst{0.0f, 1.0f, -0.0f};
-  Canon2 c{};
-  int shape = 0;
-  if (!lower_affine(prog, &p.aff)) {
-    p.mode = program_uses_saves(prog) ? kRdInterpSaves : kRdInterp;
-  } else if (lower_canon2(p.aff, &c, &shape)) {
-    int cmp = DC_LQ_CMP_GT;
-    for (int s = 0; s < p.aff.n_stages; ++s) {
-      if (p.aff.kind[s] == kStageFilter) {
-        cmp = (int)p.aff.op[s];
-        p.k.t = p.aff.c0[s];
-      } else {
-        p.k.a = c.a;
-        p.k.b = c.b;
-      }
-    }
-    p.mode = rd_canon(shape, cmp);
-  } else {
-    p.mode = kRdAffine;
-  }
-  return p;
-}
-
-template <int CMP>
-__device__ __attribute__((always_inline)) inline bool rd_compare(float x, float t) {
-  if constexpr (CMP == DC_LQ_CMP_GT) return x > t;
-  else if constexpr (CMP == DC_LQ_CMP_GE) return x >= t;
-  else if constexpr (CMP == DC_LQ_CMP_LT) return x < t;
-  else if constexpr (CMP == DC_LQ_CMP_LE) return x <= t;
-  else if constexpr (CMP == DC_LQ_CMP_EQ) return x == t;
-  else return x != t;  // true for NaN, as in C#
-}
-
-// The program over EPT elements with one flag per element (kept). The canonical modes compute the
-// flag with one compare, so it stays a lane mask.
-template <int RD, int EPT>
-__device__ __attribute__((always_inline)) inline void apply_reduce_flags(const dc_linq_chain& prog,
-                                                                         const AffineChain& aff, const RdConst& k,
-                                                                         float (&e)[EPT], bool (&kept)[EPT]) {
-  if constexpr (rd_is_canon(RD)) {
-    constexpr int SHAPE = rd_shape(RD), CMP = rd_cmp(RD);
-#pragma unroll
-    for (int j = 0; j < EPT; ++j) {
-      if (SHAPE == kShapeM || SHAPE == kShapeMF) {
-        e[j] = e[j] * k.a;
-        e[j] = e[j] + k.b;
-      }
-      kept[j] = SHAPE == kShapeM ? true : rd_compare<CMP>(e[j], k.t);
-      if (SHAPE == kShapeFM) {
-        e[j] = e[j] * k.a;
-        e[j] = e[j] + k.b;
-      }
-    }
-  } else {
-    uint32_t keep;
-    if constexpr (RD == kRdAffine) keep = (uint32_t)run_affine<EPT>(aff, e);
-    else keep = run_program<EPT, RD == kRdInterpSaves>(prog, e);
-#pragma unroll
-    for (int j = 0; j < EPT; ++j) kept[j] = ((keep >> j) & 1u) != 0u;
-  }
-}
-
-// Calls f(std::integral_constant<int, mode>{}) for a reduction mode chosen at run time.
-#define DC_RD_CMP_MODES(X, SHAPE)                                                                        \
-  X(rd_canon(SHAPE, DC_LQ_CMP_GT)) X(rd_canon(SHAPE, DC_LQ_CMP_GE)) X(rd_canon(SHAPE, DC_LQ_CMP_LT)) \
-  X(rd_canon(SHAPE, DC_LQ_CMP_LE)) X(rd_canon(SHAPE, DC_LQ_CMP_EQ)) X(rd_canon(SHAPE, DC_LQ_CMP_NE))
-template <class F>
-void rd_dispatch(int mode, F&& f) {
-  switch (mode) {
-#define DC_RD_CASE(m)                   \
-  case (m):                             \
-    f(std::integral_constant<int, (m)>{}); \
-    return;
-    DC_RD_CASE(kRdInterpSaves)
-    DC_RD_CASE(kRdAffine)
-    DC_RD_CASE(rd_canon(kShapeM, DC_LQ_CMP_GT))
-    DC_RD_CMP_MODES(DC_RD_CASE, kShapeF)
-    DC_RD_CMP_MODES(DC_RD_CASE, kShapeFM)
-    DC_RD_CMP_MODES(DC_RD_CASE, kShapeMF)
-#undef DC_RD_CASE
-    default:
-      f(std::integral_constant<int, kRdInterp>{});
-      return;
-  }
-}
-#undef DC_RD_CMP_MODES
 
 // Elements before the first 16-byte boundary (the whole input when it is not 4-byte aligned).
 inline int64_t reduce_head(const float* in, int64_t n) {
@@ -1343,25 +1273,17 @@ __global__ __launch_bounds__(kFinalBlock) void where_select_minmax_pass2(const f
 
 // ---- strategy choice -----------------------------------------------------------------------------
 const void* rounds_kernel(int mode) {
-  switch (mode) {
-    case kRrF: return reinterpret_cast<const void*>(&where_select_rounds_kernel<kRrF>);
-    case kRrM: return reinterpret_cast<const void*>(&where_select_rounds_kernel<kRrM>);
-    case kRrFM: return reinterpret_cast<const void*>(&where_select_rounds_kernel<kRrFM>);
-    case kRrMF: return reinterpret_cast<const void*>(&where_select_rounds_kernel<kRrMF>);
-    case kRrInterpSaves: return reinterpret_cast<const void*>(&where_select_rounds_kernel<kRrInterpSaves>);
-    default: return reinterpret_cast<const void*>(&where_select_rounds_kernel<kRrInterp>);
-  }
+  const void* fn = nullptr;
+  rd_dispatch(mode, [&](auto m) { fn = reinterpret_cast<const void*>(&where_select_rounds_kernel<decltype(m)::value>); });
+  return fn;
 }
 
-// Picks the round-robin variant for a program and fills its canonical constants.
-int rounds_mode(const dc_linq_chain& prog, Canon2* canon) {
-  AffineChain aff{};
-  int shape = 0;
-  if (lower_affine(prog, &aff) && lower_canon2(aff, canon, &shape)) {
-    return shape == kShapeF ? kRrF : shape == kShapeM ? kRrM : shape == kShapeFM ? kRrFM : kRrMF;
-  }
-  *canon = Canon2{1.0f, 0.0f, 1.0f, -0.0f, 0u, 0u, 1u};
-  return program_uses_saves(prog) ? kRrInterpSaves : kRrInterp;
+// Every program variant (rd_dispatch's cases).
+std::vector<int> all_reduce_modes() {
+  std::vector<int> m = {kRdInterp, kRdInterpSaves, kRdAffine, rd_canon(kShapeM, DC_LQ_CMP_GT)};
+  for (int shape : {kShapeF, kShapeFM, kShapeMF})
+    for (int cmp = DC_LQ_CMP_GT; cmp <= DC_LQ_CMP_NE; ++cmp) m.push_back(rd_canon(shape, cmp));
+  return m;
 }
 
 uint32_t rounds_groups(const dc_hip_ctx* ctx) { return (uint32_t)std::min(ctx->cu_count, kRrMaxGroups); }
@@ -1374,7 +1296,7 @@ bool use_rounds(dc_hip_ctx* ctx, const float* input, int64_t n) {
   if (!dc::aligned16(input) || groups == 0 || n / kRrTile < (int64_t)kRrMinRounds * groups) return false;
   if (ctx->rounds_fit < 0) {
     bool fit = true;
-    for (int mode : {kRrInterp, kRrInterpSaves, kRrF, kRrM, kRrFM, kRrMF}) {
+    for (int mode : all_reduce_modes()) {
       int per_cu = 0;
       if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, rounds_kernel(mode), kRrBlock, 0) != hipSuccess ||
           per_cu < 1)
@@ -1418,8 +1340,10 @@ DC_HIP_API int32_t dc_hip_linq_where_select_f32(dc_hip_ctx* ctx, const dc_linq_c
   if (n >= (int64_t)1 << 40) return DC_ERR_INVALID_ARGUMENT;  // 40-bit counts in the status words
   DC_CTX_ENTER(ctx);
   if ((chain->flags & DC_LINQ_FLAG_ORDERED_GRID) == 0 && use_rounds(ctx, input, n)) {
-    Canon2 canon{};
-    const void* fn = rounds_kernel(rounds_mode(*chain, &canon));
+    const ReducePlan plan = reduce_plan(*chain);
+    const void* fn = rounds_kernel(plan.mode);
+    AffineChain aff = plan.aff;
+    RdConst canon = plan.k;
     const uint32_t groups = rounds_groups(ctx);
     const int64_t tiles = (n + kRrTile - 1) / kRrTile;
     const size_t words = (size_t)((tiles + groups - 1) / groups + 1) * groups;
@@ -1433,7 +1357,8 @@ DC_HIP_API int32_t dc_hip_linq_where_select_f32(dc_hip_ctx* ctx, const dc_linq_c
     uint32_t* counts_arg = ctx->round_counts;
     uint32_t groups_arg = groups;
     uint32_t* done_arg = ctx->counters + DC_SLOT_LINQ_DONE;
-    void* args[] = {&prog, &canon, &in_arg, &n_arg, &out_arg, &count_arg, &counts_arg, &epoch16, &groups_arg, &done_arg};
+    void* args[] = {&prog, &aff, &canon, &in_arg, &n_arg, &out_arg, &count_arg, &counts_arg, &epoch16, &groups_arg,
+                    &done_arg};
     // One workgroup per CU, each needing most of a CU's LDS, on an otherwise idle device: every
     // workgroup is resident at once (an ordinary launch; measured faster than a cooperative one).
     DC_RETURN_IF(dc::resident_launch_begin(ctx));
