@@ -642,7 +642,7 @@ constexpr int kRrChunk = dc::kWave * kRrEpt;             // 512 elements per wor
 constexpr int64_t kRrTile = (int64_t)kRrWorkers * kRrChunk;  // 7680 elements = 30 KiB
 constexpr int kRrAhead = 4;
 constexpr int kRrDelay = 4;                              // measured: 3 -> 4 saves ~4 us at 256M
-constexpr int kRrRing = (kRrDelay + 1) * kRrChunk;       // floats per worker wave: 10 KiB, 150 KiB per workgroup
+constexpr int kRrRing = (kRrDelay + 1) * kRrChunk;       // floats per worker wave: 10 KiB, 154 KiB per workgroup
 constexpr int kRrCountsPerLane = 4;
 constexpr int kRrMaxGroups = dc::kWave * kRrCountsPerLane;  // P <= 256
 constexpr uint32_t kRrSpinLimit = 1u << 22;              // ~seconds: a wait that never ends reports
@@ -706,7 +706,7 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
     float* __restrict__ out,
     int64_t* __restrict__ count_out, uint32_t* __restrict__ counts, uint32_t epoch16, uint32_t P,
     uint32_t* __restrict__ done) {
-  __shared__ float s_ring[kRrWorkers][kRrRing];
+  __shared__ float s_ring[kRrWorkers][kRrRing + dc::kWave];  // + a discard slot per lane
   // ring positions stay in [0, kRrRing); a position below 2 * kRrRing wraps with one unsigned min
   auto wrap = [](uint32_t q) __attribute__((always_inline)) { return min(q, q - (uint32_t)kRrRing); };
   __shared__ uint32_t s_wcount[8][16];  // kept count of (tile slot, worker wave)
@@ -793,8 +793,12 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
     for (int j = 0; j < kRrVec; ++j) {
       uint32_t p = head + pos[j];
 #pragma unroll
-      for (int k = 0; k < 4; ++k)
-        if (kept[4 * j + k]) ring[wrap(p++)] = e[4 * j + k];
+      for (int k = 0; k < 4; ++k) {
+        // branch-free: a dropped element goes to the lane's discard slot past the ring
+        const uint32_t q = kept[4 * j + k] ? wrap(p) : (uint32_t)(kRrRing + lane);
+        ring[q] = e[4 * j + k];
+        p += kept[4 * j + k] ? 1u : 0u;
+      }
     }
     head = wrap(head + run);
     if (lane == 0) {
