@@ -629,20 +629,23 @@ __global__ __launch_bounds__(kBlock) void where_select_kernel(const dc_linq_chai
 //   - the program is one of the compile-time variants (shape and comparison fixed for the one- and
 //     two-stage affine chains): the kernel is bound by its instruction issue at this rate, so
 //     the per-element work is kept to a compare, the map, and the ballot ranking.
-// Roles inside the 1024-thread workgroup: wave 0 reads and checks the count words and broadcasts the
-// output offset; waves 1..15 each own a contiguous 512-element chunk of every tile, rank their kept
+// Roles inside the 576-thread workgroup: wave 0 reads and checks the count words and broadcasts the
+// output offset; waves 1..8 each own a contiguous 1024-element chunk of every tile, rank their kept
 // elements with ballot + mbcnt, stage them in a private LDS ring (in input order) and later write
 // them as one contiguous run. The last wave to finish a tile (an LDS atomic) publishes its count.
 // One workgroup barrier per round.
-constexpr int kRrBlock = 1024;
-constexpr int kRrWorkers = kRrBlock / dc::kWave - 1;     // 15 worker waves
-constexpr int kRrVec = 2;                                // 16-byte loads per lane per tile
-constexpr int kRrEpt = 4 * kRrVec;                       // 8 elements per lane
-constexpr int kRrChunk = dc::kWave * kRrEpt;             // 512 elements per worker wave
-constexpr int64_t kRrTile = (int64_t)kRrWorkers * kRrChunk;  // 7680 elements = 30 KiB
+// Geometry (measured at 256M, 50% kept: 8 workers x 4 vectors 290 us, 15 x 2 293 us, 12 x 3 297 us):
+// fewer, wider worker waves spread the per-round fixed work (ranking tables, the barrier) over
+// more elements.
+constexpr int kRrBlock = 9 * dc::kWave;
+constexpr int kRrWorkers = kRrBlock / dc::kWave - 1;     // 8 worker waves
+constexpr int kRrVec = 4;                                // 16-byte loads per lane per tile
+constexpr int kRrEpt = 4 * kRrVec;                       // 16 elements per lane
+constexpr int kRrChunk = dc::kWave * kRrEpt;             // 1024 elements per worker wave
+constexpr int64_t kRrTile = (int64_t)kRrWorkers * kRrChunk;  // 8192 elements = 32 KiB
 constexpr int kRrAhead = 4;
-constexpr int kRrDelay = 4;                              // measured: 3 -> 4 saves ~4 us at 256M
-constexpr int kRrRing = (kRrDelay + 1) * kRrChunk;       // floats per worker wave: 10 KiB, 154 KiB per workgroup
+constexpr int kRrDelay = 3;
+constexpr int kRrRing = (kRrDelay + 1) * kRrChunk;       // floats per worker wave: 16 KiB, 130 KiB per workgroup
 constexpr int kRrCountsPerLane = 4;
 constexpr int kRrMaxGroups = dc::kWave * kRrCountsPerLane;  // P <= 256
 constexpr uint32_t kRrSpinLimit = 1u << 22;              // ~seconds: a wait that never ends reports
@@ -1293,7 +1296,7 @@ std::vector<int> all_reduce_modes() {
 uint32_t rounds_groups(const dc_hip_ctx* ctx) { return (uint32_t)std::min(ctx->cu_count, kRrMaxGroups); }
 
 // The round-robin kernel needs a 16-byte aligned input of at least kRrMinRounds full rounds and
-// room for one 1024-thread workgroup per CU (every program variant; asked once per context). The
+// room for one workgroup per CU (every program variant; asked once per context). The
 // caller holds the context lock.
 bool use_rounds(dc_hip_ctx* ctx, const float* input, int64_t n) {
   const uint32_t groups = rounds_groups(ctx);

@@ -276,8 +276,8 @@ def test_affine_fast_path_matches_interpreter(ctx, idx):
 
 
 # ---- the round-robin kernel (large, 16-byte aligned inputs) ------------------------------------
-# Tiles of 15 worker waves x 64 lanes x 8 elements; used from 4 full rounds of min(CUs, 256) tiles.
-RR_TILE = 15 * 64 * 8
+# Tiles of 8 worker waves x 64 lanes x 16 elements; used from 4 full rounds of min(CUs, 256) tiles.
+RR_TILE = 8 * 64 * 16
 
 
 def rr_min_n():
