@@ -49,7 +49,8 @@ struct dc_hip_ctx {
   uint32_t round_epoch = 0;
   // Whether one 1024-thread workgroup of each round-robin kernel fits on a CU: -1 not yet asked.
   int rounds_fit = -1;
-  // Completion event of this context's last resident-grid launch (see dc::resident_launch_*).
+  // Recorded on this context's stream when another context's resident grid must follow this one's
+  // (dc::ResidentLaunch).
   hipEvent_t resident_done = nullptr;
 
   // Device address of the static scratch array of dc_hip_linq_where_select_sum_f32_noalloc on this
@@ -108,13 +109,27 @@ int32_t ensure_round_counts(dc_hip_ctx* ctx, size_t words, uint32_t* epoch_out);
 // Resident grids (kernels whose workgroups wait for each other, launched with one workgroup per CU)
 // must not share the device with another resident grid: two such grids could each hold half of
 // the CUs while waiting for workgroups that cannot start. Every resident launch of this library
-// on a device is therefore ordered after the previous one, from any context of the process:
-// resident_launch_begin makes the context stream wait for the previous resident grid of the
-// device; resident_launch_end records this launch as the new last one. The caller holds the
-// context lock. (Other processes on the same device are not covered; the kernels' waits are
-// bounded and report a failure instead of hanging.)
-int32_t resident_launch_begin(dc_hip_ctx* ctx);
-int32_t resident_launch_end(dc_hip_ctx* ctx);
+// on a device is therefore ordered after the previous one, from any context of the process. A
+// ResidentLaunch holds the device's slot lock from construction to destruction, so resident
+// enqueues on a device never interleave; when the previous resident grid came from another
+// context, the constructor records an event on that context's stream (behind its grid) and makes
+// this context's stream wait for it. A context that follows itself records nothing. The caller
+// holds the context lock, enqueues the grid, then calls done(). (Other processes on the same
+// device are not covered; the kernels' waits are bounded and report a failure instead of hanging.)
+class ResidentLaunch {
+ public:
+  explicit ResidentLaunch(dc_hip_ctx* ctx);
+  ~ResidentLaunch();
+  ResidentLaunch(const ResidentLaunch&) = delete;
+  ResidentLaunch& operator=(const ResidentLaunch&) = delete;
+  int32_t status() const { return status_; }
+  void done();  // the grid is enqueued: this context now holds the device's last resident grid
+
+ private:
+  dc_hip_ctx* ctx_;
+  std::mutex* mu_ = nullptr;
+  int32_t status_ = 0;
+};
 // Forgets the context's event (context destruction).
 void resident_forget(dc_hip_ctx* ctx);
 // Looks up the device address of the no-alloc LINQ Sum's static scratch for ctx->device (the

@@ -1368,10 +1368,12 @@ DC_HIP_API int32_t dc_hip_linq_where_select_f32(dc_hip_ctx* ctx, const dc_linq_c
                     &done_arg};
     // One workgroup per CU, each needing most of a CU's LDS, on an otherwise idle device: every
     // workgroup is resident at once (an ordinary launch; measured faster than a cooperative one).
-    DC_RETURN_IF(dc::resident_launch_begin(ctx));
+    dc::ResidentLaunch resident(ctx);
+    DC_RETURN_IF(resident.status());
     DC_RETURN_IF_HIP(hipLaunchKernel(fn, dim3(groups), dim3(kRrBlock), args, 0, ctx->stream));
     DC_RETURN_IF(dc::last_launch_status());
-    return dc::resident_launch_end(ctx);
+    resident.done();
+    return DC_OK;
   }
 
   AffineChain aff{};

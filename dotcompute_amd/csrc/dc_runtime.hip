@@ -181,21 +181,29 @@ struct ResidentSlot {
 ResidentSlot g_resident[64];
 }  // namespace
 
-int32_t resident_launch_begin(dc_hip_ctx* ctx) {
-  if (ctx->device < 0 || ctx->device >= 64) return DC_ERR_UNSUPPORTED;
-  if (!ctx->resident_done) DC_RETURN_IF_HIP(hipEventCreateWithFlags(&ctx->resident_done, hipEventDisableTiming));
+ResidentLaunch::ResidentLaunch(dc_hip_ctx* ctx) : ctx_(ctx) {
+  if (ctx->device < 0 || ctx->device >= 64) {
+    status_ = DC_ERR_UNSUPPORTED;
+    return;
+  }
   ResidentSlot& slot = g_resident[ctx->device];
-  std::lock_guard<std::mutex> lock(slot.mu);
-  if (slot.last_ctx && slot.last_ctx != ctx) DC_RETURN_IF_HIP(hipStreamWaitEvent(ctx->stream, slot.last_ctx->resident_done, 0));
-  return DC_OK;
+  slot.mu.lock();
+  mu_ = &slot.mu;
+  dc_hip_ctx* prev = slot.last_ctx;
+  if (!prev || prev == ctx) return;
+  hipError_t e = hipSuccess;
+  if (!prev->resident_done) e = hipEventCreateWithFlags(&prev->resident_done, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventRecord(prev->resident_done, prev->stream);
+  if (e == hipSuccess) e = hipStreamWaitEvent(ctx->stream, prev->resident_done, 0);
+  status_ = (int32_t)e;
 }
 
-int32_t resident_launch_end(dc_hip_ctx* ctx) {
-  ResidentSlot& slot = g_resident[ctx->device];
-  std::lock_guard<std::mutex> lock(slot.mu);
-  DC_RETURN_IF_HIP(hipEventRecord(ctx->resident_done, ctx->stream));
-  slot.last_ctx = ctx;
-  return DC_OK;
+ResidentLaunch::~ResidentLaunch() {
+  if (mu_) mu_->unlock();
+}
+
+void ResidentLaunch::done() {
+  if (mu_) g_resident[ctx_->device].last_ctx = ctx_;
 }
 
 void resident_forget(dc_hip_ctx* ctx) {
