@@ -151,6 +151,9 @@ def main() -> int:
         from bench_extras import bench_spmv  # noqa: E402
 
         extra.update(bench_spmv(ctx, log, warm_timer, roofline, HBM_PEAK_GBS, cpu=not args.skip_cpu))
+        for leg in ("spmv_power20_1M", "spmv_power20_16M"):  # bytes per step, as `achieved`
+            if leg in extra:
+                extra[leg]["roofline"]["traffic"] = measured_traffic("spmv_power_traffic.md", leg)
 
     # ---------------- fused Where->Select->Sum and plain Sum at 256M --------------------------
     if want("linq_sum"):
