@@ -1,8 +1,8 @@
 // dc_streaming.hip — HBM-bound streaming kernels for gfx950: VectorAdd and the deterministic
 // float64-accumulated / int64-exact sum reductions.
 //
-// Layout: inputs are contiguous 1-D arrays in HBM; every thread moves 16-byte vectors
-// (global_load_dwordx4) with a grid-stride loop, several loads in flight per thread.
+// Layout: inputs are contiguous 1-D arrays in HBM; every workgroup streams one contiguous chunk
+// of 16-byte vectors (global_load_dwordx4), several loads in flight per thread.
 // Reductions: per-thread accumulators in a fixed order -> DPP wave tree -> LDS block tree ->
 // per-block partial -> a one-block pass sums the partials in block order. Fixed grid size for a
 // given n, so the result is bit-reproducible run to run.
@@ -19,19 +19,32 @@ constexpr int kBlock = 256;
 // ---------------------------------------------------------------------------------------------
 // VectorAdd: result[i] = a[i] + b[i] (one rounding per element, bit-exact with any IEEE CPU).
 // ---------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(kBlock) void vector_add_f32x4_kernel(const dc::f32x4* __restrict__ a,
-                                                                  const dc::f32x4* __restrict__ b,
-                                                                  dc::f32x4* __restrict__ r, int64_t n4,
-                                                                  const float* __restrict__ a_tail,
-                                                                  const float* __restrict__ b_tail,
-                                                                  float* __restrict__ r_tail, int tail) {
-  int64_t i = blockIdx.x * (int64_t)kBlock + threadIdx.x;
-  const int64_t stride = (int64_t)gridDim.x * kBlock;
-  for (; i < n4; i += stride) {
-    dc::f32x4 x = dc::load_stream(a + i);
-    dc::f32x4 y = dc::load_stream(b + i);
-    __builtin_nontemporal_store(x + y, r + i);
+// 16-byte aligned operands: each workgroup adds one contiguous chunk, every thread with
+// kVaUnroll vector pairs in flight, non-temporal loads and stores (the output is written in whole
+// lines and not read again here). Measured at 256M (3.2 GB): 566 us with 512-thread workgroups,
+// 4 per CU and 2 pairs in flight, against 613 us for a grid-stride loop.
+constexpr int kVaBlock = 512;
+constexpr int kVaUnroll = 2;
+__global__ __launch_bounds__(kVaBlock) void vector_add_f32x4_kernel(const dc::f32x4* __restrict__ a,
+                                                                    const dc::f32x4* __restrict__ b,
+                                                                    dc::f32x4* __restrict__ r, int64_t n4,
+                                                                    const float* __restrict__ a_tail,
+                                                                    const float* __restrict__ b_tail,
+                                                                    float* __restrict__ r_tail, int tail) {
+  const int64_t per = (n4 + gridDim.x - 1) / gridDim.x;
+  const int64_t v0 = min(n4, (int64_t)blockIdx.x * per), v1 = min(n4, v0 + per);
+  int64_t i = v0 + threadIdx.x;
+  for (; i + (kVaUnroll - 1) * kVaBlock < v1; i += kVaUnroll * kVaBlock) {
+    dc::f32x4 x[kVaUnroll], y[kVaUnroll];
+#pragma unroll
+    for (int u = 0; u < kVaUnroll; ++u) {
+      x[u] = dc::load_stream(a + i + u * kVaBlock);
+      y[u] = dc::load_stream(b + i + u * kVaBlock);
+    }
+#pragma unroll
+    for (int u = 0; u < kVaUnroll; ++u) __builtin_nontemporal_store(x[u] + y[u], r + i + u * kVaBlock);
   }
+  for (; i < v1; i += kVaBlock) __builtin_nontemporal_store(dc::load_stream(a + i) + dc::load_stream(b + i), r + i);
   if (blockIdx.x == 0 && threadIdx.x < tail) r_tail[threadIdx.x] = a_tail[threadIdx.x] + b_tail[threadIdx.x];
 }
 
@@ -410,8 +423,10 @@ DC_HIP_API int32_t dc_hip_vector_add_f32(dc_hip_ctx* ctx, const float* a, const 
   if (dc::aligned16(a) && dc::aligned16(b) && dc::aligned16(result)) {
     int64_t n4 = n >> 2;
     int tail = (int)(n & 3);
-    int64_t blocks = std::max<int64_t>(1, std::min<int64_t>((n4 + kBlock - 1) / kBlock, 32768));
-    vector_add_f32x4_kernel<<<(unsigned)blocks, kBlock, 0, ctx->stream>>>(
+    // four workgroups per CU; small inputs: one vector per thread (the latency of one round trip)
+    const int64_t blocks = std::max<int64_t>(
+        1, std::min<int64_t>((n4 + kVaBlock - 1) / kVaBlock, 4 * (int64_t)std::max(ctx->cu_count, 1)));
+    vector_add_f32x4_kernel<<<(unsigned)blocks, kVaBlock, 0, ctx->stream>>>(
         reinterpret_cast<const dc::f32x4*>(a), reinterpret_cast<const dc::f32x4*>(b),
         reinterpret_cast<dc::f32x4*>(result), n4, a + (n4 << 2), b + (n4 << 2), result + (n4 << 2), tail);
   } else {
