@@ -1006,6 +1006,13 @@ void plan_shape(dc_hip_spmv_plan* p, int64_t rows, int64_t cols, int64_t nnz, in
     if (cols <= 2 * wmax) S = 2;
     else if (cols <= 4 * wmax) S = 4;
     else S = std::min<int64_t>(kMaxSlices, kXcds * ((cols + kXcds * wmax - 1) / (kXcds * wmax)));
+  } else if (slice_cols_max == 0) {
+    // x fits one slice, but every XCD gathering from all of it (with the nonzeros streaming
+    // through the same L2) misses far more than an XCD holding a share of at most 512 KB: with
+    // S < 8 slices, XCD j takes slice j % S. Measured at 1M rows: S = 1 58.8 us per SpMV, S = 2
+    // 51.5, S = 4 48.5, S = 8 48.3, S = 16 56.7 (more segments than the cache saves).
+    const int64_t xbytes = cols * 4;
+    S = xbytes <= (int64_t{512} << 10) ? 1 : xbytes <= (int64_t{1} << 20) ? 2 : xbytes <= (int64_t{2} << 20) ? 4 : 8;
   }
   p->slices = (int32_t)S;
   p->slice_cols = std::max<int64_t>(1, (cols + S - 1) / S);

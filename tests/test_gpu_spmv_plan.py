@@ -75,9 +75,12 @@ def check(rp, col, val, x, y, width):
     assert np.array_equal(y[ok].view(np.uint32), ref32[ok].view(np.uint32))
 
 
-# (rows, cols, slice_cols_max) -> expected number of slices
+# (rows, cols, slice_cols_max) -> expected number of slices. Default width (0): one slice up to
+# 512 KB of x, else 2 / 4 / 8 slices up to 1 / 2 / 4 MB (an XCD's share of x at most 512 KB).
 SHAPES = [
     (5000, 5000, 0, 1),
+    (200_000, 200_000, 0, 2),
+    (600_000, 600_000, 0, 8),
     (5000, 5000, 2500, 2),
     (5000, 5000, 1250, 4),
     (5000, 5000, 625, 8),
@@ -120,12 +123,13 @@ def test_plan_signed_values_and_long_segments(ctx):
 
 
 def test_plan_one_slice_equals_sequential_reference(ctx):
-    """One slice: every row is one segment, so rows of at most 32 nonzeros (about 99% of the rows
-    of this graph) are the sequential float32 row sum of SparseOps.SpMV bit for bit."""
+    """One slice (asked for with a slice width of all the columns): every row is one segment, so
+    rows of at most 32 nonzeros (about 99% of the rows of this graph) are the sequential float32
+    row sum of SparseOps.SpMV bit for bit."""
     rows = 300_000
     rp, col, val = oracle.gen_zipf_csr(rows, 7)
     x = oracle.gen_uniform_f32(rows, 7, 5, unit_interval=True)
-    y, (s, _, _) = run_plan(ctx, rp, col, val, x, 0, repeat=1)
+    y, (s, _, _) = run_plan(ctx, rp, col, val, x, rows, repeat=1)
     assert s == 1
     ref = oracle.spmv_csr_f32(rp, col, val, x)
     short = np.diff(rp) <= SEQ_SEG
