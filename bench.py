@@ -213,6 +213,11 @@ def main() -> int:
                             "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
             log(f"[bench] {label}: {ms*1e3:.2f} us -> {gbs:.0f} GB/s")
             ctx.free(b)
+    # HBM bytes per launch of the streaming legs, from their FETCH_SIZE / WRITE_SIZE counters
+    for leg in ("sum_f32_256M", "sum_i32_256M", "where_select_sum_f32_256M", "where_select_min_f32_256M",
+                "where_select_max_f32_256M", "vector_add_f32_100K", "vector_add_f32_256M"):
+        if leg in extra:
+            extra[leg]["roofline"]["traffic"] = measured_traffic("streaming_legs_traffic.md", leg)
 
     # ---------------- cache-resident sizes of the streaming configs (1M and 16M elements) ------
     # 4 MB and 64 MB inputs stay in the 256 MB memory-side cache between launches: these rates are
