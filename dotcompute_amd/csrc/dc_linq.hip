@@ -711,7 +711,21 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
     uint32_t* __restrict__ done) {
   __shared__ float s_ring[kRrWorkers][kRrRing + dc::kWave];  // + a discard slot per lane
   // ring positions stay in [0, kRrRing); a position below 2 * kRrRing wraps with one unsigned min
-  auto wrap = [](uint32_t q) __attribute__((always_inline)) { return min(q, q - (uint32_t)kRrRing); };
+  auto wrap = [](uint32_t q) __attribute__((always_inline)) {
+    if constexpr ((kRrRing & (kRrRing - 1)) == 0) return q & (uint32_t)(kRrRing - 1);
+    else return min(q, q - (uint32_t)kRrRing);
+  };
+  // Filter-then-map chains stage the raw value and map it when the run is written: only the
+  // kept elements pay for the map.
+  constexpr bool kLazyMap = rd_is_canon(RD) && rd_shape(RD) == kShapeFM;
+  auto apply = [&](float (&e)[kRrEpt], bool (&kept)[kRrEpt]) __attribute__((always_inline)) {
+    if constexpr (kLazyMap) {
+#pragma unroll
+      for (int j = 0; j < kRrEpt; ++j) kept[j] = rd_compare<rd_cmp(RD)>(e[j], canon.t);
+    } else {
+      apply_reduce_flags<RD, kRrEpt>(prog, aff, canon, e, kept);
+    }
+  };
   __shared__ uint32_t s_wcount[8][16];  // kept count of (tile slot, worker wave)
   __shared__ uint32_t s_acc[8];         // (waves finished << 24) | kept so far, per tile slot
   __shared__ int64_t s_off[2];          // output offset of the tile being written, by round parity
@@ -822,7 +836,14 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
       cnt = i == ww ? c : cnt;
     }
     float* dst = out + s_off[parity] + before;
-    for (uint32_t i = lane; i < cnt; i += dc::kWave) dst[i] = ring[wrap(tail + i)];
+    for (uint32_t i = lane; i < cnt; i += dc::kWave) {
+      float v = ring[wrap(tail + i)];
+      if constexpr (kLazyMap) {
+        v = v * canon.a;
+        v = v + canon.b;
+      }
+      dst[i] = v;
+    }
     tail = wrap(tail + cnt);
   };
 
@@ -845,7 +866,7 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
   auto round = [&](float (&ec)[kRrEpt], float (&en)[kRrEpt]) __attribute__((always_inline)) {
     load(en, min(r + kRrAhead, last));
     bool kept[kRrEpt];
-    apply_reduce_flags<RD, kRrEpt>(prog, aff, canon, ec, kept);
+    apply(ec, kept);
     stage(ec, kept, r);
     __syncthreads();
     if (r >= (uint32_t)kRrDelay) write(r - kRrDelay, r & 1);
@@ -873,7 +894,7 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
       valid |= ((1u << (uint32_t)nv) - 1u) << (4 * j);
     }
     bool kept[kRrEpt];
-    apply_reduce_flags<RD, kRrEpt>(prog, aff, canon, e, kept);
+    apply(e, kept);
 #pragma unroll
     for (int i = 0; i < kRrEpt; ++i) kept[i] = kept[i] && ((valid >> i) & 1u);
     stage(e, kept, R0);
