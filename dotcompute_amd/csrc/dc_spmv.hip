@@ -213,46 +213,45 @@ int32_t check_csr(const int32_t* rp, const int32_t* col, const float* val, int64
 }
 
 // =============================================================================================
-// Column-sliced plan for repeated SpMV (the power iteration; any CsrMatrix multiplied many times).
+// Tiled plan for repeated SpMV (the power iteration; any CsrMatrix multiplied many times).
 //
-// Random 4-byte gathers from a vector far larger than one XCD's 4 MB L2 miss in L2 and are served
-// by the memory-side cache at ~60 G gathers/s on MI355X; gathers confined to a 4 MB range per XCD
-// hit in L2 and run ~4x faster (measured with a standalone probe). The plan therefore cuts the
-// columns into S slices of at most kSliceCols columns (4 MB of x) and rebuilds the matrix slice by
-// slice: slice s holds the nonzeros of every row whose column falls in s, in row order, as
-// "segments" (one segment per nonempty (row, slice) pair). Workgroup w runs on XCD w % 8 (the
-// dispatcher's round-robin; correctness never depends on it), and XCD j only processes windows of
-// the slices s with s % 8 == j (S >= 8), or its share of slice j % S (S < 8), so each XCD gathers
-// from one 4 MB range at a time.
-//   gather pass: one wave per window of kWW nonzeros; products into the wave's LDS, then one lane
-//     per segment adds them in index order -> partial[segment].
-//   combine pass: one thread per row adds its segments' partials in slice order (0.0f + p0 + p1
-//     ...). With S == 1 every row is one segment and the result equals the sequential row sum.
-// Segments longer than kLongSeg go to a workgroup-per-segment pass (fixed-order tree).
-// The analysis (count, scan, scatter, window descriptors) runs on the device, once per plan.
+// The cost of a CSR SpMV is its random 4-byte gathers from x. Served by L2 they are bound by the
+// rate of L1-miss requests a CU keeps in flight (about 0.3 per cycle per CU on MI355X), served by
+// the memory-side cache by far less. The plan moves every gather into LDS:
+//   - columns are cut into slices of at most kTileCols columns (a 128 KB tile of x, one CU's LDS);
+//   - rows are cut into blocks: row r is in block rp[r] / kBlockSpan + r / kBlockRows, so a block
+//     holds fewer than kStage nonzeros unless it ends with a giant row (more than kGiantRow
+//     nonzeros; at most one per block, always its last row: the next row starts past the block's
+//     span);
+//   - the plan keeps a slice-major copy of the nonzeros: slice s holds, block after block, the
+//     nonzeros of block b whose column falls in s (the run (b, s)), each with its column within
+//     the slice (uint16), its value, and its position within the block's CSR range (uint16).
+//     Giant rows are kept in CSR order in one more region (slice index S), their column split over
+//     the two uint16 arrays.
+// product pass: persistent workgroups split the slice-major entries evenly; a workgroup loads the
+//   x tile of each slice its share touches into LDS and streams p = val · x_tile[col16] (16-byte
+//   loads and stores).
+// row pass: a workgroup per block stages the block's products from its runs into LDS at their CSR
+//   positions, then sums each row: rows of at most kSeqRow nonzeros one lane each, sequentially in
+//   index order (0.0f + p_0 + p_1 + ...: the reference's float32 row sum bit for bit), longer rows
+//   by the whole wave (lane k adds products k, k + 64, ... in order, then a fixed DPP tree); giant
+//   rows the same way with their products formed from x directly.
+// Both passes stream; only the LDS gathers are random. The analysis (block bounds, per-(slice,
+// block) counts, their scans, the scatter) runs on the device, once per plan.
 // =============================================================================================
-constexpr int kRB = 256;                  // rows per analysis / combine workgroup (a thread per row)
-constexpr int kMaxSlices = 32;
-constexpr int64_t kSliceCols = 1 << 20;   // columns per slice: 4 MB of x, one XCD's L2
-constexpr int kWW = 512;                  // nonzeros per wave window
-constexpr int kLongSeg = 256;             // longer segments go to the long-segment pass
-constexpr int kSeqSeg = 32;               // longer segments are summed by the whole wave
-constexpr int kSpan = kWW + kLongSeg;     // products a window can hold (its segments end before this)
+constexpr int kTileCols = 32768;          // columns per slice: a 128 KB x tile
+constexpr int kBlockSpan = 8192;          // row r is in block rp[r] / kBlockSpan + r / kBlockRows
+constexpr int kBlockRows = 16384;
+constexpr int kStage = 2 * kBlockSpan;    // products of a block's rows other than a giant one (64 KB)
+constexpr int kGiantRow = kBlockSpan;     // longer rows are giant
+constexpr int kSeqRow = 32;               // rows up to this length are summed by one lane
+constexpr int kPass = 1024;               // threads per workgroup of the plan kernels
+constexpr int kPassWaves = kPass / 64;
+constexpr int kMaxSlices = 32768;         // (1 << 30) columns / kTileCols
+constexpr int kPad = 8;                   // slice regions start at multiples of 8 entries
+constexpr int kRowRuns = 1024;            // up to this many slices, blocks are staged through LDS tables
+constexpr int kRowPre = 2;                // row pass: row steps whose bounds are loaded before staging
 constexpr int kXcds = 8;
-constexpr int kGatherBlock = 256;         // 4 waves, each with its own windows
-constexpr int kXcdWords = 8;              // per (phase, XCD): nranges, total, (start, count, stride)
-constexpr int kMaxPhases = kMaxSlices / 8;
-constexpr int kScanBlock = 1024;
-
-__device__ inline uint32_t lane_rank(uint64_t m) {
-  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-}
-
-__device__ inline void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 __device__ inline int32_t wave_incl_scan(int32_t v) {
   const int lane = threadIdx.x & 63;
@@ -267,333 +266,17 @@ __device__ inline int32_t wave_incl_scan(int32_t v) {
 // Column -> slice. Columns outside [0, cols) are clamped into range, so a malformed matrix can never
 // index outside x or the slice tables (the managed CsrMatrix rejects such columns before this).
 __device__ inline uint32_t clamp_col(int32_t c, uint32_t cols) { return (uint32_t)c < cols ? (uint32_t)c : cols - 1; }
+__device__ inline int32_t clamp_nz(int32_t v, int32_t nnz) { return min(max(v, 0), nnz); }
 
-// The nonzeros of 64 consecutive rows are contiguous in CSR order, so a wave streams them in
-// coalesced chunks of 64. Lane l holds the first nonzero of row rw0 + l (clamped into the wave's
-// range); the row of element i is the last lane whose start is <= i.
-struct WaveRows {
-  int32_t start;     // this lane's row start (nz1 for lanes past the last row)
-  int32_t nz0, nz1;  // nonzero range of the wave's rows, clamped to [0, nnz]
-};
-
-__device__ inline WaveRows wave_rows(const int32_t* __restrict__ rp, int64_t rw0, int64_t rows, int32_t nnz) {
-  const int lane = threadIdx.x & 63;
-  const int64_t rw1 = min(rw0 + 64, rows);
-  WaveRows w;
-  w.nz0 = min(max(rp[rw0], 0), nnz);
-  w.nz1 = min(max(rp[rw1], w.nz0), nnz);
-  const int64_t r = rw0 + lane;
-  w.start = r < rw1 ? min(max(rp[r], w.nz0), w.nz1) : w.nz1;
-  return w;
-}
-
-// Lane (0..63) of the row holding element i: six shuffles over the lanes' row starts.
-__device__ inline int wave_row_of(int32_t start, int32_t i) {
-  int l = 0;
-#pragma unroll
-  for (int step = 32; step > 0; step >>= 1)
-    if (__shfl(start, l + step, 64) <= i) l += step;
-  return l;
-}
-
-// Counts the wave's rows into cnt[row][slice] (LDS adds without return). kChunks chunks of column
-// loads go out together, so a wave waits one memory round trip per kChunks * 64 nonzeros.
-constexpr int kChunks = 4;
-template <int SMAX>
-__device__ inline void wave_count(const int32_t* __restrict__ col, const WaveRows& w, uint32_t cols, uint32_t width,
-                                  int32_t (*cnt)[SMAX + 1]) {
-  const int lane = threadIdx.x & 63;
-  for (int32_t base = w.nz0; base < w.nz1; base += 64 * kChunks) {
-    int32_t c[kChunks];
-#pragma unroll
-    for (int u = 0; u < kChunks; ++u) c[u] = col[min(base + 64 * u + lane, w.nz1 - 1)];  // base < nz1
-#pragma unroll
-    for (int u = 0; u < kChunks; ++u) {
-      const int32_t i = base + 64 * u + lane;
-      const int l = wave_row_of(w.start, i);
-      if (i < w.nz1) atomicAdd(&cnt[l][clamp_col(c[u], cols) / width], 1);
-    }
-  }
-}
-
-// Row blocks are handed to workgroups XCD by XCD: workgroup w (on XCD w % 8) takes block
-// (w % 8) * per + w / 8, so each XCD works through one contiguous range of rows and the
-// slice-major lines it writes are not shared with another XCD's L2. -1: no block for w.
+// Blocks are handed to workgroups XCD by XCD: workgroup w (on XCD w % 8) takes block
+// (w % 8) * per + w / 8, so each XCD works through one contiguous range of blocks, and the cache
+// lines that neighbouring blocks' runs share are fetched into one L2. -1: no block for w (the grid
+// is 8 * per).
 __device__ inline int32_t xcd_block(int32_t nblocks) {
   const int32_t per = (nblocks + kXcds - 1) / kXcds;
   const int32_t b = (int32_t)(blockIdx.x % kXcds) * per + (int32_t)(blockIdx.x / kXcds);
   return b < nblocks ? b : -1;
 }
-
-// P1: per (slice, block of kRB rows), the number of nonzeros and of segments. SMAX >= S sizes the
-// LDS table.
-template <int SMAX>
-__global__ __launch_bounds__(kRB) void plan_count(const int32_t* __restrict__ rp, const int32_t* __restrict__ col,
-                                                  int64_t rows, int32_t nnz, int32_t S, uint32_t width, uint32_t cols,
-                                                  int32_t* __restrict__ tn, int32_t* __restrict__ ts, int32_t ld,
-                                                  int32_t nblocks) {
-  __shared__ int32_t cnt[kRB][SMAX + 1];
-  const int32_t blk = xcd_block(nblocks);
-  if (blk < 0) return;  // whole workgroup
-  const int t = threadIdx.x, wave = t >> 6;
-  for (int s = 0; s < S; ++s) cnt[t][s] = 0;
-  __syncthreads();
-  const int64_t rw0 = (int64_t)blk * kRB + wave * 64;
-  if (rw0 < rows) wave_count<SMAX>(col, wave_rows(rp, rw0, rows, nnz), cols, width, cnt + wave * 64);
-  __syncthreads();
-  // Column sums over the block's rows: thread t -> slice t / 8, rows (t % 8) * 32 .. + 31.
-  const int s = t >> 3, part = t & 7;
-  int32_t n = 0, g = 0;
-  if (s < S) {
-    for (int k = 0; k < 32; ++k) {
-      const int32_t c = cnt[part * 32 + k][s];
-      n += c;
-      g += c > 0 ? 1 : 0;
-    }
-  }
-#pragma unroll
-  for (int off = 1; off < 8; off <<= 1) {
-    n += __shfl_xor(n, off, 64);
-    g += __shfl_xor(g, off, 64);
-  }
-  if (s < S && part == 0) {
-    tn[(int64_t)s * ld + blk] = n;
-    ts[(int64_t)s * ld + blk] = g;
-  }
-}
-
-// P2: workgroup s turns row s of tn and ts (entries 0..nblocks-1, leading dimension ld) into
-// exclusive prefix sums, with the slice total at entry nblocks; tot[s] / tot[S + s] = totals.
-__global__ __launch_bounds__(kScanBlock) void plan_scan(int32_t* __restrict__ tn, int32_t* __restrict__ ts,
-                                                        int32_t nblocks, int32_t ld, int32_t S,
-                                                        int32_t* __restrict__ tot) {
-  __shared__ int32_t wsum[2][kScanBlock / 64];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  int32_t* rn = tn + (int64_t)blockIdx.x * ld;
-  int32_t* rs = ts + (int64_t)blockIdx.x * ld;
-  int32_t carry_n = 0, carry_g = 0;
-  for (int32_t base = 0; base < nblocks; base += 4 * kScanBlock) {
-    int32_t vn[4], vg[4];
-    int32_t sn = 0, sg = 0;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int32_t i = base + 4 * t + k;
-      vn[k] = i < nblocks ? rn[i] : 0;
-      vg[k] = i < nblocks ? rs[i] : 0;
-      sn += vn[k];
-      sg += vg[k];
-    }
-    const int32_t in = wave_incl_scan(sn), ig = wave_incl_scan(sg);
-    if (lane == 63) {
-      wsum[0][wave] = in;
-      wsum[1][wave] = ig;
-    }
-    __syncthreads();
-    int32_t pn = carry_n, pg = carry_g, totn = 0, totg = 0;
-    for (int w = 0; w < kScanBlock / 64; ++w) {
-      if (w < wave) {
-        pn += wsum[0][w];
-        pg += wsum[1][w];
-      }
-      totn += wsum[0][w];
-      totg += wsum[1][w];
-    }
-    pn += in - sn;
-    pg += ig - sg;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int32_t i = base + 4 * t + k;
-      if (i < nblocks) {
-        rn[i] = pn;
-        rs[i] = pg;
-      }
-      pn += vn[k];
-      pg += vg[k];
-    }
-    carry_n += totn;
-    carry_g += totg;
-    __syncthreads();
-  }
-  if (t == 0) {
-    rn[nblocks] = carry_n;
-    rs[nblocks] = carry_g;
-    tot[blockIdx.x] = carry_n;
-    tot[S + blockIdx.x] = carry_g;
-  }
-}
-
-// P3 (one thread): slice bases (nb = nonzero offsets, sb = segment offsets), the segment sentinel,
-// the per-(phase, XCD) window ranges, and the long-segment counters.
-__global__ void plan_bases(const int32_t* __restrict__ tot, int32_t S, int32_t* __restrict__ nb,
-                           int32_t* __restrict__ sb, int32_t* __restrict__ seg_ptr, int32_t* __restrict__ xcd,
-                           uint32_t* __restrict__ long_cnt) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
-  nb[0] = 0;
-  sb[0] = 0;
-  for (int s = 0; s < S; ++s) {
-    nb[s + 1] = nb[s] + tot[s];
-    sb[s + 1] = sb[s] + tot[S + s];
-  }
-  seg_ptr[sb[S]] = nb[S];
-  // Phase p (one gather launch each) gives XCD j one window range: slice j + 8 p when S >= 8, so
-  // an XCD never has two slices live in its L2; with S < 8 a single phase, XCD j taking every
-  // (8 / S)-th window of slice j % S.
-  const int phases = S >= kXcds ? S / kXcds : 1;
-  for (int ph = 0; ph < phases; ++ph) {
-    for (int j = 0; j < kXcds; ++j) {
-      int32_t* xr = xcd + (ph * kXcds + j) * kXcdWords;
-      const int s = S >= kXcds ? j + kXcds * ph : j % S;
-      const int member = S >= kXcds ? 0 : j / S, members = S >= kXcds ? 1 : kXcds / S;
-      const int32_t w0 = (nb[s] + kWW - 1) / kWW, w1 = (nb[s + 1] + kWW - 1) / kWW;
-      const int32_t count = w1 - w0 > member ? (w1 - w0 - member + members - 1) / members : 0;
-      xr[0] = 1;
-      xr[1] = count;
-      xr[2] = w0 + member;
-      xr[3] = count;
-      xr[4] = members;
-    }
-  }
-  for (int j = 0; j < kXcds; ++j) long_cnt[j] = 0;
-}
-
-// P4: stable scatter of every row's nonzeros into the slice-major copy, plus per (row, slice)
-// segment its first nonzero (seg_ptr) and its row within the block (seg_row). The per-row counts
-// are recomputed exactly as plan_count computes them, so both passes agree.
-template <int SMAX>
-__global__ __launch_bounds__(kRB) void plan_scatter(const int32_t* __restrict__ rp, const int32_t* __restrict__ col,
-                                                    const float* __restrict__ val, int64_t rows, int32_t nnz, int32_t S,
-                                                    uint32_t width, uint32_t cols, const int32_t* __restrict__ tn,
-                                                    const int32_t* __restrict__ ts, int32_t ld,
-                                                    const int32_t* __restrict__ nb, const int32_t* __restrict__ sb,
-                                                    int32_t* __restrict__ col_s, float* __restrict__ val_s,
-                                                    int32_t* __restrict__ seg_ptr, uint8_t* __restrict__ seg_row,
-                                                    int32_t* __restrict__ long_list, uint32_t* __restrict__ long_cnt,
-                                                    int32_t long_cap, int32_t nblocks) {
-  __shared__ int32_t cnt[kRB][SMAX + 1];
-  __shared__ int32_t wn[kRB / 64][SMAX], wg[kRB / 64][SMAX];
-  const int32_t blk = xcd_block(nblocks);
-  if (blk < 0) return;  // whole workgroup
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  for (int s = 0; s < S; ++s) cnt[t][s] = 0;
-  __syncthreads();
-  const int64_t rw0 = (int64_t)blk * kRB + wave * 64;
-  const bool active = rw0 < rows;  // wave-uniform
-  WaveRows w{0, 0, 0};
-  if (active) {
-    w = wave_rows(rp, rw0, rows, nnz);
-    wave_count<SMAX>(col, w, cols, width, cnt + wave * 64);
-  }
-  __syncthreads();
-  for (int s = 0; s < S; ++s) {
-    const int32_t c = cnt[t][s];
-    const int32_t incl = wave_incl_scan(c);
-    const uint64_t bal = __ballot(c > 0);
-    if (lane == 63) wn[wave][s] = incl;
-    if (lane == 0) wg[wave][s] = __builtin_popcountll(bal);
-  }
-  __syncthreads();
-  for (int s = 0; s < S; ++s) {
-    const int32_t c = cnt[t][s];
-    const int32_t excl = wave_incl_scan(c) - c;
-    const uint64_t bal = __ballot(c > 0);
-    int32_t pn = 0, pg = 0;
-    for (int v = 0; v < wave; ++v) {
-      pn += wn[v][s];
-      pg += wg[v][s];
-    }
-    if (c > 0) {
-      const int64_t k = (int64_t)s * ld + blk;
-      const int32_t p = nb[s] + tn[k] + pn + excl;
-      const int32_t g = sb[s] + ts[k] + pg + (int32_t)lane_rank(bal);
-      seg_ptr[g] = p;
-      seg_row[g] = (uint8_t)t;
-      if (c > kLongSeg) {
-        // the XCD that gathers this slice; with S < 8 slices the XCDs sharing it take turns
-        const int j = S >= kXcds ? (s & (kXcds - 1)) : s + S * (int)((uint32_t)g % (uint32_t)(kXcds / S));
-        const uint32_t slot = atomicAdd(long_cnt + j, 1u);
-        if (slot < (uint32_t)long_cap) long_list[(int64_t)j * long_cap + slot] = g;
-      }
-      cnt[t][s] = p;  // becomes this row's write cursor in slice s
-    }
-  }
-  __syncthreads();
-  if (!active) return;
-  // Stream the wave's nonzeros again. Within a chunk, the lanes of one (row, slice) pair keep their
-  // index order: rank = lanes below this one with the same slice, from the row's first lane on.
-  int32_t (*cur)[SMAX + 1] = cnt + wave * 64;
-  for (int32_t base0 = w.nz0; base0 < w.nz1; base0 += 64 * kChunks) {
-    uint32_t cc[kChunks];
-    float vv[kChunks];
-    // Unconditional loads from a clamped index (base0 < nz1 here), so all of them go out together;
-    // lanes past nz1 are dropped below.
-#pragma unroll
-    for (int u = 0; u < kChunks; ++u) {
-      const int32_t i = min(base0 + 64 * u + lane, w.nz1 - 1);
-      cc[u] = (uint32_t)col[i];
-      vv[u] = val[i];
-    }
-#pragma unroll
-    for (int u = 0; u < kChunks; ++u) cc[u] = clamp_col((int32_t)cc[u], cols);
-#pragma unroll
-    for (int u = 0; u < kChunks; ++u) {
-      const int32_t base = base0 + 64 * u;
-      const int32_t i = base + lane;
-      const bool valid = i < w.nz1;
-      const int l = wave_row_of(w.start, i);
-      const int32_t s = valid ? (int32_t)(cc[u] / width) : S;
-      const int first = max(__shfl(w.start, l, 64) - base, 0);
-      uint64_t mine = 0;
-      for (int q = 0; q < S; ++q) {
-        const uint64_t m = __ballot(s == q);
-        if (s == q) mine = m;
-      }
-      const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-      const int32_t rank = __builtin_popcountll(mine & below & (~0ull << first));
-      if (valid) {
-        const int32_t pos = cur[l][s] + rank;
-        col_s[pos] = (int32_t)cc[u];
-        val_s[pos] = vv[u];
-      }
-      wave_lds_sync();
-      if (valid) atomicAdd(&cur[l][s], 1);
-      wave_lds_sync();
-    }
-  }
-}
-
-// P5: window k covers nonzeros [k·kWW, (k+1)·kWW) of the slice-major copy; it owns the segments
-// that start there, {g0, g1}, and loads the products [b, e) of those segments. A segment longer
-// than kLongSeg can only be the window's last one (it reaches past the window), and is excluded.
-__global__ __launch_bounds__(256) void plan_desc(const int32_t* __restrict__ seg_ptr, const int32_t* __restrict__ nb,
-                                                 const int32_t* __restrict__ sb, int32_t S, int64_t nwin,
-                                                 int4* __restrict__ desc) {
-  const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (k >= nwin) return;
-  const int32_t G = sb[S], Z = nb[S];
-  const int64_t lo = k * kWW, hi = min(lo + kWW, (int64_t)Z);
-  if (lo >= Z) {
-    desc[k] = make_int4(G, G, Z, Z);
-    return;
-  }
-  auto lower_bound = [&](int64_t target) {
-    int32_t a = 0, z = G;
-    while (a < z) {
-      const int32_t mid = (a + z) >> 1;
-      if ((int64_t)seg_ptr[mid] < target) a = mid + 1; else z = mid;
-    }
-    return a;
-  };
-  const int32_t g0 = lower_bound(lo), g1 = lower_bound(hi);
-  const int32_t b = seg_ptr[g0];
-  int32_t e = b;
-  if (g1 > g0) {
-    const int32_t lb = seg_ptr[g1 - 1], le = seg_ptr[g1];
-    e = (le - lb > kLongSeg) ? lb : le;
-  }
-  e = min(e, b + kSpan);  // a consistent plan never needs this; it keeps the LDS span in bounds
-  desc[k] = make_int4(g0, g1, b, e);
-}
-
 
 // Sequential sum of p[i0..i1) (index order), LDS reads four at a time.
 __device__ inline float lds_seq_sum(const float* __restrict__ p, int32_t i0, int32_t i1) {
@@ -610,45 +293,6 @@ __device__ inline float lds_seq_sum(const float* __restrict__ p, int32_t i0, int
   return sum;
 }
 
-// Buffer resources (dc::range_rsrc): loads past a range's end return 0 and stores past it are
-// dropped by the hardware range check, so a window's loads and stores need no branches.
-using dc::range_rsrc;
-constexpr int kNt = dc::kBufNt;
-constexpr uint32_t kDrop = 0x80000000u;  // a buffer offset past any range: the access is dropped
-constexpr int kChunksW = kSpan / 256;    // 16-byte loads per lane covering a window's span
-constexpr int kSegChunks = (kWW + 1 + 255) / 256;  // ... and its segment starts plus the end
-
-// A window's loads, 16 bytes per lane: lane l holds elements 256 k + 4 l .. + 3 of chunk k.
-struct WindowLoads {
-  dc::i32x4 sp[kSegChunks];  // seg_ptr[g0 + ...]
-  dc::i32x4 c[kChunksW];     // col_s[b + ...]
-  dc::f32x4 v[kChunksW];     // val_s[b + ...]
-};
-
-// Ranges are rounded up to whole 16-byte groups (the arrays carry 16 bytes of slack), so a load is
-// either wholly inside or wholly past the range; elements past e (or past g1) are ignored.
-__device__ inline void window_issue(const int4 d, const int32_t* __restrict__ seg_ptr,
-                                    const int32_t* __restrict__ col_s, const float* __restrict__ val_s,
-                                    WindowLoads& w) {
-  const uint32_t lane16 = (threadIdx.x & 63) * 16;
-  const auto rs = range_rsrc(seg_ptr + d.x, ((d.y - d.x + 1 + 3) & ~3) * 4);
-  const auto rc = range_rsrc(col_s + d.z, ((d.w - d.z + 3) & ~3) * 4);
-  const auto rv = range_rsrc(val_s + d.z, ((d.w - d.z + 3) & ~3) * 4);
-#pragma unroll
-  for (int k = 0; k < kSegChunks; ++k)
-    w.sp[k] = __builtin_bit_cast(dc::i32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, lane16 + 1024 * k, 0, kNt));
-#pragma unroll
-  for (int k = 0; k < kChunksW; ++k) {
-    w.c[k] = __builtin_bit_cast(dc::i32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, lane16 + 1024 * k, 0, kNt));
-    w.v[k] = __builtin_bit_cast(dc::f32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, lane16 + 1024 * k, 0, kNt));
-  }
-}
-
-__device__ inline int4 uniform_int4(int4 d) {
-  return make_int4(__builtin_amdgcn_readfirstlane(d.x), __builtin_amdgcn_readfirstlane(d.y),
-                   __builtin_amdgcn_readfirstlane(d.z), __builtin_amdgcn_readfirstlane(d.w));
-}
-
 // Float sum over the wave's 64 lanes in a fixed DPP tree order (result broadcast from lane 63).
 __device__ inline float wave_sum_f32(float v) {
   auto step = [](float a, uint32_t b) { return a + __builtin_bit_cast(float, b); };
@@ -661,280 +305,485 @@ __device__ inline float wave_sum_f32(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
-__device__ inline int32_t elem(const dc::i32x4& v, int j) { return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w; }
+// Exclusive prefix sum of a[0..n) in place (global or LDS) by one kPass-thread workgroup; returns
+// the total to every thread. Called by every thread of the workgroup.
+__device__ int32_t block_scan_inplace(int32_t* a, int32_t n, int32_t* wsum) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  int32_t carry = 0;
+  for (int32_t base = 0; base < n; base += 4 * kPass) {
+    int32_t v[4], sum = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int32_t i = base + 4 * t + k;
+      v[k] = i < n ? a[i] : 0;
+      sum += v[k];
+    }
+    const int32_t incl = wave_incl_scan(sum);
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int32_t pre = carry, tot = 0;
+#pragma unroll
+    for (int w = 0; w < kPassWaves; ++w) {
+      const int32_t x = wsum[w];
+      if (w < wave) pre += x;
+      tot += x;
+    }
+    pre += incl - sum;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int32_t i = base + 4 * t + k;
+      if (i < n) a[i] = pre;
+      pre += v[k];
+    }
+    carry += tot;
+    __syncthreads();
+  }
+  return carry;
+}
 
+__device__ inline int64_t block_of(int32_t start, int32_t nnz, int64_t r) {
+  return (int64_t)clamp_nz(start, nnz) / kBlockSpan + r / kBlockRows;
+}
 
-// Gather pass: persistent grid, XCD-affine; each wave walks its XCD's windows. Per window: one
-// round trip for the 16-byte column/value/segment-start loads, one for the gathers (only the
-// chunks that hold products), products to the wave's LDS (one 16-byte write per chunk), then the
-// segment sums. The address unit is the limit here, so the number of memory instructions per
-// window is what this layout minimises. Segment sums: up to kSeqSeg products, one lane adds them
-// in index order; longer segments (up to kLongSeg) are summed by the whole wave: lane k adds
-// products k, k + 64, ... in order, then a fixed DPP tree. Lane l owns segments 256 k + 4 l + j.
-__global__ __launch_bounds__(kGatherBlock) void spmv_slice_windows(const int4* __restrict__ desc,
-                                                                   const int32_t* __restrict__ seg_ptr,
-                                                                   const int32_t* __restrict__ col_s,
-                                                                   const float* __restrict__ val_s,
-                                                                   const float* __restrict__ x,
-                                                                   float* __restrict__ partial,
-                                                                   const int32_t* __restrict__ xcd, int32_t cols,
-                                                                   const double* __restrict__ sums_in, int32_t nsums,
-                                                                   double* __restrict__ sum_out) {
-  __shared__ dc::f32x4 prod[kGatherBlock / 64][kSpan / 4];
+// Rows [r0, r1) of block b; its nonzeros other than a giant row's are [j0, j1), the giant row's
+// (if any) [j1, jg). A consistent matrix has j1 - j0 < kStage; the clamp keeps a malformed one's
+// positions inside the stage (its results are then meaningless, but every access stays in range).
+// The plan keeps them per block (binfo: two int4 per block), so a pass reads them in one load.
+struct BlockRange {
+  int32_t r0, r1, j0, j1, jg;
+};
+__device__ inline BlockRange load_block(const int4* __restrict__ binfo, int32_t b) {
+  const int4 a = binfo[2 * b], c = binfo[2 * b + 1];
+  return BlockRange{a.x, a.y, a.z, a.w, c.x};
+}
+
+// A1: first row of each block (blk_row[nblocks] = rows).
+__global__ __launch_bounds__(256) void plan_blocks(const int32_t* __restrict__ rp, int64_t rows, int32_t nnz,
+                                                   int32_t nblocks, int32_t* __restrict__ blk_row) {
+  const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (k > nblocks) return;
+  int64_t a = 0, z = rows;  // first row whose block is >= k
+  while (a < z) {
+    const int64_t m = (a + z) >> 1;
+    if (block_of(rp[m], nnz, m) < k) a = m + 1; else z = m;
+  }
+  blk_row[k] = (int32_t)a;
+}
+
+// A1b: the bounds of each block (BlockRange) from blk_row and the row pointers.
+__global__ __launch_bounds__(256) void plan_block_info(const int32_t* __restrict__ rp, int32_t nnz,
+                                                       const int32_t* __restrict__ blk_row, int32_t nblocks,
+                                                       int4* __restrict__ binfo) {
+  const int32_t b = (int32_t)(blockIdx.x * 256 + threadIdx.x);
+  if (b >= nblocks) return;
+  BlockRange g;
+  g.r0 = blk_row[b];
+  g.r1 = max(blk_row[b + 1], g.r0);
+  g.j0 = g.r0 < g.r1 ? clamp_nz(rp[g.r0], nnz) : 0;
+  g.j1 = g.jg = g.j0;
+  if (g.r0 < g.r1) {
+    const int32_t last = max(clamp_nz(rp[g.r1 - 1], nnz), g.j0), end = max(clamp_nz(rp[g.r1], nnz), last);
+    const bool giant = end - last > kGiantRow;
+    g.j1 = min(giant ? last : end, g.j0 + kStage);
+    g.jg = giant ? end : g.j1;
+  }
+  binfo[2 * b] = make_int4(g.r0, g.r1, g.j0, g.j1);
+  binfo[2 * b + 1] = make_int4(g.jg, 0, 0, 0);
+}
+
+// A2: tcnt[s][b] = nonzeros of block b in slice s (s < S), and of its giant row (s = S). SMAX >= S + 1
+// sizes the LDS histogram.
+template <int SMAX>
+__global__ __launch_bounds__(kPass) void plan_tile_count(const int32_t* __restrict__ col,
+                                                         const int4* __restrict__ binfo, int32_t nblocks, int32_t S,
+                                                         uint32_t width, uint32_t cols, int32_t* __restrict__ tcnt) {
+  __shared__ int32_t hist[SMAX];
+  const int32_t b = xcd_block(nblocks);
+  if (b < 0) return;  // whole workgroup
+  const int t = threadIdx.x;
+  for (int s = t; s <= S; s += kPass) hist[s] = 0;
+  __syncthreads();
+  const BlockRange g = load_block(binfo, b);
+  for (int32_t j0 = g.j0 + t; j0 < g.j1; j0 += 4 * kPass) {
+    int32_t c[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) c[u] = j0 + u * kPass < g.j1 ? col[j0 + u * kPass] : 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (j0 + u * kPass < g.j1) atomicAdd(&hist[clamp_col(c[u], cols) / width], 1);
+  }
+  if (t == 0) hist[S] += g.jg - g.j1;
+  __syncthreads();
+  for (int s = t; s <= S; s += kPass) tcnt[(int64_t)s * nblocks + b] = hist[s];
+}
+
+// A3: workgroup s turns row s of tcnt into run offsets within the slice (exclusive prefix over
+// blocks); tot[s] = the slice's total.
+__global__ __launch_bounds__(kPass) void plan_tile_scan(int32_t* __restrict__ tcnt, int32_t nblocks,
+                                                        int32_t* __restrict__ tot) {
+  __shared__ int32_t wsum[kPassWaves];
+  const int32_t total = block_scan_inplace(tcnt + (int64_t)blockIdx.x * nblocks, nblocks, wsum);
+  if (threadIdx.x == 0) tot[blockIdx.x] = total;
+}
+
+// A4 (one workgroup): region starts sbase[0..S+1] (each slice region rounded up to whole groups of
+// kPad entries; the giant region S last), the padding entries (column 0, value 0), and the share of
+// each of the nwg product-pass workgroups: wrange[w] = {first entry, end, slice of the first entry}
+// (equal shares of whole kPad-entry groups of the slice regions [0, sbase[S])).
+__global__ __launch_bounds__(kPass) void plan_tile_bases(const int32_t* __restrict__ tot, int32_t S,
+                                                         int32_t* __restrict__ sbase, uint16_t* __restrict__ col16,
+                                                         uint16_t* __restrict__ dest16, float* __restrict__ val_s,
+                                                         int32_t nwg, int4* __restrict__ wrange) {
+  __shared__ int32_t wsum[kPassWaves];
+  for (int s = threadIdx.x; s <= S; s += kPass) sbase[s] = (tot[s] + kPad - 1) & ~(kPad - 1);
+  __syncthreads();
+  const int32_t total = block_scan_inplace(sbase, S + 1, wsum);
+  if (threadIdx.x == 0) sbase[S + 1] = total;
+  __syncthreads();
+  for (int s = threadIdx.x; s <= S; s += kPass)
+    for (int32_t i = sbase[s] + tot[s]; i < sbase[s + 1]; ++i) {
+      col16[i] = 0;
+      dest16[i] = 0;
+      val_s[i] = 0.0f;
+    }
+  const int32_t Z = sbase[S];
+  const int64_t per = ((int64_t)(Z + nwg - 1) / nwg + kPad - 1) & ~(int64_t)(kPad - 1);
+  for (int w = threadIdx.x; w < nwg; w += kPass) {
+    const int32_t lo = (int32_t)min((int64_t)w * per, (int64_t)Z);
+    const int32_t hi = (int32_t)min((int64_t)lo + per, (int64_t)Z);
+    int32_t a = 0, z = S - 1;  // last slice whose region starts at or before lo
+    while (a < z) {
+      const int32_t m = (a + z + 1) >> 1;
+      if (sbase[m] <= lo) a = m; else z = m - 1;
+    }
+    wrange[w] = make_int4(lo, hi, a, 0);
+  }
+}
+
+// A5: the scatter. Run (b, s) starts at toff[b][s] = sbase[s] + its offset within the slice
+// (toff[nblocks][s] = the slice's end). A giant row's entries go to region S in CSR order, column
+// low half in col16 and high half in dest16. With kStaged (S < kRowRuns), the block's entries are
+// first sorted by slice in LDS (the order within a slice is that of LDS atomics, which the results
+// do not depend on: every product is staged at its CSR position), then written run by run, the
+// lanes of a wave on consecutive positions (wave w takes runs w, w + 16, ...; their bounds sit in
+// its lanes' registers); otherwise each entry is written where its atomic cursor lands.
+template <int SMAX, bool kStaged>
+__global__ __launch_bounds__(kPass) void plan_tile_scatter(
+    const int32_t* __restrict__ col, const float* __restrict__ val, const int4* __restrict__ binfo,
+    int32_t nblocks, int32_t S, uint32_t width, uint32_t cols, const int32_t* __restrict__ tcnt,
+    const int32_t* __restrict__ tot, const int32_t* __restrict__ sbase, int32_t* __restrict__ toff,
+    uint16_t* __restrict__ col16, float* __restrict__ val_s, uint16_t* __restrict__ dest16) {
+  __shared__ int32_t cur[SMAX];
+  __shared__ int32_t gbase[kStaged ? SMAX : 1];
+  __shared__ int32_t lpre[kStaged ? SMAX : 1];
+  __shared__ uint32_t st_cd[kStaged ? kStage : 1];
+  __shared__ float st_v[kStaged ? kStage : 1];
+  __shared__ int32_t wsum[kPassWaves];
+  const int32_t b = xcd_block(nblocks);
+  if (b < 0) return;  // whole workgroup
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int32_t S1 = S + 1;
+  int32_t n = 0;  // kStaged: thread t's run length (t < S)
+  for (int s = t; s <= S; s += kPass) {
+    const int32_t o = sbase[s] + tcnt[(int64_t)s * nblocks + b];
+    const int32_t next = b + 1 < nblocks ? sbase[s] + tcnt[(int64_t)s * nblocks + b + 1] : sbase[s] + tot[s];
+    cur[s] = o;
+    toff[(int64_t)b * S1 + s] = o;
+    if (b == nblocks - 1) toff[(int64_t)nblocks * S1 + s] = next;
+    if (kStaged && s == t && s < S) n = next - o;
+  }
+  const BlockRange g = load_block(binfo, b);
+  int32_t E = 0;
+  if constexpr (kStaged) {
+    // local slice-major numbering: thread t (run t) takes its first local position from a scan
+    static_assert(SMAX <= kPass, "one thread per run");
+    const int32_t incl = wave_incl_scan(n);
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int32_t pre = incl - n;
+#pragma unroll
+    for (int w = 0; w < kPassWaves; ++w) {
+      const int32_t v = wsum[w];
+      if (w < wave) pre += v;
+      E += v;
+    }
+    E = min(E, kStage);
+    if (t < S) {
+      gbase[t] = cur[t] - pre;  // local position li of run t goes to gbase[t] + li
+      lpre[t] = pre;
+      cur[t] = pre;
+    }
+  }
+  __syncthreads();
+  for (int32_t j0 = g.j0 + t; j0 < g.j1; j0 += 4 * kPass) {
+    int32_t c[4];
+    float v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int32_t j = j0 + u * kPass;
+      c[u] = j < g.j1 ? col[j] : 0;
+      v[u] = j < g.j1 ? val[j] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int32_t j = j0 + u * kPass;
+      if (j < g.j1) {
+        const uint32_t cc = clamp_col(c[u], cols), s = cc / width;
+        const int32_t pos = atomicAdd(&cur[s], 1);
+        if constexpr (kStaged) {
+          if (pos < kStage) {
+            st_cd[pos] = (cc - s * width) | ((uint32_t)(j - g.j0) << 16);
+            st_v[pos] = v[u];
+          }
+        } else {
+          col16[pos] = (uint16_t)(cc - s * width);
+          val_s[pos] = v[u];
+          dest16[pos] = (uint16_t)(j - g.j0);
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if constexpr (kStaged) {
+    const int s = lane * kPassWaves + wave;  // this lane's run
+    int32_t lo = 0, hi = 0, gb = 0;
+    if (s < S) {
+      lo = lpre[s];
+      hi = min(cur[s], E);  // the cursor ends at the run's end
+      gb = gbase[s];
+    }
+    for (uint64_t m = __ballot(lo < hi); m; m &= m - 1) {  // wave-uniform
+      const int L = __builtin_ctzll(m);
+      const int32_t rlo = __builtin_amdgcn_readlane(lo, L), rhi = __builtin_amdgcn_readlane(hi, L);
+      const int32_t rgb = __builtin_amdgcn_readlane(gb, L);
+      for (int32_t li = rlo + lane; li < rhi; li += 64) {
+        const uint32_t cd = st_cd[li];
+        col16[rgb + li] = (uint16_t)(cd & 0xFFFFu);
+        dest16[rgb + li] = (uint16_t)(cd >> 16);
+        val_s[rgb + li] = st_v[li];
+      }
+    }
+  }
+  const int32_t gpos = cur[S];  // the giant row's run (no atomic moves cur[S])
+  for (int32_t j = g.j1 + t; j < g.jg; j += kPass) {
+    const uint32_t cc = clamp_col(col[j], cols);
+    col16[gpos + (j - g.j1)] = (uint16_t)(cc & 0xFFFFu);
+    dest16[gpos + (j - g.j1)] = (uint16_t)(cc >> 16);
+    val_s[gpos + (j - g.j1)] = val[j];
+  }
+}
+
+// Product pass: p[i] = val_s[i] * x_tile[col16[i]] over the slice regions [0, sbase[S]). Workgroup
+// w takes the share wrange[w] (equal shares of whole kPad-entry groups); at each slice its share
+// enters it loads that slice's x tile into LDS (16 waves, 8 loads in flight per lane). With sum_out, workgroup 0 first
+// adds sums_in[0..nsums) in a fixed order (the power iteration's previous L1 norm).
+__global__ __launch_bounds__(kPass) void spmv_tile_products(const uint16_t* __restrict__ col16,
+                                                            const float* __restrict__ val_s,
+                                                            const int32_t* __restrict__ sbase,
+                                                            const int4* __restrict__ wrange, uint32_t width,
+                                                            const float* __restrict__ x, uint32_t cols,
+                                                            float* __restrict__ p, const double* __restrict__ sums_in,
+                                                            int32_t nsums, double* __restrict__ sum_out) {
+  __shared__ float xt[kTileCols];
+  __shared__ double red[kPassWaves];
+  const int t = threadIdx.x;
   if (sum_out && blockIdx.x == 0) {
-    // The power iteration's previous L1 norm: workgroup 0 adds the previous SpMV's block sums in a
-    // fixed order (thread t takes t, t + 256, ...; eight loads in flight), then its windows.
-    __shared__ double red[kGatherBlock / 64];
     double a = 0.0;
-    for (int32_t i0 = threadIdx.x; i0 < nsums; i0 += 8 * kGatherBlock) {
+    for (int32_t i0 = t; i0 < nsums; i0 += 8 * kPass) {
       double v[8];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = i0 + k * kGatherBlock < nsums ? sums_in[i0 + k * kGatherBlock] : 0.0;
+      for (int k = 0; k < 8; ++k) v[k] = i0 + k * kPass < nsums ? sums_in[i0 + k * kPass] : 0.0;
 #pragma unroll
       for (int k = 0; k < 8; ++k) a += v[k];
     }
-    const double total = dc::block_sum64<kGatherBlock>(a, red);
-    if (threadIdx.x == 0) *sum_out = total;
+    const double total = dc::block_sum64<kPass>(a, red);
+    if (t == 0) *sum_out = total;
   }
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int j = blockIdx.x & (kXcds - 1);
-  const int32_t per_xcd_waves = (int32_t)(gridDim.x / kXcds) * (kGatherBlock / 64);
-  const int32_t v = (int32_t)(blockIdx.x / kXcds) * (kGatherBlock / 64) + wave;
-  const int32_t* xr = xcd + j * kXcdWords;
-  const int32_t nr = xr[0], total = xr[1];
-  if (v >= total) return;
-  dc::f32x4* wp4 = prod[wave];
-  const float* wp = reinterpret_cast<const float*>(prod[wave]);
-  const auto rx = range_rsrc(x, (int32_t)((uint32_t)cols * 4u));  // x < 4 GB (checked at plan creation)
-  auto window_desc = [&](int32_t l) {
-    if (l >= total) return make_int4(0, 0, 0, 0);
-    int32_t rem = l, k = 0;
-    for (int q = 0; q < nr; ++q) {
-      const int32_t cnt = xr[3 + 3 * q];
-      if (rem < cnt) {
-        k = xr[2 + 3 * q] + rem * xr[4 + 3 * q];
-        break;
-      }
-      rem -= cnt;
+  const int4 wr = wrange[blockIdx.x];
+  int32_t lo = wr.x, s = wr.z;
+  const int32_t hi = wr.y;
+  for (; lo < hi; ++s) {
+    const int32_t e = min(hi, sbase[s + 1]);
+    if (lo >= e) continue;  // workgroup-uniform
+    __syncthreads();        // the previous tile's readers are done
+    const uint32_t c0 = (uint32_t)s * width;
+    const int32_t tw = (int32_t)min(width, cols - c0);
+    const auto rx = dc::range_rsrc(x + c0, tw * 4);
+    for (int32_t cb = 0; cb < tw; cb += 8 * kPass) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        v[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, (uint32_t)(cb + u * kPass + t) * 4u, 0, 0));
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (cb + u * kPass + t < kTileCols) xt[cb + u * kPass + t] = v[u];
     }
-    return uniform_int4(desc[k]);
-  };
-  int4 d = window_desc(v);
-  for (int32_t l = v; l < total; l += per_xcd_waves) {
-    const int32_t g0 = d.x, g1 = d.y, b = d.z, e = d.w;
-    WindowLoads w;
-    window_issue(d, seg_ptr, col_s, val_s, w);
-    const int4 dn = window_desc(l + per_xcd_waves);
-    const int32_t span = e - b;
-    // gathers: only chunks that hold products (a wave-uniform skip); x[0] for elements past e
-    dc::f32x4 xv[kChunksW];
-#pragma unroll
-    for (int k = 0; k < kChunksW; ++k) {
-      xv[k] = dc::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      if (256 * k < span) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float g = __builtin_bit_cast(
-              float, __builtin_amdgcn_raw_buffer_load_b32(rx, (uint32_t)elem(w.c[k], q) * 4u, 0, 0));
-          if (q == 0) xv[k].x = g; else if (q == 1) xv[k].y = g; else if (q == 2) xv[k].z = g; else xv[k].w = g;
-        }
+    __syncthreads();
+    for (int32_t i = lo + kPad * t; i < e; i += 2 * kPad * kPass) {
+      const int32_t i2 = i + kPad * kPass;
+      const bool two = i2 < e;
+      const dc::i32x4 c1 = __builtin_nontemporal_load(reinterpret_cast<const dc::i32x4*>(col16 + i));
+      const dc::f32x4 a1 = __builtin_nontemporal_load(reinterpret_cast<const dc::f32x4*>(val_s + i));
+      const dc::f32x4 b1 = __builtin_nontemporal_load(reinterpret_cast<const dc::f32x4*>(val_s + i + 4));
+      dc::i32x4 c2 = {0, 0, 0, 0};
+      dc::f32x4 a2 = {0.0f, 0.0f, 0.0f, 0.0f}, b2 = a2;
+      if (two) {
+        c2 = __builtin_nontemporal_load(reinterpret_cast<const dc::i32x4*>(col16 + i2));
+        a2 = __builtin_nontemporal_load(reinterpret_cast<const dc::f32x4*>(val_s + i2));
+        b2 = __builtin_nontemporal_load(reinterpret_cast<const dc::f32x4*>(val_s + i2 + 4));
       }
-    }
-#pragma unroll
-    for (int k = 0; k < kChunksW; ++k)
-      if (256 * k + 4 * lane < span) wp4[64 * k + lane] = w.v[k] * xv[k];  // products past e are never read
-    wave_lds_sync();
-    // segment sums: lane l, chunk k, element q -> segment s = 256 k + 4 l + q
-    constexpr int kSumChunks = kWW / 256;  // a window owns at most kWW segments; the last chunk of
-    constexpr int kSegSlots = kSumChunks * 4;  // starts only supplies the final segment's end
-    float psum[kSegSlots];
-    uint32_t off[kSegSlots];
-    uint64_t wide[kSegSlots];
-    const int32_t nseg = g1 - g0;
-#pragma unroll
-    for (int k = 0; k < kSumChunks; ++k) {
-      const int32_t next_lane = __shfl(w.sp[k].x, (lane + 1) & 63, 64);  // lane l + 1's first start
-      const int32_t next_chunk = __shfl(w.sp[k + 1].x, 0, 64);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int si = 4 * k + q;
-        const int32_t sidx = 256 * k + 4 * lane + q;
-        const int32_t rb = elem(w.sp[k], q);
-        const int32_t re = q < 3 ? elem(w.sp[k], q + 1) : (lane < 63 ? next_lane : next_chunk);
-        const bool in = sidx < nseg;
-        const bool seq = in && re - rb <= kSeqSeg;
-        wide[si] = __ballot(in && re - rb > kSeqSeg && re - rb <= kLongSeg);
-        psum[si] = seq ? lds_seq_sum(wp, rb - b, min(re, e) - b) : 0.0f;
-        off[si] = seq ? (uint32_t)sidx * 4u : kDrop;
+      auto lo16 = [](int32_t w) { return (uint32_t)w & 0xFFFFu; };
+      auto hi16 = [](int32_t w) { return (uint32_t)w >> 16; };
+      const dc::f32x4 p1a = {a1.x * xt[lo16(c1.x)], a1.y * xt[hi16(c1.x)], a1.z * xt[lo16(c1.y)], a1.w * xt[hi16(c1.y)]};
+      const dc::f32x4 p1b = {b1.x * xt[lo16(c1.z)], b1.y * xt[hi16(c1.z)], b1.z * xt[lo16(c1.w)], b1.w * xt[hi16(c1.w)]};
+      *reinterpret_cast<dc::f32x4*>(p + i) = p1a;
+      *reinterpret_cast<dc::f32x4*>(p + i + 4) = p1b;
+      if (two) {
+        const dc::f32x4 p2a = {a2.x * xt[lo16(c2.x)], a2.y * xt[hi16(c2.x)], a2.z * xt[lo16(c2.y)], a2.w * xt[hi16(c2.y)]};
+        const dc::f32x4 p2b = {b2.x * xt[lo16(c2.z)], b2.y * xt[hi16(c2.z)], b2.z * xt[lo16(c2.w)], b2.w * xt[hi16(c2.w)]};
+        *reinterpret_cast<dc::f32x4*>(p + i2) = p2a;
+        *reinterpret_cast<dc::f32x4*>(p + i2 + 4) = p2b;
       }
     }
-#pragma unroll
-    for (int si = 0; si < kSegSlots; ++si) {
-      for (uint64_t m = wide[si]; m; m &= m - 1) {  // wave-uniform loop over this slot's wide segments
-        const int L = __builtin_ctzll(m);
-        const int k = si / 4, q = si % 4;
-        const int32_t rb = __shfl(elem(w.sp[k], q), L, 64);
-        int32_t re;
-        if (q < 3) re = __shfl(elem(w.sp[k], q + 1), L, 64);
-        else if (L < 63) re = __shfl(w.sp[k].x, L + 1, 64);
-        else re = __shfl(w.sp[k + 1].x, 0, 64);
-        float t = 0.0f;
-        for (int32_t i = rb - b + lane; i < min(re, e) - b; i += 64) t += wp[i];
-        const float tw = wave_sum_f32(t);
-        if (lane == L) {
-          psum[si] = tw;
-          off[si] = (uint32_t)(256 * k + 4 * L + q) * 4u;
-        }
-      }
-    }
-    const auto rp = range_rsrc(partial + g0, nseg * 4);
-#pragma unroll
-    for (int k = 0; k < kSumChunks; ++k) {
-      if (256 * k < nseg) {  // wave-uniform: groups holding no segment issue no store
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int32_t, psum[4 * k + q]), rp, off[4 * k + q], 0, kNt);
-      }
-    }
-    wave_lds_sync();
-    d = dn;
+    lo = e;
   }
 }
 
-// Long segments (more than kLongSeg nonzeros in one slice): one wavefront per segment, on the XCD
-// that owns its slice. A segment's cost is a chain of dependent round trips (its bounds, its
-// columns and values, its gathers), so the pass is latency-bound: a wavefront per segment keeps as
-// many segments in flight as the device holds waves, and kLongBatch loads per lane cover segments
-// of up to kLongBatch * 64 nonzeros in one round trip each. Lane k adds products k, k + 64, ... in
-// order, then a fixed DPP tree: deterministic.
-constexpr int kLongWave = 64;
-constexpr int kLongBatch = 32;
-__global__ __launch_bounds__(kLongWave) void spmv_slice_long(const int32_t* __restrict__ seg_ptr,
-                                                             const int32_t* __restrict__ col_s,
-                                                             const float* __restrict__ val_s,
-                                                             const float* __restrict__ x, float* __restrict__ partial,
-                                                             const int32_t* __restrict__ long_list,
-                                                             const uint32_t* __restrict__ long_cnt, int32_t long_cap) {
-  const int j = blockIdx.x & (kXcds - 1);
-  const int lane = threadIdx.x;
-  const uint32_t n_long = min(long_cnt[j], (uint32_t)long_cap);
-  for (uint32_t t = blockIdx.x / kXcds; t < n_long; t += gridDim.x / kXcds) {
-    const int32_t g = long_list[(int64_t)j * long_cap + t];
-    const int32_t b = seg_ptr[g], e = seg_ptr[g + 1];
-    float sum = 0.0f;
-    for (int32_t i0 = b + lane; i0 < e; i0 += kLongBatch * kLongWave) {
-      int32_t c[kLongBatch];
-      float v[kLongBatch], xv[kLongBatch];
+// Row pass, a workgroup per block (XCD-contiguous; 64 KB of LDS, two workgroups per CU). With
+// kTable (S <= kRowRuns) the staging is one round trip: the block's run lengths go to LDS, a prefix
+// over them numbers its products in slice-major order, every product's run is written to a table
+// (held in the stage buffer until the products arrive), and thread t loads products t, t + kPass,
+// ... before writing any of them to their CSR positions. Without it (more slices), a wave stages
+// whole runs. The bounds of the first kRowPre row steps are loaded before the staging. Then the
+// rows, a lane per row, 64 consecutive rows per wave step. With `scale`, y = (float)((double)row
+// sum / *scale) (the power iteration's previous normalisation moved onto this product); with
+// block_sums, the block's float64 sum of y in a fixed order.
+template <bool kTable>
+__global__ __launch_bounds__(kPass) void spmv_tile_rows(
+    const int32_t* __restrict__ rp, int32_t nnz, const int4* __restrict__ binfo, int32_t nblocks,
+    const int32_t* __restrict__ toff, int32_t S, const float* __restrict__ p, const uint16_t* __restrict__ dest16,
+    const uint16_t* __restrict__ col16, const float* __restrict__ val_s, const float* __restrict__ x, uint32_t cols,
+    float* __restrict__ y, double* __restrict__ block_sums, const double* __restrict__ scale) {
+  __shared__ float stage[kStage];
+  __shared__ int32_t run_base[kTable ? kRowRuns : 1];
+  __shared__ int32_t wsum[kPassWaves];
+  __shared__ double red[kPassWaves];
+  const int32_t b = xcd_block(nblocks);
+  if (b < 0) return;  // whole workgroup
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int32_t S1 = S + 1;
+  const int32_t* t0 = toff + (int64_t)b * S1;
+  const int32_t* t1 = t0 + S1;
+  const BlockRange g = load_block(binfo, b);
+  int32_t pb[kRowPre], pe[kRowPre];  // bounds of the rows of the first kRowPre row steps
 #pragma unroll
-      for (int k = 0; k < kLongBatch; ++k) {
-        const int32_t i = i0 + k * kLongWave;
-        c[k] = 0;
-        v[k] = 0.0f;
-        if (i < e) {
-          c[k] = __builtin_nontemporal_load(col_s + i);
-          v[k] = __builtin_nontemporal_load(val_s + i);
-        }
-      }
-#pragma unroll
-      for (int k = 0; k < kLongBatch; ++k) xv[k] = x[c[k]];  // c = 0 past e: gathered, then dropped below
-#pragma unroll
-      for (int k = 0; k < kLongBatch; ++k) sum += (i0 + k * kLongWave < e) ? v[k] * xv[k] : 0.0f;
-    }
-    const float total = wave_sum_f32(sum);
-    if (lane == 0) partial[g] = total;
+  for (int k = 0; k < kRowPre; ++k) {
+    const int32_t r = g.r0 + wave * 64 + lane + k * kPass;
+    pb[k] = r < g.r1 ? rp[r] : 0;
+    pe[k] = r < g.r1 ? rp[r + 1] : 0;
   }
-}
-
-// Combine pass, a workgroup per block of kRB rows: the block's segments of each slice are one
-// contiguous run of the slice-major arrays; every thread takes runs' entries (kCombineBatch
-// loads in flight) and drops each partial into tab[row][slice]; then thread r adds its row in
-// slice order: y = 0.0f + tab[r][0] + tab[r][1] + ... (absent slices hold +0.0f, which leaves a
-// sum that starts at +0.0f unchanged). With kSums, also the block's float64 sum of y (fixed
-// order) for the power iteration. SMAX >= S sizes the LDS table.
-constexpr int kCombineBatch = 4;
-// With `scale` (the power iteration), y = (float)((double)row sum / *scale): the previous step's
-// normalisation x = y / s applied to this step's product instead (A·(u / s) = (A·u) / s).
-template <bool kSums, int SMAX>
-__global__ __launch_bounds__(kRB) void spmv_slice_combine(const int32_t* __restrict__ ts, int32_t ld, int32_t S,
-                                                          const int32_t* __restrict__ sb,
-                                                          const uint8_t* __restrict__ seg_row,
-                                                          const float* __restrict__ partial, float* __restrict__ y,
-                                                          int64_t rows, double* __restrict__ block_sums,
-                                                          const double* __restrict__ scale) {
-  __shared__ float tab[kRB][SMAX + 1];
-  __shared__ int32_t run_pre[SMAX + 1], run_base[SMAX];
-  __shared__ double red[kRB / 64];
-  const int t = threadIdx.x;
-#pragma unroll
-  for (int s = 0; s < SMAX; ++s) tab[t][s] = 0.0f;
-  if (t < 64) {  // wave 0: run lengths and their prefix over slices
-    int32_t n = 0;
+  if constexpr (kTable) {
+    // thread t holds run t (S <= kRowRuns == kPass): its length, and its first product's number from
+    // a workgroup scan kept in registers; then it writes its products' entries of the run table
+    static_assert(kRowRuns == kPass, "one thread per run");
+    int32_t o = 0, n = 0;
     if (t < S) {
-      const int64_t k = (int64_t)t * ld + blockIdx.x;
-      const int32_t a = ts[k];
-      n = ts[k + 1] - a;
-      run_base[t] = sb[t] + a;
+      o = t0[t];
+      n = t1[t] - o;
     }
     const int32_t incl = wave_incl_scan(n);
-    if (t < S) run_pre[t] = incl - n;
-    if (t == S - 1) run_pre[S] = incl;
-  }
-  __syncthreads();
-  const int32_t total = run_pre[S];
-  for (int32_t q0 = t; q0 < total; q0 += kCombineBatch * kRB) {
-    int ss[kCombineBatch];
-    uint32_t rr[kCombineBatch];
-    float pv[kCombineBatch];
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int32_t pre = incl - n, E = 0;
 #pragma unroll
-    for (int u = 0; u < kCombineBatch; ++u) {
-      const int32_t q = q0 + u * kRB;
-      int s = 0;  // last slice whose run starts at or before q
+    for (int w = 0; w < kPassWaves; ++w) {
+      const int32_t v = wsum[w];
+      if (w < wave) pre += v;
+      E += v;
+    }
+    E = min(E, kStage);
+    if (t < S) run_base[t] = o - pre;  // product li of run t is at run_base[t] + li
+    int16_t* run_of = reinterpret_cast<int16_t*>(stage);  // kStage int16 fit in half the stage
+    for (int32_t li = pre; li < min(pre + n, E); ++li) run_of[li] = (int16_t)t;
+    __syncthreads();
+    constexpr int kIt = kStage / kPass;
+    const int32_t nit = (E + kPass - 1) / kPass;
+    float pv[kIt];
+    uint32_t dv[kIt];
 #pragma unroll
-      for (int step = SMAX / 2; step > 0; step >>= 1)
-        if (s + step < S && run_pre[s + step] <= q) s += step;
-      ss[u] = s;
-      rr[u] = 0;
-      pv[u] = 0.0f;
-      if (q < total) {
-        const int32_t g = run_base[s] + (q - run_pre[s]);
-        rr[u] = seg_row[g];
-        pv[u] = __builtin_nontemporal_load(partial + g);
+    for (int k = 0; k < kIt; ++k) {
+      pv[k] = 0.0f;
+      dv[k] = kStage;
+      const int32_t li = t + k * kPass;
+      if (k < nit && li < E) {
+        const int32_t at = run_base[run_of[li]] + li;
+        pv[k] = p[at];
+        dv[k] = dest16[at];
       }
     }
+    __syncthreads();  // every run_of read is done before the stage is overwritten
 #pragma unroll
-    for (int u = 0; u < kCombineBatch; ++u)
-      if (q0 + u * kRB < total) tab[rr[u]][ss[u]] = pv[u];
+    for (int k = 0; k < kIt; ++k)
+      if (k < nit && dv[k] < (uint32_t)kStage) stage[dv[k]] = pv[k];
+  } else {
+    for (int s = wave; s < S; s += kPassWaves) {
+      const int32_t o = t0[s], n = t1[s] - o;
+      for (int32_t k = lane; k < n; k += 64) {
+        const uint32_t d = dest16[o + k];
+        if (d < (uint32_t)kStage) stage[d] = p[o + k];
+      }
+    }
   }
   __syncthreads();
-  float acc = 0.0f;
-#pragma unroll
-  for (int s = 0; s < SMAX; ++s)
-    if (s < S) acc += tab[t][s];
-  if (scale) acc = (float)((double)acc / *scale);
-  const int64_t r = (int64_t)blockIdx.x * kRB + t;
-  if (r < rows) y[r] = acc;
-  if constexpr (kSums) {
-    const double tsum = dc::block_sum64<kRB>(r < rows ? (double)acc : 0.0, red);
-    if (t == 0) block_sums[blockIdx.x] = tsum;
+  const int32_t gpos = t0[S];  // the giant row's entries (region S, CSR order)
+  double dsum = 0.0;
+  int it = 0;
+  for (int32_t rr = g.r0 + wave * 64; rr < g.r1; rr += kPass, ++it) {  // wave-uniform
+    const int32_t r = rr + lane;
+    const bool in = r < g.r1;
+    int32_t rb = 0, re = 0;
+    if (in) {
+      static_assert(kRowPre == 2, "the prefetched bounds are picked by two selects");
+      const int32_t lb = it == 0 ? pb[0] : it == 1 ? pb[1] : rp[r];
+      const int32_t le = it == 0 ? pe[0] : it == 1 ? pe[1] : rp[r + 1];
+      rb = min(max(clamp_nz(lb, nnz), g.j0), g.jg);
+      re = min(max(clamp_nz(le, nnz), rb), g.jg);
+    }
+    const int32_t d = re - rb;
+    float acc = 0.0f;
+    if (in && d <= kSeqRow) acc = lds_seq_sum(stage, rb - g.j0, min(re, g.j1) - g.j0);
+    for (uint64_t m = __ballot(in && d > kSeqRow && re <= g.j1); m; m &= m - 1) {
+      const int L = __builtin_ctzll(m);
+      const int32_t lb = __builtin_amdgcn_readlane(rb, L) - g.j0, le = __builtin_amdgcn_readlane(re, L) - g.j0;
+      float tt = 0.0f;
+      for (int32_t i = lb + lane; i < le; i += 64) tt += stage[i];
+      const float tw = wave_sum_f32(tt);
+      if (lane == L) acc = tw;
+    }
+    for (uint64_t m = __ballot(in && d > kSeqRow && re > g.j1); m; m &= m - 1) {  // the giant row
+      const int L = __builtin_ctzll(m);
+      const int32_t gb = max(__builtin_amdgcn_readlane(rb, L) - g.j1, 0);
+      const int32_t ge = __builtin_amdgcn_readlane(re, L) - g.j1;
+      float tt = 0.0f;
+      for (int32_t i = gb + lane; i < ge; i += 64) {
+        const uint32_t c = (uint32_t)col16[gpos + i] | ((uint32_t)dest16[gpos + i] << 16);
+        tt += __fmul_rn(val_s[gpos + i], x[min(c, cols - 1)]);
+      }
+      const float tw = wave_sum_f32(tt);
+      if (lane == L) acc = tw;
+    }
+    if (scale) acc = (float)((double)acc / *scale);
+    if (in) {
+      y[r] = acc;
+      dsum += (double)acc;
+    }
   }
-}
-
-template <bool kSums>
-int32_t launch_combine(dc_hip_ctx* ctx, unsigned grid, const int32_t* ts, int32_t ld, int32_t S, const int32_t* sb,
-                       const uint8_t* seg_row, const float* partial, float* y, int64_t rows, double* block_sums,
-                       const double* scale) {
-#define DC_COMBINE(SM)                                                                                          \
-  spmv_slice_combine<kSums, SM><<<grid, kRB, 0, ctx->stream>>>(ts, ld, S, sb, seg_row, partial, y, rows, block_sums, \
-                                                               scale)
-  if (S <= 1) DC_COMBINE(1);
-  else if (S <= 2) DC_COMBINE(2);
-  else if (S <= 4) DC_COMBINE(4);
-  else if (S <= 8) DC_COMBINE(8);
-  else if (S <= 16) DC_COMBINE(16);
-  else DC_COMBINE(32);
-#undef DC_COMBINE
-  return dc::last_launch_status();
+  if (block_sums) {
+    const double tsum = dc::block_sum64<kPass>(dsum, red);
+    if (t == 0) block_sums[b] = tsum;
+  }
 }
 
 }  // namespace
@@ -944,19 +793,17 @@ struct dc_hip_spmv_plan {
   int device = 0;
   int64_t rows = 0, cols = 0, nnz = 0;
   int32_t slices = 1;
-  int64_t slice_cols = 0;
-  int32_t nblocks = 0;
-  int64_t nwin = 0;
-  int32_t long_cap = 1;
+  int64_t slice_cols = 1;
+  int32_t nblocks = 1;
+  int64_t zcap = 0;
   bool owns_mem = false;
   void* mem = nullptr;
   size_t bytes = 0;
-  int32_t *col_s = nullptr, *seg_ptr = nullptr, *tn = nullptr, *ts = nullptr, *tot = nullptr, *nb = nullptr,
-          *sb = nullptr, *xcd = nullptr, *long_list = nullptr;
-  uint8_t* seg_row = nullptr;
-  uint32_t* long_cnt = nullptr;
-  float *val_s = nullptr, *partial = nullptr;
-  int4* desc = nullptr;
+  uint16_t *col16 = nullptr, *dest16 = nullptr;
+  float *val_s = nullptr, *p = nullptr;
+  int32_t *rp = nullptr, *tcnt = nullptr, *toff = nullptr, *tot = nullptr, *sbase = nullptr, *blk_row = nullptr;
+  int4 *binfo = nullptr, *wrange = nullptr;
+  int32_t nwg = 1;  // product-pass workgroups (one per CU)
   double *block_sums = nullptr, *scalars = nullptr;
 };
 
@@ -971,147 +818,108 @@ void plan_layout(dc_hip_spmv_plan* p, void* mem) {
     off += (bytes + 255) & ~(size_t)255;
     return q;
   };
-  const size_t nz = (size_t)std::max<int64_t>(p->nnz, 1);
-  const size_t tab = (size_t)p->slices * (p->nblocks + 1) * 4;
-  // col_s, val_s and seg_ptr are read with 16-byte loads over ranges rounded up to whole groups:
-  // 16 bytes of slack after each keeps those loads inside the allocation
-  p->col_s = reinterpret_cast<int32_t*>(take(nz * 4 + 16));
-  p->val_s = reinterpret_cast<float*>(take(nz * 4 + 16));
-  p->seg_ptr = reinterpret_cast<int32_t*>(take((nz + 1) * 4 + 16));
-  p->partial = reinterpret_cast<float*>(take(nz * 4));
-  p->seg_row = reinterpret_cast<uint8_t*>(take(nz));
-  p->tn = reinterpret_cast<int32_t*>(take(tab));
-  p->ts = reinterpret_cast<int32_t*>(take(tab));
-  p->tot = reinterpret_cast<int32_t*>(take(2 * kMaxSlices * 4));
-  p->nb = reinterpret_cast<int32_t*>(take((kMaxSlices + 1) * 4));
-  p->sb = reinterpret_cast<int32_t*>(take((kMaxSlices + 1) * 4));
-  p->xcd = reinterpret_cast<int32_t*>(take(kMaxPhases * kXcds * kXcdWords * 4));
-  p->desc = reinterpret_cast<int4*>(take((size_t)std::max<int64_t>(p->nwin, 1) * 16));
-  p->long_cnt = reinterpret_cast<uint32_t*>(take(kXcds * 4));
-  p->long_list = reinterpret_cast<int32_t*>(take((size_t)kXcds * p->long_cap * 4));
-  p->block_sums = reinterpret_cast<double*>(take((size_t)p->nblocks * 8));
+  const size_t z = (size_t)p->zcap, S1 = (size_t)p->slices + 1, nb = (size_t)p->nblocks;
+  p->col16 = reinterpret_cast<uint16_t*>(take(z * 2));
+  p->dest16 = reinterpret_cast<uint16_t*>(take(z * 2));
+  p->val_s = reinterpret_cast<float*>(take(z * 4));
+  p->p = reinterpret_cast<float*>(take(z * 4));
+  p->rp = reinterpret_cast<int32_t*>(take((size_t)(p->rows + 1) * 4));
+  p->tcnt = reinterpret_cast<int32_t*>(take(S1 * nb * 4));
+  p->toff = reinterpret_cast<int32_t*>(take(S1 * (nb + 1) * 4));
+  p->tot = reinterpret_cast<int32_t*>(take(S1 * 4));
+  p->sbase = reinterpret_cast<int32_t*>(take((S1 + 1) * 4));
+  p->blk_row = reinterpret_cast<int32_t*>(take((nb + 1) * 4));
+  p->binfo = reinterpret_cast<int4*>(take(nb * 32));
+  p->wrange = reinterpret_cast<int4*>(take((size_t)p->nwg * 16));
+  p->block_sums = reinterpret_cast<double*>(take(nb * 8));
   p->scalars = reinterpret_cast<double*>(take(8 * 8));
   p->mem = mem;
   p->bytes = off;
 }
 
-// Shape of the plan (slices, sizes) and the bytes it needs.
-void plan_shape(dc_hip_spmv_plan* p, int64_t rows, int64_t cols, int64_t nnz, int64_t slice_cols_max) {
+// Shape of the plan (slices, blocks, sizes) and the bytes it needs.
+int32_t plan_shape(dc_hip_spmv_plan* p, int64_t rows, int64_t cols, int64_t nnz, int64_t slice_cols_max,
+                   int cu_count) {
   p->rows = rows;
+  p->nwg = std::max(1, cu_count);
   p->cols = cols;
   p->nnz = nnz;
-  const int64_t wmax = slice_cols_max > 0 ? slice_cols_max : kSliceCols;
-  int64_t S = 1;
-  if (cols > wmax) {
-    if (cols <= 2 * wmax) S = 2;
-    else if (cols <= 4 * wmax) S = 4;
-    else S = std::min<int64_t>(kMaxSlices, kXcds * ((cols + kXcds * wmax - 1) / (kXcds * wmax)));
-  } else if (slice_cols_max == 0) {
-    // x fits one slice, but every XCD gathering from all of it (with the nonzeros streaming
-    // through the same L2) misses far more than an XCD holding a share of at most 512 KB: with
-    // S < 8 slices, XCD j takes slice j % S. Measured at 1M rows: S = 1 58.8 us per SpMV, S = 2
-    // 51.5, S = 4 48.5, S = 8 48.3, S = 16 56.7 (more segments than the cache saves).
-    const int64_t xbytes = cols * 4;
-    S = xbytes <= (int64_t{512} << 10) ? 1 : xbytes <= (int64_t{1} << 20) ? 2 : xbytes <= (int64_t{2} << 20) ? 4 : 8;
-  }
+  int64_t W = slice_cols_max > 0 ? std::min<int64_t>(slice_cols_max, kTileCols) : kTileCols;
+  if ((cols + W - 1) / W > kMaxSlices) W = (cols + kMaxSlices - 1) / kMaxSlices;
+  const int64_t S = std::max<int64_t>(1, (cols + W - 1) / W);
   p->slices = (int32_t)S;
-  p->slice_cols = std::max<int64_t>(1, (cols + S - 1) / S);
-  p->nblocks = (int32_t)std::max<int64_t>(1, (rows + kRB - 1) / kRB);
-  p->nwin = (nnz + kWW - 1) / kWW;
-  p->long_cap = (int32_t)(nnz / (kLongSeg + 1) + 1);
+  p->slice_cols = W;
+  p->nblocks = (int32_t)(nnz / kBlockSpan + (rows > 0 ? (rows - 1) / kBlockRows : 0) + 1);
+  p->zcap = nnz + (S + 1) * kPad + kPad;
+  // positions are int32 and the (slice, block) tables are indexed with int32 products of their sides
+  if (p->zcap > INT32_MAX || (S + 1) * (int64_t)(p->nblocks + 1) > (int64_t{1} << 29)) return DC_ERR_UNSUPPORTED;
   plan_layout(p, nullptr);
+  return DC_OK;
 }
 
 // The analysis kernels, on the context stream.
 int32_t plan_build(dc_hip_ctx* ctx, dc_hip_spmv_plan* p, const int32_t* rp, const int32_t* col, const float* val) {
-  const int32_t S = p->slices, ld = p->nblocks + 1;
-  const uint32_t width = (uint32_t)p->slice_cols, cols = (uint32_t)std::max<int64_t>(p->cols, 1);
-  const int32_t nnz = (int32_t)p->nnz;
   if (p->rows == 0) return DC_OK;
-  const unsigned agrid = (unsigned)(kXcds * ((p->nblocks + kXcds - 1) / kXcds));
-#define DC_PLAN_COUNT(SM)                                                                                      \
-  plan_count<SM><<<agrid, kRB, 0, ctx->stream>>>(rp, col, p->rows, nnz, S, width, cols, p->tn, p->ts, ld, \
-                                                 p->nblocks)
-  if (S <= 1) DC_PLAN_COUNT(1);
-  else if (S <= 2) DC_PLAN_COUNT(2);
-  else if (S <= 4) DC_PLAN_COUNT(4);
-  else if (S <= 8) DC_PLAN_COUNT(8);
-  else if (S <= 16) DC_PLAN_COUNT(16);
-  else DC_PLAN_COUNT(32);
-#undef DC_PLAN_COUNT
+  const int32_t S = p->slices, nb = p->nblocks, nnz = (int32_t)p->nnz;
+  const uint32_t width = (uint32_t)p->slice_cols, cols = (uint32_t)std::max<int64_t>(p->cols, 1);
+  DC_RETURN_IF_HIP(hipMemcpyAsync(p->rp, rp, (size_t)(p->rows + 1) * 4, hipMemcpyDeviceToDevice, ctx->stream));
+  plan_blocks<<<(unsigned)((nb + 1 + 255) / 256), 256, 0, ctx->stream>>>(p->rp, p->rows, nnz, nb, p->blk_row);
   DC_RETURN_IF(dc::last_launch_status());
-  plan_scan<<<(unsigned)S, kScanBlock, 0, ctx->stream>>>(p->tn, p->ts, p->nblocks, ld, S, p->tot);
+  plan_block_info<<<(unsigned)((nb + 255) / 256), 256, 0, ctx->stream>>>(p->rp, nnz, p->blk_row, nb, p->binfo);
   DC_RETURN_IF(dc::last_launch_status());
-  plan_bases<<<1, 64, 0, ctx->stream>>>(p->tot, S, p->nb, p->sb, p->seg_ptr, p->xcd, p->long_cnt);
+  const unsigned bgrid = (unsigned)(kXcds * ((nb + kXcds - 1) / kXcds));
+#define DC_TILE_COUNT(SM)                                                                                   \
+  plan_tile_count<SM><<<bgrid, kPass, 0, ctx->stream>>>(col, p->binfo, nb, S, width, cols, p->tcnt)
+  if (S + 1 <= 1024) DC_TILE_COUNT(1024);
+  else if (S + 1 <= 8192) DC_TILE_COUNT(8192);
+  else DC_TILE_COUNT(kMaxSlices + 8);
+#undef DC_TILE_COUNT
   DC_RETURN_IF(dc::last_launch_status());
-#define DC_PLAN_SCATTER(SM)                                                                                 \
-  plan_scatter<SM><<<agrid, kRB, 0, ctx->stream>>>(rp, col, val, p->rows, nnz, S, width, cols, p->tn, p->ts, ld, \
-                                                   p->nb, p->sb, p->col_s, p->val_s, p->seg_ptr, p->seg_row,      \
-                                                   p->long_list, p->long_cnt, p->long_cap, p->nblocks)
-  if (S <= 1) DC_PLAN_SCATTER(1);
-  else if (S <= 2) DC_PLAN_SCATTER(2);
-  else if (S <= 4) DC_PLAN_SCATTER(4);
-  else if (S <= 8) DC_PLAN_SCATTER(8);
-  else if (S <= 16) DC_PLAN_SCATTER(16);
-  else DC_PLAN_SCATTER(32);
-#undef DC_PLAN_SCATTER
+  plan_tile_scan<<<(unsigned)(S + 1), kPass, 0, ctx->stream>>>(p->tcnt, nb, p->tot);
   DC_RETURN_IF(dc::last_launch_status());
-  if (p->nwin > 0) {
-    plan_desc<<<(unsigned)((p->nwin + 255) / 256), 256, 0, ctx->stream>>>(p->seg_ptr, p->nb, p->sb, S, p->nwin,
-                                                                           p->desc);
-    DC_RETURN_IF(dc::last_launch_status());
-  }
-  return DC_OK;
+  plan_tile_bases<<<1, kPass, 0, ctx->stream>>>(p->tot, S, p->sbase, p->col16, p->dest16, p->val_s, p->nwg,
+                                                p->wrange);
+  DC_RETURN_IF(dc::last_launch_status());
+#define DC_TILE_SCATTER(SM, ST)                                                                         \
+  plan_tile_scatter<SM, ST><<<bgrid, kPass, 0, ctx->stream>>>(col, val, p->binfo, nb, S, width, cols, p->tcnt,  \
+                                                              p->tot, p->sbase, p->toff, p->col16, p->val_s,  \
+                                                              p->dest16)
+  if (S < kRowRuns) DC_TILE_SCATTER(kRowRuns, true);
+  else if (S + 1 <= 8192) DC_TILE_SCATTER(8192, false);
+  else DC_TILE_SCATTER(kMaxSlices + 8, false);
+#undef DC_TILE_SCATTER
+  return dc::last_launch_status();
 }
 
 // One SpMV through the plan: y = A·x (with `sums`, also the per-block float64 sums of y). With
-// `scale`, y = (A·x) / *scale (the power iteration's normalisation of x, applied to the product).
-// With `prev_sum_out`, *prev_sum_out = the sum of the block sums as they stand (the previous
-// SpMV's), computed before this SpMV's combine replaces them: by the first gather launch, so it
-// costs no launch of its own.
+// `scale`, y = (A·x) / *scale. With `prev_sum_out`, *prev_sum_out = the sum of the block sums as
+// they stand (the previous SpMV's), formed by the product pass before this SpMV's row pass
+// replaces them, so it costs no launch of its own.
 int32_t plan_spmv(dc_hip_ctx* ctx, const dc_hip_spmv_plan* p, const float* x, float* y, bool sums = false,
                   const double* scale = nullptr, double* prev_sum_out = nullptr) {
   if (p->rows == 0) return DC_OK;
-  const int ld = p->nblocks + 1;
-  if (p->nwin > 0) {
-    const int per_xcd_cus = std::max(1, ctx->cu_count / kXcds);
-    const int phases = p->slices >= kXcds ? p->slices / kXcds : 1;
-    // resident gather workgroups per CU (registers and LDS decide it), asked once per process
-    static const int per_cu = [] {
-      int n = 0;
-      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, spmv_slice_windows, kGatherBlock, 0) != hipSuccess || n < 1)
-        n = 4;
-      return n;
-    }();
-    const int64_t want = (p->nwin / phases / kXcds + 3) / 4 + 1;  // workgroups per XCD, one window per wave
-    const int64_t per_xcd = std::min<int64_t>(want, (int64_t)per_xcd_cus * per_cu);
-    for (int ph = 0; ph < phases; ++ph) {
-      spmv_slice_windows<<<(unsigned)(per_xcd * kXcds), kGatherBlock, 0, ctx->stream>>>(
-          p->desc, p->seg_ptr, p->col_s, p->val_s, x, p->partial, p->xcd + ph * kXcds * kXcdWords,
-          (int32_t)p->cols, p->block_sums, p->nblocks, ph == 0 ? prev_sum_out : nullptr);
-      DC_RETURN_IF(dc::last_launch_status());
-    }
-    // A wavefront per long segment (up to 16 resident per CU); those past the device-side count
-    // return at once.
-    const int64_t lgrid = std::min<int64_t>((int64_t)p->long_cap, (int64_t)per_xcd_cus * 16);
-    spmv_slice_long<<<(unsigned)(std::max<int64_t>(1, lgrid) * kXcds), kLongWave, 0, ctx->stream>>>(
-        p->seg_ptr, p->col_s, p->val_s, x, p->partial, p->long_list, p->long_cnt, p->long_cap);
-    DC_RETURN_IF(dc::last_launch_status());
-  } else if (prev_sum_out) {
-    DC_RETURN_IF(dc::launch_reduce_partials_f64(ctx, p->block_sums, p->nblocks, prev_sum_out));
-  }
-  if (sums)
-    return launch_combine<true>(ctx, (unsigned)p->nblocks, p->ts, ld, p->slices, p->sb, p->seg_row, p->partial, y,
-                                p->rows, p->block_sums, scale);
-  return launch_combine<false>(ctx, (unsigned)p->nblocks, p->ts, ld, p->slices, p->sb, p->seg_row, p->partial, y,
-                               p->rows, nullptr, scale);
+  const uint32_t width = (uint32_t)p->slice_cols, cols = (uint32_t)std::max<int64_t>(p->cols, 1);
+  spmv_tile_products<<<(unsigned)p->nwg, kPass, 0, ctx->stream>>>(
+      p->col16, p->val_s, p->sbase, p->wrange, width, x, (uint32_t)p->cols, p->p, p->block_sums, p->nblocks,
+      prev_sum_out);
+  DC_RETURN_IF(dc::last_launch_status());
+  const unsigned bgrid = (unsigned)(kXcds * ((p->nblocks + kXcds - 1) / kXcds));
+  double* bs = sums ? p->block_sums : nullptr;
+#define DC_TILE_ROWS(TABLE)                                                                                    \
+  spmv_tile_rows<TABLE><<<bgrid, kPass, 0, ctx->stream>>>(p->rp, (int32_t)p->nnz, p->binfo, p->nblocks, p->toff,  \
+                                                          p->slices, p->p, p->dest16, p->col16, p->val_s, x, cols, \
+                                                          y, bs, scale)
+  if (p->slices <= kRowRuns) DC_TILE_ROWS(true);
+  else DC_TILE_ROWS(false);
+#undef DC_TILE_ROWS
+  return dc::last_launch_status();
 }
 
-// y_k = A·x_k; s_k = Σ y_k; x_{k+1} = y_k / s_k. The division moves into the next step's combine
+// y_k = A·x_k; s_k = Σ y_k; x_{k+1} = y_k / s_k. The division moves into the next step's row pass
 // (y_{k+1} = (A·y_k) / s_k), so the unnormalised y_k is the next step's input as it stands and the
 // buffers swap roles (x, y, x, ...); the last y is normalised into x once at the end. s_k is formed
-// by step k + 1's first gather launch, from step k's block sums, before step k + 1's combine
-// (which divides by it) overwrites them, so it costs no launch of its own.
+// by step k + 1's product pass from step k's block sums, before step k + 1's row pass (which
+// divides by it) overwrites them.
 int32_t plan_power_iterate(dc_hip_ctx* ctx, const dc_hip_spmv_plan* p, float* x, float* y, int32_t iterations,
                            double* last_sum_out) {
   if (p->rows == 0 || iterations == 0) return DC_OK;
@@ -1166,7 +974,11 @@ DC_HIP_API int32_t dc_hip_spmv_plan_create(dc_hip_ctx* ctx, const int32_t* row_p
   dc_hip_spmv_plan* p = new (std::nothrow) dc_hip_spmv_plan;
   if (!p) return DC_ERR_OUT_OF_MEMORY;
   p->device = ctx->device;
-  plan_shape(p, rows, cols, nnz, slice_cols_max);
+  const int32_t shape_st = plan_shape(p, rows, cols, nnz, slice_cols_max, ctx->cu_count);
+  if (shape_st != DC_OK) {
+    delete p;
+    return shape_st;
+  }
   void* mem = nullptr;
   if (hipMalloc(&mem, p->bytes) != hipSuccess) {
     delete p;
@@ -1232,7 +1044,7 @@ DC_HIP_API int32_t dc_hip_spmv_power_iterate_f32(dc_hip_ctx* ctx, const int32_t*
   // The plan lives in context scratch (reused by the next call; calls on a context are ordered).
   dc_hip_spmv_plan p;
   p.device = ctx->device;
-  plan_shape(&p, rows, rows, nnz, 0);
+  DC_RETURN_IF(plan_shape(&p, rows, rows, nnz, 0, ctx->cu_count));
   DC_RETURN_IF(dc::ensure_spmv_plan_mem(ctx, p.bytes));
   plan_layout(&p, ctx->spmv_plan_mem);
   DC_RETURN_IF(plan_build(ctx, &p, row_pointers, col_indices, values));

@@ -378,24 +378,26 @@ DC_HIP_API int32_t dc_hip_spmv_csr_f32(dc_hip_ctx* ctx, const int32_t* row_point
  *   y = A·x;  s = Σ y (float64);  x = y / s
  * leaving the normalised vector in x (rows == cols required). `y` is caller-provided scratch of
  * rows floats. The final L1 norm before the last normalisation is written to *last_sum_out
- * (device double, may be NULL). Builds a column-sliced plan (below) in context scratch first and
- * runs every iteration through it. */
+ * (device double, may be NULL). Builds a tiled plan (below) in context scratch first and runs
+ * every iteration through it. */
 DC_HIP_API int32_t dc_hip_spmv_power_iterate_f32(dc_hip_ctx* ctx, const int32_t* row_pointers,
                                                  const int32_t* col_indices, const float* values,
                                                  float* x, float* y, int64_t rows, int64_t nnz,
                                                  int32_t iterations, double* last_sum_out);
 
-/* Column-sliced SpMV plan: an analysis of a CSR matrix, built once on the device, for matrices
- * that are multiplied many times (CsrMatrix<T> reused across SparseOps.SpMV calls,
+/* Tiled SpMV plan: an analysis of a CSR matrix, built once on the device, for matrices that are
+ * multiplied many times (CsrMatrix<T> reused across SparseOps.SpMV calls,
  * src/Extensions/DotCompute.Algorithms/Sparse/SparseMatrix.cs:669-692; the power iteration).
- * The plan holds its own slice-major copy of the nonzeros (device memory owned by the plan), so
- * the CSR arrays may be freed once the creating call's stream work has run. Columns are cut into
- * slices of at most `slice_cols_max` columns (0 = the default, 1M columns = 4 MB of x, one XCD's
- * L2) and each XCD gathers from its own slices. Result: y[r] = 0.0f + (partial of slice 0) +
- * (partial of slice 1) + ..., each partial summed in index order, so with one slice (cols <=
- * slice width) rows of at most 256 nonzeros equal the sequential row sum bit for bit; otherwise
- * the row sum is reassociated by slice (within the fp32 tolerance). Column indices outside
- * [0, cols) are clamped into range on the device (they never fault); callers validate first. */
+ * The plan holds its own slice-major copy of the nonzeros and of the row pointers (device memory
+ * owned by the plan), so the CSR arrays may be freed once the creating call's stream work has run.
+ * Columns are cut into slices of at most `slice_cols_max` columns (0 = the default and the
+ * maximum, 32768 columns: a 128 KB tile of x in one CU's LDS; widened when more than 32768 slices
+ * would be needed); every product val·x[col] is formed once from an LDS tile, and each row is
+ * summed from its products in index order. Result: rows of at most 32 nonzeros equal the
+ * sequential float32 row sum (0.0f + p_0 + p_1 + ...) bit for bit, whatever the slice count;
+ * longer rows are summed in a fixed order (lane k of a wave adds products k, k + 64, ..., then a
+ * fixed tree), within the fp32 tolerance. Column indices outside [0, cols) are clamped into range
+ * on the device (they never fault); callers validate first. */
 typedef struct dc_hip_spmv_plan dc_hip_spmv_plan;
 DC_HIP_API int32_t dc_hip_spmv_plan_create(dc_hip_ctx* ctx, const int32_t* row_pointers,
                                            const int32_t* col_indices, const float* values,

@@ -1,13 +1,14 @@
-"""GPU parity: the column-sliced SpMV plan (dc_hip_spmv_plan_*), which the power iteration uses.
+"""GPU parity: the tiled SpMV plan (dc_hip_spmv_plan_*), which the power iteration uses.
 
 Reference semantics: SparseOps.SpMV (SparseMatrix.cs:669-692), a sequential float32 row sum. The
-plan sums each row slice by slice: partial_s = sequential sum of the row's products whose column
-falls in slice s (index order) for segments of at most 32 products (longer ones: a fixed-order
-wave reduction), then y = 0.0f + partial_0 + partial_1 + ... in slice order. Two checks per case:
+plan forms every product val * x[col] once (x tiles of up to 32768 columns in LDS) and stages each
+row block's products at their CSR positions, so a row of at most 32 nonzeros is summed by one lane
+in index order (0.0f + p_0 + p_1 + ...), whatever the number of column slices; longer rows are
+summed by a wave (lane k adds products k, k + 64, ... in order, then a fixed tree). Two checks per
+case:
   - parity: |y - y64| <= 1e-4 * sum_i |v_i x_c(i)| per row, y64 the float64 row sum;
-  - exactness of the order: rows whose segments are all at most 32 nonzeros must equal, bit for
-    bit, the same slice-ordered sum composed from the oracle's sequential float32 SpMV applied to
-    each slice's sub-matrix (a different order than one sequential pass would be caught).
+  - exactness of the order: rows of at most 32 nonzeros equal the oracle's sequential float32
+    SpMV bit for bit (a product formed twice, dropped, misplaced or summed out of order fails it).
 """
 import numpy as np
 import pytest
@@ -18,7 +19,9 @@ from dotcompute_amd import hip
 pytestmark = pytest.mark.gpu
 
 REL = 1e-4
-SEQ_SEG = 32  # segments up to this length are summed sequentially on the GPU
+SEQ_ROW = 32          # rows up to this length are summed sequentially on the GPU
+TILE_COLS = 32768     # widest slice (one x tile in LDS)
+GIANT_ROW = 8192      # longer rows are summed with their products formed from x directly
 
 
 def upload_csr(ctx, rp, col, val):
@@ -30,22 +33,11 @@ def row_scale(rp, col, val, x):
     return oracle.spmv_csr_f64(rp, col, np.abs(val), np.abs(x).astype(np.float64))
 
 
-def sliced_reference(rp, col, val, x, width):
-    """Slice-ordered float32 sum from the oracle's sequential SpMV on each slice's sub-matrix; also
-    returns, per row, whether any of its segments is longer than SEQ_SEG (tree-summed on the GPU)."""
-    rows = rp.size - 1
-    slices = (int(x.size) + width - 1) // width
-    row_of = np.repeat(np.arange(rows), np.diff(rp))
-    y = np.zeros(rows, np.float32)
-    has_long = np.zeros(rows, bool)
-    for s in range(slices):
-        keep = (col // width) == s
-        counts = np.bincount(row_of[keep], minlength=rows).astype(np.int64)
-        sub_rp = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
-        part = oracle.spmv_csr_f32(sub_rp, np.ascontiguousarray(col[keep]), np.ascontiguousarray(val[keep]), x)
-        y = (y + part).astype(np.float32)
-        has_long |= counts > SEQ_SEG
-    return y, has_long
+def expected_slices(cols, width):
+    w = min(width, TILE_COLS) if width > 0 else TILE_COLS
+    if -(-cols // w) > 32768:
+        w = -(-cols // 32768)
+    return max(1, -(-cols // w)), w
 
 
 def run_plan(ctx, rp, col, val, x, slice_cols_max=0, repeat=2):
@@ -67,26 +59,29 @@ def run_plan(ctx, rp, col, val, x, slice_cols_max=0, repeat=2):
     return ys[0], info
 
 
-def check(rp, col, val, x, y, width):
+def check(rp, col, val, x, y):
     ref64 = oracle.spmv_csr_f64(rp, col, val, x.astype(np.float64))
     assert np.all(np.abs(y - ref64) <= REL * row_scale(rp, col, val, x) + 1e-30)
-    ref32, has_long = sliced_reference(rp, col, val, x, width)
-    ok = ~has_long
+    ref32 = oracle.spmv_csr_f32(rp, col, val, x)
+    ok = np.diff(rp) <= SEQ_ROW
     assert np.array_equal(y[ok].view(np.uint32), ref32[ok].view(np.uint32))
 
 
-# (rows, cols, slice_cols_max) -> expected number of slices. Default width (0): one slice up to
-# 512 KB of x, else 2 / 4 / 8 slices up to 1 / 2 / 4 MB (an XCD's share of x at most 512 KB).
+# (rows, cols, slice_cols_max) -> expected number of slices: ceil(cols / w), w = slice_cols_max
+# capped at 32768 columns (0 = 32768), widened when more than 32768 slices would be needed.
 SHAPES = [
     (5000, 5000, 0, 1),
-    (200_000, 200_000, 0, 2),
-    (600_000, 600_000, 0, 8),
+    (200_000, 200_000, 0, 7),
+    (600_000, 600_000, 0, 19),
+    (100_000, 100_000, 1 << 20, 4),   # wider than one x tile: capped at 32768 columns
     (5000, 5000, 2500, 2),
     (5000, 5000, 1250, 4),
     (5000, 5000, 625, 8),
-    (5000, 5000, 300, 24),
-    (20000, 20000, 100, 32),     # capped at 32 slices: wider than asked
-    (3000, 70000, 4000, 24),     # rectangular, more columns than rows
+    (5000, 5000, 300, 17),
+    (20000, 20000, 100, 200),
+    (20000, 20000, 7, 2858),          # more slices than the row pass's LDS chunk table holds
+    (70000, 70000, 1, 23334),         # more than 32768 slices asked for: widened to 3 columns
+    (3000, 70000, 4000, 18),          # rectangular, more columns than rows
     (1, 1, 0, 1),
     (64, 64, 16, 4),
 ]
@@ -101,53 +96,69 @@ def test_plan_slices_vs_oracle(ctx, rows, cols, width, slices):
         rp, col, val = oracle.gen_zipf_csr(rows, seed, max_degree=min(4096, cols - 1), cols=cols)
     x = oracle.gen_uniform_f32(cols, seed, 5, unit_interval=True)
     y, (s, w, nbytes) = run_plan(ctx, rp, col, val, x, width)
-    assert s == slices and w == (cols + s - 1) // s and nbytes > 0
-    check(rp, col, val, x, y, w)
+    assert (s, w) == expected_slices(cols, width) and s == slices and nbytes > 0
+    check(rp, col, val, x, y)
 
 
-def test_plan_signed_values_and_long_segments(ctx):
-    """Negative values, rows of 0 / 1 / 4096 / 3000 nonzeros; segments summed sequentially (up to
-    32), by the whole wave (33-256) and by a workgroup (longer), at each threshold; empty rows
-    exactly zero."""
-    lens = [0, 1, 4096, 0, 3000, 7, 129, 128, 0, 600, 257, 256, 513, 512, 32, 33, 31, 64, 65]
+def test_plan_signed_values_long_and_giant_rows(ctx):
+    """Negative values; rows of 0 / 1 / 31-33 / 4096 / 3000 nonzeros; rows at the giant threshold
+    (8192 nonzeros: staged; 8193 and 40000: summed from x directly), each followed by more rows;
+    empty rows exactly zero."""
+    lens = [0, 1, 4096, 0, 3000, 7, 129, 128, 0, 600, 257, 256, 513, 512, 32, 33, 31, 64, 65,
+            GIANT_ROW, 5, GIANT_ROW + 1, 0, 3, 40000, 2, 1, 0, 17]
     rp = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
     cols = 5000
     col = (np.arange(rp[-1]) * 7919 % cols).astype(np.int32)
     val = oracle.gen_uniform_f32(int(rp[-1]), 9, 0)
     x = oracle.gen_uniform_f32(cols, 9, 1)
-    for width, slices in ((0, 1), (2500, 2), (625, 8)):
+    for width in (0, 2500, 625, 3):
         y, (s, w, _) = run_plan(ctx, rp, col, val, x, width)
-        assert s == slices
-        check(rp, col, val, x, y, w)
-        assert y[0] == 0 and y[3] == 0 and y[8] == 0
+        assert (s, w) == expected_slices(cols, width)
+        check(rp, col, val, x, y)
+        assert y[0] == 0 and y[3] == 0 and y[8] == 0 and y[22] == 0 and y[27] == 0
 
 
-def test_plan_one_slice_equals_sequential_reference(ctx):
-    """One slice (asked for with a slice width of all the columns): every row is one segment, so
-    rows of at most 32 nonzeros (about 99% of the rows of this graph) are the sequential float32
-    row sum of SparseOps.SpMV bit for bit."""
+def test_plan_many_row_blocks_of_empty_rows(ctx):
+    """Blocks are also cut every 16384 rows: 100,000 rows, mostly empty, a few short rows spread
+    among them."""
+    rows, cols = 100_000, 1000
+    lens = np.zeros(rows, np.int64)
+    lens[::997] = 3
+    lens[50_000:50_010] = 40
+    rp = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    col = (np.arange(rp[-1]) * 613 % cols).astype(np.int32)
+    val = oracle.gen_uniform_f32(int(rp[-1]), 3, 0)
+    x = oracle.gen_uniform_f32(cols, 3, 1)
+    y, _ = run_plan(ctx, rp, col, val, x, 0)
+    check(rp, col, val, x, y)
+    assert np.all(y[lens == 0] == 0)
+
+
+def test_plan_equals_sequential_reference(ctx):
+    """Rows of at most 32 nonzeros (about 99% of the rows of this graph) are the sequential
+    float32 row sum of SparseOps.SpMV bit for bit, with 10 column slices."""
     rows = 300_000
     rp, col, val = oracle.gen_zipf_csr(rows, 7)
     x = oracle.gen_uniform_f32(rows, 7, 5, unit_interval=True)
-    y, (s, _, _) = run_plan(ctx, rp, col, val, x, rows, repeat=1)
-    assert s == 1
+    y, (s, _, _) = run_plan(ctx, rp, col, val, x, 0, repeat=1)
+    assert s == 10
     ref = oracle.spmv_csr_f32(rp, col, val, x)
-    short = np.diff(rp) <= SEQ_SEG
+    short = np.diff(rp) <= SEQ_ROW
     assert short.sum() > 0.98 * rows
     assert np.array_equal(y[short].view(np.uint32), ref[short].view(np.uint32))
 
 
-@pytest.mark.parametrize("width,slices", [(1 << 16, 16), (1 << 15, 32), (1 << 18, 4)])
+@pytest.mark.parametrize("width,slices", [(0, 31), (1 << 12, 245), (1000, 1000)])
 def test_plan_1m_many_slices(ctx, width, slices):
     rows = 1_000_000
     rp, col, val = oracle.gen_zipf_csr(rows, 42)
     x = oracle.gen_uniform_f32(rows, 42, 5, unit_interval=True)
     y, (s, w, _) = run_plan(ctx, rp, col, val, x, width, repeat=2)
     assert s == slices
-    check(rp, col, val, x, y, w)
+    check(rp, col, val, x, y)
 
 
-@pytest.mark.parametrize("width", [0, 1 << 16])
+@pytest.mark.parametrize("width", [0, 1 << 12])
 def test_plan_power_iteration_1m_vs_oracle(ctx, width):
     rows, iters = 1_000_000, 20
     rp, col, val = oracle.gen_zipf_csr(rows, 42)
@@ -174,11 +185,11 @@ def test_plan_power_iteration_1m_vs_oracle(ctx, width):
 
 def test_plan_empty_matrices(ctx):
     # rows but no nonzeros: y must be all zeros
-    rows = 1000
-    rp = np.zeros(rows + 1, np.int32)
-    x = np.ones(rows, np.float32)
-    y, (s, _, _) = run_plan(ctx, rp, np.zeros(0, np.int32), np.zeros(0, np.float32), x, 0, repeat=1)
-    assert s == 1 and np.all(y == 0)
+    for rows in (1000, 40_000):
+        rp = np.zeros(rows + 1, np.int32)
+        x = np.ones(rows, np.float32)
+        y, (s, _, _) = run_plan(ctx, rp, np.zeros(0, np.int32), np.zeros(0, np.float32), x, 0, repeat=1)
+        assert s == -(-rows // TILE_COLS) and np.all(y == 0)
 
 
 def test_plan_argument_errors(ctx):
