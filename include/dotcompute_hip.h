@@ -390,10 +390,11 @@ DC_HIP_API int32_t dc_hip_spmv_power_iterate_f32(dc_hip_ctx* ctx, const int32_t*
  * src/Extensions/DotCompute.Algorithms/Sparse/SparseMatrix.cs:669-692; the power iteration).
  * The plan holds its own slice-major copy of the nonzeros and of the row pointers (device memory
  * owned by the plan), so the CSR arrays may be freed once the creating call's stream work has run.
- * Columns are cut into slices of at most `slice_cols_max` columns (0 = the default and the
- * maximum, 32768 columns: a 128 KB tile of x in one CU's LDS; widened when more than 32768 slices
- * would be needed); every product val·x[col] is formed once from an LDS tile, and each row is
- * summed from its products in index order. Result: rows of at most 32 nonzeros equal the
+ * Columns are cut into slices of at most `slice_cols_max` columns (at most 32768: a 128 KB tile
+ * of x in one CU's LDS; 0 = the default, the widest power of two from 4096 to 32768 columns that
+ * is at most nnz / (2 x the device's CU count), wide enough for at most 1024 slices where 32768
+ * allows; widened when more than 32768 slices would be needed); every product val·x[col] is
+ * formed once from an LDS tile, and each row is summed from its products in index order. Result: rows of at most 32 nonzeros equal the
  * sequential float32 row sum (0.0f + p_0 + p_1 + ...) bit for bit, whatever the slice count;
  * longer rows are summed in a fixed order (lane k of a wave adds products k, k + 64, ..., then a
  * fixed tree), within the fp32 tolerance. Column indices outside [0, cols) are clamped into range

@@ -33,8 +33,17 @@ def row_scale(rp, col, val, x):
     return oracle.spmv_csr_f64(rp, col, np.abs(val), np.abs(x).astype(np.float64))
 
 
-def expected_slices(cols, width):
-    w = min(width, TILE_COLS) if width > 0 else TILE_COLS
+def expected_slices(cols, width, nnz=0):
+    """(slices, columns per slice) the plan picks: slice_cols_max capped at 32768, or by default
+    the widest power of two in [4096, 32768] with w <= nnz / (2 * CUs), widened while more than
+    1024 slices would be needed; then widened when more than 32768 slices would be needed."""
+    if width > 0:
+        w = min(width, TILE_COLS)
+    else:
+        cus = max(1, hip.device_info(0).compute_units)
+        w = 4096
+        while w < TILE_COLS and (2 * w <= nnz // (2 * cus) or -(-cols // w) > 1024):
+            w *= 2
     if -(-cols // w) > 32768:
         w = -(-cols // 32768)
     return max(1, -(-cols // w)), w
@@ -68,11 +77,12 @@ def check(rp, col, val, x, y):
 
 
 # (rows, cols, slice_cols_max) -> expected number of slices: ceil(cols / w), w = slice_cols_max
-# capped at 32768 columns (0 = 32768), widened when more than 32768 slices would be needed.
+# capped at 32768 columns, widened when more than 32768 slices would be needed (None: the
+# default width, which depends on the number of nonzeros and of CUs; see expected_slices).
 SHAPES = [
-    (5000, 5000, 0, 1),
-    (200_000, 200_000, 0, 7),
-    (600_000, 600_000, 0, 19),
+    (5000, 5000, 0, None),
+    (200_000, 200_000, 0, None),
+    (600_000, 600_000, 0, None),
     (100_000, 100_000, 1 << 20, 4),   # wider than one x tile: capped at 32768 columns
     (5000, 5000, 2500, 2),
     (5000, 5000, 1250, 4),
@@ -82,7 +92,7 @@ SHAPES = [
     (20000, 20000, 7, 2858),          # more slices than the row pass's LDS chunk table holds
     (70000, 70000, 1, 23334),         # more than 32768 slices asked for: widened to 3 columns
     (3000, 70000, 4000, 18),          # rectangular, more columns than rows
-    (1, 1, 0, 1),
+    (1, 1, 0, None),
     (64, 64, 16, 4),
 ]
 
@@ -96,7 +106,7 @@ def test_plan_slices_vs_oracle(ctx, rows, cols, width, slices):
         rp, col, val = oracle.gen_zipf_csr(rows, seed, max_degree=min(4096, cols - 1), cols=cols)
     x = oracle.gen_uniform_f32(cols, seed, 5, unit_interval=True)
     y, (s, w, nbytes) = run_plan(ctx, rp, col, val, x, width)
-    assert (s, w) == expected_slices(cols, width) and s == slices and nbytes > 0
+    assert (s, w) == expected_slices(cols, width, col.size) and s == (slices or s) and nbytes > 0
     check(rp, col, val, x, y)
 
 
@@ -113,7 +123,7 @@ def test_plan_signed_values_long_and_giant_rows(ctx):
     x = oracle.gen_uniform_f32(cols, 9, 1)
     for width in (0, 2500, 625, 3):
         y, (s, w, _) = run_plan(ctx, rp, col, val, x, width)
-        assert (s, w) == expected_slices(cols, width)
+        assert (s, w) == expected_slices(cols, width, col.size)
         check(rp, col, val, x, y)
         assert y[0] == 0 and y[3] == 0 and y[8] == 0 and y[22] == 0 and y[27] == 0
 
@@ -136,29 +146,29 @@ def test_plan_many_row_blocks_of_empty_rows(ctx):
 
 def test_plan_equals_sequential_reference(ctx):
     """Rows of at most 32 nonzeros (about 99% of the rows of this graph) are the sequential
-    float32 row sum of SparseOps.SpMV bit for bit, with 10 column slices."""
+    float32 row sum of SparseOps.SpMV bit for bit, with the default slices (tens of them)."""
     rows = 300_000
     rp, col, val = oracle.gen_zipf_csr(rows, 7)
     x = oracle.gen_uniform_f32(rows, 7, 5, unit_interval=True)
-    y, (s, _, _) = run_plan(ctx, rp, col, val, x, 0, repeat=1)
-    assert s == 10
+    y, (s, w, _) = run_plan(ctx, rp, col, val, x, 0, repeat=1)
+    assert (s, w) == expected_slices(rows, 0, col.size) and s > 1
     ref = oracle.spmv_csr_f32(rp, col, val, x)
     short = np.diff(rp) <= SEQ_ROW
     assert short.sum() > 0.98 * rows
     assert np.array_equal(y[short].view(np.uint32), ref[short].view(np.uint32))
 
 
-@pytest.mark.parametrize("width,slices", [(0, 31), (1 << 12, 245), (1000, 1000)])
+@pytest.mark.parametrize("width,slices", [(0, None), (1 << 15, 31), (1 << 12, 245), (1000, 1000)])
 def test_plan_1m_many_slices(ctx, width, slices):
     rows = 1_000_000
     rp, col, val = oracle.gen_zipf_csr(rows, 42)
     x = oracle.gen_uniform_f32(rows, 42, 5, unit_interval=True)
     y, (s, w, _) = run_plan(ctx, rp, col, val, x, width, repeat=2)
-    assert s == slices
+    assert (s, w) == expected_slices(rows, width, col.size) and s == (slices or s)
     check(rp, col, val, x, y)
 
 
-@pytest.mark.parametrize("width", [0, 1 << 12])
+@pytest.mark.parametrize("width", [0, 1 << 15])
 def test_plan_power_iteration_1m_vs_oracle(ctx, width):
     rows, iters = 1_000_000, 20
     rp, col, val = oracle.gen_zipf_csr(rows, 42)
@@ -188,8 +198,8 @@ def test_plan_empty_matrices(ctx):
     for rows in (1000, 40_000):
         rp = np.zeros(rows + 1, np.int32)
         x = np.ones(rows, np.float32)
-        y, (s, _, _) = run_plan(ctx, rp, np.zeros(0, np.int32), np.zeros(0, np.float32), x, 0, repeat=1)
-        assert s == -(-rows // TILE_COLS) and np.all(y == 0)
+        y, (s, w, _) = run_plan(ctx, rp, np.zeros(0, np.int32), np.zeros(0, np.float32), x, 0, repeat=1)
+        assert (s, w) == expected_slices(rows, 0, 0) and np.all(y == 0)
 
 
 def test_plan_argument_errors(ctx):
