@@ -358,28 +358,28 @@ __device__ inline BlockRange load_block(const int4* __restrict__ binfo, int32_t 
   return BlockRange{a.x, a.y, a.z, a.w, c.x};
 }
 
-// A1: first row of each block (blk_row[nblocks] = rows).
+// A1: first row of each block (blk_row[nblocks] = rows): thread r compares row r's block with
+// row r - 1's and writes the blocks that start at r (one thread per row, no search).
 __global__ __launch_bounds__(256) void plan_blocks(const int32_t* __restrict__ rp, int64_t rows, int32_t nnz,
                                                    int32_t nblocks, int32_t* __restrict__ blk_row) {
-  const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (k > nblocks) return;
-  int64_t a = 0, z = rows;  // first row whose block is >= k
-  while (a < z) {
-    const int64_t m = (a + z) >> 1;
-    if (block_of(rp[m], nnz, m) < k) a = m + 1; else z = m;
-  }
-  blk_row[k] = (int32_t)a;
+  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r > rows) return;
+  const int64_t here = r < rows ? min(block_of(rp[r], nnz, r), (int64_t)nblocks - 1) : (int64_t)nblocks;
+  const int64_t prev = r > 0 ? min(block_of(rp[r - 1], nnz, r - 1), (int64_t)nblocks - 1) : -1;
+  for (int64_t k = max(prev, (int64_t)-1) + 1; k <= here; ++k) blk_row[k] = (int32_t)r;
 }
 
 // A1b: the bounds of each block (BlockRange) from blk_row and the row pointers.
-__global__ __launch_bounds__(256) void plan_block_info(const int32_t* __restrict__ rp, int32_t nnz,
+// Row bounds are clamped into [0, rows]: with row pointers that are not monotone some blk_row
+// entries are never written, and the passes must still stay in range.
+__global__ __launch_bounds__(256) void plan_block_info(const int32_t* __restrict__ rp, int32_t rows, int32_t nnz,
                                                        const int32_t* __restrict__ blk_row, int32_t nblocks,
                                                        int4* __restrict__ binfo) {
   const int32_t b = (int32_t)(blockIdx.x * 256 + threadIdx.x);
   if (b >= nblocks) return;
   BlockRange g;
-  g.r0 = blk_row[b];
-  g.r1 = max(blk_row[b + 1], g.r0);
+  g.r0 = min(max(blk_row[b], 0), rows);
+  g.r1 = min(max(blk_row[b + 1], g.r0), rows);
   g.j0 = g.r0 < g.r1 ? clamp_nz(rp[g.r0], nnz) : 0;
   g.j1 = g.jg = g.j0;
   if (g.r0 < g.r1) {
@@ -877,9 +877,10 @@ int32_t plan_build(dc_hip_ctx* ctx, dc_hip_spmv_plan* p, const int32_t* rp, cons
   const int32_t S = p->slices, nb = p->nblocks, nnz = (int32_t)p->nnz;
   const uint32_t width = (uint32_t)p->slice_cols, cols = (uint32_t)std::max<int64_t>(p->cols, 1);
   DC_RETURN_IF_HIP(hipMemcpyAsync(p->rp, rp, (size_t)(p->rows + 1) * 4, hipMemcpyDeviceToDevice, ctx->stream));
-  plan_blocks<<<(unsigned)((nb + 1 + 255) / 256), 256, 0, ctx->stream>>>(p->rp, p->rows, nnz, nb, p->blk_row);
+  plan_blocks<<<(unsigned)((p->rows + 1 + 255) / 256), 256, 0, ctx->stream>>>(p->rp, p->rows, nnz, nb, p->blk_row);
   DC_RETURN_IF(dc::last_launch_status());
-  plan_block_info<<<(unsigned)((nb + 255) / 256), 256, 0, ctx->stream>>>(p->rp, nnz, p->blk_row, nb, p->binfo);
+  plan_block_info<<<(unsigned)((nb + 255) / 256), 256, 0, ctx->stream>>>(p->rp, (int32_t)p->rows, nnz, p->blk_row,
+                                                                         nb, p->binfo);
   DC_RETURN_IF(dc::last_launch_status());
   const unsigned bgrid = (unsigned)(kXcds * ((nb + kXcds - 1) / kXcds));
 #define DC_TILE_COUNT(SM)                                                                                   \
