@@ -279,10 +279,17 @@ __device__ inline int32_t xcd_block(int32_t nblocks) {
   return b < nblocks ? b : -1;
 }
 
-// Sequential sum of p[i0..i1) (index order), LDS reads four at a time.
+// Sequential sum of p[i0..i1) (index order), LDS reads eight, then four at a time.
 __device__ inline float lds_seq_sum(const float* __restrict__ p, int32_t i0, int32_t i1) {
   float sum = 0.0f;
   int32_t i = i0;
+  for (; i + 8 <= i1; i += 8) {
+    float a[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) a[u] = p[i + u];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) sum += a[u];
+  }
   for (; i + 4 <= i1; i += 4) {
     const float a0 = p[i], a1 = p[i + 1], a2 = p[i + 2], a3 = p[i + 3];
     sum += a0;
@@ -665,7 +672,7 @@ __global__ __launch_bounds__(kPass) void spmv_tile_rows(
     const int32_t* __restrict__ rp, int32_t nnz, const int4* __restrict__ binfo, int32_t nblocks,
     const int32_t* __restrict__ toff, int32_t S, const float* __restrict__ p, const uint16_t* __restrict__ dest16,
     const uint16_t* __restrict__ col16, const float* __restrict__ val_s, const float* __restrict__ x, uint32_t cols,
-    float* __restrict__ y, double* __restrict__ block_sums, const double* __restrict__ scale) {
+    float* __restrict__ y, double* __restrict__ block_sums, const double* __restrict__ scale, uint32_t pbytes) {
   __shared__ float stage[kStage];
   __shared__ int32_t run_base[kTable ? kRowRuns : 1];
   __shared__ int32_t wsum[kPassWaves];
@@ -713,15 +720,18 @@ __global__ __launch_bounds__(kPass) void spmv_tile_rows(
     const int32_t nit = (E + kPass - 1) / kPass;
     float pv[kIt];
     uint32_t dv[kIt];
+    // buffer loads: 32-bit offsets on a scalar base (the plan keeps p below 4 GiB for this path)
+    const auto rp4 = dc::range_rsrc(p, (int32_t)(uint32_t)(pbytes));
+    const auto rd2 = dc::range_rsrc(dest16, (int32_t)(uint32_t)(pbytes / 2));
 #pragma unroll
     for (int k = 0; k < kIt; ++k) {
       pv[k] = 0.0f;
       dv[k] = kStage;
       const int32_t li = t + k * kPass;
       if (k < nit && li < E) {
-        const int32_t at = run_base[run_of[li]] + li;
-        pv[k] = p[at];
-        dv[k] = dest16[at];
+        const uint32_t at = (uint32_t)(run_base[run_of[li]] + li);
+        pv[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp4, at * 4u, 0, 0));
+        dv[k] = __builtin_amdgcn_raw_buffer_load_b16(rd2, at * 2u, 0, 0);
       }
     }
     __syncthreads();  // every run_of read is done before the stage is overwritten
@@ -923,8 +933,9 @@ int32_t plan_spmv(dc_hip_ctx* ctx, const dc_hip_spmv_plan* p, const float* x, fl
 #define DC_TILE_ROWS(TABLE)                                                                                    \
   spmv_tile_rows<TABLE><<<bgrid, kPass, 0, ctx->stream>>>(p->rp, (int32_t)p->nnz, p->binfo, p->nblocks, p->toff,  \
                                                           p->slices, p->p, p->dest16, p->col16, p->val_s, x, cols, \
-                                                          y, bs, scale)
-  if (p->slices <= kRowRuns) DC_TILE_ROWS(true);
+                                                          y, bs, scale, (uint32_t)(p->zcap * 4))
+  // the table path addresses the products with 32-bit byte offsets
+  if (p->slices <= kRowRuns && p->zcap * 4 <= (int64_t)UINT32_MAX) DC_TILE_ROWS(true);
   else DC_TILE_ROWS(false);
 #undef DC_TILE_ROWS
   return dc::last_launch_status();
