@@ -219,8 +219,9 @@ int32_t check_csr(const int32_t* rp, const int32_t* col, const float* val, int64
 // rate of L1-miss requests a CU keeps in flight (about 0.3 per cycle per CU on MI355X), served by
 // the memory-side cache by far less. The plan moves every gather into LDS:
 //   - columns are cut into slices of at most kTileCols columns (a 128 KB tile of x, one CU's LDS);
-//   - rows are cut into blocks: row r is in block rp[r] / kBlockSpan + r / kBlockRows, so a block
-//     holds fewer than kStage nonzeros unless it ends with a giant row (more than kGiantRow
+//   - rows are cut into blocks: row r is in block rp[r] / span + r / kBlockRows (span = 4096 or
+//     8192 nonzeros, chosen per plan), so a block holds fewer than 2 span nonzeros unless it ends
+//     with a giant row (more than span
 //     nonzeros; at most one per block, always its last row: the next row starts past the block's
 //     span);
 //   - the plan keeps a slice-major copy of the nonzeros: slice s holds, block after block, the
@@ -241,16 +242,16 @@ int32_t check_csr(const int32_t* rp, const int32_t* col, const float* val, int64
 // =============================================================================================
 constexpr int kTileCols = 32768;          // widest slice: a 128 KB x tile
 constexpr int kMinTileCols = 4096;        // narrowest default slice
-constexpr int kBlockSpan = 8192;          // row r is in block rp[r] / kBlockSpan + r / kBlockRows
+constexpr int kSpanBig = 8192;            // block span (nonzeros) of large matrices; small ones
+constexpr int kSpanSmall = 4096;          // take half, with row-pass workgroups of half the size
 constexpr int kBlockRows = 16384;
-constexpr int kStage = 2 * kBlockSpan;    // products of a block's rows other than a giant one (64 KB)
-constexpr int kGiantRow = kBlockSpan;     // longer rows are giant
+constexpr int kStage = 2 * kSpanBig;      // most products of a block's rows other than a giant one
 constexpr int kSeqRow = 32;               // rows up to this length are summed by one lane
 constexpr int kPass = 1024;               // threads per workgroup of the plan kernels
 constexpr int kPassWaves = kPass / 64;
 constexpr int kMaxSlices = 32768;         // (1 << 30) columns / kTileCols
 constexpr int kPad = 8;                   // slice regions start at multiples of 8 entries
-constexpr int kRowRuns = 1024;            // up to this many slices, blocks are staged through LDS tables
+constexpr int kRowRuns = 1024;            // up to this many slices, the scatter stages through LDS
 constexpr int kRowPre = 2;                // row pass: row steps whose bounds are loaded before staging
 constexpr int kXcds = 8;
 
@@ -349,12 +350,12 @@ __device__ int32_t block_scan_inplace(int32_t* a, int32_t n, int32_t* wsum) {
   return carry;
 }
 
-__device__ inline int64_t block_of(int32_t start, int32_t nnz, int64_t r) {
-  return (int64_t)clamp_nz(start, nnz) / kBlockSpan + r / kBlockRows;
+__device__ inline int64_t block_of(int32_t start, int32_t nnz, int64_t r, int32_t span) {
+  return (int64_t)clamp_nz(start, nnz) / span + r / kBlockRows;
 }
 
 // Rows [r0, r1) of block b; its nonzeros other than a giant row's are [j0, j1), the giant row's
-// (if any) [j1, jg). A consistent matrix has j1 - j0 < kStage; the clamp keeps a malformed one's
+// (if any) [j1, jg). A consistent matrix has j1 - j0 < 2 span; the clamp keeps a malformed one's
 // positions inside the stage (its results are then meaningless, but every access stays in range).
 // The plan keeps them per block (binfo: two int4 per block), so a pass reads them in one load.
 struct BlockRange {
@@ -368,11 +369,11 @@ __device__ inline BlockRange load_block(const int4* __restrict__ binfo, int32_t 
 // A1: first row of each block (blk_row[nblocks] = rows): thread r compares row r's block with
 // row r - 1's and writes the blocks that start at r (one thread per row, no search).
 __global__ __launch_bounds__(256) void plan_blocks(const int32_t* __restrict__ rp, int64_t rows, int32_t nnz,
-                                                   int32_t nblocks, int32_t* __restrict__ blk_row) {
+                                                   int32_t nblocks, int32_t span, int32_t* __restrict__ blk_row) {
   const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (r > rows) return;
-  const int64_t here = r < rows ? min(block_of(rp[r], nnz, r), (int64_t)nblocks - 1) : (int64_t)nblocks;
-  const int64_t prev = r > 0 ? min(block_of(rp[r - 1], nnz, r - 1), (int64_t)nblocks - 1) : -1;
+  const int64_t here = r < rows ? min(block_of(rp[r], nnz, r, span), (int64_t)nblocks - 1) : (int64_t)nblocks;
+  const int64_t prev = r > 0 ? min(block_of(rp[r - 1], nnz, r - 1, span), (int64_t)nblocks - 1) : -1;
   for (int64_t k = max(prev, (int64_t)-1) + 1; k <= here; ++k) blk_row[k] = (int32_t)r;
 }
 
@@ -381,7 +382,7 @@ __global__ __launch_bounds__(256) void plan_blocks(const int32_t* __restrict__ r
 // entries are never written, and the passes must still stay in range.
 __global__ __launch_bounds__(256) void plan_block_info(const int32_t* __restrict__ rp, int32_t rows, int32_t nnz,
                                                        const int32_t* __restrict__ blk_row, int32_t nblocks,
-                                                       int4* __restrict__ binfo) {
+                                                       int32_t span, int4* __restrict__ binfo) {
   const int32_t b = (int32_t)(blockIdx.x * 256 + threadIdx.x);
   if (b >= nblocks) return;
   BlockRange g;
@@ -391,8 +392,8 @@ __global__ __launch_bounds__(256) void plan_block_info(const int32_t* __restrict
   g.j1 = g.jg = g.j0;
   if (g.r0 < g.r1) {
     const int32_t last = max(clamp_nz(rp[g.r1 - 1], nnz), g.j0), end = max(clamp_nz(rp[g.r1], nnz), last);
-    const bool giant = end - last > kGiantRow;
-    g.j1 = min(giant ? last : end, g.j0 + kStage);
+    const bool giant = end - last > span;
+    g.j1 = min(giant ? last : end, g.j0 + 2 * span);
     g.jg = giant ? end : g.j1;
   }
   binfo[2 * b] = make_int4(g.r0, g.r1, g.j0, g.j1);
@@ -658,8 +659,9 @@ __global__ __launch_bounds__(kPass) void spmv_tile_products(const uint16_t* __re
   }
 }
 
-// Row pass, a workgroup per block (XCD-contiguous; 64 KB of LDS, two workgroups per CU). With
-// kTable (S <= kRowRuns) the staging is one round trip: the block's run lengths go to LDS, a prefix
+// Row pass, a workgroup of SPAN / 8 threads per block (XCD-contiguous; 8 B of LDS per span
+// nonzero: two workgroups per CU with span 8192, four with 4096). With kTable (S <= SPAN / 8)
+// the staging is one round trip: the block's run lengths go to LDS, a prefix
 // over them numbers its products in slice-major order, every product's run is written to a table
 // (held in the stage buffer until the products arrive), and thread t loads products t, t + kPass,
 // ... before writing any of them to their CSR positions. Without it (more slices), a wave stages
@@ -667,16 +669,17 @@ __global__ __launch_bounds__(kPass) void spmv_tile_products(const uint16_t* __re
 // rows, a lane per row, 64 consecutive rows per wave step. With `scale`, y = (float)((double)row
 // sum / *scale) (the power iteration's previous normalisation moved onto this product); with
 // block_sums, the block's float64 sum of y in a fixed order.
-template <bool kTable>
-__global__ __launch_bounds__(kPass) void spmv_tile_rows(
+template <bool kTable, int SPAN>
+__global__ __launch_bounds__(SPAN / 8) void spmv_tile_rows(
     const int32_t* __restrict__ rp, int32_t nnz, const int4* __restrict__ binfo, int32_t nblocks,
     const int32_t* __restrict__ toff, int32_t S, const float* __restrict__ p, const uint16_t* __restrict__ dest16,
     const uint16_t* __restrict__ col16, const float* __restrict__ val_s, const float* __restrict__ x, uint32_t cols,
     float* __restrict__ y, double* __restrict__ block_sums, const double* __restrict__ scale, uint32_t pbytes) {
-  __shared__ float stage[kStage];
-  __shared__ int32_t run_base[kTable ? kRowRuns : 1];
-  __shared__ int32_t wsum[kPassWaves];
-  __shared__ double red[kPassWaves];
+  constexpr int kThreads = SPAN / 8, kWaves = kThreads / 64, kSt = 2 * SPAN;  // kSt: stage entries
+  __shared__ float stage[kSt];
+  __shared__ int32_t run_base[kTable ? kThreads : 1];
+  __shared__ int32_t wsum[kWaves];
+  __shared__ double red[kWaves];
   const int32_t b = xcd_block(nblocks);
   if (b < 0) return;  // whole workgroup
   const int t = threadIdx.x, lane = t & 63;
@@ -688,14 +691,13 @@ __global__ __launch_bounds__(kPass) void spmv_tile_rows(
   int32_t pb[kRowPre], pe[kRowPre];  // bounds of the rows of the first kRowPre row steps
 #pragma unroll
   for (int k = 0; k < kRowPre; ++k) {
-    const int32_t r = g.r0 + wave * 64 + lane + k * kPass;
+    const int32_t r = g.r0 + wave * 64 + lane + k * kThreads;
     pb[k] = r < g.r1 ? rp[r] : 0;
     pe[k] = r < g.r1 ? rp[r + 1] : 0;
   }
   if constexpr (kTable) {
-    // thread t holds run t (S <= kRowRuns == kPass): its length, and its first product's number from
-    // a workgroup scan kept in registers; then it writes its products' entries of the run table
-    static_assert(kRowRuns == kPass, "one thread per run");
+    // thread t holds run t (S <= kThreads): its length, and its first product's number from a
+    // workgroup scan kept in registers; then it writes its products' entries of the run table
     int32_t o = 0, n = 0;
     if (t < S) {
       o = t0[t];
@@ -706,18 +708,18 @@ __global__ __launch_bounds__(kPass) void spmv_tile_rows(
     __syncthreads();
     int32_t pre = incl - n, E = 0;
 #pragma unroll
-    for (int w = 0; w < kPassWaves; ++w) {
+    for (int w = 0; w < kWaves; ++w) {
       const int32_t v = wsum[w];
       if (w < wave) pre += v;
       E += v;
     }
-    E = min(E, kStage);
+    E = min(E, kSt);
     if (t < S) run_base[t] = o - pre;  // product li of run t is at run_base[t] + li
-    int16_t* run_of = reinterpret_cast<int16_t*>(stage);  // kStage int16 fit in half the stage
+    int16_t* run_of = reinterpret_cast<int16_t*>(stage);  // kSt int16 fit in half the stage
     for (int32_t li = pre; li < min(pre + n, E); ++li) run_of[li] = (int16_t)t;
     __syncthreads();
-    constexpr int kIt = kStage / kPass;
-    const int32_t nit = (E + kPass - 1) / kPass;
+    constexpr int kIt = kSt / kThreads;
+    const int32_t nit = (E + kThreads - 1) / kThreads;
     float pv[kIt];
     uint32_t dv[kIt];
     // buffer loads: 32-bit offsets on a scalar base (the plan keeps p below 4 GiB for this path)
@@ -726,8 +728,8 @@ __global__ __launch_bounds__(kPass) void spmv_tile_rows(
 #pragma unroll
     for (int k = 0; k < kIt; ++k) {
       pv[k] = 0.0f;
-      dv[k] = kStage;
-      const int32_t li = t + k * kPass;
+      dv[k] = kSt;
+      const int32_t li = t + k * kThreads;
       if (k < nit && li < E) {
         const uint32_t at = (uint32_t)(run_base[run_of[li]] + li);
         pv[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp4, at * 4u, 0, 0));
@@ -737,13 +739,13 @@ __global__ __launch_bounds__(kPass) void spmv_tile_rows(
     __syncthreads();  // every run_of read is done before the stage is overwritten
 #pragma unroll
     for (int k = 0; k < kIt; ++k)
-      if (k < nit && dv[k] < (uint32_t)kStage) stage[dv[k]] = pv[k];
+      if (k < nit && dv[k] < (uint32_t)kSt) stage[dv[k]] = pv[k];
   } else {
-    for (int s = wave; s < S; s += kPassWaves) {
+    for (int s = wave; s < S; s += kWaves) {
       const int32_t o = t0[s], n = t1[s] - o;
       for (int32_t k = lane; k < n; k += 64) {
         const uint32_t d = dest16[o + k];
-        if (d < (uint32_t)kStage) stage[d] = p[o + k];
+        if (d < (uint32_t)kSt) stage[d] = p[o + k];
       }
     }
   }
@@ -751,7 +753,7 @@ __global__ __launch_bounds__(kPass) void spmv_tile_rows(
   const int32_t gpos = t0[S];  // the giant row's entries (region S, CSR order)
   double dsum = 0.0;
   int it = 0;
-  for (int32_t rr = g.r0 + wave * 64; rr < g.r1; rr += kPass, ++it) {  // wave-uniform
+  for (int32_t rr = g.r0 + wave * 64; rr < g.r1; rr += kThreads, ++it) {  // wave-uniform
     const int32_t r = rr + lane;
     const bool in = r < g.r1;
     int32_t rb = 0, re = 0;
@@ -792,7 +794,7 @@ __global__ __launch_bounds__(kPass) void spmv_tile_rows(
     }
   }
   if (block_sums) {
-    const double tsum = dc::block_sum64<kPass>(dsum, red);
+    const double tsum = dc::block_sum64<kThreads>(dsum, red);
     if (t == 0) block_sums[b] = tsum;
   }
 }
@@ -814,6 +816,7 @@ struct dc_hip_spmv_plan {
   float *val_s = nullptr, *p = nullptr;
   int32_t *rp = nullptr, *tcnt = nullptr, *toff = nullptr, *tot = nullptr, *sbase = nullptr, *blk_row = nullptr;
   int4 *binfo = nullptr, *wrange = nullptr;
+  int32_t span = kSpanBig;  // block span in nonzeros
   int32_t nwg = 1;  // product-pass workgroups (one per CU)
   double *block_sums = nullptr, *scalars = nullptr;
 };
@@ -855,6 +858,12 @@ int32_t plan_shape(dc_hip_spmv_plan* p, int64_t rows, int64_t cols, int64_t nnz,
   p->nwg = std::max(1, cu_count);
   p->cols = cols;
   p->nnz = nnz;
+  // Blocks of 8192 nonzeros, or of 4096 when that still gives fewer than four blocks per CU:
+  // row-pass workgroups of half the size, four per CU, hide more of each block's two round trips
+  // (1M rows of 5.4 nonzeros: row pass 19.6 against 22.5 us; at 16M rows both spans take the same
+  // time and the larger one halves the plan's per-block tables and scatter work).
+  const int64_t rows_term = rows > 0 ? (rows - 1) / kBlockRows : 0;
+  p->span = nnz / kSpanBig + rows_term + 1 < 4 * (int64_t)p->nwg ? kSpanSmall : kSpanBig;
   int64_t W;
   if (slice_cols_max > 0) {
     W = std::min<int64_t>(slice_cols_max, kTileCols);
@@ -864,16 +873,16 @@ int32_t plan_shape(dc_hip_spmv_plan* p, int64_t rows, int64_t cols, int64_t nnz,
     // widest power of two up to kTileCols with W <= nnz / (2 nwg) keeps the tiles a small share
     // (at 1M rows of 5.4 nonzeros on 256 CUs: 8192 columns, 39.0 us per power step against 42.3
     // with 32768), but no narrower than kMinTileCols and wide enough for the row pass's LDS
-    // tables (at most kRowRuns slices) while that is possible.
+    // tables (at most span / 8 slices) while that is possible.
     W = kMinTileCols;
     const int64_t want = nnz / (2 * (int64_t)p->nwg);
-    while (W < kTileCols && (2 * W <= want || (cols + W - 1) / W > kRowRuns)) W *= 2;
+    while (W < kTileCols && (2 * W <= want || (cols + W - 1) / W > p->span / 8)) W *= 2;
   }
   if ((cols + W - 1) / W > kMaxSlices) W = (cols + kMaxSlices - 1) / kMaxSlices;
   const int64_t S = std::max<int64_t>(1, (cols + W - 1) / W);
   p->slices = (int32_t)S;
   p->slice_cols = W;
-  p->nblocks = (int32_t)(nnz / kBlockSpan + (rows > 0 ? (rows - 1) / kBlockRows : 0) + 1);
+  p->nblocks = (int32_t)(nnz / p->span + rows_term + 1);
   p->zcap = nnz + (S + 1) * kPad + kPad;
   // positions are int32 and the (slice, block) tables are indexed with int32 products of their sides
   if (p->zcap > INT32_MAX || (S + 1) * (int64_t)(p->nblocks + 1) > (int64_t{1} << 29)) return DC_ERR_UNSUPPORTED;
@@ -887,10 +896,11 @@ int32_t plan_build(dc_hip_ctx* ctx, dc_hip_spmv_plan* p, const int32_t* rp, cons
   const int32_t S = p->slices, nb = p->nblocks, nnz = (int32_t)p->nnz;
   const uint32_t width = (uint32_t)p->slice_cols, cols = (uint32_t)std::max<int64_t>(p->cols, 1);
   DC_RETURN_IF_HIP(hipMemcpyAsync(p->rp, rp, (size_t)(p->rows + 1) * 4, hipMemcpyDeviceToDevice, ctx->stream));
-  plan_blocks<<<(unsigned)((p->rows + 1 + 255) / 256), 256, 0, ctx->stream>>>(p->rp, p->rows, nnz, nb, p->blk_row);
+  plan_blocks<<<(unsigned)((p->rows + 1 + 255) / 256), 256, 0, ctx->stream>>>(p->rp, p->rows, nnz, nb, p->span,
+                                                                               p->blk_row);
   DC_RETURN_IF(dc::last_launch_status());
   plan_block_info<<<(unsigned)((nb + 255) / 256), 256, 0, ctx->stream>>>(p->rp, (int32_t)p->rows, nnz, p->blk_row,
-                                                                         nb, p->binfo);
+                                                                         nb, p->span, p->binfo);
   DC_RETURN_IF(dc::last_launch_status());
   const unsigned bgrid = (unsigned)(kXcds * ((nb + kXcds - 1) / kXcds));
 #define DC_TILE_COUNT(SM)                                                                                   \
@@ -930,13 +940,19 @@ int32_t plan_spmv(dc_hip_ctx* ctx, const dc_hip_spmv_plan* p, const float* x, fl
   DC_RETURN_IF(dc::last_launch_status());
   const unsigned bgrid = (unsigned)(kXcds * ((p->nblocks + kXcds - 1) / kXcds));
   double* bs = sums ? p->block_sums : nullptr;
-#define DC_TILE_ROWS(TABLE)                                                                                    \
-  spmv_tile_rows<TABLE><<<bgrid, kPass, 0, ctx->stream>>>(p->rp, (int32_t)p->nnz, p->binfo, p->nblocks, p->toff,  \
-                                                          p->slices, p->p, p->dest16, p->col16, p->val_s, x, cols, \
-                                                          y, bs, scale, (uint32_t)(p->zcap * 4))
+#define DC_TILE_ROWS(TABLE, SP)                                                                                 \
+  spmv_tile_rows<TABLE, SP><<<bgrid, SP / 8, 0, ctx->stream>>>(p->rp, (int32_t)p->nnz, p->binfo, p->nblocks, p->toff, \
+                                                               p->slices, p->p, p->dest16, p->col16, p->val_s, x,    \
+                                                               cols, y, bs, scale, (uint32_t)(p->zcap * 4))
   // the table path addresses the products with 32-bit byte offsets
-  if (p->slices <= kRowRuns && p->zcap * 4 <= (int64_t)UINT32_MAX) DC_TILE_ROWS(true);
-  else DC_TILE_ROWS(false);
+  const bool table = p->slices <= p->span / 8 && p->zcap * 4 <= (int64_t)UINT32_MAX;
+  if (p->span == kSpanSmall) {
+    if (table) DC_TILE_ROWS(true, kSpanSmall);
+    else DC_TILE_ROWS(false, kSpanSmall);
+  } else {
+    if (table) DC_TILE_ROWS(true, kSpanBig);
+    else DC_TILE_ROWS(false, kSpanBig);
+  }
 #undef DC_TILE_ROWS
   return dc::last_launch_status();
 }

@@ -392,8 +392,9 @@ DC_HIP_API int32_t dc_hip_spmv_power_iterate_f32(dc_hip_ctx* ctx, const int32_t*
  * owned by the plan), so the CSR arrays may be freed once the creating call's stream work has run.
  * Columns are cut into slices of at most `slice_cols_max` columns (at most 32768: a 128 KB tile
  * of x in one CU's LDS; 0 = the default, the widest power of two from 4096 to 32768 columns that
- * is at most nnz / (2 x the device's CU count), wide enough for at most 1024 slices where 32768
- * allows; widened when more than 32768 slices would be needed); every product val·x[col] is
+ * is at most nnz / (2 x the device's CU count), wide enough for at most 512 or 1024 slices (the
+ * row pass's LDS tables, by matrix size) where 32768 allows; widened when more than 32768 slices
+ * would be needed); every product val·x[col] is
  * formed once from an LDS tile, and each row is summed from its products in index order. Result: rows of at most 32 nonzeros equal the
  * sequential float32 row sum (0.0f + p_0 + p_1 + ...) bit for bit, whatever the slice count;
  * longer rows are summed in a fixed order (lane k of a wave adds products k, k + 64, ..., then a

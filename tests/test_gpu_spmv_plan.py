@@ -21,7 +21,7 @@ pytestmark = pytest.mark.gpu
 REL = 1e-4
 SEQ_ROW = 32          # rows up to this length are summed sequentially on the GPU
 TILE_COLS = 32768     # widest slice (one x tile in LDS)
-GIANT_ROW = 8192      # longer rows are summed with their products formed from x directly
+GIANT_ROW = 4096      # longer rows are summed with their products formed from x directly
 
 
 def upload_csr(ctx, rp, col, val):
@@ -33,16 +33,20 @@ def row_scale(rp, col, val, x):
     return oracle.spmv_csr_f64(rp, col, np.abs(val), np.abs(x).astype(np.float64))
 
 
-def expected_slices(cols, width, nnz=0):
+def expected_slices(cols, width, nnz=0, rows=None):
     """(slices, columns per slice) the plan picks: slice_cols_max capped at 32768, or by default
     the widest power of two in [4096, 32768] with w <= nnz / (2 * CUs), widened while more than
-    1024 slices would be needed; then widened when more than 32768 slices would be needed."""
+    span / 8 slices would be needed (span: the plan's block span, 4096 nonzeros when that gives
+    fewer than 4 blocks per CU, else 8192); then widened when more than 32768 slices would be
+    needed."""
     if width > 0:
         w = min(width, TILE_COLS)
     else:
         cus = max(1, hip.device_info(0).compute_units)
+        rows = cols if rows is None else rows
+        span = 4096 if nnz // 8192 + max(rows - 1, 0) // 16384 + 1 < 4 * cus else 8192
         w = 4096
-        while w < TILE_COLS and (2 * w <= nnz // (2 * cus) or -(-cols // w) > 1024):
+        while w < TILE_COLS and (2 * w <= nnz // (2 * cus) or -(-cols // w) > span // 8):
             w *= 2
     if -(-cols // w) > 32768:
         w = -(-cols // 32768)
@@ -106,13 +110,13 @@ def test_plan_slices_vs_oracle(ctx, rows, cols, width, slices):
         rp, col, val = oracle.gen_zipf_csr(rows, seed, max_degree=min(4096, cols - 1), cols=cols)
     x = oracle.gen_uniform_f32(cols, seed, 5, unit_interval=True)
     y, (s, w, nbytes) = run_plan(ctx, rp, col, val, x, width)
-    assert (s, w) == expected_slices(cols, width, col.size) and s == (slices or s) and nbytes > 0
+    assert (s, w) == expected_slices(cols, width, col.size, rows) and s == (slices or s) and nbytes > 0
     check(rp, col, val, x, y)
 
 
 def test_plan_signed_values_long_and_giant_rows(ctx):
     """Negative values; rows of 0 / 1 / 31-33 / 4096 / 3000 nonzeros; rows at the giant threshold
-    (8192 nonzeros: staged; 8193 and 40000: summed from x directly), each followed by more rows;
+    (4096 nonzeros: staged; 4097 and 40000: summed from x directly), each followed by more rows;
     empty rows exactly zero."""
     lens = [0, 1, 4096, 0, 3000, 7, 129, 128, 0, 600, 257, 256, 513, 512, 32, 33, 31, 64, 65,
             GIANT_ROW, 5, GIANT_ROW + 1, 0, 3, 40000, 2, 1, 0, 17]
@@ -123,7 +127,7 @@ def test_plan_signed_values_long_and_giant_rows(ctx):
     x = oracle.gen_uniform_f32(cols, 9, 1)
     for width in (0, 2500, 625, 3):
         y, (s, w, _) = run_plan(ctx, rp, col, val, x, width)
-        assert (s, w) == expected_slices(cols, width, col.size)
+        assert (s, w) == expected_slices(cols, width, col.size, rp.size - 1)
         check(rp, col, val, x, y)
         assert y[0] == 0 and y[3] == 0 and y[8] == 0 and y[22] == 0 and y[27] == 0
 
