@@ -221,9 +221,8 @@ int32_t check_csr(const int32_t* rp, const int32_t* col, const float* val, int64
 //   - columns are cut into slices of at most kTileCols columns (a 128 KB tile of x, one CU's LDS);
 //   - rows are cut into blocks: row r is in block rp[r] / span + r / kBlockRows (span = 4096 or
 //     8192 nonzeros, chosen per plan), so a block holds fewer than 2 span nonzeros unless it ends
-//     with a giant row (more than span
-//     nonzeros; at most one per block, always its last row: the next row starts past the block's
-//     span);
+//     with a giant row (more than span nonzeros; at most one per block, always its last row: the
+//     next row starts past the block's span);
 //   - the plan keeps a slice-major copy of the nonzeros: slice s holds, block after block, the
 //     nonzeros of block b whose column falls in s (the run (b, s)), each with its column within
 //     the slice (uint16), its value, and its position within the block's CSR range (uint16).
@@ -232,8 +231,8 @@ int32_t check_csr(const int32_t* rp, const int32_t* col, const float* val, int64
 // product pass: persistent workgroups split the slice-major entries evenly; a workgroup loads the
 //   x tile of each slice its share touches into LDS and streams p = val · x_tile[col16] (16-byte
 //   loads and stores).
-// row pass: a workgroup per block stages the block's products from its runs into LDS at their CSR
-//   positions, then sums each row: rows of at most kSeqRow nonzeros one lane each, sequentially in
+// row pass: a workgroup per block (span / 8 threads) stages the block's products from its runs
+//   into LDS at their CSR positions, then sums each row: rows of at most kSeqRow nonzeros one lane each, sequentially in
 //   index order (0.0f + p_0 + p_1 + ...: the reference's float32 row sum bit for bit), longer rows
 //   by the whole wave (lane k adds products k, k + 64, ... in order, then a fixed DPP tree); giant
 //   rows the same way with their products formed from x directly.
@@ -251,7 +250,7 @@ constexpr int kPass = 1024;               // threads per workgroup of the plan k
 constexpr int kPassWaves = kPass / 64;
 constexpr int kMaxSlices = 32768;         // (1 << 30) columns / kTileCols
 constexpr int kPad = 8;                   // slice regions start at multiples of 8 entries
-constexpr int kRowRuns = 1024;            // up to this many slices, the scatter stages through LDS
+constexpr int kScatterRuns = 1024;            // below this many slices, the scatter stages through LDS
 constexpr int kRowPre = 2;                // row pass: row steps whose bounds are loaded before staging
 constexpr int kXcds = 8;
 
@@ -471,7 +470,7 @@ __global__ __launch_bounds__(kPass) void plan_tile_bases(const int32_t* __restri
 
 // A5: the scatter. Run (b, s) starts at toff[b][s] = sbase[s] + its offset within the slice
 // (toff[nblocks][s] = the slice's end). A giant row's entries go to region S in CSR order, column
-// low half in col16 and high half in dest16. With kStaged (S < kRowRuns), the block's entries are
+// low half in col16 and high half in dest16. With kStaged (S < kScatterRuns), the block's entries are
 // first sorted by slice in LDS (the order within a slice is that of LDS atomics, which the results
 // do not depend on: every product is staged at its CSR position), then written run by run, the
 // lanes of a wave on consecutive positions (wave w takes runs w, w + 16, ...; their bounds sit in
@@ -585,8 +584,9 @@ __global__ __launch_bounds__(kPass) void plan_tile_scatter(
 
 // Product pass: p[i] = val_s[i] * x_tile[col16[i]] over the slice regions [0, sbase[S]). Workgroup
 // w takes the share wrange[w] (equal shares of whole kPad-entry groups); at each slice its share
-// enters it loads that slice's x tile into LDS (16 waves, 8 loads in flight per lane). With sum_out, workgroup 0 first
-// adds sums_in[0..nsums) in a fixed order (the power iteration's previous L1 norm).
+// enters it loads that slice's x tile into LDS (16 waves, 8 loads in flight per lane). With
+// sum_out, workgroup 0 first adds sums_in[0..nsums) in a fixed order (the power iteration's
+// previous L1 norm).
 __global__ __launch_bounds__(kPass) void spmv_tile_products(const uint16_t* __restrict__ col16,
                                                             const float* __restrict__ val_s,
                                                             const int32_t* __restrict__ sbase,
@@ -919,7 +919,7 @@ int32_t plan_build(dc_hip_ctx* ctx, dc_hip_spmv_plan* p, const int32_t* rp, cons
   plan_tile_scatter<SM, ST><<<bgrid, kPass, 0, ctx->stream>>>(col, val, p->binfo, nb, S, width, cols, p->tcnt,  \
                                                               p->tot, p->sbase, p->toff, p->col16, p->val_s,  \
                                                               p->dest16)
-  if (S < kRowRuns) DC_TILE_SCATTER(kRowRuns, true);
+  if (S < kScatterRuns) DC_TILE_SCATTER(kScatterRuns, true);
   else if (S + 1 <= 8192) DC_TILE_SCATTER(8192, false);
   else DC_TILE_SCATTER(kMaxSlices + 8, false);
 #undef DC_TILE_SCATTER
