@@ -162,6 +162,54 @@ def test_plan_equals_sequential_reference(ctx):
     assert np.array_equal(y[short].view(np.uint32), ref[short].view(np.uint32))
 
 
+def random_structure(kind, rows, cols, seed):
+    """CSR matrices of other shapes than the Zipf graph: uniform degrees, rows whose columns cluster
+    (several products of a row in one run), hub columns, and rows that are all hubs."""
+    rng = np.random.default_rng(seed)
+    if kind == "uniform":
+        deg = rng.integers(0, 65, rows)
+    else:
+        deg = rng.integers(0, 41, rows)
+    rp = np.concatenate([[0], np.cumsum(deg)]).astype(np.int32)
+    nnz = int(rp[-1])
+    if kind == "uniform":
+        col = rng.integers(0, cols, nnz)
+    elif kind == "clustered":
+        centre = np.repeat(rng.integers(0, cols, rows), deg)
+        col = np.clip(centre + rng.integers(-500, 501, nnz), 0, cols - 1)
+    else:  # hubs: 30% of the nonzeros point at 10 columns
+        col = rng.integers(0, cols, nnz)
+        hub = rng.random(nnz) < 0.3
+        col[hub] = rng.integers(0, 10, int(hub.sum())) * (cols // 10)
+    val = (rng.standard_normal(nnz)).astype(np.float32)
+    return rp, col.astype(np.int32), val
+
+
+@pytest.mark.parametrize("kind,rows,cols", [("uniform", 100_000, 300_000), ("clustered", 200_000, 200_000),
+                                            ("hubs", 150_000, 1_000_000)])
+def test_plan_random_structures(ctx, kind, rows, cols):
+    rp, col, val = random_structure(kind, rows, cols, rows + cols)
+    x = oracle.gen_uniform_f32(cols, 11, 2)
+    for width in (0, 2048):
+        y, (s, w, _) = run_plan(ctx, rp, col, val, x, width)
+        assert (s, w) == expected_slices(cols, width, col.size, rows)
+        check(rp, col, val, x, y)
+
+
+def test_plan_large_blocks_equal_sequential_reference(ctx):
+    """A matrix with enough nonzeros for 8192-nonzero blocks and 1024-thread row-pass workgroups
+    (2M rows of the Zipf graph, 10.8M nonzeros): rows of at most 32 nonzeros are the sequential
+    float32 row sum bit for bit, the rest within the tolerance."""
+    rows = 2_000_000
+    rp, col, val = oracle.gen_zipf_csr(rows, 5)
+    cus = max(1, hip.device_info(0).compute_units)
+    assert col.size // 8192 + (rows - 1) // 16384 + 1 >= 4 * cus, "the case must take the 8192 span"
+    x = oracle.gen_uniform_f32(rows, 5, 5, unit_interval=True)
+    y, (s, w, _) = run_plan(ctx, rp, col, val, x, 0)
+    assert (s, w) == expected_slices(rows, 0, col.size, rows)
+    check(rp, col, val, x, y)
+
+
 @pytest.mark.parametrize("width,slices", [(0, None), (1 << 15, 31), (1 << 12, 245), (1000, 1000)])
 def test_plan_1m_many_slices(ctx, width, slices):
     rows = 1_000_000
