@@ -153,7 +153,7 @@ def bench_spmv(ctx, log, time_launches, roofline, hbm_peak, sizes=(1_000_000, 16
         ms1 = time_launches(ctx, single, 10)
         spmv_bytes = 8 * nnz + 4 * (rows + 1) + 4 * rows + 4 * rows
         gbs1 = spmv_bytes / (ms1 * 1e-3) / 1e9
-        # the column-sliced plan: analysis once, then SpMV through it
+        # the tiled plan: analysis once, then SpMV through it
         t_build = ctx.event(), ctx.event()
         t_build[0].record()
         plan = ctx.spmv_plan(drp, dcol, dval, rows, rows, nnz)

@@ -30,7 +30,7 @@ struct dc_hip_ctx {
   int32_t* spmv_windows = nullptr;  // first row of each nonzero window
   size_t spmv_windows_cap = 0;
   double* scalars = nullptr;  // 64 doubles
-  // Device memory of the column-sliced SpMV plan built by dc_hip_spmv_power_iterate_f32 (grows).
+  // Device memory of the tiled SpMV plan built by dc_hip_spmv_power_iterate_f32 (grows).
   void* spmv_plan_mem = nullptr;
   size_t spmv_plan_bytes = 0;
 

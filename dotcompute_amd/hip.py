@@ -412,7 +412,7 @@ class Context:
 
 
 class SpmvPlan:
-    """Column-sliced SpMV plan (dc_hip_spmv_plan_*): built once, executed many times."""
+    """Tiled SpMV plan (dc_hip_spmv_plan_*): built once, executed many times."""
 
     def __init__(self, ctx: "Context", handle, rows: int, cols: int):
         self.ctx, self.handle, self.rows, self.cols = ctx, handle, rows, cols
