@@ -472,9 +472,10 @@ __global__ __launch_bounds__(kPass) void plan_tile_bases(const int32_t* __restri
 // (toff[nblocks][s] = the slice's end). A giant row's entries go to region S in CSR order, column
 // low half in col16 and high half in dest16. With kStaged (S < kScatterRuns), the block's entries are
 // first sorted by slice in LDS (the order within a slice is that of LDS atomics, which the results
-// do not depend on: every product is staged at its CSR position), then written run by run, the
-// lanes of a wave on consecutive positions (wave w takes runs w, w + 16, ...; their bounds sit in
-// its lanes' registers); otherwise each entry is written where its atomic cursor lands.
+// do not depend on: every product is staged at its CSR position), then written out with the
+// threads on consecutive local positions li: the run holding li is first_k[li / 64] plus the run
+// starts in (64 (li / 64), li] (a bitmap of run starts), and nz_gb of that run maps li to its global
+// position; otherwise each entry is written where its atomic cursor lands.
 template <int SMAX, bool kStaged>
 __global__ __launch_bounds__(kPass) void plan_tile_scatter(
     const int32_t* __restrict__ col, const float* __restrict__ val, const int4* __restrict__ binfo,
@@ -482,17 +483,21 @@ __global__ __launch_bounds__(kPass) void plan_tile_scatter(
     const int32_t* __restrict__ tot, const int32_t* __restrict__ sbase, int32_t* __restrict__ toff,
     uint16_t* __restrict__ col16, float* __restrict__ val_s, uint16_t* __restrict__ dest16) {
   __shared__ int32_t cur[SMAX];
-  __shared__ int32_t gbase[kStaged ? SMAX : 1];
-  __shared__ int32_t lpre[kStaged ? SMAX : 1];
+  __shared__ int32_t nz_gb[kStaged ? SMAX : 1];              // k-th non-empty run: global base - local start
+  __shared__ uint32_t starts[kStaged ? kStage / 32 : 1];     // bit li: a non-empty run starts at li
+  __shared__ int32_t first_k[kStaged ? kStage / 64 : 1];     // the run holding local position 64c
   __shared__ uint32_t st_cd[kStaged ? kStage : 1];
   __shared__ float st_v[kStaged ? kStage : 1];
   __shared__ int32_t wsum[kPassWaves];
+  __shared__ int32_t wcnt[kPassWaves];
   const int32_t b = xcd_block(nblocks);
   if (b < 0) return;  // whole workgroup
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int32_t S1 = S + 1;
   int32_t n = 0;  // kStaged: thread t's run length (t < S)
+  if constexpr (kStaged)
+    for (int i = t; i < kStage / 32; i += kPass) starts[i] = 0;
   for (int s = t; s <= S; s += kPass) {
     const int32_t o = sbase[s] + tcnt[(int64_t)s * nblocks + b];
     const int32_t next = b + 1 < nblocks ? sbase[s] + tcnt[(int64_t)s * nblocks + b + 1] : sbase[s] + tot[s];
@@ -507,19 +512,30 @@ __global__ __launch_bounds__(kPass) void plan_tile_scatter(
     // local slice-major numbering: thread t (run t) takes its first local position from a scan
     static_assert(SMAX <= kPass, "one thread per run");
     const int32_t incl = wave_incl_scan(n);
-    if (lane == 63) wsum[wave] = incl;
+    const uint64_t ne = __ballot(n > 0);
+    if (lane == 63) {
+      wsum[wave] = incl;
+      wcnt[wave] = __builtin_popcountll(ne);
+    }
     __syncthreads();
     int32_t pre = incl - n;
+    int32_t k = __builtin_popcountll(ne & ((1ull << lane) - 1));  // non-empty runs before run t
 #pragma unroll
     for (int w = 0; w < kPassWaves; ++w) {
       const int32_t v = wsum[w];
-      if (w < wave) pre += v;
+      if (w < wave) {
+        pre += v;
+        k += wcnt[w];
+      }
       E += v;
     }
     E = min(E, kStage);
     if (t < S) {
-      gbase[t] = cur[t] - pre;  // local position li of run t goes to gbase[t] + li
-      lpre[t] = pre;
+      if (n > 0 && pre < kStage) {
+        nz_gb[k] = cur[t] - pre;  // local position li of run t goes to nz_gb[k] + li
+        atomicOr(&starts[pre >> 5], 1u << (pre & 31));
+        for (int32_t c = (pre + 63) >> 6; c < kStage / 64 && (c << 6) < pre + n; ++c) first_k[c] = k;
+      }
       cur[t] = pre;
     }
   }
@@ -554,23 +570,16 @@ __global__ __launch_bounds__(kPass) void plan_tile_scatter(
   }
   __syncthreads();
   if constexpr (kStaged) {
-    const int s = lane * kPassWaves + wave;  // this lane's run
-    int32_t lo = 0, hi = 0, gb = 0;
-    if (s < S) {
-      lo = lpre[s];
-      hi = min(cur[s], E);  // the cursor ends at the run's end
-      gb = gbase[s];
-    }
-    for (uint64_t m = __ballot(lo < hi); m; m &= m - 1) {  // wave-uniform
-      const int L = __builtin_ctzll(m);
-      const int32_t rlo = __builtin_amdgcn_readlane(lo, L), rhi = __builtin_amdgcn_readlane(hi, L);
-      const int32_t rgb = __builtin_amdgcn_readlane(gb, L);
-      for (int32_t li = rlo + lane; li < rhi; li += 64) {
-        const uint32_t cd = st_cd[li];
-        col16[rgb + li] = (uint16_t)(cd & 0xFFFFu);
-        dest16[rgb + li] = (uint16_t)(cd >> 16);
-        val_s[rgb + li] = st_v[li];
-      }
+    for (int32_t li = t; li < E; li += kPass) {
+      const int32_t c = li >> 6;
+      const uint64_t word = (uint64_t)starts[2 * c] | ((uint64_t)starts[2 * c + 1] << 32);
+      const uint64_t below = (2ull << lane) - 1;  // bits 0..lane (lane 63: all)
+      const int32_t k = first_k[c] + __builtin_popcountll(word & below & ~1ull);
+      const int32_t dst = nz_gb[k] + li;
+      const uint32_t cd = st_cd[li];
+      col16[dst] = (uint16_t)(cd & 0xFFFFu);
+      dest16[dst] = (uint16_t)(cd >> 16);
+      val_s[dst] = st_v[li];
     }
   }
   const int32_t gpos = cur[S];  // the giant row's run (no atomic moves cur[S])
