@@ -97,6 +97,9 @@ def main() -> int:
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only", default="",
                     help="comma list of extras to run (sum,linq_sum,linq_minmax,vector_add,gemm,spmv,cache,orchestrator)")
+    ap.add_argument("--vendor-gemm", action="store_true",
+                    help="also time torch.mm (ROCm's BLAS kernels) on the GEMM legs' shapes, as `vendor` in each "
+                         "GEMM leg (imports torch: the first import on a fresh machine can take minutes)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one 1 GiB device-to-device copy, the known-size reference for the HBM byte "
                          "counters (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) that give roofline.traffic")
@@ -105,6 +108,13 @@ def main() -> int:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
               file=sys.stderr)
         return 2
+
+    vendor = None
+    if args.vendor_gemm and not args.skip_extras and (not args.only or "gemm" in args.only.split(",")):
+        from bench_extras import vendor_gemm_run  # noqa: E402
+
+        log("[bench] vendor GEMM timing (torch.mm) in a child process, before this process uses the GPU")
+        vendor = vendor_gemm_run(LEG_WARM_MS)
 
     from dotcompute_amd import hip
 
@@ -146,6 +156,10 @@ def main() -> int:
         for leg in ("gemm_f32_8192", "gemm_bf16_8192"):
             if leg in extra:
                 extra[leg]["roofline"]["traffic"] = measured_traffic("gemm_f32_bf16_8192.md", leg)
+        if vendor is not None:
+            from bench_extras import attach_vendor  # noqa: E402
+
+            attach_vendor(extra, vendor, log)
     # ---------------- CSR SpMV x20 ---------------------------------------------------------------
     if want("spmv"):
         from bench_extras import bench_spmv  # noqa: E402

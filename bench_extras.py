@@ -106,6 +106,81 @@ def bench_gemm(ctx, log, time_launches, roofline, fp32_peak, bf16_peak, sizes=(1
     return out
 
 
+def vendor_gemm_times(sizes, warm_ms: float) -> list:
+    """torch.mm on the GEMM legs' shapes (fp32, and bf16 inputs with an fp32 result at the largest
+    size): ROCm's own BLAS kernels, which torch dispatches to. Timed like the legs: untimed launches
+    until the device has been busy for `warm_ms`, then HIP events around back-to-back launches on
+    torch's stream. Uniform [0, 1) inputs; the products are not checked (they are not this
+    library's). Runs in a process of its own (see vendor_gemm_run)."""
+    import torch
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(42)
+
+    def timed(fn, iters):
+        t0 = time.perf_counter()
+        for _ in range(1000):
+            fn()
+            torch.cuda.synchronize()
+            if (time.perf_counter() - t0) * 1e3 >= warm_ms:
+                break
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        e1.synchronize()
+        return e0.elapsed_time(e1) / iters
+
+    res = []
+    for n in sizes:
+        a = torch.rand(n, n, device=dev, generator=g)
+        b = torch.rand(n, n, device=dev, generator=g)
+        c = torch.empty(n, n, device=dev)
+        cases = [(f"gemm_f32_{n}", lambda: torch.mm(a, b, out=c), "torch.mm fp32")]
+        if n == sizes[-1]:
+            ab, bb = a.bfloat16(), b.bfloat16()
+            cases.append((f"gemm_bf16_{n}", lambda: torch.mm(ab, bb, out_dtype=torch.float32),
+                          "torch.mm bf16 inputs, out_dtype float32"))
+        for leg, fn, what in cases:
+            ms = timed(fn, 20 if n <= 4096 else 10)
+            res.append({"leg": leg, "call": what, "torch": torch.__version__, "ms": round(ms, 4),
+                        "TFLOP/s": round(2.0 * n ** 3 / (ms * 1e-3) / 1e12, 2)})
+        del a, b, c
+    torch.cuda.synchronize()
+    return res
+
+
+def vendor_gemm_run(warm_ms: float, sizes=(1024, 4096, 8192)) -> list:
+    """torch.mm's times on the GEMM legs' shapes (vendor_gemm_times), run in a child process (this
+    file run as a script) that the caller starts before it touches the GPU itself: torch brings its
+    own HIP runtime, which does not find the device once this library's runtime holds it in the
+    same process."""
+    import json
+    import subprocess
+    import sys
+
+    cmd = [sys.executable, os.path.abspath(__file__), "--vendor-gemm", ",".join(map(str, sizes)), str(warm_ms)]
+    p = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
+    if p.returncode != 0:
+        raise RuntimeError(f"vendor GEMM timing failed (exit {p.returncode}): {p.stderr[-2000:]}")
+    return json.loads(p.stdout.strip().splitlines()[-1])
+
+
+def attach_vendor(out: dict, res: list, log) -> None:
+    """Record each torch.mm time beside its GEMM leg as `vendor`, a reference point for this
+    library's kernels (this_over_vendor_time < 1: this library's kernel is faster)."""
+    for v in res:
+        v = dict(v)
+        leg = v.pop("leg")
+        if leg in out:
+            v["this_over_vendor_time"] = round(out[leg]["ms"] / v["ms"], 3)
+            out[leg]["vendor"] = v
+        log(f"[bench] vendor {leg}: {v['ms']:.3f} ms -> {v['TFLOP/s']:.1f} TFLOP/s ({v['call']})")
+
+
 def spmv_cpu_baseline(rp, col, val, rows: int, iters: int, per_iter_bytes: int, log) -> dict:
     """SparseMatrix.Multiply's row loop followed by the L1 normalisation (oracle restatement, one
     thread) on the same CSR matrix and start vector. Above 10M non-zeros one iteration is timed and
@@ -281,3 +356,13 @@ def bench_orchestrator(log, cpu: bool = True) -> dict:
                                            "CPU invoker loop over the same host arrays (the reference's CPU path "
                                            "adds a Task.Run around it)", higher_is_better=False)
     return {"vector_add_100K_orchestrator_e2e": leg}
+
+
+if __name__ == "__main__":
+    import json
+    import sys
+
+    if len(sys.argv) == 4 and sys.argv[1] == "--vendor-gemm":
+        print(json.dumps(vendor_gemm_times(tuple(int(v) for v in sys.argv[2].split(",")), float(sys.argv[3]))))
+    else:
+        sys.exit("usage: bench_extras.py --vendor-gemm SIZES WARM_MS (bench.py runs it)")
