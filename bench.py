@@ -97,9 +97,10 @@ def main() -> int:
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only", default="",
                     help="comma list of extras to run (sum,linq_sum,linq_minmax,vector_add,gemm,spmv,cache,orchestrator)")
-    ap.add_argument("--vendor-gemm", action="store_true",
-                    help="also time torch.mm (ROCm's BLAS kernels) on the GEMM legs' shapes, as `vendor` in each "
-                         "GEMM leg (imports torch: the first import on a fresh machine can take minutes)")
+    ap.add_argument("--vendor", action="store_true",
+                    help="also time the same operations composed from torch's ops (hipBLASLt for MatMul), as "
+                         "`vendor` beside the headline and the GEMM / Sum / VectorAdd legs (imports torch in a "
+                         "child process: the first import on a fresh machine can take minutes)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one 1 GiB device-to-device copy, the known-size reference for the HBM byte "
                          "counters (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) that give roofline.traffic")
@@ -110,11 +111,11 @@ def main() -> int:
         return 2
 
     vendor = None
-    if args.vendor_gemm and not args.skip_extras and (not args.only or "gemm" in args.only.split(",")):
-        from bench_extras import vendor_gemm_run  # noqa: E402
+    if args.vendor:
+        from bench_extras import vendor_run  # noqa: E402
 
-        log("[bench] vendor GEMM timing (torch.mm) in a child process, before this process uses the GPU")
-        vendor = vendor_gemm_run(LEG_WARM_MS)
+        log("[bench] vendor timing (torch) in a child process, before this process uses the GPU")
+        vendor = vendor_run(LEG_WARM_MS)
 
     from dotcompute_amd import hip
 
@@ -156,10 +157,6 @@ def main() -> int:
         for leg in ("gemm_f32_8192", "gemm_bf16_8192"):
             if leg in extra:
                 extra[leg]["roofline"]["traffic"] = measured_traffic("gemm_f32_bf16_8192.md", leg)
-        if vendor is not None:
-            from bench_extras import attach_vendor  # noqa: E402
-
-            attach_vendor(extra, vendor, log)
     # ---------------- CSR SpMV x20 ---------------------------------------------------------------
     if want("spmv"):
         from bench_extras import bench_spmv  # noqa: E402
@@ -333,6 +330,14 @@ def main() -> int:
         del hx
 
     ctx.close()
+    head_vendor = None
+    if vendor is not None:
+        from bench_extras import attach_vendor  # noqa: E402
+
+        attach_vendor(extra, vendor, log)
+        head_vendor = next(dict(v) for v in vendor if v["leg"] == "headline")
+        head_vendor.pop("leg")
+        head_vendor["this_over_vendor_time"] = round(ms_per_step / head_vendor["ms"], 3)
     if want("orchestrator"):
         from bench_extras import bench_orchestrator  # noqa: E402
 
@@ -358,6 +363,8 @@ def main() -> int:
         "cpu_baseline": cpu,
         "extra": extra,
     }
+    if head_vendor is not None:
+        result["vendor"] = head_vendor
     print(json.dumps(result), flush=True)
     return 0
 

@@ -106,12 +106,16 @@ def bench_gemm(ctx, log, time_launches, roofline, fp32_peak, bf16_peak, sizes=(1
     return out
 
 
-def vendor_gemm_times(sizes, warm_ms: float) -> list:
-    """torch.mm on the GEMM legs' shapes (fp32, and bf16 inputs with an fp32 result at the largest
-    size): ROCm's own BLAS kernels, which torch dispatches to. Timed like the legs: untimed launches
-    until the device has been busy for `warm_ms`, then HIP events around back-to-back launches on
-    torch's stream. Uniform [0, 1) inputs; the products are not checked (they are not this
-    library's). Runs in a process of its own (see vendor_gemm_run)."""
+def vendor_times(warm_ms: float, gemm_sizes=(1024, 4096, 8192), n_stream: int = 1 << 28) -> list:
+    """The same operations composed from torch's own ops, which run ROCm's vendor kernels (hipBLASLt
+    for torch.mm, torch's HIP kernels for the rest), as a reference point for this library's
+    kernels: torch.mm on the GEMM legs' shapes (fp32, and bf16 inputs with an fp32 result at the
+    largest size), and at n_stream float32 elements (uniform [-1, 1)) `x[x > 0] * 2 + 1` (the
+    headline ToArray; the boolean index waits for its count on the host, as torch's must),
+    `x.sum()`, `torch.where(x > 0, x * 2 + 1, 0).sum()` and `torch.add(a, b, out=c)`. Timed like
+    the legs: untimed calls until the device has been busy for `warm_ms`, then HIP events around
+    back-to-back calls on torch's stream. The results are not checked (they are not this
+    library's). Runs in a process of its own (see vendor_run)."""
     import torch
 
     torch.backends.cuda.matmul.allow_tf32 = False
@@ -135,12 +139,12 @@ def vendor_gemm_times(sizes, warm_ms: float) -> list:
         return e0.elapsed_time(e1) / iters
 
     res = []
-    for n in sizes:
+    for n in gemm_sizes:
         a = torch.rand(n, n, device=dev, generator=g)
         b = torch.rand(n, n, device=dev, generator=g)
         c = torch.empty(n, n, device=dev)
         cases = [(f"gemm_f32_{n}", lambda: torch.mm(a, b, out=c), "torch.mm fp32")]
-        if n == sizes[-1]:
+        if n == gemm_sizes[-1]:
             ab, bb = a.bfloat16(), b.bfloat16()
             cases.append((f"gemm_bf16_{n}", lambda: torch.mm(ab, bb, out_dtype=torch.float32),
                           "torch.mm bf16 inputs, out_dtype float32"))
@@ -149,36 +153,51 @@ def vendor_gemm_times(sizes, warm_ms: float) -> list:
             res.append({"leg": leg, "call": what, "torch": torch.__version__, "ms": round(ms, 4),
                         "TFLOP/s": round(2.0 * n ** 3 / (ms * 1e-3) / 1e12, 2)})
         del a, b, c
+    n = n_stream
+    x = torch.rand(n, device=dev, generator=g).mul_(2.0).sub_(1.0)
+    kept = int((x > 0).sum().item())
+    y = torch.rand(n, device=dev, generator=g)
+    z = torch.empty(n, device=dev)
+    for leg, fn, what, nbytes in (
+            ("headline", lambda: x[x > 0] * 2 + 1, "x[x > 0] * 2 + 1", 4 * n + 4 * kept),
+            ("sum_f32_256M", lambda: x.sum(), "x.sum()", 4 * n),
+            ("where_select_sum_f32_256M", lambda: torch.where(x > 0, x * 2 + 1, 0).sum(),
+             "torch.where(x > 0, x * 2 + 1, 0).sum()", 4 * n),
+            ("vector_add_f32_256M", lambda: torch.add(x, y, out=z), "torch.add(a, b, out=c)", 12 * n)):
+        ms = timed(fn, 20)
+        res.append({"leg": leg, "call": what, "torch": torch.__version__, "ms": round(ms, 4),
+                    "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)})
+    del x, y, z
     torch.cuda.synchronize()
     return res
 
 
-def vendor_gemm_run(warm_ms: float, sizes=(1024, 4096, 8192)) -> list:
-    """torch.mm's times on the GEMM legs' shapes (vendor_gemm_times), run in a child process (this
-    file run as a script) that the caller starts before it touches the GPU itself: torch brings its
-    own HIP runtime, which does not find the device once this library's runtime holds it in the
-    same process."""
+def vendor_run(warm_ms: float) -> list:
+    """vendor_times in a child process (this file run as a script) that the caller starts before it
+    touches the GPU itself: torch brings its own HIP runtime, which does not find the device once
+    this library's runtime holds it in the same process."""
     import json
     import subprocess
     import sys
 
-    cmd = [sys.executable, os.path.abspath(__file__), "--vendor-gemm", ",".join(map(str, sizes)), str(warm_ms)]
+    cmd = [sys.executable, os.path.abspath(__file__), "--vendor", str(warm_ms)]
     p = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
     if p.returncode != 0:
-        raise RuntimeError(f"vendor GEMM timing failed (exit {p.returncode}): {p.stderr[-2000:]}")
+        raise RuntimeError(f"vendor timing failed (exit {p.returncode}): {p.stderr[-2000:]}")
     return json.loads(p.stdout.strip().splitlines()[-1])
 
 
 def attach_vendor(out: dict, res: list, log) -> None:
-    """Record each torch.mm time beside its GEMM leg as `vendor`, a reference point for this
-    library's kernels (this_over_vendor_time < 1: this library's kernel is faster)."""
+    """Record each vendor time beside its leg of `out` as `vendor` (this_over_vendor_time < 1: this
+    library is faster); the `headline` entry is left to the caller."""
     for v in res:
         v = dict(v)
         leg = v.pop("leg")
         if leg in out:
             v["this_over_vendor_time"] = round(out[leg]["ms"] / v["ms"], 3)
             out[leg]["vendor"] = v
-        log(f"[bench] vendor {leg}: {v['ms']:.3f} ms -> {v['TFLOP/s']:.1f} TFLOP/s ({v['call']})")
+        rate = f"{v['TFLOP/s']:.1f} TFLOP/s" if "TFLOP/s" in v else f"{v['GB/s']:.0f} GB/s"
+        log(f"[bench] vendor {leg}: {v['ms']:.3f} ms -> {rate} ({v['call']})")
 
 
 def spmv_cpu_baseline(rp, col, val, rows: int, iters: int, per_iter_bytes: int, log) -> dict:
@@ -362,7 +381,7 @@ if __name__ == "__main__":
     import json
     import sys
 
-    if len(sys.argv) == 4 and sys.argv[1] == "--vendor-gemm":
-        print(json.dumps(vendor_gemm_times(tuple(int(v) for v in sys.argv[2].split(",")), float(sys.argv[3]))))
+    if len(sys.argv) == 3 and sys.argv[1] == "--vendor":
+        print(json.dumps(vendor_times(float(sys.argv[2]))))
     else:
-        sys.exit("usage: bench_extras.py --vendor-gemm SIZES WARM_MS (bench.py runs it)")
+        sys.exit("usage: bench_extras.py --vendor WARM_MS (bench.py --vendor runs it)")
