@@ -284,8 +284,9 @@ def main() -> int:
         f"-> {achieved:.0f} GB/s")
 
     # ---------------- what the same memory can do in this run: the ceilings beside the peak -----
-    # a 1 GiB device-to-device copy (read 1 GiB + write 1 GiB), and the headline kernel with every
-    # element kept (x > -2f: read 1 GiB + write 1 GiB) and with none kept (x > 2f: read only)
+    # a 1 GiB device-to-device copy through hipMemcpyAsync (read 1 GiB + write 1 GiB), and the
+    # headline kernel with every element kept (x > -2f: read 1 GiB + write 1 GiB) and with none
+    # kept (x > 2f: read only)
     ceiling = {}
     cp = lambda: hip.check(hip.load().dc_hip_memcpy_d2d_async(ctx.handle, out.ptr, x.ptr, 4 * n), "d2d copy")
     ms_cp = time_launches(ctx, cp, 20, warm_ms=LEG_WARM_MS)
@@ -297,11 +298,23 @@ def main() -> int:
         g = lambda: ctx.where_select_f32(ch, x, out, cnt, n)
         ms_g = time_launches(ctx, g, 20, warm_ms=LEG_WARM_MS)
         ceiling[f"to_array_{name}_256M"] = {"ms": round(ms_g, 4), "GB/s": round((4 * n + wbytes) / (ms_g * 1e-3) / 1e9, 1)}
-    copy_gbs = ceiling["d2d_copy_1GiB"]["GB/s"]
+    # plain streaming kernels (one 16-byte vector per thread over a covering grid): a copy, the
+    # headline's own mix at half kept (read 1 GiB, write 512 MiB) and a read of 1 GiB
+    for name, kind, nbytes in (("stream_copy_1GiB", hip.PROBE_COPY, 8 * n),
+                               ("stream_read1GiB_write512MiB", hip.PROBE_READ2_WRITE1, 6 * n),
+                               ("stream_read_1GiB", hip.PROBE_READ, 4 * n)):
+        pf = lambda: ctx.stream_probe(kind, x, out, n)
+        ms_p = time_launches(ctx, pf, 20, warm_ms=LEG_WARM_MS)
+        ceiling[name] = {"ms": round(ms_p, 4), "GB/s": round(nbytes / (ms_p * 1e-3) / 1e9, 1)}
+    copy_gbs = ceiling["stream_copy_1GiB"]["GB/s"]
+    mix_gbs = ceiling["stream_read1GiB_write512MiB"]["GB/s"]
     ceiling["frac_of_copy"] = round(achieved / copy_gbs, 4)
-    log(f"[bench] ceilings: copy {copy_gbs:.0f} GB/s, all-kept ToArray {ceiling['to_array_all_kept_256M']['GB/s']:.0f} "
-        f"GB/s, none-kept {ceiling['to_array_none_kept_256M']['GB/s']:.0f} GB/s; headline = "
-        f"{100 * ceiling['frac_of_copy']:.1f}% of the copy")
+    ceiling["frac_of_same_mix"] = round(achieved / mix_gbs, 4)
+    log(f"[bench] ceilings: hipMemcpy d2d {ceiling['d2d_copy_1GiB']['GB/s']:.0f} GB/s, copy kernel {copy_gbs:.0f} GB/s, "
+        f"read 1 GiB + write 512 MiB {mix_gbs:.0f} GB/s ({ceiling['stream_read1GiB_write512MiB']['ms'] * 1e3:.1f} us), "
+        f"read {ceiling['stream_read_1GiB']['GB/s']:.0f} GB/s; all-kept ToArray "
+        f"{ceiling['to_array_all_kept_256M']['GB/s']:.0f} GB/s, none-kept {ceiling['to_array_none_kept_256M']['GB/s']:.0f} "
+        f"GB/s; headline = {100 * ceiling['frac_of_same_mix']:.1f}% of the same mix")
     ctx.free(out)
     ctx.free(x)
 

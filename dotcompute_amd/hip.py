@@ -15,6 +15,7 @@ import numpy as np
 PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.path.join(PKG, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libdotcompute_hip.so")
+PROBE_COPY, PROBE_READ2_WRITE1, PROBE_READ = 0, 1, 2  # dc_hip_stream_probe kinds
 HEADER = os.path.join(os.path.dirname(PKG), "include", "dotcompute_hip.h")
 
 DC_OK = 0
@@ -133,6 +134,7 @@ SIGNATURES: dict[str, list] = {
     "dc_hip_memcpy_d2h_async": [_P, _P, _P, _sz],
     "dc_hip_memcpy_d2d_async": [_P, _P, _P, _sz],
     "dc_hip_memset_async": [_P, _P, _i32, _sz],
+    "dc_hip_stream_probe": [_P, _i32, _P, _P, _i64],
     "dc_hip_mem_info": [_P, C.POINTER(_sz), C.POINTER(_sz)],
     "dc_hip_event_create": [_P, _PP],
     "dc_hip_event_destroy": [_P],
@@ -341,6 +343,10 @@ class Context:
     def vector_add_f32(self, a: DeviceArray, b: DeviceArray, r: DeviceArray, n: int | None = None) -> None:
         n = r.size if n is None else n
         check(load().dc_hip_vector_add_f32(self.handle, a.ptr, b.ptr, r.ptr, n), "dc_hip_vector_add_f32")
+
+    def stream_probe(self, kind: int, src: DeviceArray, dst: DeviceArray, n: int) -> None:
+        """Measurement-only streaming probe (PROBE_COPY / PROBE_READ2_WRITE1 / PROBE_READ)."""
+        check(load().dc_hip_stream_probe(self.handle, kind, src.ptr, dst.ptr, n), "dc_hip_stream_probe")
 
     def reduce_sum_f32(self, x: DeviceArray, out: DeviceArray, n: int | None = None) -> None:
         n = x.size if n is None else n

@@ -202,6 +202,22 @@ DC_HIP_API int32_t dc_hip_vector_add_f32(dc_hip_ctx* ctx, const float* a, const 
                                          float* result, int64_t n);
 
 /* ---------------------------------------------------------------------------------------------
+ * Streaming probes — measurement only, no counterpart in the reference: what plain streaming
+ * kernels reach on this device for a given read/write mix, the ceilings the benchmark reports
+ * beside the fused kernels. One 16-byte vector per thread over a grid that covers the input
+ * (1024-thread workgroups), non-temporal loads and stores. `n` floats, a multiple of 8; `src` and
+ * `dst` 16-byte aligned (DC_ERR_MISALIGNED otherwise).
+ *   DC_PROBE_COPY:           dst[i] = src[i], i < n                    (reads 4n B, writes 4n B)
+ *   DC_PROBE_READ2_WRITE1:   dst[i] = src[i] + src[n/2 + i], i < n/2   (reads 4n B, writes 2n B)
+ *   DC_PROBE_READ:           reads src[0, n) and writes nothing (each value is compared with
+ *                            a NaN passed at run time, which never compares equal)  (reads 4n B)
+ * ------------------------------------------------------------------------------------------- */
+#define DC_PROBE_COPY 0
+#define DC_PROBE_READ2_WRITE1 1
+#define DC_PROBE_READ 2
+DC_HIP_API int32_t dc_hip_stream_probe(dc_hip_ctx* ctx, int32_t kind, const float* src, float* dst, int64_t n);
+
+/* ---------------------------------------------------------------------------------------------
  * Sum reductions (deterministic: fixed per-thread order, fixed tree, last-block combine).
  * f32: accumulated in float64, result written as a double; the managed caller casts to float,
  *      as Enumerable.Sum(IEnumerable<float>) does (reached from

@@ -297,3 +297,37 @@ def test_sum_256m_f32_and_i32(ctx):
     assert oi.to_host()[0] == oracle.sum_i32_exact(xi)
     for a in (out, di, oi, ovf):
         ctx.free(a)
+
+
+# ---------------------------------------------------------------- streaming probes (bench ceilings)
+@pytest.mark.parametrize("n", [0, 8, 4096, 1_000_000])
+def test_stream_probes(ctx, n):
+    """The measurement-only probes the bench reports as ceilings do what they claim: a copy, the
+    sum of the two halves, and a read that writes nothing."""
+    x = oracle.gen_uniform_f32(n, 5, 0)
+    dx, dd = ctx.to_device(x), ctx.empty(max(n, 8), np.float32)
+    sentinel = np.full(max(n, 8), 7.0, np.float32)
+    dd.copy_from(sentinel)
+    ctx.stream_probe(hip.PROBE_COPY, dx, dd, n)
+    ctx.synchronize()
+    assert np.array_equal(dd.to_host(n).view(np.uint32), x.view(np.uint32))
+    ctx.stream_probe(hip.PROBE_READ2_WRITE1, dx, dd, n)
+    ctx.synchronize()
+    h = n // 2
+    assert np.array_equal(dd.to_host(h), (x[:h] + x[h:]).astype(np.float32))
+    before = dd.to_host()
+    ctx.stream_probe(hip.PROBE_READ, dx, dd, n)
+    ctx.synchronize()
+    assert np.array_equal(dd.to_host().view(np.uint32), before.view(np.uint32))
+    for x_ in (dx, dd):
+        ctx.free(x_)
+
+
+def test_stream_probe_arguments(ctx):
+    dx, dd = ctx.empty(16, np.float32), ctx.empty(16, np.float32)
+    lib = hip.load()
+    assert lib.dc_hip_stream_probe(ctx.handle, hip.PROBE_COPY, dx.ptr, dd.ptr, 12) == hip.DC_ERR_INVALID_ARGUMENT
+    assert lib.dc_hip_stream_probe(ctx.handle, 3, dx.ptr, dd.ptr, 8) == hip.DC_ERR_INVALID_ARGUMENT
+    assert lib.dc_hip_stream_probe(ctx.handle, hip.PROBE_COPY, dx.ptr + 4, dd.ptr, 8) == hip.DC_ERR_MISALIGNED
+    for x_ in (dx, dd):
+        ctx.free(x_)
