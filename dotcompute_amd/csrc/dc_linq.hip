@@ -616,7 +616,8 @@ __global__ __launch_bounds__(kBlock) void where_select_kernel(const dc_linq_chai
 }
 
 // ---- Where/Select -> ToArray, round-robin kernel for large inputs --------------------------------
-// A resident grid of P workgroups (one per CU, all running at once). Workgroup w owns tile r*P + w of
+// A resident grid of P workgroups (one per CU, all running at once). The workgroup at tile position w
+// (w follows the XCDs: see the kernel) owns tile r*P + w of
 // round r, so every round is a contiguous stretch of P tiles. Each tile publishes its kept count as
 // one epoch-tagged word; the output offset of tile (r, w) is
 //     base_r + sum_{w' < w} count(r, w'),   base_{r+1} = base_r + sum_{w'} count(r, w'),
@@ -730,7 +731,11 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
   __shared__ uint32_t s_acc[8];         // (waves finished << 24) | kept so far, per tile slot
   __shared__ int64_t s_off[2];          // output offset of the tile being written, by round parity
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t w = blockIdx.x;
+  // This workgroup's tile position in every round. Workgroups go to the XCDs round-robin, so
+  // positions are dealt out XCD by XCD: consecutive tiles (and the partly written cache line
+  // where one tile's output ends and the next one's begins) then share one XCD's L2, which merges
+  // the two halves of that line before it is written back.
+  const uint32_t w = (P % 8u == 0u) ? (blockIdx.x % 8u) * (P / 8u) + blockIdx.x / 8u : blockIdx.x;
   const int64_t num_tiles = (n + kRrTile - 1) / kRrTile;
   const uint32_t R0 = (uint32_t)((n / kRrTile) / P);  // rounds in which every tile is full
   const uint32_t rounds = R0 > 0 ? R0 + kRrDelay : 0;
