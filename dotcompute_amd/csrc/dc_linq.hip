@@ -630,11 +630,14 @@ __global__ __launch_bounds__(kBlock) void where_select_kernel(const dc_linq_chai
 //   - the program is one of the compile-time variants (shape and comparison fixed for the one- and
 //     two-stage affine chains): the kernel is bound by its instruction issue at this rate, so
 //     the per-element work is kept to a compare, the map, and the ballot ranking.
-// Roles inside the 576-thread workgroup: wave 0 reads and checks the count words and broadcasts the
-// output offset; waves 1..8 each own a contiguous 1024-element chunk of every tile, rank their kept
-// elements with ballot + mbcnt, stage them in a private LDS ring (in input order) and later write
-// them as one contiguous run. The last wave to finish a tile (an LDS atomic) publishes its count.
-// One workgroup barrier per round.
+// Roles inside the 576-thread workgroup: waves 0..7 each own a contiguous 1024-element chunk of every
+// tile, rank their kept elements with ballot + mbcnt, stage them in a private LDS ring (in input
+// order) and later write them as one contiguous run; wave 8 reads and checks the count words and
+// broadcasts the output offset. The last wave to finish a tile (an LDS atomic) publishes its count.
+// One workgroup barrier per round. Wave w runs on SIMD w mod 4 and a SIMD issues for its oldest
+// ready wave first, so the control wave is the youngest: it shares SIMD 0 with workers 0 and 4
+// without delaying them (as wave 0 it made worker 8 the slowest wave of every workgroup and
+// every round waited for it: 274.6 against 267.5 us at 256M, 50 % kept).
 // Geometry (measured at 256M, 50% kept: 8 workers x 4 vectors 290 us, 15 x 2 293 us, 12 x 3 297 us):
 // fewer, wider worker waves spread the per-round fixed work (ranking tables, the barrier) over
 // more elements.
@@ -672,7 +675,7 @@ __device__ inline void rr_issue_counts(uint32_t (&c)[kRrCountsPerLane], const ui
   }
 }
 
-// Wave 0: re-reads until every count word of `round` carries this launch's epoch (bounded), then
+// The control wave: re-reads until every count word of `round` carries this launch's epoch (bounded), then
 // returns the sum of the counts of workgroups before `me` and the round total.
 __device__ inline bool rr_resolve(uint32_t (&c)[kRrCountsPerLane], const uint32_t* __restrict__ counts, uint32_t round,
                                   uint32_t P, uint32_t epoch16, uint32_t me, uint32_t* pref, uint32_t* total) {
@@ -743,8 +746,8 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
   if (tid < 8) s_acc[tid] = 0;
   __syncthreads();
 
-  if (wave == 0) {
-    // ---------------- control wave
+  if (wave == kRrWorkers) {
+    // ---------------- control wave (the youngest wave: see the roles above)
     int64_t base = 0;
     uint32_t c[kRrCountsPerLane];
     bool ok = true;
@@ -782,7 +785,7 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
   }
 
   // ---------------- worker waves
-  const int ww = wave - 1;
+  const int ww = wave;
   float* ring = s_ring[ww];
   uint32_t head = 0, tail = 0;
   const int64_t chunk = (int64_t)ww * kRrChunk;
