@@ -476,7 +476,7 @@ __global__ __launch_bounds__(kPass) void plan_tile_bases(const int32_t* __restri
 // threads on consecutive local positions li: the run holding li is first_k[li / 64] plus the run
 // starts in (64 (li / 64), li] (a bitmap of run starts), and nz_gb of that run maps li to its global
 // position; otherwise each entry is written where its atomic cursor lands.
-template <int SMAX, bool kStaged>
+template <int SMAX, bool kStaged, int STAGE = kStage>
 __global__ __launch_bounds__(kPass) void plan_tile_scatter(
     const int32_t* __restrict__ col, const float* __restrict__ val, const int4* __restrict__ binfo,
     int32_t nblocks, int32_t S, uint32_t width, uint32_t cols, const int32_t* __restrict__ tcnt,
@@ -484,10 +484,10 @@ __global__ __launch_bounds__(kPass) void plan_tile_scatter(
     uint16_t* __restrict__ col16, float* __restrict__ val_s, uint16_t* __restrict__ dest16) {
   __shared__ int32_t cur[SMAX];
   __shared__ int32_t nz_gb[kStaged ? SMAX : 1];              // k-th non-empty run: global base - local start
-  __shared__ uint32_t starts[kStaged ? kStage / 32 : 1];     // bit li: a non-empty run starts at li
-  __shared__ int32_t first_k[kStaged ? kStage / 64 : 1];     // the run holding local position 64c
-  __shared__ uint32_t st_cd[kStaged ? kStage : 1];
-  __shared__ float st_v[kStaged ? kStage : 1];
+  __shared__ uint32_t starts[kStaged ? STAGE / 32 : 1];     // bit li: a non-empty run starts at li
+  __shared__ int32_t first_k[kStaged ? STAGE / 64 : 1];     // the run holding local position 64c
+  __shared__ uint32_t st_cd[kStaged ? STAGE : 1];
+  __shared__ float st_v[kStaged ? STAGE : 1];
   __shared__ int32_t wsum[kPassWaves];
   __shared__ int32_t wcnt[kPassWaves];
   const int32_t b = xcd_block(nblocks);
@@ -497,7 +497,7 @@ __global__ __launch_bounds__(kPass) void plan_tile_scatter(
   const int32_t S1 = S + 1;
   int32_t n = 0;  // kStaged: thread t's run length (t < S)
   if constexpr (kStaged)
-    for (int i = t; i < kStage / 32; i += kPass) starts[i] = 0;
+    for (int i = t; i < STAGE / 32; i += kPass) starts[i] = 0;
   for (int s = t; s <= S; s += kPass) {
     const int32_t o = sbase[s] + tcnt[(int64_t)s * nblocks + b];
     const int32_t next = b + 1 < nblocks ? sbase[s] + tcnt[(int64_t)s * nblocks + b + 1] : sbase[s] + tot[s];
@@ -529,12 +529,12 @@ __global__ __launch_bounds__(kPass) void plan_tile_scatter(
       }
       E += v;
     }
-    E = min(E, kStage);
+    E = min(E, STAGE);
     if (t < S) {
-      if (n > 0 && pre < kStage) {
+      if (n > 0 && pre < STAGE) {
         nz_gb[k] = cur[t] - pre;  // local position li of run t goes to nz_gb[k] + li
         atomicOr(&starts[pre >> 5], 1u << (pre & 31));
-        for (int32_t c = (pre + 63) >> 6; c < kStage / 64 && (c << 6) < pre + n; ++c) first_k[c] = k;
+        for (int32_t c = (pre + 63) >> 6; c < STAGE / 64 && (c << 6) < pre + n; ++c) first_k[c] = k;
       }
       cur[t] = pre;
     }
@@ -556,7 +556,7 @@ __global__ __launch_bounds__(kPass) void plan_tile_scatter(
         const uint32_t cc = clamp_col(c[u], cols), s = cc / width;
         const int32_t pos = atomicAdd(&cur[s], 1);
         if constexpr (kStaged) {
-          if (pos < kStage) {
+          if (pos < STAGE) {
             st_cd[pos] = (cc - s * width) | ((uint32_t)(j - g.j0) << 16);
             st_v[pos] = v[u];
           }
@@ -924,13 +924,16 @@ int32_t plan_build(dc_hip_ctx* ctx, dc_hip_spmv_plan* p, const int32_t* rp, cons
   plan_tile_bases<<<1, kPass, 0, ctx->stream>>>(p->tot, S, p->sbase, p->col16, p->dest16, p->val_s, p->nwg,
                                                 p->wrange);
   DC_RETURN_IF(dc::last_launch_status());
-#define DC_TILE_SCATTER(SM, ST)                                                                         \
-  plan_tile_scatter<SM, ST><<<bgrid, kPass, 0, ctx->stream>>>(col, val, p->binfo, nb, S, width, cols, p->tcnt,  \
-                                                              p->tot, p->sbase, p->toff, p->col16, p->val_s,  \
-                                                              p->dest16)
-  if (S < kScatterRuns) DC_TILE_SCATTER(kScatterRuns, true);
-  else if (S + 1 <= 8192) DC_TILE_SCATTER(8192, false);
-  else DC_TILE_SCATTER(kMaxSlices + 8, false);
+#define DC_TILE_SCATTER(SM, ST, STG)                                                                          \
+  plan_tile_scatter<SM, ST, STG><<<bgrid, kPass, 0, ctx->stream>>>(col, val, p->binfo, nb, S, width, cols, p->tcnt,  \
+                                                                   p->tot, p->sbase, p->toff, p->col16, p->val_s,  \
+                                                                   p->dest16)
+  // staging sized for the block span (a block holds fewer than 2 * span entries besides a giant
+  // row): 4096-entry spans stage in half the LDS, so two workgroups fit per CU
+  if (S < kScatterRuns && p->span == kSpanSmall) DC_TILE_SCATTER(kScatterRuns, true, 2 * kSpanSmall);
+  else if (S < kScatterRuns) DC_TILE_SCATTER(kScatterRuns, true, kStage);
+  else if (S + 1 <= 8192) DC_TILE_SCATTER(8192, false, kStage);
+  else DC_TILE_SCATTER(kMaxSlices + 8, false, kStage);
 #undef DC_TILE_SCATTER
   return dc::last_launch_status();
 }
