@@ -591,10 +591,10 @@ __global__ __launch_bounds__(kPass) void plan_tile_scatter(
   }
 }
 
-// A6 (table path of the row pass): per block, each run's first product minus its local start and
-// the local start (the block's runs numbered slice by slice), and the block's total in entry S.
+// A6 (table path of the row pass): per block, each run's local start (the block's runs numbered
+// slice by slice; below 2 * span, so 16 bits) and the block's total in entry S.
 __global__ __launch_bounds__(kPass) void plan_run_tables(const int32_t* __restrict__ toff, int32_t nblocks, int32_t S,
-                                                         int2* __restrict__ rtab) {
+                                                         uint16_t* __restrict__ rpre) {
   __shared__ int32_t wsum[kPassWaves];
   const int32_t b = xcd_block(nblocks);
   if (b < 0) return;  // whole workgroup
@@ -616,9 +616,9 @@ __global__ __launch_bounds__(kPass) void plan_run_tables(const int32_t* __restri
     if (w < wave) pre += v;
     E += v;
   }
-  int2* row = rtab + (int64_t)b * S1;
-  if (t < S) row[t] = make_int2(o - pre, pre);
-  if (t == 0) row[S] = make_int2(0, E);
+  uint16_t* row = rpre + (int64_t)b * S1;
+  if (t < S) row[t] = (uint16_t)min(pre, 65535);
+  if (t == 0) row[S] = (uint16_t)min(E, 65535);
 }
 
 // Product pass: p[i] = val_s[i] * x_tile[col16[i]] over the slice regions [0, sbase[S]). Workgroup
@@ -711,7 +711,7 @@ __global__ __launch_bounds__(kPass) void spmv_tile_products(const uint16_t* __re
 template <bool kTable, int SPAN>
 __global__ __launch_bounds__(SPAN / 8) void spmv_tile_rows(
     const int32_t* __restrict__ rp, int32_t nnz, const int4* __restrict__ binfo, int32_t nblocks,
-    const int32_t* __restrict__ toff, const int2* __restrict__ rtab, int32_t S, const float* __restrict__ p,
+    const int32_t* __restrict__ toff, const uint16_t* __restrict__ rpre, int32_t S, const float* __restrict__ p,
     const uint16_t* __restrict__ dest16,
     const uint16_t* __restrict__ col16, const float* __restrict__ val_s, const float* __restrict__ x, uint32_t cols,
     float* __restrict__ y, double* __restrict__ block_sums, const double* __restrict__ scale, uint32_t pbytes) {
@@ -735,17 +735,18 @@ __global__ __launch_bounds__(SPAN / 8) void spmv_tile_rows(
     pe[k] = r < g.r1 ? rp[r + 1] : 0;
   }
   if constexpr (kTable) {
-    // thread t holds run t (S <= kThreads): its local start and length and its first product,
-    // precomputed once per plan by plan_run_tables; it writes its products' entries of the run table
-    const int2* rt = rtab + (int64_t)b * S1;
+    // thread t holds run t (S <= kThreads): its offsets from the two rows of run offsets it shares
+    // with the neighbouring blocks, and its local start, precomputed once per plan by
+    // plan_run_tables; it writes its products' entries of the run table
+    const uint16_t* rt = rpre + (int64_t)b * S1;
     int32_t pre = 0, n = 0;
     if (t < S) {
-      const int2 a = rt[t];
-      pre = a.y;
-      n = rt[t + 1].y - pre;
-      run_base[t] = a.x;  // product li of run t is at run_base[t] + li
+      const int32_t o = t0[t];
+      pre = rt[t];
+      n = t1[t] - o;
+      run_base[t] = o - pre;  // product li of run t is at run_base[t] + li
     }
-    const int32_t E = min(rt[S].y, kSt);
+    const int32_t E = min((int32_t)rt[S], kSt);
     int16_t* run_of = reinterpret_cast<int16_t*>(stage);  // kSt int16 fit in half the stage
     for (int32_t li = pre; li < min(pre + n, E); ++li) run_of[li] = (int16_t)t;
     __syncthreads();
@@ -847,7 +848,7 @@ struct dc_hip_spmv_plan {
   float *val_s = nullptr, *p = nullptr;
   int32_t *rp = nullptr, *tcnt = nullptr, *toff = nullptr, *tot = nullptr, *sbase = nullptr, *blk_row = nullptr;
   int4 *binfo = nullptr, *wrange = nullptr;
-  int2* rtab = nullptr;  // per (block, run): {first product - local start, local start}; run S: {0, total}
+  uint16_t* rpre = nullptr;  // per (block, run): the run's local start; run S: the block's total
   int32_t span = kSpanBig;  // block span in nonzeros
   int32_t nwg = 1;  // product-pass workgroups (one per CU)
   double *block_sums = nullptr, *scalars = nullptr;
@@ -876,7 +877,7 @@ void plan_layout(dc_hip_spmv_plan* p, void* mem) {
   p->sbase = reinterpret_cast<int32_t*>(take((S1 + 1) * 4));
   p->blk_row = reinterpret_cast<int32_t*>(take((nb + 1) * 4));
   p->binfo = reinterpret_cast<int4*>(take(nb * 32));
-  p->rtab = reinterpret_cast<int2*>(take(S1 * nb * 8));
+  p->rpre = reinterpret_cast<uint16_t*>(take(S1 * nb * 2));
   p->wrange = reinterpret_cast<int4*>(take((size_t)p->nwg * 16));
   p->block_sums = reinterpret_cast<double*>(take(nb * 8));
   p->scalars = reinterpret_cast<double*>(take(8 * 8));
@@ -961,7 +962,7 @@ int32_t plan_build(dc_hip_ctx* ctx, dc_hip_spmv_plan* p, const int32_t* rp, cons
 #undef DC_TILE_SCATTER
   DC_RETURN_IF(dc::last_launch_status());
   if (S <= p->span / 8 && S <= kPass)  // the row pass's table path reads the run tables
-    plan_run_tables<<<bgrid, kPass, 0, ctx->stream>>>(p->toff, nb, S, p->rtab);
+    plan_run_tables<<<bgrid, kPass, 0, ctx->stream>>>(p->toff, nb, S, p->rpre);
   return dc::last_launch_status();
 }
 
@@ -980,7 +981,7 @@ int32_t plan_spmv(dc_hip_ctx* ctx, const dc_hip_spmv_plan* p, const float* x, fl
   const unsigned bgrid = (unsigned)(kXcds * ((p->nblocks + kXcds - 1) / kXcds));
   double* bs = sums ? p->block_sums : nullptr;
 #define DC_TILE_ROWS(TABLE, SP)                                                                                 \
-  spmv_tile_rows<TABLE, SP><<<bgrid, SP / 8, 0, ctx->stream>>>(p->rp, (int32_t)p->nnz, p->binfo, p->nblocks, p->toff, p->rtab, \
+  spmv_tile_rows<TABLE, SP><<<bgrid, SP / 8, 0, ctx->stream>>>(p->rp, (int32_t)p->nnz, p->binfo, p->nblocks, p->toff, p->rpre, \
                                                                p->slices, p->p, p->dest16, p->col16, p->val_s, x,    \
                                                                cols, y, bs, scale, (uint32_t)(p->zcap * 4))
   // the table path addresses the products with 32-bit byte offsets
