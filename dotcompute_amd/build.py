@@ -5,6 +5,8 @@ Produces, in-tree:
   dotcompute_amd/lib/dc_kernels_gfx950.hsaco  code object for the generic module-load path: the
                                               kernels generated from dotcompute_amd/kernels/*.cs
   dotcompute_amd/lib/libdotcompute_host.so    C++ host layer (orchestrator, LINQ provider, algorithms)
+  dotcompute_amd/lib/libdotcompute_bench.so   measurement-only streaming probes (bench.py's ceilings;
+                                              not part of the product library)
   dotcompute_amd/lib/dc_host_tests             C++ tests of the host layer
   dotcompute_amd/lib/dc_orchestrator_bench     end-to-end orchestrator timing (bench.py runs it)
 Run: python -m dotcompute_amd.build
@@ -64,6 +66,19 @@ def build_hip_library(jobs: int = 8) -> str:
     return out
 
 
+def build_probe_library() -> str:
+    """The measurement-only streaming probes (dotcompute_amd/probes), a library of their own so that
+    the product library carries no benchmark code."""
+    os.makedirs(BUILD, exist_ok=True)
+    os.makedirs(LIB, exist_ok=True)
+    obj = os.path.join(BUILD, "dc_bench_probes.o")
+    _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(PKG, "probes", "dc_bench_probes.hip"), "-o", obj])
+    out = os.path.join(LIB, "libdotcompute_bench.so")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", out + ".tmp", obj])
+    os.replace(out + ".tmp", out)
+    return out
+
+
 def generate_kernels() -> list:
     """Translates the [Kernel] methods of dotcompute_amd/kernels/*.cs: the HIP kernels go into the
     code object, the registry into the host library (KernelRegistry.g.cpp)."""
@@ -118,11 +133,13 @@ def build_oracle() -> str:
 
 def build_all() -> None:
     generate_kernels()
-    with cf.ThreadPoolExecutor(max_workers=3) as ex:
+    with cf.ThreadPoolExecutor(max_workers=4) as ex:
         f_lib = ex.submit(build_hip_library)
         f_co = ex.submit(build_code_object)
         f_or = ex.submit(build_oracle)
+        f_pr = ex.submit(build_probe_library)
         f_lib.result()
+        f_pr.result()
         f_co.result()
         f_or.result()
     build_host_layer()

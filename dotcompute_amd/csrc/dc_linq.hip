@@ -63,28 +63,69 @@ __device__ inline float net_max(float a, float b) {
 // waits for every outstanding streaming load of the thread. Two dword reads at a wave-uniform
 // address stay scalar loads.
 struct Instr {
-  uint32_t op, src, mode;
-  float imm;
+  uint32_t op, src, mode, imm;  // imm: the constant's bits (float32 or int32 by program type)
 };
 __device__ inline Instr fetch_instr(const dc_linq_chain& prog, int pc) {
   const uint32_t* w = reinterpret_cast<const uint32_t*>(&prog.code[pc]);
   const uint32_t w0 = w[0];
-  return Instr{w0 & 0xFFu, (w0 >> 8) & 0xFFu, (w0 >> 16) & 0xFFu, __builtin_bit_cast(float, w[1])};
+  return Instr{w0 & 0xFFu, (w0 >> 8) & 0xFFu, (w0 >> 16) & 0xFFu, w[1]};
 }
 
-// Runs the program over the EPT elements of one thread. Returns the keep mask (bit j = element j).
+// Exceptions of an int32 program, per element: bit j of `hit` is set once element j has thrown
+// (at its first throwing operation; C# stops evaluating the element there), and bit j of `ovf`
+// tells that this operation threw OverflowException (else DivideByZeroException).
+struct Faults {
+  uint32_t hit = 0, ovf = 0;
+};
+
+// Records the exceptions of one operation applied to element j: only elements still kept
+// (`live`), and only their first exception.
+__device__ __attribute__((always_inline)) inline void note_fault(Faults& f, int j, uint32_t live, bool dz, bool ov) {
+  const uint32_t bit = ((dz || ov) && ((live >> j) & 1u)) ? ((1u << j) & ~f.hit) : 0u;
+  f.hit |= bit;
+  f.ovf |= ov ? bit : 0u;
+}
+
+// C# int arithmetic (unchecked context): + - * wrap; / and % throw for a zero divisor and
+// overflow for int.MinValue / -1 (and % -1, as .NET on x64 does); the result of a throwing
+// element is never used.
+// C#'s float % (truncated remainder, exact). Kept out of line: a program with a remainder is rare,
+// and fmodf inlined into every unrolled interpreter loop would bloat each kernel variant.
+__device__ __attribute__((noinline)) float net_rem(float a, float b) { return ::fmodf(a, b); }
+
+__device__ inline int32_t wrap_add(int32_t a, int32_t b) { return (int32_t)((uint32_t)a + (uint32_t)b); }
+__device__ inline int32_t wrap_sub(int32_t a, int32_t b) { return (int32_t)((uint32_t)a - (uint32_t)b); }
+__device__ inline int32_t wrap_mul(int32_t a, int32_t b) { return (int32_t)((uint32_t)a * (uint32_t)b); }
+__device__ __attribute__((always_inline)) inline int32_t checked_div(int32_t a, int32_t b, int j, uint32_t live,
+                                                                    Faults& f) {
+  const bool dz = b == 0, ov = (b == -1) && (a == INT32_MIN);
+  note_fault(f, j, live, dz, ov);
+  return a / ((dz || ov) ? 1 : b);
+}
+__device__ __attribute__((always_inline)) inline int32_t checked_rem(int32_t a, int32_t b, int j, uint32_t live,
+                                                                    Faults& f) {
+  const bool dz = b == 0, ov = (b == -1) && (a == INT32_MIN);
+  note_fault(f, j, live, dz, ov);
+  return a % ((dz || ov) ? 1 : b);
+}
+
+// Runs the program over the EPT elements of one thread. Returns the keep mask (bit j = element j),
+// which starts as `live` (the elements that exist). T is the element type: float (no exceptions)
+// or int32_t (C# int semantics, exceptions into `f`).
 // SAVES = false drops the s0/s1 registers for programs that never use them (the common case),
 // which keeps the kernels at a higher occupancy. Operands are read in place (an immediate stays a
 // scalar operand of the vector instruction), so no per-element operand copy is materialised.
-template <int EPT, bool SAVES>
-__device__ __attribute__((always_inline)) inline uint32_t run_program(const dc_linq_chain& prog, float (&e)[EPT]) {
-  float v[EPT];
-  float s0[SAVES ? EPT : 1], s1[SAVES ? EPT : 1];
+template <typename T, int EPT, bool SAVES>
+__device__ __attribute__((always_inline)) inline uint32_t run_program(const dc_linq_chain& prog, T (&e)[EPT],
+                                                                       uint32_t live, Faults& f) {
+  constexpr bool kInt = std::is_same<T, int32_t>::value;
+  T v[EPT];
+  T s0[SAVES ? EPT : 1], s1[SAVES ? EPT : 1];
 #pragma unroll
-  for (int j = 0; j < EPT; ++j) v[j] = 0.0f;
+  for (int j = 0; j < EPT; ++j) v[j] = T(0);
 #pragma unroll
-  for (int j = 0; j < (SAVES ? EPT : 1); ++j) { s0[j] = 0.0f; s1[j] = 0.0f; }
-  uint32_t p = 0, q = 0, keep = (EPT == 32) ? 0xFFFFFFFFu : ((1u << EPT) - 1u);
+  for (int j = 0; j < (SAVES ? EPT : 1); ++j) { s0[j] = T(0); s1[j] = T(0); }
+  uint32_t p = 0, q = 0, keep = live;
   const int n = prog.n_instr;
   for (int pc = 0; pc < n; ++pc) {
     const Instr ins = fetch_instr(prog, pc);
@@ -94,37 +135,99 @@ __device__ __attribute__((always_inline)) inline uint32_t run_program(const dc_l
 #define DC_LQ_APPLY(body)                                                                   \
   do {                                                                                      \
     if (ins.src == DC_LQ_SRC_ELEM) {                                                        \
-      _Pragma("unroll") for (int j = 0; j < EPT; ++j) { const float O = e[j]; body; }       \
+      _Pragma("unroll") for (int j = 0; j < EPT; ++j) { const T O = e[j]; body; }           \
     } else if (SAVES && ins.src == DC_LQ_SRC_S0) {                                          \
-      _Pragma("unroll") for (int j = 0; j < EPT; ++j) { const float O = s0[SAVES ? j : 0]; body; } \
+      _Pragma("unroll") for (int j = 0; j < EPT; ++j) { const T O = s0[SAVES ? j : 0]; body; } \
     } else if (SAVES && ins.src == DC_LQ_SRC_S1) {                                          \
-      _Pragma("unroll") for (int j = 0; j < EPT; ++j) { const float O = s1[SAVES ? j : 0]; body; } \
+      _Pragma("unroll") for (int j = 0; j < EPT; ++j) { const T O = s1[SAVES ? j : 0]; body; } \
     } else {                                                                                \
-      const float O = ins.imm;                                                              \
+      const T O = __builtin_bit_cast(T, ins.imm);                                           \
       _Pragma("unroll") for (int j = 0; j < EPT; ++j) { body; }                             \
     }                                                                                       \
   } while (0)
     switch (ins.op) {
       case DC_LQ_LOAD: DC_LQ_APPLY(v[j] = O); break;
-      case DC_LQ_ADD: DC_LQ_APPLY(v[j] = v[j] + O); break;
-      case DC_LQ_SUB: DC_LQ_APPLY(v[j] = v[j] - O); break;
-      case DC_LQ_RSUB: DC_LQ_APPLY(v[j] = O - v[j]); break;
-      case DC_LQ_MUL: DC_LQ_APPLY(v[j] = v[j] * O); break;
-      case DC_LQ_DIV: DC_LQ_APPLY(v[j] = v[j] / O); break;
-      case DC_LQ_RDIV: DC_LQ_APPLY(v[j] = O / v[j]); break;
-      case DC_LQ_MIN: DC_LQ_APPLY(v[j] = net_min(v[j], O)); break;
-      case DC_LQ_MAX: DC_LQ_APPLY(v[j] = net_max(v[j], O)); break;
+      case DC_LQ_ADD:
+        if constexpr (kInt) DC_LQ_APPLY(v[j] = wrap_add(v[j], O));
+        else DC_LQ_APPLY(v[j] = v[j] + O);
+        break;
+      case DC_LQ_SUB:
+        if constexpr (kInt) DC_LQ_APPLY(v[j] = wrap_sub(v[j], O));
+        else DC_LQ_APPLY(v[j] = v[j] - O);
+        break;
+      case DC_LQ_RSUB:
+        if constexpr (kInt) DC_LQ_APPLY(v[j] = wrap_sub(O, v[j]));
+        else DC_LQ_APPLY(v[j] = O - v[j]);
+        break;
+      case DC_LQ_MUL:
+        if constexpr (kInt) DC_LQ_APPLY(v[j] = wrap_mul(v[j], O));
+        else DC_LQ_APPLY(v[j] = v[j] * O);
+        break;
+      case DC_LQ_DIV:
+        if constexpr (kInt) DC_LQ_APPLY(v[j] = checked_div(v[j], O, j, keep, f));
+        else DC_LQ_APPLY(v[j] = v[j] / O);
+        break;
+      case DC_LQ_RDIV:
+        if constexpr (kInt) DC_LQ_APPLY(v[j] = checked_div(O, v[j], j, keep, f));
+        else DC_LQ_APPLY(v[j] = O / v[j]);
+        break;
+      case DC_LQ_REM:
+        if constexpr (kInt) DC_LQ_APPLY(v[j] = checked_rem(v[j], O, j, keep, f));
+        else DC_LQ_APPLY(v[j] = net_rem(v[j], O));
+        break;
+      case DC_LQ_RREM:
+        if constexpr (kInt) DC_LQ_APPLY(v[j] = checked_rem(O, v[j], j, keep, f));
+        else DC_LQ_APPLY(v[j] = net_rem(O, v[j]));
+        break;
+      case DC_LQ_MIN:
+        if constexpr (kInt) DC_LQ_APPLY(v[j] = min(v[j], O));
+        else DC_LQ_APPLY(v[j] = net_min(v[j], O));
+        break;
+      case DC_LQ_MAX:
+        if constexpr (kInt) DC_LQ_APPLY(v[j] = max(v[j], O));
+        else DC_LQ_APPLY(v[j] = net_max(v[j], O));
+        break;
       case DC_LQ_NEG:
 #pragma unroll
-        for (int j = 0; j < EPT; ++j) v[j] = -v[j];
+        for (int j = 0; j < EPT; ++j) {
+          if constexpr (kInt) v[j] = wrap_sub(0, v[j]);
+          else v[j] = -v[j];
+        }
         break;
       case DC_LQ_ABS:
 #pragma unroll
-        for (int j = 0; j < EPT; ++j) v[j] = __builtin_fabsf(v[j]);
+        for (int j = 0; j < EPT; ++j) {
+          if constexpr (kInt) {
+            note_fault(f, j, keep, false, v[j] == INT32_MIN);  // Math.Abs(int.MinValue) throws
+            v[j] = v[j] < 0 ? wrap_sub(0, v[j]) : v[j];
+          } else {
+            v[j] = __builtin_fabsf(v[j]);
+          }
+        }
         break;
       case DC_LQ_SQRT:
+        if constexpr (!kInt) {
 #pragma unroll
-        for (int j = 0; j < EPT; ++j) v[j] = __builtin_sqrtf(v[j]);
+          for (int j = 0; j < EPT; ++j) v[j] = __builtin_sqrtf(v[j]);
+        }
+        break;
+      case DC_LQ_FLOOR:
+        if constexpr (!kInt) {
+#pragma unroll
+          for (int j = 0; j < EPT; ++j) v[j] = __builtin_floorf(v[j]);
+        }
+        break;
+      case DC_LQ_CEIL:
+        if constexpr (!kInt) {
+#pragma unroll
+          for (int j = 0; j < EPT; ++j) v[j] = __builtin_ceilf(v[j]);
+        }
+        break;
+      case DC_LQ_ROUND:
+        if constexpr (!kInt) {
+#pragma unroll
+          for (int j = 0; j < EPT; ++j) v[j] = __builtin_rintf(v[j]);  // ties to even, as MathF.Round
+        }
         break;
       case DC_LQ_STORE_S0:
         if (SAVES) {
@@ -163,6 +266,48 @@ __device__ __attribute__((always_inline)) inline uint32_t run_program(const dc_l
     }
   }
   return keep;
+}
+
+// Float programs (no exceptions), every element present.
+template <int EPT, bool SAVES>
+__device__ __attribute__((always_inline)) inline uint32_t run_program_f32(const dc_linq_chain& prog, float (&e)[EPT]) {
+  Faults none;
+  return run_program<float, EPT, SAVES>(prog, e, (EPT == 32) ? 0xFFFFFFFFu : ((1u << EPT) - 1u), none);
+}
+
+// An int32 program over elements held as float bit patterns (the kernels move 32-bit words and
+// do not care for their type): converts in registers, runs, converts back.
+template <int EPT, bool SAVES>
+__device__ __attribute__((always_inline)) inline uint32_t run_program_i32(const dc_linq_chain& prog, float (&e)[EPT],
+                                                                           uint32_t live, Faults& f) {
+  int32_t x[EPT];
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) x[j] = __builtin_bit_cast(int32_t, e[j]);
+  const uint32_t keep = run_program<int32_t, EPT, SAVES>(prog, x, live, f);
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) e[j] = __builtin_bit_cast(float, x[j]);
+  return keep;
+}
+
+// Fault word of the int32 entry points (in ctx->counters, 0 between launches): the largest
+// ~(4 * index + kind) over the throwing elements, i.e. the first element's code, complemented.
+__device__ inline void publish_fault(uint64_t* word, int64_t index, bool overflow) {
+  const uint64_t code = (uint64_t)index * 4u + (overflow ? DC_LINQ_FAULT_OVERFLOW : DC_LINQ_FAULT_DIVIDE_BY_ZERO);
+  __hip_atomic_fetch_max(word, ~code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The first faulting element of a thread's group: its position j (lowest set bit; the callers lay
+// elements out so that j increases with the sequence index) and kind.
+__device__ inline int first_fault(const Faults& f, bool* overflow) {
+  const int j = __builtin_ctz(f.hit);
+  *overflow = ((f.ovf >> j) & 1u) != 0u;
+  return j;
+}
+
+__global__ void fault_finish_kernel(uint64_t* __restrict__ word, int64_t* __restrict__ fault_out) {
+  const uint64_t w = *word;
+  *fault_out = w ? (int64_t)~w : (int64_t)DC_LINQ_FAULT_NONE;
+  *word = 0;
 }
 
 // True when the program reads or writes s0/s1 (selects the larger kernel variant).
@@ -346,7 +491,8 @@ __device__ inline uint64_t run_affine(const AffineChain& ch, float (&e)[EPT]) {
   return keep;
 }
 
-enum ProgramMode : int { kModeInterp = 0, kModeInterpSaves = 1, kModeAffine = 2 };
+enum ProgramMode : int { kModeInterp = 0, kModeInterpSaves = 1, kModeAffine = 2, kModeInterpI32 = 3, kModeInterpI32Saves = 4 };
+constexpr bool mode_is_int(int m) { return m == kModeInterpI32 || m == kModeInterpI32Saves; }
 
 // ---- one- and two-stage affine chains -------------------------------------------------------------
 // A chain of one filter `x <cmp> t`, one map `x * a + b`, or one of each in either order is
@@ -387,7 +533,10 @@ inline bool lower_canon2(const AffineChain& ch, int* shape, int* cmp, RdConst* o
 // interpreter (with or without save registers), any affine chain, and the one- and two-stage
 // affine chains with the shape and comparison fixed at compile time. Canonical modes are
 // kRdCanon + 8 * shape + (comparison - DC_LQ_CMP_GT).
-enum ReduceMode : int { kRdInterp = 0, kRdInterpSaves = 1, kRdAffine = 2, kRdCanon = 16 };
+// kRdInterpI32 / kRdInterpI32Saves: the int32 interpreter (programs over int32 elements).
+enum ReduceMode : int { kRdInterp = 0, kRdInterpSaves = 1, kRdAffine = 2, kRdInterpI32 = 3, kRdInterpI32Saves = 4,
+                        kRdCanon = 16 };
+constexpr bool rd_is_int(int rd) { return rd == kRdInterpI32 || rd == kRdInterpI32Saves; }
 constexpr int rd_canon(int shape, int cmp) { return kRdCanon + 8 * shape + (cmp - DC_LQ_CMP_GT); }
 constexpr bool rd_is_canon(int rd) { return rd >= kRdCanon; }
 constexpr int rd_shape(int rd) { return (rd - kRdCanon) >> 3; }
@@ -398,6 +547,14 @@ struct ReducePlan {
   AffineChain aff;
   RdConst k;
 };
+
+// Plan of an int32 program: the int32 interpreter, with or without save registers.
+inline ReducePlan reduce_plan_i32(const dc_linq_chain& prog) {
+  ReducePlan p{};
+  p.k = RdConst{0.0f, 1.0f, -0.0f};
+  p.mode = program_uses_saves(prog) ? kRdInterpI32Saves : kRdInterpI32;
+  return p;
+}
 
 inline ReducePlan reduce_plan(const dc_linq_chain& prog) {
   ReducePlan p{};
@@ -442,9 +599,25 @@ __device__ __attribute__((always_inline)) inline void apply_reduce_flags(const d
   } else {
     uint32_t keep;
     if constexpr (RD == kRdAffine) keep = (uint32_t)run_affine<EPT>(aff, e);
-    else keep = run_program<EPT, RD == kRdInterpSaves>(prog, e);
+    else keep = run_program_f32<EPT, RD == kRdInterpSaves>(prog, e);
 #pragma unroll
     for (int j = 0; j < EPT; ++j) kept[j] = ((keep >> j) & 1u) != 0u;
+  }
+}
+
+// apply_reduce_flags for every mode, the int32 ones included: elements outside `live` are not kept
+// (int32 modes; the float modes are only called on present elements), and the exceptions of an
+// int32 program go to `f`.
+template <int RD, int EPT>
+__device__ __attribute__((always_inline)) inline void eval_flags(const dc_linq_chain& prog, const AffineChain& aff,
+                                                                 const RdConst& k, float (&e)[EPT], bool (&kept)[EPT],
+                                                                 uint32_t live, Faults& f) {
+  if constexpr (rd_is_int(RD)) {
+    const uint32_t keep = run_program_i32<EPT, RD == kRdInterpI32Saves>(prog, e, live, f);
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) kept[j] = ((keep >> j) & 1u) != 0u;
+  } else {
+    apply_reduce_flags<RD, EPT>(prog, aff, k, e, kept);
   }
 }
 
@@ -473,6 +646,13 @@ void rd_dispatch(int mode, F&& f) {
 }
 #undef DC_RD_CMP_MODES
 
+// rd_dispatch for the int32 modes.
+template <class F>
+void rd_dispatch_i32(int mode, F&& f) {
+  if (mode == kRdInterpI32Saves) f(std::integral_constant<int, kRdInterpI32Saves>{});
+  else f(std::integral_constant<int, kRdInterpI32>{});
+}
+
 // ---- Where/Select -> ToArray ------------------------------------------------------------------
 // One tile per workgroup, claimed by ticket. Element order inside a tile is (vector j, wave, lane,
 // slot k): thread t loads 16-byte vectors j = 0..7 at tile + 2048 j + 4 t. After the lookback each
@@ -486,11 +666,32 @@ __device__ inline uint32_t take_ticket(uint32_t* __restrict__ ticket, uint32_t t
 }
 
 
+// The program over a thread's 32 elements; `valid` marks the elements that exist. For the int32
+// modes, bit b of *fhit / *fovf is element b's first exception and its kind (OverflowException).
 template <int MODE>
 __device__ inline uint64_t apply_program(const dc_linq_chain& prog, const AffineChain& aff,
-                                         float (&e)[kElemPerThread]) {
+                                         float (&e)[kElemPerThread], uint64_t valid, uint64_t* fhit,
+                                         uint64_t* fovf) {
   if constexpr (MODE == kModeAffine) {
-    return run_affine<kElemPerThread>(aff, e);
+    return run_affine<kElemPerThread>(aff, e) & valid;
+  } else if constexpr (mode_is_int(MODE)) {
+    uint64_t keep = 0, hit = 0, ovf = 0;
+#pragma unroll
+    for (int c = 0; c < kElemPerThread / kChunk; ++c) {
+      float sub[kChunk];
+#pragma unroll
+      for (int i = 0; i < kChunk; ++i) sub[i] = e[c * kChunk + i];
+      Faults f;
+      const uint32_t live = (uint32_t)(valid >> (c * kChunk)) & ((1u << kChunk) - 1u);
+      keep |= (uint64_t)run_program_i32<kChunk, MODE == kModeInterpI32Saves>(prog, sub, live, f) << (c * kChunk);
+      hit |= (uint64_t)f.hit << (c * kChunk);
+      ovf |= (uint64_t)f.ovf << (c * kChunk);
+#pragma unroll
+      for (int i = 0; i < kChunk; ++i) e[c * kChunk + i] = sub[i];
+    }
+    *fhit = hit;
+    *fovf = ovf;
+    return keep;
   } else {
     uint64_t keep = 0;
 #pragma unroll
@@ -498,11 +699,11 @@ __device__ inline uint64_t apply_program(const dc_linq_chain& prog, const Affine
       float sub[kChunk];
 #pragma unroll
       for (int i = 0; i < kChunk; ++i) sub[i] = e[c * kChunk + i];
-      keep |= (uint64_t)run_program<kChunk, MODE == kModeInterpSaves>(prog, sub) << (c * kChunk);
+      keep |= (uint64_t)run_program_f32<kChunk, MODE == kModeInterpSaves>(prog, sub) << (c * kChunk);
 #pragma unroll
       for (int i = 0; i < kChunk; ++i) e[c * kChunk + i] = sub[i];
     }
-    return keep;
+    return keep & valid;
   }
 }
 
@@ -514,7 +715,8 @@ __global__ __launch_bounds__(kBlock) void where_select_kernel(const dc_linq_chai
                                                               int64_t* __restrict__ count_out,
                                                               uint64_t* __restrict__ status,
                                                               uint32_t* __restrict__ ticket, uint32_t epoch,
-                                                              uint32_t num_tiles, int vec_ok) {
+                                                              uint32_t num_tiles, int vec_ok,
+                                                              uint64_t* __restrict__ fault) {
   static_assert(kVecPerThread * kWaves == 64, "the group scan gives one (j, wave) group to each lane of wave 0");
   __shared__ uint32_t s_tile;
   __shared__ uint32_t s_offset[kVecPerThread][kWaves];
@@ -558,7 +760,12 @@ __global__ __launch_bounds__(kBlock) void where_select_kernel(const dc_linq_chai
       }
   }
 
-  const uint64_t keep = apply_program<MODE>(prog, aff, e) & valid;
+  uint64_t fhit = 0, fovf = 0;
+  const uint64_t keep = apply_program<MODE>(prog, aff, e, valid, &fhit, &fovf);
+  if (mode_is_int(MODE) && fhit) {  // element 4j + k of this thread is tile element 2048 j + 4 t + k
+    const int b = __builtin_ctzll(fhit);
+    publish_fault(fault, base + (int64_t)(b >> 2) * (4 * kBlock) + tid * 4 + (b & 3), ((fovf >> b) & 1u) != 0u);
+  }
 
   // Kept count of every (j, wave) group, and this lane's rank inside it (ballot + mbcnt per slot).
   uint32_t below[kVecPerThread];
@@ -712,7 +919,7 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
     const dc_linq_chain prog, const AffineChain aff, const RdConst canon, const float* __restrict__ in, int64_t n,
     float* __restrict__ out,
     int64_t* __restrict__ count_out, uint32_t* __restrict__ counts, uint32_t epoch16, uint32_t P,
-    uint32_t* __restrict__ done) {
+    uint32_t* __restrict__ done, uint64_t* __restrict__ fault) {
   __shared__ float s_ring[kRrWorkers][kRrRing + dc::kWave];  // + a discard slot per lane
   // ring positions stay in [0, kRrRing); a position below 2 * kRrRing wraps with one unsigned min
   auto wrap = [](uint32_t q) __attribute__((always_inline)) {
@@ -722,10 +929,23 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
   // Filter-then-map chains stage the raw value and map it when the run is written: only the
   // kept elements pay for the map.
   constexpr bool kLazyMap = rd_is_canon(RD) && rd_shape(RD) == kShapeFM;
-  auto apply = [&](float (&e)[kRrEpt], bool (&kept)[kRrEpt]) __attribute__((always_inline)) {
+  // int32 programs: the lane's first exception over every round, as ~(4 * index + kind) (0 = none),
+  // published once at the end, so the round loop stays free of branches.
+  uint64_t lane_fault = 0;
+  // `first` = sequence index of element 0 of this lane's chunk of the tile; element 4j + k sits at
+  // first + 256 j + k. `live` = the elements that exist.
+  auto apply = [&](float (&e)[kRrEpt], bool (&kept)[kRrEpt], int64_t first, uint32_t live)
+                   __attribute__((always_inline)) {
     if constexpr (kLazyMap) {
 #pragma unroll
       for (int j = 0; j < kRrEpt; ++j) kept[j] = rd_compare<rd_cmp(RD)>(e[j], canon.t);
+    } else if constexpr (rd_is_int(RD)) {
+      Faults f;
+      eval_flags<RD, kRrEpt>(prog, aff, canon, e, kept, live, f);
+      const int b = __builtin_ctz(f.hit | 0x80000000u);
+      const uint64_t code = (uint64_t)(first + (b >> 2) * (4 * dc::kWave) + (b & 3)) * 4u +
+                            (((f.ovf >> b) & 1u) ? DC_LINQ_FAULT_OVERFLOW : DC_LINQ_FAULT_DIVIDE_BY_ZERO);
+      lane_fault = max(lane_fault, f.hit ? ~code : (uint64_t)0);
     } else {
       apply_reduce_flags<RD, kRrEpt>(prog, aff, canon, e, kept);
     }
@@ -874,7 +1094,7 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
   auto round = [&](float (&ec)[kRrEpt], float (&en)[kRrEpt]) __attribute__((always_inline)) {
     load(en, min(r + kRrAhead, last));
     bool kept[kRrEpt];
-    apply(ec, kept);
+    apply(ec, kept, ((int64_t)r * P + w) * kRrTile + chunk + 4 * lane, ~0u);
     stage(ec, kept, r);
     __syncthreads();
     if (r >= (uint32_t)kRrDelay) write(r - kRrDelay, r & 1);
@@ -902,13 +1122,16 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
       valid |= ((1u << (uint32_t)nv) - 1u) << (4 * j);
     }
     bool kept[kRrEpt];
-    apply(e, kept);
+    apply(e, kept, t * kRrTile + chunk + 4 * lane, valid);
 #pragma unroll
     for (int i = 0; i < kRrEpt; ++i) kept[i] = kept[i] && ((valid >> i) & 1u);
     stage(e, kept, R0);
     __syncthreads();
     __syncthreads();
     write(R0, 0);
+  }
+  if constexpr (rd_is_int(RD)) {
+    if (lane_fault) __hip_atomic_fetch_max(fault, lane_fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -936,11 +1159,24 @@ inline int64_t reduce_head(const float* in, int64_t n) {
 // element by element, in sequence order after the halves. loose(x, kept, index): head and tail
 // elements (last workgroup, out of order). The steps run a workgroup-uniform number of times, so
 // their kept elements are counted per wave with ballots (scalar work) and credited to lane 0.
+// int32 modes: *fault (per thread) becomes the largest ~(4 * index + kind) over the elements
+// that throw, 0 if none.
 template <int RD, class Half, class Single, class Loose>
 __device__ __attribute__((always_inline)) inline int64_t visit_chunk(const dc_linq_chain& prog, const AffineChain& aff,
                                                                      const RdConst& canon, const float* __restrict__ in,
                                                                      int64_t n, int64_t h, Half&& half, Single&& single,
-                                                                     Loose&& loose) {
+                                                                     Loose&& loose, uint64_t* fault = nullptr) {
+  uint64_t lane_fault = 0;
+  // Folds the first exception of a group of elements into lane_fault; index_of(b) = the
+  // sequence index of the group's element b (increasing with b).
+  auto note = [&](const Faults& f, auto index_of) __attribute__((always_inline)) {
+    if constexpr (rd_is_int(RD)) {
+      const int b = __builtin_ctz(f.hit | 0x80000000u);
+      const uint64_t code = (uint64_t)index_of(b) * 4u +
+                            (((f.ovf >> b) & 1u) ? DC_LINQ_FAULT_OVERFLOW : DC_LINQ_FAULT_DIVIDE_BY_ZERO);
+      lane_fault = max(lane_fault, f.hit ? ~code : (uint64_t)0);
+    }
+  };
   const int64_t n4 = (n - h) >> 2;
   const int64_t per = (n4 + gridDim.x - 1) / gridDim.x;
   const int64_t v0 = min(n4, (int64_t)blockIdx.x * per), v1 = min(n4, v0 + per);
@@ -964,10 +1200,13 @@ __device__ __attribute__((always_inline)) inline int64_t visit_chunk(const dc_li
         e[4 * m + 2] = v[4 * g + m].z;
         e[4 * m + 3] = v[4 * g + m].w;
       }
-      apply_reduce_flags<RD, 16>(prog, aff, canon, e, kept);
+      Faults f;
+      eval_flags<RD, 16>(prog, aff, canon, e, kept, 0xFFFFu, f);
+      const int64_t base = i + (int64_t)(4 * g) * kSumBlock;
+      note(f, [&](int b) { return h + 4 * (base + (int64_t)(b >> 2) * kSumBlock) + (b & 3); });
 #pragma unroll
       for (int j = 0; j < 16; ++j) wave_cnt += (uint64_t)__builtin_popcountll(__ballot(kept[j]));
-      half(e, kept, i + (int64_t)(4 * g) * kSumBlock);
+      half(e, kept, base);
     }
   }
   if ((threadIdx.x & (dc::kWave - 1)) == 0) cnt += (int64_t)wave_cnt;
@@ -975,7 +1214,9 @@ __device__ __attribute__((always_inline)) inline int64_t visit_chunk(const dc_li
     const dc::f32x4 x = dc::load_stream(xa + i);
     float e[4] = {x.x, x.y, x.z, x.w};
     bool kept[4];
-    apply_reduce_flags<RD, 4>(prog, aff, canon, e, kept);
+    Faults f;
+    eval_flags<RD, 4>(prog, aff, canon, e, kept, 0xFu, f);
+    note(f, [&](int b) { return h + 4 * i + b; });
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       single(e[j], kept[j], h + 4 * i + j);
@@ -986,13 +1227,16 @@ __device__ __attribute__((always_inline)) inline int64_t visit_chunk(const dc_li
     auto one = [&](int64_t s) __attribute__((always_inline)) {
       float e[1] = {in[s]};
       bool kept[1];
-      apply_reduce_flags<RD, 1>(prog, aff, canon, e, kept);
+      Faults f;
+      eval_flags<RD, 1>(prog, aff, canon, e, kept, 1u, f);
+      note(f, [&](int) { return s; });
       loose(e[0], kept[0], s);
       cnt += kept[0] ? 1 : 0;
     };
     for (int64_t s = threadIdx.x; s < h; s += kSumBlock) one(s);
     for (int64_t s = h + 4 * n4 + threadIdx.x; s < n; s += kSumBlock) one(s);
   }
+  if (fault) *fault = lane_fault;
   return cnt;
 }
 
@@ -1068,6 +1312,281 @@ unsigned where_select_sum_grid(const dc_hip_ctx* ctx, int64_t n) {
 }
 
 
+// ---- Where/Select -> Sum / Count over int32 ------------------------------------------------------
+// After Where/Select the reference's Sum() runs Enumerable.Sum over an iterator, which adds element
+// by element with checked int32 adds: OverflowException as soon as a prefix sum of the kept, mapped
+// elements (in sequence order) leaves int32. Pass 1 gives each workgroup one contiguous chunk of the
+// aligned region (as the float Sum does) and sums the chunk's positive parts and negative parts
+// separately (exact and order-free); the loose head and tail elements form two more chunks, the
+// first and last in sequence order. Every prefix inside a chunk lies in [S - neg, S + pos], S being
+// the prefix before the chunk, and S + pos - neg is itself a prefix (the chunk's end). Pass 2 (one
+// workgroup) scans the chunk sums in sequence order: a chunk end outside int32 is an overflow; a
+// chunk whose bounds leave int32 while its end does not is re-checked exactly (its elements
+// re-read and re-evaluated in sequence order, combining (sum, max prefix, min prefix) in order).
+// The screen clears chunks whose running totals stay well inside int32 (the common case), so the
+// exact check is the exception.
+enum MinMaxOp : int { kOpMin = DC_LINQ_MIN, kOpMax = DC_LINQ_MAX };
+constexpr int kI32Fields = 4;  // per chunk: pos, neg (a magnitude), kept count, ~first fault code
+
+__device__ inline void add_parts(uint64_t& pos, uint64_t& neg, int32_t x) {
+  pos += (uint32_t)max(x, 0);
+  neg += 0u - (uint32_t)min(x, 0);  // |x| of a negative x, 2^31 for int.MinValue
+}
+
+template <int RD>
+__global__ __launch_bounds__(kSumBlock) void where_select_sum_i32_pass1(const dc_linq_chain prog,
+                                                                        const float* __restrict__ in, int64_t n,
+                                                                        int64_t h, int64_t* __restrict__ part) {
+  __shared__ int64_t lds[kSumBlock / dc::kWave];
+  __shared__ unsigned long long s_fault;
+  const int G = gridDim.x, C = G + 2;  // chunk c of workgroup c; G = head, G + 1 = tail
+  uint64_t pos = 0, neg = 0, hpos = 0, hneg = 0, tpos = 0, tneg = 0, fault = 0;
+  const AffineChain aff{};
+  const RdConst canon{0.0f, 1.0f, -0.0f};
+  const int64_t cnt = visit_chunk<RD>(
+      prog, aff, canon, in, n, h,
+      [&](const float (&e)[16], const bool (&kept)[16], int64_t) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) add_parts(pos, neg, kept[j] ? __builtin_bit_cast(int32_t, e[j]) : 0);
+      },
+      [&](float x, bool kept, int64_t) __attribute__((always_inline)) {
+        add_parts(pos, neg, kept ? __builtin_bit_cast(int32_t, x) : 0);
+      },
+      [&](float x, bool kept, int64_t i) __attribute__((always_inline)) {
+        const int32_t v = kept ? __builtin_bit_cast(int32_t, x) : 0;
+        if (i < h) add_parts(hpos, hneg, v);
+        else add_parts(tpos, tneg, v);
+      },
+      &fault);
+  if (threadIdx.x == 0) s_fault = 0;
+  const int64_t bpos = dc::block_sum64<kSumBlock>((int64_t)pos, lds);
+  const int64_t bneg = dc::block_sum64<kSumBlock>((int64_t)neg, lds);
+  const int64_t bcnt = dc::block_sum64<kSumBlock>(cnt, lds);
+  if (fault) atomicMax(&s_fault, (unsigned long long)fault);
+  const bool last = blockIdx.x == (unsigned)G - 1u;  // uniform: the block sums below are collective
+  int64_t lp[4] = {0, 0, 0, 0};
+  if (last) {
+    lp[0] = dc::block_sum64<kSumBlock>((int64_t)hpos, lds);
+    lp[1] = dc::block_sum64<kSumBlock>((int64_t)hneg, lds);
+    lp[2] = dc::block_sum64<kSumBlock>((int64_t)tpos, lds);
+    lp[3] = dc::block_sum64<kSumBlock>((int64_t)tneg, lds);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int b = blockIdx.x;
+    part[b] = bpos;
+    part[C + b] = bneg;
+    part[2 * C + b] = bcnt;  // the loose elements' kept count is in the last chunk's count
+    part[3 * C + b] = (int64_t)s_fault;
+    if (last) {
+      part[G] = lp[0];
+      part[C + G] = lp[1];
+      part[G + 1] = lp[2];
+      part[C + G + 1] = lp[3];
+      part[2 * C + G] = part[2 * C + G + 1] = 0;
+      part[3 * C + G] = part[3 * C + G + 1] = 0;
+    }
+  }
+}
+
+__device__ inline bool fits_i32(int64_t v) { return v >= (int64_t)INT32_MIN && v <= (int64_t)INT32_MAX; }
+
+template <int RD>
+__global__ __launch_bounds__(kFinalBlock) void where_select_sum_i32_pass2(
+    const dc_linq_chain prog, const float* __restrict__ in, int64_t n, int64_t h, const int64_t* __restrict__ part,
+    int G, int64_t* __restrict__ sum_out, int64_t* __restrict__ count_out, int32_t* __restrict__ overflow_out,
+    int64_t* __restrict__ fault_out) {
+  constexpr int W = kFinalBlock / dc::kWave;
+  __shared__ int64_t lds[W];
+  __shared__ int64_t wpre[W];
+  __shared__ unsigned long long s_fault;
+  __shared__ int s_ovf, s_nflag;
+  __shared__ int s_flag[kFinalBlock];
+  __shared__ int64_t s_start[kFinalBlock];
+  __shared__ int64_t tr_s[kFinalBlock], tr_max[kFinalBlock], tr_min[kFinalBlock];
+  const int C = G + 2;
+  const int t = threadIdx.x, lane = t & (dc::kWave - 1), wave = t / dc::kWave;
+  // sequence slot t: 0 = head, 1 .. G = chunk t - 1, G + 1 = tail
+  const int c = t == 0 ? G : (t <= G ? t - 1 : (t == G + 1 ? G + 1 : -1));
+  int64_t pos = 0, neg = 0, cnt = 0;
+  uint64_t fault = 0;
+  if (c >= 0) {
+    pos = part[c];
+    neg = part[C + c];
+    cnt = part[2 * C + c];
+    fault = (uint64_t)part[3 * C + c];
+  }
+  if (t == 0) {
+    s_fault = 0;
+    s_ovf = 0;
+    s_nflag = 0;
+  }
+  const int64_t sum = pos - neg;
+  // exclusive scan of the chunk sums in sequence order: within each wave, then over the wave totals
+  const int64_t incl = dc::wave_inclusive_scan64(sum);
+  if (lane == dc::kWave - 1) lds[wave] = incl;
+  __syncthreads();
+  if (t == 0) {
+    int64_t run = 0;
+    for (int w = 0; w < W; ++w) {
+      wpre[w] = run;
+      run += lds[w];
+    }
+  }
+  __syncthreads();
+  const int64_t S = wpre[wave] + incl - sum;
+  if (fault) atomicMax(&s_fault, (unsigned long long)fault);
+  bool flagged = false;
+  if (c >= 0) {
+    if (!fits_i32(S + sum)) atomicOr(&s_ovf, 1);
+    else if (!fits_i32(S + pos) || !fits_i32(S - neg)) flagged = true;
+  }
+  const int64_t total = dc::block_sum64<kFinalBlock>(sum, lds);
+  const int64_t total_cnt = dc::block_sum64<kFinalBlock>(cnt, lds);
+  if (flagged) {
+    const int k = atomicAdd(&s_nflag, 1);
+    s_flag[k] = t;
+    s_start[k] = S;
+  }
+  __syncthreads();
+  const int64_t n4 = (n - h) >> 2;
+  const int64_t per = (n4 + G - 1) / G;
+  const AffineChain aff{};
+  const RdConst canon{0.0f, 1.0f, -0.0f};
+  // Exact check of the flagged chunks (none when a fault or an overflow is already known).
+  for (int k = 0; k < s_nflag && s_fault == 0 && s_ovf == 0; ++k) {
+    const int slot = s_flag[k];
+    int64_t a, b;
+    if (slot == 0) {
+      a = 0;
+      b = h;
+    } else if (slot == G + 1) {
+      a = h + 4 * n4;
+      b = n;
+    } else {
+      const int64_t v0 = min(n4, (int64_t)(slot - 1) * per), v1 = min(n4, v0 + per);
+      a = h + 4 * v0;
+      b = h + 4 * v1;
+    }
+    const int64_t piece = (b - a + kFinalBlock - 1) / kFinalBlock;
+    const int64_t i0 = min(b, a + t * piece), i1 = min(b, i0 + piece);
+    int64_t rs = 0, mx = 0, mn = 0;  // prefix relative to the chunk start, its max and min (empty prefix included)
+    for (int64_t i = i0; i < i1; ++i) {
+      float e[1] = {in[i]};
+      bool kept[1];
+      Faults f;
+      eval_flags<RD, 1>(prog, aff, canon, e, kept, 1u, f);
+      rs += kept[0] ? (int64_t)__builtin_bit_cast(int32_t, e[0]) : 0;
+      mx = max(mx, rs);
+      mn = min(mn, rs);
+    }
+    tr_s[t] = rs;
+    tr_max[t] = mx;
+    tr_min[t] = mn;
+    __syncthreads();
+    for (int stride = 1; stride < kFinalBlock; stride <<= 1) {
+      if ((t & (2 * stride - 1)) == 0) {  // (left = t, right = t + stride), in sequence order
+        const int r = t + stride;
+        const int64_t ls = tr_s[t];
+        tr_max[t] = max(tr_max[t], ls + tr_max[r]);
+        tr_min[t] = min(tr_min[t], ls + tr_min[r]);
+        tr_s[t] = ls + tr_s[r];
+      }
+      __syncthreads();
+    }
+    if (t == 0 && (!fits_i32(s_start[k] + tr_max[0]) || !fits_i32(s_start[k] + tr_min[0]))) s_ovf = 1;
+    __syncthreads();
+  }
+  if (t == 0) {
+    if (sum_out) *sum_out = total;
+    if (count_out) *count_out = total_cnt;
+    if (overflow_out) *overflow_out = s_ovf;
+    if (fault_out) *fault_out = s_fault ? (int64_t)~(uint64_t)s_fault : (int64_t)DC_LINQ_FAULT_NONE;
+  }
+}
+
+// ---- Where/Select -> Min / Max over int32 --------------------------------------------------------
+// Math.Min/Max over int32 has no ties to break (equal elements are the same value) and no NaN, so a
+// plain min/max tree is the enumerator's result.
+template <int OP>
+__device__ inline int32_t pick(int32_t a, int32_t b) { return OP == kOpMin ? min(a, b) : max(a, b); }
+
+template <int OP, int BLOCK>
+__device__ inline int32_t block_pick(int32_t v, int32_t* scratch) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = pick<OP>(v, __shfl_xor(v, off, 64));
+  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
+  __syncthreads();
+  v = scratch[0];
+  for (int w = 1; w < BLOCK / dc::kWave; ++w) v = pick<OP>(v, scratch[w]);
+  __syncthreads();
+  return v;
+}
+
+template <int RD, int OP>
+__global__ __launch_bounds__(kSumBlock) void where_select_minmax_i32_pass1(const dc_linq_chain prog,
+                                                                           const float* __restrict__ in, int64_t n,
+                                                                           int64_t h, int64_t* __restrict__ part) {
+  __shared__ int64_t lds[kSumBlock / dc::kWave];
+  __shared__ int32_t lds_v[kSumBlock / dc::kWave];
+  __shared__ unsigned long long s_fault;
+  const int G = gridDim.x;
+  int32_t best = OP == kOpMin ? INT32_MAX : INT32_MIN;  // the identity: an empty chunk changes nothing
+  uint64_t fault = 0;
+  auto take = [&](float x, bool kept) __attribute__((always_inline)) {
+    best = kept ? pick<OP>(best, __builtin_bit_cast(int32_t, x)) : best;
+  };
+  const AffineChain aff{};
+  const RdConst canon{0.0f, 1.0f, -0.0f};
+  const int64_t cnt = visit_chunk<RD>(
+      prog, aff, canon, in, n, h,
+      [&](const float (&e)[16], const bool (&kept)[16], int64_t) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) take(e[j], kept[j]);
+      },
+      [&](float x, bool kept, int64_t) __attribute__((always_inline)) { take(x, kept); },
+      [&](float x, bool kept, int64_t) __attribute__((always_inline)) { take(x, kept); }, &fault);
+  if (threadIdx.x == 0) s_fault = 0;
+  const int32_t bbest = block_pick<OP, kSumBlock>(best, lds_v);
+  const int64_t bcnt = dc::block_sum64<kSumBlock>(cnt, lds);
+  if (fault) atomicMax(&s_fault, (unsigned long long)fault);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    part[blockIdx.x] = bbest;
+    part[G + blockIdx.x] = bcnt;
+    part[2 * G + blockIdx.x] = (int64_t)s_fault;
+  }
+}
+
+template <int OP>
+__global__ __launch_bounds__(kFinalBlock) void where_select_minmax_i32_pass2(const int64_t* __restrict__ part, int G,
+                                                                             int32_t* __restrict__ value_out,
+                                                                             int64_t* __restrict__ count_out,
+                                                                             int64_t* __restrict__ fault_out) {
+  __shared__ int64_t lds[kFinalBlock / dc::kWave];
+  __shared__ int32_t lds_v[kFinalBlock / dc::kWave];
+  __shared__ unsigned long long s_fault;
+  int32_t v = OP == kOpMin ? INT32_MAX : INT32_MIN;
+  int64_t c = 0;
+  uint64_t fault = 0;
+  for (int b = threadIdx.x; b < G; b += kFinalBlock) {
+    v = pick<OP>(v, (int32_t)part[b]);
+    c += part[G + b];
+    fault = max(fault, (uint64_t)part[2 * G + b]);
+  }
+  if (threadIdx.x == 0) s_fault = 0;
+  const int32_t bv = block_pick<OP, kFinalBlock>(v, lds_v);
+  const int64_t bc = dc::block_sum64<kFinalBlock>(c, lds);
+  if (fault) atomicMax(&s_fault, (unsigned long long)fault);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    if (value_out) *value_out = bv;
+    if (count_out) *count_out = bc;
+    if (fault_out) *fault_out = s_fault ? (int64_t)~(uint64_t)s_fault : (int64_t)DC_LINQ_FAULT_NONE;
+  }
+}
+
+
 // Scratch of dc_hip_linq_where_select_sum_f32_noalloc: one launch's per-workgroup partials (a
 // float64 sum and an int64 count per workgroup, at most kSumBlocksMax workgroups), 16 KiB. One copy
 // per GPU, held until the process ends; every call on a GPU uses it, so calls that overlap on one
@@ -1107,7 +1626,6 @@ namespace {
 // combination breaks ties by index. That combination is commutative and associative, so the grid's
 // result is the enumerator's bit for bit (signed zeros and NaN payloads included), whatever the
 // order in which lanes, waves and workgroups meet. An index of -1 marks "no element yet".
-enum MinMaxOp : int { kOpMin = DC_LINQ_MIN, kOpMax = DC_LINQ_MAX };
 
 template <int OP>
 __device__ inline void mm_take(float& v, int64_t& i, float cv, int64_t ci) {
@@ -1310,13 +1828,16 @@ __global__ __launch_bounds__(kFinalBlock) void where_select_minmax_pass2(const f
 // ---- strategy choice -----------------------------------------------------------------------------
 const void* rounds_kernel(int mode) {
   const void* fn = nullptr;
-  rd_dispatch(mode, [&](auto m) { fn = reinterpret_cast<const void*>(&where_select_rounds_kernel<decltype(m)::value>); });
+  auto pick = [&](auto m) { fn = reinterpret_cast<const void*>(&where_select_rounds_kernel<decltype(m)::value>); };
+  if (rd_is_int(mode)) rd_dispatch_i32(mode, pick);
+  else rd_dispatch(mode, pick);
   return fn;
 }
 
-// Every program variant (rd_dispatch's cases).
+// Every program variant (rd_dispatch's and rd_dispatch_i32's cases).
 std::vector<int> all_reduce_modes() {
-  std::vector<int> m = {kRdInterp, kRdInterpSaves, kRdAffine, rd_canon(kShapeM, DC_LQ_CMP_GT)};
+  std::vector<int> m = {kRdInterp, kRdInterpSaves, kRdAffine, kRdInterpI32, kRdInterpI32Saves,
+                        rd_canon(kShapeM, DC_LQ_CMP_GT)};
   for (int shape : {kShapeF, kShapeFM, kShapeMF})
     for (int cmp = DC_LQ_CMP_GT; cmp <= DC_LQ_CMP_NE; ++cmp) m.push_back(rd_canon(shape, cmp));
   return m;
@@ -1343,6 +1864,84 @@ bool use_rounds(dc_hip_ctx* ctx, const float* input, int64_t n) {
   return ctx->rounds_fit == 1;
 }
 
+// ToArray for both element types (the caller holds the context lock and has validated the chain):
+// the round-robin kernel for large aligned inputs, else the ticket-ordered lookback kernel. int32
+// programs publish their exceptions into the context's fault word.
+int32_t launch_to_array(dc_hip_ctx* ctx, const dc_linq_chain* chain, bool is_int, const float* input, int64_t n,
+                        float* output, int64_t* count_out) {
+  uint64_t* fault_word = reinterpret_cast<uint64_t*>(ctx->counters + DC_SLOT_LINQ_FAULT);
+  if ((chain->flags & DC_LINQ_FLAG_ORDERED_GRID) == 0 && use_rounds(ctx, input, n)) {
+    const ReducePlan plan = is_int ? reduce_plan_i32(*chain) : reduce_plan(*chain);
+    const void* fn = rounds_kernel(plan.mode);
+    AffineChain aff = plan.aff;
+    RdConst canon = plan.k;
+    const uint32_t groups = rounds_groups(ctx);
+    const int64_t tiles = (n + kRrTile - 1) / kRrTile;
+    const size_t words = (size_t)((tiles + groups - 1) / groups + 1) * groups;
+    uint32_t epoch16 = 0;
+    DC_RETURN_IF(dc::ensure_round_counts(ctx, words, &epoch16));
+    dc_linq_chain prog = *chain;
+    const float* in_arg = input;
+    int64_t n_arg = n;
+    float* out_arg = output;
+    int64_t* count_arg = count_out;
+    uint32_t* counts_arg = ctx->round_counts;
+    uint32_t groups_arg = groups;
+    uint32_t* done_arg = ctx->counters + DC_SLOT_LINQ_DONE;
+    uint64_t* fault_arg = fault_word;
+    void* args[] = {&prog,  &aff,       &canon,   &in_arg,   &n_arg,     &out_arg, &count_arg,
+                    &counts_arg, &epoch16, &groups_arg, &done_arg, &fault_arg};
+    // One workgroup per CU, each needing most of a CU's LDS, on an otherwise idle device: every
+    // workgroup is resident at once (an ordinary launch; measured faster than a cooperative one).
+    dc::ResidentLaunch resident(ctx);
+    DC_RETURN_IF(resident.status());
+    DC_RETURN_IF_HIP(hipLaunchKernel(fn, dim3(groups), dim3(kRrBlock), args, 0, ctx->stream));
+    DC_RETURN_IF(dc::last_launch_status());
+    resident.done();
+    return DC_OK;
+  }
+
+  AffineChain aff{};
+  const bool saves = program_uses_saves(*chain);
+  const bool affine = !is_int && lower_affine(*chain, &aff);
+  const int mode = is_int ? (saves ? kModeInterpI32Saves : kModeInterpI32)
+                          : affine ? kModeAffine : (saves ? kModeInterpSaves : kModeInterp);
+  const int64_t tiles = std::max<int64_t>(1, (n + kTile - 1) / kTile);
+  if (tiles > 0x7FFFFFFFll) return DC_ERR_INVALID_ARGUMENT;
+  uint32_t epoch = 0;
+  DC_RETURN_IF(dc::ensure_status(ctx, (size_t)tiles, &epoch));
+  auto kernel = mode == kModeAffine            ? where_select_kernel<kModeAffine>
+              : mode == kModeInterpSaves       ? where_select_kernel<kModeInterpSaves>
+              : mode == kModeInterpI32         ? where_select_kernel<kModeInterpI32>
+              : mode == kModeInterpI32Saves    ? where_select_kernel<kModeInterpI32Saves>
+                                               : where_select_kernel<kModeInterp>;
+  kernel<<<(unsigned)tiles, kBlock, 0, ctx->stream>>>(*chain, aff, input, n, output, count_out, ctx->status,
+                                                      ctx->counters + DC_SLOT_LINQ_TICKET, epoch, (uint32_t)tiles,
+                                                      dc::aligned16(input) ? 1 : 0, fault_word);
+  return dc::last_launch_status();
+}
+
+// Structural validation plus the int32 rule: no SQRT / FLOOR / CEIL / ROUND (no int form).
+int32_t validate_i32(const dc_linq_chain* chain) {
+  DC_RETURN_IF(dc_linq_chain_validate(chain));
+  for (int i = 0; i < chain->n_instr; ++i) {
+    const uint8_t op = chain->code[i].op;
+    if (op == DC_LQ_SQRT || op == DC_LQ_FLOOR || op == DC_LQ_CEIL || op == DC_LQ_ROUND) return DC_ERR_UNSUPPORTED;
+  }
+  return DC_OK;
+}
+
+bool can_fault_i32(const dc_linq_chain& chain) {
+  for (int i = 0; i < chain.n_instr; ++i) {
+    const dc_linq_instr& in = chain.code[i];
+    if (in.op == DC_LQ_ABS || in.op == DC_LQ_RDIV || in.op == DC_LQ_RREM) return true;
+    if ((in.op == DC_LQ_DIV || in.op == DC_LQ_REM) &&
+        (in.src != DC_LQ_SRC_IMM || in.imm_i32 == 0 || in.imm_i32 == -1))
+      return true;
+  }
+  return false;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1354,7 +1953,7 @@ DC_HIP_API int32_t dc_linq_chain_validate(const dc_linq_chain* chain) {
     return DC_ERR_INVALID_ARGUMENT;
   for (int i = 0; i < chain->n_instr; ++i) {
     const dc_linq_instr& in = chain->code[i];
-    const bool op_ok = (in.op <= DC_LQ_STORE_S1) || (in.op >= DC_LQ_CMP_GT && in.op <= DC_LQ_MAP);
+    const bool op_ok = (in.op <= DC_LQ_ROUND) || (in.op >= DC_LQ_CMP_GT && in.op <= DC_LQ_MAP);
     if (!op_ok || in.src > DC_LQ_SRC_S1) return DC_ERR_UNSUPPORTED;
     if (in.op >= DC_LQ_CMP_GT && in.op <= DC_LQ_CMP_NE && in.mode > DC_LQ_CMP_OR) return DC_ERR_UNSUPPORTED;
   }
@@ -1375,49 +1974,80 @@ DC_HIP_API int32_t dc_hip_linq_where_select_f32(dc_hip_ctx* ctx, const dc_linq_c
   DC_RETURN_IF(dc_linq_chain_validate(chain));
   if (n >= (int64_t)1 << 40) return DC_ERR_INVALID_ARGUMENT;  // 40-bit counts in the status words
   DC_CTX_ENTER(ctx);
-  if ((chain->flags & DC_LINQ_FLAG_ORDERED_GRID) == 0 && use_rounds(ctx, input, n)) {
-    const ReducePlan plan = reduce_plan(*chain);
-    const void* fn = rounds_kernel(plan.mode);
-    AffineChain aff = plan.aff;
-    RdConst canon = plan.k;
-    const uint32_t groups = rounds_groups(ctx);
-    const int64_t tiles = (n + kRrTile - 1) / kRrTile;
-    const size_t words = (size_t)((tiles + groups - 1) / groups + 1) * groups;
-    uint32_t epoch16 = 0;
-    DC_RETURN_IF(dc::ensure_round_counts(ctx, words, &epoch16));
-    dc_linq_chain prog = *chain;
-    const float* in_arg = input;
-    int64_t n_arg = n;
-    float* out_arg = output;
-    int64_t* count_arg = count_out;
-    uint32_t* counts_arg = ctx->round_counts;
-    uint32_t groups_arg = groups;
-    uint32_t* done_arg = ctx->counters + DC_SLOT_LINQ_DONE;
-    void* args[] = {&prog, &aff, &canon, &in_arg, &n_arg, &out_arg, &count_arg, &counts_arg, &epoch16, &groups_arg,
-                    &done_arg};
-    // One workgroup per CU, each needing most of a CU's LDS, on an otherwise idle device: every
-    // workgroup is resident at once (an ordinary launch; measured faster than a cooperative one).
-    dc::ResidentLaunch resident(ctx);
-    DC_RETURN_IF(resident.status());
-    DC_RETURN_IF_HIP(hipLaunchKernel(fn, dim3(groups), dim3(kRrBlock), args, 0, ctx->stream));
-    DC_RETURN_IF(dc::last_launch_status());
-    resident.done();
-    return DC_OK;
-  }
+  return launch_to_array(ctx, chain, false, input, n, output, count_out);
+}
 
-  AffineChain aff{};
-  const bool affine = lower_affine(*chain, &aff);
-  const int mode = affine ? kModeAffine : (program_uses_saves(*chain) ? kModeInterpSaves : kModeInterp);
-  const int64_t tiles = std::max<int64_t>(1, (n + kTile - 1) / kTile);
-  if (tiles > 0x7FFFFFFFll) return DC_ERR_INVALID_ARGUMENT;
-  uint32_t epoch = 0;
-  DC_RETURN_IF(dc::ensure_status(ctx, (size_t)tiles, &epoch));
-  auto kernel = mode == kModeAffine ? where_select_kernel<kModeAffine>
-              : mode == kModeInterpSaves ? where_select_kernel<kModeInterpSaves>
-                                         : where_select_kernel<kModeInterp>;
-  kernel<<<(unsigned)tiles, kBlock, 0, ctx->stream>>>(*chain, aff, input, n, output, count_out, ctx->status,
-                                                      ctx->counters + DC_SLOT_LINQ_TICKET, epoch, (uint32_t)tiles,
-                                                      dc::aligned16(input) ? 1 : 0);
+DC_HIP_API int32_t dc_linq_chain_can_fault_i32(const dc_linq_chain* chain, int32_t* can_fault_out) {
+  if (!can_fault_out) return DC_ERR_INVALID_ARGUMENT;
+  DC_RETURN_IF(validate_i32(chain));
+  *can_fault_out = can_fault_i32(*chain) ? 1 : 0;
+  return DC_OK;
+}
+
+DC_HIP_API int32_t dc_hip_linq_where_select_i32(dc_hip_ctx* ctx, const dc_linq_chain* chain, const int32_t* input,
+                                                int64_t n, int32_t* output, int64_t* count_out, int64_t* fault_out) {
+  if (n < 0 || !count_out || (n > 0 && (!input || !output))) return DC_ERR_INVALID_ARGUMENT;
+  DC_RETURN_IF(validate_i32(chain));
+  if (!fault_out && can_fault_i32(*chain)) return DC_ERR_INVALID_ARGUMENT;
+  if (n >= (int64_t)1 << 40) return DC_ERR_INVALID_ARGUMENT;  // 40-bit counts in the status words
+  DC_CTX_ENTER(ctx);
+  DC_RETURN_IF(launch_to_array(ctx, chain, true, reinterpret_cast<const float*>(input), n,
+                               reinterpret_cast<float*>(output), count_out));
+  if (fault_out) {
+    fault_finish_kernel<<<1, 1, 0, ctx->stream>>>(reinterpret_cast<uint64_t*>(ctx->counters + DC_SLOT_LINQ_FAULT),
+                                                  fault_out);
+    DC_RETURN_IF(dc::last_launch_status());
+  }
+  return DC_OK;
+}
+
+DC_HIP_API int32_t dc_hip_linq_where_select_sum_i32(dc_hip_ctx* ctx, const dc_linq_chain* chain, const int32_t* input,
+                                                    int64_t n, int64_t* sum_out, int64_t* count_out,
+                                                    int32_t* overflow_out, int64_t* fault_out) {
+  if (n < 0 || (n > 0 && !input)) return DC_ERR_INVALID_ARGUMENT;
+  if (n >= ((int64_t)1 << 32)) return DC_ERR_INVALID_ARGUMENT;  // int64 partial sums stay exact below 2^32 elements
+  DC_RETURN_IF(validate_i32(chain));
+  if (!fault_out && can_fault_i32(*chain)) return DC_ERR_INVALID_ARGUMENT;
+  DC_CTX_ENTER(ctx);
+  const unsigned grid = std::min<unsigned>(where_select_sum_grid(ctx, n), kFinalBlock - 2);
+  DC_RETURN_IF(dc::ensure_partials(ctx, (size_t)(grid + 2) * kI32Fields * sizeof(int64_t)));
+  int64_t* part = static_cast<int64_t*>(ctx->partials);
+  const float* in = reinterpret_cast<const float*>(input);
+  const int64_t h = reduce_head(in, n);
+  rd_dispatch_i32(reduce_plan_i32(*chain).mode, [&](auto mode) {
+    constexpr int RD = decltype(mode)::value;
+    where_select_sum_i32_pass1<RD><<<grid, kSumBlock, 0, ctx->stream>>>(*chain, in, n, h, part);
+    where_select_sum_i32_pass2<RD><<<1, kFinalBlock, 0, ctx->stream>>>(*chain, in, n, h, part, (int)grid, sum_out,
+                                                                      count_out, overflow_out, fault_out);
+  });
+  return dc::last_launch_status();
+}
+
+DC_HIP_API int32_t dc_hip_linq_where_select_minmax_i32(dc_hip_ctx* ctx, const dc_linq_chain* chain,
+                                                       const int32_t* input, int64_t n, int32_t op, int32_t* value_out,
+                                                       int64_t* count_out, int64_t* fault_out) {
+  if (n < 0 || (n > 0 && !input) || (op != DC_LINQ_MIN && op != DC_LINQ_MAX)) return DC_ERR_INVALID_ARGUMENT;
+  DC_RETURN_IF(validate_i32(chain));
+  if (!fault_out && can_fault_i32(*chain)) return DC_ERR_INVALID_ARGUMENT;
+  DC_CTX_ENTER(ctx);
+  const unsigned grid = where_select_sum_grid(ctx, n);
+  DC_RETURN_IF(dc::ensure_partials(ctx, (size_t)grid * 3 * sizeof(int64_t)));
+  int64_t* part = static_cast<int64_t*>(ctx->partials);
+  const float* in = reinterpret_cast<const float*>(input);
+  const int64_t h = reduce_head(in, n);
+  rd_dispatch_i32(reduce_plan_i32(*chain).mode, [&](auto mode) {
+    constexpr int RD = decltype(mode)::value;
+    if (op == DC_LINQ_MIN)
+      where_select_minmax_i32_pass1<RD, kOpMin><<<grid, kSumBlock, 0, ctx->stream>>>(*chain, in, n, h, part);
+    else
+      where_select_minmax_i32_pass1<RD, kOpMax><<<grid, kSumBlock, 0, ctx->stream>>>(*chain, in, n, h, part);
+  });
+  if (op == DC_LINQ_MIN)
+    where_select_minmax_i32_pass2<kOpMin><<<1, kFinalBlock, 0, ctx->stream>>>(part, (int)grid, value_out, count_out,
+                                                                             fault_out);
+  else
+    where_select_minmax_i32_pass2<kOpMax><<<1, kFinalBlock, 0, ctx->stream>>>(part, (int)grid, value_out, count_out,
+                                                                             fault_out);
   return dc::last_launch_status();
 }
 

@@ -308,10 +308,88 @@ class KernelEmitter:
         return "\n".join(lines)
 
 
+def _is_work_index(e, idx_names: set) -> bool:
+    return (isinstance(e, cs.Intrinsic) and e.kind == "ThreadId" and e.axis == "X") or \
+        (isinstance(e, cs.Name) and e.ident in idx_names)
+
+
+def _walk(node):
+    """Every statement and expression node under `node`."""
+    yield node
+    if isinstance(node, list):
+        for x in node:
+            yield from _walk(x)
+        return
+    for v in getattr(node, "__dict__", {}).values():
+        if isinstance(v, (cs.Stmt, cs.Expr, list)):
+            yield from _walk(v)
+        elif isinstance(v, tuple):
+            for x in v:
+                if isinstance(x, (cs.Stmt, cs.Expr, list)):
+                    yield from _walk(x)
+
+
+def covered_buffers(km: KernelMethod, dims: int) -> set:
+    """Buffers whose every element the body writes: a 1-D kernel whose work size is the buffer's
+    length (the orchestrator sizes the work by the first writable span) and whose body assigns
+    `buf[i] = ...` as an unconditional top-level statement, i being KernelContext.ThreadId.X or a
+    local initialised from it and never assigned again, optionally under `if (i < buf.Length)` with
+    no else, and with no `return` before it. Such a buffer need not be copied to the device before
+    the launch: nothing of its old contents can come back. Every other written buffer is copied in,
+    as the reference copies every array (KernelExecutionService.cs:755-763)."""
+    if dims != 1:
+        return set()
+    writable = [p for p in km.params if p.is_buffer and not p.read_only]
+    if not writable:
+        return set()
+    w = writable[0].name
+    body = km.body.body
+    idx_names = set()
+    for s in body:
+        if isinstance(s, cs.LocalDecl):
+            for name, init in s.names:
+                if init is not None and _is_work_index(init, set()):
+                    idx_names.add(name)
+    for node in _walk(body):  # an index variable assigned again is no longer the work index
+        if isinstance(node, cs.Assign) and isinstance(node.target, cs.Name):
+            idx_names.discard(node.target.ident)
+        if isinstance(node, cs.Unary) and node.op in ("++", "--") and isinstance(node.expr, cs.Name):
+            idx_names.discard(node.expr.ident)
+
+    def is_full_write(st) -> bool:
+        return isinstance(st, cs.ExprStmt) and isinstance(st.expr, cs.Assign) and st.expr.op == "=" and \
+            isinstance(st.expr.target, cs.Index) and st.expr.target.buffer == w and \
+            _is_work_index(st.expr.target.index, idx_names)
+
+    def has_return(st) -> bool:
+        return any(isinstance(n, cs.Return) for n in _walk(st))
+
+    def first_write(stmts) -> bool:
+        for st in stmts:
+            if is_full_write(st):
+                return True
+            if has_return(st):
+                return False
+        return False
+
+    for st in body:
+        if is_full_write(st):
+            return {w}
+        if isinstance(st, cs.If) and st.other is None and isinstance(st.cond, cs.Binary) and st.cond.op == "<" and \
+                _is_work_index(st.cond.left, idx_names) and isinstance(st.cond.right, cs.Length) and \
+                st.cond.right.buffer == w:
+            inner = st.then.body if isinstance(st.then, cs.Block) else [st.then]
+            if first_write(inner):
+                return {w}
+        if has_return(st):
+            return set()
+    return set()
+
+
 def translate(km: KernelMethod, entry: str) -> dict:
     """Returns the registry record of one kernel, with HIP source when the body is translatable."""
     info = {"km": km, "entry": None, "source": None, "dims": 1, "needs_length": False, "reads": set(),
-            "writes": set(), "error": km.error}
+            "writes": set(), "covered": set(), "error": km.error}
     if km.error:  # its parameter list is already outside the subset
         return info
     try:
@@ -320,6 +398,7 @@ def translate(km: KernelMethod, entry: str) -> dict:
         info["needs_length"] = checker.uses_length
         info["reads"] = checker.reads
         info["writes"] = checker.writes
+        info["covered"] = covered_buffers(km, checker.dims)
         info["source"] = KernelEmitter(km, checker).kernel(entry)
         info["entry"] = entry
     except Unsupported as e:
@@ -365,8 +444,10 @@ def registry_cpp(records: list[dict], sources: list[str]) -> str:
             et = ELEMENT_TYPE[p.element]
             read = p.name in r["reads"] or r["error"] is not None
             written = p.is_buffer and (p.name in r["writes"] or (r["error"] is not None and not p.read_only))
+            covered = p.name in r["covered"] and not read
             out.append(f'        {{"{p.name}", ElementType::{et}, {str(p.is_buffer).lower()}, '
-                       f'{str(p.read_only).lower()}, {str(read).lower()}, {str(written).lower()}}},')
+                       f'{str(p.read_only).lower()}, {str(read).lower()}, {str(written).lower()}, '
+                       f'{str(covered).lower()}}},')
         out.append("    };")
         if r["entry"]:
             out.append(f'    k.HipEntryPoint = "{r["entry"]}";')

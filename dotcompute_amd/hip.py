@@ -15,7 +15,8 @@ import numpy as np
 PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.path.join(PKG, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libdotcompute_hip.so")
-PROBE_COPY, PROBE_READ2_WRITE1, PROBE_READ = 0, 1, 2  # dc_hip_stream_probe kinds
+BENCH_LIB_PATH = os.path.join(LIB_DIR, "libdotcompute_bench.so")  # measurement-only probes
+PROBE_COPY, PROBE_READ2_WRITE1, PROBE_READ = 0, 1, 2  # dc_bench_stream_probe kinds
 HEADER = os.path.join(os.path.dirname(PKG), "include", "dotcompute_hip.h")
 
 DC_OK = 0
@@ -40,11 +41,14 @@ DC_LINQ_MAX_INSTR = 48
 
 # dc_linq_op
 NOP, LOAD, ADD, SUB, RSUB, MUL, DIV, RDIV, MIN, MAX, NEG, ABS, SQRT, STORE_S0, STORE_S1 = range(15)
+REM, RREM, FLOOR, CEIL, ROUND = range(15, 20)
 CMP_GT, CMP_GE, CMP_LT, CMP_LE, CMP_EQ, CMP_NE, PNOT, PSTORE, PAND_Q, POR_Q, FILTER, MAP = range(20, 32)
 # dc_linq_src
 SRC_IMM, SRC_ELEM, SRC_S0, SRC_S1 = range(4)
 # dc_linq_cmp_mode
 CMP_SET, CMP_AND, CMP_OR = range(3)
+# int32 chains: fault word = -1 or 4 * index + kind
+LINQ_FAULT_NONE, LINQ_FAULT_DIVIDE_BY_ZERO, LINQ_FAULT_OVERFLOW = -1, 1, 2
 
 
 class DeviceInfo(C.Structure):
@@ -77,16 +81,22 @@ class GenLaunch(C.Structure):
                 ("error", C.c_void_p), ("len", C.c_int64 * DC_GEN_MAX_BUFFERS)]
 
 
+class _LinqImm(C.Union):
+    _fields_ = [("imm", C.c_float), ("imm_i32", C.c_int32)]
+
+
 class LinqInstr(C.Structure):
-    _fields_ = [("op", C.c_uint8), ("src", C.c_uint8), ("mode", C.c_uint8), ("pad", C.c_uint8), ("imm", C.c_float)]
+    _anonymous_ = ("u",)
+    _fields_ = [("op", C.c_uint8), ("src", C.c_uint8), ("mode", C.c_uint8), ("pad", C.c_uint8), ("u", _LinqImm)]
 
 
 class LinqChain(C.Structure):
     _fields_ = [("n_instr", C.c_int32), ("flags", C.c_int32), ("code", LinqInstr * DC_LINQ_MAX_INSTR)]
 
     @classmethod
-    def assemble(cls, instrs) -> "LinqChain":
-        """Build a program from (op, src, imm[, mode]) tuples."""
+    def assemble(cls, instrs, int32: bool = False) -> "LinqChain":
+        """Build a program from (op, src, imm[, mode]) tuples; int32=True stores the constants as
+        int32 (a program for the _i32 entry points)."""
         ch = cls()
         if len(instrs) > DC_LINQ_MAX_INSTR:
             raise ValueError("program too long")
@@ -95,8 +105,21 @@ class LinqChain(C.Structure):
         for i, t in enumerate(instrs):
             op, src, imm = t[0], t[1], t[2]
             mode = t[3] if len(t) > 3 else CMP_SET
-            ch.code[i] = LinqInstr(op, src, mode, 0, float(imm))
+            ins = LinqInstr()
+            ins.op, ins.src, ins.mode, ins.pad = op, src, mode, 0
+            if int32:
+                ins.imm_i32 = int(imm)
+            else:
+                ins.imm = float(imm)
+            ch.code[i] = ins
         return ch
+
+
+def can_fault_i32(chain: LinqChain) -> bool:
+    """Whether an int32 program can throw (then the _i32 entry points need a fault word)."""
+    out = C.c_int32(-1)
+    check(load().dc_linq_chain_can_fault_i32(C.byref(chain), C.byref(out)), "dc_linq_chain_can_fault_i32")
+    return bool(out.value)
 
 
 def where_gt0_select_2x_plus_1() -> LinqChain:
@@ -134,7 +157,6 @@ SIGNATURES: dict[str, list] = {
     "dc_hip_memcpy_d2h_async": [_P, _P, _P, _sz],
     "dc_hip_memcpy_d2d_async": [_P, _P, _P, _sz],
     "dc_hip_memset_async": [_P, _P, _i32, _sz],
-    "dc_hip_stream_probe": [_P, _i32, _P, _P, _i64],
     "dc_hip_mem_info": [_P, C.POINTER(_sz), C.POINTER(_sz)],
     "dc_hip_event_create": [_P, _PP],
     "dc_hip_event_destroy": [_P],
@@ -163,6 +185,10 @@ SIGNATURES: dict[str, list] = {
     "dc_hip_host_device_pointer": [_P, _P, _P],
     "dc_hip_linq_where_select_minmax_f32": [_P, C.POINTER(LinqChain), _P, _i64, _i32, _P, _P],
     "dc_hip_linq_to_array_strategy": [_P, _P, _i64, _P],
+    "dc_linq_chain_can_fault_i32": [C.POINTER(LinqChain), C.POINTER(_i32)],
+    "dc_hip_linq_where_select_i32": [_P, C.POINTER(LinqChain), _P, _i64, _P, _P, _P],
+    "dc_hip_linq_where_select_sum_i32": [_P, C.POINTER(LinqChain), _P, _i64, _P, _P, _P, _P],
+    "dc_hip_linq_where_select_minmax_i32": [_P, C.POINTER(LinqChain), _P, _i64, _i32, _P, _P, _P],
     "dc_hip_gemm_f32": [_P, _P, _P, _P, _i64, _i64, _i64],
     "dc_hip_gemm_bf16": [_P, _P, _P, _P, _i64, _i64, _i64],
     "dc_hip_convert_f32_to_bf16": [_P, _P, _P, _i64],
@@ -192,6 +218,24 @@ def load() -> C.CDLL:
             fn.restype = _RESTYPES.get(name, C.c_int32)
         _lib = L
     return _lib
+
+
+_bench_lib: C.CDLL | None = None
+
+
+def load_bench() -> C.CDLL:
+    """The measurement-only probe library (dotcompute_amd/probes), loaded after the product library
+    whose contexts it runs on."""
+    global _bench_lib
+    if _bench_lib is None:
+        load()
+        if not os.path.exists(BENCH_LIB_PATH):
+            raise ImportError(f"{BENCH_LIB_PATH} is missing: build it with `python -m dotcompute_amd.build`")
+        L = C.CDLL(BENCH_LIB_PATH)
+        L.dc_bench_stream_probe.argtypes = [_P, _i32, _P, _P, _i64]
+        L.dc_bench_stream_probe.restype = C.c_int32
+        _bench_lib = L
+    return _bench_lib
 
 
 def error_string(status: int) -> str:
@@ -345,8 +389,9 @@ class Context:
         check(load().dc_hip_vector_add_f32(self.handle, a.ptr, b.ptr, r.ptr, n), "dc_hip_vector_add_f32")
 
     def stream_probe(self, kind: int, src: DeviceArray, dst: DeviceArray, n: int) -> None:
-        """Measurement-only streaming probe (PROBE_COPY / PROBE_READ2_WRITE1 / PROBE_READ)."""
-        check(load().dc_hip_stream_probe(self.handle, kind, src.ptr, dst.ptr, n), "dc_hip_stream_probe")
+        """Measurement-only streaming probe (PROBE_COPY / PROBE_READ2_WRITE1 / PROBE_READ), from the
+        separate probe library."""
+        check(load_bench().dc_bench_stream_probe(self.handle, kind, src.ptr, dst.ptr, n), "dc_bench_stream_probe")
 
     def reduce_sum_f32(self, x: DeviceArray, out: DeviceArray, n: int | None = None) -> None:
         n = x.size if n is None else n
@@ -387,6 +432,30 @@ class Context:
                                                         value_out.ptr if value_out else None,
                                                         count.ptr if count else None),
               "dc_hip_linq_where_select_minmax_f32")
+
+    # ---- int32 chains (C# int semantics); fault: int64[1] (device) or None for programs that cannot throw
+    def where_select_i32(self, chain: LinqChain, x: DeviceArray, out: DeviceArray, count: DeviceArray,
+                         fault: DeviceArray | None, n: int | None = None) -> None:
+        n = x.size if n is None else n
+        check(load().dc_hip_linq_where_select_i32(self.handle, C.byref(chain), x.ptr, n, out.ptr, count.ptr,
+                                                 fault.ptr if fault else None), "dc_hip_linq_where_select_i32")
+
+    def where_select_sum_i32(self, chain: LinqChain, x: DeviceArray, sum_out: DeviceArray | None,
+                             count: DeviceArray | None, overflow: DeviceArray | None, fault: DeviceArray | None,
+                             n: int | None = None) -> None:
+        n = x.size if n is None else n
+        check(load().dc_hip_linq_where_select_sum_i32(self.handle, C.byref(chain), x.ptr, n,
+                                                     sum_out.ptr if sum_out else None, count.ptr if count else None,
+                                                     overflow.ptr if overflow else None, fault.ptr if fault else None),
+              "dc_hip_linq_where_select_sum_i32")
+
+    def where_select_minmax_i32(self, chain: LinqChain, x: DeviceArray, op: int, value_out: DeviceArray | None,
+                                count: DeviceArray | None, fault: DeviceArray | None, n: int | None = None) -> None:
+        n = x.size if n is None else n
+        check(load().dc_hip_linq_where_select_minmax_i32(self.handle, C.byref(chain), x.ptr, n, op,
+                                                        value_out.ptr if value_out else None,
+                                                        count.ptr if count else None, fault.ptr if fault else None),
+              "dc_hip_linq_where_select_minmax_i32")
 
     def gemm_f32(self, a: DeviceArray, b: DeviceArray, c: DeviceArray, m: int, n: int, k: int) -> None:
         check(load().dc_hip_gemm_f32(self.handle, a.ptr, b.ptr, c.ptr, m, n, k), "dc_hip_gemm_f32")

@@ -149,8 +149,13 @@ class HipAccelerator final : public IAccelerator {
 
   // Error words of generated kernels (dc_gen_launch.error): pinned host memory the device writes
   // directly. NextLaunchEpoch() tags one launch; after it completes, ThrowIfGeneratedKernelFailed
-  // raises the C# exception a word carrying that epoch stands for.
+  // raises the C# exception a word carrying that epoch stands for. The words are shared by every
+  // generated launch on this accelerator, so a caller holds GeneratedLaunchMutex() from
+  // NextLaunchEpoch() until ThrowIfGeneratedKernelFailed() returns: a second launch cannot then
+  // overwrite a word before the first launch's caller has read it, and the words are only cleared
+  // (when the epoch counter wraps) while no generated kernel runs.
   uint32_t* GeneratedErrorWordsDevice() const { return err_device_; }
+  std::mutex& GeneratedLaunchMutex() { return gen_mu_; }
   uint32_t NextLaunchEpoch();
   void ThrowIfGeneratedKernelFailed(uint32_t epoch, const std::string& kernel) const;
 
@@ -166,6 +171,7 @@ class HipAccelerator final : public IAccelerator {
   HipMemoryManager memory_;
   HipBackendOptions options_;
   std::mutex module_mu_;
+  std::mutex gen_mu_;  // one generated launch at a time, from its epoch to its error check
   std::map<std::string, std::shared_ptr<dc_hip_module>> modules_;  // loaded code objects by path
 };
 

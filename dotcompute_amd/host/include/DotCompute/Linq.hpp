@@ -1,4 +1,4 @@
-// Linq.hpp — the LINQ provider for the HIP backend: expression trees for float lambdas, the
+// Linq.hpp — the LINQ provider for the HIP backend: expression trees for float and int lambdas, the
 // operation graph, the fusion planner that lowers a Where/Select(/Sum) chain to ONE prebuilt
 // gfx950 kernel (a dc_linq_chain register program), and the queryable front end.
 //
@@ -13,11 +13,14 @@
 // Lambdas are written with a small expression DSL, e.g.
 //   auto x = Linq::Param();
 //   AsComputeQueryable(src).Where(x > 0.0f).Select(x * 2.0f + 1.0f).ToArray();
-// which builds the same tree C# builds for `x => x > 0f` and `x => x * 2f + 1f`.
+// which builds the same tree C# builds for `x => x > 0f` and `x => x * 2f + 1f`. The parameter takes
+// the element type of the query (float or int, ComputeQueryable<T>); constants keep their own type
+// (2 is an int, 2.0f a float), and an int constant in a float lambda is converted as C# converts it.
 #pragma once
 
 #include <functional>
 #include <optional>
+#include <type_traits>
 
 #include "Abstractions.hpp"
 #include "Backends/Hip.hpp"
@@ -27,21 +30,25 @@ namespace DotCompute::Linq {
 // ---- expression trees ---------------------------------------------------------------------------
 enum class ExprKind {
   Parameter, Constant,
-  Negate, Abs, Sqrt,
-  Add, Subtract, Multiply, Divide, Min, Max,
+  Negate, Abs, Sqrt, Floor, Ceiling, Round,
+  Add, Subtract, Multiply, Divide, Modulo, Min, Max,
   GreaterThan, GreaterThanOrEqual, LessThan, LessThanOrEqual, Equal, NotEqual,
   AndAlso, OrElse, Not
 };
 
 struct ExprNode {
   ExprKind Kind;
-  float Value = 0.0f;  // Constant
+  float Value = 0.0f;     // float Constant
+  int32_t IValue = 0;     // int Constant
+  bool IsInt = false;     // Constant: an int literal
   std::shared_ptr<const ExprNode> Left, Right;
 };
 
 class Expr {
  public:
-  Expr(float constant);  // implicit: a float literal in a lambda body
+  Expr(float constant);    // implicit: a float literal in a lambda body (2f)
+  Expr(double constant);   // implicit: taken as the float literal it is rounded to
+  Expr(int32_t constant);  // implicit: an int literal (2)
   explicit Expr(std::shared_ptr<const ExprNode> n) : node_(std::move(n)) {}
   static Expr Parameter();
   const ExprNode& Node() const { return *node_; }
@@ -58,6 +65,7 @@ Expr operator+(const Expr& a, const Expr& b);
 Expr operator-(const Expr& a, const Expr& b);
 Expr operator*(const Expr& a, const Expr& b);
 Expr operator/(const Expr& a, const Expr& b);
+Expr operator%(const Expr& a, const Expr& b);
 Expr operator-(const Expr& a);
 Expr operator>(const Expr& a, const Expr& b);
 Expr operator>=(const Expr& a, const Expr& b);
@@ -72,9 +80,17 @@ Expr operator!(const Expr& a);
 namespace MathF {  // System.MathF members usable in lambdas
 Expr Abs(const Expr& a);
 Expr Sqrt(const Expr& a);
+Expr Floor(const Expr& a);
+Expr Ceiling(const Expr& a);
+Expr Round(const Expr& a);  // MidpointRounding.ToEven
 Expr Min(const Expr& a, const Expr& b);
 Expr Max(const Expr& a, const Expr& b);
 }  // namespace MathF
+namespace Math {  // System.Math members over int (Math.Abs(int.MinValue) throws OverflowException)
+Expr Abs(const Expr& a);
+Expr Min(const Expr& a, const Expr& b);
+Expr Max(const Expr& a, const Expr& b);
+}  // namespace Math
 
 // ---- query representation: the Queryable.* method-call chain -------------------------------------
 struct MethodCall {
@@ -132,6 +148,9 @@ enum class Terminal { ToArray, Sum, Count, LongCount, Average, Min, Max };
 struct FusedKernelPlan {
   dc_linq_chain Program{};                // one fused program for all Filter/Map stages
   Terminal Term = Terminal::ToArray;
+  ElementType Element = ElementType::Float32;  // the chain's element type (float32 or int32 kernels)
+  bool BareSource = true;                 // no Where/Select: the terminal runs on the source array itself
+  bool CanFault = false;                  // an int32 program that can throw (DivideByZero / Overflow)
   std::vector<std::string> FusedOperationIds;
   std::string Listing() const;            // human-readable program
 };
@@ -139,32 +158,46 @@ struct FusedKernelPlan {
 class HipKernelGenerator {
  public:
   // Lowers the graph to one fused kernel: all Filter/Map stages (CanBeFused chains) plus an
-  // optional terminal Reduce that selects the Sum/Count or Min/Max kernel. Throws
-  // NotSupportedException for graphs the prebuilt kernels cannot run (OrderBy, GroupBy, Join, non-float lambdas,
-  // expressions needing more than two saved registers).
-  FusedKernelPlan GenerateHipKernel(const OperationGraph& graph) const;
+  // optional terminal Reduce that selects the Sum/Count or Min/Max kernel. `element` is the
+  // query's element type. Throws NotSupportedException for graphs the prebuilt kernels cannot run
+  // (OrderBy, GroupBy, Join, lambdas that change the element type, expressions needing more than
+  // two saved registers, an int division or remainder or Math.Abs in the right operand of && / ||).
+  FusedKernelPlan GenerateHipKernel(const OperationGraph& graph, ElementType element = ElementType::Float32) const;
   // CudaKernelGenerator.cs:1163-1226: consecutive Map/Filter operations form one group.
   static std::vector<const Operation*> IdentifyFusableOperations(const OperationGraph& graph);
   static bool CanBeFused(const Operation& op);
   // Appends the register program of one lambda: a value (ends in v) or a predicate (ends in p).
-  static void CompileLambda(const Expr& lambda, bool predicate, std::vector<dc_linq_instr>& code);
+  static void CompileLambda(const Expr& lambda, bool predicate, std::vector<dc_linq_instr>& code,
+                            ElementType element = ElementType::Float32);
 };
 
 // ---- execution -------------------------------------------------------------------------------------
+template <typename T>
 struct QueryResult {
-  std::vector<float> Values;  // ToArray
-  double Sum = 0.0;           // Sum / Average (float64 accumulator)
-  float Extreme = 0.0f;       // Min / Max
+  std::vector<T> Values;      // ToArray
+  double Sum = 0.0;           // float sources: Sum / Average (float64 accumulator)
+  int64_t IntSum = 0;         // int32 sources: the exact total
+  bool SumOverflowed = false; // int32 sources: the checked int32 Sum throws OverflowException
+  T Extreme{};                // Min / Max
   int64_t Count = 0;
 };
+
+// Element types the HIP LINQ kernels take (the reference's provider accepts any unmanaged T,
+// ComputeQueryableExtensions.cs:249-259; the kernels here exist for float and int).
+template <typename T>
+inline constexpr bool IsLinqElement = std::is_same<T, float>::value || std::is_same<T, int32_t>::value;
 
 class RuntimeExecutor {
  public:
   explicit RuntimeExecutor(std::shared_ptr<Backends::Hip::HipAccelerator> accelerator) : acc_(std::move(accelerator)) {}
-  // Host source: allocate, copy in, launch, copy back only the compacted result.
-  QueryResult Execute(const FusedKernelPlan& plan, const float* data, size_t n);
+  // Host source: allocate, copy in, launch, copy back only the compacted result. An int32 program
+  // that throws for some element raises the exception LINQ-to-objects raises first
+  // (DivideByZeroException / OverflowException).
+  template <typename T>
+  QueryResult<T> Execute(const FusedKernelPlan& plan, const T* data, size_t n);
   // Device-resident source (no host round trip for the input).
-  QueryResult Execute(const FusedKernelPlan& plan, const IUnifiedMemoryBuffer& source, size_t n);
+  template <typename T>
+  QueryResult<T> Execute(const FusedKernelPlan& plan, const IUnifiedMemoryBuffer& source, size_t n);
   Backends::Hip::HipAccelerator& Accelerator() { return *acc_; }
 
   // Interprets the count the compaction kernel wrote. k >= 0 is the kept count. k == -1 means the
@@ -173,9 +206,12 @@ class RuntimeExecutor {
   // through `rerunOrdered`, which uses the ticket-ordered lookback grid (it cannot stall), and
   // that count is returned. Anything else, or a second -1, throws InvalidOperationException.
   static int64_t ResolveCompactedCount(int64_t k, const std::function<int64_t()>& rerunOrdered);
+  // Throws the exception of an int32 fault word (4 * index + kind); returns for -1.
+  static void ThrowIfFaulted(int64_t fault);
 
  private:
-  QueryResult Run(const FusedKernelPlan& plan, const float* device_in, size_t n);
+  QueryResult<float> Run(const FusedKernelPlan& plan, const float* device_in, size_t n);
+  QueryResult<int32_t> Run(const FusedKernelPlan& plan, const int32_t* device_in, size_t n);
   std::shared_ptr<Backends::Hip::HipAccelerator> acc_;
 };
 
@@ -190,17 +226,26 @@ class ComputeQueryProvider {
   bool HasAccelerator() const { return executor_ != nullptr; }
   // Stages of ExecuteTyped (ComputeQueryableExtensions.cs:329-443): visit -> select backend ->
   // generate the fused kernel -> run it.
-  QueryResult Execute(const std::vector<MethodCall>& chain, Terminal terminal, const float* host, size_t n,
-                      const IUnifiedMemoryBuffer* device);
-  FusedKernelPlan Plan(const std::vector<MethodCall>& chain, Terminal terminal, size_t n) const;
+  template <typename T>
+  QueryResult<T> Execute(const std::vector<MethodCall>& chain, Terminal terminal, const T* host, size_t n,
+                         const IUnifiedMemoryBuffer* device);
+  FusedKernelPlan Plan(const std::vector<MethodCall>& chain, Terminal terminal, size_t n,
+                       ElementType element = ElementType::Float32) const;
 
  private:
   std::unique_ptr<RuntimeExecutor> executor_;
 };
 
+// ComputeQueryable<T> (ComputeQueryableExtensions.cs:74-118) for T = float or int.
+template <typename T>
 class ComputeQueryable {
+  static_assert(IsLinqElement<T>, "the HIP LINQ kernels take float or int sources");
+
  public:
-  ComputeQueryable(const float* data, size_t n, std::shared_ptr<ComputeQueryProvider> provider);
+  // Enumerable.Average returns float for float sources and double for int sources.
+  using AverageType = std::conditional_t<std::is_same<T, int32_t>::value, double, float>;
+
+  ComputeQueryable(const T* data, size_t n, std::shared_ptr<ComputeQueryProvider> provider);
   ComputeQueryable(const IUnifiedMemoryBuffer& device, std::shared_ptr<ComputeQueryProvider> provider);
 
   ComputeQueryable Where(const Expr& predicate) const;
@@ -211,14 +256,17 @@ class ComputeQueryable {
   // with NotSupportedException (as the reference's generators reject them).
   ComputeQueryable OrderBy(const Expr& key) const;
 
-  std::vector<float> ToArray() const;
-  std::vector<float> ToComputeArray() const { return ToArray(); }
-  float Sum() const;          // float64 accumulator, cast to float (Enumerable.Sum(IEnumerable<float>))
+  std::vector<T> ToArray() const;
+  std::vector<T> ToComputeArray() const { return ToArray(); }
+  // float: float64 accumulator, cast to float (Enumerable.Sum(IEnumerable<float>)). int: checked
+  // int32 total, OverflowException by the BCL's rule for the source: its vectorised lane rule over a
+  // bare array, the element-by-element running total after Where/Select.
+  T Sum() const;
   int32_t Count() const;      // throws OverflowException above int.MaxValue
   int64_t LongCount() const;
-  float Average() const;      // throws InvalidOperationException on an empty sequence
-  float Min() const;          // throws InvalidOperationException on an empty sequence
-  float Max() const;          // throws InvalidOperationException on an empty sequence
+  AverageType Average() const;  // throws InvalidOperationException on an empty sequence
+  T Min() const;              // throws InvalidOperationException on an empty sequence
+  T Max() const;              // throws InvalidOperationException on an empty sequence
   // Any / All (Reduce operators, ExpressionTreeVisitor.cs:244-245) on the count kernel: Any(p) is
   // "Where(p) keeps something", All(p) is "Where(!p) keeps nothing" (a NaN fails any comparison,
   // so !p keeps it and All is false, as Enumerable.All evaluates p per element).
@@ -230,18 +278,29 @@ class ComputeQueryable {
   FusedKernelPlan Explain(Terminal terminal = Terminal::ToArray) const;
 
  private:
-  QueryResult Run(Terminal t) const;
-  const float* host_ = nullptr;
+  QueryResult<T> Run(Terminal t) const;
+  const T* host_ = nullptr;
   const IUnifiedMemoryBuffer* device_ = nullptr;
   size_t n_ = 0;
   std::shared_ptr<ComputeQueryProvider> provider_;
   std::vector<MethodCall> chain_;
 };
 
+extern template class ComputeQueryable<float>;
+extern template class ComputeQueryable<int32_t>;
+
 // AsComputeQueryable (ComputeQueryableExtensions.cs:19-23). The source must outlive the query.
-ComputeQueryable AsComputeQueryable(const std::vector<float>& source,
-                                    std::shared_ptr<ComputeQueryProvider> provider = nullptr);
-ComputeQueryable AsComputeQueryable(const float* data, size_t n, std::shared_ptr<ComputeQueryProvider> provider = nullptr);
-ComputeQueryable AsComputeQueryable(const IUnifiedMemoryBuffer& device, std::shared_ptr<ComputeQueryProvider> provider = nullptr);
+ComputeQueryable<float> AsComputeQueryable(const std::vector<float>& source,
+                                           std::shared_ptr<ComputeQueryProvider> provider = nullptr);
+ComputeQueryable<float> AsComputeQueryable(const float* data, size_t n,
+                                           std::shared_ptr<ComputeQueryProvider> provider = nullptr);
+ComputeQueryable<int32_t> AsComputeQueryable(const std::vector<int32_t>& source,
+                                             std::shared_ptr<ComputeQueryProvider> provider = nullptr);
+ComputeQueryable<int32_t> AsComputeQueryable(const int32_t* data, size_t n,
+                                             std::shared_ptr<ComputeQueryProvider> provider = nullptr);
+// Device-resident source of element type T (the buffer's type must match: checked at execution).
+template <typename T = float>
+ComputeQueryable<T> AsComputeQueryable(const IUnifiedMemoryBuffer& device,
+                                       std::shared_ptr<ComputeQueryProvider> provider = nullptr);
 
 }  // namespace DotCompute::Linq

@@ -48,10 +48,13 @@ struct KernelParameterInfo {
   ElementType Type = ElementType::Float32;
   bool IsBuffer = false;
   bool IsReadOnly = true;   // ReadOnlySpan<T> (KernelExecutionMetadataEmitter.GetIsReadOnly)
-  // What the body does with a buffer (from the generator's analysis): the orchestrator copies in
-  // only buffers the kernel reads and copies back only those it writes. Conservative defaults.
+  // What the body does with a buffer (from the generator's analysis), conservative by default.
+  // The orchestrator copies back only the buffers the kernel writes, and copies in every buffer
+  // except one that is written in full and never read (IsCovered: the body assigns every element
+  // of [0, Length) unconditionally, so no element of its old device contents can come back).
   bool IsRead = true;
   bool IsWritten = !IsReadOnly;
+  bool IsCovered = false;
 };
 
 // How a registry kernel's HIP entry point takes its arguments.

@@ -2,6 +2,8 @@
 // and queryable of the HIP LINQ provider.
 #include "DotCompute/Linq.hpp"
 
+#include <cmath>
+#include <cstring>
 #include <limits>
 #include <mutex>
 #include <sstream>
@@ -14,26 +16,52 @@ using Backends::Hip::Check;
 
 namespace {
 std::shared_ptr<const ExprNode> MakeNode(ExprKind k, std::shared_ptr<const ExprNode> l = nullptr,
-                                     std::shared_ptr<const ExprNode> r = nullptr, float v = 0.0f) {
+                                     std::shared_ptr<const ExprNode> r = nullptr) {
   auto n = std::make_shared<ExprNode>();
   n->Kind = k;
-  n->Value = v;
   n->Left = std::move(l);
   n->Right = std::move(r);
   return n;
 }
 bool IsConst(const Expr& e) { return e.Node().Kind == ExprKind::Constant; }
+// The value of a constant as a float (an int constant converted as C#'s implicit int -> float).
+float AsFloat(const ExprNode& n) { return n.IsInt ? (float)n.IValue : n.Value; }
+
+// C# constant folding of int operands: constant expressions are evaluated in a checked context,
+// where an overflow or a division by constant zero is a compile-time error (CS0220, CS0020).
+int32_t FoldInt(ExprKind k, int32_t x, int32_t y) {
+  int64_t r = 0;
+  switch (k) {
+    case ExprKind::Add: r = (int64_t)x + y; break;
+    case ExprKind::Subtract: r = (int64_t)x - y; break;
+    case ExprKind::Multiply: r = (int64_t)x * y; break;
+    case ExprKind::Divide:
+    case ExprKind::Modulo:
+      if (y == 0) throw DivideByZeroException("Division by constant zero");
+      if (x == std::numeric_limits<int32_t>::min() && y == -1)
+        throw OverflowException("The operation overflows at compile time in checked mode");
+      r = k == ExprKind::Divide ? x / y : x % y;
+      break;
+    default: throw NotSupportedException("not a foldable operation");
+  }
+  if (r < std::numeric_limits<int32_t>::min() || r > std::numeric_limits<int32_t>::max())
+    throw OverflowException("The operation overflows at compile time in checked mode");
+  return (int32_t)r;
+}
 
 // Binary arithmetic with constant folding of constant operands (the C# compiler folds constant
-// sub-expressions of a lambda before building its expression tree), each fold rounding to float.
+// sub-expressions of a lambda before building its expression tree): int with int folds as int,
+// otherwise as float (the int operand converted), each float fold rounding to float.
 Expr Arith(ExprKind k, const Expr& a, const Expr& b) {
   if (IsConst(a) && IsConst(b)) {
-    const float x = a.Node().Value, y = b.Node().Value;
+    if (a.Node().IsInt && b.Node().IsInt) return Expr(FoldInt(k, a.Node().IValue, b.Node().IValue));
+    const float x = AsFloat(a.Node()), y = AsFloat(b.Node());
     switch (k) {
       case ExprKind::Add: return Expr(x + y);
       case ExprKind::Subtract: return Expr(x - y);
       case ExprKind::Multiply: return Expr(x * y);
       case ExprKind::Divide: return Expr(x / y);
+      case ExprKind::Modulo: return Expr(std::fmod(x, y));
       default: break;
     }
   }
@@ -43,7 +71,20 @@ bool IsCompareKind(ExprKind k) { return k >= ExprKind::GreaterThan && k <= ExprK
 bool IsPredicateKind(ExprKind k) { return IsCompareKind(k) || k == ExprKind::AndAlso || k == ExprKind::OrElse || k == ExprKind::Not; }
 }  // namespace
 
-Expr::Expr(float constant) : node_(MakeNode(ExprKind::Constant, nullptr, nullptr, constant)) {}
+Expr::Expr(float constant) {
+  auto n = std::make_shared<ExprNode>();
+  n->Kind = ExprKind::Constant;
+  n->Value = constant;
+  node_ = std::move(n);
+}
+Expr::Expr(double constant) : Expr((float)constant) {}
+Expr::Expr(int32_t constant) {
+  auto n = std::make_shared<ExprNode>();
+  n->Kind = ExprKind::Constant;
+  n->IValue = constant;
+  n->IsInt = true;
+  node_ = std::move(n);
+}
 Expr Expr::Parameter() { return Expr(MakeNode(ExprKind::Parameter)); }
 bool Expr::IsPredicate() const { return IsPredicateKind(node_->Kind); }
 
@@ -54,16 +95,23 @@ std::string Expr::ToString() const {
   std::ostringstream os;
   switch (n.Kind) {
     case ExprKind::Parameter: return "x";
-    case ExprKind::Constant: os << n.Value << "f"; return os.str();
+    case ExprKind::Constant:
+      if (n.IsInt) os << n.IValue;
+      else os << n.Value << "f";
+      return os.str();
     case ExprKind::Negate: return "-(" + L() + ")";
-    case ExprKind::Abs: return "MathF.Abs(" + L() + ")";
+    case ExprKind::Abs: return "Abs(" + L() + ")";
     case ExprKind::Sqrt: return "MathF.Sqrt(" + L() + ")";
+    case ExprKind::Floor: return "MathF.Floor(" + L() + ")";
+    case ExprKind::Ceiling: return "MathF.Ceiling(" + L() + ")";
+    case ExprKind::Round: return "MathF.Round(" + L() + ")";
     case ExprKind::Add: return "(" + L() + " + " + R() + ")";
     case ExprKind::Subtract: return "(" + L() + " - " + R() + ")";
     case ExprKind::Multiply: return "(" + L() + " * " + R() + ")";
     case ExprKind::Divide: return "(" + L() + " / " + R() + ")";
-    case ExprKind::Min: return "MathF.Min(" + L() + ", " + R() + ")";
-    case ExprKind::Max: return "MathF.Max(" + L() + ", " + R() + ")";
+    case ExprKind::Modulo: return "(" + L() + " % " + R() + ")";
+    case ExprKind::Min: return "Min(" + L() + ", " + R() + ")";
+    case ExprKind::Max: return "Max(" + L() + ", " + R() + ")";
     case ExprKind::GreaterThan: return "(" + L() + " > " + R() + ")";
     case ExprKind::GreaterThanOrEqual: return "(" + L() + " >= " + R() + ")";
     case ExprKind::LessThan: return "(" + L() + " < " + R() + ")";
@@ -81,7 +129,12 @@ Expr operator+(const Expr& a, const Expr& b) { return Arith(ExprKind::Add, a, b)
 Expr operator-(const Expr& a, const Expr& b) { return Arith(ExprKind::Subtract, a, b); }
 Expr operator*(const Expr& a, const Expr& b) { return Arith(ExprKind::Multiply, a, b); }
 Expr operator/(const Expr& a, const Expr& b) { return Arith(ExprKind::Divide, a, b); }
-Expr operator-(const Expr& a) { return IsConst(a) ? Expr(-a.Node().Value) : Expr(MakeNode(ExprKind::Negate, a.Ptr())); }
+Expr operator%(const Expr& a, const Expr& b) { return Arith(ExprKind::Modulo, a, b); }
+Expr operator-(const Expr& a) {
+  if (!IsConst(a)) return Expr(MakeNode(ExprKind::Negate, a.Ptr()));
+  if (!a.Node().IsInt) return Expr(-a.Node().Value);
+  return Expr(FoldInt(ExprKind::Subtract, 0, a.Node().IValue));  // -int.MinValue does not fold
+}
 Expr operator>(const Expr& a, const Expr& b) { return Expr(MakeNode(ExprKind::GreaterThan, a.Ptr(), b.Ptr())); }
 Expr operator>=(const Expr& a, const Expr& b) { return Expr(MakeNode(ExprKind::GreaterThanOrEqual, a.Ptr(), b.Ptr())); }
 Expr operator<(const Expr& a, const Expr& b) { return Expr(MakeNode(ExprKind::LessThan, a.Ptr(), b.Ptr())); }
@@ -95,9 +148,18 @@ Expr operator!(const Expr& a) { return Expr(MakeNode(ExprKind::Not, a.Ptr())); }
 namespace MathF {
 Expr Abs(const Expr& a) { return Expr(MakeNode(ExprKind::Abs, a.Ptr())); }
 Expr Sqrt(const Expr& a) { return Expr(MakeNode(ExprKind::Sqrt, a.Ptr())); }
+Expr Floor(const Expr& a) { return Expr(MakeNode(ExprKind::Floor, a.Ptr())); }
+Expr Ceiling(const Expr& a) { return Expr(MakeNode(ExprKind::Ceiling, a.Ptr())); }
+Expr Round(const Expr& a) { return Expr(MakeNode(ExprKind::Round, a.Ptr())); }
 Expr Min(const Expr& a, const Expr& b) { return Expr(MakeNode(ExprKind::Min, a.Ptr(), b.Ptr())); }
 Expr Max(const Expr& a, const Expr& b) { return Expr(MakeNode(ExprKind::Max, a.Ptr(), b.Ptr())); }
 }  // namespace MathF
+
+namespace Math {
+Expr Abs(const Expr& a) { return MathF::Abs(a); }
+Expr Min(const Expr& a, const Expr& b) { return MathF::Min(a, b); }
+Expr Max(const Expr& a, const Expr& b) { return MathF::Max(a, b); }
+}  // namespace Math
 
 // ---- visitor ---------------------------------------------------------------------------------------
 
@@ -148,13 +210,13 @@ namespace {
 
 constexpr int kSaveRegisters = 2;
 
-dc_linq_instr Instr(uint8_t op, uint8_t src = DC_LQ_SRC_IMM, float imm = 0.0f, uint8_t mode = DC_LQ_CMP_SET) {
+dc_linq_instr Instr(uint8_t op, uint8_t src = DC_LQ_SRC_IMM, uint32_t imm_bits = 0, uint8_t mode = DC_LQ_CMP_SET) {
   dc_linq_instr i;
   i.op = op;
   i.src = src;
   i.mode = mode;
   i.pad = 0;
-  i.imm = imm;
+  i.imm_i32 = (int32_t)imm_bits;
   return i;
 }
 
@@ -168,18 +230,13 @@ bool RightIsOperand(const ExprNode& n) {
   return !(n.Right->Kind == ExprKind::Parameter && n.Left->Kind == ExprKind::Constant);
 }
 
-// Operand source for a leaf: the element itself, or an immediate.
-std::pair<uint8_t, float> LeafSource(const ExprNode& n) {
-  return n.Kind == ExprKind::Parameter ? std::make_pair((uint8_t)DC_LQ_SRC_ELEM, 0.0f)
-                                       : std::make_pair((uint8_t)DC_LQ_SRC_IMM, n.Value);
-}
-
 uint8_t ArithOp(ExprKind k) {
   switch (k) {
     case ExprKind::Add: return DC_LQ_ADD;
     case ExprKind::Subtract: return DC_LQ_SUB;
     case ExprKind::Multiply: return DC_LQ_MUL;
     case ExprKind::Divide: return DC_LQ_DIV;
+    case ExprKind::Modulo: return DC_LQ_REM;
     case ExprKind::Min: return DC_LQ_MIN;
     case ExprKind::Max: return DC_LQ_MAX;
     default: throw NotSupportedException("not an arithmetic node");
@@ -187,7 +244,7 @@ uint8_t ArithOp(ExprKind k) {
 }
 
 // Operation with its operands swapped (v = operand OP v): exact for +, *, min, max (IEEE + and *
-// commute; MathF.Min/Max are symmetric), and via RSUB/RDIV for - and /.
+// commute, as do wrapping int + and *; Min/Max are symmetric), and via RSUB/RDIV/RREM for -, /, %.
 uint8_t ReversedArithOp(ExprKind k) {
   switch (k) {
     case ExprKind::Add: return DC_LQ_ADD;
@@ -196,6 +253,7 @@ uint8_t ReversedArithOp(ExprKind k) {
     case ExprKind::Max: return DC_LQ_MAX;
     case ExprKind::Subtract: return DC_LQ_RSUB;
     case ExprKind::Divide: return DC_LQ_RDIV;
+    case ExprKind::Modulo: return DC_LQ_RREM;
     default: throw NotSupportedException("not an arithmetic node");
   }
 }
@@ -212,8 +270,14 @@ uint8_t CompareOp(ExprKind k, bool swapped) {
   }
 }
 
+bool IsBinaryArith(ExprKind k) {
+  return k == ExprKind::Add || k == ExprKind::Subtract || k == ExprKind::Multiply || k == ExprKind::Divide ||
+         k == ExprKind::Modulo || k == ExprKind::Min || k == ExprKind::Max;
+}
+
 struct Compiler {
   std::vector<dc_linq_instr>& code;
+  bool is_int;  // the element type: int32 (C# int semantics) or float32
 
   void Emit(const dc_linq_instr& i) {
     if (code.size() >= (size_t)DC_LINQ_MAX_INSTR)
@@ -222,39 +286,87 @@ struct Compiler {
     code.push_back(i);
   }
 
-  // Leaves the value of `n` in v. Saved registers with index >= `free_save` may be used.
+  // Whether evaluating `n` can throw for some element (int: / and % by anything but a constant
+  // other than 0 and -1, and Math.Abs); float arithmetic never throws.
+  bool CanThrow(const ExprNode& n) const {
+    if (!is_int || IsLeaf(n)) return false;
+    if (n.Kind == ExprKind::Abs) return true;
+    if (n.Kind == ExprKind::Divide || n.Kind == ExprKind::Modulo) {
+      const ExprNode& d = *n.Right;
+      if (d.Kind != ExprKind::Constant || d.IValue == 0 || d.IValue == -1) return true;
+    }
+    return (n.Left && CanThrow(*n.Left)) || (n.Right && CanThrow(*n.Right));
+  }
+
+  // The immediate bits of a constant in the program's element type. An int constant in a float
+  // lambda is converted as C# converts it; a float constant in an int lambda would make the lambda
+  // float-typed (a different element type), which one fused kernel cannot change to.
+  uint32_t ImmBits(const ExprNode& n) const {
+    if (is_int) {
+      if (!n.IsInt)
+        throw NotSupportedException("a float constant in a lambda over int elements changes the element type; the "
+                                    "fused HIP kernels keep one element type per chain");
+      return (uint32_t)n.IValue;
+    }
+    const float f = AsFloat(n);
+    uint32_t b;
+    std::memcpy(&b, &f, sizeof(b));
+    return b;
+  }
+
+  // Operand source for a leaf: the element itself, or an immediate.
+  std::pair<uint8_t, uint32_t> LeafSource(const ExprNode& n) const {
+    return n.Kind == ExprKind::Parameter ? std::make_pair((uint8_t)DC_LQ_SRC_ELEM, 0u)
+                                         : std::make_pair((uint8_t)DC_LQ_SRC_IMM, ImmBits(n));
+  }
+
+  // Leaves the value of `n` in v. Saved registers with index >= `free_save` may be used. Operands
+  // are evaluated left before right wherever the left one can throw, so an element that throws in
+  // both raises the left one's exception, as C# evaluates operands left to right.
   void Value(const ExprNode& n, int free_save) {
     switch (n.Kind) {
       case ExprKind::Parameter: Emit(Instr(DC_LQ_LOAD, DC_LQ_SRC_ELEM)); return;
-      case ExprKind::Constant: Emit(Instr(DC_LQ_LOAD, DC_LQ_SRC_IMM, n.Value)); return;
+      case ExprKind::Constant: Emit(Instr(DC_LQ_LOAD, DC_LQ_SRC_IMM, ImmBits(n))); return;
       case ExprKind::Negate: Value(*n.Left, free_save); Emit(Instr(DC_LQ_NEG)); return;
       case ExprKind::Abs: Value(*n.Left, free_save); Emit(Instr(DC_LQ_ABS)); return;
-      case ExprKind::Sqrt: Value(*n.Left, free_save); Emit(Instr(DC_LQ_SQRT)); return;
-      case ExprKind::Add:
-      case ExprKind::Subtract:
-      case ExprKind::Multiply:
-      case ExprKind::Divide:
-      case ExprKind::Min:
-      case ExprKind::Max: {
-        if (RightIsOperand(n)) {
-          Value(*n.Left, free_save);
-          auto [src, imm] = LeafSource(*n.Right);
-          Emit(Instr(ArithOp(n.Kind), src, imm));
-        } else if (IsLeaf(*n.Left)) {
-          Value(*n.Right, free_save);
-          auto [src, imm] = LeafSource(*n.Left);
-          Emit(Instr(ReversedArithOp(n.Kind), src, imm));
-        } else {
-          const int s = Save(free_save);
-          Value(*n.Right, free_save);
-          Emit(Instr(s == 0 ? DC_LQ_STORE_S0 : DC_LQ_STORE_S1));
-          Value(*n.Left, free_save + 1);
-          Emit(Instr(ArithOp(n.Kind), s == 0 ? DC_LQ_SRC_S0 : DC_LQ_SRC_S1));
-        }
+      case ExprKind::Sqrt:
+      case ExprKind::Floor:
+      case ExprKind::Ceiling:
+      case ExprKind::Round: {
+        if (is_int)
+          throw NotSupportedException("Math.Sqrt/Floor/Ceiling/Round of an int yields a double; the fused HIP "
+                                      "kernels keep one element type per chain");
+        Value(*n.Left, free_save);
+        const uint8_t op = n.Kind == ExprKind::Sqrt ? DC_LQ_SQRT : n.Kind == ExprKind::Floor ? DC_LQ_FLOOR
+                           : n.Kind == ExprKind::Ceiling ? DC_LQ_CEIL : DC_LQ_ROUND;
+        Emit(Instr(op));
         return;
       }
       default:
-        throw NotSupportedException("a boolean expression cannot be used as a float value in the HIP kernels");
+        break;
+    }
+    if (!IsBinaryArith(n.Kind))
+      throw NotSupportedException("a boolean expression cannot be used as a value in the HIP kernels");
+    if (RightIsOperand(n)) {
+      Value(*n.Left, free_save);
+      auto [src, imm] = LeafSource(*n.Right);
+      Emit(Instr(ArithOp(n.Kind), src, imm));
+    } else if (IsLeaf(*n.Left)) {
+      Value(*n.Right, free_save);
+      auto [src, imm] = LeafSource(*n.Left);
+      Emit(Instr(ReversedArithOp(n.Kind), src, imm));
+    } else if (CanThrow(*n.Left)) {
+      const int s = Save(free_save);
+      Value(*n.Left, free_save);
+      Emit(Instr(s == 0 ? DC_LQ_STORE_S0 : DC_LQ_STORE_S1));
+      Value(*n.Right, free_save + 1);
+      Emit(Instr(ReversedArithOp(n.Kind), s == 0 ? DC_LQ_SRC_S0 : DC_LQ_SRC_S1));
+    } else {
+      const int s = Save(free_save);
+      Value(*n.Right, free_save);
+      Emit(Instr(s == 0 ? DC_LQ_STORE_S0 : DC_LQ_STORE_S1));
+      Value(*n.Left, free_save + 1);
+      Emit(Instr(ArithOp(n.Kind), s == 0 ? DC_LQ_SRC_S0 : DC_LQ_SRC_S1));
     }
   }
 
@@ -285,11 +397,16 @@ struct Compiler {
         Value(*n.Right, 0);
         auto [src, imm] = LeafSource(*n.Left);
         Emit(Instr(CompareOp(n.Kind, true), src, imm, mode));
+      } else if (CanThrow(*n.Left)) {
+        Value(*n.Left, 0);
+        Emit(Instr(DC_LQ_STORE_S0));
+        Value(*n.Right, 1);
+        Emit(Instr(CompareOp(n.Kind, true), DC_LQ_SRC_S0, 0, mode));
       } else {
         Value(*n.Right, 0);
         Emit(Instr(DC_LQ_STORE_S0));
         Value(*n.Left, 1);
-        Emit(Instr(CompareOp(n.Kind, false), DC_LQ_SRC_S0, 0.0f, mode));
+        Emit(Instr(CompareOp(n.Kind, false), DC_LQ_SRC_S0, 0, mode));
       }
       return;
     }
@@ -301,8 +418,13 @@ struct Compiler {
         return;
       case ExprKind::AndAlso:
       case ExprKind::OrElse: {
+        // C# evaluates the right operand only when the left one does not decide: the program
+        // evaluates both, which is the same as long as the right one cannot throw.
+        if (CanThrow(*n.Right))
+          throw NotSupportedException("an int division, remainder or Math.Abs in the right operand of && or || is "
+                                      "evaluated conditionally in C#; the fused HIP kernel evaluates both operands");
         const uint8_t combine = n.Kind == ExprKind::AndAlso ? DC_LQ_CMP_AND : DC_LQ_CMP_OR;
-        // Both sides are side-effect free, so they may be evaluated in either order.
+        // Neither side has an effect an element could observe, so they may run in either order.
         if (IsCompareKind(n.Right->Kind)) {
           Predicate(*n.Left, DC_LQ_CMP_SET, q_busy);
           Predicate(*n.Right, combine, q_busy);
@@ -335,11 +457,16 @@ const char* OpName(uint8_t op) {
     case DC_LQ_MUL: return "MUL";
     case DC_LQ_DIV: return "DIV";
     case DC_LQ_RDIV: return "RDIV";
+    case DC_LQ_REM: return "REM";
+    case DC_LQ_RREM: return "RREM";
     case DC_LQ_MIN: return "MIN";
     case DC_LQ_MAX: return "MAX";
     case DC_LQ_NEG: return "NEG";
     case DC_LQ_ABS: return "ABS";
     case DC_LQ_SQRT: return "SQRT";
+    case DC_LQ_FLOOR: return "FLOOR";
+    case DC_LQ_CEIL: return "CEIL";
+    case DC_LQ_ROUND: return "ROUND";
     case DC_LQ_STORE_S0: return "STORE_S0";
     case DC_LQ_STORE_S1: return "STORE_S1";
     case DC_LQ_CMP_GT: return "CMP_GT";
@@ -358,15 +485,23 @@ const char* OpName(uint8_t op) {
   return "?";
 }
 
+bool HasOperand(uint8_t op) {
+  return op == DC_LQ_LOAD || (op >= DC_LQ_ADD && op <= DC_LQ_MAX) || op == DC_LQ_REM || op == DC_LQ_RREM ||
+         (op >= DC_LQ_CMP_GT && op <= DC_LQ_CMP_NE);
+}
+
 }  // namespace
 
-void HipKernelGenerator::CompileLambda(const Expr& lambda, bool predicate, std::vector<dc_linq_instr>& code) {
-  Compiler c{code};
+void HipKernelGenerator::CompileLambda(const Expr& lambda, bool predicate, std::vector<dc_linq_instr>& code,
+                                       ElementType element) {
+  if (element != ElementType::Float32 && element != ElementType::Int32)
+    throw NotSupportedException("the HIP LINQ kernels take float or int elements");
+  Compiler c{code, element == ElementType::Int32};
   if (predicate) {
     if (!lambda.IsPredicate()) throw NotSupportedException("Where() needs a boolean lambda");
     c.Predicate(lambda.Node(), DC_LQ_CMP_SET, false);
   } else {
-    if (lambda.IsPredicate()) throw NotSupportedException("Select() to bool is not supported by the float32 HIP kernels");
+    if (lambda.IsPredicate()) throw NotSupportedException("Select() to bool is not supported by the HIP kernels");
     c.Value(lambda.Node(), 0);
   }
 }
@@ -384,8 +519,9 @@ std::vector<const Operation*> HipKernelGenerator::IdentifyFusableOperations(cons
   return out;
 }
 
-FusedKernelPlan HipKernelGenerator::GenerateHipKernel(const OperationGraph& graph) const {
+FusedKernelPlan HipKernelGenerator::GenerateHipKernel(const OperationGraph& graph, ElementType element) const {
   FusedKernelPlan plan;
+  plan.Element = element;
   const auto fused = IdentifyFusableOperations(graph);
   std::vector<dc_linq_instr> code;
   for (const Operation* op : fused) {
@@ -393,11 +529,12 @@ FusedKernelPlan HipKernelGenerator::GenerateHipKernel(const OperationGraph& grap
       throw NotSupportedException("LINQ method '" + op->Method + "' has no HIP kernel");
     if (!op->Lambda) throw ArgumentNullException(op->Method + " needs a lambda");
     const bool is_filter = op->Type == OperationType::Filter;
-    CompileLambda(*op->Lambda, is_filter, code);
+    CompileLambda(*op->Lambda, is_filter, code, element);
     if (code.size() >= (size_t)DC_LINQ_MAX_INSTR) throw NotSupportedException("fused chain too long");
     code.push_back(Instr(is_filter ? DC_LQ_FILTER : DC_LQ_MAP));
     plan.FusedOperationIds.push_back(op->Id);
   }
+  plan.BareSource = fused.empty();
   const size_t rest = graph.Operations.size() - fused.size();
   if (rest > 1) throw NotSupportedException("only one terminal operator may follow the fused Where/Select chain");
   if (rest == 1) {
@@ -419,6 +556,11 @@ FusedKernelPlan HipKernelGenerator::GenerateHipKernel(const OperationGraph& grap
   plan.Program.flags = 0;
   for (size_t i = 0; i < code.size(); ++i) plan.Program.code[i] = code[i];
   Check(dc_linq_chain_validate(&plan.Program), "dc_linq_chain_validate");
+  if (element == ElementType::Int32) {
+    int32_t can = 0;
+    Check(dc_linq_chain_can_fault_i32(&plan.Program, &can), "dc_linq_chain_can_fault_i32");
+    plan.CanFault = can != 0;
+  }
   return plan;
 }
 
@@ -427,14 +569,17 @@ std::string FusedKernelPlan::Listing() const {
   const char* term = Term == Terminal::ToArray ? "ToArray" : Term == Terminal::Sum ? "Sum"
                      : Term == Terminal::Average ? "Average" : Term == Terminal::Min ? "Min"
                      : Term == Terminal::Max ? "Max" : "Count";
-  os << "terminal " << term << "\n";
+  os << "terminal " << term << (Element == ElementType::Int32 ? " (int32)" : " (float32)") << "\n";
   for (int i = 0; i < Program.n_instr; ++i) {
     const dc_linq_instr& in = Program.code[i];
     os << i << ": " << OpName(in.op);
-    if (in.op != DC_LQ_NEG && in.op != DC_LQ_ABS && in.op != DC_LQ_SQRT && in.op != DC_LQ_FILTER && in.op != DC_LQ_MAP &&
-        in.op < DC_LQ_PNOT && in.op != DC_LQ_STORE_S0 && in.op != DC_LQ_STORE_S1) {
-      if (in.src == DC_LQ_SRC_IMM) os << " " << in.imm;
-      else os << (in.src == DC_LQ_SRC_ELEM ? " e" : in.src == DC_LQ_SRC_S0 ? " s0" : " s1");
+    if (HasOperand(in.op)) {
+      if (in.src == DC_LQ_SRC_IMM) {
+        if (Element == ElementType::Int32) os << " " << in.imm_i32;
+        else os << " " << in.imm;
+      } else {
+        os << (in.src == DC_LQ_SRC_ELEM ? " e" : in.src == DC_LQ_SRC_S0 ? " s0" : " s1");
+      }
       if (in.op >= DC_LQ_CMP_GT && in.op <= DC_LQ_CMP_NE && in.mode != DC_LQ_CMP_SET)
         os << (in.mode == DC_LQ_CMP_AND ? " (and)" : " (or)");
     }
@@ -453,12 +598,18 @@ int64_t RuntimeExecutor::ResolveCompactedCount(int64_t k, const std::function<in
   }
   throw InvalidOperationException(
       "The HIP compaction kernel did not complete: its resident grid could not run all of its workgroups at "
-      "once, and the re-run on the ticket-ordered grid reported count " + std::to_string(k) + ".");
+      "once, and the re-run on the ordered grid reported count " + std::to_string(k) + ".");
 }
 
-QueryResult RuntimeExecutor::Run(const FusedKernelPlan& plan, const float* device_in, size_t n) {
+void RuntimeExecutor::ThrowIfFaulted(int64_t fault) {
+  if (fault < 0) return;
+  if ((fault & 3) == DC_LINQ_FAULT_DIVIDE_BY_ZERO) throw DivideByZeroException("Attempted to divide by zero.");
+  throw OverflowException("Arithmetic operation resulted in an overflow.");
+}
+
+QueryResult<float> RuntimeExecutor::Run(const FusedKernelPlan& plan, const float* device_in, size_t n) {
   dc_hip_ctx* ctx = acc_->Context();
-  QueryResult r;
+  QueryResult<float> r;
   auto& mem = acc_->Memory();
   if (plan.Term == Terminal::ToArray) {
     auto out = mem.AllocateAsync<float>(std::max<size_t>(n, 1));
@@ -503,16 +654,112 @@ QueryResult RuntimeExecutor::Run(const FusedKernelPlan& plan, const float* devic
   return r;
 }
 
-QueryResult RuntimeExecutor::Execute(const FusedKernelPlan& plan, const float* data, size_t n) {
-  auto in = acc_->Memory().AllocateAsync<float>(std::max<size_t>(n, 1));
-  if (n) in->CopyFromHost(data, n * sizeof(float));
+// int32 chains. A program that can throw brings a fault word; the first throwing element's
+// exception is raised instead of a result, unless (Sum) the checked running total already
+// overflowed before that element, which LINQ-to-objects would have raised first.
+QueryResult<int32_t> RuntimeExecutor::Run(const FusedKernelPlan& plan, const int32_t* device_in, size_t n) {
+  dc_hip_ctx* ctx = acc_->Context();
+  QueryResult<int32_t> r;
+  auto& mem = acc_->Memory();
+  std::shared_ptr<IUnifiedMemoryBufferT<int64_t>> fault;
+  if (plan.CanFault) fault = mem.AllocateAsync<int64_t>(1);
+  int64_t* fault_ptr = fault ? fault->Data() : nullptr;
+  auto read_fault = [&]() {
+    int64_t f = DC_LINQ_FAULT_NONE;
+    if (fault) fault->CopyToHost(&f, sizeof(f));
+    return f;
+  };
+  if (plan.Term == Terminal::ToArray) {
+    auto out = mem.AllocateAsync<int32_t>(std::max<size_t>(n, 1));
+    auto cnt = mem.AllocateAsync<int64_t>(1);
+    auto run = [&](const dc_linq_chain& prog) {
+      Check(dc_hip_linq_where_select_i32(ctx, &prog, device_in, (int64_t)n, out->Data(), cnt->Data(), fault_ptr),
+            "dc_hip_linq_where_select_i32");
+      acc_->Synchronize();
+      int64_t k = 0;
+      cnt->CopyToHost(&k, sizeof(k));
+      return k;
+    };
+    int64_t k = run(plan.Program);
+    k = ResolveCompactedCount(k, [&]() {
+      dc_linq_chain ordered = plan.Program;
+      ordered.flags |= DC_LINQ_FLAG_ORDERED_GRID;
+      return run(ordered);
+    });
+    ThrowIfFaulted(read_fault());
+    r.Count = k;
+    r.Values.resize((size_t)k);
+    out->CopyToHost(r.Values.data(), (size_t)k * sizeof(int32_t));
+  } else if (plan.Term == Terminal::Min || plan.Term == Terminal::Max) {
+    auto val = mem.AllocateAsync<int32_t>(1);
+    auto cnt = mem.AllocateAsync<int64_t>(1);
+    Check(dc_hip_linq_where_select_minmax_i32(ctx, &plan.Program, device_in, (int64_t)n,
+                                              plan.Term == Terminal::Min ? DC_LINQ_MIN : DC_LINQ_MAX, val->Data(),
+                                              cnt->Data(), fault_ptr),
+          "dc_hip_linq_where_select_minmax_i32");
+    acc_->Synchronize();
+    ThrowIfFaulted(read_fault());
+    val->CopyToHost(&r.Extreme, sizeof(int32_t));
+    cnt->CopyToHost(&r.Count, sizeof(int64_t));
+  } else if (plan.Term == Terminal::Sum && plan.BareSource) {
+    // Sum() of the array itself: the BCL's vectorised rule (Enumerable.Sum over a span).
+    auto sum = mem.AllocateAsync<int64_t>(1);
+    auto ovf = mem.AllocateAsync<int32_t>(1);
+    Check(dc_hip_reduce_sum_i32(ctx, device_in, (int64_t)n, sum->Data(), ovf->Data()), "dc_hip_reduce_sum_i32");
+    acc_->Synchronize();
+    int32_t o = 0;
+    sum->CopyToHost(&r.IntSum, sizeof(int64_t));
+    ovf->CopyToHost(&o, sizeof(int32_t));
+    r.SumOverflowed = o != 0;
+    r.Count = (int64_t)n;
+  } else {
+    // Sum after Where/Select (the element-by-element checked total), Count, LongCount, Average.
+    auto sum = mem.AllocateAsync<int64_t>(1);
+    auto cnt = mem.AllocateAsync<int64_t>(1);
+    auto ovf = mem.AllocateAsync<int32_t>(1);
+    auto run = [&](size_t len) {
+      Check(dc_hip_linq_where_select_sum_i32(ctx, &plan.Program, device_in, (int64_t)len, sum->Data(), cnt->Data(),
+                                             ovf->Data(), fault_ptr),
+            "dc_hip_linq_where_select_sum_i32");
+      acc_->Synchronize();
+      int32_t o = 0;
+      ovf->CopyToHost(&o, sizeof(int32_t));
+      return o != 0;
+    };
+    bool overflowed = run(n);
+    const int64_t f = read_fault();
+    if (f >= 0) {
+      // Which exception comes first: the running total over the elements before the throwing one.
+      if (plan.Term == Terminal::Sum && run((size_t)(f / 4)))
+        throw OverflowException("Arithmetic operation resulted in an overflow.");
+      ThrowIfFaulted(f);
+    }
+    sum->CopyToHost(&r.IntSum, sizeof(int64_t));
+    cnt->CopyToHost(&r.Count, sizeof(int64_t));
+    r.SumOverflowed = overflowed;
+  }
+  return r;
+}
+
+template <typename T>
+QueryResult<T> RuntimeExecutor::Execute(const FusedKernelPlan& plan, const T* data, size_t n) {
+  auto in = acc_->Memory().AllocateAsync<T>(std::max<size_t>(n, 1));
+  if (n) in->CopyFromHost(data, n * sizeof(T));
   return Run(plan, in->Data(), n);
 }
 
-QueryResult RuntimeExecutor::Execute(const FusedKernelPlan& plan, const IUnifiedMemoryBuffer& source, size_t n) {
-  if (source.Type() != ElementType::Float32) throw NotSupportedException("the HIP LINQ kernels take float32 sources");
-  return Run(plan, static_cast<const float*>(source.DevicePointer()), n);
+template <typename T>
+QueryResult<T> RuntimeExecutor::Execute(const FusedKernelPlan& plan, const IUnifiedMemoryBuffer& source, size_t n) {
+  if (source.Type() != ElementTypeOf<T>::value)
+    throw NotSupportedException("the device buffer's element type does not match the query's");
+  return Run(plan, static_cast<const T*>(source.DevicePointer()), n);
 }
+
+template QueryResult<float> RuntimeExecutor::Execute<float>(const FusedKernelPlan&, const float*, size_t);
+template QueryResult<int32_t> RuntimeExecutor::Execute<int32_t>(const FusedKernelPlan&, const int32_t*, size_t);
+template QueryResult<float> RuntimeExecutor::Execute<float>(const FusedKernelPlan&, const IUnifiedMemoryBuffer&, size_t);
+template QueryResult<int32_t> RuntimeExecutor::Execute<int32_t>(const FusedKernelPlan&, const IUnifiedMemoryBuffer&,
+                                                                size_t);
 
 // ---- provider ----------------------------------------------------------------------------------------
 
@@ -532,7 +779,8 @@ std::shared_ptr<ComputeQueryProvider> ComputeQueryProvider::Default() {
   return provider;
 }
 
-FusedKernelPlan ComputeQueryProvider::Plan(const std::vector<MethodCall>& chain, Terminal terminal, size_t n) const {
+FusedKernelPlan ComputeQueryProvider::Plan(const std::vector<MethodCall>& chain, Terminal terminal, size_t n,
+                                           ElementType element) const {
   std::vector<MethodCall> full = chain;
   switch (terminal) {
     case Terminal::Sum: full.push_back({"Sum", std::nullopt}); break;
@@ -547,100 +795,160 @@ FusedKernelPlan ComputeQueryProvider::Plan(const std::vector<MethodCall>& chain,
   OperationGraph graph = ExpressionTreeVisitor().Visit(full);
   // Stage 2: fused kernel for the graph.
   (void)n;
-  return HipKernelGenerator().GenerateHipKernel(graph);
+  return HipKernelGenerator().GenerateHipKernel(graph, element);
 }
 
-QueryResult ComputeQueryProvider::Execute(const std::vector<MethodCall>& chain, Terminal terminal, const float* host,
-                                          size_t n, const IUnifiedMemoryBuffer* device) {
-  FusedKernelPlan plan = Plan(chain, terminal, n);
+template <typename T>
+QueryResult<T> ComputeQueryProvider::Execute(const std::vector<MethodCall>& chain, Terminal terminal, const T* host,
+                                             size_t n, const IUnifiedMemoryBuffer* device) {
+  FusedKernelPlan plan = Plan(chain, terminal, n, ElementTypeOf<T>::value);
   WorkloadCharacteristics w;
   w.DataSize = n;
   w.OperationCount = (int)plan.FusedOperationIds.size();
   w.HasReduction = terminal != Terminal::ToArray;
   BackendSelector(HasAccelerator()).SelectBackend(w);  // throws without a HIP device
-  return device ? executor_->Execute(plan, *device, n) : executor_->Execute(plan, host, n);
+  return device ? executor_->Execute<T>(plan, *device, n) : executor_->Execute<T>(plan, host, n);
 }
+
+template QueryResult<float> ComputeQueryProvider::Execute<float>(const std::vector<MethodCall>&, Terminal,
+                                                                 const float*, size_t, const IUnifiedMemoryBuffer*);
+template QueryResult<int32_t> ComputeQueryProvider::Execute<int32_t>(const std::vector<MethodCall>&, Terminal,
+                                                                     const int32_t*, size_t,
+                                                                     const IUnifiedMemoryBuffer*);
 
 // ---- queryable ----------------------------------------------------------------------------------------
 
-ComputeQueryable::ComputeQueryable(const float* data, size_t n, std::shared_ptr<ComputeQueryProvider> provider)
+template <typename T>
+ComputeQueryable<T>::ComputeQueryable(const T* data, size_t n, std::shared_ptr<ComputeQueryProvider> provider)
     : host_(data), n_(n), provider_(std::move(provider)) {
   if (!data && n) throw ArgumentNullException("source");
 }
 
-ComputeQueryable::ComputeQueryable(const IUnifiedMemoryBuffer& device, std::shared_ptr<ComputeQueryProvider> provider)
+template <typename T>
+ComputeQueryable<T>::ComputeQueryable(const IUnifiedMemoryBuffer& device, std::shared_ptr<ComputeQueryProvider> provider)
     : device_(&device), n_(device.Length()), provider_(std::move(provider)) {}
 
-ComputeQueryable ComputeQueryable::Where(const Expr& predicate) const {
+template <typename T>
+ComputeQueryable<T> ComputeQueryable<T>::Where(const Expr& predicate) const {
   ComputeQueryable q = *this;
   q.chain_.push_back({"Where", predicate});
   return q;
 }
 
-ComputeQueryable ComputeQueryable::Select(const Expr& selector) const {
+template <typename T>
+ComputeQueryable<T> ComputeQueryable<T>::Select(const Expr& selector) const {
   ComputeQueryable q = *this;
   q.chain_.push_back({"Select", selector});
   return q;
 }
 
-ComputeQueryable ComputeQueryable::OrderBy(const Expr& key) const {
+template <typename T>
+ComputeQueryable<T> ComputeQueryable<T>::OrderBy(const Expr& key) const {
   ComputeQueryable q = *this;
   q.chain_.push_back({"OrderBy", key});
   return q;
 }
 
-QueryResult ComputeQueryable::Run(Terminal t) const { return provider_->Execute(chain_, t, host_, n_, device_); }
+template <typename T>
+QueryResult<T> ComputeQueryable<T>::Run(Terminal t) const {
+  return provider_->Execute<T>(chain_, t, host_, n_, device_);
+}
 
-FusedKernelPlan ComputeQueryable::Explain(Terminal terminal) const { return provider_->Plan(chain_, terminal, n_); }
+template <typename T>
+FusedKernelPlan ComputeQueryable<T>::Explain(Terminal terminal) const {
+  return provider_->Plan(chain_, terminal, n_, ElementTypeOf<T>::value);
+}
 
-std::vector<float> ComputeQueryable::ToArray() const { return Run(Terminal::ToArray).Values; }
+template <typename T>
+std::vector<T> ComputeQueryable<T>::ToArray() const { return Run(Terminal::ToArray).Values; }
 
-float ComputeQueryable::Sum() const { return (float)Run(Terminal::Sum).Sum; }
+template <typename T>
+T ComputeQueryable<T>::Sum() const {
+  QueryResult<T> r = Run(Terminal::Sum);
+  if constexpr (std::is_same<T, int32_t>::value) {
+    if (r.SumOverflowed) throw OverflowException("Arithmetic operation resulted in an overflow.");
+    return (int32_t)r.IntSum;
+  } else {
+    return (float)r.Sum;
+  }
+}
 
-int64_t ComputeQueryable::LongCount() const { return Run(Terminal::LongCount).Count; }
+template <typename T>
+int64_t ComputeQueryable<T>::LongCount() const { return Run(Terminal::LongCount).Count; }
 
-int32_t ComputeQueryable::Count() const {
+template <typename T>
+int32_t ComputeQueryable<T>::Count() const {
   const int64_t c = Run(Terminal::Count).Count;
   if (c > std::numeric_limits<int32_t>::max()) throw OverflowException("Arithmetic operation resulted in an overflow.");
   return (int32_t)c;
 }
 
-float ComputeQueryable::Average() const {
-  QueryResult r = Run(Terminal::Average);
+// Enumerable.Average: float sources accumulate in float64 and return float; int sources sum in
+// int64 and return double (the sum divided by the count).
+template <typename T>
+typename ComputeQueryable<T>::AverageType ComputeQueryable<T>::Average() const {
+  QueryResult<T> r = Run(Terminal::Average);
   if (r.Count == 0) throw InvalidOperationException("Sequence contains no elements");
-  return (float)(r.Sum / (double)r.Count);
+  if constexpr (std::is_same<T, int32_t>::value) return (double)r.IntSum / (double)r.Count;
+  else return (float)(r.Sum / (double)r.Count);
 }
 
-// BCL Enumerable.Min/Max(IEnumerable<float>) semantics (the reference runs these as LINQ-to-objects):
-// the device reduction returns the same element bit for bit; an empty sequence throws.
-float ComputeQueryable::Min() const {
-  QueryResult r = Run(Terminal::Min);
+// BCL Enumerable.Min/Max semantics (the reference runs these as LINQ-to-objects): the device
+// reduction returns the same element bit for bit; an empty sequence throws.
+template <typename T>
+T ComputeQueryable<T>::Min() const {
+  QueryResult<T> r = Run(Terminal::Min);
   if (r.Count == 0) throw InvalidOperationException("Sequence contains no elements");
   return r.Extreme;
 }
 
-float ComputeQueryable::Max() const {
-  QueryResult r = Run(Terminal::Max);
+template <typename T>
+T ComputeQueryable<T>::Max() const {
+  QueryResult<T> r = Run(Terminal::Max);
   if (r.Count == 0) throw InvalidOperationException("Sequence contains no elements");
   return r.Extreme;
 }
 
-bool ComputeQueryable::Any() const { return LongCount() > 0; }
+template <typename T>
+bool ComputeQueryable<T>::Any() const { return LongCount() > 0; }
 
-bool ComputeQueryable::Any(const Expr& predicate) const { return Where(predicate).LongCount() > 0; }
+template <typename T>
+bool ComputeQueryable<T>::Any(const Expr& predicate) const { return Where(predicate).LongCount() > 0; }
 
-bool ComputeQueryable::All(const Expr& predicate) const { return Where(!predicate).LongCount() == 0; }
+template <typename T>
+bool ComputeQueryable<T>::All(const Expr& predicate) const { return Where(!predicate).LongCount() == 0; }
 
-ComputeQueryable AsComputeQueryable(const std::vector<float>& source, std::shared_ptr<ComputeQueryProvider> provider) {
-  return ComputeQueryable(source.data(), source.size(), provider ? provider : ComputeQueryProvider::Default());
+template class ComputeQueryable<float>;
+template class ComputeQueryable<int32_t>;
+
+ComputeQueryable<float> AsComputeQueryable(const std::vector<float>& source,
+                                           std::shared_ptr<ComputeQueryProvider> provider) {
+  return ComputeQueryable<float>(source.data(), source.size(), provider ? provider : ComputeQueryProvider::Default());
 }
 
-ComputeQueryable AsComputeQueryable(const float* data, size_t n, std::shared_ptr<ComputeQueryProvider> provider) {
-  return ComputeQueryable(data, n, provider ? provider : ComputeQueryProvider::Default());
+ComputeQueryable<float> AsComputeQueryable(const float* data, size_t n, std::shared_ptr<ComputeQueryProvider> provider) {
+  return ComputeQueryable<float>(data, n, provider ? provider : ComputeQueryProvider::Default());
 }
 
-ComputeQueryable AsComputeQueryable(const IUnifiedMemoryBuffer& device, std::shared_ptr<ComputeQueryProvider> provider) {
-  return ComputeQueryable(device, provider ? provider : ComputeQueryProvider::Default());
+ComputeQueryable<int32_t> AsComputeQueryable(const std::vector<int32_t>& source,
+                                             std::shared_ptr<ComputeQueryProvider> provider) {
+  return ComputeQueryable<int32_t>(source.data(), source.size(),
+                                   provider ? provider : ComputeQueryProvider::Default());
 }
+
+ComputeQueryable<int32_t> AsComputeQueryable(const int32_t* data, size_t n,
+                                             std::shared_ptr<ComputeQueryProvider> provider) {
+  return ComputeQueryable<int32_t>(data, n, provider ? provider : ComputeQueryProvider::Default());
+}
+
+template <typename T>
+ComputeQueryable<T> AsComputeQueryable(const IUnifiedMemoryBuffer& device, std::shared_ptr<ComputeQueryProvider> provider) {
+  return ComputeQueryable<T>(device, provider ? provider : ComputeQueryProvider::Default());
+}
+
+template ComputeQueryable<float> AsComputeQueryable<float>(const IUnifiedMemoryBuffer&,
+                                                           std::shared_ptr<ComputeQueryProvider>);
+template ComputeQueryable<int32_t> AsComputeQueryable<int32_t>(const IUnifiedMemoryBuffer&,
+                                                               std::shared_ptr<ComputeQueryProvider>);
 
 }  // namespace DotCompute::Linq

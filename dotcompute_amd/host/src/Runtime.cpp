@@ -416,6 +416,8 @@ std::vector<float> KernelExecutionService::ExecuteGenerated(const KernelRegistra
       throw DivideByZeroException("Attempted to divide by zero. (kernel '" + reg.Name + "': a zero extent)");
   }
 
+  // The accelerator's error words serve one generated launch at a time (see GeneratedLaunchMutex).
+  std::lock_guard<std::mutex> serial(accelerator.GeneratedLaunchMutex());
   dc_gen_launch launch{};
   launch.work = (int64_t)totalWork;
   launch.epoch = accelerator.NextLaunchEpoch();
@@ -430,10 +432,13 @@ std::vector<float> KernelExecutionService::ExecuteGenerated(const KernelRegistra
       if (nbuf >= DC_GEN_MAX_BUFFERS) throw NotSupportedException("more than 16 buffer parameters");
       IUnifiedMemoryBuffer* dev = nullptr;
       if (auto* h = std::get_if<HostArray>(&args[i])) {
-        // Only what the body reads goes in and only what it writes comes back; the memory comes
-        // from the accelerator's pool (no device allocation once the sizes have been seen).
+        // Every array goes in (as the reference copies them, KernelExecutionService.cs:755-763),
+        // except one the body overwrites in full without reading it: the pool recycles device
+        // blocks without clearing them, so an element the kernel leaves alone must arrive from the
+        // host. Only what the body writes comes back. The memory comes from the accelerator's pool
+        // (no device allocation once the sizes have been seen).
         auto buf = accelerator.Memory().AllocateRaw(h->Length, h->Type);
-        if (p.IsRead) buf->EnqueueCopyFromHost(h->Data, h->Length * ElementSize(h->Type));
+        if (p.IsRead || !p.IsCovered) buf->EnqueueCopyFromHost(h->Data, h->Length * ElementSize(h->Type));
         if (p.IsWritten) copyBacks.push_back({buf, *h});
         dev = buf.get();
         owned.push_back(std::move(buf));

@@ -64,6 +64,16 @@ namespace DotCompute.Samples
             }
         }
 
+        // A conditional write: elements whose input is not positive keep what the caller's output
+        // array held, so the orchestrator must copy that array in before the launch.
+        [Kernel(Backends = KernelBackends.CPU | KernelBackends.HIP)]
+        public static void CopyPositive(ReadOnlySpan<float> input, Span<float> output)
+        {
+            int i = KernelContext.ThreadId.X;
+            if (i < output.Length && input[i] > 0f)
+                output[i] = input[i];
+        }
+
         // Indices read from memory: an index outside the source throws IndexOutOfRangeException.
         [Kernel(Backends = KernelBackends.CPU | KernelBackends.HIP)]
         public static void Gather(ReadOnlySpan<float> source, ReadOnlySpan<int> index, Span<float> destination)

@@ -202,22 +202,6 @@ DC_HIP_API int32_t dc_hip_vector_add_f32(dc_hip_ctx* ctx, const float* a, const 
                                          float* result, int64_t n);
 
 /* ---------------------------------------------------------------------------------------------
- * Streaming probes — measurement only, no counterpart in the reference: what plain streaming
- * kernels reach on this device for a given read/write mix, the ceilings the benchmark reports
- * beside the fused kernels. One 16-byte vector per thread over a grid that covers the input
- * (1024-thread workgroups), non-temporal loads and stores. `n` floats, a multiple of 8; `src` and
- * `dst` 16-byte aligned (DC_ERR_MISALIGNED otherwise).
- *   DC_PROBE_COPY:           dst[i] = src[i], i < n                    (reads 4n B, writes 4n B)
- *   DC_PROBE_READ2_WRITE1:   dst[i] = src[i] + src[n/2 + i], i < n/2   (reads 4n B, writes 2n B)
- *   DC_PROBE_READ:           reads src[0, n) and writes nothing (each value is compared with
- *                            a NaN passed at run time, which never compares equal)  (reads 4n B)
- * ------------------------------------------------------------------------------------------- */
-#define DC_PROBE_COPY 0
-#define DC_PROBE_READ2_WRITE1 1
-#define DC_PROBE_READ 2
-DC_HIP_API int32_t dc_hip_stream_probe(dc_hip_ctx* ctx, int32_t kind, const float* src, float* dst, int64_t n);
-
-/* ---------------------------------------------------------------------------------------------
  * Sum reductions (deterministic: fixed per-thread order, fixed tree, last-block combine).
  * f32: accumulated in float64, result written as a double; the managed caller casts to float,
  *      as Enumerable.Sum(IEnumerable<float>) does (reached from
@@ -248,14 +232,26 @@ DC_HIP_API int32_t dc_hip_reduce_sum_i32(dc_hip_ctx* ctx, const int32_t* input, 
  * Program model. Per element the kernel holds: e (the pipeline element), v (accumulator), s0, s1
  * (saved values), p and q (predicate registers) and k (keep flag, initially true).
  * Each instruction: op, src (operand source), imm (constant operand).
- *   value ops   v = f(v, operand)         LOAD ADD SUB RSUB MUL DIV RDIV MIN MAX NEG ABS SQRT
+ *   value ops   v = f(v, operand)         LOAD ADD SUB RSUB MUL DIV RDIV REM RREM MIN MAX
+ *               v = f(v)                  NEG ABS SQRT FLOOR CEIL ROUND
  *   STORE_S0/1  s0/s1 = v
  *   CMP_*       c = (v <cmp> operand); p = c (mode SET), p && c (AND), p || c (OR)
  *   PNOT        p = !p;  PSTORE q = p;  PAND_Q p = p && q;  POR_Q p = p || q
  *   FILTER      k = k && p                 (ends a Where stage)
  *   MAP         e = v                      (ends a Select stage)
- * Every float operation rounds once to float32 (no contraction), matching .NET's scalar float
- * arithmetic, so outputs are bit-identical to LINQ-to-objects for the same lambdas.
+ * The element type is the entry point's (_f32 or _i32); `imm` is read as that type.
+ * float32 programs: every operation rounds once to float32 (no contraction), matching .NET's
+ *   scalar float arithmetic, so outputs are bit-identical to LINQ-to-objects for the same lambdas.
+ *   REM is C#'s float `%` (truncated remainder, exact, the sign of the dividend); FLOOR, CEIL and
+ *   ROUND are MathF.Floor, MathF.Ceiling and MathF.Round (ties to even).
+ * int32 programs: C# `int` arithmetic in an unchecked context. + - * and NEG wrap; DIV/RDIV and
+ *   REM/RREM truncate toward zero and throw on a zero divisor (DivideByZeroException) and on
+ *   int.MinValue divided by -1 (OverflowException, as .NET on x64 also does for %); ABS is
+ *   Math.Abs (OverflowException for int.MinValue); MIN/MAX are Math.Min/Max. SQRT, FLOOR, CEIL and
+ *   ROUND have no int32 form (DC_ERR_UNSUPPORTED). A throwing operation is evaluated only for
+ *   elements still kept at that point of the chain, as LINQ-to-objects evaluates a Select only for
+ *   the elements its Where passed; the kernels report the first element (in sequence order) that
+ *   throws through `fault_out` (below) instead of an output.
  * ------------------------------------------------------------------------------------------- */
 #define DC_LINQ_MAX_INSTR 48
 
@@ -275,6 +271,11 @@ enum dc_linq_op {
   DC_LQ_SQRT = 12,
   DC_LQ_STORE_S0 = 13,
   DC_LQ_STORE_S1 = 14,
+  DC_LQ_REM = 15,   /* v = v % operand */
+  DC_LQ_RREM = 16,  /* v = operand % v */
+  DC_LQ_FLOOR = 17, /* float32 only */
+  DC_LQ_CEIL = 18,  /* float32 only */
+  DC_LQ_ROUND = 19, /* float32 only: ties to even */
   DC_LQ_CMP_GT = 20,
   DC_LQ_CMP_GE = 21,
   DC_LQ_CMP_LT = 22,
@@ -303,7 +304,10 @@ typedef struct dc_linq_instr {
   uint8_t src;   /* enum dc_linq_src (value and CMP ops) */
   uint8_t mode;  /* enum dc_linq_cmp_mode (CMP ops) */
   uint8_t pad;
-  float imm;
+  union {
+    float imm;        /* float32 programs */
+    int32_t imm_i32;  /* int32 programs */
+  };
 } dc_linq_instr;
 
 /* dc_linq_chain.flags bits. DC_LINQ_FLAG_ORDERED_GRID: run a ToArray on the ticket-ordered lookback
@@ -318,6 +322,10 @@ typedef struct dc_linq_chain {
 
 /* Checks a program for structural validity (opcodes, operand sources, length). */
 DC_HIP_API int32_t dc_linq_chain_validate(const dc_linq_chain* chain);
+/* Whether an int32 program can throw for some input (a DIV/RDIV/REM/RREM whose divisor is not an
+ * immediate other than 0 and -1, or an ABS): *can_fault_out = 1 or 0. The int32 entry points need a
+ * fault_out word for such programs and accept NULL for the others. */
+DC_HIP_API int32_t dc_linq_chain_can_fault_i32(const dc_linq_chain* chain, int32_t* can_fault_out);
 
 /* Where/Select → ToArray: writes the kept, mapped elements in input order to `output` (capacity n)
  * and their number to *count_out (device int64). One pass over the input. Large 16-byte aligned
@@ -361,6 +369,46 @@ enum dc_linq_minmax { DC_LINQ_MIN = 0, DC_LINQ_MAX = 1 };
 DC_HIP_API int32_t dc_hip_linq_where_select_minmax_f32(dc_hip_ctx* ctx, const dc_linq_chain* chain,
                                                        const float* input, int64_t n, int32_t op,
                                                        float* value_out, int64_t* count_out);
+
+/* ---------------------------------------------------------------------------------------------
+ * Fused LINQ chains over int32 sources (AsComputeQueryable over an int[]; the reference's provider
+ * types any unmanaged T, src/Extensions/DotCompute.Linq/ComputeQueryableExtensions.cs:249-259,329,
+ * and its generator maps int to CUDA `int` with the `%` operator, CodeGeneration/
+ * CudaKernelGenerator.cs:1351,1399-1416). Same program model and kernels as the float32 entry
+ * points, with C# int semantics (above).
+ *
+ * Faults. `fault_out` (device int64) receives -1 when no element throws, else 4 * i + kind for the
+ * first element i (in sequence order) whose evaluation throws, kind DC_LINQ_FAULT_*: the exception
+ * LINQ-to-objects would raise there. The other outputs are then unspecified. fault_out may be NULL
+ * only for programs that cannot throw (dc_linq_chain_can_fault_i32); otherwise DC_ERR_INVALID_ARGUMENT.
+ * ------------------------------------------------------------------------------------------- */
+#define DC_LINQ_FAULT_NONE (-1)
+#define DC_LINQ_FAULT_DIVIDE_BY_ZERO 1 /* System.DivideByZeroException */
+#define DC_LINQ_FAULT_OVERFLOW 2       /* System.OverflowException     */
+
+/* Where/Select -> ToArray over int32: as dc_hip_linq_where_select_f32 (order-preserving compaction,
+ * *count_out -1 when the resident grid gave up and the chain must be re-run with
+ * DC_LINQ_FLAG_ORDERED_GRID). */
+DC_HIP_API int32_t dc_hip_linq_where_select_i32(dc_hip_ctx* ctx, const dc_linq_chain* chain,
+                                                const int32_t* input, int64_t n, int32_t* output,
+                                                int64_t* count_out, int64_t* fault_out);
+/* Where/Select -> Sum / Count / Average over int32: the exact int64 total of the kept, mapped elements
+ * to *sum_out and their number to *count_out (either may be NULL). *overflow_out (device int32, may
+ * be NULL) is set to 1 when a checked int32 running total over those elements in sequence order
+ * leaves the int32 range at some element, the rule of Enumerable.Sum(IEnumerable<int>) over an
+ * iterator (a Where/Select result, which has no span, so the BCL adds element by element with
+ * checked adds), else 0. Sum() over a bare int[] follows the BCL's vectorised rule instead:
+ * dc_hip_reduce_sum_i32. Deterministic. */
+DC_HIP_API int32_t dc_hip_linq_where_select_sum_i32(dc_hip_ctx* ctx, const dc_linq_chain* chain,
+                                                    const int32_t* input, int64_t n, int64_t* sum_out,
+                                                    int64_t* count_out, int32_t* overflow_out,
+                                                    int64_t* fault_out);
+/* Where/Select -> Min or Max over int32 (Math.Min/Max order; *value_out unspecified when
+ * *count_out is 0, the empty sequence). */
+DC_HIP_API int32_t dc_hip_linq_where_select_minmax_i32(dc_hip_ctx* ctx, const dc_linq_chain* chain,
+                                                       const int32_t* input, int64_t n, int32_t op,
+                                                       int32_t* value_out, int64_t* count_out,
+                                                       int64_t* fault_out);
 
 /* ---------------------------------------------------------------------------------------------
  * Dense GEMM, row-major: C[m×n] = A[m×k] · B[k×n].

@@ -55,6 +55,10 @@ def lib() -> C.CDLL:
             "oracle_linq_where_select_min": (_i64, [_P, _P, _i64, _P]),
             "oracle_linq_where_select_max": (_i64, [_P, _P, _i64, _P]),
             "oracle_where_gt0_select_2x_plus_1_minmax": (_i64, [_P, _i64, _i32, _P]),
+            "oracle_linq_eval_i32": (_i32, [_P, _i32, _P, _P]),
+            "oracle_linq_where_select_i32": (_i64, [_P, _P, _i64, _P, _P]),
+            "oracle_linq_where_select_sum_i32": (_i64, [_P, _P, _i64, _P, _P, _P]),
+            "oracle_linq_where_select_minmax_i32": (_i64, [_P, _P, _i64, _i32, _P, _P]),
             "oracle_gemm_f32_naive": (None, [_P, _P, _P, _i64, _i64, _i64, _i32]),
             "oracle_gemm_f32_naive_rows": (None, [_P, _P, _P, _i64, _i64, _i64, _i64, _i64, _i32]),
             "oracle_gemm_f32_blocked": (None, [_P, _P, _P, _i64, _i64, _i64]),
@@ -215,6 +219,48 @@ def where_gt0_select_2x_plus_1_minmax(x: np.ndarray, op: str):
     out = np.zeros(1, np.float32)
     k = lib().oracle_where_gt0_select_2x_plus_1_minmax(_p(x), x.size, 0 if op == "min" else 1, _p(out))
     return out[0], int(k)
+
+
+# ---- int32 chains (C# int semantics). fault: -1, or 4 * index + kind (1 DivideByZero, 2 Overflow)
+# of the first element that throws; the results cover the elements before it.
+def linq_where_select_i32(chain, x: np.ndarray):
+    """Returns (kept mapped int32 values, fault)."""
+    x = np.ascontiguousarray(x, dtype=np.int32)
+    out = np.empty_like(x)
+    fault = C.c_int64()
+    k = lib().oracle_linq_where_select_i32(C.byref(chain), _p(x), x.size, _p(out), C.byref(fault))
+    if k < 0:
+        raise ValueError(f"malformed chain ({k})")
+    return out[:k].copy(), fault.value
+
+
+def linq_where_select_sum_i32(chain, x: np.ndarray):
+    """Returns (exact int64 total, kept count, overflowed, fault) of the checked running total."""
+    x = np.ascontiguousarray(x, dtype=np.int32)
+    total, ovf, fault = C.c_int64(), C.c_int32(), C.c_int64()
+    k = lib().oracle_linq_where_select_sum_i32(C.byref(chain), _p(x), x.size, C.byref(total), C.byref(ovf),
+                                               C.byref(fault))
+    if k < 0:
+        raise ValueError(f"malformed chain ({k})")
+    return total.value, int(k), bool(ovf.value), fault.value
+
+
+def linq_where_select_minmax_i32(chain, x: np.ndarray, op: str):
+    """Returns (min or max, kept count, fault); the value is meaningless when the count is 0."""
+    x = np.ascontiguousarray(x, dtype=np.int32)
+    v, fault = C.c_int32(), C.c_int64()
+    k = lib().oracle_linq_where_select_minmax_i32(C.byref(chain), _p(x), x.size, 0 if op == "min" else 1,
+                                                  C.byref(v), C.byref(fault))
+    if k < 0:
+        raise ValueError(f"malformed chain ({k})")
+    return v.value, int(k), fault.value
+
+
+def linq_eval_i32(chain, x: int):
+    """Returns (kept, mapped value, fault kind 0/1/2) for one element."""
+    y, kind = C.c_int32(), C.c_int32()
+    r = lib().oracle_linq_eval_i32(C.byref(chain), int(x), C.byref(y), C.byref(kind))
+    return r, y.value, kind.value
 
 
 def linq_eval(chain, x: float):

@@ -343,6 +343,11 @@ int32_t oracle_linq_eval(const dc_linq_chain* chain, float x, float* y_out) {
       case DC_LQ_NEG: v = -v; break;
       case DC_LQ_ABS: v = fabsf(v); break;
       case DC_LQ_SQRT: v = sqrtf(v); break;
+      case DC_LQ_REM: v = fmodf(v, o); break;   /* C# float %: truncated remainder, exact */
+      case DC_LQ_RREM: v = fmodf(o, v); break;
+      case DC_LQ_FLOOR: v = floorf(v); break;   /* MathF.Floor */
+      case DC_LQ_CEIL: v = ceilf(v); break;     /* MathF.Ceiling */
+      case DC_LQ_ROUND: v = rintf(v); break;    /* MathF.Round: to nearest, ties to even */
       case DC_LQ_STORE_S0: s0 = v; break;
       case DC_LQ_STORE_S1: s1 = v; break;
       case DC_LQ_CMP_GT: c = v > o; is_cmp = 1; break;
@@ -396,6 +401,153 @@ float oracle_linq_where_select_sum(const dc_linq_chain* chain, const float* in, 
   if (count) *count = k;
   if (as_double) *as_double = s;
   return (float)s;
+}
+
+/* ---- int32 chains: C# `int` arithmetic (ECMA-334 12.10 / 12.12, unchecked context) ---------
+ * + - * and unary - wrap modulo 2^32; / and % truncate toward zero (ECMA-335 III.3.31 div,
+ * III.3.55 rem) and throw DivideByZeroException for a zero divisor and an ArithmeticException
+ * (OverflowException on x64 .NET) for int.MinValue / -1 and int.MinValue % -1; Math.Abs(int)
+ * throws OverflowException for int.MinValue; Math.Min/Max(int, int). Elements are evaluated one at
+ * a time, stage by stage, and an element dropped by a Where stage is not evaluated further (the
+ * iterator never passes it to the next stage), as LINQ-to-objects runs the chain
+ * (ComputeQueryableExtensions.cs:628-633). The reference's generator types `int` lambdas this way
+ * (CodeGeneration/CudaKernelGenerator.cs:1351 `%`, :1399-1416 `int`). */
+static int32_t wrap32(int64_t v) { return (int32_t)(uint32_t)(uint64_t)v; }
+
+int32_t oracle_linq_eval_i32(const dc_linq_chain* chain, int32_t x, int32_t* y_out, int32_t* fault_out) {
+  int32_t e = x, v = 0, s0 = 0, s1 = 0;
+  int p = 0, q = 0, keep = 1;
+  if (fault_out) *fault_out = 0;
+  if (!chain || chain->n_instr < 0 || chain->n_instr > DC_LINQ_MAX_INSTR) return DC_ERR_INVALID_ARGUMENT;
+  for (int32_t pc = 0; pc < chain->n_instr && keep; ++pc) {
+    const dc_linq_instr* in = &chain->code[pc];
+    int32_t o;
+    switch (in->src) {
+      case DC_LQ_SRC_IMM: o = in->imm_i32; break;
+      case DC_LQ_SRC_ELEM: o = e; break;
+      case DC_LQ_SRC_S0: o = s0; break;
+      case DC_LQ_SRC_S1: o = s1; break;
+      default: return DC_ERR_INVALID_ARGUMENT;
+    }
+    int c = 0, is_cmp = 0;
+    int32_t num = 0, den = 1;
+    switch (in->op) {
+      case DC_LQ_NOP: break;
+      case DC_LQ_LOAD: v = o; break;
+      case DC_LQ_ADD: v = wrap32((int64_t)v + o); break;
+      case DC_LQ_SUB: v = wrap32((int64_t)v - o); break;
+      case DC_LQ_RSUB: v = wrap32((int64_t)o - v); break;
+      case DC_LQ_MUL: v = wrap32((int64_t)v * o); break;
+      case DC_LQ_DIV: case DC_LQ_REM: num = v; den = o; break;
+      case DC_LQ_RDIV: case DC_LQ_RREM: num = o; den = v; break;
+      case DC_LQ_MIN: v = v < o ? v : o; break;
+      case DC_LQ_MAX: v = v > o ? v : o; break;
+      case DC_LQ_NEG: v = wrap32(-(int64_t)v); break;
+      case DC_LQ_ABS:
+        if (v == INT32_MIN) { if (fault_out) *fault_out = DC_LINQ_FAULT_OVERFLOW; return 0; }
+        v = v < 0 ? -v : v;
+        break;
+      case DC_LQ_STORE_S0: s0 = v; break;
+      case DC_LQ_STORE_S1: s1 = v; break;
+      case DC_LQ_CMP_GT: c = v > o; is_cmp = 1; break;
+      case DC_LQ_CMP_GE: c = v >= o; is_cmp = 1; break;
+      case DC_LQ_CMP_LT: c = v < o; is_cmp = 1; break;
+      case DC_LQ_CMP_LE: c = v <= o; is_cmp = 1; break;
+      case DC_LQ_CMP_EQ: c = v == o; is_cmp = 1; break;
+      case DC_LQ_CMP_NE: c = v != o; is_cmp = 1; break;
+      case DC_LQ_PNOT: p = !p; break;
+      case DC_LQ_PSTORE: q = p; break;
+      case DC_LQ_PAND_Q: p = p && q; break;
+      case DC_LQ_POR_Q: p = p || q; break;
+      case DC_LQ_FILTER: keep = keep && p; break;
+      case DC_LQ_MAP: e = v; break;
+      default: return DC_ERR_UNSUPPORTED; /* SQRT, FLOOR, CEIL, ROUND: no int form */
+    }
+    if (in->op == DC_LQ_DIV || in->op == DC_LQ_RDIV || in->op == DC_LQ_REM || in->op == DC_LQ_RREM) {
+      if (den == 0) { if (fault_out) *fault_out = DC_LINQ_FAULT_DIVIDE_BY_ZERO; return 0; }
+      if (den == -1 && num == INT32_MIN) { if (fault_out) *fault_out = DC_LINQ_FAULT_OVERFLOW; return 0; }
+      v = (in->op == DC_LQ_DIV || in->op == DC_LQ_RDIV) ? num / den : num % den; /* C99: truncation */
+    }
+    if (is_cmp) {
+      if (in->mode == DC_LQ_CMP_SET) p = c;
+      else if (in->mode == DC_LQ_CMP_AND) p = p && c;
+      else if (in->mode == DC_LQ_CMP_OR) p = p || c;
+      else return DC_ERR_INVALID_ARGUMENT;
+    }
+  }
+  if (y_out) *y_out = e;
+  return keep;
+}
+
+/* Runs element i; returns 1 kept, 0 dropped, or -1 when it throws (then *fault = 4 i + kind). */
+static int eval_i32_at(const dc_linq_chain* chain, const int32_t* in, int64_t i, int32_t* y, int64_t* fault) {
+  int32_t kind = 0;
+  const int32_t r = oracle_linq_eval_i32(chain, in[i], y, &kind);
+  if (r < 0) { *fault = r; return -2; }
+  if (kind) { *fault = 4 * i + kind; return -1; }
+  return r;
+}
+
+int64_t oracle_linq_where_select_i32(const dc_linq_chain* chain, const int32_t* in, int64_t n, int32_t* out,
+                                     int64_t* fault_out) {
+  int64_t k = 0, fault = DC_LINQ_FAULT_NONE;
+  for (int64_t i = 0; i < n; ++i) {
+    int32_t y;
+    const int r = eval_i32_at(chain, in, i, &y, &fault);
+    if (r == -2) return fault;
+    if (r < 0) break;
+    if (r) out[k++] = y;
+  }
+  if (fault_out) *fault_out = fault;
+  return k;
+}
+
+/* Enumerable.Sum(IEnumerable<int>) over the Where/Select iterator (no span): `checked(sum += x)`
+ * element by element. Up to the first element that throws (*fault_out = its code, else -1):
+ * *total_out = the exact int64 sum of the kept, mapped elements, *overflow_out = 1 if the checked
+ * int32 running total left int32 at some element. Returns the kept count. The exception C# raises
+ * is the earlier of the two events; a caller that needs it checks the overflow on the elements
+ * before the fault (oracle_linq_where_select_sum_i32 over n = fault index). */
+int64_t oracle_linq_where_select_sum_i32(const dc_linq_chain* chain, const int32_t* in, int64_t n,
+                                         int64_t* total_out, int32_t* overflow_out, int64_t* fault_out) {
+  int64_t k = 0, s = 0, fault = DC_LINQ_FAULT_NONE;
+  int32_t ovf = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    int32_t y;
+    const int r = eval_i32_at(chain, in, i, &y, &fault);
+    if (r == -2) return fault;
+    if (r < 0) break;
+    if (r) {
+      s += y;
+      if (s < INT32_MIN || s > INT32_MAX) ovf = 1;
+      ++k;
+    }
+  }
+  if (total_out) *total_out = s;
+  if (overflow_out) *overflow_out = ovf;
+  if (fault_out) *fault_out = fault;
+  return k;
+}
+
+/* Enumerable.Min / Max(IEnumerable<int>) (op 0 = Min, 1 = Max): the smallest / largest kept,
+ * mapped element up to the first throwing element. Returns the kept count (0 = empty sequence). */
+int64_t oracle_linq_where_select_minmax_i32(const dc_linq_chain* chain, const int32_t* in, int64_t n, int32_t op,
+                                            int32_t* value_out, int64_t* fault_out) {
+  int64_t k = 0, fault = DC_LINQ_FAULT_NONE;
+  int32_t best = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    int32_t y;
+    const int r = eval_i32_at(chain, in, i, &y, &fault);
+    if (r == -2) return fault;
+    if (r < 0) break;
+    if (r) {
+      if (k == 0 || (op == 0 ? y < best : y > best)) best = y;
+      ++k;
+    }
+  }
+  if (value_out) *value_out = best;
+  if (fault_out) *fault_out = fault;
+  return k;
 }
 
 /* BCL Enumerable.Min / Max(IEnumerable<float>), .NET 10 (global.json:3-4), as one step per kept,

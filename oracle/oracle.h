@@ -77,6 +77,16 @@ int64_t oracle_linq_where_select_max(const dc_linq_chain* chain, const float* in
  * (op 0 = Min, 1 = Max): the CPU baseline of the fused Min/Max leg. */
 int64_t oracle_where_gt0_select_2x_plus_1_minmax(const float* in, int64_t n, int32_t op, float* out);
 
+/* ---- LINQ Where/Select over int32 (C# int semantics, exceptions reported as 4 * index + kind,
+ * kind DC_LINQ_FAULT_*; -1 = none) ---- */
+int32_t oracle_linq_eval_i32(const dc_linq_chain* chain, int32_t x, int32_t* y_out, int32_t* fault_out);
+int64_t oracle_linq_where_select_i32(const dc_linq_chain* chain, const int32_t* in, int64_t n, int32_t* out,
+                                     int64_t* fault_out);
+int64_t oracle_linq_where_select_sum_i32(const dc_linq_chain* chain, const int32_t* in, int64_t n,
+                                         int64_t* total_out, int32_t* overflow_out, int64_t* fault_out);
+int64_t oracle_linq_where_select_minmax_i32(const dc_linq_chain* chain, const int32_t* in, int64_t n, int32_t op,
+                                            int32_t* value_out, int64_t* fault_out);
+
 /* ---- GEMM ---- */
 void oracle_gemm_f32_naive(const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k,
                            int32_t threads);

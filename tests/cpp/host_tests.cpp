@@ -3,7 +3,9 @@
 // are checked against the CPU oracle (oracle/liboracle.so), which this test binary links as the
 // checker only.
 #include <algorithm>
+#include <atomic>
 #include <cmath>
+#include <thread>
 #include <cstring>
 #include <random>
 
@@ -36,7 +38,7 @@ bool BitsEqual(const std::vector<float>& a, const std::vector<float>& b) {
 }
 
 std::string Listing(const Expr& where, const Expr& select) {
-  auto q = ComputeQueryable(nullptr, 0, std::make_shared<ComputeQueryProvider>(nullptr)).Where(where).Select(select);
+  auto q = ComputeQueryable<float>(nullptr, 0, std::make_shared<ComputeQueryProvider>(nullptr)).Where(where).Select(select);
   return q.Explain().Listing();
 }
 
@@ -87,7 +89,7 @@ bool EvalPred(const ExprNode& n, float x) {
 // Planner output for a Where(pred).Select(sel) chain, run by the oracle's interpreter, must equal
 // the direct evaluation of the two trees on every input.
 void CheckProgramAgainstTree(const Expr& pred, const Expr& sel, const std::vector<float>& xs) {
-  auto q = ComputeQueryable(nullptr, 0, std::make_shared<ComputeQueryProvider>(nullptr)).Where(pred).Select(sel);
+  auto q = ComputeQueryable<float>(nullptr, 0, std::make_shared<ComputeQueryProvider>(nullptr)).Where(pred).Select(sel);
   FusedKernelPlan plan = q.Explain();
   for (float x : xs) {
     float y = 0.0f;
@@ -100,6 +102,101 @@ void CheckProgramAgainstTree(const Expr& pred, const Expr& sel, const std::vecto
       CHECK((std::isnan(ref) && std::isnan(y)) || std::memcmp(&ref, &y, 4) == 0);
     }
   }
+}
+
+// C# `int` evaluation of a lambda tree (unchecked + - *, / and % truncating, throwing
+// DivideByZeroException / OverflowException, Math.Abs throwing for int.MinValue, operands left to
+// right, && and || short-circuiting). Returns the fault kind (0 none) through `fault`.
+struct IntEval {
+  int fault = 0;
+  int32_t Value(const ExprNode& n, int32_t x) {
+    if (fault) return 0;
+    switch (n.Kind) {
+      case ExprKind::Parameter: return x;
+      case ExprKind::Constant: return n.IValue;
+      case ExprKind::Negate: return (int32_t)(0u - (uint32_t)Value(*n.Left, x));
+      case ExprKind::Abs: {
+        const int32_t v = Value(*n.Left, x);
+        if (!fault && v == INT32_MIN) fault = DC_LINQ_FAULT_OVERFLOW;
+        return v < 0 ? -v : v;
+      }
+      default: break;
+    }
+    const int32_t a = Value(*n.Left, x);
+    const int32_t b = Value(*n.Right, x);
+    if (fault) return 0;
+    switch (n.Kind) {
+      case ExprKind::Add: return (int32_t)((uint32_t)a + (uint32_t)b);
+      case ExprKind::Subtract: return (int32_t)((uint32_t)a - (uint32_t)b);
+      case ExprKind::Multiply: return (int32_t)((uint32_t)a * (uint32_t)b);
+      case ExprKind::Divide:
+      case ExprKind::Modulo:
+        if (b == 0) { fault = DC_LINQ_FAULT_DIVIDE_BY_ZERO; return 0; }
+        if (b == -1 && a == INT32_MIN) { fault = DC_LINQ_FAULT_OVERFLOW; return 0; }
+        return n.Kind == ExprKind::Divide ? a / b : a % b;
+      case ExprKind::Min: return std::min(a, b);
+      case ExprKind::Max: return std::max(a, b);
+      default: throw std::logic_error("not an int value");
+    }
+  }
+  bool Pred(const ExprNode& n, int32_t x) {
+    if (fault) return false;
+    switch (n.Kind) {
+      case ExprKind::AndAlso: return Pred(*n.Left, x) && Pred(*n.Right, x);
+      case ExprKind::OrElse: return Pred(*n.Left, x) || Pred(*n.Right, x);
+      case ExprKind::Not: return !Pred(*n.Left, x);
+      default: break;
+    }
+    const int32_t a = Value(*n.Left, x), b = Value(*n.Right, x);
+    switch (n.Kind) {
+      case ExprKind::GreaterThan: return a > b;
+      case ExprKind::GreaterThanOrEqual: return a >= b;
+      case ExprKind::LessThan: return a < b;
+      case ExprKind::LessThanOrEqual: return a <= b;
+      case ExprKind::Equal: return a == b;
+      case ExprKind::NotEqual: return a != b;
+      default: throw std::logic_error("not a predicate");
+    }
+  }
+};
+
+FusedKernelPlan PlanI32(const Expr& pred, const Expr& sel) {
+  return ComputeQueryable<int32_t>(nullptr, 0, std::make_shared<ComputeQueryProvider>(nullptr)).Where(pred).Select(sel)
+      .Explain();
+}
+
+// The int32 program of Where(pred).Select(sel), run by the oracle's interpreter, must keep, map
+// and throw exactly as the C# evaluation of the two trees does, element by element.
+void CheckProgramAgainstTreeI32(const Expr& pred, const Expr& sel, const std::vector<int32_t>& xs) {
+  FusedKernelPlan plan = PlanI32(pred, sel);
+  CHECK(plan.Element == ElementType::Int32);
+  for (int32_t x : xs) {
+    int32_t y = 0, kind = 0;
+    const int32_t keep = oracle_linq_eval_i32(&plan.Program, x, &y, &kind);
+    CHECK(keep >= 0);
+    IntEval ev;
+    const bool want = ev.Pred(pred.Node(), x);
+    int32_t ref = 0;
+    if (!ev.fault && want) ref = ev.Value(sel.Node(), x);
+    CHECK(kind == ev.fault);
+    if (!ev.fault) {
+      CHECK((keep == 1) == want);
+      if (want) CHECK(y == ref);
+    }
+  }
+}
+
+std::vector<int32_t> IntSamples(size_t n, uint64_t seed) {
+  std::vector<int32_t> v(n);
+  oracle_gen_uniform_i32(v.data(), (int64_t)n, seed, 1, -1000, 1000);
+  for (int32_t e : {0, 1, -1, 2, -2, 46341, -46341, INT32_MAX, INT32_MIN, INT32_MIN + 1}) v.push_back(e);
+  return v;
+}
+
+std::vector<int32_t> Range(int32_t start, int32_t count) {  // Enumerable.Range
+  std::vector<int32_t> v((size_t)count);
+  for (int32_t i = 0; i < count; ++i) v[(size_t)i] = start + i;
+  return v;
 }
 
 std::shared_ptr<Backends::Hip::HipAccelerator> Gpu() {
@@ -115,19 +212,19 @@ std::shared_ptr<Backends::Hip::HipAccelerator> Gpu() {
 TEST_CPU(planner_emits_the_benchmark_chain) {
   auto x = Param();
   const std::string l = Listing(x > 0.0f, x * 2.0f + 1.0f);
-  CHECK(l == "terminal ToArray\n0: LOAD e\n1: CMP_GT 0\n2: FILTER\n3: LOAD e\n4: MUL 2\n5: ADD 1\n6: MAP\n");
+  CHECK(l == "terminal ToArray (float32)\n0: LOAD e\n1: CMP_GT 0\n2: FILTER\n3: LOAD e\n4: MUL 2\n5: ADD 1\n6: MAP\n");
 }
 
 TEST_CPU(planner_swaps_constant_on_the_left) {
   auto x = Param();
-  CHECK(Listing(0.5f < x, 2.0f - x) == "terminal ToArray\n0: LOAD e\n1: CMP_GT 0.5\n2: FILTER\n3: LOAD e\n4: RSUB 2\n5: MAP\n");
-  CHECK(Listing(1.0f >= x, 3.0f / x) == "terminal ToArray\n0: LOAD e\n1: CMP_LE 1\n2: FILTER\n3: LOAD e\n4: RDIV 3\n5: MAP\n");
+  CHECK(Listing(0.5f < x, 2.0f - x) == "terminal ToArray (float32)\n0: LOAD e\n1: CMP_GT 0.5\n2: FILTER\n3: LOAD e\n4: RSUB 2\n5: MAP\n");
+  CHECK(Listing(1.0f >= x, 3.0f / x) == "terminal ToArray (float32)\n0: LOAD e\n1: CMP_LE 1\n2: FILTER\n3: LOAD e\n4: RDIV 3\n5: MAP\n");
 }
 
 TEST_CPU(planner_folds_constants_like_csharp) {
   auto x = Param();
   CHECK(Listing(x > (1.0f - 1.0f), x * (2.0f + 1.0f)) ==
-        "terminal ToArray\n0: LOAD e\n1: CMP_GT 0\n2: FILTER\n3: LOAD e\n4: MUL 3\n5: MAP\n");
+        "terminal ToArray (float32)\n0: LOAD e\n1: CMP_GT 0\n2: FILTER\n3: LOAD e\n4: MUL 3\n5: MAP\n");
 }
 
 TEST_CPU(planner_uses_save_registers_for_two_subtrees) {
@@ -195,7 +292,7 @@ TEST_CPU(visitor_maps_methods_like_the_reference) {
 TEST_CPU(planner_terminals_and_unsupported_operators) {
   auto x = Param();
   auto p = std::make_shared<ComputeQueryProvider>(nullptr);
-  auto q = ComputeQueryable(nullptr, 0, p).Where(x > 0.0f).Select(x * 2.0f + 1.0f);
+  auto q = ComputeQueryable<float>(nullptr, 0, p).Where(x > 0.0f).Select(x * 2.0f + 1.0f);
   CHECK(q.Explain(Terminal::Sum).Term == Terminal::Sum);
   CHECK(q.Explain(Terminal::Average).Term == Terminal::Average);
   CHECK(q.Explain(Terminal::Count).FusedOperationIds.size() == 3);
@@ -203,6 +300,60 @@ TEST_CPU(planner_terminals_and_unsupported_operators) {
   CHECK(q.Explain(Terminal::Max).Term == Terminal::Max);
   CHECK_THROWS(NotSupportedException, q.OrderBy(x).Explain());
   CHECK_THROWS(InvalidOperationException, q.Min());  // no HIP device behind this provider
+}
+
+TEST_CPU(planner_int_chains_follow_csharp_int_semantics) {
+  auto x = Param();
+  // Range(1, 100).Where(x => x % 2 == 0).Select(x => x * x) (LinqBackendIntegrationTests.cs:309-325)
+  CHECK(PlanI32(x % 2 == 0, x * x).Listing() ==
+        "terminal ToArray (int32)\n0: LOAD e\n1: REM 2\n2: CMP_EQ 0\n3: FILTER\n4: LOAD e\n5: MUL e\n6: MAP\n");
+  CHECK(!PlanI32(x % 2 == 0, x * x).CanFault);
+  CHECK(PlanI32(x != 0, 100 / x).CanFault);
+  CHECK(PlanI32(x > 0, x / -1).CanFault);  // int.MinValue / -1
+  CHECK(PlanI32(x > 0, Math::Abs(x)).CanFault);
+  const auto xs = IntSamples(4000, 5);
+  CheckProgramAgainstTreeI32(x % 2 == 0, x * x, xs);
+  CheckProgramAgainstTreeI32(x > 2, x * 2, xs);
+  CheckProgramAgainstTreeI32(x % 7 != 3 && x < 500, (x + 1) * (x - 1) - x % 5, xs);
+  CheckProgramAgainstTreeI32(x != 0, 1000 / x + 1000 % x, xs);
+  CheckProgramAgainstTreeI32(x > -5, 100 / x, xs);        // throws for x == 0
+  CheckProgramAgainstTreeI32(x < 0 || x > 10, -x * 3, xs);  // wraps for int.MinValue
+  CheckProgramAgainstTreeI32(x >= INT32_MIN, Math::Abs(x) % 1000, xs);
+  CheckProgramAgainstTreeI32(x * x > 100, Math::Min(x, 7) + Math::Max(x * 3, -9), xs);
+  CheckProgramAgainstTreeI32(x != 1, (x / (x - 1)) + (x % (x + 1)), xs);  // both operands throw
+  CheckProgramAgainstTreeI32(!(x > 0), x / -1, xs);       // OverflowException for int.MinValue
+}
+
+TEST_CPU(planner_int_chains_reject_type_changes_and_conditional_throws) {
+  auto x = Param();
+  CHECK_THROWS(NotSupportedException, PlanI32(x > 0.5f, x));          // x > 0.5f is a float comparison
+  CHECK_THROWS(NotSupportedException, PlanI32(x > 0, x * 2.0f));      // Select to float
+  CHECK_THROWS(NotSupportedException, PlanI32(x > 0, MathF::Sqrt(x)));
+  CHECK_THROWS(NotSupportedException, PlanI32(x != 0 && 10 / x > 1, x));  // evaluated only when x != 0
+  CHECK_THROWS(NotSupportedException, PlanI32(x == 0 || 10 % x > 1, x));
+  PlanI32(10 / x > 1 && x != 0, x);  // a throwing left operand is always evaluated: fine
+  // C# constant folding is checked
+  CHECK_THROWS(OverflowException, Expr(INT32_MAX) + Expr(1));
+  CHECK_THROWS(DivideByZeroException, Expr(1) / Expr(0));
+  CHECK(((Expr(7) + Expr(5)) % Expr(5)).Node().IValue == 2);
+  // an int literal in a float lambda is converted to float (x > 0 means x > 0f)
+  CHECK(Listing(x > 0, x * 2 + 1) == Listing(x > 0.0f, x * 2.0f + 1.0f));
+}
+
+TEST_CPU(planner_float_remainder_and_rounding_match_tree_evaluation) {
+  auto x = Param();
+  auto q = ComputeQueryable<float>(nullptr, 0, std::make_shared<ComputeQueryProvider>(nullptr));
+  const FusedKernelPlan plan = q.Where(x % 0.25f != 0.0f).Select(MathF::Floor(x * 8.0f) + MathF::Ceiling(x) +
+                                                                 MathF::Round(x * 3.0f)).Explain();
+  for (float v : Uniform(5000, 21)) {
+    float y = 0.0f;
+    const int32_t keep = oracle_linq_eval(&plan.Program, v, &y);
+    CHECK((keep == 1) == (std::fmod(v, 0.25f) != 0.0f));
+    if (keep == 1) {
+      const float ref = (std::floor(v * 8.0f) + std::ceil(v)) + std::nearbyint(v * 3.0f);
+      CHECK(std::memcmp(&ref, &y, 4) == 0);
+    }
+  }
 }
 
 // ============================== CPU: runtime, registry, no-device behaviour =======================
@@ -236,7 +387,7 @@ TEST_CPU(generated_registry_describes_every_kernel) {
   // KernelExecutionMetadataTests' checks, on this build's generated registry: dimensionality,
   // parameter descriptors, the HIP slot, and CPU-only registration when a body has no translation.
   auto regs = Generated::KernelRegistry::GetAllKernels();
-  CHECK(regs.size() == 11);
+  CHECK(regs.size() == 12);
   const auto& t = Registered(regs, "Transpose");
   CHECK(t.Dimensions == 2 && t.FullName == "DotCompute.Samples.Grids.Transpose");
   CHECK((t.SupportedBackends == std::vector<std::string>{"CPU", "HIP"}));
@@ -247,8 +398,13 @@ TEST_CPU(generated_registry_describes_every_kernel) {
   const auto& saxpy = Registered(regs, "Saxpy");  // reads and writes y; only reads x
   CHECK(saxpy.Parameters[0].IsRead && !saxpy.Parameters[0].IsWritten);
   CHECK(saxpy.Parameters[1].IsRead && saxpy.Parameters[1].IsWritten);
-  const auto& vadd = Registered(regs, "VectorAdd");  // the output is never read: not copied in
-  CHECK(!vadd.Parameters[2].IsRead && vadd.Parameters[2].IsWritten);
+  const auto& vadd = Registered(regs, "VectorAdd");  // the output is written in full, never read: not copied in
+  CHECK(!vadd.Parameters[2].IsRead && vadd.Parameters[2].IsWritten && vadd.Parameters[2].IsCovered);
+  // Outputs written under a condition (or in two branches) are copied in: elements the body leaves
+  // alone must come back as the caller's values.
+  CHECK(!Registered(regs, "CopyPositive").Parameters[1].IsCovered);
+  CHECK(!Registered(regs, "ScaleClamp").Parameters[1].IsCovered);
+  CHECK(Registered(regs, "HashMix").Parameters[1].IsCovered);
   CHECK((vadd.SupportedBackends == std::vector<std::string>{"CPU"}));
   const auto& soft = Registered(regs, "Softplus");
   CHECK(soft.HipEntryPoint.empty() && soft.HipDiagnostic.find("MathF.Log") != std::string::npos);
@@ -533,6 +689,47 @@ TEST_GPU(generated_elementwise_kernels_match_oracle) {
   }
 }
 
+TEST_GPU(generated_partial_writes_keep_the_callers_elements) {
+  // A kernel that writes only some elements of its output must hand back the caller's values for
+  // the rest, even when the device block it runs in last held another launch's data.
+  auto orch = HipOrchestrator();
+  const size_t n = 300001;
+  std::vector<float> a(n, 7.0f), b(n, 8.0f), r(n, 0.0f);
+  orch->ExecuteAsync("VectorAdd", "HIP", {Arg(a), Arg(b), Arg(r)}).get();  // leaves 15.0f in a pooled block
+  auto in = Uniform(n, 81, 0);
+  for (int round = 0; round < 2; ++round) {
+    std::vector<float> out(n, -5.0f), ref(n);
+    for (size_t i = 0; i < n; ++i) ref[i] = in[i] > 0.0f ? in[i] : -5.0f;
+    std::vector<float> res = orch->ExecuteAsync("CopyPositive", "HIP", {Arg(in), Arg(out)}).get();
+    CHECK(BitsEqual(out, ref) && BitsEqual(res, ref));
+  }
+}
+
+TEST_GPU(generated_kernel_exceptions_are_not_lost_between_threads) {
+  // Two threads launch generated kernels on one accelerator at the same time; every launch that
+  // divides by zero must raise its exception, whatever the other thread's launch reported.
+  auto orch = HipOrchestrator();
+  std::atomic<int> thrown{0}, wrong{0};
+  auto worker = [&](bool faulting) {
+    for (int it = 0; it < 20; ++it) {
+      std::vector<int32_t> a(50000, 7), b(50000, 1), q(50000);
+      if (faulting) b[12345] = 0;
+      try {
+        orch->ExecuteAsync("IntDivide", "HIP", {Arg(a), Arg(b), Arg(q)}).get();
+        if (faulting) ++wrong;
+      } catch (const DivideByZeroException&) {
+        if (faulting) ++thrown;
+        else ++wrong;
+      }
+    }
+  };
+  std::thread t1(worker, true), t2(worker, false), t3(worker, true);
+  t1.join();
+  t2.join();
+  t3.join();
+  CHECK(thrown.load() == 40 && wrong.load() == 0);
+}
+
 TEST_GPU(generated_grid_kernels_match_oracle) {
   auto orch = HipOrchestrator();
   {  // 2-D transpose, rows x cols not a multiple of anything
@@ -638,6 +835,105 @@ TEST_GPU(linq_reference_golden_vectors) {
   std::vector<float> with_nan{1.0f, NAN, 2.0f};
   CHECK(!AsComputeQueryable(with_nan, p).All(x > 0.0f));  // NaN > 0 is false
   CHECK(AsComputeQueryable(with_nan, p).Any(x != x));     // and NaN != NaN is true
+}
+
+TEST_GPU(linq_reference_golden_vectors_on_int_sources) {
+  // The reference's LINQ known answers, as written: int sources and int lambdas.
+  auto x = Param();
+  auto p = std::make_shared<ComputeQueryProvider>(Gpu());
+  // ComputeQueryProviderTests.cs:341-365: {1..5}.Where(x > 3) -> {4, 5}; {1,2,3}.Select(x * 2) -> {2, 4, 6}
+  std::vector<int32_t> s15{1, 2, 3, 4, 5}, s3{1, 2, 3};
+  CHECK((AsComputeQueryable(s15, p).Where(x > 3).ToArray() == std::vector<int32_t>{4, 5}));
+  CHECK((AsComputeQueryable(s3, p).Select(x * 2).ToArray() == std::vector<int32_t>{2, 4, 6}));
+  // :602-612: Sum of {1..5} = 15
+  CHECK(AsComputeQueryable(s15, p).Sum() == 15);
+  // LinqBackendIntegrationTests.cs:51-66: Where(x > 2).Select(x * 2) -> {6, 8, 10}
+  CHECK((AsComputeQueryable(s15, p).Where(x > 2).Select(x * 2).ToArray() == std::vector<int32_t>{6, 8, 10}));
+  // :139-161: {1..10}.Where(x > 3).Select(x * 3) -> {12, ..., 30}
+  CHECK((AsComputeQueryable(Range(1, 10), p).Where(x > 3).Select(x * 3).ToArray() ==
+         std::vector<int32_t>{12, 15, 18, 21, 24, 27, 30}));
+  // :164-176: Enumerable.Range(1, 1000).Sum() == 500500
+  const auto r1000 = Range(1, 1000);
+  CHECK(AsComputeQueryable(r1000, p).Sum() == 500500);
+  // :309-325: Range(1, 100).Where(x % 2 == 0).Select(x * x): 50 elements, first 4, last 10000
+  const auto r100 = Range(1, 100);
+  const auto sq = AsComputeQueryable(r100, p).Where(x % 2 == 0).Select(x * x).ToArray();
+  CHECK(sq.size() == 50 && sq.front() == 4 && sq.back() == 10000);
+  CHECK(AsComputeQueryable(r100, p).Where(x % 2 == 0).Select(x * x).Sum() == 171700);  // 4 * (1^2 + ... + 50^2)
+  CHECK(AsComputeQueryable(r100, p).Where(x % 2 == 0).Count() == 50);
+  CHECK(AsComputeQueryable(r100, p).Average() == 50.5);
+  CHECK(AsComputeQueryable(r100, p).Where(x > 10).Min() == 11 && AsComputeQueryable(r100, p).Max() == 100);
+  std::vector<int32_t> empty;
+  CHECK(AsComputeQueryable(empty, p).Sum() == 0);
+  CHECK_THROWS(InvalidOperationException, AsComputeQueryable(empty, p).Max());
+  CHECK_THROWS(InvalidOperationException, AsComputeQueryable(s15, p).Where(x > 9).Average());
+}
+
+TEST_GPU(linq_int_exceptions_follow_linq_to_objects) {
+  auto x = Param();
+  auto p = std::make_shared<ComputeQueryProvider>(Gpu());
+  std::vector<int32_t> z{5, 0, 7};
+  CHECK_THROWS(DivideByZeroException, AsComputeQueryable(z, p).Select(100 / x).ToArray());
+  CHECK_THROWS(DivideByZeroException, AsComputeQueryable(z, p).Select(100 % x).Sum());
+  // a Where that drops the zero keeps the Select from ever dividing by it
+  CHECK((AsComputeQueryable(z, p).Where(x != 0).Select(100 / x).ToArray() == std::vector<int32_t>{20, 14}));
+  std::vector<int32_t> m{3, INT32_MIN};
+  CHECK_THROWS(OverflowException, AsComputeQueryable(m, p).Select(x / -1).ToArray());
+  CHECK_THROWS(OverflowException, AsComputeQueryable(m, p).Select(Math::Abs(x)).Max());
+  CHECK(AsComputeQueryable(m, p).Select(-x).Min() == INT32_MIN);  // unchecked negation wraps
+  // Sum: which comes first, the overflow of the running total or the throwing element
+  std::vector<int32_t> a{INT32_MAX, 1, 0};  // x + 1000 / x: MaxValue, 1001 (the total overflows), then / 0
+  CHECK_THROWS(OverflowException, AsComputeQueryable(a, p).Select(x + 1000 / x).Sum());
+  CHECK_THROWS(DivideByZeroException, AsComputeQueryable(a, p).Select(x + 1000 / x).Count());
+  std::vector<int32_t> b{INT32_MAX, 0, 1};
+  CHECK_THROWS(DivideByZeroException, AsComputeQueryable(b, p).Select(x / x).Sum());
+  // The two overflow rules of Enumerable.Sum(int): a bare array (span, 8 lanes) against the
+  // element-by-element running total after Select. [int.MaxValue, 1, -1]: both throw.
+  std::vector<int32_t> c{INT32_MAX, 1, -1};
+  CHECK_THROWS(OverflowException, AsComputeQueryable(c, p).Sum());
+  CHECK_THROWS(OverflowException, AsComputeQueryable(c, p).Select(x).Sum());
+  // 32 elements, x0 = int.MaxValue, x1 = 1, x8 = -1: lane 0 holds MaxValue - 1, lane 1 holds 1, and
+  // the lane totals add to MaxValue: no exception over the array; the running total overflows at x1.
+  std::vector<int32_t> d(32, 0);
+  d[0] = INT32_MAX;
+  d[1] = 1;
+  d[8] = -1;
+  CHECK(AsComputeQueryable(d, p).Sum() == INT32_MAX);
+  CHECK_THROWS(OverflowException, AsComputeQueryable(d, p).Select(x).Sum());
+  CHECK(AsComputeQueryable(d, p).Select(x).Average() == (double)INT32_MAX / 32.0);  // a long sum: no overflow
+}
+
+TEST_GPU(linq_int_chains_match_oracle_at_1m) {
+  auto x = Param();
+  auto p = std::make_shared<ComputeQueryProvider>(Gpu());
+  std::vector<int32_t> src(1 << 20);
+  oracle_gen_uniform_i32(src.data(), (int64_t)src.size(), 45, 1, -1000, 1000);
+  auto q = AsComputeQueryable(src, p).Where(x % 3 != 0).Select(x * x - 7 * x);
+  const FusedKernelPlan plan = q.Explain();
+  std::vector<int32_t> ref(src.size());
+  int64_t fault = 0;
+  const int64_t k = oracle_linq_where_select_i32(&plan.Program, src.data(), (int64_t)src.size(), ref.data(), &fault);
+  ref.resize((size_t)k);
+  CHECK(fault == DC_LINQ_FAULT_NONE && q.ToArray() == ref);
+  int64_t total = 0;
+  int32_t ovf = 0;
+  const FusedKernelPlan ps = q.Explain(Terminal::Sum);
+  CHECK(oracle_linq_where_select_sum_i32(&ps.Program, src.data(), (int64_t)src.size(), &total, &ovf, &fault) == k);
+  CHECK(ovf == 1);  // about 700k values of ~3e5 each: the running total leaves int32
+  CHECK_THROWS(OverflowException, q.Sum());
+  CHECK(q.LongCount() == k);
+  CHECK(q.Average() == (double)total / (double)k);
+  int32_t mn = 0, mx = 0;
+  const FusedKernelPlan pm = q.Explain(Terminal::Min);
+  oracle_linq_where_select_minmax_i32(&pm.Program, src.data(), (int64_t)src.size(), 0, &mn, &fault);
+  oracle_linq_where_select_minmax_i32(&pm.Program, src.data(), (int64_t)src.size(), 1, &mx, &fault);
+  CHECK(q.Min() == mn && q.Max() == mx);
+  auto q2 = AsComputeQueryable(src, p).Where(x > 0).Select(x - 500);  // small values: no overflow
+  CHECK(q2.Sum() == (int32_t)[&] {
+    int64_t s = 0;
+    for (int32_t v : src) s += v > 0 ? v - 500 : 0;
+    return s;
+  }());
 }
 
 TEST_GPU(linq_min_max_match_enumerable) {

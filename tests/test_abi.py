@@ -69,7 +69,7 @@ def test_chain_validation():
     L = hip.load()
     good = hip.where_gt0_select_2x_plus_1()
     assert L.dc_linq_chain_validate(C.byref(good)) == 0
-    bad_op = hip.LinqChain.assemble([(17, hip.SRC_IMM, 0)])
+    bad_op = hip.LinqChain.assemble([(40, hip.SRC_IMM, 0)])
     assert L.dc_linq_chain_validate(C.byref(bad_op)) == hip.DC_ERR_UNSUPPORTED
     bad_src = hip.LinqChain.assemble([(hip.LOAD, 9, 0)])
     assert L.dc_linq_chain_validate(C.byref(bad_src)) == hip.DC_ERR_UNSUPPORTED
@@ -106,7 +106,8 @@ CSHARP_LAYOUTS = {
         ("wave_size", 328, 4), ("max_threads_per_block", 332, 4), ("clock_khz", 336, 4),
         ("memory_clock_khz", 340, 4), ("memory_bus_width_bits", 344, 4), ("l2_cache_bytes", 348, 4),
         ("total_global_mem", 352, 8), ("lds_per_block", 360, 8), ("pci_bus_id", 368, 4), ("is_gfx950", 372, 4)]),
-    "dc_linq_instr": (8, [("op", 0, 1), ("src", 1, 1), ("mode", 2, 1), ("pad", 3, 1), ("imm", 4, 4)]),
+    "dc_linq_instr": (8, [("op", 0, 1), ("src", 1, 1), ("mode", 2, 1), ("pad", 3, 1), ("imm", 4, 4),
+                          ("imm_i32", 4, 4)]),
     "dc_linq_chain": (8 + 8 * 48, [("n_instr", 0, 4), ("flags", 4, 4), ("code", 8, 8 * 48)]),
     "dc_gen_launch": (152, [("work", 0, 8), ("epoch", 8, 4), ("reserved", 12, 4), ("error", 16, 8),
                             ("len", 24, 8 * 16)]),

@@ -325,9 +325,9 @@ def test_stream_probes(ctx, n):
 
 def test_stream_probe_arguments(ctx):
     dx, dd = ctx.empty(16, np.float32), ctx.empty(16, np.float32)
-    lib = hip.load()
-    assert lib.dc_hip_stream_probe(ctx.handle, hip.PROBE_COPY, dx.ptr, dd.ptr, 12) == hip.DC_ERR_INVALID_ARGUMENT
-    assert lib.dc_hip_stream_probe(ctx.handle, 3, dx.ptr, dd.ptr, 8) == hip.DC_ERR_INVALID_ARGUMENT
-    assert lib.dc_hip_stream_probe(ctx.handle, hip.PROBE_COPY, dx.ptr + 4, dd.ptr, 8) == hip.DC_ERR_MISALIGNED
+    lib = hip.load_bench()
+    assert lib.dc_bench_stream_probe(ctx.handle, hip.PROBE_COPY, dx.ptr, dd.ptr, 12) == hip.DC_ERR_INVALID_ARGUMENT
+    assert lib.dc_bench_stream_probe(ctx.handle, 3, dx.ptr, dd.ptr, 8) == hip.DC_ERR_INVALID_ARGUMENT
+    assert lib.dc_bench_stream_probe(ctx.handle, hip.PROBE_COPY, dx.ptr + 4, dd.ptr, 8) == hip.DC_ERR_MISALIGNED
     for x_ in (dx, dd):
         ctx.free(x_)

@@ -30,8 +30,8 @@ def test_corpus_registers_every_kernel(tmp_path):
     recs = generate(sorted(os.path.join(KERNELS, f) for f in os.listdir(KERNELS) if f.endswith(".cs")),
                     str(tmp_path), root=ROOT)
     by = {r["km"].name: r for r in recs}
-    assert set(by) == {"VectorAdd", "Saxpy", "ScaleClamp", "HashMix", "LongMix", "Gather", "IntDivide", "Softplus",
-                       "Transpose", "MatMulNaive", "Stencil3D"}
+    assert set(by) == {"VectorAdd", "Saxpy", "ScaleClamp", "HashMix", "LongMix", "CopyPositive", "Gather", "IntDivide",
+                       "Softplus", "Transpose", "MatMulNaive", "Stencil3D"}
     assert by["VectorAdd"]["km"].full_name == "Kernels.VectorAdd" and by["VectorAdd"]["km"].backends == ["CPU"]
     assert by["Saxpy"]["km"].full_name == "DotCompute.Samples.Elementwise.Saxpy"
     assert by["Saxpy"]["km"].backends == ["CPU", "HIP"]
@@ -39,13 +39,30 @@ def test_corpus_registers_every_kernel(tmp_path):
     assert by["Softplus"]["entry"] is None and "MathF.Log" in by["Softplus"]["error"]
     hip = (tmp_path / "dc_generated_kernels.hip").read_text()
     reg = (tmp_path / "KernelRegistry.g.cpp").read_text()
-    assert hip.count('extern "C" __global__') == 10
+    assert hip.count('extern "C" __global__') == 11
     assert 'k.Name = "Transpose";' in reg and "k.Dimensions = 2;" in reg and "HipKernelAbi::Generated" in reg
     assert 'k.HipDiagnostic = "call to MathF.Log";' in reg
     # the generated files of the build are exactly what the generator writes for this corpus
     built = os.path.join(ROOT, "dotcompute_amd", "_build", "generated", "KernelRegistry.g.cpp")
     if os.path.exists(built):
         assert open(built).read() == reg
+
+
+def test_full_write_analysis_is_conservative():
+    """Only a buffer written in full (the work-size buffer, assigned at the work index, at most under
+    the bounds guard, before any return) may skip the copy to the device: anything else is copied in."""
+    cov = lambda body, params="ReadOnlySpan<float> a, Span<float> b": kernel(body, params)["covered"]
+    assert cov("int i = KernelContext.ThreadId.X; if (i < b.Length) b[i] = a[i];") == {"b"}
+    assert cov("int i = KernelContext.ThreadId.X; b[i] = a[i] * 2f;") == {"b"}
+    assert cov("int i = KernelContext.ThreadId.X; if (i < b.Length) { float t = a[i]; b[i] = t; }") == {"b"}
+    assert cov("int i = KernelContext.ThreadId.X; if (i < b.Length && a[i] > 0f) b[i] = a[i];") == set()
+    assert cov("int i = KernelContext.ThreadId.X; if (a[i] > 0f) b[i] = 1f; else b[i] = 2f;") == set()
+    assert cov("int i = KernelContext.ThreadId.X; if (a[i] > 0f) return; b[i] = 1f;") == set()
+    assert cov("int i = KernelContext.ThreadId.X; i = i / 2; b[i] = 1f;") == set()
+    assert cov("int i = KernelContext.ThreadId.X; b[i / 2] = 1f;") == set()
+    # the work size is the FIRST writable span: a second output is not covered by its index
+    assert cov("int i = KernelContext.ThreadId.X; if (i < b.Length) { b[i] = a[i]; c[i] = a[i]; }",
+               "ReadOnlySpan<float> a, Span<float> b, Span<float> c") == {"b"}
 
 
 def test_transpose_2d_coordinates_and_intrinsics():

@@ -221,6 +221,75 @@ def test_benchmark_chain_matches_numpy_golden_and_interpreter():
     assert oracle.where_gt0_select_2x_plus_1(edge).tolist() == [np.inf, np.float32(1e-45) * 2 + 1]
 
 
+def _ichain(code):
+    from dotcompute_amd.hip import LinqChain
+    return LinqChain.assemble(code, int32=True)
+
+
+def test_int_chains_reference_known_answers():
+    """The reference's LINQ known answers on int sources (LinqBackendIntegrationTests.cs:51-66,
+    :164-176, :309-325): the oracle's int interpreter against closed forms."""
+    from dotcompute_amd.hip import CMP_EQ, CMP_GT, FILTER, LOAD, MAP, MUL, REM, SRC_ELEM, SRC_IMM
+    even_sq = _ichain([(LOAD, SRC_ELEM, 0), (REM, SRC_IMM, 2), (CMP_EQ, SRC_IMM, 0), (FILTER, SRC_IMM, 0),
+                       (LOAD, SRC_ELEM, 0), (MUL, SRC_ELEM, 0), (MAP, SRC_IMM, 0)])
+    r100 = np.arange(1, 101, dtype=np.int32)
+    out, fault = oracle.linq_where_select_i32(even_sq, r100)
+    assert fault == -1 and out.tolist() == [(2 * k) ** 2 for k in range(1, 51)]
+    total, k, ovf, fault = oracle.linq_where_select_sum_i32(even_sq, r100)
+    assert (total, k, ovf, fault) == (4 * 50 * 51 * 101 // 6, 50, False, -1)  # 4 * sum of k^2 = 171700
+    ws = _ichain([(LOAD, SRC_ELEM, 0), (CMP_GT, SRC_IMM, 2), (FILTER, SRC_IMM, 0),
+                  (LOAD, SRC_ELEM, 0), (MUL, SRC_IMM, 2), (MAP, SRC_IMM, 0)])
+    assert oracle.linq_where_select_i32(ws, np.arange(1, 6, dtype=np.int32))[0].tolist() == [6, 8, 10]
+    ident = _ichain([(LOAD, SRC_ELEM, 0), (MAP, SRC_IMM, 0)])
+    assert oracle.linq_where_select_sum_i32(ident, np.arange(1, 1001, dtype=np.int32))[0] == 500500
+
+
+def test_int_chains_match_numpy_wrapping_arithmetic():
+    """Where(x % 3 != 0).Select(x * x - 7 * x) over the whole int range: numpy's int32 arithmetic
+    wraps as C#'s unchecked int does, and np.fmod truncates as C#'s % does (not Python's %)."""
+    from dotcompute_amd.hip import CMP_NE, FILTER, LOAD, MAP, MUL, REM, SRC_ELEM, SRC_IMM, SRC_S0, STORE_S0, SUB
+    poly = _ichain([(LOAD, SRC_ELEM, 0), (REM, SRC_IMM, 3), (CMP_NE, SRC_IMM, 0), (FILTER, SRC_IMM, 0),
+                    (LOAD, SRC_ELEM, 0), (MUL, SRC_IMM, 7), (STORE_S0, SRC_IMM, 0),
+                    (LOAD, SRC_ELEM, 0), (MUL, SRC_ELEM, 0), (SUB, SRC_S0, 0), (MAP, SRC_IMM, 0)])
+    x = oracle.gen_uniform_i32(200_000, 60, 1, -2_147_483_647, 2_147_483_647)
+    x[:4] = [-2**31, 2**31 - 1, -7, -8]
+    with np.errstate(over="ignore"):
+        keep = np.fmod(x, np.int32(3)) != 0
+        y = x[keep] * x[keep] - np.int32(7) * x[keep]
+    got, fault = oracle.linq_where_select_i32(poly, x)
+    assert fault == -1 and np.array_equal(got, y)
+    # the checked running total: the first prefix outside int32, from an int64 cumulative sum
+    small = oracle.gen_uniform_i32(300_000, 61, 1, -1000, 1000)
+    with np.errstate(over="ignore"):
+        ys = (small[np.fmod(small, 3) != 0].astype(np.int64) ** 2) - 7 * small[np.fmod(small, 3) != 0]
+    cs = np.cumsum(ys)
+    total, k, ovf, fault = oracle.linq_where_select_sum_i32(poly, small)
+    assert (total, k, fault) == (int(cs[-1]), ys.size, -1)
+    assert ovf == bool((cs > 2**31 - 1).any() or (cs < -2**31).any()) and ovf
+
+
+def test_int_division_truncates_and_throws_like_csharp():
+    """C#: -8 / 7 == -1 and -8 % 7 == -1 (truncation, not floor); a zero divisor throws
+    DivideByZeroException and int.MinValue / -1, int.MinValue % -1 and Math.Abs(int.MinValue) throw
+    OverflowException (kind 1 and 2 of the fault code 4 * index + kind)."""
+    from dotcompute_amd.hip import ABS, DIV, LOAD, MAP, REM, RDIV, SRC_ELEM, SRC_IMM
+    div7 = _ichain([(LOAD, SRC_ELEM, 0), (DIV, SRC_IMM, 7), (MAP, SRC_IMM, 0)])
+    rem7 = _ichain([(LOAD, SRC_ELEM, 0), (REM, SRC_IMM, 7), (MAP, SRC_IMM, 0)])
+    v = np.array([-8, 8, -7, 6, -6, -2**31], np.int32)
+    assert oracle.linq_where_select_i32(div7, v)[0].tolist() == [-1, 1, -1, 0, 0, -306783378]
+    assert oracle.linq_where_select_i32(rem7, v)[0].tolist() == [-1, 1, 0, 6, -6, -2]
+    inv = _ichain([(LOAD, SRC_ELEM, 0), (RDIV, SRC_IMM, 100), (MAP, SRC_IMM, 0)])
+    out, fault = oracle.linq_where_select_i32(inv, np.array([3, 50, 0, 0, 1], np.int32))
+    assert out.tolist() == [33, 2] and fault == 4 * 2 + 1
+    for code in ([(LOAD, SRC_ELEM, 0), (DIV, SRC_IMM, -1), (MAP, SRC_IMM, 0)],
+                 [(LOAD, SRC_ELEM, 0), (REM, SRC_IMM, -1), (MAP, SRC_IMM, 0)],
+                 [(LOAD, SRC_ELEM, 0), (ABS, SRC_IMM, 0), (MAP, SRC_IMM, 0)]):
+        out, fault = oracle.linq_where_select_i32(_ichain(code), np.array([5, -5, -2**31, 9], np.int32))
+        assert fault == 4 * 2 + 2 and out.size == 2
+    # a planted mistake: a floor-division restatement would be caught by the known answers above
+    assert (-8) // 7 == -2 and int(np.fmod(np.int32(-8), np.int32(7))) == -1
+
+
 def test_planted_mistake_is_caught():
     """The bit comparison the GPU tests use must reject an off-by-one-ulp or reordered result."""
     a = oracle.gen_uniform_f32(10_000, 3, 0)
