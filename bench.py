@@ -96,7 +96,8 @@ def main() -> int:
     ap.add_argument("--skip-extras", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only", default="",
-                    help="comma list of extras to run (sum,linq_sum,linq_minmax,vector_add,gemm,spmv,cache,orchestrator)")
+                    help="comma list of extras to run (sum,linq_sum,linq_minmax,vector_add,gemm,spmv,cache,misaligned,"
+                         "linq_i32,orchestrator)")
     ap.add_argument("--vendor", action="store_true",
                     help="also time the same operations composed from torch's ops (hipBLASLt for MatMul), as "
                          "`vendor` beside the headline and the GEMM / Sum / VectorAdd legs (imports torch in a "
@@ -282,6 +283,51 @@ def main() -> int:
     achieved = step_bytes / (ms_kernel * 1e-3) / 1e9
     log(f"[bench] where_select 256M: kept={kept} kernel={ms_kernel*1e3:.1f} us wall/step={ms_per_step*1e3:.1f} us "
         f"-> {achieved:.0f} GB/s")
+
+    # ---------------- the same chain on an input that starts one float past a 16-byte boundary:
+    # the round-robin grid peels the 3 head elements; reported beside the aligned headline
+    if want("misaligned"):
+        xv = hip.DeviceArray(ctx, x.ptr + 4, 4 * (n - 1), np.dtype(np.float32), (n - 1,))
+        g = lambda: ctx.where_select_f32(chain, xv, out, cnt, n - 1)
+        g(); ctx.synchronize()
+        ms_off = time_launches(ctx, g, 50, warm_ms=LEG_WARM_MS)
+        nb = 4 * (n - 1) + 4 * int(cnt.to_host()[0])
+        gbs = nb / (ms_off * 1e-3) / 1e9
+        extra["where_select_to_array_f32_256M_offset1"] = {
+            "ms": round(ms_off, 4), "GB/s": round(gbs, 1),
+            "strategy": "rounds" if ctx.to_array_strategy(xv, n - 1) == hip.STRATEGY_ROUNDS else "lookback",
+            "time_vs_aligned": round(ms_off / ms_kernel, 4), "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
+        log(f"[bench] where_select 256M, start 1 float past a 16-byte boundary: {ms_off*1e3:.1f} us "
+            f"({100 * (ms_off / ms_kernel - 1):+.1f}% against aligned)")
+    # ---------------- int32 sources: Where(x % 2 == 0).Select(x * x) over 256M ints in [-1000, 1000]
+    if want("linq_i32"):
+        xi = ctx.empty(n, np.int32)
+        ctx.fill_uniform_i32(xi, seed=43, stream=1)
+        oi = hip.DeviceArray(ctx, out.ptr, 4 * n, np.dtype(np.int32), (n,))
+        ich = hip.LinqChain.assemble([(hip.LOAD, hip.SRC_ELEM, 0), (hip.REM, hip.SRC_IMM, 2), (hip.CMP_EQ, hip.SRC_IMM, 0),
+                                      (hip.FILTER, 0, 0), (hip.LOAD, hip.SRC_ELEM, 0), (hip.MUL, hip.SRC_ELEM, 0),
+                                      (hip.MAP, 0, 0)], int32=True)
+        g = lambda: ctx.where_select_i32(ich, xi, oi, cnt, None, n)
+        g(); ctx.synchronize()
+        ms_i = time_launches(ctx, g, 20, warm_ms=LEG_WARM_MS)
+        ki = int(cnt.to_host()[0])
+        gbs = (4 * n + 4 * ki) / (ms_i * 1e-3) / 1e9
+        extra["where_select_to_array_i32_256M"] = {"ms": round(ms_i, 4), "GB/s": round(gbs, 1), "kept": ki,
+                                                   "workload": "Where(x % 2 == 0).Select(x * x), int32 [-1000, 1000]",
+                                                   "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
+        log(f"[bench] where_select_i32 256M: {ms_i*1e3:.1f} us -> {gbs:.0f} GB/s")
+        si, ci, ovi = ctx.empty(1, np.int64), ctx.empty(1, np.int64), ctx.empty(1, np.int32)
+        g = lambda: ctx.where_select_sum_i32(ich, xi, si, ci, ovi, None, n)
+        g(); ctx.synchronize()
+        ms_s = time_launches(ctx, g, 20, warm_ms=LEG_WARM_MS)
+        gbs = 4 * n / (ms_s * 1e-3) / 1e9
+        extra["where_select_sum_i32_256M"] = {"ms": round(ms_s, 4), "GB/s": round(gbs, 1),
+                                              "overflowed": bool(ovi.to_host()[0]),
+                                              "workload": "Where(x % 2 == 0).Select(x * x).Sum(), checked int32",
+                                              "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
+        log(f"[bench] where_select_sum_i32 256M: {ms_s*1e3:.1f} us -> {gbs:.0f} GB/s")
+        for a_ in (xi, si, ci, ovi):
+            ctx.free(a_)
 
     # ---------------- what the same memory can do in this run: the ceilings beside the peak -----
     # a 1 GiB device-to-device copy through hipMemcpyAsync (read 1 GiB + write 1 GiB), and the

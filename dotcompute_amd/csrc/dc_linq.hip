@@ -30,6 +30,7 @@
 
 #include "dc_device.hpp"
 #include "dc_internal.hpp"
+#include "dc_intdiv.hpp"
 
 namespace {
 
@@ -41,6 +42,15 @@ constexpr int kTile = kBlock * kElemPerThread;     // 16384 elements = 64 KiB of
 constexpr int kChunk = 16;                         // elements interpreted per program pass
 constexpr int kLookbackPerLane = 4;                // status words read per lane per lookback round
 constexpr int kSumBlocksMax = 1024;
+
+// Calls f(std::integral_constant<int, U>) for U = 0, 1, ... in order: a compile-time unrolled loop, so
+// the index into an array of register buffers is a constant whatever the size of the body (a
+// `#pragma unroll` loop stays a loop when its unrolled body exceeds the compiler's size limit, and
+// its register arrays then go to scratch memory).
+template <typename F, int... U>
+__device__ __attribute__((always_inline)) inline void for_each_index(F&& f, std::integer_sequence<int, U...>) {
+  (f(std::integral_constant<int, U>{}), ...);
+}
 
 // ---- interpreter -------------------------------------------------------------------------------
 
@@ -127,8 +137,12 @@ __device__ __attribute__((always_inline)) inline uint32_t run_program(const dc_l
   for (int j = 0; j < (SAVES ? EPT : 1); ++j) { s0[j] = T(0); s1[j] = T(0); }
   uint32_t p = 0, q = 0, keep = live;
   const int n = prog.n_instr;
+  // The next instruction's scalar load is issued before the current one runs, so its latency
+  // overlaps the work of the current instruction instead of stalling the dispatch.
+  Instr next = fetch_instr(prog, 0);
   for (int pc = 0; pc < n; ++pc) {
-    const Instr ins = fetch_instr(prog, pc);
+    const Instr ins = next;
+    next = fetch_instr(prog, min(pc + 1, DC_LINQ_MAX_INSTR - 1));
     uint32_t c = 0;
     bool is_cmp = false;
 // Applies `body` (which reads the operand as O) to every element, for the instruction's source.
@@ -164,16 +178,36 @@ __device__ __attribute__((always_inline)) inline uint32_t run_program(const dc_l
         else DC_LQ_APPLY(v[j] = v[j] * O);
         break;
       case DC_LQ_DIV:
-        if constexpr (kInt) DC_LQ_APPLY(v[j] = checked_div(v[j], O, j, keep, f));
-        else DC_LQ_APPLY(v[j] = v[j] / O);
+        if constexpr (kInt) {
+          const int32_t d = (int32_t)ins.imm;
+          if (ins.src == DC_LQ_SRC_IMM && d != 0 && d != -1 && d != 1) {  // never throws
+            const dc::DivMagic g = dc::div_magic(d);
+#pragma unroll
+            for (int j = 0; j < EPT; ++j) v[j] = dc::div_by_magic(v[j], g);
+          } else {
+            DC_LQ_APPLY(v[j] = checked_div(v[j], O, j, keep, f));
+          }
+        } else {
+          DC_LQ_APPLY(v[j] = v[j] / O);
+        }
         break;
       case DC_LQ_RDIV:
         if constexpr (kInt) DC_LQ_APPLY(v[j] = checked_div(O, v[j], j, keep, f));
         else DC_LQ_APPLY(v[j] = O / v[j]);
         break;
       case DC_LQ_REM:
-        if constexpr (kInt) DC_LQ_APPLY(v[j] = checked_rem(v[j], O, j, keep, f));
-        else DC_LQ_APPLY(v[j] = net_rem(v[j], O));
+        if constexpr (kInt) {
+          const int32_t d = (int32_t)ins.imm;
+          if (ins.src == DC_LQ_SRC_IMM && d != 0 && d != -1 && d != 1) {  // never throws
+            const dc::DivMagic g = dc::div_magic(d);
+#pragma unroll
+            for (int j = 0; j < EPT; ++j) v[j] = wrap_sub(v[j], wrap_mul(dc::div_by_magic(v[j], g), d));
+          } else {
+            DC_LQ_APPLY(v[j] = checked_rem(v[j], O, j, keep, f));
+          }
+        } else {
+          DC_LQ_APPLY(v[j] = net_rem(v[j], O));
+        }
         break;
       case DC_LQ_RREM:
         if constexpr (kInt) DC_LQ_APPLY(v[j] = checked_rem(O, v[j], j, keep, f));
@@ -608,11 +642,34 @@ __device__ __attribute__((always_inline)) inline void apply_reduce_flags(const d
 // apply_reduce_flags for every mode, the int32 ones included: elements outside `live` are not kept
 // (int32 modes; the float modes are only called on present elements), and the exceptions of an
 // int32 program go to `f`.
-template <int RD, int EPT>
+// The interpreters run over at most CHUNK elements at a time. The round-robin kernel passes 8:
+// with 16, the interpreters' registers (values, save registers, operands) on top of its look-ahead
+// buffers spill to scratch.
+template <int RD, int EPT, int CHUNK = EPT>
 __device__ __attribute__((always_inline)) inline void eval_flags(const dc_linq_chain& prog, const AffineChain& aff,
                                                                  const RdConst& k, float (&e)[EPT], bool (&kept)[EPT],
                                                                  uint32_t live, Faults& f) {
-  if constexpr (rd_is_int(RD)) {
+  constexpr bool kInterp = rd_is_int(RD) || RD == kRdInterp || RD == kRdInterpSaves;
+  constexpr int kInterpChunk = CHUNK;
+  if constexpr (kInterp && EPT > kInterpChunk) {
+    static_assert(EPT % kInterpChunk == 0, "whole chunks");
+    for_each_index([&](auto C) __attribute__((always_inline)) {
+      constexpr int c = decltype(C)::value;
+      float sub[kInterpChunk];
+      bool ks[kInterpChunk];
+#pragma unroll
+      for (int i = 0; i < kInterpChunk; ++i) sub[i] = e[c * kInterpChunk + i];
+      Faults fc;
+      eval_flags<RD, kInterpChunk>(prog, aff, k, sub, ks, (live >> (c * kInterpChunk)) & ((1u << kInterpChunk) - 1u), fc);
+#pragma unroll
+      for (int i = 0; i < kInterpChunk; ++i) {
+        e[c * kInterpChunk + i] = sub[i];
+        kept[c * kInterpChunk + i] = ks[i];
+      }
+      f.hit |= fc.hit << (c * kInterpChunk);
+      f.ovf |= fc.ovf << (c * kInterpChunk);
+    }, std::make_integer_sequence<int, EPT / kInterpChunk>{});
+  } else if constexpr (rd_is_int(RD)) {
     const uint32_t keep = run_program_i32<EPT, RD == kRdInterpI32Saves>(prog, e, live, f);
 #pragma unroll
     for (int j = 0; j < EPT; ++j) kept[j] = ((keep >> j) & 1u) != 0u;
@@ -675,20 +732,21 @@ __device__ inline uint64_t apply_program(const dc_linq_chain& prog, const Affine
   if constexpr (MODE == kModeAffine) {
     return run_affine<kElemPerThread>(aff, e) & valid;
   } else if constexpr (mode_is_int(MODE)) {
+    constexpr int C = kChunk;
     uint64_t keep = 0, hit = 0, ovf = 0;
+    for_each_index([&](auto CI) __attribute__((always_inline)) {
+      constexpr int c = decltype(CI)::value;
+      float sub[C];
 #pragma unroll
-    for (int c = 0; c < kElemPerThread / kChunk; ++c) {
-      float sub[kChunk];
-#pragma unroll
-      for (int i = 0; i < kChunk; ++i) sub[i] = e[c * kChunk + i];
+      for (int i = 0; i < C; ++i) sub[i] = e[c * C + i];
       Faults f;
-      const uint32_t live = (uint32_t)(valid >> (c * kChunk)) & ((1u << kChunk) - 1u);
-      keep |= (uint64_t)run_program_i32<kChunk, MODE == kModeInterpI32Saves>(prog, sub, live, f) << (c * kChunk);
-      hit |= (uint64_t)f.hit << (c * kChunk);
-      ovf |= (uint64_t)f.ovf << (c * kChunk);
+      const uint32_t live = (uint32_t)(valid >> (c * C)) & ((1u << C) - 1u);
+      keep |= (uint64_t)run_program_i32<C, MODE == kModeInterpI32Saves>(prog, sub, live, f) << (c * C);
+      hit |= (uint64_t)f.hit << (c * C);
+      ovf |= (uint64_t)f.ovf << (c * C);
 #pragma unroll
-      for (int i = 0; i < kChunk; ++i) e[c * kChunk + i] = sub[i];
-    }
+      for (int i = 0; i < C; ++i) e[c * C + i] = sub[i];
+    }, std::make_integer_sequence<int, kElemPerThread / C>{});
     *fhit = hit;
     *fovf = ovf;
     return keep;
@@ -864,12 +922,6 @@ constexpr int kRrMinRounds = 4;                          // below this the ticke
 static_assert((kRrDelay + 1) * kRrChunk <= kRrRing, "the ring holds every staged tile at 100% selectivity");
 static_assert(kRrDelay < 8 && kRrDelay >= 2, "per-tile LDS tables are indexed modulo 8");
 
-// Calls f(std::integral_constant<int, U>) for U = 0, 1, ... in order: a compile-time unrolled loop, so
-// the index into an array of register buffers is a constant.
-template <typename F, int... U>
-__device__ __attribute__((always_inline)) inline void for_each_index(F&& f, std::integer_sequence<int, U...>) {
-  (f(std::integral_constant<int, U>{}), ...);
-}
 
 // Count words of `round` for workgroups q*64 + lane (q < 4): four coalesced 256-byte loads.
 __device__ inline void rr_issue_counts(uint32_t (&c)[kRrCountsPerLane], const uint32_t* __restrict__ counts,
@@ -914,12 +966,16 @@ __device__ inline bool rr_resolve(uint32_t (&c)[kRrCountsPerLane], const uint32_
   return true;
 }
 
+// `head_in` holds the head_n (0..3) elements of a 4-byte aligned input that come before its first
+// 16-byte boundary; `in` (16-byte aligned) holds the n elements after them. Every control wave
+// evaluates the head itself (its kept count is the output offset of round 0) and workgroup 0 writes
+// its kept elements first.
 template <int RD>
 __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
     const dc_linq_chain prog, const AffineChain aff, const RdConst canon, const float* __restrict__ in, int64_t n,
     float* __restrict__ out,
     int64_t* __restrict__ count_out, uint32_t* __restrict__ counts, uint32_t epoch16, uint32_t P,
-    uint32_t* __restrict__ done, uint64_t* __restrict__ fault) {
+    uint32_t* __restrict__ done, uint64_t* __restrict__ fault, const float* __restrict__ head_in, int head_n) {
   __shared__ float s_ring[kRrWorkers][kRrRing + dc::kWave];  // + a discard slot per lane
   // ring positions stay in [0, kRrRing); a position below 2 * kRrRing wraps with one unsigned min
   auto wrap = [](uint32_t q) __attribute__((always_inline)) {
@@ -939,13 +995,15 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
     if constexpr (kLazyMap) {
 #pragma unroll
       for (int j = 0; j < kRrEpt; ++j) kept[j] = rd_compare<rd_cmp(RD)>(e[j], canon.t);
-    } else if constexpr (rd_is_int(RD)) {
+    } else if constexpr (rd_is_int(RD) || RD == kRdInterp || RD == kRdInterpSaves) {
       Faults f;
-      eval_flags<RD, kRrEpt>(prog, aff, canon, e, kept, live, f);
-      const int b = __builtin_ctz(f.hit | 0x80000000u);
-      const uint64_t code = (uint64_t)(first + (b >> 2) * (4 * dc::kWave) + (b & 3)) * 4u +
-                            (((f.ovf >> b) & 1u) ? DC_LINQ_FAULT_OVERFLOW : DC_LINQ_FAULT_DIVIDE_BY_ZERO);
-      lane_fault = max(lane_fault, f.hit ? ~code : (uint64_t)0);
+      eval_flags<RD, kRrEpt, kRrEpt / 2>(prog, aff, canon, e, kept, live, f);
+      if constexpr (rd_is_int(RD)) {
+        const int b = __builtin_ctz(f.hit | 0x80000000u);
+        const uint64_t code = (uint64_t)(head_n + first + (b >> 2) * (4 * dc::kWave) + (b & 3)) * 4u +
+                              (((f.ovf >> b) & 1u) ? DC_LINQ_FAULT_OVERFLOW : DC_LINQ_FAULT_DIVIDE_BY_ZERO);
+        lane_fault = max(lane_fault, f.hit ? ~code : (uint64_t)0);
+      }
     } else {
       apply_reduce_flags<RD, kRrEpt>(prog, aff, canon, e, kept);
     }
@@ -969,6 +1027,19 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
   if (wave == kRrWorkers) {
     // ---------------- control wave (the youngest wave: see the roles above)
     int64_t base = 0;
+    if (head_n > 0) {  // the peeled head: lane l evaluates element l
+      const bool present = lane < head_n;
+      float e[1] = {present ? head_in[lane] : 0.0f};
+      bool kept[1];
+      Faults f;
+      eval_flags<RD, 1>(prog, aff, canon, e, kept, present ? 1u : 0u, f);
+      const bool k = kept[0] && present;
+      const uint64_t b = __ballot(k);
+      if (w == 0 && k)
+        out[__builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u))] = e[0];
+      if (rd_is_int(RD) && f.hit) publish_fault(fault, lane, (f.ovf & 1u) != 0u);
+      base = __builtin_popcountll(b);
+    }
     uint32_t c[kRrCountsPerLane];
     bool ok = true;
     for (uint32_t r = 0; r < rounds; ++r) {
@@ -1189,8 +1260,8 @@ __device__ __attribute__((always_inline)) inline int64_t visit_chunk(const dc_li
     dc::f32x4 v[kRdUnroll];
 #pragma unroll
     for (int u = 0; u < kRdUnroll; ++u) v[u] = dc::load_stream(xa + i + u * kSumBlock);
-#pragma unroll
-    for (int g = 0; g < kRdUnroll / 4; ++g) {
+    for_each_index([&](auto G) __attribute__((always_inline)) {
+      constexpr int g = decltype(G)::value;
       float e[16];
       bool kept[16];
 #pragma unroll
@@ -1207,7 +1278,7 @@ __device__ __attribute__((always_inline)) inline int64_t visit_chunk(const dc_li
 #pragma unroll
       for (int j = 0; j < 16; ++j) wave_cnt += (uint64_t)__builtin_popcountll(__ballot(kept[j]));
       half(e, kept, base);
-    }
+    }, std::make_integer_sequence<int, kRdUnroll / 4>{});
   }
   if ((threadIdx.x & (dc::kWave - 1)) == 0) cnt += (int64_t)wave_cnt;
   for (; i < v1; i += kSumBlock) {
@@ -1845,12 +1916,21 @@ std::vector<int> all_reduce_modes() {
 
 uint32_t rounds_groups(const dc_hip_ctx* ctx) { return (uint32_t)std::min(ctx->cu_count, kRrMaxGroups); }
 
-// The round-robin kernel needs a 16-byte aligned input of at least kRrMinRounds full rounds and
-// room for one workgroup per CU (every program variant; asked once per context). The
-// caller holds the context lock.
+// Elements before the first 16-byte boundary of a 4-byte aligned input (0..3, at most n), or -1
+// for an input that is not 4-byte aligned.
+int64_t head16(const float* input, int64_t n) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(input);
+  if (a & 3) return -1;
+  return std::min<int64_t>(n, (int64_t)(((16 - (a & 15)) & 15) >> 2));
+}
+
+// The round-robin kernel needs a 4-byte aligned input whose 16-byte aligned part (after the 0..3
+// head elements it peels) holds at least kRrMinRounds full rounds, and room for one workgroup per
+// CU (every program variant; asked once per context). The caller holds the context lock.
 bool use_rounds(dc_hip_ctx* ctx, const float* input, int64_t n) {
   const uint32_t groups = rounds_groups(ctx);
-  if (!dc::aligned16(input) || groups == 0 || n / kRrTile < (int64_t)kRrMinRounds * groups) return false;
+  const int64_t h = head16(input, n);
+  if (h < 0 || groups == 0 || (n - h) / kRrTile < (int64_t)kRrMinRounds * groups) return false;
   if (ctx->rounds_fit < 0) {
     bool fit = true;
     for (int mode : all_reduce_modes()) {
@@ -1876,21 +1956,24 @@ int32_t launch_to_array(dc_hip_ctx* ctx, const dc_linq_chain* chain, bool is_int
     AffineChain aff = plan.aff;
     RdConst canon = plan.k;
     const uint32_t groups = rounds_groups(ctx);
-    const int64_t tiles = (n + kRrTile - 1) / kRrTile;
+    const int head_n = (int)head16(input, n);  // 0..3: use_rounds accepted the input
+    const int64_t tiles = (n - head_n + kRrTile - 1) / kRrTile;
     const size_t words = (size_t)((tiles + groups - 1) / groups + 1) * groups;
     uint32_t epoch16 = 0;
     DC_RETURN_IF(dc::ensure_round_counts(ctx, words, &epoch16));
     dc_linq_chain prog = *chain;
-    const float* in_arg = input;
-    int64_t n_arg = n;
+    const float* in_arg = input + head_n;
+    int64_t n_arg = n - head_n;
+    const float* head_arg = input;
+    int head_arg_n = head_n;
     float* out_arg = output;
     int64_t* count_arg = count_out;
     uint32_t* counts_arg = ctx->round_counts;
     uint32_t groups_arg = groups;
     uint32_t* done_arg = ctx->counters + DC_SLOT_LINQ_DONE;
     uint64_t* fault_arg = fault_word;
-    void* args[] = {&prog,  &aff,       &canon,   &in_arg,   &n_arg,     &out_arg, &count_arg,
-                    &counts_arg, &epoch16, &groups_arg, &done_arg, &fault_arg};
+    void* args[] = {&prog,       &aff,     &canon,      &in_arg,   &n_arg,     &out_arg,  &count_arg,
+                    &counts_arg, &epoch16, &groups_arg, &done_arg, &fault_arg, &head_arg, &head_arg_n};
     // One workgroup per CU, each needing most of a CU's LDS, on an otherwise idle device: every
     // workgroup is resident at once (an ordinary launch; measured faster than a cooperative one).
     dc::ResidentLaunch resident(ctx);

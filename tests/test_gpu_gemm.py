@@ -154,6 +154,7 @@ def test_gemm_bf16_8192_sampled(ctx):
     br = oracle.bf16_to_f32(oracle.f32_to_bf16(b)).reshape(n, n)
     rows = np.unique(np.concatenate([[0, n - 1], np.random.default_rng(5).integers(0, n, 16)]))
     check_rows(c, ar, br, rows)
+    freivalds(c, ar, br)  # every entry, through C·r against A·(B·r) on the bf16-rounded inputs
 
 
 def test_convert_f32_to_bf16_bit_exact(ctx):

@@ -316,11 +316,36 @@ def test_round_robin_sizes_bit_exact(ctx, extra):
 def test_round_robin_threshold_and_alignment(ctx):
     n = rr_min_n()
     x = oracle.gen_uniform_f32(n + 3, 61, 0)
-    # one element short of four rounds, and a misaligned start: the lookback kernel, same result
+    # one element short of four rounds: the lookback kernel, same result
     got = run_to_array_checked(ctx, CHAIN, x[: n - 1], hip.STRATEGY_LOOKBACK)
     assert np.array_equal(bits(got), bits(oracle.where_gt0_select_2x_plus_1(x[: n - 1])))
-    got = run_to_array_checked(ctx, CHAIN, x, hip.STRATEGY_LOOKBACK, offset=1)
-    assert np.array_equal(bits(got), bits(oracle.where_gt0_select_2x_plus_1(x)))
+    # a start 1-3 floats past a 16-byte boundary: the round-robin grid peels the 3-1 head elements
+    # (the aligned part still holds four rounds), bit-exact; one element fewer: the lookback kernel
+    for offset in (1, 2, 3):
+        h = 4 - offset
+        got = run_to_array_checked(ctx, CHAIN, x, hip.STRATEGY_ROUNDS, offset=offset)
+        assert np.array_equal(bits(got), bits(oracle.where_gt0_select_2x_plus_1(x)))
+        short = x[: n + h - 1]
+        got = run_to_array_checked(ctx, CHAIN, short, hip.STRATEGY_LOOKBACK, offset=offset)
+        assert np.array_equal(bits(got), bits(oracle.where_gt0_select_2x_plus_1(short)))
+
+
+@pytest.mark.parametrize("offset", [1, 2, 3])
+@pytest.mark.parametrize("head", ["kept", "dropped", "mixed"])
+def test_round_robin_peeled_head_every_program_kind(ctx, offset, head):
+    # the head elements decide the offset of everything after them: kept, dropped or mixed heads,
+    # on the canonical, affine and interpreter variants
+    x = oracle.gen_uniform_f32(rr_min_n() + 5, 62 + offset, 0)
+    x[:3] = {"kept": [0.5, 0.25, 0.75], "dropped": [-0.5, -0.25, -0.75], "mixed": [-0.5, 0.25, -0.75]}[head]
+    progs = [CHAIN,
+             LinqChain.assemble([(LOAD, SRC_ELEM, 0), (MUL, SRC_IMM, 3.0), (ADD, SRC_IMM, -0.5), (MAP, SRC_IMM, 0),
+                                 (LOAD, SRC_ELEM, 0), (CMP_GT, SRC_IMM, 0.0), (FILTER, SRC_IMM, 0),
+                                 (LOAD, SRC_ELEM, 0), (MUL, SRC_IMM, 0.5), (MAP, SRC_IMM, 0)]),
+             LinqChain.assemble([(LOAD, SRC_ELEM, 0), (ABS, SRC_IMM, 0), (CMP_LT, SRC_IMM, 0.6), (FILTER, SRC_IMM, 0),
+                                 (LOAD, SRC_ELEM, 0), (SQRT, SRC_IMM, 0), (MAP, SRC_IMM, 0)])]
+    for prog in progs:
+        got = run_to_array_checked(ctx, prog, x, hip.STRATEGY_ROUNDS, offset=offset)
+        assert same_floats(got, oracle.linq_where_select(prog, x))
 
 
 @pytest.mark.parametrize("cmp,imm", [(CMP_GT, -2.0), (CMP_GT, 2.0), (CMP_LT, -0.999)])

@@ -128,6 +128,25 @@ def test_to_array_misaligned(ctx, offset):
     assert f == -1 and np.array_equal(got, ref)
 
 
+@pytest.mark.parametrize("offset", [1, 2, 3])
+def test_to_array_round_robin_misaligned(ctx, offset):
+    # large enough for the round-robin grid after the 3-1 peeled head elements, with faults in the
+    # head and in the body reported at their sequence index
+    n = 4 * min(hip.device_info(0).compute_units, 256) * 8192 + 7
+    x = oracle.gen_uniform_i32(n, 57, 1, -1000, 1000)
+    d, src = put(ctx, x, offset)
+    assert ctx.to_array_strategy(src, n) == hip.STRATEGY_ROUNDS
+    ctx.free(d)
+    got, k, f = run_to_array(ctx, POLY, x, offset)
+    ref, rf = oracle.linq_where_select_i32(POLY, x)
+    assert f == rf == -1 and k == ref.size and np.array_equal(got, ref)
+    for zero in (4 - offset - 1, n - 5):  # the last head element, then an element near the end
+        y = x.copy()
+        y[y == 0] = 1
+        y[zero] = 0
+        assert run_to_array(ctx, DIV_BY_X, y, offset)[2] == 4 * zero + hip.LINQ_FAULT_DIVIDE_BY_ZERO
+
+
 def test_to_array_256m_bit_exact(ctx):
     n = 256 * 1024 * 1024
     x = oracle.gen_uniform_i32(n, 48, 1, -1000, 1000)

@@ -295,6 +295,19 @@ def test_sum_256m_f32_and_i32(ctx):
     ctx.synchronize()
     xi = oracle.gen_uniform_i32(n, 43, 1)
     assert oi.to_host()[0] == oracle.sum_i32_exact(xi)
+    assert ovf.to_host()[0] == 0 and oracle.sum_i32_bcl(xi) == int(oracle.sum_i32_exact(xi))
+    # the BCL's lane rule at full size: elements 0, 8 and 16 (lane 0) push lane 0 past
+    # int.MaxValue and back, while the total stays small: OverflowException by the rule, not by the total
+    planted = {0: 1000, 8: 2**31 - 500, 16: -(2**31 - 500)}
+    for i, v in planted.items():
+        xi[i] = v
+        hip.check(hip.load().dc_hip_memcpy_h2d_async(ctx.handle, di.ptr + 4 * i, xi[i:i + 1].ctypes.data, 4), "h2d")
+    ctx.reduce_sum_i32(di, oi, ovf)
+    ctx.synchronize()
+    assert oi.to_host()[0] == oracle.sum_i32_exact(xi)
+    with pytest.raises(OverflowError):
+        oracle.sum_i32_bcl(xi)
+    assert ovf.to_host()[0] == 1
     for a in (out, di, oi, ovf):
         ctx.free(a)
 
