@@ -49,9 +49,11 @@ struct dc_hip_ctx {
   uint32_t round_epoch = 0;
   // Whether one 1024-thread workgroup of each round-robin kernel fits on a CU: -1 not yet asked.
   int rounds_fit = -1;
-  // Recorded on this context's stream when another context's resident grid must follow this one's
-  // (dc::ResidentLaunch).
-  hipEvent_t resident_done = nullptr;
+  // Recorded on this context's stream when another context's launch of the same kind must follow
+  // this one's (dc::ResidentLaunch): [kOrderResident] resident grids, [kOrderNoAlloc] the calls
+  // that share a device's static no-alloc scratch (that event is created with the context, since
+  // the no-alloc path creates nothing).
+  hipEvent_t order_done[2] = {nullptr, nullptr};
 
   // Device address of the static scratch array of dc_hip_linq_where_select_sum_f32_noalloc on this
   // context's device (resolved once per device at context creation), and the status of that lookup.
@@ -68,6 +70,8 @@ struct dc_hip_module {
   hipModule_t mod = nullptr;
   int device = 0;
 };
+
+#define DC_ORDER_KINDS 2
 
 // Counter slots inside ctx->counters.
 enum dc_counter_slot : int {
@@ -108,19 +112,22 @@ int32_t ensure_partials(dc_hip_ctx* ctx, size_t bytes);
 int32_t ensure_status(dc_hip_ctx* ctx, size_t words, uint32_t* epoch_out);
 // Grows ctx->round_counts to at least `words` and returns the 16-bit epoch for the next launch.
 int32_t ensure_round_counts(dc_hip_ctx* ctx, size_t words, uint32_t* epoch_out);
-// Resident grids (kernels whose workgroups wait for each other, launched with one workgroup per CU)
-// must not share the device with another resident grid: two such grids could each hold half of
-// the CUs while waiting for workgroups that cannot start. Every resident launch of this library
-// on a device is therefore ordered after the previous one, from any context of the process. A
-// ResidentLaunch holds the device's slot lock from construction to destruction, so resident
-// enqueues on a device never interleave; when the previous resident grid came from another
-// context, the constructor records an event on that context's stream (behind its grid) and makes
-// this context's stream wait for it. A context that follows itself records nothing. The caller
-// holds the context lock, enqueues the grid, then calls done(). (Other processes on the same
-// device are not covered; the kernels' waits are bounded and report a failure instead of hanging.)
+// Launches that must not overlap another launch of the same kind on a device, from any context of
+// the process. kOrderResident: resident grids (kernels whose workgroups wait for each other,
+// launched with one workgroup per CU): two such grids could each hold half of the CUs while
+// waiting for workgroups that cannot start. kOrderNoAlloc: the allocation-free LINQ Sum, whose
+// partials live in one static array per device. A ResidentLaunch holds the device's slot lock of
+// its kind from construction to destruction, so those enqueues on a device never interleave; when
+// the previous launch of the kind came from another context, the constructor records an event on
+// that context's stream (behind its launch) and makes this context's stream wait for it. A context
+// that follows itself records nothing. The caller holds the context lock, enqueues the launch,
+// then calls done(). (Other processes on the same device are not covered; the resident kernels'
+// waits are bounded and report a failure instead of hanging.)
+constexpr int kOrderResident = 0;
+constexpr int kOrderNoAlloc = 1;
 class ResidentLaunch {
  public:
-  explicit ResidentLaunch(dc_hip_ctx* ctx);
+  explicit ResidentLaunch(dc_hip_ctx* ctx, int kind = kOrderResident);
   ~ResidentLaunch();
   ResidentLaunch(const ResidentLaunch&) = delete;
   ResidentLaunch& operator=(const ResidentLaunch&) = delete;
@@ -129,10 +136,11 @@ class ResidentLaunch {
 
  private:
   dc_hip_ctx* ctx_;
+  int kind_;
   std::mutex* mu_ = nullptr;
   int32_t status_ = 0;
 };
-// Forgets the context's event (context destruction).
+// Forgets the context's order events (context destruction).
 void resident_forget(dc_hip_ctx* ctx);
 // Looks up the device address of the no-alloc LINQ Sum's static scratch for ctx->device (the
 // device must be current) and stores it in ctx->noalloc_scratch. Calls no allocator.

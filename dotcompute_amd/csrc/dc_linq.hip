@@ -1660,8 +1660,9 @@ __global__ __launch_bounds__(kFinalBlock) void where_select_minmax_i32_pass2(con
 
 // Scratch of dc_hip_linq_where_select_sum_f32_noalloc: one launch's per-workgroup partials (a
 // float64 sum and an int64 count per workgroup, at most kSumBlocksMax workgroups), 16 KiB. One copy
-// per GPU, held until the process ends; every call on a GPU uses it, so calls that overlap on one
-// GPU race. Pass 1 writes every entry pass 2 reads, so nothing needs clearing between calls.
+// per GPU, held until the process ends; every call on a GPU uses it, and the calls of this process
+// on one GPU are ordered one after another (dc::ResidentLaunch, kind kOrderNoAlloc). Pass 1 writes
+// every entry pass 2 reads, so nothing needs clearing between calls.
 constexpr size_t kNoAllocScratchBytes = (size_t)kSumBlocksMax * (sizeof(double) + sizeof(int64_t));
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
@@ -2158,7 +2159,13 @@ DC_HIP_API int32_t dc_hip_linq_where_select_sum_f32_noalloc(dc_hip_ctx* ctx, con
   if ((size_t)grid * 16 > kNoAllocScratchBytes) return DC_ERR_OUT_OF_MEMORY;
   double* psum = static_cast<double*>(ctx->noalloc_scratch);  // never `scratch` itself: a host stand-in
   int64_t* pcnt = reinterpret_cast<int64_t*>(psum + grid);
-  return launch_where_select_sum(ctx, chain, input, n, grid, psum, pcnt, sum_out, count_out);
+  // Calls from different contexts on one device share the array: each is ordered behind the
+  // previous one (an event recorded on that context's stream; nothing is allocated).
+  dc::ResidentLaunch order(ctx, dc::kOrderNoAlloc);
+  DC_RETURN_IF(order.status());
+  DC_RETURN_IF(launch_where_select_sum(ctx, chain, input, n, grid, psum, pcnt, sum_out, count_out));
+  order.done();
+  return DC_OK;
 }
 
 DC_HIP_API int32_t dc_hip_linq_where_select_minmax_f32(dc_hip_ctx* ctx, const dc_linq_chain* chain,

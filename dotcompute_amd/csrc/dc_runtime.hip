@@ -174,27 +174,29 @@ int32_t ensure_round_counts(dc_hip_ctx* ctx, size_t words, uint32_t* epoch_out) 
 }
 
 namespace {
-struct ResidentSlot {
+struct OrderSlot {
   std::mutex mu;
-  dc_hip_ctx* last_ctx = nullptr;  // context whose resident_done event marks the last resident grid
+  dc_hip_ctx* last_ctx = nullptr;  // context whose order event marks the last launch of this kind
 };
-ResidentSlot g_resident[64];
+OrderSlot g_order[DC_ORDER_KINDS][64];
 }  // namespace
 
-ResidentLaunch::ResidentLaunch(dc_hip_ctx* ctx) : ctx_(ctx) {
-  if (ctx->device < 0 || ctx->device >= 64) {
+ResidentLaunch::ResidentLaunch(dc_hip_ctx* ctx, int kind) : ctx_(ctx), kind_(kind) {
+  if (ctx->device < 0 || ctx->device >= 64 || kind < 0 || kind >= DC_ORDER_KINDS) {
     status_ = DC_ERR_UNSUPPORTED;
     return;
   }
-  ResidentSlot& slot = g_resident[ctx->device];
+  OrderSlot& slot = g_order[kind][ctx->device];
   slot.mu.lock();
   mu_ = &slot.mu;
   dc_hip_ctx* prev = slot.last_ctx;
   if (!prev || prev == ctx) return;
   hipError_t e = hipSuccess;
-  if (!prev->resident_done) e = hipEventCreateWithFlags(&prev->resident_done, hipEventDisableTiming);
-  if (e == hipSuccess) e = hipEventRecord(prev->resident_done, prev->stream);
-  if (e == hipSuccess) e = hipStreamWaitEvent(ctx->stream, prev->resident_done, 0);
+  hipEvent_t& ev = prev->order_done[kind];
+  // The no-alloc kind's events exist from context creation (that path creates nothing).
+  if (!ev) e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventRecord(ev, prev->stream);
+  if (e == hipSuccess) e = hipStreamWaitEvent(ctx->stream, ev, 0);
   status_ = (int32_t)e;
 }
 
@@ -203,16 +205,18 @@ ResidentLaunch::~ResidentLaunch() {
 }
 
 void ResidentLaunch::done() {
-  if (mu_) g_resident[ctx_->device].last_ctx = ctx_;
+  if (mu_) g_order[kind_][ctx_->device].last_ctx = ctx_;
 }
 
 void resident_forget(dc_hip_ctx* ctx) {
   if (ctx->device < 0 || ctx->device >= 64) return;
-  ResidentSlot& slot = g_resident[ctx->device];
-  std::lock_guard<std::mutex> lock(slot.mu);
-  if (slot.last_ctx == ctx) slot.last_ctx = nullptr;
-  if (ctx->resident_done) (void)hipEventDestroy(ctx->resident_done);
-  ctx->resident_done = nullptr;
+  for (int kind = 0; kind < DC_ORDER_KINDS; ++kind) {
+    OrderSlot& slot = g_order[kind][ctx->device];
+    std::lock_guard<std::mutex> lock(slot.mu);
+    if (slot.last_ctx == ctx) slot.last_ctx = nullptr;
+    if (ctx->order_done[kind]) (void)hipEventDestroy(ctx->order_done[kind]);
+    ctx->order_done[kind] = nullptr;
+  }
 }
 
 }  // namespace dc
@@ -325,6 +329,8 @@ DC_HIP_API int32_t dc_hip_ctx_create(int32_t device, dc_hip_ctx** out) {
   // Set-up of the allocation-free entry point (device current): its status is kept and returned by
   // that entry point, so a failed lookup does not stop the context from serving everything else.
   ctx->noalloc_status = dc::linq_noalloc_setup(ctx);
+  if (ctx->noalloc_status == DC_OK)  // the event that orders no-alloc calls across contexts
+    ctx->noalloc_status = (int32_t)hipEventCreateWithFlags(&ctx->order_done[dc::kOrderNoAlloc], hipEventDisableTiming);
   *out = ctx;
   return DC_OK;
 }

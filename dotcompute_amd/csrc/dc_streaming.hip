@@ -362,8 +362,9 @@ __global__ __launch_bounds__(kFinalBlock) void reduce_partials(const Acc* __rest
   if (threadIdx.x == 0) *out = total;
 }
 
-// Grid for a reduction over n elements: a fixed function of n (not of the device), so results
-// are reproducible across runs and devices.
+// Grid for a reduction over n elements: a fixed function of n and of the device's CU count, so
+// results are reproducible run to run on one device (and on devices with the same CU count); the
+// partial order, and with it the last bits of a float64 sum, can differ between CU counts.
 unsigned reduce_grid(const dc_hip_ctx* ctx, int64_t n) {
   const int64_t per_block = (int64_t)kRedBlock * 4 * kRedUnroll;  // elements per block-iteration
   const int64_t g = (n + per_block - 1) / per_block;

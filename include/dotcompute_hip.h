@@ -353,7 +353,9 @@ DC_HIP_API int32_t dc_hip_linq_where_select_sum_f32(dc_hip_ctx* ctx, const dc_li
  * No counterpart in the reference. Same kernels, same results bit for bit; the per-workgroup partials
  * live in a 16 KiB static device array (one per GPU, resolved at context creation) instead of
  * context scratch that grows on demand. Every n fits (the grid is capped at 1024 workgroups).
- * Calls that overlap on one GPU, from any context, share that array and race: serialise them. */
+ * All calls of this process on one GPU share that array (another process loads its own copy): the
+ * library orders them one after another, a call from another context waiting, on its stream, for
+ * the previous call's stream position. */
 DC_HIP_API int32_t dc_hip_linq_where_select_sum_f32_noalloc(dc_hip_ctx* ctx, const dc_linq_chain* chain,
                                                             const float* input, int64_t n,
                                                             double* sum_out, int64_t* count_out);

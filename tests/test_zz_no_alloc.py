@@ -62,3 +62,36 @@ def test_noalloc_sum_general_chain_and_errors(ctx):
         == hip.DC_ERR_INVALID_ARGUMENT
     ctx.free(s)
     ctx.free(dx)
+
+
+def test_noalloc_calls_from_two_contexts_do_not_race(ctx):
+    """Two contexts on one GPU share the static partials: calls enqueued back to back from both,
+    without synchronising in between, each return their own input's sum (the library orders each
+    call behind the other context's previous one)."""
+    chain = hip.where_gt0_select_2x_plus_1()
+    other = hip.Context(0)
+    try:
+        xa = oracle.gen_uniform_f32(8_000_003, 48, 0)
+        xb = oracle.gen_uniform_f32(6_000_001, 49, 0)
+        da, db = ctx.to_device(xa), other.to_device(xb)
+        ref_a = run(ctx, "dc_hip_linq_where_select_sum_f32", chain, da, xa.size)
+        ref_b = run(other, "dc_hip_linq_where_select_sum_f32", chain, db, xb.size)
+        outs = []
+        L = hip.load()
+        for it in range(6):
+            for c, d, n in ((ctx, da, xa.size), (other, db, xb.size)):
+                s, k = c.empty(1, np.float64), c.empty(1, np.int64)
+                hip.check(L.dc_hip_linq_where_select_sum_f32_noalloc(c.handle, C.byref(chain), d.ptr, n, s.ptr, k.ptr),
+                          "noalloc")
+                outs.append((c, s, k))
+        ctx.synchronize()
+        other.synchronize()
+        for i, (c, s, k) in enumerate(outs):
+            want = ref_a if i % 2 == 0 else ref_b
+            assert (float(s.to_host()[0]), int(k.to_host()[0])) == want, i
+            c.free(s)
+            c.free(k)
+        ctx.free(da)
+        other.free(db)
+    finally:
+        other.close()
