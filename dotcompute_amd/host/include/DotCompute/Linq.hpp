@@ -50,7 +50,9 @@ class Expr {
   Expr(double constant);   // implicit: taken as the float literal it is rounded to
   Expr(int32_t constant);  // implicit: an int literal (2)
   explicit Expr(std::shared_ptr<const ExprNode> n) : node_(std::move(n)) {}
-  static Expr Parameter();
+  // Lambda parameter `index`: 0 is the element (x => ...); Aggregate's (acc, x) => ... names the
+  // accumulator 0 and the element 1.
+  static Expr Parameter(int index = 0);
   const ExprNode& Node() const { return *node_; }
   std::shared_ptr<const ExprNode> Ptr() const { return node_; }
   bool IsPredicate() const;  // comparison or logical node
@@ -60,7 +62,7 @@ class Expr {
   std::shared_ptr<const ExprNode> node_;
 };
 
-inline Expr Param() { return Expr::Parameter(); }
+inline Expr Param(int index = 0) { return Expr::Parameter(index); }
 Expr operator+(const Expr& a, const Expr& b);
 Expr operator-(const Expr& a, const Expr& b);
 Expr operator*(const Expr& a, const Expr& b);
@@ -96,6 +98,8 @@ Expr Max(const Expr& a, const Expr& b);
 struct MethodCall {
   std::string Method;          // "Where", "Select", "Sum", "Count", "OrderBy", ...
   std::optional<Expr> Lambda;  // absent for parameterless operators (Sum(), Count())
+  std::optional<int64_t> Count = std::nullopt;  // Take(n) / Skip(n)
+  std::optional<Expr> Seed = std::nullopt;      // Aggregate(seed, func)
 };
 
 // ---- operation graph ------------------------------------------------------------------------------
@@ -143,7 +147,14 @@ class BackendSelector {
 };
 
 // ---- fusion planner / HIP kernel generator -------------------------------------------------------
-enum class Terminal { ToArray, Sum, Count, LongCount, Average, Min, Max };
+enum class Terminal {
+  ToArray, Sum, Count, LongCount, Average, Min, Max,
+  First, FirstOrDefault, Last, LastOrDefault, Single, SingleOrDefault, Aggregate
+};
+
+// Aggregate folds the HIP kernels run exactly: int (acc, x) => acc + x (unchecked, so the fold is
+// the exact total wrapped to 32 bits, whatever the order) and Math.Min / Math.Max over int.
+enum class AggregateKind { None, Add, Min, Max };
 
 struct FusedKernelPlan {
   dc_linq_chain Program{};                // one fused program for all Filter/Map stages
@@ -151,6 +162,8 @@ struct FusedKernelPlan {
   ElementType Element = ElementType::Float32;  // the chain's element type (float32 or int32 kernels)
   bool BareSource = true;                 // no Where/Select: the terminal runs on the source array itself
   bool CanFault = false;                  // an int32 program that can throw (DivideByZero / Overflow)
+  AggregateKind Fold = AggregateKind::None;  // Terminal::Aggregate
+  std::optional<int32_t> Seed;            // Aggregate(seed, func) over int
   std::vector<std::string> FusedOperationIds;
   std::string Listing() const;            // human-readable program
 };
@@ -174,7 +187,7 @@ class HipKernelGenerator {
 // ---- execution -------------------------------------------------------------------------------------
 template <typename T>
 struct QueryResult {
-  std::vector<T> Values;      // ToArray
+  std::vector<T> Values;      // ToArray; First / Last / Single: the element, when Count > 0
   double Sum = 0.0;           // float sources: Sum / Average (float64 accumulator)
   int64_t IntSum = 0;         // int32 sources: the exact total
   bool SumOverflowed = false; // int32 sources: the checked int32 Sum throws OverflowException
@@ -212,6 +225,22 @@ class RuntimeExecutor {
  private:
   QueryResult<float> Run(const FusedKernelPlan& plan, const float* device_in, size_t n);
   QueryResult<int32_t> Run(const FusedKernelPlan& plan, const int32_t* device_in, size_t n);
+ public:
+  // A chain cut by Take/Skip: `segments` are the fused Where/Select programs between the cuts,
+  // cuts[i] the Take(k) or Skip(k) after segment i (one fewer than the segments), the last plan
+  // carries the terminal. Each cut segment is compacted on the device and the cut applied to the
+  // compacted range; nothing comes back to the host but the terminal's result.
+  template <typename T>
+  QueryResult<T> RunSegments(const std::vector<FusedKernelPlan>& segments, const std::vector<MethodCall>& cuts,
+                             const T* device_in, size_t n);
+
+ private:
+  // Compaction of one program over [device_in, +n) into `out`: the kept count. With `limit`, the
+  // consumer stops pulling after `limit` kept elements (Take, First, Single), so an element that
+  // throws after them is never evaluated in C#: the count is then that of the elements before it.
+  template <typename T>
+  int64_t ToArrayLimited(const FusedKernelPlan& plan, const T* device_in, size_t n, T* out,
+                         std::optional<int64_t> limit);
   std::shared_ptr<Backends::Hip::HipAccelerator> acc_;
 };
 
@@ -255,8 +284,27 @@ class ComputeQueryable {
   // Operators the HIP kernels do not implement: accepted into the chain, rejected at execution
   // with NotSupportedException (as the reference's generators reject them).
   ComputeQueryable OrderBy(const Expr& key) const;
+  // Take / Skip (mapped to Filter operations by the reference, ExpressionTreeVisitor.cs:263-265):
+  // the first n elements of the sequence at that point, or all but them. n <= 0: Take gives an
+  // empty sequence, Skip the whole one (Enumerable semantics).
+  ComputeQueryable Take(int64_t count) const;
+  ComputeQueryable Skip(int64_t count) const;
 
   std::vector<T> ToArray() const;
+  // Element operators (ExpressionTreeVisitor.cs:264-265), with Enumerable's exceptions:
+  // InvalidOperationException "Sequence contains no elements" / "... more than one element".
+  T First() const;
+  T First(const Expr& predicate) const { return Where(predicate).First(); }
+  T FirstOrDefault() const;   // default(T) = 0 on an empty sequence
+  T Last() const;
+  T LastOrDefault() const;
+  T Single() const;
+  T SingleOrDefault() const;  // 0 when empty; more than one element still throws
+  // Aggregate((acc, x) => ...) and Aggregate(seed, (acc, x) => ...): the folds AggregateKind names,
+  // with Param(0) the accumulator and Param(1) the element; other folds (float + and * depend on
+  // the order of their roundings) throw NotSupportedException.
+  T Aggregate(const Expr& func) const;
+  T Aggregate(T seed, const Expr& func) const;
   std::vector<T> ToComputeArray() const { return ToArray(); }
   // float: float64 accumulator, cast to float (Enumerable.Sum(IEnumerable<float>)). int: checked
   // int32 total, OverflowException by the BCL's rule for the source: its vectorised lane rule over a
@@ -278,7 +326,7 @@ class ComputeQueryable {
   FusedKernelPlan Explain(Terminal terminal = Terminal::ToArray) const;
 
  private:
-  QueryResult<T> Run(Terminal t) const;
+  QueryResult<T> Run(Terminal t, const std::vector<MethodCall>* chain = nullptr) const;
   const T* host_ = nullptr;
   const IUnifiedMemoryBuffer* device_ = nullptr;
   size_t n_ = 0;

@@ -85,7 +85,12 @@ Expr::Expr(int32_t constant) {
   n->IsInt = true;
   node_ = std::move(n);
 }
-Expr Expr::Parameter() { return Expr(MakeNode(ExprKind::Parameter)); }
+Expr Expr::Parameter(int index) {
+  auto n = std::make_shared<ExprNode>();
+  n->Kind = ExprKind::Parameter;
+  n->IValue = index;
+  return Expr(std::move(n));
+}
 bool Expr::IsPredicate() const { return IsPredicateKind(node_->Kind); }
 
 std::string Expr::ToString() const {
@@ -94,7 +99,7 @@ std::string Expr::ToString() const {
   auto R = [&] { return Expr(n.Right).ToString(); };
   std::ostringstream os;
   switch (n.Kind) {
-    case ExprKind::Parameter: return "x";
+    case ExprKind::Parameter: return n.IValue == 0 ? "x" : "x" + std::to_string(n.IValue);
     case ExprKind::Constant:
       if (n.IsInt) os << n.IValue;
       else os << n.Value << "f";
@@ -316,6 +321,8 @@ struct Compiler {
 
   // Operand source for a leaf: the element itself, or an immediate.
   std::pair<uint8_t, uint32_t> LeafSource(const ExprNode& n) const {
+    if (n.Kind == ExprKind::Parameter && n.IValue != 0)
+      throw NotSupportedException("Where/Select lambdas take one parameter");
     return n.Kind == ExprKind::Parameter ? std::make_pair((uint8_t)DC_LQ_SRC_ELEM, 0u)
                                          : std::make_pair((uint8_t)DC_LQ_SRC_IMM, ImmBits(n));
   }
@@ -325,7 +332,10 @@ struct Compiler {
   // both raises the left one's exception, as C# evaluates operands left to right.
   void Value(const ExprNode& n, int free_save) {
     switch (n.Kind) {
-      case ExprKind::Parameter: Emit(Instr(DC_LQ_LOAD, DC_LQ_SRC_ELEM)); return;
+      case ExprKind::Parameter:
+        if (n.IValue != 0) throw NotSupportedException("Where/Select lambdas take one parameter");
+        Emit(Instr(DC_LQ_LOAD, DC_LQ_SRC_ELEM));
+        return;
       case ExprKind::Constant: Emit(Instr(DC_LQ_LOAD, DC_LQ_SRC_IMM, ImmBits(n))); return;
       case ExprKind::Negate: Value(*n.Left, free_save); Emit(Instr(DC_LQ_NEG)); return;
       case ExprKind::Abs: Value(*n.Left, free_save); Emit(Instr(DC_LQ_ABS)); return;
@@ -741,6 +751,139 @@ QueryResult<int32_t> RuntimeExecutor::Run(const FusedKernelPlan& plan, const int
   return r;
 }
 
+namespace {
+
+bool IsCut(const MethodCall& m) { return m.Method == "Take" || m.Method == "Skip"; }
+
+bool IsElementTerminal(Terminal t) {
+  return t == Terminal::First || t == Terminal::FirstOrDefault || t == Terminal::Last || t == Terminal::LastOrDefault ||
+         t == Terminal::Single || t == Terminal::SingleOrDefault;
+}
+
+int32_t LaunchToArray(dc_hip_ctx* ctx, const dc_linq_chain& prog, const float* in, int64_t n, float* out,
+                      int64_t* cnt, int64_t*) {
+  return dc_hip_linq_where_select_f32(ctx, &prog, in, n, out, cnt);
+}
+int32_t LaunchToArray(dc_hip_ctx* ctx, const dc_linq_chain& prog, const int32_t* in, int64_t n, int32_t* out,
+                      int64_t* cnt, int64_t* fault) {
+  return dc_hip_linq_where_select_i32(ctx, &prog, in, n, out, cnt, fault);
+}
+
+}  // namespace
+
+template <typename T>
+int64_t RuntimeExecutor::ToArrayLimited(const FusedKernelPlan& plan, const T* device_in, size_t n, T* out,
+                                        std::optional<int64_t> limit) {
+  dc_hip_ctx* ctx = acc_->Context();
+  auto& mem = acc_->Memory();
+  auto cnt = mem.AllocateAsync<int64_t>(1);
+  std::shared_ptr<IUnifiedMemoryBufferT<int64_t>> fault;
+  if (plan.CanFault) fault = mem.AllocateAsync<int64_t>(1);
+  auto run = [&](size_t len) {
+    auto once = [&](const dc_linq_chain& prog) {
+      Check(LaunchToArray(ctx, prog, device_in, (int64_t)len, out, cnt->Data(), fault ? fault->Data() : nullptr),
+            "dc_hip_linq_where_select");
+      acc_->Synchronize();
+      int64_t k = 0;
+      cnt->CopyToHost(&k, sizeof(k));
+      return k;
+    };
+    return ResolveCompactedCount(once(plan.Program), [&]() {
+      dc_linq_chain ordered = plan.Program;
+      ordered.flags |= DC_LINQ_FLAG_ORDERED_GRID;
+      return once(ordered);
+    });
+  };
+  const int64_t k = run(n);
+  int64_t f = DC_LINQ_FAULT_NONE;
+  if (fault) fault->CopyToHost(&f, sizeof(f));
+  if (f < 0) return k;
+  // Element f / 4 throws. The elements before it do not; if they already hold `limit` kept
+  // elements, the consumer stopped pulling before it and LINQ-to-objects never evaluates it.
+  if (limit) {
+    const int64_t k_before = run((size_t)(f / 4));
+    if (k_before >= *limit) return k_before;
+  }
+  ThrowIfFaulted(f);
+  return k;
+}
+
+template <typename T>
+QueryResult<T> RuntimeExecutor::RunSegments(const std::vector<FusedKernelPlan>& segments,
+                                            const std::vector<MethodCall>& cuts, const T* device_in, size_t n) {
+  auto& mem = acc_->Memory();
+  const T* src = device_in;
+  size_t len = n;
+  std::vector<std::shared_ptr<IUnifiedMemoryBufferT<T>>> held;  // compacted segments still read
+  for (size_t i = 0; i + 1 < segments.size(); ++i) {
+    const bool take = cuts[i].Method == "Take";
+    const size_t c = (size_t)std::max<int64_t>(0, *cuts[i].Count);
+    if (segments[i].Program.n_instr > 0) {  // an empty segment leaves the sequence as it is
+      auto out = mem.AllocateAsync<T>(std::max<size_t>(len, 1));
+      const int64_t k = ToArrayLimited<T>(segments[i], src, len, out->Data(),
+                                          take ? std::optional<int64_t>((int64_t)c) : std::nullopt);
+      held.push_back(out);
+      src = out->Data();
+      len = (size_t)k;
+    }
+    if (take) {
+      len = std::min(len, c);
+    } else {
+      const size_t skip = std::min(len, c);
+      src += skip;
+      len -= skip;
+    }
+  }
+  const FusedKernelPlan& last = segments.back();
+  if (IsElementTerminal(last.Term)) {
+    // First stops pulling after one kept element, Single after two (the second one is already an
+    // error), Last reads the whole sequence.
+    const bool first = last.Term == Terminal::First || last.Term == Terminal::FirstOrDefault;
+    const bool single = last.Term == Terminal::Single || last.Term == Terminal::SingleOrDefault;
+    std::optional<int64_t> limit;
+    if (first) limit = 1;
+    if (single) limit = 2;
+    const T* seq = src;
+    int64_t k = (int64_t)len;
+    std::shared_ptr<IUnifiedMemoryBufferT<T>> out;
+    if (last.Program.n_instr > 0) {
+      out = mem.AllocateAsync<T>(std::max<size_t>(len, 1));
+      k = ToArrayLimited<T>(last, src, len, out->Data(), limit);
+      seq = out->Data();
+    }
+    QueryResult<T> r;
+    r.Count = k;
+    if (k > 0) {
+      const int64_t at = (first || single) ? 0 : k - 1;
+      T v{};
+      Check(dc_hip_memcpy_d2h_async(acc_->Context(), &v, seq + at, sizeof(T)), "dc_hip_memcpy_d2h_async");
+      acc_->Synchronize();
+      r.Values.push_back(v);
+    }
+    return r;
+  }
+  if (last.Term == Terminal::Aggregate) {
+    // Add: the exact total (Count's kernel, which has no overflow rule; the fold is unchecked
+    // and wraps); Min / Max: the Min / Max kernels.
+    FusedKernelPlan p = last;
+    p.Term = last.Fold == AggregateKind::Add ? Terminal::Count
+             : last.Fold == AggregateKind::Min ? Terminal::Min : Terminal::Max;
+    p.BareSource = false;
+    return Run(p, src, len);
+  }
+  return Run(last, src, len);
+}
+
+template int64_t RuntimeExecutor::ToArrayLimited<float>(const FusedKernelPlan&, const float*, size_t, float*,
+                                                        std::optional<int64_t>);
+template int64_t RuntimeExecutor::ToArrayLimited<int32_t>(const FusedKernelPlan&, const int32_t*, size_t, int32_t*,
+                                                          std::optional<int64_t>);
+template QueryResult<float> RuntimeExecutor::RunSegments<float>(const std::vector<FusedKernelPlan>&,
+                                                                const std::vector<MethodCall>&, const float*, size_t);
+template QueryResult<int32_t> RuntimeExecutor::RunSegments<int32_t>(const std::vector<FusedKernelPlan>&,
+                                                                    const std::vector<MethodCall>&, const int32_t*,
+                                                                    size_t);
+
 template <typename T>
 QueryResult<T> RuntimeExecutor::Execute(const FusedKernelPlan& plan, const T* data, size_t n) {
   auto in = acc_->Memory().AllocateAsync<T>(std::max<size_t>(n, 1));
@@ -779,9 +922,47 @@ std::shared_ptr<ComputeQueryProvider> ComputeQueryProvider::Default() {
   return provider;
 }
 
+namespace {
+
+// The fold of an Aggregate lambda (acc, x) => ...: Add, Min or Max of the two parameters, in either
+// order, over int elements. Everything else is refused: float + and * fold with one rounding per
+// step in enumeration order, which a parallel reduction does not reproduce, and MathF.Min/Max
+// fold signed zeros and NaNs differently from the Min/Max kernels.
+AggregateKind ParseFold(const Expr& func, ElementType element) {
+  const ExprNode& n = func.Node();
+  auto is_param = [](const std::shared_ptr<const ExprNode>& c, int i) {
+    return c && c->Kind == ExprKind::Parameter && c->IValue == i;
+  };
+  const bool two_params = n.Left && n.Right && ((is_param(n.Left, 0) && is_param(n.Right, 1)) ||
+                                                (is_param(n.Left, 1) && is_param(n.Right, 0)));
+  if (!two_params || element != ElementType::Int32)
+    throw NotSupportedException("Aggregate(" + func.ToString() + ") has no exact HIP kernel: the kernels fold int "
+                                "(acc, x) => acc + x, Math.Min(acc, x) and Math.Max(acc, x)");
+  switch (n.Kind) {
+    case ExprKind::Add: return AggregateKind::Add;
+    case ExprKind::Min: return AggregateKind::Min;
+    case ExprKind::Max: return AggregateKind::Max;
+    default:
+      throw NotSupportedException("Aggregate(" + func.ToString() + ") has no exact HIP kernel: the kernels fold int "
+                                  "(acc, x) => acc + x, Math.Min(acc, x) and Math.Max(acc, x)");
+  }
+}
+
+}  // namespace
+
+// One segment (Where/Select operations only) with its terminal: the fused program, plus the
+// element terminals and Aggregate, which run on the compacted sequence (the reference maps the
+// element operators to Filter and Aggregate to Reduce, ExpressionTreeVisitor.cs:245,263-265).
 FusedKernelPlan ComputeQueryProvider::Plan(const std::vector<MethodCall>& chain, Terminal terminal, size_t n,
                                            ElementType element) const {
   std::vector<MethodCall> full = chain;
+  std::optional<MethodCall> fold;
+  if (terminal == Terminal::Aggregate) {
+    if (full.empty() || full.back().Method != "Aggregate" || !full.back().Lambda)
+      throw ArgumentException("Aggregate needs its function as the last call of the chain");
+    fold = full.back();
+    full.pop_back();
+  }
   switch (terminal) {
     case Terminal::Sum: full.push_back({"Sum", std::nullopt}); break;
     case Terminal::Count: full.push_back({"Count", std::nullopt}); break;
@@ -789,25 +970,65 @@ FusedKernelPlan ComputeQueryProvider::Plan(const std::vector<MethodCall>& chain,
     case Terminal::Average: full.push_back({"Average", std::nullopt}); break;
     case Terminal::Min: full.push_back({"Min", std::nullopt}); break;
     case Terminal::Max: full.push_back({"Max", std::nullopt}); break;
-    case Terminal::ToArray: break;
+    default: break;  // ToArray, the element terminals and Aggregate: a Where/Select program alone
   }
+  for (const MethodCall& m : full)
+    if (IsCut(m)) throw NotSupportedException("internal: Take/Skip inside a fused segment");
   // Stage 1: expression tree -> operation graph.
   OperationGraph graph = ExpressionTreeVisitor().Visit(full);
   // Stage 2: fused kernel for the graph.
   (void)n;
-  return HipKernelGenerator().GenerateHipKernel(graph, element);
+  FusedKernelPlan plan = HipKernelGenerator().GenerateHipKernel(graph, element);
+  if (IsElementTerminal(terminal)) plan.Term = terminal;
+  if (fold) {
+    plan.Term = Terminal::Aggregate;
+    plan.Fold = ParseFold(*fold->Lambda, element);
+    if (fold->Seed) {
+      const ExprNode& sn = fold->Seed->Node();
+      if (sn.Kind != ExprKind::Constant || !sn.IsInt) throw ArgumentException("Aggregate's seed is an int constant");
+      plan.Seed = sn.IValue;
+    }
+  }
+  return plan;
 }
 
 template <typename T>
 QueryResult<T> ComputeQueryProvider::Execute(const std::vector<MethodCall>& chain, Terminal terminal, const T* host,
                                              size_t n, const IUnifiedMemoryBuffer* device) {
-  FusedKernelPlan plan = Plan(chain, terminal, n, ElementTypeOf<T>::value);
+  // Take/Skip cut the chain into segments of fused Where/Select operations; the terminal goes with
+  // the last one (an Aggregate terminal brings its function as the chain's last call).
+  std::vector<std::vector<MethodCall>> segs(1);
+  std::vector<MethodCall> cuts;
+  for (size_t i = 0; i < chain.size(); ++i) {
+    const MethodCall& m = chain[i];
+    if (IsCut(m)) {
+      if (!m.Count) throw ArgumentNullException(m.Method + " needs a count");
+      cuts.push_back(m);
+      segs.emplace_back();
+    } else {
+      segs.back().push_back(m);
+    }
+  }
+  std::vector<FusedKernelPlan> plans;
+  for (size_t i = 0; i < segs.size(); ++i)
+    plans.push_back(Plan(segs[i], i + 1 == segs.size() ? terminal : Terminal::ToArray, n, ElementTypeOf<T>::value));
+  // After a Take/Skip the sequence is an iterator, not the source array (Enumerable.Sum's span rule).
+  if (!cuts.empty()) plans.back().BareSource = false;
   WorkloadCharacteristics w;
   w.DataSize = n;
-  w.OperationCount = (int)plan.FusedOperationIds.size();
+  w.OperationCount = (int)chain.size();
   w.HasReduction = terminal != Terminal::ToArray;
   BackendSelector(HasAccelerator()).SelectBackend(w);  // throws without a HIP device
-  return device ? executor_->Execute<T>(plan, *device, n) : executor_->Execute<T>(plan, host, n);
+  if (plans.size() == 1 && !IsElementTerminal(terminal) && terminal != Terminal::Aggregate)
+    return device ? executor_->Execute<T>(plans[0], *device, n) : executor_->Execute<T>(plans[0], host, n);
+  if (device) {
+    if (device->Type() != ElementTypeOf<T>::value)
+      throw NotSupportedException("the device buffer's element type does not match the query's");
+    return executor_->RunSegments<T>(plans, cuts, static_cast<const T*>(device->DevicePointer()), n);
+  }
+  auto in = executor_->Accelerator().Memory().AllocateAsync<T>(std::max<size_t>(n, 1));
+  if (n) in->CopyFromHost(host, n * sizeof(T));
+  return executor_->RunSegments<T>(plans, cuts, in->Data(), n);
 }
 
 template QueryResult<float> ComputeQueryProvider::Execute<float>(const std::vector<MethodCall>&, Terminal,
@@ -850,8 +1071,98 @@ ComputeQueryable<T> ComputeQueryable<T>::OrderBy(const Expr& key) const {
 }
 
 template <typename T>
-QueryResult<T> ComputeQueryable<T>::Run(Terminal t) const {
-  return provider_->Execute<T>(chain_, t, host_, n_, device_);
+QueryResult<T> ComputeQueryable<T>::Run(Terminal t, const std::vector<MethodCall>* chain) const {
+  return provider_->Execute<T>(chain ? *chain : chain_, t, host_, n_, device_);
+}
+
+template <typename T>
+ComputeQueryable<T> ComputeQueryable<T>::Take(int64_t count) const {
+  ComputeQueryable q = *this;
+  q.chain_.push_back({"Take", std::nullopt, count});
+  return q;
+}
+
+template <typename T>
+ComputeQueryable<T> ComputeQueryable<T>::Skip(int64_t count) const {
+  ComputeQueryable q = *this;
+  q.chain_.push_back({"Skip", std::nullopt, count});
+  return q;
+}
+
+namespace {
+[[noreturn]] void ThrowNoElements() { throw InvalidOperationException("Sequence contains no elements"); }
+[[noreturn]] void ThrowMoreThanOne() { throw InvalidOperationException("Sequence contains more than one element"); }
+}  // namespace
+
+template <typename T>
+T ComputeQueryable<T>::First() const {
+  QueryResult<T> r = Run(Terminal::First);
+  if (r.Count == 0) ThrowNoElements();
+  return r.Values[0];
+}
+
+template <typename T>
+T ComputeQueryable<T>::FirstOrDefault() const {
+  QueryResult<T> r = Run(Terminal::FirstOrDefault);
+  return r.Count == 0 ? T{} : r.Values[0];
+}
+
+template <typename T>
+T ComputeQueryable<T>::Last() const {
+  QueryResult<T> r = Run(Terminal::Last);
+  if (r.Count == 0) ThrowNoElements();
+  return r.Values[0];
+}
+
+template <typename T>
+T ComputeQueryable<T>::LastOrDefault() const {
+  QueryResult<T> r = Run(Terminal::LastOrDefault);
+  return r.Count == 0 ? T{} : r.Values[0];
+}
+
+template <typename T>
+T ComputeQueryable<T>::Single() const {
+  QueryResult<T> r = Run(Terminal::Single);
+  if (r.Count == 0) ThrowNoElements();
+  if (r.Count > 1) ThrowMoreThanOne();
+  return r.Values[0];
+}
+
+template <typename T>
+T ComputeQueryable<T>::SingleOrDefault() const {
+  QueryResult<T> r = Run(Terminal::SingleOrDefault);
+  if (r.Count > 1) ThrowMoreThanOne();
+  return r.Count == 0 ? T{} : r.Values[0];
+}
+
+// Aggregate(func): the fold starts from the first element (an empty sequence throws);
+// Aggregate(seed, func) from the seed. Add wraps as C#'s unchecked int +.
+template <typename T>
+T ComputeQueryable<T>::Aggregate(const Expr& func) const {
+  std::vector<MethodCall> chain = chain_;
+  chain.push_back({"Aggregate", func});
+  QueryResult<T> r = Run(Terminal::Aggregate, &chain);
+  if (r.Count == 0) ThrowNoElements();
+  if constexpr (std::is_same<T, int32_t>::value) {
+    return func.Node().Kind == ExprKind::Add ? (int32_t)(uint32_t)(uint64_t)r.IntSum : r.Extreme;
+  } else {
+    return r.Extreme;  // not reached: float folds are refused by the planner
+  }
+}
+
+template <typename T>
+T ComputeQueryable<T>::Aggregate(T seed, const Expr& func) const {
+  std::vector<MethodCall> chain = chain_;
+  chain.push_back({"Aggregate", func, std::nullopt, Expr(seed)});
+  QueryResult<T> r = Run(Terminal::Aggregate, &chain);
+  if constexpr (std::is_same<T, int32_t>::value) {
+    const ExprKind k = func.Node().Kind;
+    if (k == ExprKind::Add) return (int32_t)((uint32_t)seed + (uint32_t)(uint64_t)r.IntSum);
+    if (r.Count == 0) return seed;
+    return k == ExprKind::Min ? std::min(seed, r.Extreme) : std::max(seed, r.Extreme);
+  } else {
+    return r.Count == 0 ? seed : r.Extreme;  // not reached: float folds are refused by the planner
+  }
 }
 
 template <typename T>

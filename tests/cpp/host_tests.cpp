@@ -936,6 +936,70 @@ TEST_GPU(linq_int_chains_match_oracle_at_1m) {
   }());
 }
 
+TEST_GPU(linq_take_skip_and_element_operators) {
+  // Take/Skip/First/Last/Single (the reference maps them to Filter operations,
+  // ExpressionTreeVisitor.cs:263-265) with Enumerable's results and exceptions.
+  auto x = Param();
+  auto p = std::make_shared<ComputeQueryProvider>(Gpu());
+  const auto r100 = Range(1, 100);
+  CHECK((AsComputeQueryable(r100, p).Where(x % 2 == 0).Skip(5).Take(10).ToArray() ==
+         std::vector<int32_t>{12, 14, 16, 18, 20, 22, 24, 26, 28, 30}));
+  CHECK((AsComputeQueryable(r100, p).Take(3).Select(x * 10).ToArray() == std::vector<int32_t>{10, 20, 30}));
+  CHECK((AsComputeQueryable(r100, p).Skip(97).ToArray() == std::vector<int32_t>{98, 99, 100}));
+  CHECK(AsComputeQueryable(r100, p).Skip(200).ToArray().empty() && AsComputeQueryable(r100, p).Take(-1).ToArray().empty());
+  CHECK(AsComputeQueryable(r100, p).Where(x > 10).Take(5).Sum() == 11 + 12 + 13 + 14 + 15);
+  CHECK(AsComputeQueryable(r100, p).Skip(90).Count() == 10);
+  CHECK(AsComputeQueryable(r100, p).First() == 1 && AsComputeQueryable(r100, p).Last() == 100);
+  CHECK(AsComputeQueryable(r100, p).First(x > 41) == 42);
+  CHECK(AsComputeQueryable(r100, p).Where(x % 7 == 0).Last() == 98);
+  CHECK(AsComputeQueryable(r100, p).Where(x > 99).Single() == 100);
+  CHECK(AsComputeQueryable(r100, p).Where(x > 100).FirstOrDefault() == 0);
+  CHECK(AsComputeQueryable(r100, p).Where(x > 100).LastOrDefault() == 0);
+  CHECK(AsComputeQueryable(r100, p).Where(x > 100).SingleOrDefault() == 0);
+  CHECK_THROWS(InvalidOperationException, AsComputeQueryable(r100, p).Where(x > 100).First());
+  CHECK_THROWS(InvalidOperationException, AsComputeQueryable(r100, p).Where(x > 98).Single());
+  CHECK_THROWS(InvalidOperationException, AsComputeQueryable(r100, p).Where(x > 98).SingleOrDefault());
+  std::vector<float> f{0.5f, -1.0f, 2.5f, 4.0f};
+  CHECK(AsComputeQueryable(f, p).Where(x < 0.0f).Single() == -1.0f);
+  CHECK((AsComputeQueryable(f, p).Skip(1).Take(2).Select(x * 2.0f).ToArray() == std::vector<float>{-2.0f, 5.0f}));
+  // Pull semantics: Take and First stop before an element that would throw; Last and Skip do not.
+  std::vector<int32_t> z{1, 2, 3, 0, 5};
+  CHECK((AsComputeQueryable(z, p).Select(100 / x).Take(3).ToArray() == std::vector<int32_t>{100, 50, 33}));
+  CHECK_THROWS(DivideByZeroException, AsComputeQueryable(z, p).Select(100 / x).Take(4).ToArray());
+  CHECK(AsComputeQueryable(z, p).Select(100 / x).First() == 100);
+  CHECK_THROWS(DivideByZeroException, AsComputeQueryable(z, p).Select(100 / x).Last());
+  CHECK_THROWS(DivideByZeroException, AsComputeQueryable(z, p).Select(100 / x).Skip(4).ToArray());
+  CHECK_THROWS(InvalidOperationException, AsComputeQueryable(z, p).Select(100 / x).Single());  // 2 elements first
+  // at 1M elements against the same chain evaluated on the host
+  std::vector<int32_t> big(1 << 20);
+  oracle_gen_uniform_i32(big.data(), (int64_t)big.size(), 58, 1, -1000, 1000);
+  std::vector<int32_t> ref;
+  for (int32_t v : big)
+    if (v % 3 == 0) ref.push_back(v * 2);
+  std::vector<int32_t> mid(ref.begin() + 1000, ref.begin() + 6000);
+  CHECK(AsComputeQueryable(big, p).Where(x % 3 == 0).Select(x * 2).Skip(1000).Take(5000).ToArray() == mid);
+  CHECK(AsComputeQueryable(big, p).Where(x % 3 == 0).Select(x * 2).Last() == ref.back());
+}
+
+TEST_GPU(linq_aggregate_folds) {
+  auto acc = Param(0), x = Param(1), e = Param();
+  auto p = std::make_shared<ComputeQueryProvider>(Gpu());
+  const auto r100 = Range(1, 100);
+  CHECK(AsComputeQueryable(r100, p).Aggregate(acc + x) == 5050);
+  CHECK(AsComputeQueryable(r100, p).Aggregate(x + acc) == 5050);
+  CHECK(AsComputeQueryable(r100, p).Aggregate(1000, acc + x) == 6050);
+  CHECK(AsComputeQueryable(r100, p).Where(e % 2 == 1).Aggregate(Math::Max(acc, x)) == 99);
+  CHECK(AsComputeQueryable(r100, p).Aggregate(-5, Math::Min(acc, x)) == -5);
+  std::vector<int32_t> w{INT32_MAX, 1};
+  CHECK(AsComputeQueryable(w, p).Aggregate(acc + x) == INT32_MIN);  // unchecked: wraps, no exception
+  std::vector<int32_t> none;
+  CHECK_THROWS(InvalidOperationException, AsComputeQueryable(none, p).Aggregate(acc + x));
+  CHECK(AsComputeQueryable(none, p).Aggregate(7, acc + x) == 7);
+  std::vector<float> f{1.0f, 2.0f};
+  CHECK_THROWS(NotSupportedException, AsComputeQueryable(f, p).Aggregate(acc + x));  // order of float roundings
+  CHECK_THROWS(NotSupportedException, AsComputeQueryable(r100, p).Aggregate(acc * x));
+}
+
 TEST_GPU(linq_min_max_match_enumerable) {
   auto x = Param();
   auto p = std::make_shared<ComputeQueryProvider>(Gpu());
