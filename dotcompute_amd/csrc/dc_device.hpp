@@ -122,6 +122,13 @@ __device__ inline uint32_t load_agent_u32(const uint32_t* p) {
 __device__ inline void store_agent_u32(uint32_t* p, uint32_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ inline uint32_t fetch_add_relaxed_agent_u32(uint32_t* p, uint32_t v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Waits until this wave's outstanding memory operations, stores included, have completed. After an
+// agent-scope atomic store (which writes through the XCD's L2) this makes the store visible to
+// every XCD before what follows, without the L2 write-back of an agent-scope release fence.
+__device__ inline void wait_memory_ops() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 __device__ inline void fence_release_agent() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
 __device__ inline void fence_acquire_agent() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
 

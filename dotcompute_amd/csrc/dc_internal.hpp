@@ -78,6 +78,7 @@ enum dc_counter_slot : int {
   DC_SLOT_LINQ_TICKET = 0,   // tile ticket of the compaction kernel (returned to 0 by the kernel)
   DC_SLOT_SPMV_LONG = 1,     // number of long rows found by the SpMV classification pass
   DC_SLOT_LINQ_DONE = 2,     // finished-workgroup word of the round-robin compaction (returned to 0)
+  DC_SLOT_REDUCE_DONE = 3,   // finished-workgroup word of the one-launch reductions (returned to 0)
   DC_SLOT_LINQ_FAULT = 4,    // 64-bit (slots 4-5): first exception of an int32 LINQ ToArray, ~(4 * index +
                              // kind), 0 when none (returned to 0 by the kernel that reports it)
   DC_SLOT_COUNT = 1024

@@ -7,10 +7,12 @@
 // thread holds in registers.
 //
 // ToArray (order-preserving stream compaction, one pass over the input), two kernels:
-//  - large 16-byte aligned inputs: the round-robin kernel (where_select_rounds_kernel, described
-//    at its definition): a resident grid, one workgroup per CU, tile counts published per round
-//    and summed by every workgroup, so no prefix travels from tile to tile;
-//  - everything else: a ticket-ordered grid with a decoupled lookback. tile = 512 threads x 32
+//  - 4-byte aligned inputs of any size: the round-robin kernel (where_select_rounds_kernel,
+//    described at its definition): a resident grid, one workgroup per CU (one per tile for inputs
+//    of fewer tiles), tile counts published per round and summed by every workgroup, so no prefix
+//    travels from tile to tile;
+//  - inputs that are not 4-byte aligned, and the retry after a resident grid gave up
+//    (DC_LINQ_FLAG_ORDERED_GRID): a ticket-ordered grid with a decoupled lookback. tile = 512 threads x 32
 //    elements = 16384 consecutive elements (64 KiB), claimed through an atomic ticket (so a tile
 //    only ever waits on tiles that started before it); thread t loads 16-byte vectors j = 0..7 at
 //    tile + j*2048 + t*4; for each vector j and slot k the wave takes ballot(keep) -> the element's
@@ -918,7 +920,6 @@ constexpr int kRrRing = (kRrDelay + 1) * kRrChunk;       // floats per worker wa
 constexpr int kRrCountsPerLane = 4;
 constexpr int kRrMaxGroups = dc::kWave * kRrCountsPerLane;  // P <= 256
 constexpr uint32_t kRrSpinLimit = 1u << 22;              // ~seconds: a wait that never ends reports
-constexpr int kRrMinRounds = 4;                          // below this the ticket kernel is used
 static_assert((kRrDelay + 1) * kRrChunk <= kRrRing, "the ring holds every staged tile at 100% selectivity");
 static_assert(kRrDelay < 8 && kRrDelay >= 2, "per-tile LDS tables are indexed modulo 8");
 
@@ -1018,7 +1019,9 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
   // the two halves of that line before it is written back.
   const uint32_t w = (P % 8u == 0u) ? (blockIdx.x % 8u) * (P / 8u) + blockIdx.x / 8u : blockIdx.x;
   const int64_t num_tiles = (n + kRrTile - 1) / kRrTile;
-  const uint32_t R0 = (uint32_t)((n / kRrTile) / P);  // rounds in which every tile is full
+  // Rounds in which every tile is full. A grid with one tile per workgroup (fewer tiles than CUs)
+  // runs its only round as the tail round: no pipeline to fill and drain.
+  const uint32_t R0 = (n / kRrTile) / P == 1 && num_tiles == P ? 0u : (uint32_t)((n / kRrTile) / P);
   const uint32_t rounds = R0 > 0 ? R0 + kRrDelay : 0;
   const bool tail_round = (int64_t)R0 * P < num_tiles;
   if (tid < 8) s_acc[tid] = 0;
@@ -1065,8 +1068,11 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
     if (lane == 0) {
       // Completion word: low 16 bits count finished workgroups, the rest counts failed ones. The last
       // workgroup writes the total (every workgroup holds the same base) or -1 if any wait gave up.
+      // Relaxed: the last workgroup reads nothing the others wrote except this word (every
+      // workgroup holds the same base), and an agent-scope release here would write back the
+      // XCD's L2 once per workgroup.
       const uint32_t add = 1u | (ok ? 0u : (1u << 16));
-      const uint32_t prev = __hip_atomic_fetch_add(done, add, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t prev = __hip_atomic_fetch_add(done, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if ((prev & 0xFFFFu) == P - 1) {
         *count_out = ((prev >> 16) == 0 && ok) ? base : (int64_t)-1;
         dc::store_agent_u32(done, 0u);
@@ -1176,9 +1182,9 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
                    std::make_integer_sequence<int, kBufs>{});
   for_each_index([&](auto U) __attribute__((always_inline)) { if (r < R0) round(e[U.value], e[(U.value + kRrAhead) % kBufs]); },
                  std::make_integer_sequence<int, kRrAhead>{});
-  for (; r < rounds; ++r) {  // drain: the last kRrDelay staged tiles
+  for (; r < rounds; ++r) {  // drain: the last kRrDelay staged tiles (fewer when R0 < kRrDelay)
     __syncthreads();
-    write(r - kRrDelay, r & 1);
+    if (r >= (uint32_t)kRrDelay) write(r - kRrDelay, r & 1);
   }
   if (tail_round) {  // tiles R0*P .. num_tiles-1 (full, partial or none), bounded loads
     const int64_t t = (int64_t)R0 * P + w;
@@ -1187,9 +1193,14 @@ __global__ __launch_bounds__(kRrBlock) void where_select_rounds_kernel(
 #pragma unroll
     for (int j = 0; j < kRrVec; ++j) {
       const int64_t at = t * kRrTile + chunk + j * 4 * dc::kWave + 4 * lane;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) e[4 * j + k] = (t < num_tiles && at + k < n) ? in[at + k] : 0.0f;
       const int64_t nv = t < num_tiles ? min(max(n - at, (int64_t)0), (int64_t)4) : 0;
+      if (nv == 4) {  // a whole vector (in is 16-byte aligned)
+        const dc::f32x4 v = dc::load_stream(reinterpret_cast<const dc::f32x4*>(in + at));
+        e[4 * j] = v.x; e[4 * j + 1] = v.y; e[4 * j + 2] = v.z; e[4 * j + 3] = v.w;
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) e[4 * j + k] = k < nv ? in[at + k] : 0.0f;
+      }
       valid |= ((1u << (uint32_t)nv) - 1u) << (4 * j);
     }
     bool kept[kRrEpt];
@@ -1915,7 +1926,12 @@ std::vector<int> all_reduce_modes() {
   return m;
 }
 
-uint32_t rounds_groups(const dc_hip_ctx* ctx) { return (uint32_t)std::min(ctx->cu_count, kRrMaxGroups); }
+// Workgroups of the round-robin grid over n (16-byte aligned) elements: one per CU, or one per
+// tile when the input has fewer tiles than CUs (then each owns one tile of the only round).
+uint32_t rounds_groups(const dc_hip_ctx* ctx, int64_t n) {
+  const int64_t tiles = (n + kRrTile - 1) / kRrTile;
+  return (uint32_t)std::max<int64_t>(1, std::min<int64_t>(tiles, std::min(ctx->cu_count, kRrMaxGroups)));
+}
 
 // Elements before the first 16-byte boundary of a 4-byte aligned input (0..3, at most n), or -1
 // for an input that is not 4-byte aligned.
@@ -1925,13 +1941,14 @@ int64_t head16(const float* input, int64_t n) {
   return std::min<int64_t>(n, (int64_t)(((16 - (a & 15)) & 15) >> 2));
 }
 
-// The round-robin kernel needs a 4-byte aligned input whose 16-byte aligned part (after the 0..3
-// head elements it peels) holds at least kRrMinRounds full rounds, and room for one workgroup per
-// CU (every program variant; asked once per context). The caller holds the context lock.
+// The round-robin kernel takes every 4-byte aligned input (it peels the 0..3 head elements before
+// the first 16-byte boundary) when one workgroup fits per CU (every program variant; asked once
+// per context). Measured against the lookback kernel (50 % kept, cache-resident below 64M): 16K
+// elements 5.1 against 6.7 us, 1M 7.2 against 10.1, 4M 10.0 against 15.1, 8M 14.7 against 24.1;
+// at 3M, one full round plus a tail round, 13.5 against 13.1. The caller holds the context lock.
 bool use_rounds(dc_hip_ctx* ctx, const float* input, int64_t n) {
-  const uint32_t groups = rounds_groups(ctx);
   const int64_t h = head16(input, n);
-  if (h < 0 || groups == 0 || (n - h) / kRrTile < (int64_t)kRrMinRounds * groups) return false;
+  if (h < 0 || ctx->cu_count <= 0) return false;
   if (ctx->rounds_fit < 0) {
     bool fit = true;
     for (int mode : all_reduce_modes()) {
@@ -1956,8 +1973,8 @@ int32_t launch_to_array(dc_hip_ctx* ctx, const dc_linq_chain* chain, bool is_int
     const void* fn = rounds_kernel(plan.mode);
     AffineChain aff = plan.aff;
     RdConst canon = plan.k;
-    const uint32_t groups = rounds_groups(ctx);
     const int head_n = (int)head16(input, n);  // 0..3: use_rounds accepted the input
+    const uint32_t groups = rounds_groups(ctx, n - head_n);
     const int64_t tiles = (n - head_n + kRrTile - 1) / kRrTile;
     const size_t words = (size_t)((tiles + groups - 1) / groups + 1) * groups;
     uint32_t epoch16 = 0;

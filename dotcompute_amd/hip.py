@@ -32,6 +32,7 @@ DC_ERR_NOT_FOUND = -8
 # dc_linq_strategy: which kernel dc_hip_linq_where_select_f32 runs for an input
 STRATEGY_LOOKBACK = 0
 STRATEGY_ROUNDS = 1
+LINQ_FLAG_ORDERED_GRID = 1  # dc_linq_chain.flags: run ToArray on the ticket-ordered lookback grid
 
 # dc_linq_minmax: which terminal dc_hip_linq_where_select_minmax_f32 computes
 LINQ_MIN = 0

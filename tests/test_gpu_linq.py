@@ -21,7 +21,17 @@ pytestmark = pytest.mark.gpu
 CHAIN = hip.where_gt0_select_2x_plus_1()
 
 
+def ordered(chain):
+    """A copy of `chain` that runs ToArray on the ticket-ordered lookback grid."""
+    ch = type(chain).from_buffer_copy(chain)
+    ch.flags |= hip.LINQ_FLAG_ORDERED_GRID
+    return ch
+
+
 def run_to_array(ctx, chain, x, offset=0):
+    """ToArray on the kernel the library picks and on the lookback grid; both must agree bit for
+    bit (the round-robin grid takes every 4-byte aligned input, so this keeps the lookback kernel
+    under the same checks)."""
     n = x.size
     dx = ctx.empty(n + offset + 1, np.float32)
     if n:
@@ -29,13 +39,17 @@ def run_to_array(ctx, chain, x, offset=0):
     src = hip.DeviceArray(ctx, dx.ptr + 4 * offset, 4 * n, np.dtype(np.float32), (n,))
     out = ctx.empty(n + 1, np.float32)
     cnt = ctx.empty(1, np.int64)
-    ctx.where_select_f32(chain, src, out, cnt, n)
-    ctx.synchronize()
-    k = int(cnt.to_host()[0])
-    got = out.to_host(k) if k else np.empty(0, np.float32)
+    res = []
+    for ch in (chain, ordered(chain)):
+        ctx.where_select_f32(ch, src, out, cnt, n)
+        ctx.synchronize()
+        k = int(cnt.to_host()[0])
+        assert k >= 0, "resident grid reported a wait that gave up"
+        res.append(out.to_host(k) if k else np.empty(0, np.float32))
     for a in (dx, out, cnt):
         ctx.free(a)
-    return got
+    assert res[0].size == res[1].size and np.array_equal(bits(res[0]), bits(res[1]))
+    return res[0]
 
 
 def run_sum(ctx, chain, x):
@@ -275,8 +289,9 @@ def test_affine_fast_path_matches_interpreter(ctx, idx):
     assert abs(s - sd) <= 1e-5 * math.log2(x.size) * max(abs(sd), 1.0)
 
 
-# ---- the round-robin kernel (large, 16-byte aligned inputs) ------------------------------------
-# Tiles of 8 worker waves x 64 lanes x 16 elements; used from 4 full rounds of min(CUs, 256) tiles.
+# ---- the round-robin kernel (every 4-byte aligned input) ----------------------------------------
+# Tiles of 8 worker waves x 64 lanes x 16 elements; rr_min_n() = 4 full rounds of min(CUs, 256)
+# tiles, the shape the software pipeline is built for.
 RR_TILE = 8 * 64 * 16
 
 
@@ -313,21 +328,35 @@ def test_round_robin_sizes_bit_exact(ctx, extra):
     assert np.array_equal(bits(got), bits(ref))
 
 
+@pytest.mark.parametrize("n", [1, 3, 100, RR_TILE - 1, RR_TILE, 2 * RR_TILE, 2 * RR_TILE + 1, 1 << 20, 1_000_000,
+                               3_000_000])
+def test_round_robin_small_inputs(ctx, n):
+    """Every 4-byte aligned input runs the round-robin grid: below one workgroup per CU each
+    workgroup owns one tile (the only round runs as the tail round), one full round plus a tail
+    round (3M), and starts 1-3 floats past a 16-byte boundary; bit-exact, and equal to the lookback
+    kernel's result."""
+    x = oracle.gen_uniform_f32(n + 3, 70 + n % 13, 0)
+    for offset in (0, 1, 3):
+        got = run_to_array_checked(ctx, CHAIN, x[:n], hip.STRATEGY_ROUNDS, offset=offset)
+        assert np.array_equal(bits(got), bits(oracle.where_gt0_select_2x_plus_1(x[:n])))
+        assert np.array_equal(bits(got), bits(run_to_array(ctx, CHAIN, x[:n], offset=offset)))
+
+
 def test_round_robin_threshold_and_alignment(ctx):
     n = rr_min_n()
     x = oracle.gen_uniform_f32(n + 3, 61, 0)
-    # one element short of four rounds: the lookback kernel, same result
-    got = run_to_array_checked(ctx, CHAIN, x[: n - 1], hip.STRATEGY_LOOKBACK)
+    # one element short of four rounds: three full rounds and a tail round, same result
+    got = run_to_array_checked(ctx, CHAIN, x[: n - 1], hip.STRATEGY_ROUNDS)
     assert np.array_equal(bits(got), bits(oracle.where_gt0_select_2x_plus_1(x[: n - 1])))
     # a start 1-3 floats past a 16-byte boundary: the round-robin grid peels the 3-1 head elements
-    # (the aligned part still holds four rounds), bit-exact; one element fewer: the lookback kernel
     for offset in (1, 2, 3):
-        h = 4 - offset
         got = run_to_array_checked(ctx, CHAIN, x, hip.STRATEGY_ROUNDS, offset=offset)
         assert np.array_equal(bits(got), bits(oracle.where_gt0_select_2x_plus_1(x)))
-        short = x[: n + h - 1]
-        got = run_to_array_checked(ctx, CHAIN, short, hip.STRATEGY_LOOKBACK, offset=offset)
-        assert np.array_equal(bits(got), bits(oracle.where_gt0_select_2x_plus_1(short)))
+    # a start that is not 4-byte aligned: the lookback kernel
+    raw = ctx.empty(n + 2, np.float32)
+    odd = hip.DeviceArray(ctx, raw.ptr + 2, 4 * n, np.dtype(np.float32), (n,))
+    assert ctx.to_array_strategy(odd, n) == hip.STRATEGY_LOOKBACK
+    ctx.free(raw)
 
 
 @pytest.mark.parametrize("offset", [1, 2, 3])

@@ -52,17 +52,28 @@ def put(ctx, x, offset=0):
 
 
 def run_to_array(ctx, ch, x, offset=0):
+    """ToArray on the kernel the library picks and on the lookback grid (flag
+    LINQ_FLAG_ORDERED_GRID): the same first exception and, without one, the same elements."""
     n = x.size
     d, src = put(ctx, x, offset)
     out, cnt, fault = ctx.empty(n + 1, np.int32), ctx.empty(1, np.int64), ctx.empty(1, np.int64)
-    ctx.where_select_i32(ch, src, out, cnt, fault, n)
-    ctx.synchronize()
-    k = int(cnt.to_host()[0])
-    f = int(fault.to_host()[0])
-    got = out.to_host(k) if k > 0 and f < 0 else np.empty(0, np.int32)
+    res = []
+    for c in (ch, type(ch).from_buffer_copy(ch)):
+        if res:
+            c.flags |= hip.LINQ_FLAG_ORDERED_GRID
+        ctx.where_select_i32(c, src, out, cnt, fault, n)
+        ctx.synchronize()
+        k = int(cnt.to_host()[0])
+        f = int(fault.to_host()[0])
+        assert k >= 0 or f >= 0, "resident grid reported a wait that gave up"
+        res.append((out.to_host(k) if k > 0 and f < 0 else np.empty(0, np.int32), k, f))
     for a in (d, out, cnt, fault):
         ctx.free(a)
-    return got, k, f
+    (g0, k0, f0), (g1, k1, f1) = res
+    assert f0 == f1
+    if f0 < 0:
+        assert k0 == k1 and np.array_equal(g0, g1)
+    return g0, k0, f0
 
 
 def run_sum(ctx, ch, x, offset=0):

@@ -255,6 +255,22 @@ def test_sum_i32_bcl_rule_on_large_inputs(ctx, n):
     assert bcl_overflows(x1) == 0 and bcl_overflows(x3) == 1
 
 
+@pytest.mark.parametrize("n", [1 << 20, 1 << 22])
+def test_sum_i32_screen_limits(ctx, n):
+    """Constant inputs at the edge of the whole-input screen (n * largest and n * smallest within
+    int32: no prefix can overflow): just inside it the total is returned with no overflow; one step
+    outside the exact lane check decides, and the BCL rule then throws on the lane totals' sum.
+    n = 2^20 runs the one-launch form (which screens), 2^22 the two-launch form (exact lane check
+    only)."""
+    lim = (2**31 - 1) // n
+    for v in (lim, lim + 1, -(lim + 1), -(lim + 2)):
+        x = np.full(n, v, np.int32)
+        total, ovf = gpu_sum_i32(ctx, x)
+        assert total == v * n
+        assert ovf == bcl_overflows(x), (n, v)
+        assert ovf == (0 if -2**31 <= v * n <= 2**31 - 1 else 1)
+
+
 def test_sum_misaligned_inputs(ctx):
     """Inputs that start 1-3 elements past a 16-byte boundary run the vector path on the aligned
     part (no single-workgroup fallback): same results as the aligned input."""
