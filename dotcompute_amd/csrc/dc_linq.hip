@@ -1323,13 +1323,21 @@ __device__ __attribute__((always_inline)) inline int64_t visit_chunk(const dc_li
 }
 
 // Where/Select -> Sum / Count: float64 sum and kept count per workgroup.
-template <int RD>
+// ONE (gridDim.x <= kSumBlock): the one-launch form. Every workgroup publishes its partials with
+// agent-scope stores (written through its XCD's L2), waits for them to complete and takes a
+// ticket; the workgroup with the last ticket adds the partials exactly as pass 2 does (its thread
+// t holds 0 + partial t; the waves past the partials add +0 to pass 2's in-order sum of the wave
+// totals), so both forms return the same bits. No fences: nothing else crosses workgroups.
+template <int RD, bool ONE>
 __global__ __launch_bounds__(kSumBlock) void where_select_sum_pass1(const dc_linq_chain prog, const AffineChain aff,
                                                                     const RdConst canon, const float* __restrict__ in,
                                                                     int64_t n, int64_t h, double* __restrict__ psum,
-                                                                    int64_t* __restrict__ pcnt) {
+                                                                    int64_t* __restrict__ pcnt, uint32_t* __restrict__ done,
+                                                                    double* __restrict__ sum_out,
+                                                                    int64_t* __restrict__ count_out) {
   __shared__ double lds_d[kSumBlock / dc::kWave];
   __shared__ int64_t lds_i[kSumBlock / dc::kWave];
+  __shared__ uint32_t s_last;
   // A dropped element adds +0.0, which leaves the float64 total unchanged (it starts at +0.0 and a
   // sum of +0.0 and -0.0 is +0.0), so the selection happens in float before the widening.
   double acc = 0.0;
@@ -1343,9 +1351,33 @@ __global__ __launch_bounds__(kSumBlock) void where_select_sum_pass1(const dc_lin
       add, add);
   const double bsum = dc::block_sum64<kSumBlock>(acc, lds_d);
   const int64_t bcnt = dc::block_sum64<kSumBlock>(cnt, lds_i);
-  if (threadIdx.x == 0) {
-    psum[blockIdx.x] = bsum;
-    pcnt[blockIdx.x] = bcnt;
+  if constexpr (!ONE) {
+    if (threadIdx.x == 0) {
+      psum[blockIdx.x] = bsum;
+      pcnt[blockIdx.x] = bcnt;
+    }
+  } else {
+    if (threadIdx.x == 0) {
+      dc::store_agent_u64(reinterpret_cast<uint64_t*>(psum) + blockIdx.x, (uint64_t)__double_as_longlong(bsum));
+      dc::store_agent_u64(reinterpret_cast<uint64_t*>(pcnt) + blockIdx.x, (uint64_t)bcnt);
+      dc::wait_memory_ops();
+      s_last = dc::fetch_add_relaxed_agent_u32(done, 1u) == gridDim.x - 1 ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    double a = 0.0;
+    int64_t c = 0;
+    if (threadIdx.x < gridDim.x) {
+      a += __longlong_as_double((long long)dc::load_agent_u64(reinterpret_cast<const uint64_t*>(psum) + threadIdx.x));
+      c += (int64_t)dc::load_agent_u64(reinterpret_cast<const uint64_t*>(pcnt) + threadIdx.x);
+    }
+    const double total = dc::block_sum64<kSumBlock>(a, lds_d);
+    const int64_t total_cnt = dc::block_sum64<kSumBlock>(c, lds_i);
+    if (threadIdx.x == 0) {
+      if (sum_out) *sum_out = total;
+      if (count_out) *count_out = total_cnt;
+      dc::store_agent_u32(done, 0u);
+    }
   }
 }
 
@@ -1371,14 +1403,24 @@ __global__ __launch_bounds__(kFinalBlock) void where_select_sum_pass2(const doub
   }
 }
 
-// Launches the two passes of Where/Select -> Sum with the partials in psum/pcnt (grid entries each).
+// Launches Where/Select -> Sum with the partials in psum/pcnt (grid entries each): one launch up
+// to kSumOneLaunchMax elements, else pass 1 and pass 2.
+constexpr int64_t kSumOneLaunchMax = (int64_t)1 << 21;
 int32_t launch_where_select_sum(dc_hip_ctx* ctx, const dc_linq_chain* chain, const float* input, int64_t n,
                                 unsigned grid, double* psum, int64_t* pcnt, double* sum_out, int64_t* count_out) {
   const ReducePlan p = reduce_plan(*chain);
   const int64_t h = reduce_head(input, n);
+  uint32_t* done = ctx->counters + DC_SLOT_REDUCE_DONE;
+  if (n <= kSumOneLaunchMax && grid <= (unsigned)kSumBlock) {
+    rd_dispatch(p.mode, [&](auto mode) {
+      where_select_sum_pass1<decltype(mode)::value, true>
+          <<<grid, kSumBlock, 0, ctx->stream>>>(*chain, p.aff, p.k, input, n, h, psum, pcnt, done, sum_out, count_out);
+    });
+    return dc::last_launch_status();
+  }
   rd_dispatch(p.mode, [&](auto mode) {
-    where_select_sum_pass1<decltype(mode)::value>
-        <<<grid, kSumBlock, 0, ctx->stream>>>(*chain, p.aff, p.k, input, n, h, psum, pcnt);
+    where_select_sum_pass1<decltype(mode)::value, false>
+        <<<grid, kSumBlock, 0, ctx->stream>>>(*chain, p.aff, p.k, input, n, h, psum, pcnt, nullptr, nullptr, nullptr);
   });
   where_select_sum_pass2<<<1, kFinalBlock, 0, ctx->stream>>>(psum, pcnt, (int)grid, sum_out, count_out);
   return dc::last_launch_status();
