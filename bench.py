@@ -66,21 +66,27 @@ def time_launches(ctx, fn, iters: int, warm_ms: float = 0.0) -> float:
     return ms
 
 
-def measured_traffic(profile: str, leg: str | None = None):
-    """HBM bytes per launch that rocprofv3's FETCH_SIZE / WRITE_SIZE counters measured for a kernel
-    (calibrated against a copy of known size), from the `traffic_bytes_per_launch:` line (or
-    `traffic_bytes_per_launch[<leg>]:` for a summary covering several legs) of its summary under
-    profiles/; None when there is no such summary."""
+def profiled_value(profile: str, name: str, leg: str | None = None):
+    """The `<name>:` line (or `<name>[<leg>]:` for a summary covering several legs) of a rocprofv3
+    summary under profiles/, as a number; None when there is no such line."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", profile)
-    key = "traffic_bytes_per_launch" + (f"[{leg}]" if leg else "") + ":"
+    key = name + (f"[{leg}]" if leg else "") + ":"
     try:
         with open(path) as f:
             for line in f:
                 if line.startswith(key):
-                    return int(line.split(":", 1)[1])
-    except OSError:
+                    v = float(line.split(":", 1)[1])
+                    return int(v) if v.is_integer() else v
+    except (OSError, ValueError):
         pass
     return None
+
+
+def measured_traffic(profile: str, leg: str | None = None):
+    """HBM bytes per launch that rocprofv3's FETCH_SIZE / WRITE_SIZE counters measured for a kernel
+    (calibrated against a copy of known size), from the `traffic_bytes_per_launch:` line of its
+    summary under profiles/; None when there is no such summary."""
+    return profiled_value(profile, "traffic_bytes_per_launch", leg)
 
 
 def roofline(bound: str, achieved: float, peak: float, unit: str, traffic=None) -> dict:
@@ -158,6 +164,18 @@ def main() -> int:
         for leg in ("gemm_f32_8192", "gemm_bf16_8192"):
             if leg in extra:
                 extra[leg]["roofline"]["traffic"] = measured_traffic("gemm_f32_bf16_8192.md", leg)
+        # The bf16 GEMM runs at a power-limited shader clock: the matrix-core peak at the clock the
+        # counters measured under this kernel (GRBM_GUI_ACTIVE per XCD over the launch) bounds it.
+        leg = extra.get("gemm_bf16_8192")
+        clk = profiled_value("gemm_f32_bf16_8192.md", "shader_clock_GHz", "gemm_bf16_8192")
+        if leg and clk:
+            peak_at_clk = BF16_MFMA_PEAK_TFLOPS * clk / 2.4
+            leg["roofline"]["ceiling"] = {
+                "shader_clock_GHz": clk, "nominal_clock_GHz": 2.4,
+                "clock_limited_peak_TFLOP/s": round(peak_at_clk, 1),
+                "frac_of_clock_limited": round(leg["TFLOP/s"] / peak_at_clk, 4),
+                "mfma_busy": profiled_value("gemm_f32_bf16_8192.md", "mfma_busy", "gemm_bf16_8192"),
+                "source": "profiles/gemm_f32_bf16_8192.md (rocprofv3 --pmc)"}
     # ---------------- CSR SpMV x20 ---------------------------------------------------------------
     if want("spmv"):
         from bench_extras import bench_spmv  # noqa: E402
