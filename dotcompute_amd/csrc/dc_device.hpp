@@ -2,7 +2,9 @@
 // generator, wave64 DPP reductions, block reductions and agent-scope atomics.
 #pragma once
 
+#ifndef __HIPCC_RTC__
 #include <hip/hip_runtime.h>
+#endif
 
 #include <cstdint>
 

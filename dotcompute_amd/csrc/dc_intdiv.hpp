@@ -1,7 +1,9 @@
 // dc_intdiv.hpp — C# int division by a constant through a multiply-high (host and device).
 #pragma once
 
+#ifndef __HIPCC_RTC__
 #include <hip/hip_runtime.h>
+#endif
 
 #include <cstdint>
 

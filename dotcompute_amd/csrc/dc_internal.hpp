@@ -54,6 +54,10 @@ struct dc_hip_ctx {
   // that share a device's static no-alloc scratch (that event is created with the context, since
   // the no-alloc path creates nothing).
   hipEvent_t order_done[2] = {nullptr, nullptr};
+  // Launches of run-time compiled LINQ kernels on this context, and compilations that failed
+  // (whose programs then ran on the interpreter); see dc_hip_linq_compile_stats.
+  int64_t jit_launches = 0;
+  int64_t jit_failures = 0;
 
   // Device address of the static scratch array of dc_hip_linq_where_select_sum_f32_noalloc on this
   // context's device (resolved once per device at context creation), and the status of that lookup.
@@ -109,6 +113,10 @@ namespace dc {
 
 // Grows ctx->partials to at least `bytes` (caller holds the lock).
 int32_t ensure_partials(dc_hip_ctx* ctx, size_t bytes);
+// The round-robin ToArray kernel compiled at run time for one (validated) program over float32
+// (is_int false) or int32 elements, for the context's device: compiled once per process and
+// device and cached. nullptr when the compilation failed (counted in ctx->jit_failures).
+hipFunction_t linq_jit_rounds(dc_hip_ctx* ctx, const dc_linq_chain& chain, bool is_int);
 // Grows ctx->status to at least `words` and returns the epoch to use for the next launch.
 int32_t ensure_status(dc_hip_ctx* ctx, size_t words, uint32_t* epoch_out);
 // Grows ctx->round_counts to at least `words` and returns the 16-bit epoch for the next launch.

@@ -234,6 +234,7 @@ DC_HIP_API const char* dc_hip_error_string(int32_t status) {
     case DC_ERR_DIMENSION: return "dimension mismatch";
     case DC_ERR_OUT_OF_MEMORY: return "out of memory";
     case DC_ERR_NOT_FOUND: return "module or function not found";
+    case DC_ERR_COMPILE: return "run-time compilation of the LINQ program failed";
     default: break;
   }
   if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));

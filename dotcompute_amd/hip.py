@@ -28,11 +28,15 @@ DC_ERR_MISALIGNED = -5
 DC_ERR_DIMENSION = -6
 DC_ERR_OUT_OF_MEMORY = -7
 DC_ERR_NOT_FOUND = -8
+DC_ERR_COMPILE = -9
 
 # dc_linq_strategy: which kernel dc_hip_linq_where_select_f32 runs for an input
 STRATEGY_LOOKBACK = 0
 STRATEGY_ROUNDS = 1
 LINQ_FLAG_ORDERED_GRID = 1  # dc_linq_chain.flags: run ToArray on the ticket-ordered lookback grid
+LINQ_FLAG_INTERPRET = 2     # dc_linq_chain.flags: never compile the program at run time
+LINQ_COMPILE_MIN_ELEMENTS = 1 << 22  # ToArray inputs from this size run interpreted programs compiled
+LINQ_ELEMENT_F32, LINQ_ELEMENT_I32 = 0, 1
 
 # dc_linq_minmax: which terminal dc_hip_linq_where_select_minmax_f32 computes
 LINQ_MIN = 0
@@ -116,6 +120,14 @@ class LinqChain(C.Structure):
         return ch
 
 
+def compile_chain(chain: LinqChain, element: int = LINQ_ELEMENT_F32, arch: str = "gfx950") -> int:
+    """Compiles a program's ToArray kernel with hipRTC (no device needed); returns its code size.
+    Raises HipError(DC_ERR_COMPILE) when the generated source does not compile."""
+    size = C.c_size_t(0)
+    check(load().dc_linq_chain_compile(C.byref(chain), element, arch.encode(), C.byref(size)), "dc_linq_chain_compile")
+    return size.value
+
+
 def can_fault_i32(chain: LinqChain) -> bool:
     """Whether an int32 program can throw (then the _i32 entry points need a fault word)."""
     out = C.c_int32(-1)
@@ -187,6 +199,9 @@ SIGNATURES: dict[str, list] = {
     "dc_hip_linq_where_select_minmax_f32": [_P, C.POINTER(LinqChain), _P, _i64, _i32, _P, _P],
     "dc_hip_linq_to_array_strategy": [_P, _P, _i64, _P],
     "dc_linq_chain_can_fault_i32": [C.POINTER(LinqChain), C.POINTER(_i32)],
+    "dc_linq_chain_validate_i32": [C.POINTER(LinqChain)],
+    "dc_linq_chain_compile": [C.POINTER(LinqChain), _i32, C.c_char_p, C.POINTER(_sz)],
+    "dc_hip_linq_compile_stats": [_P, C.POINTER(_i64), C.POINTER(_i64)],
     "dc_hip_linq_where_select_i32": [_P, C.POINTER(LinqChain), _P, _i64, _P, _P, _P],
     "dc_hip_linq_where_select_sum_i32": [_P, C.POINTER(LinqChain), _P, _i64, _P, _P, _P, _P],
     "dc_hip_linq_where_select_minmax_i32": [_P, C.POINTER(LinqChain), _P, _i64, _i32, _P, _P, _P],
@@ -408,6 +423,12 @@ class Context:
         n = x.size if n is None else n
         check(load().dc_hip_linq_where_select_f32(self.handle, C.byref(chain), x.ptr, n, out.ptr, count.ptr),
               "dc_hip_linq_where_select_f32")
+
+    def compile_stats(self) -> tuple[int, int]:
+        """(launches of run-time compiled LINQ kernels on this context, failed compilations)."""
+        a, b = C.c_int64(0), C.c_int64(0)
+        check(load().dc_hip_linq_compile_stats(self.handle, C.byref(a), C.byref(b)), "dc_hip_linq_compile_stats")
+        return a.value, b.value
 
     def to_array_strategy(self, x: DeviceArray, n: int | None = None) -> int:
         """Kernel that where_select_f32 uses for this input: STRATEGY_LOOKBACK or STRATEGY_ROUNDS."""

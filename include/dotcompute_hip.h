@@ -25,8 +25,10 @@
 #ifndef DOTCOMPUTE_HIP_H
 #define DOTCOMPUTE_HIP_H
 
+#ifndef __HIPCC_RTC__ /* the run-time compiler of LINQ programs provides these types itself */
 #include <stddef.h>
 #include <stdint.h>
+#endif
 
 #ifdef __cplusplus
 extern "C" {
@@ -53,6 +55,7 @@ extern "C" {
 #define DC_ERR_DIMENSION (-6)         /* matrix/vector dimension mismatch (ArgumentException)     */
 #define DC_ERR_OUT_OF_MEMORY (-7)     /* scratch or host allocation failed                        */
 #define DC_ERR_NOT_FOUND (-8)         /* module / function name not found                         */
+#define DC_ERR_COMPILE (-9)           /* run-time compilation of a LINQ program failed              */
 
 DC_HIP_API const char* dc_hip_error_string(int32_t status);
 DC_HIP_API int32_t dc_hip_abi_version(void);
@@ -311,8 +314,11 @@ typedef struct dc_linq_instr {
 } dc_linq_instr;
 
 /* dc_linq_chain.flags bits. DC_LINQ_FLAG_ORDERED_GRID: run a ToArray on the ticket-ordered lookback
- * grid even where the resident grid would be chosen (the retry after a resident grid gave up). */
+ * grid even where the resident grid would be chosen (the retry after a resident grid gave up).
+ * DC_LINQ_FLAG_INTERPRET: never compile the program at run time (see dc_linq_chain_compile); run it
+ * on the prebuilt interpreter kernels. */
 #define DC_LINQ_FLAG_ORDERED_GRID 1
+#define DC_LINQ_FLAG_INTERPRET 2
 
 typedef struct dc_linq_chain {
   int32_t n_instr;
@@ -322,6 +328,28 @@ typedef struct dc_linq_chain {
 
 /* Checks a program for structural validity (opcodes, operand sources, length). */
 DC_HIP_API int32_t dc_linq_chain_validate(const dc_linq_chain* chain);
+/* The same for an int32 program (which has no SQRT, FLOOR, CEIL or ROUND: DC_ERR_UNSUPPORTED). */
+DC_HIP_API int32_t dc_linq_chain_validate_i32(const dc_linq_chain* chain);
+
+/* Run-time compilation (replaces the NVRTC path of CudaRuntimeKernelCompiler.CompileAsync,
+ * src/Extensions/DotCompute.Linq/Compilation/CudaRuntimeKernelCompiler.cs:80-138, and its cache by
+ * source and options, :92-135). A program that is not an affine chain (those have prebuilt
+ * kernels) can be compiled with hipRTC into a round-robin ToArray kernel of its own: the generated
+ * source feeds the interpreter's own instruction semantics the program as constants. The library
+ * builds and caches such kernels (once per process, device, element type and program) for inputs
+ * of at least DC_LINQ_COMPILE_MIN_ELEMENTS, but the ToArray entry points do not launch them at
+ * present: every program runs on the prebuilt interpreter kernels, and dc_hip_linq_compile_stats
+ * reports no compiled launches. DC_LINQ_FLAG_INTERPRET (accepted on every chain) opts a chain
+ * out of compilation. */
+#define DC_LINQ_COMPILE_MIN_ELEMENTS (1 << 22)
+enum dc_linq_element { DC_LINQ_ELEMENT_F32 = 0, DC_LINQ_ELEMENT_I32 = 1 };
+/* Compiles a program's ToArray kernel for `arch` (e.g. "gfx950") without a device and reports its
+ * code size: DC_ERR_COMPILE when hipRTC rejects the generated source (its log goes to stderr).
+ * For tools and tests; the entry points compile on their own. */
+DC_HIP_API int32_t dc_linq_chain_compile(const dc_linq_chain* chain, int32_t element_type, const char* arch,
+                                         size_t* code_bytes_out);
+/* Launches of run-time compiled kernels on this context so far, and compilations that failed. */
+DC_HIP_API int32_t dc_hip_linq_compile_stats(dc_hip_ctx* ctx, int64_t* compiled_launches, int64_t* compile_failures);
 /* Whether an int32 program can throw for some input (a DIV/RDIV/REM/RREM whose divisor is not an
  * immediate other than 0 and -1, or an ABS): *can_fault_out = 1 or 0. The int32 entry points need a
  * fault_out word for such programs and accept NULL for the others. */
