@@ -290,6 +290,51 @@ def test_int_division_truncates_and_throws_like_csharp():
     assert (-8) // 7 == -2 and int(np.fmod(np.int32(-8), np.int32(7))) == -1
 
 
+def test_float_remainder_and_rounding_closed_forms():
+    """C#'s float % is the truncated remainder (C fmodf, exact); MathF.Floor/Ceiling; MathF.Round
+    rounds half to even. The interpreter's REM/RREM/FLOOR/CEIL/ROUND against numpy's fmod, floor,
+    ceil and rint, bit for bit, over ties, signed zeros, infinities and NaN."""
+    from dotcompute_amd.hip import CEIL, FLOOR, LOAD, MAP, REM, ROUND, RREM, SRC_ELEM, SRC_IMM
+    x = np.array([0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 0.0, -0.0, 3.75, -3.75, 1e-40, -7.0, 123456.5,
+                  np.inf, -np.inf, np.nan, 0.7499999, -0.75], np.float32)
+    x = np.concatenate([x, oracle.gen_uniform_f32(4096, 33, 0) * 50])
+
+    def run(code):
+        return np.array([oracle.linq_eval(_chain(code + [(MAP, SRC_IMM, 0)]), float(v))[1] for v in x], np.float32)
+
+    with np.errstate(invalid="ignore", divide="ignore"):
+        cases = [([(LOAD, SRC_ELEM, 0), (REM, SRC_IMM, 0.75)], np.fmod(x, np.float32(0.75))),
+                 ([(LOAD, SRC_ELEM, 0), (RREM, SRC_IMM, 9.0)], np.fmod(np.float32(9.0), x)),
+                 ([(LOAD, SRC_ELEM, 0), (FLOOR, SRC_IMM, 0)], np.floor(x)),
+                 ([(LOAD, SRC_ELEM, 0), (CEIL, SRC_IMM, 0)], np.ceil(x)),
+                 ([(LOAD, SRC_ELEM, 0), (ROUND, SRC_IMM, 0)], np.rint(x))]
+    for code, want in cases:
+        got = run(code)
+        same = (got.view(np.uint32) == want.astype(np.float32).view(np.uint32)) | (np.isnan(got) & np.isnan(want))
+        assert same.all(), (code, x[~same][:4], got[~same][:4], want[~same][:4])
+    assert run([(LOAD, SRC_ELEM, 0), (ROUND, SRC_IMM, 0)])[:6].tolist() == [0.0, 2.0, 2.0, -0.0, -2.0, -2.0]
+
+
+def test_int_min_max_against_numpy():
+    """Where/Select then Min/Max over int32: the extreme of the elements ToArray returns, the kept
+    count, no value for an empty result, and the first exception when one is thrown."""
+    from dotcompute_amd.hip import CMP_GT, FILTER, LOAD, MAP, MUL, RDIV, SRC_ELEM, SRC_IMM
+    x = oracle.gen_uniform_i32(100_000, 62, 1, -2_000_000_000, 2_000_000_000)
+    prog = _ichain([(LOAD, SRC_ELEM, 0), (CMP_GT, SRC_IMM, -5), (FILTER, SRC_IMM, 0),
+                    (LOAD, SRC_ELEM, 0), (MUL, SRC_IMM, 3), (MAP, SRC_IMM, 0)])
+    kept, fault = oracle.linq_where_select_i32(prog, x)
+    assert fault == -1 and kept.size > 0
+    assert kept.tolist() == ((x[x > -5].astype(np.int64) * 3 + 2**31) % 2**32 - 2**31).tolist()
+    for op, ref in (("min", int(kept.min())), ("max", int(kept.max()))):
+        v, k, f = oracle.linq_where_select_minmax_i32(prog, x, op)
+        assert (v, k, f) == (ref, kept.size, -1)
+    none = _ichain([(LOAD, SRC_ELEM, 0), (CMP_GT, SRC_IMM, 2**31 - 1), (FILTER, SRC_IMM, 0)])
+    assert oracle.linq_where_select_minmax_i32(none, x, "max")[1:] == (0, -1)
+    inv = _ichain([(LOAD, SRC_ELEM, 0), (RDIV, SRC_IMM, 7), (MAP, SRC_IMM, 0)])
+    z = np.array([3, 5, 0, 9, 0], np.int32)
+    assert oracle.linq_where_select_minmax_i32(inv, z, "min")[2] == 4 * 2 + 1  # DivideByZero at index 2
+
+
 def test_planted_mistake_is_caught():
     """The bit comparison the GPU tests use must reject an off-by-one-ulp or reordered result."""
     a = oracle.gen_uniform_f32(10_000, 3, 0)
