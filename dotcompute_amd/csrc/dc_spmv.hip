@@ -69,11 +69,25 @@ __global__ __launch_bounds__(kBlock) void spmv_classify(const int32_t* __restric
   }
 }
 
+// Element arithmetic of SparseOps.SpMV<T> (SparseMatrix.cs:669-692) for T = float, double or int:
+// one rounding per product and per addition for the floating types; for int, C#'s unchecked
+// wrapping multiply and add (so a long row's fixed-order tree gives the same bits as the
+// sequential sum).
+template <typename T>
+__device__ inline T spmv_mul(T a, T b) { return a * b; }
+template <typename T>
+__device__ inline T spmv_add(T a, T b) { return a + b; }
+template <>
+__device__ inline int32_t spmv_mul(int32_t a, int32_t b) { return (int32_t)((uint32_t)a * (uint32_t)b); }
+template <>
+__device__ inline int32_t spmv_add(int32_t a, int32_t b) { return (int32_t)((uint32_t)a + (uint32_t)b); }
+
+template <typename T>
 __global__ __launch_bounds__(kBlock) void spmv_windows_kernel(const int32_t* __restrict__ rp, const int32_t* __restrict__ col,
-                                                              const float* __restrict__ val, const float* __restrict__ x,
-                                                              float* __restrict__ y,
+                                                              const T* __restrict__ val, const T* __restrict__ x,
+                                                              T* __restrict__ y,
                                                               const int32_t* __restrict__ row_start) {
-  __shared__ float s_prod[kWindow + kLongRow];
+  __shared__ T s_prod[kWindow + kLongRow];
   const int32_t r0 = row_start[blockIdx.x], r1 = row_start[blockIdx.x + 1];
   if (r0 >= r1) return;  // uniform across the workgroup: no row starts in this window
   const int32_t b = rp[r0];
@@ -86,75 +100,76 @@ __global__ __launch_bounds__(kBlock) void spmv_windows_kernel(const int32_t* __r
   // (non-temporal); x is what the caches are for.
   constexpr int kSlots = (kWindow + kLongRow) / kBlock;
   int32_t c[kSlots];
-  float v[kSlots];
+  T v[kSlots];
 #pragma unroll
   for (int k = 0; k < kSlots; ++k) {
     const int32_t i = b + (int32_t)threadIdx.x + k * kBlock;
     c[k] = 0;
-    v[k] = 0.0f;
+    v[k] = T(0);
     if (i < e) {
       c[k] = __builtin_nontemporal_load(col + i);
       v[k] = __builtin_nontemporal_load(val + i);
     }
   }
-  float xv[kSlots];  // every gather in flight before the first product is stored (c = 0 past e)
+  T xv[kSlots];  // every gather in flight before the first product is stored (c = 0 past e)
 #pragma unroll
   for (int k = 0; k < kSlots; ++k) xv[k] = x[c[k]];
 #pragma unroll
   for (int k = 0; k < kSlots; ++k) {
     const int32_t i = b + (int32_t)threadIdx.x + k * kBlock;
-    if (i < e) s_prod[i - b] = v[k] * xv[k];
+    if (i < e) s_prod[i - b] = spmv_mul(v[k], xv[k]);
   }
   __syncthreads();
   for (int32_t r = r0 + (int32_t)threadIdx.x; r < r1; r += kBlock) {
     const int32_t rb = rp[r], re = rp[r + 1];
     if (re - rb > kLongRow) continue;
-    float sum = 0.0f;
+    T sum = T(0);
     const int32_t i0 = max(rb - b, 0), i1 = min(re - b, e - b);
-    for (int32_t i = i0; i < i1; ++i) sum += s_prod[i];
+    for (int32_t i = i0; i < i1; ++i) sum = spmv_add(sum, s_prod[i]);
     __builtin_nontemporal_store(sum, y + r);
   }
 }
 
+template <typename T>
 __global__ __launch_bounds__(kLongBlock) void spmv_long_rows(const int32_t* __restrict__ rp, const int32_t* __restrict__ col,
-                                                             const float* __restrict__ val, const float* __restrict__ x,
-                                                             float* __restrict__ y, const int32_t* __restrict__ list,
+                                                             const T* __restrict__ val, const T* __restrict__ x,
+                                                             T* __restrict__ y, const int32_t* __restrict__ list,
                                                              const uint32_t* __restrict__ count) {
-  __shared__ float lds[kLongBlock / dc::kWave];
+  __shared__ T lds[kLongBlock / dc::kWave];
   const uint32_t n_long = *count;
   for (uint32_t t = blockIdx.x; t < n_long; t += gridDim.x) {
     const int32_t row = list[t];
     const int32_t b = rp[row], e = rp[row + 1];
-    float sum = 0.0f;
+    T sum = T(0);
     // Four slots per pass: their loads and gathers are independent and overlap.
     for (int32_t i0 = b + (int32_t)threadIdx.x; i0 < e; i0 += 4 * kLongBlock) {
       int32_t c[4];
-      float v[4];
+      T v[4];
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int32_t i = i0 + k * kLongBlock;
         c[k] = 0;
-        v[k] = 0.0f;
+        v[k] = T(0);
         if (i < e) {
           c[k] = __builtin_nontemporal_load(col + i);
           v[k] = __builtin_nontemporal_load(val + i);
         }
       }
-      float xv[4], p[4];
+      T xv[4], p[4];
 #pragma unroll
       for (int k = 0; k < 4; ++k) xv[k] = x[c[k]];  // c = 0 past e: gathered, then dropped below
 #pragma unroll
-      for (int k = 0; k < 4; ++k) p[k] = (i0 + k * kLongBlock < e) ? v[k] * xv[k] : 0.0f;
-      sum += (p[0] + p[1]) + (p[2] + p[3]);
+      for (int k = 0; k < 4; ++k) p[k] = (i0 + k * kLongBlock < e) ? spmv_mul(v[k], xv[k]) : T(0);
+      sum = spmv_add(sum, spmv_add(spmv_add(p[0], p[1]), spmv_add(p[2], p[3])));
     }
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    for (int off = 32; off > 0; off >>= 1) sum = spmv_add(sum, __shfl_xor(sum, off, 64));
     if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = sum;
     __syncthreads();
     if (threadIdx.x == 0) {
-      float total = lds[0];
+      T total = lds[0];
 #pragma unroll
-      for (int w = 1; w < kLongBlock / dc::kWave; ++w) total += lds[w];
+      for (int w = 1; w < kLongBlock / dc::kWave; ++w) total = spmv_add(total, lds[w]);
       y[row] = total;
     }
     __syncthreads();
@@ -196,17 +211,18 @@ int32_t launch_analysis(dc_hip_ctx* ctx, const SpmvPlan& plan, const int32_t* rp
   return dc::last_launch_status();
 }
 
-int32_t launch_spmv(dc_hip_ctx* ctx, const SpmvPlan& plan, const int32_t* rp, const int32_t* col, const float* val,
-                    const float* x, float* y) {
-  spmv_windows_kernel<<<(unsigned)plan.windows, kBlock, 0, ctx->stream>>>(rp, col, val, x, y, ctx->spmv_windows);
+template <typename T>
+int32_t launch_spmv(dc_hip_ctx* ctx, const SpmvPlan& plan, const int32_t* rp, const int32_t* col, const T* val,
+                    const T* x, T* y) {
+  spmv_windows_kernel<T><<<(unsigned)plan.windows, kBlock, 0, ctx->stream>>>(rp, col, val, x, y, ctx->spmv_windows);
   DC_RETURN_IF(dc::last_launch_status());
   const unsigned lgrid = (unsigned)std::max<size_t>(1, std::min<size_t>(plan.list_cap, 2048));
-  spmv_long_rows<<<lgrid, kLongBlock, 0, ctx->stream>>>(rp, col, val, x, y, ctx->spmv_rows,
+  spmv_long_rows<T><<<lgrid, kLongBlock, 0, ctx->stream>>>(rp, col, val, x, y, ctx->spmv_rows,
                                                         ctx->counters + DC_SLOT_SPMV_LONG);
   return dc::last_launch_status();
 }
 
-int32_t check_csr(const int32_t* rp, const int32_t* col, const float* val, int64_t rows, int64_t nnz) {
+int32_t check_csr(const int32_t* rp, const int32_t* col, const void* val, int64_t rows, int64_t nnz) {
   if (rows < 0 || nnz < 0 || nnz > INT32_MAX - 2 * kWindow || rows >= INT32_MAX) return DC_ERR_INVALID_ARGUMENT;
   if (!rp || (nnz > 0 && (!col || !val))) return DC_ERR_INVALID_ARGUMENT;
   return DC_OK;
@@ -1021,6 +1037,19 @@ int32_t plan_power_iterate(dc_hip_ctx* ctx, const dc_hip_spmv_plan* p, float* x,
   return DC_OK;
 }
 
+// One-shot y = A·x for any element type (the entry points dc_hip_spmv_csr_f32/_f64/_i32).
+template <typename T>
+int32_t spmv_csr(dc_hip_ctx* ctx, const int32_t* row_pointers, const int32_t* col_indices, const T* values, const T* x,
+                 T* y, int64_t rows, int64_t cols, int64_t nnz) {
+  DC_RETURN_IF(check_csr(row_pointers, col_indices, values, rows, nnz));
+  if (cols < 0 || (rows > 0 && !y) || (cols > 0 && !x)) return DC_ERR_INVALID_ARGUMENT;
+  DC_CTX_ENTER(ctx);
+  if (rows == 0) return DC_OK;
+  const SpmvPlan plan = make_plan(nnz);
+  DC_RETURN_IF(launch_analysis(ctx, plan, row_pointers, rows));
+  return launch_spmv(ctx, plan, row_pointers, col_indices, values, x, y);
+}
+
 int32_t check_plan_shape(int64_t rows, int64_t cols, int64_t nnz) {
   if (cols < 0 || (nnz > 0 && cols == 0)) return DC_ERR_INVALID_ARGUMENT;
   if (cols > (int64_t{1} << 30) - 1) return DC_ERR_UNSUPPORTED;  // x is addressed with 32-bit byte offsets
@@ -1035,13 +1064,19 @@ extern "C" {
 DC_HIP_API int32_t dc_hip_spmv_csr_f32(dc_hip_ctx* ctx, const int32_t* row_pointers, const int32_t* col_indices,
                                        const float* values, const float* x, float* y, int64_t rows, int64_t cols,
                                        int64_t nnz) {
-  DC_RETURN_IF(check_csr(row_pointers, col_indices, values, rows, nnz));
-  if (cols < 0 || (rows > 0 && !y) || (cols > 0 && !x)) return DC_ERR_INVALID_ARGUMENT;
-  DC_CTX_ENTER(ctx);
-  if (rows == 0) return DC_OK;
-  const SpmvPlan plan = make_plan(nnz);
-  DC_RETURN_IF(launch_analysis(ctx, plan, row_pointers, rows));
-  return launch_spmv(ctx, plan, row_pointers, col_indices, values, x, y);
+  return spmv_csr(ctx, row_pointers, col_indices, values, x, y, rows, cols, nnz);
+}
+
+DC_HIP_API int32_t dc_hip_spmv_csr_f64(dc_hip_ctx* ctx, const int32_t* row_pointers, const int32_t* col_indices,
+                                       const double* values, const double* x, double* y, int64_t rows, int64_t cols,
+                                       int64_t nnz) {
+  return spmv_csr(ctx, row_pointers, col_indices, values, x, y, rows, cols, nnz);
+}
+
+DC_HIP_API int32_t dc_hip_spmv_csr_i32(dc_hip_ctx* ctx, const int32_t* row_pointers, const int32_t* col_indices,
+                                       const int32_t* values, const int32_t* x, int32_t* y, int64_t rows, int64_t cols,
+                                       int64_t nnz) {
+  return spmv_csr(ctx, row_pointers, col_indices, values, x, y, rows, cols, nnz);
 }
 
 DC_HIP_API int32_t dc_hip_spmv_plan_create(dc_hip_ctx* ctx, const int32_t* row_pointers, const int32_t* col_indices,

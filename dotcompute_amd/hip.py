@@ -209,6 +209,8 @@ SIGNATURES: dict[str, list] = {
     "dc_hip_gemm_bf16": [_P, _P, _P, _P, _i64, _i64, _i64],
     "dc_hip_convert_f32_to_bf16": [_P, _P, _P, _i64],
     "dc_hip_spmv_csr_f32": [_P, _P, _P, _P, _P, _P, _i64, _i64, _i64],
+    "dc_hip_spmv_csr_f64": [_P, _P, _P, _P, _P, _P, _i64, _i64, _i64],
+    "dc_hip_spmv_csr_i32": [_P, _P, _P, _P, _P, _P, _i64, _i64, _i64],
     "dc_hip_spmv_power_iterate_f32": [_P, _P, _P, _P, _P, _P, _i64, _i64, _i32, _P],
     "dc_hip_spmv_plan_create": [_P, _P, _P, _P, _i64, _i64, _i64, _i64, _PP],
     "dc_hip_spmv_plan_execute_f32": [_P, _P, _P, _P],
@@ -493,6 +495,13 @@ class Context:
                      rows: int, cols: int, nnz: int) -> None:
         check(load().dc_hip_spmv_csr_f32(self.handle, rp.ptr, col.ptr, val.ptr, x.ptr, y.ptr, rows, cols, nnz),
               "dc_hip_spmv_csr_f32")
+
+    def spmv_csr(self, rp: DeviceArray, col: DeviceArray, val: DeviceArray, x: DeviceArray, y: DeviceArray,
+                 rows: int, cols: int, nnz: int) -> None:
+        """y = A·x for float32, float64 or int32 values (the element type of `val`)."""
+        name = {np.dtype(np.float32): "dc_hip_spmv_csr_f32", np.dtype(np.float64): "dc_hip_spmv_csr_f64",
+                np.dtype(np.int32): "dc_hip_spmv_csr_i32"}[np.dtype(val.dtype)]
+        check(getattr(load(), name)(self.handle, rp.ptr, col.ptr, val.ptr, x.ptr, y.ptr, rows, cols, nnz), name)
 
     def spmv_power_iterate_f32(self, rp, col, val, x, y, rows: int, nnz: int, iterations: int,
                                last_sum: DeviceArray | None = None) -> None:

@@ -66,8 +66,13 @@ class CsrMatrix {
 
 class SparseOps {
  public:
-  // y = A·x (SparseMatrix.cs:669-692): ArgumentException when A.Columns != x.Length.
+  // y = A·x (SparseMatrix.cs:669-692): ArgumentException when A.Columns != x.Length. The reference
+  // is generic over INumber<T>; float, double and int run on the HIP kernels (int arithmetic wraps,
+  // as C#'s unchecked default).
   static std::vector<float> SpMV(const CsrMatrix<float>& a, const std::vector<float>& x, IAccelerator& accelerator);
+  static std::vector<double> SpMV(const CsrMatrix<double>& a, const std::vector<double>& x, IAccelerator& accelerator);
+  static std::vector<int32_t> SpMV(const CsrMatrix<int32_t>& a, const std::vector<int32_t>& x,
+                                   IAccelerator& accelerator);
   // The SpMV benchmark: `iterations` times y = A·x; x = y / sum(y). Returns x (rows == columns).
   static std::vector<float> PowerIterate(const CsrMatrix<float>& a, const std::vector<float>& x0, int32_t iterations,
                                          IAccelerator& accelerator, double* lastSum = nullptr);

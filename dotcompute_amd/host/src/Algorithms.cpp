@@ -64,7 +64,8 @@ std::future<Matrix> MatrixOperations::MultiplyAsync(const Matrix& a, const Matri
 namespace {
 // The kernels index values/columns/x through the row pointers: reject a malformed CSR on the host
 // (the reference would fail with IndexOutOfRangeException inside SpMV).
-void ValidateCsr(const CsrMatrix<float>& a) {
+template <typename T>
+void ValidateCsr(const CsrMatrix<T>& a) {
   if (a.Rows < 0 || a.Columns < 0) throw ArgumentException("CSR dimensions must be non-negative");
   if (a.RowPointers.empty() || a.RowPointers[0] != 0 || (int64_t)a.RowPointers.back() != a.NonZeroCount())
     throw ArgumentException("CSR rowPointers must start at 0 and end at NNZ");
@@ -74,45 +75,73 @@ void ValidateCsr(const CsrMatrix<float>& a) {
     if (c < 0 || c >= a.Columns) throw ArgumentException("CSR column index out of range");
 }
 
+template <typename T>
 struct DeviceCsr {
   std::shared_ptr<IUnifiedMemoryBufferT<int32_t>> rp, col;
-  std::shared_ptr<IUnifiedMemoryBufferT<float>> val;
+  std::shared_ptr<IUnifiedMemoryBufferT<T>> val;
 };
 
-DeviceCsr Upload(HipAccelerator& hip, const CsrMatrix<float>& a) {
-  DeviceCsr d;
+template <typename T>
+DeviceCsr<T> Upload(HipAccelerator& hip, const CsrMatrix<T>& a) {
+  DeviceCsr<T> d;
   auto& mem = hip.Memory();
   const size_t nnz = a.Values.size();
   d.rp = mem.AllocateAsync<int32_t>(a.RowPointers.size());
   d.col = mem.AllocateAsync<int32_t>(std::max<size_t>(nnz, 1));
-  d.val = mem.AllocateAsync<float>(std::max<size_t>(nnz, 1));
+  d.val = mem.AllocateAsync<T>(std::max<size_t>(nnz, 1));
   d.rp->CopyFromHost(a.RowPointers.data(), a.RowPointers.size() * sizeof(int32_t));
   if (nnz) {
     d.col->CopyFromHost(a.ColumnIndices.data(), nnz * sizeof(int32_t));
-    d.val->CopyFromHost(a.Values.data(), nnz * sizeof(float));
+    d.val->CopyFromHost(a.Values.data(), nnz * sizeof(T));
   }
   return d;
 }
-}  // namespace
 
-std::vector<float> SparseOps::SpMV(const CsrMatrix<float>& a, const std::vector<float>& x, IAccelerator& accelerator) {
+int32_t SpmvCsr(dc_hip_ctx* ctx, const int32_t* rp, const int32_t* col, const float* val, const float* x, float* y,
+                int64_t rows, int64_t cols, int64_t nnz) {
+  return dc_hip_spmv_csr_f32(ctx, rp, col, val, x, y, rows, cols, nnz);
+}
+int32_t SpmvCsr(dc_hip_ctx* ctx, const int32_t* rp, const int32_t* col, const double* val, const double* x, double* y,
+                int64_t rows, int64_t cols, int64_t nnz) {
+  return dc_hip_spmv_csr_f64(ctx, rp, col, val, x, y, rows, cols, nnz);
+}
+int32_t SpmvCsr(dc_hip_ctx* ctx, const int32_t* rp, const int32_t* col, const int32_t* val, const int32_t* x,
+                int32_t* y, int64_t rows, int64_t cols, int64_t nnz) {
+  return dc_hip_spmv_csr_i32(ctx, rp, col, val, x, y, rows, cols, nnz);
+}
+
+template <typename T>
+std::vector<T> SpMVOn(const CsrMatrix<T>& a, const std::vector<T>& x, IAccelerator& accelerator) {
   if ((int64_t)a.Columns != (int64_t)x.size())
     throw ArgumentException("SpMV dimension mismatch: matrix A is " + std::to_string(a.Rows) + "x" +
                             std::to_string(a.Columns) + " but vector x has " + std::to_string(x.size()) +
                             " element(s). For y = A·x the number of columns in A must equal the length of x.");
   HipAccelerator& hip = RequireHip(accelerator);
   ValidateCsr(a);
-  DeviceCsr d = Upload(hip, a);
-  auto dx = hip.Memory().AllocateAsync<float>(std::max<size_t>(x.size(), 1));
-  auto dy = hip.Memory().AllocateAsync<float>(std::max<int32_t>(a.Rows, 1));
-  if (!x.empty()) dx->CopyFromHost(x.data(), x.size() * sizeof(float));
-  Check(dc_hip_spmv_csr_f32(hip.Context(), d.rp->Data(), d.col->Data(), d.val->Data(), dx->Data(), dy->Data(), a.Rows,
-                            a.Columns, a.NonZeroCount()),
-        "dc_hip_spmv_csr_f32");
+  DeviceCsr<T> d = Upload(hip, a);
+  auto dx = hip.Memory().AllocateAsync<T>(std::max<size_t>(x.size(), 1));
+  auto dy = hip.Memory().AllocateAsync<T>(std::max<int32_t>(a.Rows, 1));
+  if (!x.empty()) dx->CopyFromHost(x.data(), x.size() * sizeof(T));
+  Check(SpmvCsr(hip.Context(), d.rp->Data(), d.col->Data(), d.val->Data(), dx->Data(), dy->Data(), a.Rows, a.Columns,
+                a.NonZeroCount()),
+        "dc_hip_spmv_csr");
   hip.Synchronize();
-  std::vector<float> y((size_t)a.Rows);
-  if (!y.empty()) dy->CopyToHost(y.data(), y.size() * sizeof(float));
+  std::vector<T> y((size_t)a.Rows);
+  if (!y.empty()) dy->CopyToHost(y.data(), y.size() * sizeof(T));
   return y;
+}
+}  // namespace
+
+std::vector<float> SparseOps::SpMV(const CsrMatrix<float>& a, const std::vector<float>& x, IAccelerator& accelerator) {
+  return SpMVOn(a, x, accelerator);
+}
+std::vector<double> SparseOps::SpMV(const CsrMatrix<double>& a, const std::vector<double>& x,
+                                    IAccelerator& accelerator) {
+  return SpMVOn(a, x, accelerator);
+}
+std::vector<int32_t> SparseOps::SpMV(const CsrMatrix<int32_t>& a, const std::vector<int32_t>& x,
+                                     IAccelerator& accelerator) {
+  return SpMVOn(a, x, accelerator);
 }
 
 std::vector<float> SparseOps::PowerIterate(const CsrMatrix<float>& a, const std::vector<float>& x0, int32_t iterations,
@@ -122,7 +151,7 @@ std::vector<float> SparseOps::PowerIterate(const CsrMatrix<float>& a, const std:
   if (iterations < 0) throw ArgumentException("iterations must be non-negative");
   HipAccelerator& hip = RequireHip(accelerator);
   ValidateCsr(a);
-  DeviceCsr d = Upload(hip, a);
+  DeviceCsr<float> d = Upload(hip, a);
   auto dx = hip.Memory().AllocateAsync<float>(std::max<size_t>(x0.size(), 1));
   auto dy = hip.Memory().AllocateAsync<float>(std::max<size_t>(x0.size(), 1));
   auto ds = hip.Memory().AllocateAsync<double>(1);

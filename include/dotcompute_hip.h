@@ -468,6 +468,18 @@ DC_HIP_API int32_t dc_hip_spmv_csr_f32(dc_hip_ctx* ctx, const int32_t* row_point
                                        const int32_t* col_indices, const float* values,
                                        const float* x, float* y, int64_t rows, int64_t cols,
                                        int64_t nnz);
+/* The same for SparseOps.SpMV<double> and SpMV<int> (the reference's SpMV is generic over
+ * INumber<T>, SparseMatrix.cs:669): per row T.Zero plus each product in index order for rows of
+ * at most 512 nonzeros (bit-identical to the reference loop), a fixed-order tree for longer rows;
+ * int multiplies and adds wrap (C#'s unchecked arithmetic, so every row is bit-identical). */
+DC_HIP_API int32_t dc_hip_spmv_csr_f64(dc_hip_ctx* ctx, const int32_t* row_pointers,
+                                       const int32_t* col_indices, const double* values,
+                                       const double* x, double* y, int64_t rows, int64_t cols,
+                                       int64_t nnz);
+DC_HIP_API int32_t dc_hip_spmv_csr_i32(dc_hip_ctx* ctx, const int32_t* row_pointers,
+                                       const int32_t* col_indices, const int32_t* values,
+                                       const int32_t* x, int32_t* y, int64_t rows, int64_t cols,
+                                       int64_t nnz);
 /* Power iteration used by the SpMV benchmark: repeat `iterations` times
  *   y = A·x;  s = Σ y (float64);  x = y / s
  * leaving the normalised vector in x (rows == cols required). `y` is caller-provided scratch of

@@ -67,6 +67,8 @@ def lib() -> C.CDLL:
             "oracle_bf16_to_f32": (C.c_float, [C.c_uint16]),
             "oracle_f32_to_bf16_array": (None, [_P, _P, _i64]),
             "oracle_spmv_csr_f32": (_i32, [_P, _P, _P, _P, _P, _i64, _i64, _i64]),
+            "oracle_spmv_csr_f64d": (_i32, [_P, _P, _P, _P, _P, _i64, _i64, _i64]),
+            "oracle_spmv_csr_i32": (_i32, [_P, _P, _P, _P, _P, _i64, _i64, _i64]),
             "oracle_spmv_csr_f64": (None, [_P, _P, _P, _P, _P, _i64]),
             "oracle_spmv_power_f32": (_i32, [_P, _P, _P, _P, _P, _i64, _i32, _P]),
             "oracle_net_minf": (C.c_float, [C.c_float, C.c_float]),
@@ -322,6 +324,30 @@ def spmv_csr_f64(rp, col, val, x64) -> np.ndarray:
     rows = rp.size - 1
     y = np.empty(rows, np.float64)
     lib().oracle_spmv_csr_f64(_p(rp), _p(col), _p(val), _p(x64), _p(y), rows)
+    return y
+
+
+def spmv_csr_f64d(rp, col, val, x, cols: int | None = None) -> np.ndarray:
+    """SparseOps.SpMV<double>: float64 values and x, sequential float64 row sums."""
+    rows = rp.size - 1
+    cols = x.size if cols is None else cols
+    val = np.ascontiguousarray(val, np.float64)
+    x = np.ascontiguousarray(x, np.float64)
+    y = np.empty(rows, np.float64)
+    if lib().oracle_spmv_csr_f64d(_p(rp), _p(col), _p(val), _p(x), _p(y), rows, cols, x.size) == -6:
+        raise ValueError("SpMV dimension mismatch")
+    return y
+
+
+def spmv_csr_i32(rp, col, val, x, cols: int | None = None) -> np.ndarray:
+    """SparseOps.SpMV<int>: wrapping int32 products and sums."""
+    rows = rp.size - 1
+    cols = x.size if cols is None else cols
+    val = np.ascontiguousarray(val, np.int32)
+    x = np.ascontiguousarray(x, np.int32)
+    y = np.empty(rows, np.int32)
+    if lib().oracle_spmv_csr_i32(_p(rp), _p(col), _p(val), _p(x), _p(y), rows, cols, x.size) == -6:
+        raise ValueError("SpMV dimension mismatch")
     return y
 
 

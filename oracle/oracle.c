@@ -784,6 +784,32 @@ void oracle_spmv_csr_f64(const int32_t* row_pointers, const int32_t* col_indices
   }
 }
 
+/* SparseOps.SpMV<double> (SparseMatrix.cs:669-692 with T = double): per row 0.0 plus each
+ * product in index order. */
+int32_t oracle_spmv_csr_f64d(const int32_t* row_pointers, const int32_t* col_indices, const double* values,
+                             const double* x, double* y, int64_t rows, int64_t cols, int64_t x_len) {
+  if (cols != x_len) return DC_ERR_DIMENSION;
+  for (int64_t r = 0; r < rows; ++r) {
+    double sum = 0.0;
+    for (int32_t i = row_pointers[r]; i < row_pointers[r + 1]; ++i) sum += values[i] * x[col_indices[i]];
+    y[r] = sum;
+  }
+  return DC_OK;
+}
+
+/* SparseOps.SpMV<int>: C#'s unchecked int multiply and add wrap modulo 2^32. */
+int32_t oracle_spmv_csr_i32(const int32_t* row_pointers, const int32_t* col_indices, const int32_t* values,
+                            const int32_t* x, int32_t* y, int64_t rows, int64_t cols, int64_t x_len) {
+  if (cols != x_len) return DC_ERR_DIMENSION;
+  for (int64_t r = 0; r < rows; ++r) {
+    uint32_t sum = 0;
+    for (int32_t i = row_pointers[r]; i < row_pointers[r + 1]; ++i)
+      sum += (uint32_t)values[i] * (uint32_t)x[col_indices[i]];
+    y[r] = (int32_t)sum;
+  }
+  return DC_OK;
+}
+
 /* The SpMV benchmark's power iteration: `iterations` times y = SpMV(A, x) (as above), then the
  * L1 normalisation x = y / sum(y) with the sum in float64 and each quotient rounded to float. */
 int32_t oracle_spmv_power_f32(const int32_t* row_pointers, const int32_t* col_indices, const float* values,

@@ -104,6 +104,10 @@ int32_t oracle_spmv_csr_f32(const int32_t* row_pointers, const int32_t* col_indi
                             const float* x, float* y, int64_t rows, int64_t cols, int64_t x_len);
 void oracle_spmv_csr_f64(const int32_t* row_pointers, const int32_t* col_indices, const float* values,
                          const double* x, double* y, int64_t rows);
+int32_t oracle_spmv_csr_f64d(const int32_t* row_pointers, const int32_t* col_indices, const double* values,
+                             const double* x, double* y, int64_t rows, int64_t cols, int64_t x_len);
+int32_t oracle_spmv_csr_i32(const int32_t* row_pointers, const int32_t* col_indices, const int32_t* values,
+                            const int32_t* x, int32_t* y, int64_t rows, int64_t cols, int64_t x_len);
 int32_t oracle_spmv_power_f32(const int32_t* row_pointers, const int32_t* col_indices, const float* values,
                               float* x, float* y, int64_t rows, int32_t iterations, double* last_sum);
 

@@ -1118,4 +1118,40 @@ TEST_GPU(sparse_spmv_and_power_iteration) {
   for (int64_t r = 0; r < rows; ++r) CHECK(std::fabs(xp[r] - xo[r]) <= 1e-4 * std::fabs(xo[r]) + 1e-12);
 }
 
+TEST_GPU(sparse_spmv_double_and_int) {
+  auto acc = Gpu();
+  const int64_t rows = 50000;
+  std::vector<int32_t> rp(rows + 1);
+  int64_t nnz = oracle_gen_zipf_rowptr(rows, 2.0, 4096, 43, rp.data());
+  std::vector<int32_t> col((size_t)nnz);
+  std::vector<float> valf((size_t)nnz);
+  oracle_gen_zipf_fill(rows, rows, 43, rp.data(), col.data(), valf.data());
+  // double: rows up to 512 nonzeros are summed in index order, longer ones by a fixed tree
+  std::vector<double> vd((size_t)nnz), xd((size_t)rows), yd((size_t)rows), sd((size_t)rows);
+  for (int64_t i = 0; i < nnz; ++i) vd[(size_t)i] = (double)valf[(size_t)i] * 3.0 - 0.5;
+  for (int64_t r = 0; r < rows; ++r) xd[(size_t)r] = 1.0 / (double)(r + 3);
+  CsrMatrix<double> Ad((int32_t)rows, (int32_t)rows, vd, col, rp);
+  std::vector<double> got_d = SparseOps::SpMV(Ad, xd, *acc);
+  CHECK(oracle_spmv_csr_f64d(rp.data(), col.data(), vd.data(), xd.data(), yd.data(), rows, rows, rows) == 0);
+  std::vector<double> avd(vd.size());
+  for (size_t i = 0; i < vd.size(); ++i) avd[i] = std::fabs(vd[i]);
+  CHECK(oracle_spmv_csr_f64d(rp.data(), col.data(), avd.data(), xd.data(), sd.data(), rows, rows, rows) == 0);
+  for (int64_t r = 0; r < rows; ++r) {
+    if (rp[r + 1] - rp[r] <= 512)
+      CHECK(got_d[(size_t)r] == yd[(size_t)r]);
+    else
+      CHECK(std::fabs(got_d[(size_t)r] - yd[(size_t)r]) <= 1e-12 * sd[(size_t)r]);
+  }
+  // int: wrapping products and sums, bit-identical on every row
+  std::vector<int32_t> vi((size_t)nnz), xi((size_t)rows), yi((size_t)rows);
+  for (int64_t i = 0; i < nnz; ++i) vi[(size_t)i] = (int32_t)(0x9E3779B1u * (uint32_t)(i + 1));
+  for (int64_t r = 0; r < rows; ++r) xi[(size_t)r] = (int32_t)(r % 70001) - 35000;
+  CsrMatrix<int32_t> Ai((int32_t)rows, (int32_t)rows, vi, col, rp);
+  std::vector<int32_t> got_i = SparseOps::SpMV(Ai, xi, *acc);
+  CHECK(oracle_spmv_csr_i32(rp.data(), col.data(), vi.data(), xi.data(), yi.data(), rows, rows, rows) == 0);
+  CHECK(got_i == yi);
+  std::vector<int32_t> wrong((size_t)rows - 1);
+  CHECK_THROWS(ArgumentException, SparseOps::SpMV(Ai, wrong, *acc));
+}
+
 int main(int argc, char** argv) { return dctest_main(argc, argv); }

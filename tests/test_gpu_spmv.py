@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 
 import oracle
+from dotcompute_amd import hip
 
 pytestmark = pytest.mark.gpu
 
@@ -146,3 +147,60 @@ def test_spmv_short_rows_bit_exact_with_sequential_reference(ctx):
     short = np.diff(rp) <= 512
     assert short.sum() > 0.99 * rows
     assert np.array_equal(y[short].view(np.uint32), ref[short].view(np.uint32))
+
+
+# ---- SparseOps.SpMV<T> for T = double and int (the reference is generic over INumber<T>) ----------
+def spmv_gpu_typed(ctx, rp, col, val, x):
+    rows = rp.size - 1
+    drp, dcol = ctx.to_device(rp), ctx.to_device(col if col.size else np.zeros(1, np.int32))
+    dval = ctx.to_device(val if val.size else np.zeros(1, val.dtype))
+    dx = ctx.to_device(x)
+    dy = ctx.empty(max(rows, 1), val.dtype)
+    ctx.spmv_csr(drp, dcol, dval, dx, dy, rows, x.size, col.size)
+    ctx.synchronize()
+    y = dy.to_host(rows)
+    for a in (drp, dcol, dval, dx, dy):
+        ctx.free(a)
+    return y
+
+
+@pytest.mark.parametrize("rows", [5000, 1_000_000])
+def test_spmv_double_rows_match_sequential_reference(ctx, rows):
+    """SpMV<double>: rows of at most 512 nonzeros bit-identical to the reference loop (0.0 plus each
+    product in index order), the long rows (a fixed-order tree) within 1e-12 of it."""
+    rp, col, _ = oracle.gen_zipf_csr(rows, 61)
+    val = oracle.gen_uniform_f32(int(rp[-1]), 62, 0).astype(np.float64) * np.pi
+    x = oracle.gen_uniform_f32(rows, 63, 1).astype(np.float64) / 3.0
+    y = spmv_gpu_typed(ctx, rp, col, val, x)
+    ref = oracle.spmv_csr_f64d(rp, col, val, x)
+    deg = np.diff(rp)
+    short = deg <= 512
+    assert np.array_equal(y[short].view(np.uint64), ref[short].view(np.uint64))
+    scale = oracle.spmv_csr_f64d(rp, col, np.abs(val), np.abs(x))
+    assert np.all(np.abs(y - ref) <= 1e-12 * scale + 1e-300)
+    assert (~short).any() or rows < 1_000_000  # the 1M graph has rows past the long-row threshold
+
+
+@pytest.mark.parametrize("rows", [5000, 1_000_000])
+def test_spmv_int_wraps_like_csharp(ctx, rows):
+    """SpMV<int>: every row bit-identical to the reference loop, long rows included (wrapping adds
+    give the same bits in any order); values chosen so products and sums overflow int32."""
+    rp, col, _ = oracle.gen_zipf_csr(rows, 64)
+    val = oracle.gen_uniform_i32(int(rp[-1]), 65, 1, -2_000_000_000, 2_000_000_000)
+    x = oracle.gen_uniform_i32(rows, 66, 2, -70_000, 70_000)
+    y = spmv_gpu_typed(ctx, rp, col, val, x)
+    ref = oracle.spmv_csr_i32(rp, col, val, x)
+    assert np.array_equal(y, ref)
+
+
+def test_spmv_typed_dimension_check(ctx):
+    rp = np.array([0, 1], np.int32)
+    col = np.array([0], np.int32)
+    for dt in (np.float64, np.int32):
+        drp, dcol, dval = ctx.to_device(rp), ctx.to_device(col), ctx.to_device(np.ones(1, dt))
+        dx, dy = ctx.to_device(np.ones(1, dt)), ctx.empty(1, dt)
+        with pytest.raises(hip.HipError) as e:
+            ctx.spmv_csr(drp, dcol, dval, dx, dy, -1, 1, 1)
+        assert e.value.status == hip.DC_ERR_INVALID_ARGUMENT
+        for a in (drp, dcol, dval, dx, dy):
+            ctx.free(a)

@@ -484,6 +484,50 @@ def test_spmv_dense_bruteforce_and_power_invariants():
     assert np.allclose(xp, xd, rtol=1e-4, atol=1e-9)
 
 
+def _dense_int(rp, col, val, rows, cols):
+    dense = np.zeros((rows, cols), object)
+    for r in range(rows):
+        for i in range(rp[r], rp[r + 1]):
+            dense[r, col[i]] += int(val[i])
+    return dense
+
+
+def test_spmv_double_exact_on_integers_and_index_order():
+    """SpMV<double>: integer-valued operands below 2^20 make every product and partial sum exact, so
+    the result equals the integer dense product; a row whose order matters (1e16 + 1 - 1e16) pins
+    the index order of the additions."""
+    rows = 200
+    rp, col, _ = oracle.gen_zipf_csr(rows, 7, max_degree=rows - 1)
+    rng = np.random.default_rng(7)
+    val = rng.integers(-1000, 1000, col.size).astype(np.float64)
+    x = rng.integers(-1000, 1000, rows).astype(np.float64)
+    want = _dense_int(rp, col, val, rows, rows) @ np.array([int(v) for v in x], object)
+    assert np.array_equal(oracle.spmv_csr_f64d(rp, col, val, x), np.array(want, np.float64))
+    # row 0 in index order: 2^53 + 1 ties to 2^53 (even), + 1 again, - 2^53 = 0; the reverse order
+    # gives 2 and a pairwise tree 1. Row 2 is row 0 reversed; row 1 is empty.
+    rp2 = np.array([0, 4, 4, 8], np.int32)
+    col2 = np.array([0, 1, 2, 3, 3, 2, 1, 0], np.int32)
+    val2 = np.array([2.0**53, 1.0, 1.0, -2.0**53, -2.0**53, 1.0, 1.0, 2.0**53])
+    y = oracle.spmv_csr_f64d(rp2, col2, val2, np.ones(4))
+    assert y.tolist() == [0.0, 0.0, 2.0]
+    with pytest.raises(ValueError):
+        oracle.spmv_csr_f64d(rp2, col2, val2, np.ones(4), cols=5)
+
+
+def test_spmv_int_wraps_modulo_2_32():
+    """SpMV<int>: unchecked C# arithmetic; the dense product in Python integers reduced mod 2^32."""
+    rows = 150
+    rp, col, _ = oracle.gen_zipf_csr(rows, 8, max_degree=rows - 1)
+    val = oracle.gen_uniform_i32(col.size, 8, 1, -2_000_000_000, 2_000_000_000)
+    x = oracle.gen_uniform_i32(rows, 9, 2, -70_000, 70_000)
+    want = _dense_int(rp, col, val, rows, rows) @ np.array([int(v) for v in x], object)
+    wrapped = np.array([((int(v) + 2**31) % 2**32) - 2**31 for v in want], np.int64).astype(np.int32)
+    got = oracle.spmv_csr_i32(rp, col, val, x)
+    assert np.array_equal(got, wrapped)
+    assert any(abs(int(v)) >= 2**31 for v in want)  # the case does overflow
+    assert got[np.diff(rp) == 0].tolist() == [0] * int(np.sum(np.diff(rp) == 0))
+
+
 # ------------------------------------------------------------------ [Kernel] samples
 # Each oracle restates a sample kernel body under the CPU invoker's flat-loop semantics; the pins
 # below are closed forms computed independently (numpy float32 array arithmetic, Python integers).
