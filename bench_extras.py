@@ -359,11 +359,15 @@ def bench_orchestrator(log, cpu: bool = True) -> dict:
     us = d["execute_async_us"]["median"]
     leg = {"us_per_call": us, "GB/s_host_arrays": round(12 * d["n"] / (us * 1e-6) / 1e9, 2),
            "device_resident_us_per_call": d["execute_with_buffers_us"]["median"],
+           "launch_and_wait_us": d["launch_and_wait_us"]["median"], "idle_wait_us": d["idle_wait_us"],
            "h2d_input_us": d["h2d_input_us"], "d2h_result_us": d["d2h_result_us"], "bit_exact": d["bit_exact"],
            "note": "host arrays: 2 inputs in (the result is never read by the kernel, so it is not copied in), "
-                   "launch, result out, synchronised per call; PCIe-bound, not an HBM roofline"}
+                   "launch, result out, synchronised per call; PCIe-bound, not an HBM roofline. "
+                   "launch_and_wait_us: the same compiled kernel launched directly with a prebuilt argument "
+                   "block and waited for, the floor under the device-resident call"}
     log(f"[bench] orchestrator VectorAdd 100K: {us:.1f} us per ExecuteAsync (device-resident "
-        f"{leg['device_resident_us_per_call']:.1f} us; h2d {d['h2d_input_us']:.1f} us, d2h {d['d2h_result_us']:.1f} us)")
+        f"{leg['device_resident_us_per_call']:.1f} us, of which launch and wait {leg['launch_and_wait_us']:.1f} us; "
+        f"h2d {d['h2d_input_us']:.1f} us, d2h {d['d2h_result_us']:.1f} us)")
     if cpu:
         import oracle
 

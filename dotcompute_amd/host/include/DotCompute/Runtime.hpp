@@ -9,6 +9,7 @@
 // (src/Runtime/DotCompute.Generators/Kernel/Generation/KernelRegistrationEmitter.cs:40-201).
 #pragma once
 
+#include <atomic>
 #include <functional>
 #include <map>
 #include <mutex>
@@ -187,7 +188,12 @@ class KernelExecutionService final : public IComputeOrchestrator {
                                                 const std::vector<KernelArg>& args, size_t totalWork);
 
  private:
+  using Registration = std::shared_ptr<const KernelRegistrationInfo>;
   void EnsureInitialized();
+  Registration Resolve(const std::string& name) const;
+  std::vector<std::shared_ptr<IAccelerator>> SupportedOn(const KernelRegistrationInfo& reg) const;
+  std::shared_ptr<IAccelerator> OptimalFor(const Registration& reg);
+  static bool ArgumentsMatch(const KernelRegistrationInfo& reg, const std::vector<KernelArg>& args);
   std::vector<float> ExecuteOn(const KernelRegistrationInfo& reg, IAccelerator& accelerator,
                                std::vector<KernelArg>& args);
   std::vector<float> ExecuteGenerated(const KernelRegistrationInfo& reg, Backends::Hip::HipAccelerator& accelerator,
@@ -196,9 +202,14 @@ class KernelExecutionService final : public IComputeOrchestrator {
 
   std::shared_ptr<AcceleratorRuntime> runtime_;
   mutable std::mutex mu_;
-  bool initialized_ = false;
-  std::map<std::string, KernelRegistrationInfo> registry_;     // by full and short name
-  std::map<std::string, std::shared_ptr<ICompiledKernel>> cache_;  // "<accelerator id>/<kernel>"
+  std::atomic<bool> initialized_{false};
+  // Registrations by full and short name. A record is never changed once published (RegisterKernels
+  // replaces it), so a call holds its own reference and reads it without the lock.
+  std::map<std::string, Registration> registry_;
+  // Per registration record: the optimal accelerator, and the compiled kernel per accelerator
+  // (both cleared when RegisterKernels replaces records).
+  std::map<const KernelRegistrationInfo*, std::shared_ptr<IAccelerator>> optimal_;
+  std::map<std::pair<const IAccelerator*, const KernelRegistrationInfo*>, std::shared_ptr<ICompiledKernel>> cache_;
 };
 
 }  // namespace DotCompute

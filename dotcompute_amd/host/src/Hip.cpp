@@ -189,8 +189,20 @@ std::future<void> HipCompiledKernel::ExecuteAsync(const KernelArguments& argumen
   // CudaKernelLauncher pins a void*[] of argument slots, CudaKernelLauncher.cs:226-313).
   // A struct argument (RawArgument) points at its own bytes.
   const size_t n = arguments.Buffers.size() + arguments.ScalarArguments.size();
-  std::vector<uint64_t> storage(n, 0);
-  std::vector<void*> slots(n, nullptr);
+  // Slots on the stack for the usual argument counts (no allocation per launch).
+  constexpr size_t kInline = 32;
+  uint64_t storage_inline[kInline] = {};
+  void* slots_inline[kInline] = {};
+  std::vector<uint64_t> storage_heap;
+  std::vector<void*> slots_heap;
+  uint64_t* storage = storage_inline;
+  void** slots = slots_inline;
+  if (n > kInline) {
+    storage_heap.assign(n, 0);
+    slots_heap.assign(n, nullptr);
+    storage = storage_heap.data();
+    slots = slots_heap.data();
+  }
   size_t i = 0;
   for (IUnifiedMemoryBuffer* b : arguments.Buffers) {
     if (!b) throw ArgumentNullException("null buffer argument");
@@ -214,7 +226,7 @@ std::future<void> HipCompiledKernel::ExecuteAsync(const KernelArguments& argumen
   }
   const KernelLaunchConfiguration& lc = arguments.LaunchConfiguration;
   Check(dc_hip_launch_kernel(ctx_.get(), function_, lc.GridSize.X, lc.GridSize.Y, lc.GridSize.Z, lc.BlockSize.X,
-                             lc.BlockSize.Y, lc.BlockSize.Z, lc.SharedMemoryBytes, slots.data()),
+                             lc.BlockSize.Y, lc.BlockSize.Z, lc.SharedMemoryBytes, slots),
         "dc_hip_launch_kernel");
   std::promise<void> p;
   p.set_value();

@@ -72,31 +72,42 @@ std::shared_ptr<IComputeOrchestrator> ServiceProvider::GetRequiredOrchestrator()
 KernelExecutionService::KernelExecutionService(std::shared_ptr<AcceleratorRuntime> runtime) : runtime_(std::move(runtime)) {}
 
 void KernelExecutionService::EnsureInitialized() {
+  if (initialized_.load(std::memory_order_acquire)) return;
   std::lock_guard<std::mutex> lock(mu_);
-  if (initialized_) return;
+  if (initialized_.load(std::memory_order_relaxed)) return;
   runtime_->Initialize();
   // GeneratedKernelDiscoveryService.DiscoverAndRegisterKernelsAsync: the generated registry.
   for (const auto& k : Generated::KernelRegistry::GetAllKernels()) {
-    registry_[k.FullName] = k;
-    registry_.emplace(k.Name, k);
+    auto rec = std::make_shared<const KernelRegistrationInfo>(k);
+    registry_[k.FullName] = rec;
+    registry_.emplace(k.Name, rec);
   }
-  initialized_ = true;
+  initialized_.store(true, std::memory_order_release);
 }
 
 void KernelExecutionService::RegisterKernels(const std::vector<KernelRegistrationInfo>& kernels) {
   EnsureInitialized();
   std::lock_guard<std::mutex> lock(mu_);
   for (const auto& k : kernels) {
-    registry_[k.FullName] = k;
-    registry_[k.Name] = k;  // short-name index (KernelExecutionService.cs:170-193)
+    auto rec = std::make_shared<const KernelRegistrationInfo>(k);
+    registry_[k.FullName] = rec;
+    registry_[k.Name] = rec;  // short-name index (KernelExecutionService.cs:170-193)
   }
+  // Cached choices belong to replaced records; a freed record's address may be reused.
+  optimal_.clear();
+  cache_.clear();
+}
+
+KernelExecutionService::Registration KernelExecutionService::Resolve(const std::string& name) const {
+  std::lock_guard<std::mutex> lock(mu_);
+  auto it = registry_.find(name);
+  return it == registry_.end() ? nullptr : it->second;
 }
 
 std::optional<KernelRegistrationInfo> KernelExecutionService::TryResolveKernel(const std::string& name) const {
-  std::lock_guard<std::mutex> lock(mu_);
-  auto it = registry_.find(name);
-  if (it == registry_.end()) return std::nullopt;
-  return it->second;
+  Registration r = Resolve(name);
+  if (!r) return std::nullopt;
+  return *r;
 }
 
 std::string KernelExecutionService::MapDeviceTypeToBackend(const std::string& deviceType) {
@@ -159,13 +170,10 @@ KernelLaunchConfiguration KernelExecutionService::DeriveLaunch(const KernelRegis
   return lc;
 }
 
-bool KernelExecutionService::ValidateKernelArgsAsync(const std::string& kernelName, const std::vector<KernelArg>& args) {
-  EnsureInitialized();
-  auto reg = TryResolveKernel(kernelName);
-  if (!reg) return false;
-  if (args.size() < reg->Parameters.size()) return false;
-  for (size_t i = 0; i < reg->Parameters.size(); ++i) {
-    const auto& p = reg->Parameters[i];
+bool KernelExecutionService::ArgumentsMatch(const KernelRegistrationInfo& reg, const std::vector<KernelArg>& args) {
+  if (args.size() < reg.Parameters.size()) return false;
+  for (size_t i = 0; i < reg.Parameters.size(); ++i) {
+    const auto& p = reg.Parameters[i];
     if (p.IsBuffer) {
       if (auto* h = std::get_if<HostArray>(&args[i])) {
         if (h->Type != p.Type || (h->Length > 0 && !h->Data)) return false;
@@ -181,39 +189,68 @@ bool KernelExecutionService::ValidateKernelArgsAsync(const std::string& kernelNa
   return true;
 }
 
-std::vector<std::shared_ptr<IAccelerator>> KernelExecutionService::GetSupportedAcceleratorsAsync(const std::string& kernelName) {
+bool KernelExecutionService::ValidateKernelArgsAsync(const std::string& kernelName, const std::vector<KernelArg>& args) {
   EnsureInitialized();
-  auto reg = TryResolveKernel(kernelName);
+  Registration reg = Resolve(kernelName);
+  return reg && ArgumentsMatch(*reg, args);
+}
+
+std::vector<std::shared_ptr<IAccelerator>> KernelExecutionService::SupportedOn(const KernelRegistrationInfo& reg) const {
   std::vector<std::shared_ptr<IAccelerator>> out;
-  if (!reg) return out;
   for (const auto& acc : runtime_->GetAccelerators()) {
     const std::string backend = MapDeviceTypeToBackend(acc->Info().DeviceType);
-    bool ok = std::any_of(reg->SupportedBackends.begin(), reg->SupportedBackends.end(),
+    bool ok = std::any_of(reg.SupportedBackends.begin(), reg.SupportedBackends.end(),
                           [&](const std::string& b) { return EqualsIgnoreCase(b, backend); });
     // A registry kernel with a HIP entry point runs on HIP whether or not [Kernel(Backends)] names
     // HIP, as ExecuteAsync(name, "CUDA", ...) runs a CPU-only [Kernel] on CUDA (:230-246).
-    if (backend == "HIP" && !reg->HipEntryPoint.empty()) ok = true;
+    if (backend == "HIP" && !reg.HipEntryPoint.empty()) ok = true;
     if (ok) out.push_back(acc);
   }
   return out;
 }
 
+std::vector<std::shared_ptr<IAccelerator>> KernelExecutionService::GetSupportedAcceleratorsAsync(const std::string& kernelName) {
+  EnsureInitialized();
+  Registration reg = Resolve(kernelName);
+  if (!reg) return {};
+  return SupportedOn(*reg);
+}
+
+// The accelerator of the best backend priority among those that support the kernel, chosen once
+// per registration record (the runtime's accelerators are fixed once it is initialised).
+std::shared_ptr<IAccelerator> KernelExecutionService::OptimalFor(const Registration& reg) {
+  {
+    std::lock_guard<std::mutex> lock(mu_);
+    auto it = optimal_.find(reg.get());
+    if (it != optimal_.end()) return it->second;
+  }
+  auto supported = SupportedOn(*reg);
+  std::shared_ptr<IAccelerator> best;
+  if (!supported.empty())
+    best = *std::min_element(supported.begin(), supported.end(), [](const auto& a, const auto& b) {
+      return GetBackendPriority(a->Info().DeviceType) < GetBackendPriority(b->Info().DeviceType);
+    });
+  std::lock_guard<std::mutex> lock(mu_);
+  auto cur = registry_.find(reg->FullName);
+  if (best && cur != registry_.end() && cur->second == reg) optimal_[reg.get()] = best;  // still published
+  return best;
+}
+
 std::shared_ptr<IAccelerator> KernelExecutionService::GetOptimalAcceleratorAsync(const std::string& kernelName) {
-  auto supported = GetSupportedAcceleratorsAsync(kernelName);
-  if (supported.empty()) return nullptr;
-  return *std::min_element(supported.begin(), supported.end(), [](const auto& a, const auto& b) {
-    return GetBackendPriority(a->Info().DeviceType) < GetBackendPriority(b->Info().DeviceType);
-  });
+  EnsureInitialized();
+  Registration reg = Resolve(kernelName);
+  if (!reg) return nullptr;
+  return OptimalFor(reg);
 }
 
 std::future<std::vector<float>> KernelExecutionService::ExecuteAsync(const std::string& kernelName,
                                                                      std::vector<KernelArg> args) {
   EnsureInitialized();
-  auto reg = TryResolveKernel(kernelName);
+  Registration reg = Resolve(kernelName);
   if (!reg)
     throw ArgumentException("Kernel '" + kernelName + "' is not registered. Ensure the kernel's registry is "
                             "discovered, pass the fully-qualified or short name, or register it via RegisterKernels().");
-  auto acc = GetOptimalAcceleratorAsync(kernelName);
+  auto acc = OptimalFor(reg);
   if (!acc) {
     if (runtime_->GetAccelerators().empty())
       throw InvalidOperationException("No accelerators are registered with the runtime, so kernel '" + kernelName +
@@ -243,11 +280,11 @@ std::future<std::vector<float>> KernelExecutionService::ExecuteAsync(const std::
                                                                      IAccelerator& accelerator,
                                                                      std::vector<KernelArg> args) {
   EnsureInitialized();
-  auto reg = TryResolveKernel(kernelName);
+  Registration reg = Resolve(kernelName);
   if (!reg)
     throw ArgumentException("Kernel '" + kernelName + "' is not registered. Add the kernel via RegisterKernels() "
                             "before executing, or check for typos.");
-  if (!ValidateKernelArgsAsync(kernelName, args))
+  if (!ArgumentsMatch(*reg, args))
     throw ArgumentException("Kernel argument validation failed for kernel '" + kernelName + "' (received " +
                             std::to_string(args.size()) + " arguments). Verify argument count, types, and ordering.");
   std::vector<float> result = ExecuteOn(*reg, accelerator, args);
@@ -258,7 +295,7 @@ std::future<std::vector<float>> KernelExecutionService::ExecuteAsync(const std::
 
 std::shared_ptr<ICompiledKernel> KernelExecutionService::GetCompiled(const KernelRegistrationInfo& reg,
                                                                      IAccelerator& accelerator) {
-  const std::string key = accelerator.Info().Id + "/" + reg.FullName;
+  const auto key = std::make_pair(static_cast<const IAccelerator*>(&accelerator), &reg);
   {
     std::lock_guard<std::mutex> lock(mu_);
     auto it = cache_.find(key);
@@ -273,17 +310,18 @@ std::shared_ptr<ICompiledKernel> KernelExecutionService::GetCompiled(const Kerne
   def.Language = KernelLanguage::HIP;
   auto compiled = accelerator.CompileKernelAsync(def).get();
   std::lock_guard<std::mutex> lock(mu_);
-  cache_[key] = compiled;
+  auto cur = registry_.find(reg.FullName);
+  if (cur != registry_.end() && cur->second.get() == &reg) cache_[key] = compiled;  // a published record only
   return compiled;
 }
 
 void KernelExecutionService::PrecompileKernelAsync(const std::string& kernelName, IAccelerator* accelerator) {
   EnsureInitialized();
-  auto reg = TryResolveKernel(kernelName);
+  Registration reg = Resolve(kernelName);
   if (!reg) throw ArgumentException("Kernel '" + kernelName + "' is not registered.");
   std::shared_ptr<IAccelerator> acc;
   if (!accelerator) {
-    acc = GetOptimalAcceleratorAsync(kernelName);
+    acc = OptimalFor(reg);
     if (!acc) throw InvalidOperationException("no accelerator supports kernel '" + kernelName + "'");
     accelerator = acc.get();
   }
@@ -468,11 +506,12 @@ std::future<void> KernelExecutionService::ExecuteWithBuffersAsync(const std::str
                                                                   std::vector<IUnifiedMemoryBuffer*> buffers,
                                                                   std::vector<ScalarValue> scalarArgs) {
   EnsureInitialized();
-  auto reg = TryResolveKernel(kernelName);
+  Registration reg = Resolve(kernelName);
   if (!reg) throw ArgumentException("Kernel '" + kernelName + "' is not registered.");
-  auto acc = GetOptimalAcceleratorAsync(kernelName);
+  auto acc = OptimalFor(reg);
   if (!acc) throw InvalidOperationException("no accelerator supports kernel '" + kernelName + "'");
   std::vector<KernelArg> args;
+  args.reserve(buffers.size() + scalarArgs.size());
   for (auto* b : buffers) args.push_back(b);
   for (auto& s : scalarArgs)
     std::visit(
@@ -483,7 +522,7 @@ std::future<void> KernelExecutionService::ExecuteWithBuffersAsync(const std::str
             args.push_back(v);
         },
         s);
-  if (!ValidateKernelArgsAsync(kernelName, args)) throw ArgumentException("buffer/scalar arguments do not match the kernel");
+  if (!ArgumentsMatch(*reg, args)) throw ArgumentException("buffer/scalar arguments do not match the kernel");
   ExecuteOn(*reg, *acc, args);
   std::promise<void> p;
   p.set_value();
