@@ -541,7 +541,7 @@ __device__ __attribute__((always_inline)) inline void eval_program(const dc_linq
 //     base_r + sum_{w' < w} count(r, w'),   base_{r+1} = base_r + sum_{w'} count(r, w'),
 // and every workgroup reads all P counts of a round itself, so no prefix ever has to travel from tile
 // to tile (the serial front that limits a decoupled lookback). The loop is software-pipelined:
-//   - loads run kRrAhead rounds ahead (kRrAhead + 1 register buffers per lane);
+//   - loads run kRrAhead rounds ahead (kRrAhead + 1 register buffers per lane; 2 for the int32 interpreter);
 //   - kept values of a tile wait in LDS for kRrDelay rounds before they are written, and the count
 //     words of that round are read one round before the write, so they were published
 //     kRrDelay - 2 full rounds earlier and are almost always already visible;
@@ -812,19 +812,23 @@ __device__ __attribute__((always_inline)) inline void rounds_body(
   // path-insensitive: on a path that skipped a later load, the wait for the round being staged
   // would have to cover every load still in flight, draining the pipeline.
   const uint32_t last = R0 > 0 ? R0 - 1 : 0;
-  constexpr int kBufs = kRrAhead + 1;
+  // Rounds of look-ahead: kRrAhead, or 2 for the int32 interpreter, whose per-chunk state with five
+  // buffers exceeded the 168 registers a lane may hold here and spilled to scratch (two rounds
+  // measured as fast as four on the headline kernel, so the depth is not what bounds it).
+  constexpr int kAhead = kIntProg && RD != kRdJit ? 2 : kRrAhead;
+  constexpr int kBufs = kAhead + 1;
   float e[kBufs][kRrEpt];  // register buffers: constant indices only, after full unrolling
   if (R0 > 0)
     for_each_index([&](auto U) __attribute__((always_inline)) { load(e[U.value], min((uint32_t)U.value, last)); },
-                   std::make_integer_sequence<int, kRrAhead>{});
+                   std::make_integer_sequence<int, kAhead>{});
   uint32_t r = 0;
-  // One round: issue the loads of round r + kRrAhead into buffer `en`, stage round r from `ec`,
+  // One round: issue the loads of round r + kAhead into buffer `en`, stage round r from `ec`,
   // write round r - kRrDelay. Unrolled kBufs ways so the buffers rotate without copies. The main
   // loop runs whole kBufs-round iterations with no early exit: a `break` between rounds becomes a
   // path back to the loop head after a partial iteration, and the waits at the head would then
   // assume fewer loads in flight than a full iteration leaves. The last R0 % kBufs rounds follow.
   auto round = [&](float (&ec)[kRrEpt], float (&en)[kRrEpt]) __attribute__((always_inline)) {
-    load(en, min(r + kRrAhead, last));
+    load(en, min(r + kAhead, last));
     bool kept[kRrEpt];
     apply(ec, kept, ((int64_t)r * P + w) * kRrTile + chunk + 4 * lane, ~0u);
     stage(ec, kept, r);
@@ -833,10 +837,10 @@ __device__ __attribute__((always_inline)) inline void rounds_body(
     ++r;
   };
   for (uint32_t it = R0 / kBufs; it > 0; --it)
-    for_each_index([&](auto U) __attribute__((always_inline)) { round(e[U.value], e[(U.value + kRrAhead) % kBufs]); },
+    for_each_index([&](auto U) __attribute__((always_inline)) { round(e[U.value], e[(U.value + kAhead) % kBufs]); },
                    std::make_integer_sequence<int, kBufs>{});
-  for_each_index([&](auto U) __attribute__((always_inline)) { if (r < R0) round(e[U.value], e[(U.value + kRrAhead) % kBufs]); },
-                 std::make_integer_sequence<int, kRrAhead>{});
+  for_each_index([&](auto U) __attribute__((always_inline)) { if (r < R0) round(e[U.value], e[(U.value + kAhead) % kBufs]); },
+                 std::make_integer_sequence<int, kAhead>{});
   for (; r < rounds; ++r) {  // drain: the last kRrDelay staged tiles (fewer when R0 < kRrDelay)
     __syncthreads();
     if (r >= (uint32_t)kRrDelay) write(r - kRrDelay, r & 1);
