@@ -1229,6 +1229,35 @@ bool use_rounds(dc_hip_ctx* ctx, const float* input, int64_t n) {
   return ctx->rounds_fit == 1;
 }
 
+// The chain the int32 interpreter kernels run: every DIV/REM by a constant outside {0, -1, 1}
+// preceded by a kOpDivMagic instruction carrying its multiply-high constants, computed here once
+// per launch (the original chain when the inserted instructions would not fit).
+dc_linq_chain device_chain_i32(const dc_linq_chain& c) {
+  auto const_div = [](const dc_linq_instr& in) {
+    return (in.op == DC_LQ_DIV || in.op == DC_LQ_REM) && in.src == DC_LQ_SRC_IMM && in.imm_i32 != 0 &&
+           in.imm_i32 != -1 && in.imm_i32 != 1;
+  };
+  int extra = 0;
+  for (int i = 0; i < c.n_instr; ++i) extra += const_div(c.code[i]) ? 1 : 0;
+  if (extra == 0 || c.n_instr + extra > DC_LINQ_MAX_INSTR) return c;
+  dc_linq_chain out = c;
+  int k = 0;
+  for (int i = 0; i < c.n_instr; ++i) {
+    if (const_div(c.code[i])) {
+      const dc::DivMagic g = dc::div_magic(c.code[i].imm_i32);
+      dc_linq_instr m{};
+      m.op = (uint8_t)kOpDivMagic;
+      m.src = DC_LQ_SRC_IMM;
+      m.mode = (uint8_t)g.s;
+      m.imm_i32 = g.m;
+      out.code[k++] = m;
+    }
+    out.code[k++] = c.code[i];
+  }
+  out.n_instr = k;
+  return out;
+}
+
 // Whether ToArray launches run-time compiled kernels (off; see launch_to_array).
 constexpr bool kLaunchCompiled = false;
 
@@ -1259,7 +1288,7 @@ int32_t launch_to_array(dc_hip_ctx* ctx, const dc_linq_chain* chain, bool is_int
     const size_t words = (size_t)((tiles + groups - 1) / groups + 1) * groups;
     uint32_t epoch16 = 0;
     DC_RETURN_IF(dc::ensure_round_counts(ctx, words, &epoch16));
-    dc_linq_chain prog = *chain;
+    dc_linq_chain prog = is_int ? device_chain_i32(*chain) : *chain;
     const float* in_arg = input + head_n;
     int64_t n_arg = n - head_n;
     const float* head_arg = input;
@@ -1301,7 +1330,8 @@ int32_t launch_to_array(dc_hip_ctx* ctx, const dc_linq_chain* chain, bool is_int
               : mode == kModeInterpI32         ? where_select_kernel<kModeInterpI32>
               : mode == kModeInterpI32Saves    ? where_select_kernel<kModeInterpI32Saves>
                                                : where_select_kernel<kModeInterp>;
-  kernel<<<(unsigned)tiles, kBlock, 0, ctx->stream>>>(*chain, aff, input, n, output, count_out, ctx->status,
+  kernel<<<(unsigned)tiles, kBlock, 0, ctx->stream>>>(is_int ? device_chain_i32(*chain) : *chain, aff, input, n,
+                                                     output, count_out, ctx->status,
                                                       ctx->counters + DC_SLOT_LINQ_TICKET, epoch, (uint32_t)tiles,
                                                       dc::aligned16(input) ? 1 : 0, fault_word);
   return dc::last_launch_status();
@@ -1402,10 +1432,11 @@ DC_HIP_API int32_t dc_hip_linq_where_select_sum_i32(dc_hip_ctx* ctx, const dc_li
   int64_t* part = static_cast<int64_t*>(ctx->partials);
   const float* in = reinterpret_cast<const float*>(input);
   const int64_t h = reduce_head(in, n);
+  const dc_linq_chain dev = device_chain_i32(*chain);
   rd_dispatch_i32(reduce_plan_i32(*chain).mode, [&](auto mode) {
     constexpr int RD = decltype(mode)::value;
-    where_select_sum_i32_pass1<RD><<<grid, kSumBlock, 0, ctx->stream>>>(*chain, in, n, h, part);
-    where_select_sum_i32_pass2<RD><<<1, kFinalBlock, 0, ctx->stream>>>(*chain, in, n, h, part, (int)grid, sum_out,
+    where_select_sum_i32_pass1<RD><<<grid, kSumBlock, 0, ctx->stream>>>(dev, in, n, h, part);
+    where_select_sum_i32_pass2<RD><<<1, kFinalBlock, 0, ctx->stream>>>(dev, in, n, h, part, (int)grid, sum_out,
                                                                       count_out, overflow_out, fault_out);
   });
   return dc::last_launch_status();
@@ -1423,12 +1454,13 @@ DC_HIP_API int32_t dc_hip_linq_where_select_minmax_i32(dc_hip_ctx* ctx, const dc
   int64_t* part = static_cast<int64_t*>(ctx->partials);
   const float* in = reinterpret_cast<const float*>(input);
   const int64_t h = reduce_head(in, n);
+  const dc_linq_chain dev = device_chain_i32(*chain);
   rd_dispatch_i32(reduce_plan_i32(*chain).mode, [&](auto mode) {
     constexpr int RD = decltype(mode)::value;
     if (op == DC_LINQ_MIN)
-      where_select_minmax_i32_pass1<RD, kOpMin><<<grid, kSumBlock, 0, ctx->stream>>>(*chain, in, n, h, part);
+      where_select_minmax_i32_pass1<RD, kOpMin><<<grid, kSumBlock, 0, ctx->stream>>>(dev, in, n, h, part);
     else
-      where_select_minmax_i32_pass1<RD, kOpMax><<<grid, kSumBlock, 0, ctx->stream>>>(*chain, in, n, h, part);
+      where_select_minmax_i32_pass1<RD, kOpMax><<<grid, kSumBlock, 0, ctx->stream>>>(dev, in, n, h, part);
   });
   if (op == DC_LINQ_MIN)
     where_select_minmax_i32_pass2<kOpMin><<<1, kFinalBlock, 0, ctx->stream>>>(part, (int)grid, value_out, count_out,

@@ -58,6 +58,10 @@ __device__ inline float net_max(float a, float b) {
 struct Instr {
   uint32_t op, src, mode, imm;  // imm: the constant's bits (float32 or int32 by program type)
 };
+// Internal opcode, never in a caller's chain: the multiply-high constants of the int32 DIV or REM
+// by a constant that follows it (imm = m, mode = shift). The host inserts it (once per launch) so
+// that the interpreter does not derive them again for every chunk of elements.
+constexpr uint32_t kOpDivMagic = 0x40;
 __device__ inline Instr fetch_instr(const dc_linq_chain& prog, int pc) {
   const uint32_t* w = reinterpret_cast<const uint32_t*>(&prog.code[pc]);
   const uint32_t w0 = w[0];
@@ -116,6 +120,8 @@ struct ProgramState {
   T v[EPT];
   T s0[SAVES ? EPT : 1], s1[SAVES ? EPT : 1];
   uint32_t p = 0, q = 0, keep;
+  int32_t gm = 0, gs = 0;  // constants of the next DIV/REM by a constant (kOpDivMagic), if gv
+  bool gv = false;
 
   __device__ __attribute__((always_inline)) explicit ProgramState(uint32_t live) : keep(live) {
 #pragma unroll
@@ -156,6 +162,11 @@ struct ProgramState {
     }                                                                                       \
   } while (0)
     switch (ins.op) {
+      case kOpDivMagic:
+        gm = (int32_t)ins.imm;
+        gs = (int32_t)ins.mode;
+        gv = true;
+        break;
       case DC_LQ_LOAD: DC_LQ_APPLY(v[j] = O); break;
       case DC_LQ_ADD:
         if constexpr (kInt) DC_LQ_APPLY(v[j] = wrap_add(v[j], O));
@@ -177,7 +188,8 @@ struct ProgramState {
         if constexpr (kInt) {
           const int32_t d = (int32_t)ins.imm;
           if (ins.src == DC_LQ_SRC_IMM && d != 0 && d != -1 && d != 1) {  // never throws
-            div_const(dc::div_magic(d), false);
+            div_const(gv ? dc::DivMagic{gm, gs, d} : dc::div_magic(d), false);
+            gv = false;
           } else {
             DC_LQ_APPLY(v[j] = checked_div(v[j], O, j, keep, f));
           }
@@ -193,7 +205,8 @@ struct ProgramState {
         if constexpr (kInt) {
           const int32_t d = (int32_t)ins.imm;
           if (ins.src == DC_LQ_SRC_IMM && d != 0 && d != -1 && d != 1) {  // never throws
-            div_const(dc::div_magic(d), true);
+            div_const(gv ? dc::DivMagic{gm, gs, d} : dc::div_magic(d), true);
+            gv = false;
           } else {
             DC_LQ_APPLY(v[j] = checked_rem(v[j], O, j, keep, f));
           }

@@ -315,3 +315,43 @@ def test_random_int_programs_match_oracle(ctx):
         s_ref = oracle.linq_where_select_sum_i32(ch, x)
         s_got = run_sum(ctx, ch, x)
         assert s_got == s_ref if s_ref[3] < 0 else s_got[3] == s_ref[3], (trial, code)
+
+
+DIVISORS = [2, 3, 7, -7, 10, 1000, -65536, 2**30 + 1, I32_MAX, I32_MIN, -2, 641]
+
+
+@pytest.mark.parametrize("d", DIVISORS)
+def test_division_by_constants_on_every_terminal(ctx, d):
+    """x / d and x % d for constants the kernels divide by multiply-high (the constants are computed
+    on the host once per launch): ToArray (both grids), checked Sum and Min/Max against the oracle,
+    over values that include int.MinValue, int.MaxValue, 0 and +-1."""
+    x = oracle.gen_uniform_i32(300_001, 70, 1, I32_MIN, I32_MAX)
+    x[:7] = [I32_MIN, I32_MAX, 0, 1, -1, d, -d if d != I32_MIN else 5]
+    for op in (DIV, REM):
+        ch = chain([(LOAD, SRC_ELEM, 0), (op, SRC_IMM, d), (MAP, SRC_IMM, 0)])
+        got, k, f = run_to_array(ctx, ch, x)
+        ref, rf = oracle.linq_where_select_i32(ch, x)
+        assert f == rf == -1 and k == ref.size and np.array_equal(got, ref), (op, d)
+        assert run_sum(ctx, ch, x) == oracle.linq_where_select_sum_i32(ch, x), (op, d)
+        for mop, name in ((hip.LINQ_MIN, "min"), (hip.LINQ_MAX, "max")):
+            v, c, f = run_minmax(ctx, ch, x, mop)
+            rv, rc, rf = oracle.linq_where_select_minmax_i32(ch, x, name)
+            assert (v, c, f) == (rv, rc, rf), (op, d, name)
+
+
+def test_division_constants_when_the_program_is_full(ctx):
+    """A program of 47 instructions with 23 divisions by constants: the constants no longer fit as
+    extra instructions (48 at most), and the kernels derive them themselves; results still match."""
+    code = [(LOAD, SRC_ELEM, 0)]
+    for i in range(22):
+        code.append((REM if i % 2 else DIV, SRC_IMM, 3 + 2 * i))
+        code.append((ADD, SRC_ELEM, 0))
+    code.append((DIV, SRC_IMM, 5))
+    code.append((MAP, SRC_IMM, 0))
+    assert len(code) == 47
+    ch = chain(code)
+    x = oracle.gen_uniform_i32(100_003, 71, 1, -10**6, 10**6)
+    got, k, f = run_to_array(ctx, ch, x)
+    ref, rf = oracle.linq_where_select_i32(ch, x)
+    assert f == rf == -1 and np.array_equal(got, ref)
+    assert run_sum(ctx, ch, x) == oracle.linq_where_select_sum_i32(ch, x)
