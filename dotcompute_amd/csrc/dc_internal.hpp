@@ -25,8 +25,6 @@ struct dc_hip_ctx {
   size_t partials_bytes = 0;
 
   // SpMV scratch: the list of long rows (handled a workgroup per row) and small device scalars.
-  int32_t* spmv_rows = nullptr;
-  size_t spmv_rows_cap = 0;
   int32_t* spmv_windows = nullptr;  // first row of each nonzero window
   size_t spmv_windows_cap = 0;
   double* scalars = nullptr;  // 64 doubles
@@ -80,7 +78,7 @@ struct dc_hip_module {
 // Counter slots inside ctx->counters.
 enum dc_counter_slot : int {
   DC_SLOT_LINQ_TICKET = 0,   // tile ticket of the compaction kernel (returned to 0 by the kernel)
-  DC_SLOT_SPMV_LONG = 1,     // number of long rows found by the SpMV classification pass
+  // slot 1: unused
   DC_SLOT_LINQ_DONE = 2,     // finished-workgroup word of the round-robin compaction (returned to 0)
   DC_SLOT_REDUCE_DONE = 3,   // finished-workgroup word of the one-launch reductions (returned to 0)
   DC_SLOT_LINQ_FAULT = 4,    // 64-bit (slots 4-5): first exception of an int32 LINQ ToArray, ~(4 * index +
@@ -154,8 +152,7 @@ void resident_forget(dc_hip_ctx* ctx);
 // Looks up the device address of the no-alloc LINQ Sum's static scratch for ctx->device (the
 // device must be current) and stores it in ctx->noalloc_scratch. Calls no allocator.
 int32_t linq_noalloc_setup(dc_hip_ctx* ctx);
-// Grow ctx->spmv_rows / ctx->spmv_windows to at least `count` entries (caller holds the lock).
-int32_t ensure_spmv_rows(dc_hip_ctx* ctx, size_t count);
+// Grow ctx->spmv_windows to at least `count` entries (caller holds the lock).
 int32_t ensure_spmv_windows(dc_hip_ctx* ctx, size_t count);
 int32_t ensure_spmv_plan_mem(dc_hip_ctx* ctx, size_t bytes);
 // Two-pass deterministic float64 sum of n floats into *sum_out (device), on the ctx stream.

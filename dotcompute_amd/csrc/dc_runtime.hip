@@ -85,20 +85,6 @@ int32_t ensure_partials(dc_hip_ctx* ctx, size_t bytes) {
   return DC_OK;
 }
 
-int32_t ensure_spmv_rows(dc_hip_ctx* ctx, size_t count) {
-  if (ctx->spmv_rows_cap >= count) return DC_OK;
-  size_t want = std::max<size_t>(count, 4096);
-  DC_RETURN_IF_HIP(hipStreamSynchronize(ctx->stream));
-  if (ctx->spmv_rows) DC_RETURN_IF_HIP(hipFree(ctx->spmv_rows));
-  ctx->spmv_rows = nullptr;
-  ctx->spmv_rows_cap = 0;
-  void* p = nullptr;
-  if (hipMalloc(&p, want * sizeof(int32_t)) != hipSuccess) return DC_ERR_OUT_OF_MEMORY;
-  ctx->spmv_rows = static_cast<int32_t*>(p);
-  ctx->spmv_rows_cap = want;
-  return DC_OK;
-}
-
 int32_t ensure_spmv_windows(dc_hip_ctx* ctx, size_t count) {
   if (ctx->spmv_windows_cap >= count) return DC_OK;
   size_t want = std::max<size_t>(count, 4096);
@@ -348,7 +334,6 @@ DC_HIP_API int32_t dc_hip_ctx_destroy(dc_hip_ctx* ctx) {
     dc::resident_forget(ctx);
     if (ctx->counters) (void)hipFree(ctx->counters);
     if (ctx->scalars) (void)hipFree(ctx->scalars);
-    if (ctx->spmv_rows) (void)hipFree(ctx->spmv_rows);
     if (ctx->spmv_windows) (void)hipFree(ctx->spmv_windows);
     if (ctx->spmv_plan_mem) (void)hipFree(ctx->spmv_plan_mem);
     (void)hipStreamDestroy(ctx->stream);

@@ -10,8 +10,10 @@
 //     into LDS with fully coalesced value/column loads (x is a gather, served mostly by L2 / the
 //     256 MB MALL), then one thread per row adds its products in index order — the same order as
 //     SparseOps.SpMV (SparseMatrix.cs:669-692), so short rows are bit-identical to the reference.
-//   long rows (more than kLongRow nonzeros): listed by a classification pass and handled one
-//     workgroup per row with a fixed-order block reduction (deterministic, not sequential order).
+//   long rows (more than kLongRow nonzeros): summed by the workgroup of the window in which they
+//     start, after its short rows, with a fixed-order block reduction (deterministic, not
+//     sequential order). At most two long rows start in one window (each holds kLongRow + 1 or
+//     more nonzeros, so a third would start past the window).
 // A window's product span is at most kWindow + kLongRow entries (only its last row can run past
 // the window, and it is short or excluded), which sizes the LDS buffer.
 #include <algorithm>
@@ -24,49 +26,22 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kWindow = 1024;   // nonzeros per window
-constexpr int kLongRow = 512;   // rows longer than this go to the long-row pass
-constexpr int kLongBlock = 256;
+constexpr int kLongRow = 512;   // rows longer than this are summed by the whole workgroup
+constexpr int kMaxLongPerWindow = 4;  // a well-formed CSR starts at most two long rows in a window
 
 // row_start[k] = first row whose first nonzero index is >= k·kWindow, for k in [0, windows);
-// row_start[windows] = rows.
+// row_start[windows] = rows. One thread per entry r of the row pointers (coalesced, no search):
+// the windows k with rp[r - 1] < k·kWindow <= rp[r] start at row r (for r = 0, k = 0 only). With
+// monotone row pointers every k is written exactly once.
 __global__ __launch_bounds__(kBlock) void spmv_window_starts(const int32_t* __restrict__ rp, int64_t rows,
                                                              int32_t windows, int32_t* __restrict__ row_start) {
-  const int64_t k = blockIdx.x * (int64_t)kBlock + threadIdx.x;
-  if (k > windows) return;
-  if (k == windows) {
-    row_start[k] = (int32_t)rows;
-    return;
-  }
-  const int64_t target = k * (int64_t)kWindow;
-  int64_t lo = 0, hi = rows;  // search rp[0..rows]
-  while (lo < hi) {
-    const int64_t mid = (lo + hi) >> 1;
-    if ((int64_t)rp[mid] < target) lo = mid + 1; else hi = mid;
-  }
-  row_start[k] = (int32_t)lo;
-}
-
-// Appends every row longer than kLongRow to `list`. One atomic per wave (ballot + mbcnt give each
-// long row its slot), so the counter is not hammered once per long row.
-__global__ __launch_bounds__(kBlock) void spmv_classify(const int32_t* __restrict__ rp, int64_t rows,
-                                                        int32_t* __restrict__ list, uint32_t* __restrict__ count) {
-  const int64_t stride = (int64_t)gridDim.x * kBlock;
-  const int lane = threadIdx.x & 63;
-  // Every lane of a wave runs the same number of iterations (the bound is rounded up to whole
-  // strides), so the ballot and the broadcast below always see the full wave.
-  const int64_t iters = (rows + stride - 1) / stride;
-  for (int64_t it = 0; it < iters; ++it) {
-    const int64_t r = it * stride + blockIdx.x * (int64_t)kBlock + threadIdx.x;
-    const bool is_long = r < rows && (rp[r + 1] - rp[r] > kLongRow);
-    const uint64_t m = __ballot(is_long);
-    if (m == 0) continue;
-    uint32_t base = 0;
-    if (lane == 0)
-      base = __hip_atomic_fetch_add(count, (uint32_t)__builtin_popcountll(m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
-    if (is_long)
-      list[base + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u))] = (int32_t)r;
-  }
+  const int64_t r = blockIdx.x * (int64_t)kBlock + threadIdx.x;
+  if (r > rows) return;
+  const int64_t cur = rp[r];
+  const int64_t k_lo = r == 0 ? 0 : (int64_t)rp[r - 1] / kWindow + 1;  // first k with k·W > rp[r - 1]
+  const int64_t k_hi = min(cur < 0 ? (int64_t)-1 : cur / kWindow, (int64_t)windows - 1);
+  for (int64_t k = max(k_lo, (int64_t)0); k <= k_hi; ++k) row_start[k] = (int32_t)r;
+  if (r == rows) row_start[windows] = (int32_t)rows;
 }
 
 // Element arithmetic of SparseOps.SpMV<T> (SparseMatrix.cs:669-692) for T = float, double or int:
@@ -82,17 +57,63 @@ __device__ inline int32_t spmv_mul(int32_t a, int32_t b) { return (int32_t)((uin
 template <>
 __device__ inline int32_t spmv_add(int32_t a, int32_t b) { return (int32_t)((uint32_t)a + (uint32_t)b); }
 
+// Sum of the products of nonzeros [b, e) by the whole workgroup (kBlock threads) in a fixed order:
+// thread t adds, pass by pass, the pairwise sum of its four slots t + k·kBlock; then a butterfly
+// across each wave and the waves in index order. Called by every thread; returns the total to
+// thread 0. `red` holds one value per wave.
+template <typename T>
+__device__ T long_row_sum(int32_t b, int32_t e, const int32_t* __restrict__ col, const T* __restrict__ val,
+                          const T* __restrict__ x, T* red) {
+  T sum = T(0);
+  // Four slots per pass: their loads and gathers are independent and overlap.
+  for (int32_t i0 = b + (int32_t)threadIdx.x; i0 < e; i0 += 4 * kBlock) {
+    int32_t c[4];
+    T v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int32_t i = i0 + k * kBlock;
+      c[k] = 0;
+      v[k] = T(0);
+      if (i < e) {
+        c[k] = __builtin_nontemporal_load(col + i);
+        v[k] = __builtin_nontemporal_load(val + i);
+      }
+    }
+    T xv[4], p[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) xv[k] = x[c[k]];  // c = 0 past e: gathered, then dropped below
+#pragma unroll
+    for (int k = 0; k < 4; ++k) p[k] = (i0 + k * kBlock < e) ? spmv_mul(v[k], xv[k]) : T(0);
+    sum = spmv_add(sum, spmv_add(spmv_add(p[0], p[1]), spmv_add(p[2], p[3])));
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) sum = spmv_add(sum, __shfl_xor(sum, off, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = sum;
+  __syncthreads();
+  T total = red[0];
+#pragma unroll
+  for (int w = 1; w < kBlock / dc::kWave; ++w) total = spmv_add(total, red[w]);
+  __syncthreads();  // red is reused by the next call
+  return total;
+}
+
 template <typename T>
 __global__ __launch_bounds__(kBlock) void spmv_windows_kernel(const int32_t* __restrict__ rp, const int32_t* __restrict__ col,
                                                               const T* __restrict__ val, const T* __restrict__ x,
                                                               T* __restrict__ y,
-                                                              const int32_t* __restrict__ row_start) {
+                                                              const int32_t* __restrict__ row_start, int32_t rows) {
   __shared__ T s_prod[kWindow + kLongRow];
-  const int32_t r0 = row_start[blockIdx.x], r1 = row_start[blockIdx.x + 1];
+  __shared__ int32_t s_long[kMaxLongPerWindow];
+  __shared__ uint32_t s_nlong;
+  __shared__ T s_red[kBlock / dc::kWave];
+  // (clamped: with row pointers that are not monotone an entry may be stale; the rows read stay
+  // inside [0, rows])
+  const int32_t r0 = min(max(row_start[blockIdx.x], 0), rows), r1 = min(max(row_start[blockIdx.x + 1], 0), rows);
   if (r0 >= r1) return;  // uniform across the workgroup: no row starts in this window
+  if (threadIdx.x == 0) s_nlong = 0;
   const int32_t b = rp[r0];
   const int32_t last_begin = rp[r1 - 1], last_end = rp[r1];
-  // The last row may run past the window; if it is long it belongs to the long-row pass.
+  // The last row may run past the window; if it is long it is summed after the short rows.
   int32_t e = (last_end - last_begin > kLongRow) ? last_begin : last_end;
   e = min(e, b + kWindow + kLongRow);  // a well-formed CSR never needs this clamp; it keeps LDS in bounds
   // All column/value loads of this thread's slots go out first, then all x gathers, so a window
@@ -122,57 +143,22 @@ __global__ __launch_bounds__(kBlock) void spmv_windows_kernel(const int32_t* __r
   __syncthreads();
   for (int32_t r = r0 + (int32_t)threadIdx.x; r < r1; r += kBlock) {
     const int32_t rb = rp[r], re = rp[r + 1];
-    if (re - rb > kLongRow) continue;
+    if (re - rb > kLongRow) {
+      const uint32_t slot = atomicAdd(&s_nlong, 1u);
+      if (slot < (uint32_t)kMaxLongPerWindow) s_long[slot] = r;  // more only with malformed row pointers
+      continue;
+    }
     T sum = T(0);
     const int32_t i0 = max(rb - b, 0), i1 = min(re - b, e - b);
     for (int32_t i = i0; i < i1; ++i) sum = spmv_add(sum, s_prod[i]);
     __builtin_nontemporal_store(sum, y + r);
   }
-}
-
-template <typename T>
-__global__ __launch_bounds__(kLongBlock) void spmv_long_rows(const int32_t* __restrict__ rp, const int32_t* __restrict__ col,
-                                                             const T* __restrict__ val, const T* __restrict__ x,
-                                                             T* __restrict__ y, const int32_t* __restrict__ list,
-                                                             const uint32_t* __restrict__ count) {
-  __shared__ T lds[kLongBlock / dc::kWave];
-  const uint32_t n_long = *count;
-  for (uint32_t t = blockIdx.x; t < n_long; t += gridDim.x) {
-    const int32_t row = list[t];
-    const int32_t b = rp[row], e = rp[row + 1];
-    T sum = T(0);
-    // Four slots per pass: their loads and gathers are independent and overlap.
-    for (int32_t i0 = b + (int32_t)threadIdx.x; i0 < e; i0 += 4 * kLongBlock) {
-      int32_t c[4];
-      T v[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int32_t i = i0 + k * kLongBlock;
-        c[k] = 0;
-        v[k] = T(0);
-        if (i < e) {
-          c[k] = __builtin_nontemporal_load(col + i);
-          v[k] = __builtin_nontemporal_load(val + i);
-        }
-      }
-      T xv[4], p[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) xv[k] = x[c[k]];  // c = 0 past e: gathered, then dropped below
-#pragma unroll
-      for (int k = 0; k < 4; ++k) p[k] = (i0 + k * kLongBlock < e) ? spmv_mul(v[k], xv[k]) : T(0);
-      sum = spmv_add(sum, spmv_add(spmv_add(p[0], p[1]), spmv_add(p[2], p[3])));
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) sum = spmv_add(sum, __shfl_xor(sum, off, 64));
-    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = sum;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      T total = lds[0];
-#pragma unroll
-      for (int w = 1; w < kLongBlock / dc::kWave; ++w) total = spmv_add(total, lds[w]);
-      y[row] = total;
-    }
-    __syncthreads();
+  __syncthreads();
+  const uint32_t n_long = min(s_nlong, (uint32_t)kMaxLongPerWindow);  // uniform
+  for (uint32_t t = 0; t < n_long; ++t) {
+    const int32_t row = s_long[t];
+    const T total = long_row_sum(rp[row], rp[row + 1], col, val, x, s_red);
+    if (threadIdx.x == 0) y[row] = total;
   }
 }
 
@@ -187,38 +173,27 @@ __global__ __launch_bounds__(kBlock) void normalise_kernel(const float* y, float
 
 struct SpmvPlan {
   int32_t windows;
-  size_t list_cap;
 };
 
 SpmvPlan make_plan(int64_t nnz) {
   SpmvPlan p;
   p.windows = (int32_t)(nnz / kWindow + 1);  // every first-nonzero index in [0, nnz] has a window
-  p.list_cap = (size_t)(nnz / (kLongRow + 1) + 1);
   return p;
 }
 
-// Analysis: window starts and the long-row list (once per matrix in the power iteration).
+// Analysis: the window starts (one pass over the row pointers).
 int32_t launch_analysis(dc_hip_ctx* ctx, const SpmvPlan& plan, const int32_t* rp, int64_t rows) {
-  DC_RETURN_IF(dc::ensure_spmv_rows(ctx, plan.list_cap));
   DC_RETURN_IF(dc::ensure_spmv_windows(ctx, (size_t)plan.windows + 1));
-  uint32_t* count = ctx->counters + DC_SLOT_SPMV_LONG;
-  DC_RETURN_IF(dc::zero_async(ctx, count, sizeof(uint32_t)));
-  const unsigned wgrid = (unsigned)((plan.windows + 1 + kBlock - 1) / kBlock);
-  spmv_window_starts<<<wgrid, kBlock, 0, ctx->stream>>>(rp, rows, plan.windows, ctx->spmv_windows);
-  DC_RETURN_IF(dc::last_launch_status());
-  const unsigned grid = (unsigned)std::max<int64_t>(1, std::min<int64_t>((rows + kBlock - 1) / kBlock, 16384));
-  spmv_classify<<<grid, kBlock, 0, ctx->stream>>>(rp, rows, ctx->spmv_rows, count);
+  const unsigned grid = (unsigned)((rows + 1 + kBlock - 1) / kBlock);
+  spmv_window_starts<<<grid, kBlock, 0, ctx->stream>>>(rp, rows, plan.windows, ctx->spmv_windows);
   return dc::last_launch_status();
 }
 
 template <typename T>
 int32_t launch_spmv(dc_hip_ctx* ctx, const SpmvPlan& plan, const int32_t* rp, const int32_t* col, const T* val,
-                    const T* x, T* y) {
-  spmv_windows_kernel<T><<<(unsigned)plan.windows, kBlock, 0, ctx->stream>>>(rp, col, val, x, y, ctx->spmv_windows);
-  DC_RETURN_IF(dc::last_launch_status());
-  const unsigned lgrid = (unsigned)std::max<size_t>(1, std::min<size_t>(plan.list_cap, 2048));
-  spmv_long_rows<T><<<lgrid, kLongBlock, 0, ctx->stream>>>(rp, col, val, x, y, ctx->spmv_rows,
-                                                        ctx->counters + DC_SLOT_SPMV_LONG);
+                    const T* x, T* y, int64_t rows) {
+  spmv_windows_kernel<T><<<(unsigned)plan.windows, kBlock, 0, ctx->stream>>>(rp, col, val, x, y, ctx->spmv_windows,
+                                                                             (int32_t)rows);
   return dc::last_launch_status();
 }
 
@@ -1047,7 +1022,7 @@ int32_t spmv_csr(dc_hip_ctx* ctx, const int32_t* row_pointers, const int32_t* co
   if (rows == 0) return DC_OK;
   const SpmvPlan plan = make_plan(nnz);
   DC_RETURN_IF(launch_analysis(ctx, plan, row_pointers, rows));
-  return launch_spmv(ctx, plan, row_pointers, col_indices, values, x, y);
+  return launch_spmv(ctx, plan, row_pointers, col_indices, values, x, y, rows);
 }
 
 int32_t check_plan_shape(int64_t rows, int64_t cols, int64_t nnz) {
