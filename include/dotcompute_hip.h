@@ -463,6 +463,10 @@ DC_HIP_API int32_t dc_hip_convert_f32_to_bf16(dc_hip_ctx* ctx, const float* inpu
  * src/Extensions/DotCompute.Algorithms/Sparse/SparseMatrix.cs:68-272,669-692; the never-launched
  * CUDA string kernel Kernels/LinearAlgebra/SparseMatrixKernels.cs:47-75).
  * row_pointers has rows+1 entries (int32 offsets, as CsrMatrix<T>); x has cols entries.
+ * The matrix must be a valid CSR: row_pointers non-decreasing from 0 to nnz and every column index
+ * in [0, cols) (the host CsrMatrix checks both, as the reference's does its sizes); these one-shot
+ * entry points read what the indices point at without checking them. The plan entry points below
+ * clamp every index instead.
  * ------------------------------------------------------------------------------------------- */
 DC_HIP_API int32_t dc_hip_spmv_csr_f32(dc_hip_ctx* ctx, const int32_t* row_pointers,
                                        const int32_t* col_indices, const float* values,
