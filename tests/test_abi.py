@@ -98,7 +98,7 @@ def test_code_object_ships_next_to_the_library():
     assert hip.load().dc_hip_default_module_path().decode().endswith("dc_kernels_gfx950.hsaco")
 
 
-# C# layouts written in INTEGRATION.md ([StructLayout(LayoutKind.Sequential)], natural alignment):
+# The C# struct layouts a managed binding declares ([StructLayout(LayoutKind.Sequential)], natural alignment):
 # field -> (offset, size). The C header must place every field exactly there.
 CSHARP_LAYOUTS = {
     "dc_hip_device_info": (376, [
