@@ -64,6 +64,13 @@ inline bool program_uses_saves(const dc_linq_chain& prog) {
   return false;
 }
 
+// True when the program calls a library operation (POW / RPOW: the LIBM interpreter variant).
+inline bool program_uses_libm(const dc_linq_chain& prog) {
+  for (int i = 0; i < prog.n_instr; ++i)
+    if (prog.code[i].op == DC_LQ_POW || prog.code[i].op == DC_LQ_RPOW) return true;
+  return false;
+}
+
 // ---- decoupled lookback -------------------------------------------------------------------------
 // Status word: [63:62] flag (0 invalid, 1 aggregate, 2 inclusive prefix) | [61:40] epoch |
 // [39:0] value. A word whose epoch differs from the launch's counts as invalid.
@@ -223,7 +230,8 @@ inline ReducePlan reduce_plan(const dc_linq_chain& prog) {
   ReducePlan p{};
   p.k = RdConst{0.0f, 1.0f, -0.0f};
   int shape = 0, cmp = DC_LQ_CMP_GT;
-  if (!lower_affine(prog, &p.aff)) p.mode = program_uses_saves(prog) ? kRdInterpSaves : kRdInterp;
+  if (!lower_affine(prog, &p.aff))
+    p.mode = program_uses_libm(prog) ? kRdInterpLibm : program_uses_saves(prog) ? kRdInterpSaves : kRdInterp;
   else if (lower_canon2(p.aff, &shape, &cmp, &p.k)) p.mode = rd_canon(shape, cmp);
   else p.mode = kRdAffine;
   return p;
@@ -241,6 +249,7 @@ void rd_dispatch(int mode, F&& f) {
     f(std::integral_constant<int, (m)>{}); \
     return;
     DC_RD_CASE(kRdInterpSaves)
+    DC_RD_CASE(kRdInterpLibm)
     DC_RD_CASE(kRdAffine)
     DC_RD_CASE(rd_canon(kShapeM, DC_LQ_CMP_GT))
     DC_RD_CMP_MODES(DC_RD_CASE, kShapeF)
@@ -308,7 +317,9 @@ __device__ inline uint64_t apply_program(const dc_linq_chain& prog, const Affine
       float sub[kChunk];
 #pragma unroll
       for (int i = 0; i < kChunk; ++i) sub[i] = e[c * kChunk + i];
-      keep |= (uint64_t)run_program_f32<kChunk, MODE == kModeInterpSaves>(prog, sub) << (c * kChunk);
+      keep |= (uint64_t)run_program_f32<kChunk, MODE == kModeInterpSaves || MODE == kModeInterpLibm,
+                                        MODE == kModeInterpLibm>(prog, sub)
+              << (c * kChunk);
 #pragma unroll
       for (int i = 0; i < kChunk; ++i) e[c * kChunk + i] = sub[i];
     }
@@ -1186,7 +1197,7 @@ const void* rounds_kernel(int mode) {
 
 // Every program variant (rd_dispatch's and rd_dispatch_i32's cases).
 std::vector<int> all_reduce_modes() {
-  std::vector<int> m = {kRdInterp, kRdInterpSaves, kRdAffine, kRdInterpI32, kRdInterpI32Saves,
+  std::vector<int> m = {kRdInterp, kRdInterpSaves, kRdInterpLibm, kRdAffine, kRdInterpI32, kRdInterpI32Saves,
                         rd_canon(kShapeM, DC_LQ_CMP_GT)};
   for (int shape : {kShapeF, kShapeFM, kShapeMF})
     for (int cmp = DC_LQ_CMP_GT; cmp <= DC_LQ_CMP_NE; ++cmp) m.push_back(rd_canon(shape, cmp));
@@ -1274,7 +1285,7 @@ int32_t launch_to_array(dc_hip_ctx* ctx, const dc_linq_chain* chain, bool is_int
     // (dc::linq_jit_rounds). Switched off: a compiled kernel for a filtered division faulted the
     // device and its cause is not found yet, so every program runs on the interpreter.
     hipFunction_t jit = nullptr;
-    const bool interpreted = is_int || plan.mode == kRdInterp || plan.mode == kRdInterpSaves;
+    const bool interpreted = is_int || rd_is_float_interp(plan.mode);
     if (kLaunchCompiled && interpreted && n >= DC_LINQ_COMPILE_MIN_ELEMENTS &&
         (chain->flags & DC_LINQ_FLAG_INTERPRET) == 0) {
       jit = dc::linq_jit_rounds(ctx, *chain, is_int);
@@ -1320,13 +1331,16 @@ int32_t launch_to_array(dc_hip_ctx* ctx, const dc_linq_chain* chain, bool is_int
   const bool saves = program_uses_saves(*chain);
   const bool affine = !is_int && lower_affine(*chain, &aff);
   const int mode = is_int ? (saves ? kModeInterpI32Saves : kModeInterpI32)
-                          : affine ? kModeAffine : (saves ? kModeInterpSaves : kModeInterp);
+                  : affine ? kModeAffine
+                  : program_uses_libm(*chain) ? kModeInterpLibm
+                                              : (saves ? kModeInterpSaves : kModeInterp);
   const int64_t tiles = std::max<int64_t>(1, (n + kTile - 1) / kTile);
   if (tiles > 0x7FFFFFFFll) return DC_ERR_INVALID_ARGUMENT;
   uint32_t epoch = 0;
   DC_RETURN_IF(dc::ensure_status(ctx, (size_t)tiles, &epoch));
   auto kernel = mode == kModeAffine            ? where_select_kernel<kModeAffine>
               : mode == kModeInterpSaves       ? where_select_kernel<kModeInterpSaves>
+              : mode == kModeInterpLibm        ? where_select_kernel<kModeInterpLibm>
               : mode == kModeInterpI32         ? where_select_kernel<kModeInterpI32>
               : mode == kModeInterpI32Saves    ? where_select_kernel<kModeInterpI32Saves>
                                                : where_select_kernel<kModeInterp>;
@@ -1337,12 +1351,14 @@ int32_t launch_to_array(dc_hip_ctx* ctx, const dc_linq_chain* chain, bool is_int
   return dc::last_launch_status();
 }
 
-// Structural validation plus the int32 rule: no SQRT / FLOOR / CEIL / ROUND (no int form).
+// Structural validation plus the int32 rule: no SQRT / FLOOR / CEIL / ROUND / POW (no int form).
 int32_t validate_i32(const dc_linq_chain* chain) {
   DC_RETURN_IF(dc_linq_chain_validate(chain));
   for (int i = 0; i < chain->n_instr; ++i) {
     const uint8_t op = chain->code[i].op;
-    if (op == DC_LQ_SQRT || op == DC_LQ_FLOOR || op == DC_LQ_CEIL || op == DC_LQ_ROUND) return DC_ERR_UNSUPPORTED;
+    if (op == DC_LQ_SQRT || op == DC_LQ_FLOOR || op == DC_LQ_CEIL || op == DC_LQ_ROUND || op == DC_LQ_POW ||
+        op == DC_LQ_RPOW)
+      return DC_ERR_UNSUPPORTED;
   }
   return DC_OK;
 }
@@ -1369,7 +1385,7 @@ DC_HIP_API int32_t dc_linq_chain_validate(const dc_linq_chain* chain) {
     return DC_ERR_INVALID_ARGUMENT;
   for (int i = 0; i < chain->n_instr; ++i) {
     const dc_linq_instr& in = chain->code[i];
-    const bool op_ok = (in.op <= DC_LQ_ROUND) || (in.op >= DC_LQ_CMP_GT && in.op <= DC_LQ_MAP);
+    const bool op_ok = (in.op <= DC_LQ_ROUND) || (in.op >= DC_LQ_CMP_GT && in.op <= DC_LQ_RPOW);
     if (!op_ok || in.src > DC_LQ_SRC_S1) return DC_ERR_UNSUPPORTED;
     if (in.op >= DC_LQ_CMP_GT && in.op <= DC_LQ_CMP_NE && in.mode > DC_LQ_CMP_OR) return DC_ERR_UNSUPPORTED;
   }

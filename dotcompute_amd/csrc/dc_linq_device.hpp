@@ -89,6 +89,11 @@ __device__ __attribute__((always_inline)) inline void note_fault(Faults& f, int 
 // C#'s float % (truncated remainder, exact). Kept out of line: a program with a remainder is rare,
 // and fmodf inlined into every unrolled interpreter loop would bloat each kernel variant.
 __device__ __attribute__((noinline)) float net_rem(float a, float b) { return ::fmodf(a, b); }
+// MathF.Pow: the device library's powf (the C99 Annex F special values, as .NET Core's MathF.Pow),
+// out of line for the same reason. Only the LIBM interpreter variant has it: its call sites change
+// the register allocation of a kernel (a few reloads from scratch in the round-robin kernel's
+// write-out), which the programs without it should not pay.
+__device__ __attribute__((noinline)) float net_pow(float a, float b) { return ::powf(a, b); }
 
 __device__ inline int32_t wrap_add(int32_t a, int32_t b) { return (int32_t)((uint32_t)a + (uint32_t)b); }
 __device__ inline int32_t wrap_sub(int32_t a, int32_t b) { return (int32_t)((uint32_t)a - (uint32_t)b); }
@@ -113,9 +118,9 @@ __device__ __attribute__((always_inline)) inline int32_t checked_rem(int32_t a, 
 // instructions fetched at run time; a kernel compiled at run time for one program feeds it
 // constants, and the compiler then drops every branch on the instruction, so both compute the same.
 // SAVES = false drops the s0/s1 registers for programs that never use them (the common case),
-// which keeps the kernels at a higher occupancy. Operands are read in place (an immediate stays a
+// which keeps the kernels at a higher occupancy. LIBM = true adds POW / RPOW (float32 only). Operands are read in place (an immediate stays a
 // scalar operand of the vector instruction), so no per-element operand copy is materialised.
-template <typename T, int EPT, bool SAVES>
+template <typename T, int EPT, bool SAVES, bool LIBM = false>
 struct ProgramState {
   T v[EPT];
   T s0[SAVES ? EPT : 1], s1[SAVES ? EPT : 1];
@@ -268,6 +273,12 @@ struct ProgramState {
           for (int j = 0; j < EPT; ++j) v[j] = __builtin_rintf(v[j]);  // ties to even, as MathF.Round
         }
         break;
+      case DC_LQ_POW:
+        if constexpr (!kInt && LIBM) DC_LQ_APPLY(v[j] = net_pow(v[j], O));
+        break;
+      case DC_LQ_RPOW:
+        if constexpr (!kInt && LIBM) DC_LQ_APPLY(v[j] = net_pow(O, v[j]));
+        break;
       case DC_LQ_STORE_S0:
         if (SAVES) {
 #pragma unroll
@@ -307,10 +318,10 @@ struct ProgramState {
 };
 
 // Runs the program over the EPT elements of one thread; returns the keep mask.
-template <typename T, int EPT, bool SAVES>
+template <typename T, int EPT, bool SAVES, bool LIBM = false>
 __device__ __attribute__((always_inline)) inline uint32_t run_program(const dc_linq_chain& prog, T (&e)[EPT],
                                                                        uint32_t live, Faults& f) {
-  ProgramState<T, EPT, SAVES> st(live);
+  ProgramState<T, EPT, SAVES, LIBM> st(live);
   const int n = prog.n_instr;
   // The next instruction's scalar load is issued before the current one runs, so its latency
   // overlaps the work of the current instruction instead of stalling the dispatch.
@@ -324,10 +335,10 @@ __device__ __attribute__((always_inline)) inline uint32_t run_program(const dc_l
 }
 
 // Float programs (no exceptions), every element present.
-template <int EPT, bool SAVES>
+template <int EPT, bool SAVES, bool LIBM = false>
 __device__ __attribute__((always_inline)) inline uint32_t run_program_f32(const dc_linq_chain& prog, float (&e)[EPT]) {
   Faults none;
-  return run_program<float, EPT, SAVES>(prog, e, (EPT == 32) ? 0xFFFFFFFFu : ((1u << EPT) - 1u), none);
+  return run_program<float, EPT, SAVES, LIBM>(prog, e, (EPT == 32) ? 0xFFFFFFFFu : ((1u << EPT) - 1u), none);
 }
 
 // An int32 program over elements held as float bit patterns (the kernels move 32-bit words and
@@ -411,7 +422,9 @@ __device__ inline uint64_t run_affine(const AffineChain& ch, float (&e)[EPT]) {
   return keep;
 }
 
-enum ProgramMode : int { kModeInterp = 0, kModeInterpSaves = 1, kModeAffine = 2, kModeInterpI32 = 3, kModeInterpI32Saves = 4 };
+// kModeInterpLibm: the float interpreter with save registers and the library operations (POW).
+enum ProgramMode : int { kModeInterp = 0, kModeInterpSaves = 1, kModeAffine = 2, kModeInterpI32 = 3, kModeInterpI32Saves = 4,
+                         kModeInterpLibm = 5 };
 constexpr bool mode_is_int(int m) { return m == kModeInterpI32 || m == kModeInterpI32Saves; }
 
 // ---- one- and two-stage affine chains -------------------------------------------------------------
@@ -432,10 +445,12 @@ struct RdConst {
 // affine chains with the shape and comparison fixed at compile time. Canonical modes are
 // kRdCanon + 8 * shape + (comparison - DC_LQ_CMP_GT).
 // kRdInterpI32 / kRdInterpI32Saves: the int32 interpreter (programs over int32 elements).
+// kRdInterpLibm: the float interpreter with save registers and the library operations (POW).
 // kRdJit: the program compiled into the kernel at run time (dc_linq_jit.hip).
 enum ReduceMode : int { kRdInterp = 0, kRdInterpSaves = 1, kRdAffine = 2, kRdInterpI32 = 3, kRdInterpI32Saves = 4,
-                        kRdJit = 8, kRdCanon = 16 };
+                        kRdInterpLibm = 5, kRdJit = 8, kRdCanon = 16 };
 constexpr bool rd_is_int(int rd) { return rd == kRdInterpI32 || rd == kRdInterpI32Saves; }
+constexpr bool rd_is_float_interp(int rd) { return rd == kRdInterp || rd == kRdInterpSaves || rd == kRdInterpLibm; }
 constexpr int rd_canon(int shape, int cmp) { return kRdCanon + 8 * shape + (cmp - DC_LQ_CMP_GT); }
 constexpr bool rd_is_canon(int rd) { return rd >= kRdCanon; }
 constexpr int rd_shape(int rd) { return (rd - kRdCanon) >> 3; }
@@ -474,7 +489,7 @@ __device__ __attribute__((always_inline)) inline void apply_reduce_flags(const d
   } else {
     uint32_t keep;
     if constexpr (RD == kRdAffine) keep = (uint32_t)run_affine<EPT>(aff, e);
-    else keep = run_program_f32<EPT, RD == kRdInterpSaves>(prog, e);
+    else keep = run_program_f32<EPT, RD == kRdInterpSaves || RD == kRdInterpLibm, RD == kRdInterpLibm>(prog, e);
 #pragma unroll
     for (int j = 0; j < EPT; ++j) kept[j] = ((keep >> j) & 1u) != 0u;
   }
@@ -490,7 +505,7 @@ template <int RD, int EPT, int CHUNK = EPT>
 __device__ __attribute__((always_inline)) inline void eval_flags(const dc_linq_chain& prog, const AffineChain& aff,
                                                                  const RdConst& k, float (&e)[EPT], bool (&kept)[EPT],
                                                                  uint32_t live, Faults& f) {
-  constexpr bool kInterp = rd_is_int(RD) || RD == kRdInterp || RD == kRdInterpSaves;
+  constexpr bool kInterp = rd_is_int(RD) || rd_is_float_interp(RD);
   constexpr int kInterpChunk = CHUNK;
   if constexpr (kInterp && EPT > kInterpChunk) {
     static_assert(EPT % kInterpChunk == 0, "whole chunks");
@@ -664,7 +679,7 @@ __device__ __attribute__((always_inline)) inline void rounds_body(
     if constexpr (kLazyMap) {
 #pragma unroll
       for (int j = 0; j < kRrEpt; ++j) kept[j] = rd_compare<rd_cmp(RD)>(e[j], canon.t);
-    } else if constexpr (kIntProg || RD == kRdInterp || RD == kRdInterpSaves || RD == kRdJit) {
+    } else if constexpr (kIntProg || rd_is_float_interp(RD) || RD == kRdJit) {
       Faults f;
       eval_program<RD, Gen, kRrEpt, kRrEpt / 2>(prog, aff, canon, e, kept, live, f);
       if constexpr (kIntProg) {

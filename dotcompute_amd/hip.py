@@ -48,6 +48,7 @@ DC_LINQ_MAX_INSTR = 48
 NOP, LOAD, ADD, SUB, RSUB, MUL, DIV, RDIV, MIN, MAX, NEG, ABS, SQRT, STORE_S0, STORE_S1 = range(15)
 REM, RREM, FLOOR, CEIL, ROUND = range(15, 20)
 CMP_GT, CMP_GE, CMP_LT, CMP_LE, CMP_EQ, CMP_NE, PNOT, PSTORE, PAND_Q, POR_Q, FILTER, MAP = range(20, 32)
+POW, RPOW = range(32, 34)
 # dc_linq_src
 SRC_IMM, SRC_ELEM, SRC_S0, SRC_S1 = range(4)
 # dc_linq_cmp_mode

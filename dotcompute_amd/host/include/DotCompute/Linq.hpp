@@ -31,7 +31,7 @@ namespace DotCompute::Linq {
 enum class ExprKind {
   Parameter, Constant,
   Negate, Abs, Sqrt, Floor, Ceiling, Round,
-  Add, Subtract, Multiply, Divide, Modulo, Min, Max,
+  Add, Subtract, Multiply, Divide, Modulo, Min, Max, Pow,
   GreaterThan, GreaterThanOrEqual, LessThan, LessThanOrEqual, Equal, NotEqual,
   AndAlso, OrElse, Not
 };
@@ -87,6 +87,7 @@ Expr Ceiling(const Expr& a);
 Expr Round(const Expr& a);  // MidpointRounding.ToEven
 Expr Min(const Expr& a, const Expr& b);
 Expr Max(const Expr& a, const Expr& b);
+Expr Pow(const Expr& a, const Expr& b);  // the C runtime's powf, as .NET's MathF.Pow
 }  // namespace MathF
 namespace Math {  // System.Math members over int (Math.Abs(int.MinValue) throws OverflowException)
 Expr Abs(const Expr& a);

@@ -117,6 +117,7 @@ std::string Expr::ToString() const {
     case ExprKind::Modulo: return "(" + L() + " % " + R() + ")";
     case ExprKind::Min: return "Min(" + L() + ", " + R() + ")";
     case ExprKind::Max: return "Max(" + L() + ", " + R() + ")";
+    case ExprKind::Pow: return "MathF.Pow(" + L() + ", " + R() + ")";
     case ExprKind::GreaterThan: return "(" + L() + " > " + R() + ")";
     case ExprKind::GreaterThanOrEqual: return "(" + L() + " >= " + R() + ")";
     case ExprKind::LessThan: return "(" + L() + " < " + R() + ")";
@@ -158,6 +159,7 @@ Expr Ceiling(const Expr& a) { return Expr(MakeNode(ExprKind::Ceiling, a.Ptr()));
 Expr Round(const Expr& a) { return Expr(MakeNode(ExprKind::Round, a.Ptr())); }
 Expr Min(const Expr& a, const Expr& b) { return Expr(MakeNode(ExprKind::Min, a.Ptr(), b.Ptr())); }
 Expr Max(const Expr& a, const Expr& b) { return Expr(MakeNode(ExprKind::Max, a.Ptr(), b.Ptr())); }
+Expr Pow(const Expr& a, const Expr& b) { return Expr(MakeNode(ExprKind::Pow, a.Ptr(), b.Ptr())); }
 }  // namespace MathF
 
 namespace Math {
@@ -244,12 +246,14 @@ uint8_t ArithOp(ExprKind k) {
     case ExprKind::Modulo: return DC_LQ_REM;
     case ExprKind::Min: return DC_LQ_MIN;
     case ExprKind::Max: return DC_LQ_MAX;
+    case ExprKind::Pow: return DC_LQ_POW;
     default: throw NotSupportedException("not an arithmetic node");
   }
 }
 
 // Operation with its operands swapped (v = operand OP v): exact for +, *, min, max (IEEE + and *
-// commute, as do wrapping int + and *; Min/Max are symmetric), and via RSUB/RDIV/RREM for -, /, %.
+// commute, as do wrapping int + and *; Min/Max are symmetric), and via RSUB/RDIV/RREM/RPOW for -, /,
+// % and Pow.
 uint8_t ReversedArithOp(ExprKind k) {
   switch (k) {
     case ExprKind::Add: return DC_LQ_ADD;
@@ -259,6 +263,7 @@ uint8_t ReversedArithOp(ExprKind k) {
     case ExprKind::Subtract: return DC_LQ_RSUB;
     case ExprKind::Divide: return DC_LQ_RDIV;
     case ExprKind::Modulo: return DC_LQ_RREM;
+    case ExprKind::Pow: return DC_LQ_RPOW;
     default: throw NotSupportedException("not an arithmetic node");
   }
 }
@@ -277,7 +282,7 @@ uint8_t CompareOp(ExprKind k, bool swapped) {
 
 bool IsBinaryArith(ExprKind k) {
   return k == ExprKind::Add || k == ExprKind::Subtract || k == ExprKind::Multiply || k == ExprKind::Divide ||
-         k == ExprKind::Modulo || k == ExprKind::Min || k == ExprKind::Max;
+         k == ExprKind::Modulo || k == ExprKind::Min || k == ExprKind::Max || k == ExprKind::Pow;
 }
 
 struct Compiler {
@@ -357,6 +362,9 @@ struct Compiler {
     }
     if (!IsBinaryArith(n.Kind))
       throw NotSupportedException("a boolean expression cannot be used as a value in the HIP kernels");
+    if (is_int && n.Kind == ExprKind::Pow)
+      throw NotSupportedException("MathF.Pow of an int converts it to float; the fused HIP kernels keep one "
+                                  "element type per chain");
     if (RightIsOperand(n)) {
       Value(*n.Left, free_save);
       auto [src, imm] = LeafSource(*n.Right);
@@ -477,6 +485,8 @@ const char* OpName(uint8_t op) {
     case DC_LQ_FLOOR: return "FLOOR";
     case DC_LQ_CEIL: return "CEIL";
     case DC_LQ_ROUND: return "ROUND";
+    case DC_LQ_POW: return "POW";
+    case DC_LQ_RPOW: return "RPOW";
     case DC_LQ_STORE_S0: return "STORE_S0";
     case DC_LQ_STORE_S1: return "STORE_S1";
     case DC_LQ_CMP_GT: return "CMP_GT";
@@ -497,7 +507,7 @@ const char* OpName(uint8_t op) {
 
 bool HasOperand(uint8_t op) {
   return op == DC_LQ_LOAD || (op >= DC_LQ_ADD && op <= DC_LQ_MAX) || op == DC_LQ_REM || op == DC_LQ_RREM ||
-         (op >= DC_LQ_CMP_GT && op <= DC_LQ_CMP_NE);
+         (op >= DC_LQ_CMP_GT && op <= DC_LQ_CMP_NE) || op == DC_LQ_POW || op == DC_LQ_RPOW;
 }
 
 }  // namespace

@@ -235,7 +235,7 @@ DC_HIP_API int32_t dc_hip_reduce_sum_i32(dc_hip_ctx* ctx, const int32_t* input, 
  * Program model. Per element the kernel holds: e (the pipeline element), v (accumulator), s0, s1
  * (saved values), p and q (predicate registers) and k (keep flag, initially true).
  * Each instruction: op, src (operand source), imm (constant operand).
- *   value ops   v = f(v, operand)         LOAD ADD SUB RSUB MUL DIV RDIV REM RREM MIN MAX
+ *   value ops   v = f(v, operand)         LOAD ADD SUB RSUB MUL DIV RDIV REM RREM MIN MAX POW RPOW
  *               v = f(v)                  NEG ABS SQRT FLOOR CEIL ROUND
  *   STORE_S0/1  s0/s1 = v
  *   CMP_*       c = (v <cmp> operand); p = c (mode SET), p && c (AND), p || c (OR)
@@ -246,12 +246,16 @@ DC_HIP_API int32_t dc_hip_reduce_sum_i32(dc_hip_ctx* ctx, const int32_t* input, 
  * float32 programs: every operation rounds once to float32 (no contraction), matching .NET's
  *   scalar float arithmetic, so outputs are bit-identical to LINQ-to-objects for the same lambdas.
  *   REM is C#'s float `%` (truncated remainder, exact, the sign of the dividend); FLOOR, CEIL and
- *   ROUND are MathF.Floor, MathF.Ceiling and MathF.Round (ties to even).
+ *   ROUND are MathF.Floor, MathF.Ceiling and MathF.Round (ties to even). POW / RPOW are MathF.Pow
+ *   (v = Pow(v, operand) / Pow(operand, v); the reference maps Pow to `pow`,
+ *   CudaKernelGenerator.cs:1380): the device library's powf, within 1 ulp of the exact value as the
+ *   C runtime's powf that .NET calls is, so results may differ from LINQ-to-objects by up to 2 ulp;
+ *   special values (NaN, infinities, signed zeros) follow IEEE 754 / C99 Annex F, as .NET's.
  * int32 programs: C# `int` arithmetic in an unchecked context. + - * and NEG wrap; DIV/RDIV and
  *   REM/RREM truncate toward zero and throw on a zero divisor (DivideByZeroException) and on
  *   int.MinValue divided by -1 (OverflowException, as .NET on x64 also does for %); ABS is
- *   Math.Abs (OverflowException for int.MinValue); MIN/MAX are Math.Min/Max. SQRT, FLOOR, CEIL and
- *   ROUND have no int32 form (DC_ERR_UNSUPPORTED). A throwing operation is evaluated only for
+ *   Math.Abs (OverflowException for int.MinValue); MIN/MAX are Math.Min/Max. SQRT, FLOOR, CEIL,
+ *   ROUND, POW and RPOW have no int32 form (DC_ERR_UNSUPPORTED). A throwing operation is evaluated only for
  *   elements still kept at that point of the chain, as LINQ-to-objects evaluates a Select only for
  *   the elements its Where passed; the kernels report the first element (in sequence order) that
  *   throws through `fault_out` (below) instead of an output.
@@ -290,7 +294,9 @@ enum dc_linq_op {
   DC_LQ_PAND_Q = 28,
   DC_LQ_POR_Q = 29,
   DC_LQ_FILTER = 30,
-  DC_LQ_MAP = 31
+  DC_LQ_MAP = 31,
+  DC_LQ_POW = 32,  /* float32 only: v = MathF.Pow(v, operand) */
+  DC_LQ_RPOW = 33  /* float32 only: v = MathF.Pow(operand, v) */
 };
 
 enum dc_linq_src {
@@ -328,7 +334,7 @@ typedef struct dc_linq_chain {
 
 /* Checks a program for structural validity (opcodes, operand sources, length). */
 DC_HIP_API int32_t dc_linq_chain_validate(const dc_linq_chain* chain);
-/* The same for an int32 program (which has no SQRT, FLOOR, CEIL or ROUND: DC_ERR_UNSUPPORTED). */
+/* The same for an int32 program (which has no SQRT, FLOOR, CEIL, ROUND, POW or RPOW: DC_ERR_UNSUPPORTED). */
 DC_HIP_API int32_t dc_linq_chain_validate_i32(const dc_linq_chain* chain);
 
 /* Run-time compilation (replaces the NVRTC path of CudaRuntimeKernelCompiler.CompileAsync,

@@ -348,6 +348,8 @@ int32_t oracle_linq_eval(const dc_linq_chain* chain, float x, float* y_out) {
       case DC_LQ_FLOOR: v = floorf(v); break;   /* MathF.Floor */
       case DC_LQ_CEIL: v = ceilf(v); break;     /* MathF.Ceiling */
       case DC_LQ_ROUND: v = rintf(v); break;    /* MathF.Round: to nearest, ties to even */
+      case DC_LQ_POW: v = powf(v, o); break;    /* MathF.Pow calls the C runtime's powf */
+      case DC_LQ_RPOW: v = powf(o, v); break;
       case DC_LQ_STORE_S0: s0 = v; break;
       case DC_LQ_STORE_S1: s1 = v; break;
       case DC_LQ_CMP_GT: c = v > o; is_cmp = 1; break;
@@ -461,7 +463,7 @@ int32_t oracle_linq_eval_i32(const dc_linq_chain* chain, int32_t x, int32_t* y_o
       case DC_LQ_POR_Q: p = p || q; break;
       case DC_LQ_FILTER: keep = keep && p; break;
       case DC_LQ_MAP: e = v; break;
-      default: return DC_ERR_UNSUPPORTED; /* SQRT, FLOOR, CEIL, ROUND: no int form */
+      default: return DC_ERR_UNSUPPORTED; /* SQRT, FLOOR, CEIL, ROUND, POW: no int form */
     }
     if (in->op == DC_LQ_DIV || in->op == DC_LQ_RDIV || in->op == DC_LQ_REM || in->op == DC_LQ_RREM) {
       if (den == 0) { if (fault_out) *fault_out = DC_LINQ_FAULT_DIVIDE_BY_ZERO; return 0; }

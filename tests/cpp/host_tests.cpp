@@ -55,6 +55,7 @@ float EvalValue(const ExprNode& n, float x) {
     case ExprKind::Subtract: return EvalValue(*n.Left, x) - EvalValue(*n.Right, x);
     case ExprKind::Multiply: return EvalValue(*n.Left, x) * EvalValue(*n.Right, x);
     case ExprKind::Divide: return EvalValue(*n.Left, x) / EvalValue(*n.Right, x);
+    case ExprKind::Pow: return std::pow(EvalValue(*n.Left, x), EvalValue(*n.Right, x));  // float powf
     case ExprKind::Min: {
       float a = EvalValue(*n.Left, x), b = EvalValue(*n.Right, x);
       if (std::isnan(a) || std::isnan(b)) return NAN;
@@ -354,6 +355,27 @@ TEST_CPU(planner_float_remainder_and_rounding_match_tree_evaluation) {
       CHECK(std::memcmp(&ref, &y, 4) == 0);
     }
   }
+}
+
+TEST_CPU(planner_pow_operand_order_and_element_type) {
+  auto x = Param();
+  // Pow(x, c) keeps c as the operand; Pow(c, x) takes the swapped form; Pow of two computed operands
+  // saves the exponent first.
+  CHECK(Listing(x > 0.0f, MathF::Pow(x, 2.5f)).find("1: CMP_GT 0\n2: FILTER\n3: LOAD e\n4: POW 2.5\n5: MAP") !=
+        std::string::npos);
+  CHECK(Listing(x > 0.0f, MathF::Pow(2.0f, x)).find("4: RPOW 2\n") != std::string::npos);
+  CHECK(Listing(x > 0.0f, MathF::Pow(x + 1.0f, x * 0.5f)).find("POW s0") != std::string::npos);
+  std::vector<float> xs = Uniform(4000, 23);
+  xs.push_back(0.0f);
+  xs.push_back(-0.0f);
+  xs.push_back(NAN);
+  xs.push_back(INFINITY);
+  CheckProgramAgainstTree(MathF::Pow(x, 2.0f) > 0.25f, MathF::Pow(x, 0.5f) + MathF::Pow(3.0f, x), xs);
+  CheckProgramAgainstTree(x != 0.0f, MathF::Pow(x + 1.0f, x * 0.5f) - MathF::Pow(x, x), xs);
+  CHECK(MathF::Pow(x, 2.0f).ToString() == "MathF.Pow(x, 2f)");
+  // MathF.Pow over an int converts to float: another element type than the chain's.
+  auto i = Param();
+  CHECK_THROWS(NotSupportedException, PlanI32(i > 0, MathF::Pow(i, 2)));
 }
 
 // ============================== CPU: runtime, registry, no-device behaviour =======================
@@ -1067,6 +1089,35 @@ TEST_GPU(linq_general_lambdas_match_tree_evaluation) {
     for (float v : src)
       if (EvalPred(c.w.Node(), v)) ref.push_back(EvalValue(c.s.Node(), v));
     CHECK(BitsEqual(AsComputeQueryable(src, p).Where(c.w).Select(c.s).ToArray(), ref));
+  }
+}
+
+TEST_GPU(linq_pow_lambdas_within_two_ulp) {
+  // MathF.Pow is the C runtime's powf on the CPU and the device library's on the GPU, each within
+  // 1 ulp of the exact value: same kept elements (the predicate has no Pow), values within 2 ulp.
+  auto x = Param();
+  auto p = std::make_shared<ComputeQueryProvider>(Gpu());
+  auto src = Uniform(300000, 25, 0);
+  // (x + 2)^x (both operands computed: the exponent goes through a save register) and 0.5^x: one
+  // Pow each, all results positive, so the ulp distance is the difference of the bit patterns.
+  for (const Expr& sel : {MathF::Pow(x + 2.0f, x), MathF::Pow(0.5f, x)}) {
+    std::vector<float> ref;
+    for (float v : src)
+      if (v > -0.75f) ref.push_back(EvalValue(sel.Node(), v));
+    const std::vector<float> got = AsComputeQueryable(src, p).Where(x > -0.75f).Select(sel).ToArray();
+    CHECK(got.size() == ref.size());
+    int64_t worst = 0;
+    for (size_t k = 0; k < std::min(got.size(), ref.size()); ++k) {
+      int32_t a, b;
+      std::memcpy(&a, &got[k], 4);
+      std::memcpy(&b, &ref[k], 4);
+      worst = std::max<int64_t>(worst, std::llabs((int64_t)a - (int64_t)b));
+    }
+    CHECK(worst <= 2);
+    const double sum = AsComputeQueryable(src, p).Where(x > -0.75f).Select(sel).Sum();
+    double ref_sum = 0.0;
+    for (float v : ref) ref_sum += v;
+    CHECK(std::fabs(sum - ref_sum) <= 1e-5 * std::fabs(ref_sum));
   }
 }
 

@@ -73,6 +73,14 @@ def test_chain_validation():
     assert L.dc_linq_chain_validate(C.byref(bad_op)) == hip.DC_ERR_UNSUPPORTED
     bad_src = hip.LinqChain.assemble([(hip.LOAD, 9, 0)])
     assert L.dc_linq_chain_validate(C.byref(bad_src)) == hip.DC_ERR_UNSUPPORTED
+    pow_prog = hip.LinqChain.assemble([(hip.LOAD, hip.SRC_ELEM, 0), (hip.POW, hip.SRC_IMM, 2.0),
+                                       (hip.RPOW, hip.SRC_S0, 0), (hip.MAP, hip.SRC_IMM, 0)])
+    assert L.dc_linq_chain_validate(C.byref(pow_prog)) == 0  # MathF.Pow: float32 programs only
+    ipow = hip.LinqChain.assemble([(hip.LOAD, hip.SRC_ELEM, 0), (hip.POW, hip.SRC_IMM, 2), (hip.MAP, hip.SRC_IMM, 0)],
+                                  int32=True)
+    assert L.dc_linq_chain_validate_i32(C.byref(ipow)) == hip.DC_ERR_UNSUPPORTED
+    assert L.dc_linq_chain_validate(C.byref(hip.LinqChain.assemble([(hip.RPOW + 1, hip.SRC_IMM, 0)]))) == \
+        hip.DC_ERR_UNSUPPORTED
     too_long = hip.LinqChain()
     too_long.n_instr = hip.DC_LINQ_MAX_INSTR + 1
     assert L.dc_linq_chain_validate(C.byref(too_long)) == hip.DC_ERR_INVALID_ARGUMENT

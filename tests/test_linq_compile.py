@@ -6,8 +6,9 @@ import pytest
 
 from dotcompute_amd import hip
 from dotcompute_amd.hip import (ABS, ADD, CEIL, CMP_AND, CMP_EQ, CMP_GT, CMP_LT, CMP_OR, DIV, FILTER, FLOOR, LOAD,
-                                MAP, MAX, MIN, MUL, NEG, PAND_Q, PNOT, POR_Q, PSTORE, RDIV, REM, ROUND, RREM, RSUB,
-                                SQRT, SRC_ELEM, SRC_IMM, SRC_S0, SRC_S1, STORE_S0, STORE_S1, SUB, LinqChain)
+                                MAP, MAX, MIN, MUL, NEG, PAND_Q, PNOT, POR_Q, POW, PSTORE, RDIV, REM, ROUND, RPOW,
+                                RREM, RSUB, SQRT, SRC_ELEM, SRC_IMM, SRC_S0, SRC_S1, STORE_S0, STORE_S1, SUB,
+                                LinqChain)
 
 try:
     hip.load()
@@ -21,7 +22,7 @@ EVERY_FLOAT_OP = [(LOAD, SRC_ELEM, 0), (STORE_S0, SRC_IMM, 0), (ADD, SRC_IMM, 1.
                   (RSUB, SRC_IMM, 2), (MUL, SRC_ELEM, 0), (DIV, SRC_IMM, 3), (RDIV, SRC_IMM, 5), (REM, SRC_IMM, 0.75),
                   (RREM, SRC_IMM, 9), (MIN, SRC_IMM, 4), (MAX, SRC_S0, 0), (NEG, SRC_IMM, 0), (ABS, SRC_IMM, 0),
                   (SQRT, SRC_IMM, 0), (FLOOR, SRC_IMM, 0), (CEIL, SRC_IMM, 0), (ROUND, SRC_IMM, 0),
-                  (STORE_S1, SRC_IMM, 0), (CMP_GT, SRC_S1, 0), (PSTORE, SRC_IMM, 0), (CMP_LT, SRC_IMM, 3, CMP_AND),
+                  (POW, SRC_IMM, 1.5), (RPOW, SRC_S0, 0), (STORE_S1, SRC_IMM, 0), (CMP_GT, SRC_S1, 0), (PSTORE, SRC_IMM, 0), (CMP_LT, SRC_IMM, 3, CMP_AND),
                   (CMP_EQ, SRC_IMM, 0, CMP_OR), (PAND_Q, SRC_IMM, 0), (POR_Q, SRC_IMM, 0), (PNOT, SRC_IMM, 0),
                   (FILTER, SRC_IMM, 0), (MAP, SRC_IMM, 0)]
 EVERY_INT_OP = [(LOAD, SRC_ELEM, 0), (STORE_S0, SRC_IMM, 0), (ADD, SRC_IMM, 7), (SUB, SRC_S0, 0), (RSUB, SRC_IMM, 2),

@@ -315,6 +315,54 @@ def test_float_remainder_and_rounding_closed_forms():
     assert run([(LOAD, SRC_ELEM, 0), (ROUND, SRC_IMM, 0)])[:6].tolist() == [0.0, 2.0, 2.0, -0.0, -2.0, -2.0]
 
 
+# MathF.Pow special values (IEEE 754-2008 pow, C99 Annex F; .NET Core's MathF.Pow documents the
+# same table): (base, exponent, result).
+INF, NAN = float("inf"), float("nan")
+POW_SPECIALS = [
+    (NAN, 0.0, 1.0), (NAN, -0.0, 1.0), (INF, 0.0, 1.0), (-3.5, -0.0, 1.0),    # pow(x, +-0) = 1
+    (1.0, NAN, 1.0), (1.0, INF, 1.0), (1.0, -INF, 1.0), (1.0, -2.5, 1.0),    # pow(1, y) = 1
+    (-1.0, INF, 1.0), (-1.0, -INF, 1.0),                                     # pow(-1, +-inf) = 1
+    (0.0, -3.0, INF), (-0.0, -3.0, -INF), (0.0, -2.0, INF), (-0.0, -2.0, INF), (-0.0, -0.5, INF),
+    (0.0, 3.0, 0.0), (-0.0, 3.0, -0.0), (-0.0, 2.0, 0.0), (-0.0, 0.5, 0.0), (-0.0, INF, 0.0),
+    (0.5, -INF, INF), (-0.5, -INF, INF), (2.0, -INF, 0.0), (-2.0, -INF, 0.0),
+    (0.5, INF, 0.0), (-0.5, INF, 0.0), (2.0, INF, INF), (-2.0, INF, INF),
+    (-INF, -3.0, -0.0), (-INF, -2.0, 0.0), (-INF, -0.5, 0.0), (-INF, 3.0, -INF), (-INF, 2.0, INF),
+    (-INF, 0.5, INF), (INF, -1.0, 0.0), (INF, 0.5, INF),
+    (-8.0, 1.0 / 3.0, NAN), (-2.0, 0.5, NAN), (NAN, 1.0, NAN), (2.0, NAN, NAN),   # NaN results
+    (-2.0, 3.0, -8.0), (-2.0, -2.0, 0.25), (2.0, 10.0, 1024.0), (3.0, 2.0, 9.0), (2.0, 3.0, 8.0),
+    (0.25, 0.5, 0.5), (1e-30, 2.0, 0.0), (1e30, 2.0, INF), (2.0, -149.0, 2.0 ** -149),
+]
+
+
+def test_float_pow_special_values_and_accuracy():
+    """MathF.Pow through the interpreter's POW (v = pow(v, operand)) and RPOW (v = pow(operand, v)):
+    every special value of the IEEE/C99 table bit for bit (signed zeros and infinities included),
+    operands in the right order (2^3 = 8 but 3^2 = 9), and finite results within 1 ulp of the
+    float64 pow rounded to float32 (the C runtime's powf is within 1 ulp of the exact value)."""
+    from dotcompute_amd.hip import LOAD, MAP, POW, RPOW, SRC_ELEM, SRC_IMM
+
+    def pow_of(base, exp):  # LOAD base; POW exp
+        return oracle.linq_eval(_chain([(LOAD, SRC_IMM, base), (POW, SRC_IMM, exp), (MAP, SRC_IMM, 0)]), 0.0)[1]
+
+    def rpow_of(base, exp):  # the element is the exponent: LOAD e; RPOW base
+        return oracle.linq_eval(_chain([(LOAD, SRC_ELEM, 0), (RPOW, SRC_IMM, base), (MAP, SRC_IMM, 0)]), exp)[1]
+
+    for base, exp, want in POW_SPECIALS:
+        for got in (pow_of(base, exp), rpow_of(base, exp)):
+            w = np.float32(want)
+            assert (np.isnan(got) and np.isnan(w)) or np.float32(got).view(np.uint32) == w.view(np.uint32), \
+                (base, exp, got, want)
+    x = np.abs(oracle.gen_uniform_f32(3000, 71, 0)) * 8.0 + np.float32(1e-3)
+    y = oracle.gen_uniform_f32(3000, 72, 0) * 6.0
+    for b, e in zip(x.tolist(), y.tolist()):
+        ref = np.float32(math.pow(np.float64(np.float32(b)), np.float64(np.float32(e))))
+        got = np.float32(pow_of(b, e))
+        if np.isinf(ref) or ref == 0.0:
+            assert got == ref, (b, e)
+        else:
+            assert abs(int(got.view(np.int32)) - int(ref.view(np.int32))) <= 1, (b, e, got, ref)
+
+
 def test_int_min_max_against_numpy():
     """Where/Select then Min/Max over int32: the extreme of the elements ToArray returns, the kept
     count, no value for an empty result, and the first exception when one is thrown."""
