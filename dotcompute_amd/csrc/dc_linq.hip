@@ -1186,6 +1186,82 @@ __global__ __launch_bounds__(kFinalBlock) void where_select_minmax_pass2(const f
   }
 }
 
+// ---- Where/Select -> Aggregate((acc, x) => MathF.Min(acc, x)) / MathF.Max -----------------------
+// MathF.Min and MathF.Max are IEEE 754-2019 minimum / maximum: a NaN operand gives NaN, and -0
+// orders below +0. The fold is then associative and commutative (up to which NaN it returns, and
+// .NET gives NaN payloads no meaning), so each partial is a plain value and the grid's result is the
+// sequential fold's, whatever the order in which lanes, waves and workgroups meet. A dropped
+// element contributes the identity (+inf for Min, -inf for Max), which changes no result. The
+// programs run on the interpreter variants only: an affine chain's interpreter result is the
+// specialised kernels' by construction, and the fold needs no kernel per canonical shape.
+template <int OP>
+__device__ inline float fold_op(float a, float b) {
+  return OP == kOpMin ? __builtin_elementwise_minimum(a, b) : __builtin_elementwise_maximum(a, b);
+}
+
+template <int OP>
+constexpr float fold_identity() {
+  return OP == kOpMin ? __builtin_inff() : -__builtin_inff();
+}
+
+// Block-wide fold; the result is valid in thread 0.
+template <int OP, int BLOCK>
+__device__ inline float fold_block(float v, float* scratch) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fold_op<OP>(v, __shfl_xor(v, off, 64));
+  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
+  __syncthreads();
+  if (threadIdx.x == 0)
+    for (int w = 1; w < BLOCK / dc::kWave; ++w) v = fold_op<OP>(v, scratch[w]);
+  return v;
+}
+
+template <int RD, int OP>
+__global__ __launch_bounds__(kSumBlock) void where_select_fold_pass1(const dc_linq_chain prog, const AffineChain aff,
+                                                                     const RdConst canon, const float* __restrict__ in,
+                                                                     int64_t n, int64_t h, float* __restrict__ pv,
+                                                                     int64_t* __restrict__ pcnt) {
+  __shared__ float lds_f[kSumBlock / dc::kWave];
+  __shared__ int64_t lds_i[kSumBlock / dc::kWave];
+  constexpr float kId = fold_identity<OP>();
+  float acc = kId;
+  auto one = [&](float x, bool kept, int64_t) __attribute__((always_inline)) { acc = fold_op<OP>(acc, kept ? x : kId); };
+  const int64_t cnt = visit_chunk<RD>(
+      prog, aff, canon, in, n, h,
+      [&](const float (&e)[16], const bool (&kept)[16], int64_t) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc = fold_op<OP>(acc, kept[j] ? e[j] : kId);
+      },
+      one, one);
+  const float bv = fold_block<OP, kSumBlock>(acc, lds_f);
+  const int64_t bcnt = dc::block_sum64<kSumBlock>(cnt, lds_i);
+  if (threadIdx.x == 0) {
+    pv[blockIdx.x] = bv;
+    pcnt[blockIdx.x] = bcnt;
+  }
+}
+
+template <int OP>
+__global__ __launch_bounds__(kFinalBlock) void where_select_fold_pass2(const float* __restrict__ pv,
+                                                                       const int64_t* __restrict__ pcnt, int count,
+                                                                       float* __restrict__ value_out,
+                                                                       int64_t* __restrict__ count_out) {
+  __shared__ float lds_f[kFinalBlock / dc::kWave];
+  __shared__ int64_t lds_i[kFinalBlock / dc::kWave];
+  float v = fold_identity<OP>();
+  int64_t c = 0;
+  for (int b = threadIdx.x; b < count; b += kFinalBlock) {
+    v = fold_op<OP>(v, pv[b]);
+    c += pcnt[b];
+  }
+  v = fold_block<OP, kFinalBlock>(v, lds_f);
+  const int64_t total = dc::block_sum64<kFinalBlock>(c, lds_i);
+  if (threadIdx.x == 0) {
+    if (value_out) *value_out = total ? v : 0.0f;
+    if (count_out) *count_out = total;
+  }
+}
+
 // ---- strategy choice -----------------------------------------------------------------------------
 const void* rounds_kernel(int mode) {
   const void* fn = nullptr;
@@ -1523,7 +1599,7 @@ DC_HIP_API int32_t dc_hip_linq_where_select_sum_f32_noalloc(dc_hip_ctx* ctx, con
 DC_HIP_API int32_t dc_hip_linq_where_select_minmax_f32(dc_hip_ctx* ctx, const dc_linq_chain* chain,
                                                        const float* input, int64_t n, int32_t op, float* value_out,
                                                        int64_t* count_out) {
-  if (n < 0 || (n > 0 && !input) || (op != DC_LINQ_MIN && op != DC_LINQ_MAX)) return DC_ERR_INVALID_ARGUMENT;
+  if (n < 0 || (n > 0 && !input) || op < DC_LINQ_MIN || op > DC_LINQ_FOLD_MAX) return DC_ERR_INVALID_ARGUMENT;
   DC_RETURN_IF(dc_linq_chain_validate(chain));
   DC_CTX_ENTER(ctx);
   const unsigned grid = where_select_sum_grid(ctx, n);
@@ -1533,6 +1609,24 @@ DC_HIP_API int32_t dc_hip_linq_where_select_minmax_f32(dc_hip_ctx* ctx, const dc
   float* pv = reinterpret_cast<float*>(pcnt + grid);
   const ReducePlan p = reduce_plan(*chain);
   const int64_t h = reduce_head(input, n);
+  if (op == DC_LINQ_FOLD_MIN || op == DC_LINQ_FOLD_MAX) {
+    const int rd = program_uses_libm(*chain) ? kRdInterpLibm : program_uses_saves(*chain) ? kRdInterpSaves : kRdInterp;
+    auto launch = [&](auto mode) {
+      constexpr int RD = decltype(mode)::value;
+      if (op == DC_LINQ_FOLD_MIN)
+        where_select_fold_pass1<RD, kOpMin><<<grid, kSumBlock, 0, ctx->stream>>>(*chain, p.aff, p.k, input, n, h, pv, pcnt);
+      else
+        where_select_fold_pass1<RD, kOpMax><<<grid, kSumBlock, 0, ctx->stream>>>(*chain, p.aff, p.k, input, n, h, pv, pcnt);
+    };
+    if (rd == kRdInterpLibm) launch(std::integral_constant<int, kRdInterpLibm>{});
+    else if (rd == kRdInterpSaves) launch(std::integral_constant<int, kRdInterpSaves>{});
+    else launch(std::integral_constant<int, kRdInterp>{});
+    if (op == DC_LINQ_FOLD_MIN)
+      where_select_fold_pass2<kOpMin><<<1, kFinalBlock, 0, ctx->stream>>>(pv, pcnt, (int)grid, value_out, count_out);
+    else
+      where_select_fold_pass2<kOpMax><<<1, kFinalBlock, 0, ctx->stream>>>(pv, pcnt, (int)grid, value_out, count_out);
+    return dc::last_launch_status();
+  }
   rd_dispatch(p.mode, [&](auto mode) {
     constexpr int RD = decltype(mode)::value;
     if (op == DC_LINQ_MIN)

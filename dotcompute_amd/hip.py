@@ -41,6 +41,9 @@ LINQ_ELEMENT_F32, LINQ_ELEMENT_I32 = 0, 1
 # dc_linq_minmax: which terminal dc_hip_linq_where_select_minmax_f32 computes
 LINQ_MIN = 0
 LINQ_MAX = 1
+# Aggregate((acc, x) => MathF.Min(acc, x)) / MathF.Max: IEEE minimum / maximum folds
+LINQ_FOLD_MIN = 2
+LINQ_FOLD_MAX = 3
 
 DC_LINQ_MAX_INSTR = 48
 
@@ -451,7 +454,8 @@ class Context:
 
     def where_select_minmax_f32(self, chain: LinqChain, x: DeviceArray, op: int, value_out: DeviceArray | None,
                                 count: DeviceArray | None, n: int | None = None) -> None:
-        """op = LINQ_MIN or LINQ_MAX; value_out: float32[1], count: int64[1] (device)."""
+        """op = LINQ_MIN, LINQ_MAX, LINQ_FOLD_MIN or LINQ_FOLD_MAX; value_out: float32[1], count:
+        int64[1] (device)."""
         n = x.size if n is None else n
         check(load().dc_hip_linq_where_select_minmax_f32(self.handle, C.byref(chain), x.ptr, n, op,
                                                         value_out.ptr if value_out else None,

@@ -154,7 +154,8 @@ enum class Terminal {
 };
 
 // Aggregate folds the HIP kernels run exactly: int (acc, x) => acc + x (unchecked, so the fold is
-// the exact total wrapped to 32 bits, whatever the order) and Math.Min / Math.Max over int.
+// the exact total wrapped to 32 bits, whatever the order), Math.Min / Math.Max over int, and
+// MathF.Min / MathF.Max over float (IEEE minimum / maximum: associative).
 enum class AggregateKind { None, Add, Min, Max };
 
 struct FusedKernelPlan {
@@ -302,8 +303,8 @@ class ComputeQueryable {
   T Single() const;
   T SingleOrDefault() const;  // 0 when empty; more than one element still throws
   // Aggregate((acc, x) => ...) and Aggregate(seed, (acc, x) => ...): the folds AggregateKind names,
-  // with Param(0) the accumulator and Param(1) the element; other folds (float + and * depend on
-  // the order of their roundings) throw NotSupportedException.
+  // with Param(0) the accumulator and Param(1) the element (over float: MathF.Min / MathF.Max);
+  // other folds (float + and * depend on the order of their roundings) throw NotSupportedException.
   T Aggregate(const Expr& func) const;
   T Aggregate(T seed, const Expr& func) const;
   std::vector<T> ToComputeArray() const { return ToArray(); }

@@ -652,11 +652,16 @@ QueryResult<float> RuntimeExecutor::Run(const FusedKernelPlan& plan, const float
     r.Count = k;
     r.Values.resize((size_t)k);
     out->CopyToHost(r.Values.data(), (size_t)k * sizeof(float));  // only the compacted prefix comes back
-  } else if (plan.Term == Terminal::Min || plan.Term == Terminal::Max) {
+  } else if (plan.Term == Terminal::Min || plan.Term == Terminal::Max || plan.Term == Terminal::Aggregate) {
+    if (plan.Term == Terminal::Aggregate && plan.Fold != AggregateKind::Min && plan.Fold != AggregateKind::Max)
+      throw NotSupportedException("internal: a float Aggregate other than MathF.Min / MathF.Max");
+    const int32_t op = plan.Term == Terminal::Min   ? DC_LINQ_MIN
+                       : plan.Term == Terminal::Max ? DC_LINQ_MAX
+                       : plan.Fold == AggregateKind::Min ? DC_LINQ_FOLD_MIN
+                                                         : DC_LINQ_FOLD_MAX;
     auto val = mem.AllocateAsync<float>(1);
     auto cnt = mem.AllocateAsync<int64_t>(1);
-    Check(dc_hip_linq_where_select_minmax_f32(ctx, &plan.Program, device_in, (int64_t)n,
-                                              plan.Term == Terminal::Min ? DC_LINQ_MIN : DC_LINQ_MAX, val->Data(),
+    Check(dc_hip_linq_where_select_minmax_f32(ctx, &plan.Program, device_in, (int64_t)n, op, val->Data(),
                                               cnt->Data()),
           "dc_hip_linq_where_select_minmax_f32");
     acc_->Synchronize();
@@ -873,8 +878,10 @@ QueryResult<T> RuntimeExecutor::RunSegments(const std::vector<FusedKernelPlan>& 
     return r;
   }
   if (last.Term == Terminal::Aggregate) {
-    // Add: the exact total (Count's kernel, which has no overflow rule; the fold is unchecked
-    // and wraps); Min / Max: the Min / Max kernels.
+    // float: the MathF.Min / MathF.Max fold kernels. int: Add is the exact total (Count's kernel,
+    // which has no overflow rule; the fold is unchecked and wraps); Min / Max are the Min / Max
+    // kernels (over int, Math.Min / Math.Max fold to Enumerable.Min / Max).
+    if constexpr (std::is_same<T, float>::value) return Run(last, src, len);
     FusedKernelPlan p = last;
     p.Term = last.Fold == AggregateKind::Add ? Terminal::Count
              : last.Fold == AggregateKind::Min ? Terminal::Min : Terminal::Max;
@@ -935,9 +942,9 @@ std::shared_ptr<ComputeQueryProvider> ComputeQueryProvider::Default() {
 namespace {
 
 // The fold of an Aggregate lambda (acc, x) => ...: Add, Min or Max of the two parameters, in either
-// order, over int elements. Everything else is refused: float + and * fold with one rounding per
-// step in enumeration order, which a parallel reduction does not reproduce, and MathF.Min/Max
-// fold signed zeros and NaNs differently from the Min/Max kernels.
+// order. int: all three. float: MathF.Min and MathF.Max (IEEE minimum / maximum, associative, on
+// their own fold kernels); float + and * fold with one rounding per step in enumeration order,
+// which a parallel reduction does not reproduce, so they are refused.
 AggregateKind ParseFold(const Expr& func, ElementType element) {
   const ExprNode& n = func.Node();
   auto is_param = [](const std::shared_ptr<const ExprNode>& c, int i) {
@@ -945,17 +952,13 @@ AggregateKind ParseFold(const Expr& func, ElementType element) {
   };
   const bool two_params = n.Left && n.Right && ((is_param(n.Left, 0) && is_param(n.Right, 1)) ||
                                                 (is_param(n.Left, 1) && is_param(n.Right, 0)));
-  if (!two_params || element != ElementType::Int32)
-    throw NotSupportedException("Aggregate(" + func.ToString() + ") has no exact HIP kernel: the kernels fold int "
-                                "(acc, x) => acc + x, Math.Min(acc, x) and Math.Max(acc, x)");
-  switch (n.Kind) {
-    case ExprKind::Add: return AggregateKind::Add;
-    case ExprKind::Min: return AggregateKind::Min;
-    case ExprKind::Max: return AggregateKind::Max;
-    default:
-      throw NotSupportedException("Aggregate(" + func.ToString() + ") has no exact HIP kernel: the kernels fold int "
-                                  "(acc, x) => acc + x, Math.Min(acc, x) and Math.Max(acc, x)");
-  }
+  const bool is_int = element == ElementType::Int32;
+  if (two_params && n.Kind == ExprKind::Add && is_int) return AggregateKind::Add;
+  if (two_params && n.Kind == ExprKind::Min) return AggregateKind::Min;
+  if (two_params && n.Kind == ExprKind::Max) return AggregateKind::Max;
+  throw NotSupportedException("Aggregate(" + func.ToString() + ") has no exact HIP kernel: the kernels fold int "
+                              "(acc, x) => acc + x, Math.Min(acc, x) and Math.Max(acc, x), and float "
+                              "MathF.Min(acc, x) and MathF.Max(acc, x)");
 }
 
 }  // namespace
@@ -995,8 +998,11 @@ FusedKernelPlan ComputeQueryProvider::Plan(const std::vector<MethodCall>& chain,
     plan.Fold = ParseFold(*fold->Lambda, element);
     if (fold->Seed) {
       const ExprNode& sn = fold->Seed->Node();
-      if (sn.Kind != ExprKind::Constant || !sn.IsInt) throw ArgumentException("Aggregate's seed is an int constant");
-      plan.Seed = sn.IValue;
+      if (sn.Kind != ExprKind::Constant) throw ArgumentException("Aggregate's seed is a constant");
+      if (element == ElementType::Int32) {
+        if (!sn.IsInt) throw ArgumentException("Aggregate's seed over int is an int constant");
+        plan.Seed = sn.IValue;
+      }
     }
   }
   return plan;
@@ -1145,6 +1151,24 @@ T ComputeQueryable<T>::SingleOrDefault() const {
   return r.Count == 0 ? T{} : r.Values[0];
 }
 
+namespace {
+
+// MathF.Min / MathF.Max (.NET Core 3.0 and later): NaN if either operand is NaN, -0 below +0.
+float NetMinF(float a, float b) {
+  if (std::isnan(a)) return a;
+  if (std::isnan(b)) return b;
+  if (a == b) return std::signbit(a) ? a : b;
+  return a < b ? a : b;
+}
+float NetMaxF(float a, float b) {
+  if (std::isnan(a)) return a;
+  if (std::isnan(b)) return b;
+  if (a == b) return std::signbit(a) ? b : a;
+  return a > b ? a : b;
+}
+
+}  // namespace
+
 // Aggregate(func): the fold starts from the first element (an empty sequence throws);
 // Aggregate(seed, func) from the seed. Add wraps as C#'s unchecked int +.
 template <typename T>
@@ -1156,7 +1180,7 @@ T ComputeQueryable<T>::Aggregate(const Expr& func) const {
   if constexpr (std::is_same<T, int32_t>::value) {
     return func.Node().Kind == ExprKind::Add ? (int32_t)(uint32_t)(uint64_t)r.IntSum : r.Extreme;
   } else {
-    return r.Extreme;  // not reached: float folds are refused by the planner
+    return r.Extreme;  // the MathF.Min / MathF.Max fold from the first element
   }
 }
 
@@ -1171,7 +1195,9 @@ T ComputeQueryable<T>::Aggregate(T seed, const Expr& func) const {
     if (r.Count == 0) return seed;
     return k == ExprKind::Min ? std::min(seed, r.Extreme) : std::max(seed, r.Extreme);
   } else {
-    return r.Count == 0 ? seed : r.Extreme;  // not reached: float folds are refused by the planner
+    // MathF.Min / MathF.Max are associative: fold(seed, x1..xn) = f(seed, fold(x1..xn)).
+    if (r.Count == 0) return seed;
+    return func.Node().Kind == ExprKind::Min ? NetMinF(seed, r.Extreme) : NetMaxF(seed, r.Extreme);
   }
 }
 

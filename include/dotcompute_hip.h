@@ -400,8 +400,11 @@ DC_HIP_API int32_t dc_hip_linq_where_select_sum_f32_noalloc(dc_hip_ctx* ctx, con
  * ExpressionTreeVisitor.cs:244-245; executed as LINQ-to-objects through the scalar branch,
  * ComputeQueryableExtensions.cs:265-267) and returns what the .NET 10 BCL Enumerable.Min/Max
  * (IEnumerable<float>) returns, bit for bit: Min the first NaN, else the first smallest element;
- * Max the first largest non-NaN element, or the last NaN when all are NaN. Deterministic. */
-enum dc_linq_minmax { DC_LINQ_MIN = 0, DC_LINQ_MAX = 1 };
+ * Max the first largest non-NaN element, or the last NaN when all are NaN. Deterministic.
+ * DC_LINQ_FOLD_MIN / DC_LINQ_FOLD_MAX compute Aggregate((acc, x) => MathF.Min(acc, x)) / MathF.Max
+ * instead (Aggregate maps to Reduce, ExpressionTreeVisitor.cs:263): IEEE 754-2019 minimum /
+ * maximum, NaN if any kept element is NaN, -0 below +0; the fold without a seed. */
+enum dc_linq_minmax { DC_LINQ_MIN = 0, DC_LINQ_MAX = 1, DC_LINQ_FOLD_MIN = 2, DC_LINQ_FOLD_MAX = 3 };
 DC_HIP_API int32_t dc_hip_linq_where_select_minmax_f32(dc_hip_ctx* ctx, const dc_linq_chain* chain,
                                                        const float* input, int64_t n, int32_t op,
                                                        float* value_out, int64_t* count_out);

@@ -54,6 +54,7 @@ def lib() -> C.CDLL:
             "oracle_linq_where_select_sum": (C.c_float, [_P, _P, _i64, _P, _P]),
             "oracle_linq_where_select_min": (_i64, [_P, _P, _i64, _P]),
             "oracle_linq_where_select_max": (_i64, [_P, _P, _i64, _P]),
+            "oracle_linq_where_select_fold": (_i64, [_P, _P, _i64, _i32, _P]),
             "oracle_where_gt0_select_2x_plus_1_minmax": (_i64, [_P, _i64, _i32, _P]),
             "oracle_linq_eval_i32": (_i32, [_P, _i32, _P, _P]),
             "oracle_linq_where_select_i32": (_i64, [_P, _P, _i64, _P, _P]),
@@ -210,6 +211,18 @@ def linq_where_select_minmax(chain, x: np.ndarray, op: str):
     out = np.zeros(1, np.float32)  # written through a pointer: NaN payload bits are kept
     fn = lib().oracle_linq_where_select_min if op == "min" else lib().oracle_linq_where_select_max
     k = fn(C.byref(chain), _p(x), x.size, _p(out))
+    if k < 0:
+        raise ValueError(f"malformed chain ({k})")
+    return out[0], int(k)
+
+
+def linq_where_select_fold(chain, x: np.ndarray, op: str):
+    """Aggregate((acc, x) => MathF.Min(acc, x)) (op "min") or MathF.Max ("max") of the kept, mapped
+    elements, folded in sequence order (restated in oracle.c). Returns (value as float32, count of
+    kept elements); value is meaningless when count == 0."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(1, np.float32)
+    k = lib().oracle_linq_where_select_fold(C.byref(chain), _p(x), x.size, 0 if op == "min" else 1, _p(out))
     if k < 0:
         raise ValueError(f"malformed chain ({k})")
     return out[0], int(k)

@@ -603,6 +603,24 @@ int64_t oracle_linq_where_select_max(const dc_linq_chain* chain, const float* in
   return s.k;
 }
 
+/* Enumerable.Aggregate(func) with func = (acc, x) => MathF.Min(acc, x) (op 0) or MathF.Max (op 1)
+ * over the kept, mapped elements (Aggregate maps to Reduce, ExpressionTreeVisitor.cs:263): the
+ * accumulator starts as the first element and takes func(acc, x) for each later one, in sequence
+ * order. net_min / net_max are MathF.Min / MathF.Max (NaN if either is NaN, -0 below +0). */
+int64_t oracle_linq_where_select_fold(const dc_linq_chain* chain, const float* in, int64_t n, int32_t op, float* out) {
+  int64_t k = 0;
+  float acc = 0.0f;
+  for (int64_t i = 0; i < n; ++i) {
+    float x;
+    int32_t r = oracle_linq_eval(chain, in[i], &x);
+    if (r < 0) return r;
+    if (!r) continue;
+    acc = k++ == 0 ? x : (op == 0 ? net_min(acc, x) : net_max(acc, x));
+  }
+  if (out) *out = acc;
+  return k;
+}
+
 /* .Where(x > 0f).Select(x * 2f + 1f).Min() / .Max() with the lambdas written out, as the
  * LINQ-to-objects fallback runs them (ComputeQueryableExtensions.cs:265-267): the same steps as
  * above without the chain interpreter. op 0 = Min, 1 = Max. */

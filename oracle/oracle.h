@@ -73,6 +73,10 @@ float oracle_linq_where_select_sum(const dc_linq_chain* chain, const float* in, 
  * the caller throws InvalidOperationException), or a negative value for an invalid program. */
 int64_t oracle_linq_where_select_min(const dc_linq_chain* chain, const float* in, int64_t n, float* out);
 int64_t oracle_linq_where_select_max(const dc_linq_chain* chain, const float* in, int64_t n, float* out);
+/* Aggregate((acc, x) => MathF.Min(acc, x)) (op 0) / MathF.Max (op 1) over the kept, mapped
+ * elements, folded in sequence order from the first one: result to *out, returns the kept count
+ * (0: the caller throws InvalidOperationException) or a negative value for an invalid program. */
+int64_t oracle_linq_where_select_fold(const dc_linq_chain* chain, const float* in, int64_t n, int32_t op, float* out);
 /* The same two operators after .Where(x > 0f).Select(x * 2f + 1f) with the lambdas written out
  * (op 0 = Min, 1 = Max): the CPU baseline of the fused Min/Max leg. */
 int64_t oracle_where_gt0_select_2x_plus_1_minmax(const float* in, int64_t n, int32_t op, float* out);

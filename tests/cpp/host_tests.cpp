@@ -1022,6 +1022,41 @@ TEST_GPU(linq_aggregate_folds) {
   CHECK_THROWS(NotSupportedException, AsComputeQueryable(r100, p).Aggregate(acc * x));
 }
 
+TEST_GPU(linq_float_aggregate_min_max_folds) {
+  // Aggregate((acc, x) => MathF.Min(acc, x)) / MathF.Max: NaN if any element is NaN, -0 below +0
+  // (unlike Enumerable.Min/Max, which skip NaNs in Max and take the first of equal zeros).
+  auto acc = Param(0), x = Param(1), e = Param();
+  auto p = std::make_shared<ComputeQueryProvider>(Gpu());
+  auto bits = [](float v) {
+    uint32_t b;
+    std::memcpy(&b, &v, 4);
+    return b;
+  };
+  std::vector<float> z{0.0f, 3.0f, -0.0f, 2.0f};
+  CHECK(bits(AsComputeQueryable(z, p).Aggregate(MathF::Min(acc, x))) == bits(-0.0f));
+  CHECK(bits(AsComputeQueryable(z, p).Where(e < 1.0f).Aggregate(MathF::Max(x, acc))) == bits(0.0f));
+  CHECK(bits(AsComputeQueryable(z, p).Where(e < 1.0f).Max()) == bits(0.0f));  // the first of the zeros
+  CHECK(bits(AsComputeQueryable(z, p).Where(e < 1.0f).Min()) == bits(0.0f));
+  std::vector<float> n{1.0f, NAN, 5.0f};
+  CHECK(std::isnan(AsComputeQueryable(n, p).Aggregate(MathF::Max(acc, x))));
+  CHECK(AsComputeQueryable(n, p).Max() == 5.0f);  // Enumerable.Max skips the NaN
+  CHECK(std::isnan(AsComputeQueryable(n, p).Aggregate(-7.0f, MathF::Min(acc, x))));  // the seed does not hide it
+  std::vector<float> v = Uniform(500000, 31, 0);
+  float mn = v[0], mx = v[0];
+  for (float t : v) {
+    mn = std::min(mn, t);
+    mx = std::max(mx, t);
+  }
+  CHECK(AsComputeQueryable(v, p).Aggregate(MathF::Min(acc, x)) == mn);
+  CHECK(AsComputeQueryable(v, p).Aggregate(MathF::Max(acc, x)) == mx);
+  CHECK(AsComputeQueryable(v, p).Aggregate(100.0f, MathF::Min(acc, x)) == mn);
+  CHECK(AsComputeQueryable(v, p).Aggregate(100.0f, MathF::Max(acc, x)) == 100.0f);
+  std::vector<float> none;
+  CHECK_THROWS(InvalidOperationException, AsComputeQueryable(none, p).Aggregate(MathF::Min(acc, x)));
+  CHECK(AsComputeQueryable(none, p).Aggregate(2.5f, MathF::Max(acc, x)) == 2.5f);
+  CHECK_THROWS(NotSupportedException, AsComputeQueryable(v, p).Aggregate(acc * x));
+}
+
 TEST_GPU(linq_min_max_match_enumerable) {
   auto x = Param();
   auto p = std::make_shared<ComputeQueryProvider>(Gpu());

@@ -564,3 +564,50 @@ def test_reductions_canonical_chains_special_values(ctx, shape, cmp):
             assert abs(s - sd) <= 1e-5 * math.log2(x.size) * max(abs(sd), 1.0)
         else:
             assert (math.isnan(s) and math.isnan(sd)) or s == sd
+
+
+FOLDS = [("min", hip.LINQ_FOLD_MIN), ("max", hip.LINQ_FOLD_MAX)]
+
+
+@pytest.mark.parametrize("n", [0, 1, 1000, 70_001, 1_000_000, 16_000_000])
+@pytest.mark.parametrize("which", FOLDS)
+def test_fold_min_max_match_sequential_fold(ctx, n, which):
+    """Aggregate((acc, x) => MathF.Min(acc, x)) / MathF.Max against the oracle's in-order fold: the
+    value bit for bit (any NaN for NaN), the kept count exactly; with and without NaNs, with both
+    zero signs as the extreme, on aligned and misaligned inputs."""
+    name, op = which
+    rng = np.random.default_rng(n + op)
+    zeros = rng.choice(np.array([0x00000000, 0x80000000, 0x3F800000, 0x40000000], np.uint32), n).view(np.float32)
+    salted = _salted_input(max(n, 1), 300 + op)[:n]
+    plain = oracle.gen_uniform_f32(n, 301, 0)
+    chains = (EMPTY, CHAIN, LinqChain.assemble([(LOAD, SRC_ELEM, 0), (CMP_NE, SRC_IMM, 2.0), (FILTER, SRC_IMM, 0)]))
+    for data in (zeros, salted, plain):
+        for chain in chains:
+            for offset in ((0, 3) if n and n <= 1_000_000 else (0,)):
+                got, cnt = run_minmax(ctx, chain, data, op, offset=offset)
+                ref, rcnt = oracle.linq_where_select_fold(chain, data, name)
+                assert cnt == rcnt
+                if rcnt:
+                    assert same_floats(np.array([got]), np.array([ref])), (name, chain.n_instr, offset, got, ref)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_fold_random_programs(ctx, seed):
+    """Random programs (the interpreter with and without save registers) and one with MathF.Pow
+    (the library variant, Where(x < 0.5f).Select(x => -MathF.Pow(x, 3f))): the folds match the
+    oracle's in-order fold, bit for bit; with Pow within 2 ulp (the two libraries' powf)."""
+    rng = np.random.default_rng(900 + seed)
+    prog = _random_program(rng)
+    x = _salted_input(90_000 + 419 * seed, 400 + seed)
+    if seed == 5:
+        prog = LinqChain.assemble([(LOAD, SRC_ELEM, 0), (CMP_LT, SRC_IMM, 0.5), (FILTER, SRC_IMM, 0),
+                                   (LOAD, SRC_ELEM, 0), (hip.POW, SRC_IMM, 3.0), (NEG, SRC_IMM, 0), (MAP, SRC_IMM, 0)])
+    for name, op in FOLDS:
+        got, cnt = run_minmax(ctx, prog, x, op)
+        ref, rcnt = oracle.linq_where_select_fold(prog, x, name)
+        assert cnt == rcnt
+        if rcnt and seed == 5 and np.isfinite(ref) and ref != 0:
+            g, r = np.array([got], np.float32).view(np.int32)[0], np.array([ref], np.float32).view(np.int32)[0]
+            assert np.sign(got) == np.sign(ref) and abs(int(g) - int(r)) <= 2, (got, ref)
+        elif rcnt:
+            assert same_floats(np.array([got]), np.array([ref]))

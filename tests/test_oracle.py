@@ -363,6 +363,34 @@ def test_float_pow_special_values_and_accuracy():
             assert abs(int(got.view(np.int32)) - int(ref.view(np.int32))) <= 1, (b, e, got, ref)
 
 
+def test_float_fold_min_max_hand_cases_and_numpy():
+    """Aggregate((acc, x) => MathF.Min(acc, x)) / MathF.Max, folded in order: -0 below +0 whatever
+    the order of the zeros, NaN wherever a NaN is kept (Enumerable.Max would skip it), the
+    reference's {5, 2, 8, 1} input (ExpressionTreeVisitorTests.cs:113-147), and numpy min/max of
+    the kept, mapped values on NaN-free data without zeros, where the fold and Enumerable agree."""
+    from dotcompute_amd.hip import CMP_GT, FILTER, LOAD, MAP, MUL, SRC_ELEM, SRC_IMM
+    ident = _chain([])
+    f32 = lambda v: np.array(v, np.float32)
+    for xs, mn, mx in (([0.0, -0.0], -0.0, 0.0), ([-0.0, 0.0], -0.0, 0.0), ([5.0, 2.0, 8.0, 1.0], 1.0, 8.0),
+                       ([3.0, np.nan, 1.0], np.nan, np.nan), ([np.nan], np.nan, np.nan), ([-np.inf, 2.0], -np.inf, 2.0)):
+        for op, want in (("min", mn), ("max", mx)):
+            got, k = oracle.linq_where_select_fold(ident, f32(xs), op)
+            assert k == len(xs)
+            assert (np.isnan(got) and np.isnan(want)) or f32(got).view(np.uint32) == f32(want).view(np.uint32), \
+                (xs, op, got)
+    assert oracle.linq_where_select_fold(ident, f32([]), "min")[1] == 0
+    # Enumerable.Max skips the NaN the fold keeps; Enumerable takes the first of equal zeros
+    assert oracle.linq_where_select_minmax(ident, f32([3.0, np.nan, 1.0]), "max")[0] == 3.0
+    assert oracle.linq_where_select_minmax(ident, f32([0.0, -0.0]), "min")[0].view(np.uint32) == 0
+    x = oracle.gen_uniform_f32(50_000, 77, 0)
+    x = x[x != 0]
+    prog = _chain([(LOAD, SRC_ELEM, 0), (CMP_GT, SRC_IMM, -0.5), (FILTER, SRC_IMM, 0),
+                   (LOAD, SRC_ELEM, 0), (MUL, SRC_IMM, 3.0), (MAP, SRC_IMM, 0)])
+    kept = x[x > np.float32(-0.5)] * np.float32(3.0)
+    assert oracle.linq_where_select_fold(prog, x, "min") == (kept.min(), kept.size)
+    assert oracle.linq_where_select_fold(prog, x, "max") == (kept.max(), kept.size)
+
+
 def test_int_min_max_against_numpy():
     """Where/Select then Min/Max over int32: the extreme of the elements ToArray returns, the kept
     count, no value for an empty result, and the first exception when one is thrown."""
