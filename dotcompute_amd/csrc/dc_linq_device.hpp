@@ -840,10 +840,12 @@ __device__ __attribute__((always_inline)) inline void rounds_body(
   // path-insensitive: on a path that skipped a later load, the wait for the round being staged
   // would have to cover every load still in flight, draining the pipeline.
   const uint32_t last = R0 > 0 ? R0 - 1 : 0;
-  // Rounds of look-ahead: kRrAhead, or 2 for the int32 interpreter, whose per-chunk state with five
-  // buffers exceeded the 168 registers a lane may hold here and spilled to scratch (two rounds
-  // measured as fast as four on the headline kernel, so the depth is not what bounds it).
-  constexpr int kAhead = kIntProg && RD != kRdJit ? 2 : kRrAhead;
+  // Rounds of look-ahead: kRrAhead, or 2 for the interpreters: the int32 one's per-chunk state with
+  // five buffers exceeded the 168 registers a lane may hold here and spilled to scratch, and the
+  // float ones ran 3-33 % faster with two (149 -> 116 VGPRs without save registers, 165 -> 132 with
+  // them, and no scratch for the library variant). Two rounds measured as fast as four on the
+  // headline kernel, so the depth is not what bounds these kernels.
+  constexpr int kAhead = (kIntProg || rd_is_float_interp(RD)) && RD != kRdJit ? 2 : kRrAhead;
   constexpr int kBufs = kAhead + 1;
   float e[kBufs][kRrEpt];  // register buffers: constant indices only, after full unrolling
   if (R0 > 0)
