@@ -498,11 +498,11 @@ __device__ __attribute__((always_inline)) inline void apply_reduce_flags(const d
 // apply_reduce_flags for every mode, the int32 ones included: elements outside `live` are not kept
 // (int32 modes; the float modes are only called on present elements), and the exceptions of an
 // int32 program go to `f`.
-// The interpreters run over at most CHUNK elements at a time. The round-robin kernel passes 16 for
-// the float interpreters (their dispatch then covers twice the elements: 737 -> 507 us for a
-// general float program at 256M, 940 -> 700 us with save registers, although that variant and the
-// library one then reload 32 B from scratch) and 8 for the int32 one, whose registers (values,
-// faults, operands) on top of the look-ahead buffers spill to scratch with 16.
+// The interpreters run over at most CHUNK elements at a time. The round-robin kernel passes all 16
+// of a round's elements: each instruction's dispatch then covers twice the elements of 8-element
+// chunks, measured at 256M as 737 -> 507 us for a general float program, 940 -> 700 us with save
+// registers, 812 -> 694 us for the int32 Where(x % 2 == 0).Select(x * x). With 16 the save-register,
+// library and int32 variants keep a few values in scratch (32-176 B per lane), and are still faster.
 template <int RD, int EPT, int CHUNK = EPT>
 __device__ __attribute__((always_inline)) inline void eval_flags(const dc_linq_chain& prog, const AffineChain& aff,
                                                                  const RdConst& k, float (&e)[EPT], bool (&kept)[EPT],
@@ -683,7 +683,7 @@ __device__ __attribute__((always_inline)) inline void rounds_body(
       for (int j = 0; j < kRrEpt; ++j) kept[j] = rd_compare<rd_cmp(RD)>(e[j], canon.t);
     } else if constexpr (kIntProg || rd_is_float_interp(RD) || RD == kRdJit) {
       Faults f;
-      eval_program<RD, Gen, kRrEpt, rd_is_float_interp(RD) ? kRrEpt : kRrEpt / 2>(prog, aff, canon, e, kept, live, f);
+      eval_program<RD, Gen, kRrEpt, kRrEpt>(prog, aff, canon, e, kept, live, f);
       if constexpr (kIntProg) {
         const int b = __builtin_ctz(f.hit | 0x80000000u);
         const uint64_t code = (uint64_t)(head_n + first + (b >> 2) * (4 * dc::kWave) + (b & 3)) * 4u +
