@@ -1191,9 +1191,8 @@ __global__ __launch_bounds__(kFinalBlock) void where_select_minmax_pass2(const f
 // orders below +0. The fold is then associative and commutative (up to which NaN it returns, and
 // .NET gives NaN payloads no meaning), so each partial is a plain value and the grid's result is the
 // sequential fold's, whatever the order in which lanes, waves and workgroups meet. A dropped
-// element contributes the identity (+inf for Min, -inf for Max), which changes no result. The
-// programs run on the interpreter variants only: an affine chain's interpreter result is the
-// specialised kernels' by construction, and the fold needs no kernel per canonical shape.
+// element contributes the identity (+inf for Min, -inf for Max), which changes no result. Every
+// program variant of the other reductions runs it (the canonical shapes too).
 template <int OP>
 __device__ inline float fold_op(float a, float b) {
   return OP == kOpMin ? __builtin_elementwise_minimum(a, b) : __builtin_elementwise_maximum(a, b);
@@ -1610,17 +1609,13 @@ DC_HIP_API int32_t dc_hip_linq_where_select_minmax_f32(dc_hip_ctx* ctx, const dc
   const ReducePlan p = reduce_plan(*chain);
   const int64_t h = reduce_head(input, n);
   if (op == DC_LINQ_FOLD_MIN || op == DC_LINQ_FOLD_MAX) {
-    const int rd = program_uses_libm(*chain) ? kRdInterpLibm : program_uses_saves(*chain) ? kRdInterpSaves : kRdInterp;
-    auto launch = [&](auto mode) {
+    rd_dispatch(p.mode, [&](auto mode) {
       constexpr int RD = decltype(mode)::value;
       if (op == DC_LINQ_FOLD_MIN)
         where_select_fold_pass1<RD, kOpMin><<<grid, kSumBlock, 0, ctx->stream>>>(*chain, p.aff, p.k, input, n, h, pv, pcnt);
       else
         where_select_fold_pass1<RD, kOpMax><<<grid, kSumBlock, 0, ctx->stream>>>(*chain, p.aff, p.k, input, n, h, pv, pcnt);
-    };
-    if (rd == kRdInterpLibm) launch(std::integral_constant<int, kRdInterpLibm>{});
-    else if (rd == kRdInterpSaves) launch(std::integral_constant<int, kRdInterpSaves>{});
-    else launch(std::integral_constant<int, kRdInterp>{});
+    });
     if (op == DC_LINQ_FOLD_MIN)
       where_select_fold_pass2<kOpMin><<<1, kFinalBlock, 0, ctx->stream>>>(pv, pcnt, (int)grid, value_out, count_out);
     else
