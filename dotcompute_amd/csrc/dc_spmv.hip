@@ -739,7 +739,16 @@ __global__ __launch_bounds__(SPAN / 8) void spmv_tile_rows(
     }
     const int32_t E = min((int32_t)rt[S], kSt);
     int16_t* run_of = reinterpret_cast<int16_t*>(stage);  // kSt int16 fit in half the stage
-    for (int32_t li = pre; li < min(pre + n, E); ++li) run_of[li] = (int16_t)t;
+    if (S <= kWaves) {
+      // Few runs (a matrix of few columns, one or two x slices): one lane per run would write up
+      // to E entries alone while the workgroup waits; the whole workgroup fills each run instead.
+      for (int32_t s = 0; s < S; ++s) {
+        const int32_t ps = rt[s], pe = min(ps + (t1[s] - t0[s]), E);
+        for (int32_t li = ps + t; li < pe; li += kThreads) run_of[li] = (int16_t)s;
+      }
+    } else {
+      for (int32_t li = pre; li < min(pre + n, E); ++li) run_of[li] = (int16_t)t;
+    }
     __syncthreads();
     constexpr int kIt = kSt / kThreads;
     const int32_t nit = (E + kThreads - 1) / kThreads;
